@@ -1,0 +1,191 @@
+/*
+ * npn_spec_verify.h -- C ABI of the MI355X (gfx950) EAGLE3 verify-and-accept library.
+ *
+ * Shared library: neuron-pytorch-native_amd/libnpn_spec_verify.so
+ *
+ * Conventions (all entry points):
+ *  - Plain device pointers, element counts and a HIP stream passed as void*
+ *    (NULL = the default stream). No torch types cross this boundary.
+ *  - bf16 tensors are passed as uint16_t* holding the raw bf16 bits; fp8 weights
+ *    as int8_t* holding OCP e4m3fn bytes.
+ *  - Outputs and workspaces are allocated by the caller; the library never
+ *    allocates device memory. Pointers must be 16-byte aligned.
+ *  - Every call validates shapes and pointers on the host, enqueues its kernels
+ *    on `stream` and returns an npn_status. No call synchronises the stream.
+ *  - Head dimension of the DeltaNet state is 128 (k and v); GQA head dim is 256
+ *    with a 64-dim partial RoPE, as in the reference models.
+ *  - Calls are re-entrant; concurrent calls on different streams must use
+ *    different workspaces.
+ */
+#ifndef NPN_SPEC_VERIFY_H
+#define NPN_SPEC_VERIFY_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum npn_status {
+  NPN_OK = 0,
+  NPN_ERR_NULL = 1,        /* a required pointer is NULL */
+  NPN_ERR_SHAPE = 2,       /* a size is out of the supported range or inconsistent */
+  NPN_ERR_ALIGN = 3,       /* a pointer is not 16-byte aligned */
+  NPN_ERR_WORKSPACE = 4,   /* workspace missing or smaller than the size query returned */
+  NPN_ERR_LAUNCH = 5,      /* the HIP runtime rejected a kernel launch */
+  NPN_ERR_VALUE = 6        /* an argument value is out of range (e.g. temperature) */
+} npn_status;
+
+/* Human-readable text for a status code (static storage). */
+const char* npn_status_string(int status);
+
+/* Library ABI version (major*100 + minor). */
+int npn_abi_version(void);
+
+/* ---------------------------------------------------------------------------
+ * Gated DeltaNet.
+ * Shapes: QKV = 2*Hk*128 + Hv*128; Hv % Hk == 0.
+ * ------------------------------------------------------------------------- */
+
+/* torch.ops.deltanet.full_batched -- replaces the op registered at
+ * contrib/qwen3.6-27b/kernels/deltanet_full_batched_ops.py:22-41 (and, with B=1,
+ * deltanet::full at contrib/qwen3.6-27b/kernels/deltanet_full_ops.py:7-25).
+ * One decode token per sequence:
+ *   state       [B*Hv*128, 128] f32     mixed_qkv [B*QKV] bf16
+ *   conv_state  [B*QKV, 3] bf16         conv_weight [QKV, 4] f32, conv_bias [QKV] f32
+ *   a_out,b_out [B*Hv] f32              z [B*Hv, 128] bf16
+ *   A_log, dt_bias [Hv] f32             norm_weight [128] f32
+ * Outputs: new_state [B*Hv*128,128] f32, new_conv_state [B*QKV,3] bf16,
+ *          out [B*Hv,128] bf16. */
+int npn_deltanet_full_batched(const float* state, const uint16_t* mixed_qkv,
+                              const uint16_t* conv_state, const float* conv_weight,
+                              const float* conv_bias, const float* a_out, const float* b_out,
+                              const uint16_t* z, const float* A_log, const float* dt_bias,
+                              const float* norm_weight, float* new_state,
+                              uint16_t* new_conv_state, uint16_t* out, int B, int k_heads,
+                              int v_heads, void* stream);
+
+/* torch.ops.deltanet.verify_batched -- new op (no reference counterpart; it runs
+ * the token step of deltanet_full_batched_ops.py:22-41 over T = K+1 verify
+ * tokens and keeps every intermediate state, the trajectory of
+ * contrib/qwen3.6-27b/kernels/tests/test_spec_verify_tensor_ops.py:47-51).
+ *   state        initial state. If state_index == NULL: [B, Hv, 128, 128] f32.
+ *                Otherwise a checkpoint buffer [B, state_T, Hv, 128, 128] and the
+ *                initial state of sequence b is checkpoint state_index[b]
+ *                (index-based rollback of the previous verify step, no copy).
+ *   mixed_qkv    [B, T, QKV] bf16   conv_state [B, QKV, 3] bf16
+ *   a_out, b_out [B, T, Hv] f32     z [B, T, Hv, 128] bf16
+ * Outputs: ckpt [B, T, Hv, 128, 128] f32 (state after each token),
+ *          out  [B, T, Hv, 128] bf16 (gated RMSNorm output per token).
+ * 1 <= T <= 16. */
+int npn_deltanet_verify(const float* state, const int32_t* state_index, int state_T,
+                        const uint16_t* mixed_qkv, const uint16_t* conv_state,
+                        const float* conv_weight, const float* conv_bias, const float* a_out,
+                        const float* b_out, const uint16_t* z, const float* A_log,
+                        const float* dt_bias, const float* norm_weight, float* ckpt,
+                        uint16_t* out, int B, int T, int k_heads, int v_heads, void* stream);
+
+/* torch.ops.deltanet.rollback -- new op: roll back to the accepted prefix
+ * (contrib/qwen3.6-27b/kernels/tests/test_deltanet_spec_verify_rollback.py:153-157).
+ *   accepted [B] int32 in [0, T-1] (number of accepted drafts).
+ *   state_out [B, Hv, 128, 128] f32 = ckpt[b, accepted[b]] (may be NULL to skip
+ *   the copy when the next verify uses state_index instead);
+ *   conv_state_out [B, QKV, 3] bf16 = last 3 columns of [conv_state || x_0..x_a].
+ * Out-of-range accepted values are clamped into [0, T-1] on the device. */
+int npn_deltanet_rollback(const float* ckpt, const uint16_t* mixed_qkv,
+                          const uint16_t* conv_state, const int32_t* accepted,
+                          float* state_out, uint16_t* conv_state_out, int B, int T,
+                          int k_heads, int v_heads, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * GQA attention tail. Head dim 256, partial RoPE on dims [0, 64).
+ * ------------------------------------------------------------------------- */
+
+/* torch.ops.gqa.tail -- replaces the op registered at
+ * contrib/qwen3.6-27b/kernels/gqa_tail_ops.py:14-26 (one kv head per call):
+ *   query, gate [B*Hq, 256] f32   q_norm [256] f32   cos, sin [64] f32
+ *   cached_k, cached_v [B*S, 256] f32   mask [S] f32 (1 valid / 0 masked)
+ * Output: out [B*Hq, 256] f32 = softmax(q'k/16 + (mask-1)*1e9) V * sigmoid(gate). */
+int npn_gqa_tail(const float* query, const float* gate, const float* q_norm, const float* cos,
+                 const float* sin, const float* cached_k, const float* cached_v,
+                 const float* mask, float* out, int B, int q_heads, int S, void* stream);
+
+/* Workspace bytes for npn_gqa_tail_verify with these sizes. */
+size_t npn_gqa_tail_verify_workspace_size(int B, int T, int q_heads, int kv_heads, int s_max);
+
+/* torch.ops.gqa.tail_verify -- new op: the gqa::tail math (gqa_tail_ops.py:14-26)
+ * for T verify tokens per sequence over a bf16 KV cache, split over KV chunks.
+ *   query, gate [B, T, Hq, 256] bf16   q_norm [256] f32
+ *   cos, sin    [B, T, 64] f32 (RoPE of each query row's position)
+ *   cache_k/v   [B, Hkv, s_max, 256] bf16, rows [0, kv_len[b]+T) valid
+ *   kv_len      [B] int32, cache rows before the T verify rows (kv_len+T <= s_max)
+ * Row (b,t,h) uses kv head h/(Hq/Hkv) and attends rows [0, kv_len[b]+t].
+ * Output: out [B, T, Hq, 256] bf16. Hq/Hkv * T <= 64. */
+int npn_gqa_tail_verify(const uint16_t* query, const uint16_t* gate, const float* q_norm,
+                        const float* cos, const float* sin, const uint16_t* cache_k,
+                        const uint16_t* cache_v, const int32_t* kv_len, uint16_t* out, int B,
+                        int T, int q_heads, int kv_heads, int s_max, void* workspace,
+                        size_t workspace_bytes, void* stream);
+
+/* torch.ops.gqa.kv_append -- new op: the k-side glue of _gqa_layer
+ * (contrib/qwen3.6-27b/static_decode.py:880-910) for T rows per sequence:
+ * cache_k[b, g, kv_len[b]+t] = bf16(rope(bf16(rms_norm_1p(key[b,t,g], k_norm))));
+ * cache_v[b, g, kv_len[b]+t] = value[b,t,g].
+ *   key, value [B, T, Hkv, 256] bf16; k_norm [256] f32; cos, sin [B, T, 64] f32. */
+int npn_gqa_kv_append(const uint16_t* key, const uint16_t* value, const float* k_norm,
+                      const float* cos, const float* sin, uint16_t* cache_k, uint16_t* cache_v,
+                      const int32_t* kv_len, int B, int T, int kv_heads, int s_max,
+                      void* stream);
+
+/* ---------------------------------------------------------------------------
+ * FP8 W8A16 GEMM.
+ * ------------------------------------------------------------------------- */
+
+/* Workspace bytes for npn_fp8_matmul with these sizes (0 if none is needed). */
+size_t npn_fp8_matmul_workspace_size(int M, int K, int N);
+
+/* torch.ops.fp8.matmul -- replaces the op registered at
+ * contrib/qwen3.6-27b/kernels/fp8_matmul_ops.py:14-21:
+ *   x [M, K] bf16, w [K, N] e4m3fn bytes (pre-transposed), scale [N] f32
+ *   out [M, N] bf16 = bf16((x . w) * scale), fp32 accumulation.
+ * K % 64 == 0, N % 64 == 0, 1 <= M <= 4096 (the reference caps M at 128,
+ * fp8_matmul.py:74). */
+int npn_fp8_matmul(const uint16_t* x, const int8_t* w, const float* scale, uint16_t* out, int M,
+                   int K, int N, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Acceptance. T = K+1 verify positions per sequence, vocabulary V.
+ * Outputs: accepted [B] int32 in [0, K]; out_ids [B, T] int64: accepted drafts,
+ * then the correction/bonus token, then -1.
+ * ------------------------------------------------------------------------- */
+
+/* Workspace bytes for the acceptance calls. */
+size_t npn_accept_workspace_size(int B, int K, int V);
+
+/* torch.ops.spec.accept_greedy -- new op. Greedy verify of the reference's
+ * on-device argmax (contrib/qwen3.6-27b/static_decode.py:1313): first-index
+ * tie-break, NaN counts as the maximum.
+ *   target_logits [B, K+1, V] f32, draft_ids [B, K] int64. */
+int npn_accept_greedy(const float* target_logits, const int64_t* draft_ids, int32_t* accepted,
+                      int64_t* out_ids, int B, int K, int V, void* workspace,
+                      size_t workspace_bytes, void* stream);
+
+/* torch.ops.spec.accept_rejection -- new op. Rejection sampling (Leviathan et
+ * al. 2023, Alg. 1) under the library's integer softmax contract (see the
+ * library design notes): bit-identical to its CPU restatement for the same
+ * logits and uniforms.
+ *   target_logits [B, K+1, V] f32, draft_logits [B, K, V] f32, draft_ids [B, K]
+ *   int64, u_accept [B, K] f32 in [0,1), u_sample [B] f32 in [0,1),
+ *   inv_temperature > 0 (logits are multiplied by it). */
+int npn_accept_rejection(const float* target_logits, const float* draft_logits,
+                         const int64_t* draft_ids, const float* u_accept,
+                         const float* u_sample, float inv_temperature, int32_t* accepted,
+                         int64_t* out_ids, int B, int K, int V, void* workspace,
+                         size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NPN_SPEC_VERIFY_H */

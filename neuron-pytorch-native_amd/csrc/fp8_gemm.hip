@@ -1,0 +1,250 @@
+// FP8 (OCP e4m3fn) W8A16 GEMM for gfx950: out[M,N] = bf16((x[M,K] . W[K,N]) * scale[N]).
+//
+// Semantics of the reference op fp8::matmul (contrib/qwen3.6-27b/kernels/fp8_matmul_ops.py:14-21,
+// kernel contrib/qwen3.6-27b/kernels/fp8_matmul.py:55-184): fp8 weight bytes pre-transposed
+// to [K, N] (N contiguous), bf16 activations, fp32 accumulation, per-output-channel scale
+// applied to the fp32 sum, then a bf16 cast.
+//
+// Mapping onto v_mfma_f32_16x16x32_bf16 (A = x tile 16 rows x 32 k, B = W tile 32 k x 16 n):
+// the B operand wants 8 consecutive k of one column per lane, but [K, N] stores a column
+// with stride N. Each lane therefore loads one dword = 4 adjacent columns from each of its
+// 8 k rows (W[k0 + 8G + j][n0 + 4i .. 4i+3], j = 0..7; 64-byte runs per row across the 16
+// lanes of a group), transposes the 8x4 byte block in registers with v_perm_b32, and
+// dequantises each column's 8 bytes to bf16 with v_cvt_scalef32_pk_bf16_fp8 (exact: every
+// e4m3fn value is a bf16 value). Column ct of the lane feeds MFMA number ct, whose output
+// column i is global column n0 + 4i + ct: a 64-column wave tile is 4 MFMAs with their
+// columns interleaved, and the epilogue writes 4 adjacent bf16 per lane and row.
+//
+// Work split: workgroup = 8 waves on one 64-column tile; the waves split K, their fp32
+// partials are summed in a fixed tree through LDS (deterministic), scaled and stored.
+// For narrow N, K is also split across workgroups (split_k); partials then go through an
+// fp32 workspace and a fixed-order reduction kernel. M is covered in passes of 16*MT rows.
+#include "npn_common.h"
+
+namespace {
+
+constexpr int NW = 64;      // columns per workgroup tile
+constexpr int KSTEP = 32;   // k per MFMA
+constexpr int WAVES = 8;
+
+typedef __bf16 bf16x8 __attribute__((__vector_size__(8 * sizeof(__bf16))));
+typedef float f32x4 __attribute__((__vector_size__(4 * sizeof(float))));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((__vector_size__(2 * sizeof(__bf16))));
+
+// Bytes 0-1 (HI = false) or 2-3 (HI = true) of w -> two bf16 (OCP e4m3fn decode, scale 1).
+template <bool HI>
+__device__ __forceinline__ uint32_t fp8x2_to_bf16x2(uint32_t w) {
+  const bf16x2 v = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, HI);
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// d[0..7]: byte b of d[j] = W[k0 + 8G + j][n0 + 4i + b]. Returns, for each column b, the
+// 8 k-values as a bf16x8 MFMA B operand.
+__device__ __forceinline__ void transpose_dequant(const uint32_t (&d)[8], bf16x8 (&bop)[4]) {
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {  // k rows 0-3, then 4-7
+    const uint32_t d0 = d[4 * h], d1 = d[4 * h + 1], d2 = d[4 * h + 2], d3 = d[4 * h + 3];
+    const uint32_t t0 = __builtin_amdgcn_perm(d1, d0, 0x05010400u);  // d0[0] d1[0] d0[1] d1[1]
+    const uint32_t t1 = __builtin_amdgcn_perm(d1, d0, 0x07030602u);  // d0[2] d1[2] d0[3] d1[3]
+    const uint32_t u0 = __builtin_amdgcn_perm(d3, d2, 0x05010400u);
+    const uint32_t u1 = __builtin_amdgcn_perm(d3, d2, 0x07030602u);
+    const uint32_t e[4] = {
+        __builtin_amdgcn_perm(u0, t0, 0x05040100u),  // column 0: k rows 4h..4h+3
+        __builtin_amdgcn_perm(u0, t0, 0x07060302u),  // column 1
+        __builtin_amdgcn_perm(u1, t1, 0x05040100u),  // column 2
+        __builtin_amdgcn_perm(u1, t1, 0x07060302u),  // column 3
+    };
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) {
+      u32x4 cur = __builtin_bit_cast(u32x4, bop[ct]);
+      cur[2 * h] = fp8x2_to_bf16x2<false>(e[ct]);
+      cur[2 * h + 1] = fp8x2_to_bf16x2<true>(e[ct]);
+      bop[ct] = __builtin_bit_cast(bf16x8, cur);
+    }
+  }
+}
+
+struct GemmArgs {
+  const uint16_t* x;
+  const uint8_t* w;
+  const float* scale;
+  uint16_t* out;     // used when split_k == 1
+  float* partial;    // [split_k][M][N] when split_k > 1
+  int M, K, N, split_k;
+};
+
+template <int MT>
+__global__ __launch_bounds__(WAVES * 64) void fp8_gemm_kernel(GemmArgs a) {
+  constexpr int ROWS = 16 * MT;
+  const int n0 = blockIdx.x * NW;
+  const int sk = blockIdx.y;
+  const int m_base = blockIdx.z * ROWS;
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int i = lane & 15, G = lane >> 4;
+
+  // k steps of this wave: split evenly over split_k * WAVES workers.
+  const int nks = a.K / KSTEP;
+  const int worker = sk * WAVES + w;
+  const int workers = a.split_k * WAVES;
+  const int ks_lo = (int)(((long)nks * worker) / workers);
+  const int ks_hi = (int)(((long)nks * (worker + 1)) / workers);
+
+  f32x4 acc[MT][4];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) acc[mt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const uint8_t* wcol = a.w + n0 + 4 * i;
+  for (int ks = ks_lo; ks < ks_hi; ++ks) {
+    const int k0 = ks * KSTEP + 8 * G;
+    uint32_t d[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      d[j] = *reinterpret_cast<const uint32_t*>(wcol + (size_t)(k0 + j) * a.N);
+    bf16x8 aop[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = m_base + 16 * mt + i;
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (m < a.M) v = *reinterpret_cast<const u32x4*>(a.x + (size_t)m * a.K + k0);
+      aop[mt] = __builtin_bit_cast(bf16x8, v);
+    }
+    bf16x8 bop[4];
+    transpose_dequant(d, bop);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct)
+        acc[mt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop[mt], bop[ct], acc[mt][ct], 0, 0, 0);
+  }
+
+  // Deterministic tree over the 8 waves: (w, w+4), (w, w+2), (w, w+1).
+  __shared__ __attribute__((aligned(16))) float red[4][ROWS * NW];
+  auto slot_off = [&](int mt, int ct, int r) { return (16 * mt + 4 * G + r) * NW + 4 * i + ct; };
+#pragma unroll
+  for (int half = 4; half >= 1; half >>= 1) {
+    if (w >= half && w < 2 * half) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) red[w - half][slot_off(mt, ct, r)] = acc[mt][ct][r];
+    }
+    __syncthreads();
+    if (w < half) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[mt][ct][r] += red[w][slot_off(mt, ct, r)];
+    }
+    __syncthreads();
+  }
+  if (w != 0) return;
+
+  // Wave 0 holds the tile sum: lane (i, G) has rows 16mt + 4G + r, columns n0 + 4i + ct.
+  if (a.split_k == 1) {
+    float sc[4];
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) sc[ct] = a.scale[n0 + 4 * i + ct];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = m_base + 16 * mt + 4 * G + r;
+        if (m >= a.M) continue;
+        uint32_t lo = npn::f32_to_bf16(acc[mt][0][r] * sc[0]) |
+                      ((uint32_t)npn::f32_to_bf16(acc[mt][1][r] * sc[1]) << 16);
+        uint32_t hi = npn::f32_to_bf16(acc[mt][2][r] * sc[2]) |
+                      ((uint32_t)npn::f32_to_bf16(acc[mt][3][r] * sc[3]) << 16);
+        *reinterpret_cast<uint2*>(a.out + (size_t)m * a.N + n0 + 4 * i) = make_uint2(lo, hi);
+      }
+  } else {
+    float* part = a.partial + (size_t)sk * a.M * a.N;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = m_base + 16 * mt + 4 * G + r;
+        if (m >= a.M) continue;
+        *reinterpret_cast<float4*>(part + (size_t)m * a.N + n0 + 4 * i) =
+            make_float4(acc[mt][0][r], acc[mt][1][r], acc[mt][2][r], acc[mt][3][r]);
+      }
+  }
+}
+
+// out = bf16(scale * sum_s partial[s]), summed in order s = 0..split_k-1.
+__global__ void fp8_splitk_reduce_kernel(const float* __restrict__ partial,
+                                         const float* __restrict__ scale,
+                                         uint16_t* __restrict__ out, int M, int N, int split_k) {
+  const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const size_t total = (size_t)M * N;
+  if (idx >= total) return;
+  float s = 0.f;
+  for (int k = 0; k < split_k; ++k) s += partial[(size_t)k * total + idx];
+  out[idx] = npn::f32_to_bf16(s * scale[idx % N]);
+}
+
+struct GemmPlan {
+  int mt, passes, split_k;
+  size_t ws;
+};
+
+GemmPlan plan(int M, int K, int N) {
+  GemmPlan p{};
+  const int mtiles = (M + 15) / 16;
+  p.mt = mtiles >= 8 ? 8 : (mtiles >= 4 ? 4 : (mtiles >= 2 ? 2 : 1));
+  p.passes = (M + 16 * p.mt - 1) / (16 * p.mt);
+  const int tiles = (N / NW) * p.passes;
+  const int nks = K / KSTEP;
+  p.split_k = 1;
+  while (tiles * p.split_k < 256 && p.split_k < 4 && nks >= 2 * p.split_k * 2 * WAVES)
+    p.split_k *= 2;
+  p.ws = p.split_k > 1 ? (size_t)p.split_k * M * N * sizeof(float) : 0;
+  return p;
+}
+
+bool shape_ok(int M, int K, int N) {
+  return M >= 1 && M <= 4096 && K >= 64 && K % 64 == 0 && N >= 64 && N % 64 == 0 &&
+         (long)K * N < (1L << 40);
+}
+
+}  // namespace
+
+extern "C" size_t npn_fp8_matmul_workspace_size(int M, int K, int N) {
+  if (!shape_ok(M, K, N)) return 0;
+  return plan(M, K, N).ws;
+}
+
+extern "C" int npn_fp8_matmul(const uint16_t* x, const int8_t* w, const float* scale,
+                              uint16_t* out, int M, int K, int N, void* workspace,
+                              size_t workspace_bytes, void* stream) {
+  NPN_REQUIRE(x && w && scale && out, NPN_ERR_NULL);
+  NPN_REQUIRE(shape_ok(M, K, N), NPN_ERR_SHAPE);
+  NPN_REQUIRE(NPN_ALIGNED16(x) && NPN_ALIGNED16(w) && NPN_ALIGNED16(out), NPN_ERR_ALIGN);
+  const GemmPlan p = plan(M, K, N);
+  if (p.split_k > 1) {
+    NPN_REQUIRE(workspace != nullptr && workspace_bytes >= p.ws, NPN_ERR_WORKSPACE);
+    NPN_REQUIRE(NPN_ALIGNED16(workspace), NPN_ERR_ALIGN);
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  GemmArgs ga{x, reinterpret_cast<const uint8_t*>(w), scale, out,
+              static_cast<float*>(workspace), M, K, N, p.split_k};
+  const dim3 grid(N / NW, p.split_k, p.passes);
+  switch (p.mt) {
+    case 1: hipLaunchKernelGGL(fp8_gemm_kernel<1>, grid, dim3(WAVES * 64), 0, s, ga); break;
+    case 2: hipLaunchKernelGGL(fp8_gemm_kernel<2>, grid, dim3(WAVES * 64), 0, s, ga); break;
+    case 4: hipLaunchKernelGGL(fp8_gemm_kernel<4>, grid, dim3(WAVES * 64), 0, s, ga); break;
+    default: hipLaunchKernelGGL(fp8_gemm_kernel<8>, grid, dim3(WAVES * 64), 0, s, ga); break;
+  }
+  if (p.split_k > 1) {
+    const size_t total = (size_t)M * N;
+    hipLaunchKernelGGL(fp8_splitk_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256),
+                       0, s, static_cast<const float*>(workspace), scale, out, M, N, p.split_k);
+  }
+  return npn_launch_status();
+}

@@ -1,0 +1,50 @@
+"""torch.ops.fp8.matmul on gfx950 -- drop-in for the op registered at
+contrib/qwen3.6-27b/kernels/fp8_matmul_ops.py:14-21 (same name, schema and layouts):
+
+  fp8::matmul(x [B, K] bf16, w_fp8_T_i8 [K, N] int8 (OCP e4m3fn bytes), scale [N, 1] f32)
+      -> [B, N] bf16 = bf16((x . w) * scale), fp32 accumulation
+
+The reference kernel caps B at 128 (contrib/qwen3.6-27b/kernels/fp8_matmul.py:74); this
+one takes 1 <= B <= 4096 so the verify step can pass all B*T rows in one call.
+K and N must be multiples of 64.
+"""
+import torch
+
+from npn_native import call, query, require, stream_of
+
+
+@torch.library.custom_op("fp8::matmul", mutates_args=(), device_types="cuda")
+def fp8_matmul(
+    x: torch.Tensor,           # [B, K] bf16
+    w_fp8_T_i8: torch.Tensor,  # [K, N] int8 (fp8 bytes; reinterpreted in kernel)
+    scale: torch.Tensor,       # [N, 1] f32 (per-output-channel dequant scale)
+) -> torch.Tensor:
+    """Returns [B, N] bf16 = x @ w.T."""
+    M, K = x.shape
+    Kw, N = w_fp8_T_i8.shape
+    if Kw != K:
+        raise RuntimeError(f"x has K={K} but the weight has K={Kw}")
+    require(x, "x", torch.bfloat16, shape=(M, K))
+    if w_fp8_T_i8.dtype not in (torch.int8, torch.uint8, torch.float8_e4m3fn):
+        raise TypeError(f"w_fp8_T_i8 must hold fp8 bytes, got {w_fp8_T_i8.dtype}")
+    require(w_fp8_T_i8, "w_fp8_T_i8", w_fp8_T_i8.dtype, shape=(K, N))
+    require(scale, "scale", torch.float32, numel=N)
+    n_ws = query("npn_fp8_matmul_workspace_size", M, K, N)
+    if n_ws == 0 and not (K % 64 == 0 and N % 64 == 0 and 1 <= M <= 4096):
+        raise RuntimeError(f"unsupported fp8 matmul shape M={M} K={K} N={N}")
+    ws = torch.empty(max(n_ws, 1), dtype=torch.uint8, device=x.device)
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    call("npn_fp8_matmul", x, w_fp8_T_i8, scale, out, M, K, N, ws, n_ws, stream_of(x))
+    return out
+
+
+@fp8_matmul.register_fake
+def _(x, w_fp8_T_i8, scale):
+    return x.new_empty((x.shape[0], w_fp8_T_i8.shape[1]))
+
+
+def fp8_linear(x, w_fp8_T_i8, scale):
+    """x [..., K] bf16 -> [..., N], as the reference's fp8_linear
+    (contrib/qwen3.6-27b/static_decode.py:307-319)."""
+    flat = x.reshape(-1, x.shape[-1])
+    return torch.ops.fp8.matmul(flat, w_fp8_T_i8, scale).reshape(*x.shape[:-1], -1)

@@ -1,0 +1,18 @@
+"""Import every op module once, registering all torch.ops of the library:
+
+  torch.ops.deltanet.{full, full_batched, verify_batched, verify_from_ckpt, rollback,
+                      conv_rollback}
+  torch.ops.gqa.{tail, tail_verify, kv_append}
+  torch.ops.fp8.matmul
+  torch.ops.spec.{accept_greedy, accept_rejection}
+
+(The reference registers its ops by importing each *_ops module,
+contrib/qwen3.6-27b/static_decode.py:29-34; importing the modules one by one works
+the same way here.)
+"""
+import deltanet_full_ops  # noqa: F401
+import deltanet_full_batched_ops  # noqa: F401
+import deltanet_verify_ops  # noqa: F401
+import gqa_tail_ops  # noqa: F401
+import fp8_matmul_ops  # noqa: F401
+import spec_accept_ops  # noqa: F401

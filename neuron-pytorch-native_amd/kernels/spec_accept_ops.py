@@ -1,0 +1,77 @@
+"""Speculative-decode acceptance ops on gfx950 (new ops; the reference's sampler lives in
+an un-vendored vLLM-Neuron fork and its on-device greedy path is a plain argmax,
+contrib/qwen3.6-27b/static_decode.py:1313).
+
+  spec::accept_greedy(target_logits [B, K+1, V] f32, draft_ids [B, K] int64)
+      -> (accepted [B] int32, out_ids [B, K+1] int64)
+  spec::accept_rejection(target_logits [B, K+1, V] f32, draft_logits [B, K, V] f32,
+                         draft_ids [B, K] int64, u_accept [B, K] f32, u_sample [B] f32,
+                         inv_temperature: float = 1.0)
+      -> (accepted [B] int32, out_ids [B, K+1] int64)
+
+accepted[b] is the number of accepted drafts (0..K); out_ids[b] holds those drafts,
+then the correction (or bonus) token, then -1. Rejection sampling follows Leviathan
+et al. 2023 (Alg. 1) under the library's integer softmax contract, so its decisions
+are bit-identical to the CPU restatement for the same logits and uniforms.
+"""
+import torch
+
+from npn_native import call, query, require, stream_of
+
+
+def _workspace(B, K, V, device):
+    n = query("npn_accept_workspace_size", B, K, V)
+    if n == 0:
+        raise RuntimeError(f"unsupported acceptance shape B={B} K={K} V={V}")
+    return torch.empty(n, dtype=torch.uint8, device=device)
+
+
+@torch.library.custom_op("spec::accept_greedy", mutates_args=(), device_types="cuda")
+def accept_greedy(target_logits: torch.Tensor,
+                  draft_ids: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    B, T, V = target_logits.shape
+    K = T - 1
+    require(target_logits, "target_logits", torch.float32, shape=(B, T, V))
+    require(draft_ids, "draft_ids", torch.int64, shape=(B, K))
+    ws = _workspace(B, K, V, target_logits.device)
+    accepted = torch.empty(B, dtype=torch.int32, device=target_logits.device)
+    out_ids = torch.empty((B, T), dtype=torch.int64, device=target_logits.device)
+    call("npn_accept_greedy", target_logits, draft_ids, accepted, out_ids, B, K, V, ws,
+         ws.numel(), stream_of(target_logits))
+    return accepted, out_ids
+
+
+@accept_greedy.register_fake
+def _(target_logits, draft_ids):
+    B, T, _ = target_logits.shape
+    return (target_logits.new_empty((B,), dtype=torch.int32),
+            target_logits.new_empty((B, T), dtype=torch.int64))
+
+
+@torch.library.custom_op("spec::accept_rejection", mutates_args=(), device_types="cuda")
+def accept_rejection(target_logits: torch.Tensor, draft_logits: torch.Tensor,
+                     draft_ids: torch.Tensor, u_accept: torch.Tensor, u_sample: torch.Tensor,
+                     inv_temperature: float = 1.0) -> tuple[torch.Tensor, torch.Tensor]:
+    B, T, V = target_logits.shape
+    K = T - 1
+    require(target_logits, "target_logits", torch.float32, shape=(B, T, V))
+    require(draft_logits, "draft_logits", torch.float32, shape=(B, K, V))
+    require(draft_ids, "draft_ids", torch.int64, shape=(B, K))
+    require(u_accept, "u_accept", torch.float32, shape=(B, K))
+    require(u_sample, "u_sample", torch.float32, numel=B)
+    if not inv_temperature > 0.0:
+        raise ValueError("inv_temperature must be > 0")
+    ws = _workspace(B, K, V, target_logits.device)
+    accepted = torch.empty(B, dtype=torch.int32, device=target_logits.device)
+    out_ids = torch.empty((B, T), dtype=torch.int64, device=target_logits.device)
+    call("npn_accept_rejection", target_logits, draft_logits, draft_ids, u_accept, u_sample,
+         float(inv_temperature), accepted, out_ids, B, K, V, ws, ws.numel(),
+         stream_of(target_logits))
+    return accepted, out_ids
+
+
+@accept_rejection.register_fake
+def _(target_logits, draft_logits, draft_ids, u_accept, u_sample, inv_temperature=1.0):
+    B, T, _ = target_logits.shape
+    return (target_logits.new_empty((B,), dtype=torch.int32),
+            target_logits.new_empty((B, T), dtype=torch.int64))

@@ -1,0 +1,158 @@
+"""Acceptance oracle: greedy and rejection sampling (test infrastructure only).
+
+Greedy (pinned against the reference):
+- per position argmax with first-index (lowest id) tie-breaking, exactly
+  ``logits.argmax(-1)`` (``contrib/qwen3.6-27b/static_decode.py:1313``) and the
+  vocab-sharded exact top-1 (``contrib/qwen3.6-35b-a3b/static_decode_35b.py:1532-1570``,
+  CPU check ``contrib/qwen3.6-35b-a3b/kernels/tests/test_decode_sharded_lm_cpu.py:7-46``).
+  NaN counts as the maximum (first NaN wins), as torch.argmax does.
+- accepted a = number of leading drafts equal to the target argmax of the
+  position before them; emitted tokens = argmax(t[0..a]).
+
+Rejection sampling (textbook: Leviathan et al. 2023, Alg. 1; Chen et al. 2023).
+The reference's sampler lives in an un-vendored vLLM-Neuron fork (pinned at
+65ef8b7 on vLLM 0.21, named in ``contrib/qwen3.6-35b-a3b/VLLM_NEURON_ASSESSMENT.md:7-10``);
+no reference test or vector covers it, so against the reference it is
+"parity unpinned". It is pinned here against the mathematics instead:
+exact enumeration of the output distribution on tiny vocabularies, a chi-square
+test that emitted tokens follow p, and the special cases p == q (always accept)
+and q(x) > 0 = p(x) (always reject, residual = p restricted to p > q)
+(tests/test_oracle_accept.py).
+
+Integer softmax contract (shared bit-for-bit with ``csrc/spec_accept.hip``):
+- s_v = t_v * inv_temp (fp32 multiply), m = max_v s_v, x_v = s_v - m (fp32).
+- E_v = floor(2^32 * exp_c(x_v)) as an integer, with exp_c the fp32
+  Cody-Waite reduction + degree-7 Taylor polynomial below, evaluated with
+  separately rounded fp32 multiplies and adds only (no fused multiply-add),
+  so every step is one IEEE-754 operation that CPU and GPU round identically.
+- Z = sum_v E_v in exact integer arithmetic (order-independent).
+- p(v) = E^p_v / Z_p, q(v) = E^q_v / Z_q. Uniforms u are read as
+  U = floor(u * 2^24).
+- Accept draft x at position i iff U * E^q_x * Z_p <= 2^24 * E^p_x * Z_q
+  (integers up to 2^107).
+- At the first rejection sample from R_v = max(0, E^p_v Z_q - E^q_v Z_p); if all
+  K drafts are accepted sample the bonus from R_v = E^p_v of row K. The token is
+  the smallest v with 2^24 * sum_{w<=v} R_w > U_s * sum_w R_w.
+"""
+import numpy as np
+
+# ---- exp_c: Cody-Waite range reduction + Taylor polynomial, fp32, no FMA -------------
+
+_F = np.float32
+L2E = _F(1.4426950408889634)                     # log2(e) rounded to fp32
+_LN2 = 0.6931471805599453
+LN2_HI = np.array([_LN2], np.float32).view(np.uint32) & np.uint32(0xFFFFF000)
+LN2_HI = LN2_HI.view(np.float32)[0]              # ln2 with the low 12 mantissa bits cleared
+LN2_LO = _F(_LN2 - float(LN2_HI))                # remainder, so n*LN2_HI is exact for |n| < 2^12
+# Taylor coefficients 1/k!, k = 7..2 (1/1! and 1/0! are the final two Horner steps).
+TAYLOR = [_F(1.0 / 5040.0), _F(1.0 / 720.0), _F(1.0 / 120.0), _F(1.0 / 24.0), _F(1.0 / 6.0), _F(0.5)]
+X_MIN = _F(-32.0)                                # below this 2^32*exp(x) < 1: E = 0
+FIX_BITS = 32                                    # E = floor(2^32 * exp(x))
+U_BITS = 24                                      # U = floor(u * 2^24)
+
+
+def expfix(x):
+    """E = floor(2^32 * exp_c(x)) for fp32 x <= 0, as uint64 (elementwise).
+
+    Steps (all fp32, one rounding each):
+      kf = floor(x * L2E + 0.5); r = (x - kf*LN2_HI) - kf*LN2_LO
+      p  = ((((((c7 r + c6) r + c5) r + c4) r + c3) r + c2) r + 1) r + 1
+      E  = mantissa(p) shifted by exponent(p) + kf + 32 - 150 (integer shift, floor)
+    """
+    x = np.asarray(x, np.float32)
+    x = np.where(x < X_MIN, X_MIN, x).astype(np.float32)
+    kf = np.floor((x * L2E).astype(np.float32) + _F(0.5)).astype(np.float32)
+    r = (x - (kf * LN2_HI).astype(np.float32)).astype(np.float32)
+    r = (r - (kf * LN2_LO).astype(np.float32)).astype(np.float32)
+    p = np.full_like(r, TAYLOR[0])
+    for c in TAYLOR[1:]:
+        p = ((p * r).astype(np.float32) + c).astype(np.float32)
+    p = ((p * r).astype(np.float32) + _F(1.0)).astype(np.float32)
+    p = ((p * r).astype(np.float32) + _F(1.0)).astype(np.float32)
+    bits = p.view(np.uint32).astype(np.int64)
+    e = (bits >> 23) & 0xFF
+    m = (bits & 0x7FFFFF) | 0x800000
+    shift = e + kf.astype(np.int64) - 118                           # (e-127-23) + kf + 32
+    left = np.where(shift > 0, shift, 0)
+    right = np.where(shift < 0, np.minimum(-shift, 63), 0)
+    out = np.where(shift >= 0, m << left, m >> right).astype(np.uint64)
+    return np.where(x <= X_MIN, np.uint64(0), out).astype(np.uint64)
+
+
+def row_weights(logits_row, inv_temp=1.0):
+    """(E [V] uint64, Z python int, m fp32) for one logits row under the contract."""
+    s = (np.asarray(logits_row, np.float32) * _F(inv_temp)).astype(np.float32)
+    m = s.max()
+    E = expfix((s - m).astype(np.float32))
+    return E, int(E.sum(dtype=np.uint64)), m
+
+
+def uniform_fix(u):
+    """U = floor(u * 2^24) for fp32 u in [0, 1)."""
+    return int((np.float32(u) * _F(1 << U_BITS)).astype(np.float32).astype(np.uint32))
+
+
+def _inverse_cdf(weights, U):
+    """Smallest v with 2^24 * cumsum(weights)[v] > U * sum(weights); weights are python ints."""
+    total = sum(weights)
+    target = U * total
+    c = 0
+    for v, w in enumerate(weights):
+        c += w
+        if (c << U_BITS) > target:
+            return v
+    raise AssertionError("inverse CDF found no token (all-zero weights)")
+
+
+def accept_rejection(target, draft, draft_ids, u_accept, u_sample, inv_temp=1.0):
+    """target [B, K+1, V] f32, draft [B, K, V] f32, draft_ids [B, K] int,
+    u_accept [B, K] f32, u_sample [B] f32 -> (accepted int32 [B], out_ids int64 [B, K+1]).
+    out_ids[b, :a] = drafts, out_ids[b, a] = residual/bonus sample, rest = -1."""
+    target = np.asarray(target, np.float32)
+    draft = np.asarray(draft, np.float32)
+    B, T, V = target.shape
+    K = T - 1
+    accepted = np.zeros(B, np.int32)
+    out = np.full((B, T), -1, np.int64)
+    for b in range(B):
+        a = K
+        for i in range(K):
+            Ep, Zp, _ = row_weights(target[b, i], inv_temp)
+            Eq, Zq, _ = row_weights(draft[b, i], inv_temp)
+            x = int(draft_ids[b, i])
+            U = uniform_fix(u_accept[b, i])
+            if U * int(Eq[x]) * Zp > (int(Ep[x]) * Zq << U_BITS):
+                a = i
+                break
+        accepted[b] = a
+        out[b, :a] = np.asarray(draft_ids[b, :a], np.int64)
+        Us = uniform_fix(u_sample[b])
+        if a < K:
+            Ep, Zp, _ = row_weights(target[b, a], inv_temp)
+            Eq, Zq, _ = row_weights(draft[b, a], inv_temp)
+            R = [max(0, int(ep) * Zq - int(eq) * Zp) for ep, eq in zip(Ep.tolist(), Eq.tolist())]
+        else:
+            Ep, _, _ = row_weights(target[b, K], inv_temp)
+            R = [int(e) for e in Ep.tolist()]
+        out[b, a] = _inverse_cdf(R, Us)
+    return accepted, out
+
+
+def argmax_first(logits):
+    """argmax over the last axis, first index on ties, NaN counts as maximum."""
+    return np.argmax(np.asarray(logits, np.float32), axis=-1).astype(np.int64)
+
+
+def accept_greedy(target, draft_ids):
+    """target [B, K+1, V] f32, draft_ids [B, K] -> (accepted int32 [B], out_ids int64 [B, K+1])."""
+    tid = argmax_first(target)                                          # [B, K+1]
+    B, T = tid.shape
+    K = T - 1
+    d = np.asarray(draft_ids, np.int64)
+    match = d == tid[:, :K]
+    accepted = np.where(match.all(axis=1), K, np.argmin(match, axis=1)).astype(np.int32)
+    out = np.full((B, T), -1, np.int64)
+    for b in range(B):
+        a = int(accepted[b])
+        out[b, :a + 1] = tid[b, :a + 1]
+    return accepted, out

@@ -1,0 +1,96 @@
+"""GPU parity of spec::accept_greedy and spec::accept_rejection against the oracle
+(oracle/accept.py): accepted lengths and token ids must be bit-exact.
+
+Greedy: the tie and ownership cases of contrib/qwen3.6-35b-a3b/kernels/tests/
+test_decode_sharded_lm_cpu.py:29-46 (forced winners, equal maxima inside and across
+8192-wide chunks, all-zero rows) plus NaN rows; the single-layer workload (5 positions,
+V = 32000, draft = argmax with p = 0.5).
+Rejection: the verify workload's distributions (V = 151936, draft logits 0.8 t + 0.6 eps)
+and small vocabularies where rejection and residual sampling happen often.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import accept as oa
+
+pytestmark = pytest.mark.gpu
+
+
+def _greedy(ops, target, draft):
+    acc, out = ops.spec.accept_greedy(target.cuda(), draft.cuda())
+    torch.cuda.synchronize()
+    return acc.cpu().numpy(), out.cpu().numpy()
+
+
+def test_greedy_single_layer_workload(ops):
+    g = torch.Generator().manual_seed(0)
+    target = torch.randn(1, 5, 32000, generator=g)
+    am = target.argmax(-1)[0, :4]
+    coin = torch.rand(4, generator=g) < 0.5
+    rnd = torch.randint(0, 32000, (4,), generator=g)
+    draft = torch.where(coin, am, rnd).reshape(1, 4)
+    acc, out = _greedy(ops, target, draft)
+    racc, rout = oa.accept_greedy(target.numpy(), draft.numpy())
+    assert np.array_equal(acc, racc) and np.array_equal(out, rout)
+
+
+def test_greedy_ties_nan_and_chunk_edges(ops):
+    B, T, V = 12, 3, 40000
+    g = torch.Generator().manual_seed(20260717)
+    target = torch.randn(B, T, V, generator=g)
+    for r in range(8):
+        target[r, 0, r * 4096 + 11] = 100 + r           # winners in different chunks
+    target[8, 0, 7] = 200; target[8, 0, 13] = 200        # tie inside a chunk
+    target[9, 0, 63] = 300; target[9, 0, 8192 + 5] = 300  # tie across chunks
+    target[9, 1, 8191] = 50; target[9, 1, 8192] = 50    # tie at the chunk edge
+    target[10] = 0                                        # all-zero rows
+    target[11, 0, 9000] = float("nan")
+    target[11, 0, 30000] = float("nan")                   # first NaN wins (torch.argmax)
+    tid = target.argmax(-1)
+    draft = tid[:, :T - 1].clone()
+    draft[3, 1] = (draft[3, 1] + 1) % V                   # one mismatch
+    acc, out = _greedy(ops, target, draft)
+    racc, rout = oa.accept_greedy(target.numpy(), draft.numpy())
+    assert np.array_equal(out[:, 0], tid[:, 0].numpy())
+    assert np.array_equal(acc, racc) and np.array_equal(out, rout)
+
+
+def _rejection_inputs(B, K, V, seed, rho=0.8):
+    g = torch.Generator().manual_seed(seed)
+    target = torch.randn(B, K + 1, V, generator=g)
+    draft = rho * target[:, :K] + (1 - rho * rho) ** 0.5 * torch.randn(B, K, V, generator=g)
+    probs = torch.softmax(draft, -1).reshape(B * K, V)
+    ids = torch.multinomial(probs, 1, generator=g).reshape(B, K)
+    u = torch.rand(B, K, generator=g)
+    us = torch.rand(B, generator=g)
+    return target.contiguous(), draft.contiguous(), ids, u, us
+
+
+def _rejection(ops, target, draft, ids, u, us, inv_t=1.0):
+    acc, out = ops.spec.accept_rejection(target.cuda(), draft.cuda(), ids.cuda(), u.cuda(),
+                                         us.cuda(), inv_t)
+    torch.cuda.synchronize()
+    return acc.cpu().numpy(), out.cpu().numpy()
+
+
+@pytest.mark.parametrize("B,K,V,seed,inv_t", [
+    (4, 7, 151936, 0, 1.0),
+    (16, 7, 1000, 1, 1.0),
+    (8, 3, 17, 2, 1.0),
+    (8, 7, 50000, 3, 0.7),
+])
+def test_rejection_bit_exact(ops, B, K, V, seed, inv_t):
+    target, draft, ids, u, us = _rejection_inputs(B, K, V, seed)
+    acc, out = _rejection(ops, target, draft, ids, u, us, inv_t)
+    racc, rout = oa.accept_rejection(target.numpy(), draft.numpy(), ids.numpy(), u.numpy(),
+                                     us.numpy(), inv_t)
+    assert np.array_equal(acc, racc), (acc, racc)
+    assert np.array_equal(out, rout)
+
+
+def test_rejection_equal_distributions_always_accept(ops):
+    target, _, ids, u, us = _rejection_inputs(6, 5, 3000, 9)
+    acc, out = _rejection(ops, target, target[:, :5].contiguous(), ids, u, us)
+    assert (acc == 5).all()
+    assert np.array_equal(out[:, :5], ids.numpy())

@@ -1,0 +1,140 @@
+"""GPU parity of the gated-DeltaNet ops against the oracle (oracle/deltanet.py).
+
+Covers deltanet::full / full_batched (the reference's per-rank decode shapes, seed 11 as in
+contrib/qwen3.6-27b/kernels/tests/test_deltanet_full.py:58-73), deltanet::verify_batched at
+the single-layer workload (B=1, T=5, 4/4 heads) and full width (16/48 heads, T=8), index-based
+and copy-based rollback, and a B=32 full-size run checked on sampled sequences.
+Bar: 2e-3 relative (tests/_util.py); conv windows are data movement and must be bit-exact.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import deltanet as od
+from _util import (assert_rel_close, bits, deltanet_flat_device, deltanet_inputs,
+                   deltanet_oracle_args, BF16_U)
+
+pytestmark = pytest.mark.gpu
+
+
+def _verify_gpu(ops, d):
+    f = deltanet_flat_device(d)
+    ckpt, out = ops.deltanet.verify_batched(
+        f["state"], f["mixed_qkv"], f["conv_state"], f["conv_weight"], f["conv_bias"],
+        f["a_out"], f["b_out"], f["z"], f["A_log"], f["dt_bias"], f["norm_weight"])
+    torch.cuda.synchronize()
+    B, Hv, D, _ = d["state"].shape
+    T = d["mixed_qkv"].shape[1]
+    return (ckpt.cpu().double().numpy().reshape(B, T, Hv, D, D),
+            out.float().cpu().double().numpy().reshape(B, T, Hv, D))
+
+
+@pytest.mark.parametrize("B,T,Hk,Hv,gates", [
+    (1, 5, 4, 4, "config0"),     # single layer verify + greedy workload
+    (2, 8, 16, 48, "random"),    # full width, K=7
+    (3, 4, 4, 12, "random"),     # reference per-rank heads (TP=4 share)
+    (2, 16, 2, 6, "random"),     # longest verify block supported
+    (4, 1, 1, 3, "random"),
+])
+def test_verify_matches_oracle(ops, B, T, Hk, Hv, gates):
+    d = deltanet_inputs(B, T, Hk, Hv, seed=11 + B + T, gates=gates)
+    ck, out = od.deltanet_verify(*deltanet_oracle_args(d), Hk, Hv)
+    gck, gout = _verify_gpu(ops, d)
+    assert_rel_close(gck, ck, name="ckpt")
+    assert_rel_close(gout, out, out_unit=BF16_U, name="out")
+
+
+def test_verify_large_state_scale(ops):
+    """State magnitudes like a long prefill (std 1) keep the same relative bar."""
+    d = deltanet_inputs(1, 8, 16, 48, seed=5, state_std=1.0)
+    ck, out = od.deltanet_verify(*deltanet_oracle_args(d), 16, 48)
+    gck, gout = _verify_gpu(ops, d)
+    assert_rel_close(gck, ck, name="ckpt")
+    assert_rel_close(gout, out, out_unit=BF16_U, name="out")
+
+
+@pytest.mark.parametrize("B", [1, 8])
+def test_full_batched_reference_shapes(ops, B):
+    """deltanet::full_batched at the reference's per-rank shapes (Hk=4, Hv=12, state std 0.1,
+    seed 11; test_deltanet_full_batched.py:60-75); conv state bit-exact."""
+    d = deltanet_inputs(B, 1, 4, 12, seed=11, state_std=0.1)
+    f = deltanet_flat_device(d)
+    ns, ncs, o = ops.deltanet.full_batched(
+        f["state"], f["mixed_qkv"], f["conv_state"], f["conv_weight"], f["conv_bias"],
+        f["a_out"], f["b_out"], f["z"], f["A_log"], f["dt_bias"], f["norm_weight"])
+    torch.cuda.synchronize()
+    s_ref, cs_ref, o_ref = od.deltanet_token_step(
+        d["state"].numpy(), bits(d["mixed_qkv"])[:, 0], bits(d["conv_state"]),
+        d["conv_weight"].numpy(), d["conv_bias"].numpy(), d["a_out"].numpy()[:, 0],
+        d["b_out"].numpy()[:, 0], bits(d["z"])[:, 0], d["A_log"].numpy(),
+        d["dt_bias"].numpy(), d["norm_weight"].numpy(), 4, 12)
+    assert_rel_close(ns.cpu().double().numpy().reshape(s_ref.shape), s_ref, name="state")
+    assert np.array_equal(bits(ncs).reshape(cs_ref.shape), cs_ref)
+    assert_rel_close(o.float().cpu().double().numpy().reshape(o_ref.shape), o_ref,
+                     out_unit=BF16_U, name="out")
+    if B == 1:
+        s1, c1, o1 = ops.deltanet.full(
+            f["state"], f["mixed_qkv"], f["conv_state"].reshape(-1, 3), f["conv_weight"],
+            f["conv_bias"], f["a_out"], f["b_out"], f["z"], f["A_log"], f["dt_bias"],
+            f["norm_weight"])
+        torch.cuda.synchronize()
+        assert torch.equal(s1, ns) and torch.equal(c1, ncs) and torch.equal(o1, o)
+
+
+def test_rollback_copy_and_index(ops):
+    """Copy rollback == ckpt[b, a_b]; conv window bit-exact; index-based next verify ==
+    verify from the copied state (no copy needed)."""
+    B, T, Hk, Hv = 4, 8, 16, 48
+    d = deltanet_inputs(B, T, Hk, Hv, seed=21)
+    f = deltanet_flat_device(d)
+    ckpt, _ = ops.deltanet.verify_batched(
+        f["state"], f["mixed_qkv"], f["conv_state"], f["conv_weight"], f["conv_bias"],
+        f["a_out"], f["b_out"], f["z"], f["A_log"], f["dt_bias"], f["norm_weight"])
+    acc = torch.tensor([0, 7, 3, 5], dtype=torch.int32)
+    state, conv = ops.deltanet.rollback(ckpt, f["mixed_qkv"], f["conv_state"], acc.cuda())
+    conv_only = ops.deltanet.conv_rollback(f["mixed_qkv"], f["conv_state"], acc.cuda(), Hv)
+    torch.cuda.synchronize()
+    ck = ckpt.reshape(B, T, Hv * 128, 128)
+    for b in range(B):
+        assert torch.equal(state.reshape(B, Hv * 128, 128)[b], ck[b, int(acc[b])])
+    _, cs_ref = od.deltanet_rollback(np.zeros((B, T, 1, 1, 1)), bits(d["mixed_qkv"]),
+                                     bits(d["conv_state"]), acc.numpy())
+    assert np.array_equal(bits(conv).reshape(cs_ref.shape), cs_ref)
+    assert torch.equal(conv, conv_only)
+
+    # next verify step: from the copied state vs straight from the checkpoints
+    d2 = deltanet_inputs(B, T, Hk, Hv, seed=22)
+    f2 = deltanet_flat_device(d2)
+    args = (f2["mixed_qkv"], conv, f2["conv_weight"], f2["conv_bias"], f2["a_out"],
+            f2["b_out"], f2["z"], f2["A_log"], f2["dt_bias"], f2["norm_weight"])
+    ck_copy, out_copy = ops.deltanet.verify_batched(state, *args)
+    ck_idx, out_idx = ops.deltanet.verify_from_ckpt(ckpt, acc.cuda(), *args)
+    torch.cuda.synchronize()
+    assert torch.equal(ck_copy, ck_idx) and torch.equal(out_copy, out_idx)
+
+
+def test_full_size_b32_sampled(ops):
+    """B=32, T=8, 16/48 heads (921.7 MB of state traffic): every sequence is independent,
+    so three sampled sequences are checked against the oracle run on their slices."""
+    B, T, Hk, Hv = 32, 8, 16, 48
+    d = deltanet_inputs(B, T, Hk, Hv, seed=32)
+    gck, gout = _verify_gpu(ops, d)
+    for b in (0, 17, 31):
+        sl = {k: (v[b:b + 1] if k in ("state", "mixed_qkv", "conv_state", "a_out", "b_out", "z")
+                  else v) for k, v in d.items()}
+        ck, out = od.deltanet_verify(*deltanet_oracle_args(sl), Hk, Hv)
+        assert_rel_close(gck[b:b + 1], ck, name=f"ckpt[b={b}]")
+        assert_rel_close(gout[b:b + 1], out, out_unit=BF16_U, name=f"out[b={b}]")
+
+
+def test_rejects_bad_shapes(ops):
+    d = deltanet_inputs(1, 2, 4, 12, seed=1)
+    f = deltanet_flat_device(d)
+    with pytest.raises(RuntimeError):
+        ops.deltanet.verify_batched(f["state"][:-1], f["mixed_qkv"], f["conv_state"],
+                                    f["conv_weight"], f["conv_bias"], f["a_out"], f["b_out"],
+                                    f["z"], f["A_log"], f["dt_bias"], f["norm_weight"])
+    with pytest.raises((RuntimeError, TypeError)):
+        ops.deltanet.verify_batched(f["state"].double(), f["mixed_qkv"], f["conv_state"],
+                                    f["conv_weight"], f["conv_bias"], f["a_out"], f["b_out"],
+                                    f["z"], f["A_log"], f["dt_bias"], f["norm_weight"])

@@ -1,0 +1,69 @@
+"""GPU parity of fp8::matmul against the oracle (oracle/fp8.py): bf16((x . decode(W)) * scale)
+with fp32 accumulation, at the verify-step shapes (M = B*T in {8, 64, 256}, K = 5120,
+N in {5120, 17408, 34816}) on sampled columns, the reference's per-rank decode shapes
+(contrib/qwen3.6-27b/kernels/tests/test_fp8_matmul.py:217-236, seed 0), split-K, M
+not a multiple of 16, and the OCP-only codes 0x78..0x7E (256..448).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import fp8 as of
+from _util import BF16_U, assert_rel_close, bits, fp8_weights
+
+pytestmark = pytest.mark.gpu
+
+
+def _check(ops, M, K, N, seed, cols=None, fp8_max=448.0):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    w, scale = fp8_weights(N, K, seed + 1, fp8_max=fp8_max)
+    got = ops.fp8.matmul(x.cuda(), w.cuda(), scale.reshape(N, 1).cuda())
+    torch.cuda.synchronize()
+    got = got.float().cpu().double().numpy()
+    if cols is not None:
+        sel = np.asarray(cols)
+        ref = of.fp8_matmul(bits(x), w.numpy()[:, sel], scale.numpy()[sel])
+        got = got[:, sel]
+    else:
+        ref = of.fp8_matmul(bits(x), w.numpy(), scale.numpy())
+    assert_rel_close(got, ref, out_unit=BF16_U, name=f"fp8 M={M} K={K} N={N}")
+
+
+@pytest.mark.parametrize("M", [1, 8, 13, 64, 100, 256])
+def test_small_n(ops, M):
+    _check(ops, M, 5120, 512, seed=M)
+
+
+@pytest.mark.parametrize("M,N", [(8, 5120), (64, 17408), (256, 34816)])
+def test_verify_shapes_sampled(ops, M, N):
+    rng = np.random.default_rng(M)
+    cols = np.sort(rng.choice(N, 384, replace=False))
+    _check(ops, M, 5120, N, seed=7, cols=cols)
+
+
+@pytest.mark.parametrize("K,N", [(5120, 4352), (4352, 5120), (5120, 3072), (5120, 256),
+                                 (1536, 5120), (5120, 2560)])
+def test_reference_decode_shapes(ops, K, N):
+    """B=1 per-rank shapes from the reference's kernel test, with its FP8_MAX = 240."""
+    _check(ops, 1, K, N, seed=0, fp8_max=240.0)
+
+
+def test_ocp_only_codes(ops):
+    """Weights made only of the codes 0x78..0x7E (256..448, finite only in OCP e4m3fn)."""
+    K, N = 128, 64
+    codes = np.random.default_rng(0).integers(0x78, 0x7F, size=(K, N)).astype(np.uint8)
+    codes[::3] |= 0x80
+    w = torch.from_numpy(codes.view(np.int8))
+    x = torch.randn(4, K).to(torch.bfloat16)
+    scale = torch.full((N,), 1.0 / 448.0)
+    got = ops.fp8.matmul(x.cuda(), w.cuda(), scale.reshape(N, 1).cuda()).float().cpu().numpy()
+    ref = of.fp8_matmul(bits(x), codes, scale.numpy())
+    assert_rel_close(got, ref, out_unit=BF16_U, name="ocp codes")
+
+
+def test_rejects_bad_shapes(ops):
+    x = torch.randn(4, 100).to(torch.bfloat16).cuda()
+    w = torch.zeros(100, 64, dtype=torch.int8).cuda()
+    with pytest.raises(RuntimeError):
+        ops.fp8.matmul(x, w, torch.ones(64, 1).cuda())

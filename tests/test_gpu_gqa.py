@@ -1,0 +1,97 @@
+"""GPU parity of the GQA attention-tail ops against the oracle (oracle/gqa.py).
+
+gqa::tail at the reference's shapes (seed 0, B=8, 6 q heads, S=128, position 100, as
+contrib/qwen3.6-27b/kernels/gqa_tail_ref.py:73-102); gqa::tail_verify at reduced and full
+verify shapes (24 q / 4 kv heads, T=8) with KV lengths that cross chunk boundaries, kv_len=0,
+T=1 and other head groupings; gqa::kv_append bit-exact against the oracle's bf16 rounding
+order (at most 1 bf16 ulp where fp32 rsqrt rounding differs).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import gqa as og
+from _util import BF16_U, assert_rel_close, bits, gqa_verify_inputs
+
+pytestmark = pytest.mark.gpu
+
+
+def test_tail_reference_shapes(ops):
+    torch.manual_seed(0)
+    B, S, HQ = 8, 128, 6
+    query = torch.randn(B, HQ, 256)
+    gate = torch.randn(B, HQ, 256)
+    q_norm = torch.randn(256) * 0.1
+    cos = torch.randn(64)
+    sin = torch.randn(64)
+    ck = torch.randn(B, S, 256)
+    cv = torch.randn(B, S, 256)
+    mask = (torch.arange(S) <= 100).float()
+    ref = og.gqa_tail(query.reshape(B * HQ, 256).numpy(), gate.reshape(B * HQ, 256).numpy(),
+                      q_norm.numpy(), cos.numpy(), sin.numpy(), ck.reshape(B * S, 256).numpy(),
+                      cv.reshape(B * S, 256).numpy(), mask.reshape(1, S).numpy())
+    got = ops.gqa.tail(query.reshape(B * HQ, 256).cuda(), gate.reshape(B * HQ, 256).cuda(),
+                       q_norm.reshape(1, 256).cuda(), cos.reshape(1, 64).cuda(),
+                       sin.reshape(1, 64).cuda(), ck.reshape(B * S, 256).cuda(),
+                       cv.reshape(B * S, 256).cuda(), mask.reshape(1, S).cuda())
+    torch.cuda.synchronize()
+    assert_rel_close(got.cpu().double().numpy(), ref, name="gqa.tail")
+
+
+def _run_verify(ops, d):
+    out = ops.gqa.tail_verify(*[d[k].cuda() for k in
+                                ("query", "gate", "q_norm", "cos", "sin", "cache_k", "cache_v",
+                                 "kv_len")])
+    torch.cuda.synchronize()
+    return out.float().cpu().double().numpy()
+
+
+def _oracle_verify(d):
+    return og.gqa_tail_verify(bits(d["query"]), bits(d["gate"]), d["q_norm"].numpy(),
+                              d["cos"].numpy(), d["sin"].numpy(), bits(d["cache_k"]),
+                              bits(d["cache_v"]), d["kv_len"].numpy())
+
+
+@pytest.mark.parametrize("B,T,Hq,Hkv,kv_lens,s_max", [
+    (2, 8, 24, 4, [37, 600], 1024),          # full head layout, short caches
+    (2, 8, 24, 4, [504, 1023 - 8], 1024),    # rows straddling the 512-key chunk edge, full cache
+    (3, 8, 24, 4, [0, 1, 2000], 2048),       # empty prior cache
+    (1, 1, 6, 1, [300], 512),                # decode-like T=1, one 16-row tile
+    (2, 4, 8, 2, [100, 33], 256),            # 16 rows per kv head
+    (1, 5, 12, 2, [1500], 1536),             # 30 rows: two tiles with padding
+])
+def test_tail_verify_matches_oracle(ops, B, T, Hq, Hkv, kv_lens, s_max):
+    d = gqa_verify_inputs(B, T, Hq, Hkv, kv_lens, s_max, seed=B * 7 + T)
+    assert_rel_close(_run_verify(ops, d), _oracle_verify(d), out_unit=BF16_U, name="tail_verify")
+
+
+def test_tail_verify_full_width_long(ops):
+    """Config-2-like: 24/4 heads, T=8, KV lengths 4096..8192 (oracle-affordable)."""
+    d = gqa_verify_inputs(2, 8, 24, 4, [4096, 8000], 8200, seed=2)
+    assert_rel_close(_run_verify(ops, d), _oracle_verify(d), out_unit=BF16_U, name="tail_verify")
+
+
+def test_kv_append_then_attend_equals_cloned_cache(ops):
+    """Append-after-attention equivalence (contrib/qwen3.6-35b-a3b/kernels/tests/
+    test_gqa_stateful_cache_cpu.py:9-40): rows written by kv_append match the oracle's
+    bf16 rounding order and leave every other row untouched."""
+    B, T, Hkv, s_max = 2, 8, 4, 512
+    g = torch.Generator().manual_seed(3)
+    key = torch.randn(B, T, Hkv, 256, generator=g).to(torch.bfloat16)
+    value = torch.randn(B, T, Hkv, 256, generator=g).to(torch.bfloat16)
+    k_norm = torch.randn(256, generator=g) * 0.1
+    kv_len = torch.tensor([5, 300], dtype=torch.int32)
+    d = gqa_verify_inputs(B, T, 24, Hkv, kv_len.numpy(), s_max, seed=4)
+    ck = d["cache_k"].clone()
+    cv = d["cache_v"].clone()
+    ck_dev, cv_dev = ck.cuda(), cv.cuda()
+    ops.gqa.kv_append(key.cuda(), value.cuda(), k_norm.cuda(), d["cos"].cuda(), d["sin"].cuda(),
+                      ck_dev, cv_dev, kv_len.cuda())
+    torch.cuda.synchronize()
+    rk, rv = og.gqa_kv_append(bits(key), bits(value), k_norm.numpy(), d["cos"].numpy(),
+                              d["sin"].numpy(), bits(ck).copy(), bits(cv).copy(), kv_len.numpy())
+    gk, gv = bits(ck_dev.cpu()), bits(cv_dev.cpu())
+    assert np.array_equal(gv, rv)
+    diff = np.abs(gk.astype(np.int32) - rk.astype(np.int32))
+    assert diff.max() <= 1, f"kv_append key rows differ by {diff.max()} bf16 ulps"
+    assert (diff > 0).mean() < 0.01

@@ -1,0 +1,213 @@
+#!/usr/bin/env python3
+"""Benchmark: EAGLE3 verify+accept step on one MI355X.
+
+Workload (the verify-step metric's configuration): a random-init 4-layer slice of the
+27B hybrid at whole-model widths (3 gated-DeltaNet layers + 1 GQA layer, each with its
+MLP, FP8 W8A16 projections), B = 32 sequences, K = 7 chain drafts (T = 8 verify tokens),
+KV lengths U{4096..32768}, rejection-sampling acceptance at temperature 1 over
+[32, 8, 151936] target and [32, 7, 151936] draft logits (draft = 0.8 t + 0.6 eps),
+then rollback (DeltaNet checkpoint index, conv windows, KV lengths).
+
+A step = layers + acceptance + rollback on inputs resident in HBM. Reported:
+  value        committed tokens/s = sum_b (a_b + 1) / t_step
+  roofline     the dominant kernel's algorithmic bytes (or FLOPs) per launch over its
+               mean launch time (HIP events on the launch stream, over the timed steps)
+  cpu_baseline the CPU oracle (numpy) on one sampled sequence of the same step
+
+  python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu-baseline]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "neuron-pytorch-native_amd")
+sys.path[:0] = [ROOT, PKG, os.path.join(PKG, "kernels")]
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
+B, K, V = 32, 7, 151936
+T = K + 1
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--per-op", action="store_true", help="print per-op timings to stderr")
+    return p.parse_args()
+
+
+def kv_lengths(seed):
+    import numpy as np
+    return np.random.default_rng(seed).integers(4096, 32769, size=B).astype(np.int32)
+
+
+def algorithmic(name, kv_len_mean_rows):
+    """(bound, units per launch, unit) for an op name of the step."""
+    if name == "deltanet.verify":
+        per_seq = 48 * 128 * 128 * 4 * (1 + T) + T * 10240 * 2 + 2 * T * 48 * 4 \
+            + 2 * T * 48 * 128 * 2 + 10240 * 3 * 2
+        shared = 10240 * 4 * 4 + 10240 * 4 + 2 * 48 * 4 + 128 * 4
+        return "hbm", B * per_seq + shared, "B"
+    if name == "gqa.tail_verify":
+        kv = B * 4 * (kv_len_mean_rows + T) * 256 * 2 * 2
+        return "hbm", kv + 3 * B * T * 24 * 256 * 2 + 2 * B * T * 64 * 4, "B"
+    if name == "spec.accept_rejection":
+        return "hbm", (B * (2 * K + 1) * V + 2 * B * V) * 4, "B"
+    if name.startswith("fp8.matmul["):
+        m, k, n = (int(v) for v in name[len("fp8.matmul["):-1].split("x"))
+        return "mfma", 2 * m * n * k, "FLOP"
+    return None, None, None
+
+
+def cpu_baseline(model, x, logits, sample_b=0):
+    """Time the numpy oracle on one sequence of the same step (same weights and KV length)."""
+    import numpy as np
+    import torch
+    from oracle import verify_step as ovs
+    from oracle.gqa import rope_cos_sin
+    from spec_verify_step import DN_HV, DN_QKV
+    b = sample_b
+    L_b = int(model.kv_len[b].item())
+    layers = []
+    for L in model.layers:
+        d = {"kind": L["kind"], "in_norm": L["in_norm"].cpu().numpy(),
+             "post_norm": L["post_norm"].cpu().numpy()}
+        for nm in ("gate_up", "down", "in_proj", "out_proj", "qkv_proj", "o_proj"):
+            if nm in L:
+                d[nm] = (L[nm][0].cpu().numpy(), L[nm][1].cpu().numpy().reshape(-1))
+        if L["kind"] == "D":
+            for nm in ("conv_w", "conv_b", "A_log", "dt_bias", "norm_w"):
+                d[nm] = L[nm].cpu().numpy()
+            rng = np.random.default_rng(b)
+            d["state"] = rng.standard_normal((1, DN_HV, 128, 128)) * 0.02
+            d["conv_state"] = rng.integers(0, 1 << 15, (1, DN_QKV, 3)).astype(np.uint16) & 0x3FFF
+        else:
+            d["q_norm"], d["k_norm"] = L["q_norm"].cpu().numpy(), L["k_norm"].cpu().numpy()
+            rows = L_b + T
+            d["cache_k"] = L["cache_k"][b:b + 1, :, :rows].contiguous().cpu().view(torch.int16).numpy().view(np.uint16)
+            d["cache_v"] = L["cache_v"][b:b + 1, :, :rows].contiguous().cpu().view(torch.int16).numpy().view(np.uint16)
+        layers.append(d)
+    xb = x[b * T:(b + 1) * T].cpu().view(torch.int16).numpy().view(np.uint16)
+    tgt, drf, ids, u, us = (t[b:b + 1].cpu().numpy() for t in logits)
+    cos, sin = rope_cos_sin(L_b + np.arange(T)[None, :])
+    t0 = time.perf_counter()
+    _, acc, _, _ = ovs.verify_step(layers, xb, np.array([L_b]), 1, T, tgt, drf, ids, u, us,
+                                   cos, sin)
+    dt = time.perf_counter() - t0
+    cores = len(os.sched_getaffinity(0))
+    return {"value": round(float(acc[0] + 1) / dt, 4), "unit": "tokens/s", "cores": cores,
+            "kind": "port",
+            "sample": f"1 of {B} sequences (kv_len {L_b}) through the same 4-layer step, "
+                      f"{dt:.1f} s; numpy oracle, float64 GEMMs on BLAS threads"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (got --gpus {args.gpus}); the verify step is "
+              f"measured on a single MI355X", file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import torch
+    from spec_verify_step import HIDDEN, OpTimer, VerifySlice, synthetic_logits
+
+    dev = "cuda"
+    torch.manual_seed(args.seed)
+    kv_lens = kv_lengths(args.seed)
+    s_max = int(kv_lens.max()) + T * (args.warmup + args.steps + 2)
+    model = VerifySlice(B, K, kv_lens, s_max, pattern="DDDG", seed=args.seed, device=dev)
+    g = torch.Generator(device=dev).manual_seed(args.seed + 1)
+    x = torch.randn(B * T, HIDDEN, generator=g, device=dev).to(torch.bfloat16)
+    logits = synthetic_logits(B, K, V, args.seed + 2, dev)
+    kv_start = model.kv_len.clone()
+
+    for _ in range(args.warmup):
+        model.step(x, *logits)
+    torch.cuda.synchronize()
+    kv0 = float(model.kv_len.float().mean().item())  # mean cache rows before the timed steps
+
+    timer = OpTimer()
+    model.timer = timer
+    committed = []
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        _, acc, _ = model.step(x, *logits)
+        committed.append(acc)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    model.timer = lambda name, fn, *a: fn(*a)
+    tokens = int(sum(int((a + 1).sum().item()) for a in committed))
+    ms_per_step = elapsed * 1e3 / args.steps
+    ops = timer.summary()
+    # mean prior cache rows seen by the attention over the timed steps
+    inc = [float((a + 1).float().mean().item()) for a in committed]
+    kv_mean_rows = kv0 + float(np.mean([sum(inc[:s]) for s in range(len(inc))]))
+
+    # dominant kernel by total time in the timed steps
+    dom = max(ops, key=lambda k: ops[k]["total_ms"])
+    bound, units, unit = algorithmic(dom, kv_mean_rows)
+    mean_s = ops[dom]["mean_ms"] * 1e-3
+    if bound == "mfma":
+        achieved = units / mean_s / 1e12
+        roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": BF16_PEAK_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(achieved / BF16_PEAK_TFLOPS, 4), "traffic": None}
+    else:
+        achieved = units / mean_s / 1e9
+        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None}
+    roof["kernel"] = dom
+    roof["mean_launch_ms"] = round(ops[dom]["mean_ms"], 4)
+    roof["units_per_launch"] = units
+
+    if args.per_op:
+        for k, v in sorted(ops.items(), key=lambda kv: -kv[1]["total_ms"]):
+            bnd, u, un = algorithmic(k, kv_mean_rows)
+            rate = ""
+            if bnd == "hbm":
+                rate = f"{u / (v['mean_ms'] * 1e-3) / 1e9:8.1f} GB/s"
+            elif bnd == "mfma":
+                rate = f"{u / (v['mean_ms'] * 1e-3) / 1e12:8.1f} TFLOP/s"
+            print(f"{k:40s} x{v['launches'] // args.steps:2d}/step {v['mean_ms']:8.4f} ms "
+                  f"{v['total_ms'] / args.steps:8.4f} ms/step {rate}", file=sys.stderr)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        model.kv_len = kv_start
+        cpu = cpu_baseline(model, x, logits)
+
+    line = {
+        "metric": "verify-step tokens/s (B=32,K=7) + achieved HBM GB/s vs MI355X peak",
+        "value": round(tokens / elapsed, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random-init weights, N(0,1) activations and logits)",
+        "config": {"workload": "EAGLE3 verify+accept+rollback, 4-layer Qwen3.6-27B-width slice "
+                               "(3 gated-DeltaNet + 1 GQA, FP8 W8A16 projections), rejection "
+                               "sampling at T=1",
+                   "batch": B, "draft_len": K, "verify_tokens": T, "vocab": V,
+                   "kv_len": "U{4096..32768}", "parallelism": "single GPU"},
+        "verified_tokens_per_s": round(B * T * args.steps / elapsed, 1),
+        "committed_per_seq": round(tokens / (B * args.steps), 3),
+        "roofline": roof,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,243 @@
+"""EAGLE3 verify-and-accept step of a Qwen3.6 hybrid slice on gfx950.
+
+The caller side of the ops, mirroring the reference's decode harness
+(contrib/qwen3.6-27b/static_decode.py: _deltanet_layer :753-847, _gqa_layer :849-949,
+_mlp_layer :951-963, rms_norm :322-335, _init_rope :489-502) for T = K+1 verify tokens
+per sequence instead of one:
+
+  x [B*T, 5120] --(per layer)--> input RMSNorm(1+w)
+      DeltaNet layer: fp8 in-proj [qkv | z | a | b] -> deltanet::verify_from_ckpt -> fp8 out-proj
+      GQA layer:      fp8 [q+gate | k | v] -> gqa::kv_append -> gqa::tail_verify -> fp8 o-proj
+    -> residual -> post RMSNorm(1+w) -> fp8 gate/up -> SiLU * up -> fp8 down -> residual
+  logits -> spec::accept_rejection (or accept_greedy)
+  rollback: DeltaNet state = checkpoint[accepted] (read in place by the next step),
+            conv window rolled back, KV length += accepted + 1.
+
+Dimensions are the 27B model's whole-model widths on one GPU: hidden 5120, DeltaNet 16 k /
+48 v heads of 128, GQA 24 q / 4 kv heads of 256 with a 64-dim partial RoPE (theta 1e7),
+MLP intermediate 17408. Weights are random (e4m3fn, per-output-channel fp32 scales).
+"""
+import math
+
+import torch
+
+import npn_ops  # noqa: F401  (registers the torch.ops)
+
+HIDDEN = 5120
+DN_HK, DN_HV, DN_D = 16, 48, 128
+DN_QKV = (2 * DN_HK + DN_HV) * DN_D       # 10240
+DN_VAL = DN_HV * DN_D                     # 6144
+GQA_HQ, GQA_HKV, GQA_DH = 24, 4, 256
+GQA_QG = GQA_HQ * 2 * GQA_DH              # 12288 (query and gate interleaved per head)
+INTER = 17408
+ROPE_DIM, ROPE_THETA = 64, 1e7
+RMS_EPS = 1e-6
+DN_IN_N = DN_QKV + DN_VAL + 2 * DN_HV     # 16480 = qkv | z | a | b
+DN_IN_PAD = ((DN_IN_N + 63) // 64) * 64   # 16512 (the GEMM takes N % 64 == 0)
+
+
+def rms_norm_1p(x, w):
+    """(1 + w) * x * rsqrt(mean(x^2) + eps) in fp32, cast back (static_decode.py:322-335)."""
+    xf = x.float()
+    n = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + RMS_EPS)
+    return ((1.0 + w) * n).to(x.dtype)
+
+
+def rope_tables(positions):
+    """cos/sin [..., 64] at integer positions, fp32 as the reference table (:489-502)."""
+    inv_freq = 1.0 / (ROPE_THETA ** (torch.arange(0, ROPE_DIM, 2, device=positions.device,
+                                                  dtype=torch.float32) / ROPE_DIM))
+    freqs = positions.float().unsqueeze(-1) * inv_freq
+    emb = torch.cat([freqs, freqs], dim=-1)
+    return emb.cos().contiguous(), emb.sin().contiguous()
+
+
+def random_fp8_linear(n_out, k_in, gen, device, std=0.02, fp8_max=448.0, pad_to=None):
+    """W ~ N(0, std) [n_out, k_in] -> (w [K, N] int8 e4m3fn bytes, scale [N, 1] f32), the
+    reference's per-channel absmax quantisation (static_decode.py:283-304) with FP8_MAX=448."""
+    w = torch.randn(n_out, k_in, generator=gen, device=device, dtype=torch.float32) * std
+    w = w.to(torch.bfloat16)
+    absmax = w.abs().amax(dim=-1).float().clamp_min(1e-12)
+    scale = absmax / fp8_max
+    inv = (1.0 / scale).to(torch.bfloat16).unsqueeze(-1)
+    wq = (w * inv).clamp(-fp8_max, fp8_max).to(torch.float8_e4m3fn)
+    del w
+    wt = wq.t().contiguous().view(torch.int8)
+    scale = scale.reshape(-1, 1).contiguous()
+    if pad_to is not None and pad_to > n_out:
+        wt = torch.cat([wt, torch.zeros(k_in, pad_to - n_out, dtype=torch.int8, device=device)], 1)
+        scale = torch.cat([scale, torch.ones(pad_to - n_out, 1, device=device)], 0)
+    return wt.contiguous(), scale.contiguous()
+
+
+class OpTimer:
+    """Records a pair of HIP events around each op launch on the current stream, keyed by
+    op name; `summary()` (after a synchronize) gives per-name launch counts and mean ms."""
+
+    def __init__(self):
+        self.events = {}
+
+    def __call__(self, name, fn, *args):
+        s = torch.cuda.Event(enable_timing=True)
+        e = torch.cuda.Event(enable_timing=True)
+        s.record()
+        out = fn(*args)
+        e.record()
+        self.events.setdefault(name, []).append((s, e))
+        return out
+
+    def summary(self):
+        res = {}
+        for k, ev in self.events.items():
+            ms = [s.elapsed_time(e) for s, e in ev]
+            res[k] = {"launches": len(ms), "mean_ms": sum(ms) / len(ms), "total_ms": sum(ms)}
+        return res
+
+
+def _untimed(name, fn, *args):
+    return fn(*args)
+
+
+def fp8_linear(x, wq, timer=_untimed, name="fp8.matmul"):
+    w, s = wq
+    return timer(name, torch.ops.fp8.matmul, x, w, s)
+
+
+class VerifySlice:
+    """Random-init slice of `pattern` layers ('D' DeltaNet, 'G' GQA) plus per-layer MLPs,
+    with the decode state of B sequences."""
+
+    def __init__(self, B, K, kv_lens, s_max, pattern="DDDG", seed=0, device="cuda"):
+        self.B, self.K, self.T = B, K, K + 1
+        self.pattern = pattern
+        self.device = device
+        self.s_max = s_max
+        g = torch.Generator(device=device).manual_seed(seed)
+        self.layers = []
+        for kind in pattern:
+            L = {"kind": kind,
+                 "in_norm": (torch.randn(HIDDEN, generator=g, device=device) * 0.1),
+                 "post_norm": (torch.randn(HIDDEN, generator=g, device=device) * 0.1),
+                 "gate_up": random_fp8_linear(2 * INTER, HIDDEN, g, device),
+                 "down": random_fp8_linear(HIDDEN, INTER, g, device)}
+            if kind == "D":
+                L["in_proj"] = random_fp8_linear(DN_IN_N, HIDDEN, g, device, pad_to=DN_IN_PAD)
+                L["out_proj"] = random_fp8_linear(HIDDEN, DN_VAL, g, device)
+                L["conv_w"] = torch.randn(DN_QKV, 4, generator=g, device=device) * 0.5
+                L["conv_b"] = torch.randn(DN_QKV, generator=g, device=device) * 0.1
+                L["A_log"] = torch.randn(DN_HV, generator=g, device=device) * 0.5
+                L["dt_bias"] = torch.randn(DN_HV, generator=g, device=device)
+                L["norm_w"] = torch.randn(DN_D, generator=g, device=device) * 0.1 + 1.0
+                # decode state: one initial state per sequence; after a step the state is
+                # the previous step's checkpoint buffer plus the accepted index
+                L["state"] = torch.randn(B * DN_HV * DN_D, DN_D, generator=g, device=device) * 0.02
+                L["ckpt"] = None
+                L["conv_state"] = torch.randn(B * DN_QKV, 3, generator=g,
+                                              device=device).to(torch.bfloat16)
+            else:
+                L["qkv_proj"] = random_fp8_linear(GQA_QG + 2 * GQA_HKV * GQA_DH, HIDDEN, g, device)
+                L["o_proj"] = random_fp8_linear(HIDDEN, GQA_HQ * GQA_DH, g, device)
+                L["q_norm"] = torch.randn(GQA_DH, generator=g, device=device) * 0.1
+                L["k_norm"] = torch.randn(GQA_DH, generator=g, device=device) * 0.1
+                shape = (B, GQA_HKV, s_max, GQA_DH)
+                L["cache_k"] = torch.randn(shape, generator=g, device=device).to(torch.bfloat16)
+                L["cache_v"] = torch.randn(shape, generator=g, device=device).to(torch.bfloat16)
+            self.layers.append(L)
+        self.kv_len = torch.as_tensor(kv_lens, dtype=torch.int32, device=device).clone()
+        self.prev_accepted = None
+        self.timer = _untimed
+
+    # ---- layers --------------------------------------------------------------------------
+    def _deltanet(self, L, x):
+        B, T = self.B, self.T
+        h = rms_norm_1p(x, L["in_norm"])
+        proj = fp8_linear(h, L["in_proj"], self.timer, f"fp8.matmul[{B * T}x{HIDDEN}x{DN_IN_PAD}]")
+        mixed = proj[:, :DN_QKV].contiguous().reshape(-1)
+        z = proj[:, DN_QKV:DN_QKV + DN_VAL].contiguous().reshape(B * T * DN_HV, DN_D)
+        a = proj[:, DN_QKV + DN_VAL:DN_QKV + DN_VAL + DN_HV].float().contiguous().reshape(-1)
+        b = proj[:, DN_QKV + DN_VAL + DN_HV:DN_IN_N].float().contiguous().reshape(-1)
+        args = (mixed, L["conv_state"], L["conv_w"], L["conv_b"], a, b, z, L["A_log"],
+                L["dt_bias"], L["norm_w"])
+        if L["ckpt"] is None:
+            ckpt, out = self.timer("deltanet.verify", torch.ops.deltanet.verify_batched,
+                                   L["state"], *args)
+        else:
+            ckpt, out = self.timer("deltanet.verify", torch.ops.deltanet.verify_from_ckpt,
+                                   L["ckpt"], self.prev_accepted, *args)
+        L["pending"] = (ckpt, mixed)
+        return x + fp8_linear(out.reshape(B * T, DN_VAL), L["out_proj"], self.timer,
+                              f"fp8.matmul[{B * T}x{DN_VAL}x{HIDDEN}]")
+
+    def _gqa(self, L, x, cos, sin):
+        B, T = self.B, self.T
+        h = rms_norm_1p(x, L["in_norm"])
+        proj = fp8_linear(h, L["qkv_proj"], self.timer,
+                          f"fp8.matmul[{B * T}x{HIDDEN}x{GQA_QG + 2 * GQA_HKV * GQA_DH}]")
+        qg = proj[:, :GQA_QG].reshape(B, T, GQA_HQ, 2 * GQA_DH)
+        query = qg[..., :GQA_DH].contiguous()
+        gate = qg[..., GQA_DH:].contiguous()
+        kv = proj[:, GQA_QG:].reshape(B, T, 2, GQA_HKV, GQA_DH)
+        key = kv[:, :, 0].contiguous()
+        value = kv[:, :, 1].contiguous()
+        self.timer("gqa.kv_append", torch.ops.gqa.kv_append, key, value, L["k_norm"], cos, sin,
+                   L["cache_k"], L["cache_v"], self.kv_len)
+        attn = self.timer("gqa.tail_verify", torch.ops.gqa.tail_verify, query, gate, L["q_norm"],
+                          cos, sin, L["cache_k"], L["cache_v"], self.kv_len)
+        return x + fp8_linear(attn.reshape(B * T, GQA_HQ * GQA_DH), L["o_proj"], self.timer,
+                              f"fp8.matmul[{B * T}x{GQA_HQ * GQA_DH}x{HIDDEN}]")
+
+    def _mlp(self, L, x):
+        h = rms_norm_1p(x, L["post_norm"])
+        M = x.shape[0]
+        gu = fp8_linear(h, L["gate_up"], self.timer, f"fp8.matmul[{M}x{HIDDEN}x{2 * INTER}]")
+        act = (torch.nn.functional.silu(gu[:, :INTER].float()) * gu[:, INTER:].float()).to(torch.bfloat16)
+        return x + fp8_linear(act, L["down"], self.timer, f"fp8.matmul[{M}x{INTER}x{HIDDEN}]")
+
+    def forward(self, x):
+        """x [B*T, 5120] bf16 -> hidden after the slice (the verify positions' features)."""
+        pos = self.kv_len.long().unsqueeze(1) + torch.arange(self.T, device=x.device)
+        cos, sin = rope_tables(pos)
+        for L in self.layers:
+            x = self._deltanet(L, x) if L["kind"] == "D" else self._gqa(L, x, cos, sin)
+            x = self._mlp(L, x)
+        return x
+
+    def accept_and_rollback(self, accepted):
+        """Commit `accepted` drafts per sequence: DeltaNet continues from checkpoint
+        [accepted] (in place, next step), conv windows roll back, KV lengths advance."""
+        for L in self.layers:
+            if L["kind"] == "D":
+                ckpt, mixed = L.pop("pending")
+                L["conv_state"] = self.timer("deltanet.conv_rollback",
+                                             torch.ops.deltanet.conv_rollback, mixed,
+                                             L["conv_state"], accepted, DN_HV)
+                L["ckpt"] = ckpt
+        self.prev_accepted = accepted
+        self.kv_len = self.kv_len + accepted + 1
+
+    def step(self, x, target_logits, draft_logits, draft_ids, u_accept, u_sample, greedy=False):
+        """One verify + accept + rollback step. Returns (hidden, accepted, out_ids)."""
+        h = self.forward(x)
+        if greedy:
+            accepted, out_ids = self.timer("spec.accept_greedy", torch.ops.spec.accept_greedy,
+                                           target_logits, draft_ids)
+        else:
+            accepted, out_ids = self.timer("spec.accept_rejection",
+                                           torch.ops.spec.accept_rejection, target_logits,
+                                           draft_logits, draft_ids, u_accept, u_sample, 1.0)
+        self.accept_and_rollback(accepted)
+        return h, accepted, out_ids
+
+
+def synthetic_logits(B, K, V, seed, device, rho=0.8):
+    """Target logits [B, K+1, V] ~ N(0,1); draft logits [B, K, V] = rho*t + sqrt(1-rho^2)*eps;
+    draft ids sampled from softmax(draft); uniforms [B, K] and [B]."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    target = torch.randn(B, K + 1, V, generator=g, device=device)
+    draft = rho * target[:, :K] + math.sqrt(1 - rho * rho) * torch.randn(B, K, V, generator=g,
+                                                                         device=device)
+    ids = torch.multinomial(torch.softmax(draft, -1).reshape(B * K, V), 1,
+                            generator=g).reshape(B, K)
+    u = torch.rand(B, K, generator=g, device=device)
+    us = torch.rand(B, generator=g, device=device)
+    return target.contiguous(), draft.contiguous(), ids, u, us

@@ -72,9 +72,13 @@ def quantize_fp8_per_channel(w_bits, fp8_max=448.0):
     return np.ascontiguousarray(q.T).view(np.int8), scale
 
 
+# All 256 codes decoded once by decode_e4m3fn; large weights are decoded by table lookup.
+DECODE_LUT = decode_e4m3fn(np.arange(256, dtype=np.uint8))
+
+
 def fp8_matmul(x_bits, w_i8, scale):
     """x [M, K] bf16 bits, w [K, N] e4m3fn bytes, scale [N] (or [N,1]) f32 ->
     float64 [M, N] = (x . decode(w)) * scale, before the bf16 cast."""
     x = bf16_bits_to_f32(x_bits).astype(np.float64)
-    w = decode_e4m3fn(w_i8).astype(np.float64)
+    w = DECODE_LUT[np.asarray(w_i8).view(np.uint8)].astype(np.float64)
     return (x @ w) * np.asarray(scale, np.float64).reshape(1, -1)

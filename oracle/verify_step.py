@@ -1,0 +1,99 @@
+"""Oracle of the verify-and-accept step of a hybrid slice (test infrastructure only).
+
+Composes the op oracles the way the reference's decode harness composes its ops
+(contrib/qwen3.6-27b/static_decode.py: _deltanet_layer :753-847, _gqa_layer :849-949,
+_mlp_layer :951-963, rms_norm :322-335), for T verify tokens, rounding to bf16 at the
+same points as the device path (every op output and residual add is bf16).
+
+Layer dicts hold numpy arrays: fp8 weights as ([K, N] uint8/int8 bytes, [N] f32 scale),
+norms and DeltaNet parameters as float32, the decode state (DeltaNet state [B,Hv,128,128]
+and conv state bits [B,QKV,3]; GQA cache bits [B,Hkv,S,256]) and kv_len [B].
+
+Pinning: composition of pinned op oracles; the end-to-end GPU test compares the device
+step against it (tests/test_gpu_verify_step.py).
+"""
+import numpy as np
+
+from . import accept as oa
+from . import deltanet as od
+from . import fp8 as of
+from . import gqa as og
+from .numerics import bf16_bits_to_f32, f32_to_bf16_bits
+
+HIDDEN = 5120
+RMS_EPS = 1e-6
+
+
+def bf16(x):
+    """Round to bf16, returned as bits."""
+    return f32_to_bf16_bits(np.asarray(x, np.float32))
+
+
+def rms_norm_1p_bits(x_bits, w):
+    x = bf16_bits_to_f32(x_bits).astype(np.float32)
+    n = x * (np.float32(1.0) / np.sqrt((x * x).mean(-1, keepdims=True, dtype=np.float32) + np.float32(RMS_EPS)))
+    return bf16((np.float32(1.0) + np.asarray(w, np.float32)) * n)
+
+
+def linear(x_bits, wq):
+    w, s = wq
+    return bf16(of.fp8_matmul(x_bits, w, np.asarray(s).reshape(-1)))
+
+
+def add(a_bits, b_bits):
+    return bf16(bf16_bits_to_f32(a_bits) + bf16_bits_to_f32(b_bits))
+
+
+def deltanet_layer(L, x, B, T, hk, hv):
+    h = rms_norm_1p_bits(x, L["in_norm"])
+    proj = linear(h, L["in_proj"])
+    qkv = (2 * hk + hv) * 128
+    val = hv * 128
+    mixed = proj[:, :qkv].reshape(B, T, qkv)
+    z = proj[:, qkv:qkv + val].reshape(B, T, hv, 128)
+    a = bf16_bits_to_f32(proj[:, qkv + val:qkv + val + hv]).reshape(B, T, hv)
+    b = bf16_bits_to_f32(proj[:, qkv + val + hv:qkv + val + 2 * hv]).reshape(B, T, hv)
+    ckpt, out = od.deltanet_verify(L["state"], mixed, L["conv_state"], L["conv_w"], L["conv_b"],
+                                   a, b, z, L["A_log"], L["dt_bias"], L["norm_w"], hk, hv)
+    L["pending"] = (ckpt, mixed)
+    return add(x, linear(bf16(out.reshape(B * T, val)), L["out_proj"]))
+
+
+def gqa_layer(L, x, B, T, hq, hkv, kv_len, cos, sin):
+    h = rms_norm_1p_bits(x, L["in_norm"])
+    proj = linear(h, L["qkv_proj"])
+    qg = proj[:, :hq * 512].reshape(B, T, hq, 512)
+    query, gate = qg[..., :256], qg[..., 256:]
+    kv = proj[:, hq * 512:].reshape(B, T, 2, hkv, 256)
+    og.gqa_kv_append(kv[:, :, 0], kv[:, :, 1], L["k_norm"], cos, sin, L["cache_k"], L["cache_v"],
+                     kv_len)
+    attn = og.gqa_tail_verify(query, gate, L["q_norm"], cos, sin, L["cache_k"], L["cache_v"], kv_len)
+    return add(x, linear(bf16(attn.reshape(B * T, hq * 256)), L["o_proj"]))
+
+
+def mlp(L, x, inter):
+    h = rms_norm_1p_bits(x, L["post_norm"])
+    gu = bf16_bits_to_f32(linear(h, L["gate_up"])).astype(np.float32)
+    g, u = gu[:, :inter], gu[:, inter:]
+    act = bf16((g / (np.float32(1.0) + np.exp(-g))) * u)
+    return add(x, linear(act, L["down"]))
+
+
+def verify_step(layers, x_bits, kv_len, B, T, target, draft, draft_ids, u_accept, u_sample,
+                cos, sin, dn_heads=(16, 48), gqa_heads=(24, 4), inter=17408):
+    """One verify + accept + rollback step. Returns (hidden bits [B*T, H], accepted, out_ids);
+    layer states are updated in place (DeltaNet state = ckpt[accepted], conv rolled back,
+    GQA caches written); kv_len is returned advanced as the 4th value."""
+    x = np.asarray(x_bits, np.uint16)
+    for L in layers:
+        if L["kind"] == "D":
+            x = deltanet_layer(L, x, B, T, *dn_heads)
+        else:
+            x = gqa_layer(L, x, B, T, *gqa_heads, kv_len, cos, sin)
+        x = mlp(L, x, inter)
+    accepted, out_ids = oa.accept_rejection(target, draft, draft_ids, u_accept, u_sample, 1.0)
+    for L in layers:
+        if L["kind"] == "D":
+            ckpt, mixed = L.pop("pending")
+            L["state"], L["conv_state"] = od.deltanet_rollback(ckpt, mixed, L["conv_state"], accepted)
+    return x, accepted, out_ids, np.asarray(kv_len) + accepted + 1

@@ -177,6 +177,170 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemm_kernel(GemmArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// Wide kernel for 64 < M <= 256 rows per pass (MFMA-bound: each weight byte feeds 2*M flops).
+// The grid is one workgroup per CU. Columns are split into 16-wide units spread evenly over
+// the workgroups (u0..u1, at most NTM units each), so every CU gets the same work up to one
+// unit; workgroups are placed so logically adjacent column ranges share an XCD and its L2
+// (a range is a 128..144-byte segment of each weight row, so neighbours share lines).
+//
+// Data path, all global reads by LDS DMA (npn::lds_dma16, no VGPR staging) into a
+// 3-stage ring, two 64-k chunks ahead of the MFMAs:
+//   x chunk  [256 rows][64 k] bf16, 16-byte chunks XOR-swizzled by (row & 7)
+//   W chunk  [64 k][ncols] raw e4m3fn bytes (the [K, N] layout, one row segment per k)
+// Each of the 4 waves owns 64 rows: A operands come from the x tile (ds_read_b128), B
+// operands from the W tile with the 8-bit transposed read ds_read_b64_tr_b8 -- in each
+// 16-lane group, lane i gets byte (i & 7) of the 8-byte chunk supplied by lane 2j + (i >> 3)
+// as its j-th byte, so lanes 2j + h supply row k0 + 8G + j, columns 8h..8h+7, and lane i
+// receives column i's 8 consecutive k -- then 4 v_cvt_scalef32_pk_bf16_fp8 make the bf16
+// B operand.
+constexpr int KC = 64;          // k per pipeline chunk
+constexpr int WIDE_WG = 256;    // workgroups per pass (one per CU)
+constexpr int NSTAGE = 3;
+
+struct WideArgs {
+  const uint16_t* x;
+  const uint8_t* w;
+  const float* scale;
+  uint16_t* out;
+  float* partial;  // [split_k][M][N] when split_k > 1
+  int M, K, N, units, groups, split_k;
+};
+
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ i32x2 lds_tr8(const uint8_t* p) {
+  return __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) i32x2*)(p));
+}
+
+
+template <int NTM>
+__global__ __launch_bounds__(256, 1) void fp8_gemm_wide_kernel(WideArgs a) {
+  constexpr int XBYTES = 256 * KC * 2;                 // 32 KiB x stage
+  constexpr int WI = (KC * NTM + 255) / 256;           // W DMA instructions per thread per chunk
+  constexpr int WBYTES = WI * 256 * 16;                // W stage incl. slack for padded lanes
+  constexpr int STAGE = XBYTES + WBYTES;
+  constexpr int XI = XBYTES / (256 * 16);              // x DMA instructions per thread (8)
+  __shared__ __attribute__((aligned(16))) uint8_t smem[NSTAGE * STAGE];
+
+  const int nwg = gridDim.x;
+  const int per_xcd = nwg / 8;
+  const int logical = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+  const int sk = logical % a.split_k;
+  const int grp = logical / a.split_k;
+  if (grp >= a.groups) return;
+  const int u0 = (int)((long)grp * a.units / a.groups);
+  const int u1 = (int)((long)(grp + 1) * a.units / a.groups);
+  const int nu = u1 - u0;
+  if (nu <= 0) return;
+  const int n0 = 16 * u0;
+  const int ncols = 16 * nu;
+  const int nchunks = a.K / KC;
+  const int c_lo = (int)((long)nchunks * sk / a.split_k);
+  const int c_hi = (int)((long)nchunks * (sk + 1) / a.split_k);
+  const int m_base = blockIdx.y * 256;
+  const int tid = threadIdx.x;
+  const int wv = tid >> 6, lane = tid & 63;
+  const int i = lane & 15, G = lane >> 4;
+  const int mlast = a.M - 1;
+
+  // DMA of chunk c into stage st: x rows (8 instructions / thread), then W rows.
+  auto issue = [&](int c, int st) {
+    uint8_t* xs = smem + st * STAGE;
+    uint8_t* ws = xs + XBYTES;
+#pragma unroll
+    for (int q = 0; q < XI; ++q) {
+      const int f = q * 256 + tid;            // 16-byte slot in the x stage
+      const int row = f >> 3, pos = f & 7;    // 8 slots per 128-byte row
+      int m = m_base + row;
+      m = m <= mlast ? m : mlast;
+      const uint16_t* src = a.x + (size_t)m * a.K + c * KC + 8 * (pos ^ (row & 7));
+      npn::lds_dma16(src, xs + q * 4096 + (tid & ~63) * 16);
+    }
+#pragma unroll
+    for (int q = 0; q < WI; ++q) {
+      int f = q * 256 + tid;                  // 16-byte slot of the W stage
+      if (f >= KC * nu) f = 0;                // padded lanes re-read slot 0 into the slack
+      const int r = f / nu, cc = f - (f / nu) * nu;
+      const uint8_t* src = a.w + (size_t)(c * KC + r) * a.N + n0 + 16 * cc;
+      npn::lds_dma16(src, ws + q * 4096 + (tid & ~63) * 16);
+    }
+  };
+
+  f32x4 acc[4][NTM];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < NTM; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  if (c_lo < c_hi) issue(c_lo, 0);
+  if (c_lo + 1 < c_hi) issue(c_lo + 1, 1);
+
+  // B-operand tr8 address parts: lane supplies row 8G + (i >> 1), column half (i & 1).
+  const int trow = 8 * G + (i >> 1);
+  const int tcol = 8 * (i & 1);
+
+  for (int c = c_lo; c < c_hi; ++c) {
+    const int st = (c - c_lo) % NSTAGE;
+    // LDS here is written only by the DMA, whose completion vmcnt tracks: wait for this
+    // thread's chunk-c transfers (chunk c+1 may stay in flight), then a plain s_barrier.
+    // (__syncthreads() would add a workgroup fence, i.e. vmcnt(0), and drain the ring.)
+    if (c + 1 < c_hi) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(XI + WI) : "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();  // chunk c is in LDS for every wave; stage (c+2)%3 is free
+    asm volatile("" ::: "memory");
+    if (c + 2 < c_hi) issue(c + 2, (c + 2 - c_lo) % NSTAGE);
+    const uint8_t* xs = smem + st * STAGE;
+    const uint8_t* ws = xs + XBYTES;
+    // Every workgroup runs NTM column tiles: tiles past its own nu read in-bounds LDS
+    // (the next rows / stage slack) and are never stored, and the workgroups with nu < NTM
+    // are not the ones that set the kernel's duration.
+#pragma unroll
+    for (int ks = 0; ks < KC / 32; ++ks) {
+      bf16x8 aop[4];
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+        const int row = 64 * wv + 16 * mt + i;
+        const int pos = (4 * ks + G) ^ (row & 7);
+        aop[mt] = *reinterpret_cast<const bf16x8*>(xs + row * (KC * 2) + pos * 16);
+      }
+      i32x2 raw[NTM];
+      const uint8_t* wrow = ws + (32 * ks + trow) * ncols + tcol;
+#pragma unroll
+      for (int nt = 0; nt < NTM; ++nt) raw[nt] = lds_tr8(wrow + 16 * nt);
+#pragma unroll
+      for (int nt = 0; nt < NTM; ++nt) {
+        u32x4 bw;
+        bw[0] = fp8x2_to_bf16x2<false>((uint32_t)raw[nt][0]);
+        bw[1] = fp8x2_to_bf16x2<true>((uint32_t)raw[nt][0]);
+        bw[2] = fp8x2_to_bf16x2<false>((uint32_t)raw[nt][1]);
+        bw[3] = fp8x2_to_bf16x2<true>((uint32_t)raw[nt][1]);
+        const bf16x8 bop = __builtin_bit_cast(bf16x8, bw);
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+          acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop[mt], bop, acc[mt][nt], 0, 0, 0);
+      }
+    }
+  }
+
+  // Epilogue: lane (i, G) holds rows 64wv + 16mt + 4G + r, column n0 + 16nt + i.
+#pragma unroll
+  for (int nt = 0; nt < NTM; ++nt) {
+    if (nt >= nu) continue;
+    const int col = n0 + 16 * nt + i;
+    const float sc = a.scale[col];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = m_base + 64 * wv + 16 * mt + 4 * G + r;
+        if (m >= a.M) continue;
+        if (a.split_k == 1) a.out[(size_t)m * a.N + col] = npn::f32_to_bf16(acc[mt][nt][r] * sc);
+        else a.partial[((size_t)sk * a.M + m) * a.N + col] = acc[mt][nt][r];
+      }
+  }
+}
+
 // out = bf16(scale * sum_s partial[s]), summed in order s = 0..split_k-1.
 __global__ void fp8_splitk_reduce_kernel(const float* __restrict__ partial,
                                          const float* __restrict__ scale,
@@ -192,10 +356,52 @@ __global__ void fp8_splitk_reduce_kernel(const float* __restrict__ partial,
 struct GemmPlan {
   int mt, passes, split_k;
   size_t ws;
+  bool wide;
+  int units, groups, ntm;
 };
+
+// Wide-kernel instantiations: most 16-column units one workgroup can hold.
+constexpr int kWideNT[] = {1, 2, 3, 5, 9};
+
+// Wide-kernel split-K choice: modelled time = max(MFMA time at the balance efficiency of the
+// column split, HBM time of weights + split-K partials). MFMA at 60% of 2.5 PFLOP/s, HBM at
+// 5.5 TB/s: only the ratio of the two matters for the choice.
+bool plan_wide(int M, int K, int N, GemmPlan& p) {
+  if (M <= 64 || K % KC != 0 || N % 16 != 0) return false;
+  const int units = N / 16;
+  const double flops = 2.0 * M * (double)N * K;
+  double best = 1e30;
+  for (int s = 1; s <= 4; s *= 2) {
+    if (K / KC < 2 * s) break;
+    const int groups = units < WIDE_WG / s ? units : WIDE_WG / s;
+    const int need = (units + groups - 1) / groups;
+    int ntm = 0;
+    for (int v : kWideNT)
+      if (v >= need) { ntm = v; break; }
+    if (ntm == 0) continue;
+    const double eff = (double)units / groups / need;
+    const double bytes = (double)K * N + (s > 1 ? 2.0 * s * M * (double)N * 4 : 0.0);
+    const double t = flops / (eff * 0.6 * 2.5e15) > bytes / 5.5e12 ? flops / (eff * 0.6 * 2.5e15)
+                                                                      : bytes / 5.5e12;
+    if (t < best * 0.97) {
+      best = t;
+      p.wide = true;
+      p.units = units;
+      p.groups = groups;
+      p.split_k = s;
+      p.ntm = ntm;
+    }
+  }
+  if (!p.wide) return false;
+  p.passes = (M + 255) / 256;
+  p.ws = p.split_k > 1 ? (size_t)p.split_k * M * N * sizeof(float) : 0;
+  return true;
+}
 
 GemmPlan plan(int M, int K, int N) {
   GemmPlan p{};
+  if (plan_wide(M, K, N, p)) return p;
+  p = GemmPlan{};
   const int mtiles = (M + 15) / 16;
   p.mt = mtiles >= 8 ? 8 : (mtiles >= 4 ? 4 : (mtiles >= 2 ? 2 : 1));
   p.passes = (M + 16 * p.mt - 1) / (16 * p.mt);
@@ -232,6 +438,26 @@ extern "C" int npn_fp8_matmul(const uint16_t* x, const int8_t* w, const float* s
     NPN_REQUIRE(NPN_ALIGNED16(workspace), NPN_ERR_ALIGN);
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (p.wide) {
+    WideArgs wa{x, reinterpret_cast<const uint8_t*>(w), scale, out,
+                static_cast<float*>(workspace), M, K, N, p.units, p.groups, p.split_k};
+    const int nwg = ((p.groups * p.split_k + 7) / 8) * 8;  // multiple of 8 for the XCD map
+    const dim3 grid(nwg, p.passes);
+    switch (p.ntm) {
+      case 1: hipLaunchKernelGGL(fp8_gemm_wide_kernel<1>, grid, dim3(256), 0, s, wa); break;
+      case 2: hipLaunchKernelGGL(fp8_gemm_wide_kernel<2>, grid, dim3(256), 0, s, wa); break;
+      case 3: hipLaunchKernelGGL(fp8_gemm_wide_kernel<3>, grid, dim3(256), 0, s, wa); break;
+      case 5: hipLaunchKernelGGL(fp8_gemm_wide_kernel<5>, grid, dim3(256), 0, s, wa); break;
+      default: hipLaunchKernelGGL(fp8_gemm_wide_kernel<9>, grid, dim3(256), 0, s, wa); break;
+    }
+    if (p.split_k > 1) {
+      const size_t total = (size_t)M * N;
+      hipLaunchKernelGGL(fp8_splitk_reduce_kernel, dim3((unsigned)((total + 255) / 256)),
+                         dim3(256), 0, s, static_cast<const float*>(workspace), scale, out, M, N,
+                         p.split_k);
+    }
+    return npn_launch_status();
+  }
   GemmArgs ga{x, reinterpret_cast<const uint8_t*>(w), scale, out,
               static_cast<float*>(workspace), M, K, N, p.split_k};
   const dim3 grid(N / NW, p.split_k, p.passes);

@@ -166,9 +166,7 @@ __global__ __launch_bounds__(NRT * 64, 2) void gqa_attn_kernel(AttnArgs a) {
       key = key < kend ? key : kend - 1;
       const int sq = q ^ (isv ? vswz(r) : kswz(r));
       const uint16_t* src = (isv ? vb : kb) + (size_t)key * DH + sq * 8;
-      __builtin_amdgcn_global_load_lds(
-          (const __attribute__((address_space(1))) void*)src,
-          (__attribute__((address_space(3))) void*)(&smem[s & 1][isv][it * 2 * DH * 2]), 16, 0, 0);
+      npn::lds_dma16(src, &smem[s & 1][isv][it * 2 * DH * 2]);
     }
   };
   dma(0);
@@ -198,7 +196,8 @@ __global__ __launch_bounds__(NRT * 64, 2) void gqa_attn_kernel(AttnArgs a) {
   for (int s = 0; s < steps; ++s) {
     const int k0 = c0 + s * KS;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's DMA of step s landed
-    __syncthreads();                                  // ... and every other wave's
+    __builtin_amdgcn_s_barrier();                     // ... and every other wave's
+    asm volatile("" ::: "memory");
     if (s + 1 < steps) dma(s + 1);                    // buffer (s+1)&1 is free again
     const uint8_t* kt_lds = smem[s & 1][0];
     const uint8_t* vt_lds = smem[s & 1][1];
@@ -274,8 +273,8 @@ __global__ __launch_bounds__(NRT * 64, 2) void gqa_attn_kernel(AttnArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------
-// 3. merge chunk partials, apply sigmoid(gate), write bf16. One block per (b, kv head),
-//    thread d owns output dim d.
+// 3. merge chunk partials, apply sigmoid(gate), write bf16. One 64-thread block per
+//    (query row, b, kv head); lane l owns output dims 4l..4l+3 (float4 partial reads).
 struct MergeArgs {
   const float* part_o;
   const float* part_ml;
@@ -285,29 +284,38 @@ struct MergeArgs {
   int T, Hq, Hkv, R, nch, s_max;
 };
 
-__global__ __launch_bounds__(256) void gqa_merge_kernel(MergeArgs a) {
-  const int bg = blockIdx.x;
+__global__ __launch_bounds__(64) void gqa_merge_kernel(MergeArgs a) {
+  const int r = blockIdx.x;
+  const int bg = blockIdx.y;
   const int b = bg / a.Hkv, g = bg - b * a.Hkv;
   const int grp = a.Hq / a.Hkv;
-  const int d = threadIdx.x;
+  const int lane = threadIdx.x;
   const int L = a.kv_len[b] > 0 ? a.kv_len[b] : 0;
   const int kend = L + a.T < a.s_max ? L + a.T : a.s_max;
   const int nc = (kend + CH - 1) / CH;
-  const float* po = a.part_o + (size_t)bg * a.nch * a.R * DH;
-  const float* pml = a.part_ml + (size_t)bg * a.nch * a.R * 2;
-  for (int r = 0; r < a.T * grp; ++r) {
-    float M = kNegBig;
-    for (int c = 0; c < nc; ++c) M = fmaxf(M, pml[((size_t)c * a.R + r) * 2]);
-    float l = 0.f, o = 0.f;
-    for (int c = 0; c < nc; ++c) {
-      const float f = exp2f(pml[((size_t)c * a.R + r) * 2] - M);
-      l += f * pml[((size_t)c * a.R + r) * 2 + 1];
-      o += f * po[((size_t)c * a.R + r) * DH + d];
-    }
-    const int t = r / grp, qh = g * grp + (r - t * grp);
-    const size_t oi = (((size_t)b * a.T + t) * a.Hq + qh) * DH + d;
-    a.out[oi] = npn::f32_to_bf16(o / l * npn::sigmoid(npn::bf16_to_f32(a.gate[oi])));
+  const float* pml = a.part_ml + ((size_t)bg * a.nch * a.R + r) * 2;
+  const float* po = a.part_o + ((size_t)bg * a.nch * a.R + r) * DH + 4 * lane;
+  const size_t cstride_ml = (size_t)a.R * 2, cstride_o = (size_t)a.R * DH;
+  float M = kNegBig;
+  for (int c = 0; c < nc; ++c) M = fmaxf(M, pml[c * cstride_ml]);
+  float l = 0.f;
+  f32x4 o = {0.f, 0.f, 0.f, 0.f};
+  for (int c = 0; c < nc; ++c) {
+    const float f = exp2f(pml[c * cstride_ml] - M);
+    l += f * pml[c * cstride_ml + 1];
+    o += f * *reinterpret_cast<const f32x4*>(po + c * cstride_o);
   }
+  const int t = r / grp, qh = g * grp + (r - t * grp);
+  const size_t oi = (((size_t)b * a.T + t) * a.Hq + qh) * DH + 4 * lane;
+  const float inv = 1.0f / l;
+  uint32_t w[2];
+  for (int j = 0; j < 2; ++j) {
+    const float g0 = npn::sigmoid(npn::bf16_to_f32(a.gate[oi + 2 * j]));
+    const float g1 = npn::sigmoid(npn::bf16_to_f32(a.gate[oi + 2 * j + 1]));
+    w[j] = npn::f32_to_bf16(o[2 * j] * inv * g0) |
+           ((uint32_t)npn::f32_to_bf16(o[2 * j + 1] * inv * g1) << 16);
+  }
+  *reinterpret_cast<uint2*>(a.out + oi) = make_uint2(w[0], w[1]);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -515,7 +523,7 @@ extern "C" int npn_gqa_tail_verify(const uint16_t* query, const uint16_t* gate,
   else hipLaunchKernelGGL(gqa_attn_kernel<3>, grid, dim3(192), 0, s, aa);
 
   MergeArgs ma{po, pml, kv_len, gate, out, T, q_heads, kv_heads, p.R, p.nch, s_max};
-  hipLaunchKernelGGL(gqa_merge_kernel, dim3(B * kv_heads), dim3(DH), 0, s, ma);
+  hipLaunchKernelGGL(gqa_merge_kernel, dim3(T * p.grp, B * kv_heads), dim3(64), 0, s, ma);
   return npn_launch_status();
 }
 

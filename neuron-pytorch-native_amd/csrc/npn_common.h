@@ -49,6 +49,19 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// ---- LDS DMA -----------------------------------------------------------------------------
+// 16 bytes per lane from global address g into LDS at lds_base + 16 * lane
+// (global_load_lds_dwordx4; lds_base must be the same for the whole wave). Issued through
+// inline asm so the compiler does not add a conservative vmcnt(0) wait before later LDS
+// reads of other buffers: callers track completion themselves with s_waitcnt vmcnt(n)
+// and make it visible to the other waves with s_barrier.
+__device__ __forceinline__ void lds_dma16(const void* g, const void* lds_base) {
+  const unsigned base = __builtin_amdgcn_readfirstlane(
+      (unsigned)(uintptr_t)(__attribute__((address_space(3))) const void*)lds_base);
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(base)
+               : "memory", "m0");
+}
+
 }  // namespace npn
 
 // ---- host-side checks ------------------------------------------------------------------

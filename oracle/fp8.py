@@ -46,8 +46,9 @@ _POS_VALUES = decode_e4m3fn(_POS_CODES).astype(np.float64)
 
 
 def encode_e4m3fn(x):
-    """float -> e4m3fn bytes (uint8), round to nearest, ties to even code; values
-    beyond 448 saturate to +-448 (callers clamp first, as the reference does)."""
+    """float -> e4m3fn bytes (uint8), round to nearest, ties to even code, sign kept on
+    values that round to zero; values beyond 448 saturate to +-448 (callers clamp first,
+    as the reference does)."""
     x = np.asarray(x, np.float64)
     a = np.minimum(np.abs(x), 448.0)
     idx = np.searchsorted(_POS_VALUES, a)                          # first value >= a
@@ -56,8 +57,7 @@ def encode_e4m3fn(x):
     pick_hi = (a - lo > hi - a) | ((a - lo == hi - a) & ((idx % 2) == 0))
     code = np.where(pick_hi, idx, idx - 1).astype(np.uint8)
     code = np.where(a == 0.0, 0, code).astype(np.uint8)
-    neg = (np.signbit(x)) & (code != 0)
-    return np.where(neg, code | 0x80, code).astype(np.uint8)
+    return np.where(np.signbit(x), code | 0x80, code).astype(np.uint8)   # -0 stays -0 (0x80)
 
 
 def quantize_fp8_per_channel(w_bits, fp8_max=448.0):

@@ -31,8 +31,10 @@ ROPE_DIM = 64
 
 def rope_cos_sin(positions, theta=1e7, rope_dim=ROPE_DIM):
     """cos/sin rows for integer positions, float32 like the reference table
-    (static_decode.py:489-502): inv_freq = 1/theta^(arange(0,d,2)/d); emb = cat(f, f)."""
-    inv_freq = (1.0 / (np.float32(theta) ** (np.arange(0, rope_dim, 2, dtype=np.float32) / np.float32(rope_dim)))).astype(np.float32)
+    (static_decode.py:489-502): inv_freq = 1/theta^(arange(0,d,2)/d) rounded to fp32,
+    freqs = fp32(pos * inv_freq), emb = cat(f, f). The kernels take these tables as inputs;
+    tests feed the same table to the device and the oracle."""
+    inv_freq = (1.0 / (float(theta) ** (np.arange(0, rope_dim, 2, dtype=np.float64) / rope_dim))).astype(np.float32)
     pos = np.asarray(positions, dtype=np.float32)
     freqs = (pos[..., None] * inv_freq).astype(np.float32)
     emb = np.concatenate([freqs, freqs], axis=-1)

@@ -40,7 +40,7 @@ def silu(x):
 
 
 def sigmoid(x):
-    return 1.0 / (1.0 + np.exp(-x))
+    return np.exp(-np.logaddexp(0.0, -np.asarray(x, np.float64)))
 
 
 def softplus(x):

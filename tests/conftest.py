@@ -10,8 +10,9 @@ import sys
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-KERNELS = os.path.join(ROOT, "neuron-pytorch-native_amd", "kernels")
-for p in (ROOT, KERNELS):
+PKG = os.path.join(ROOT, "neuron-pytorch-native_amd")
+KERNELS = os.path.join(PKG, "kernels")
+for p in (ROOT, PKG, KERNELS, os.path.dirname(os.path.abspath(__file__))):
     if p not in sys.path:
         sys.path.insert(0, p)
 

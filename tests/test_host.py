@@ -1,0 +1,104 @@
+"""Host-side checks that need no GPU: the C-ABI library loads and exports every entry
+point include/npn_spec_verify.h declares (no compute calls), the host-only size queries and
+status texts, shape propagation of every registered op under FakeTensorMode, and that the
+ops refuse CPU tensors instead of falling back to a CPU path."""
+import os
+import re
+
+import pytest
+import torch
+
+from conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "npn_spec_verify.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(npn_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    import npn_native
+    lib = npn_native.lib()
+    names = _declared()
+    assert len(names) >= 14
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in the header but not exported"
+    assert set(names) == set(npn_native.SIGNATURES)
+
+
+def test_status_strings_and_version():
+    import npn_native
+    lib = npn_native.lib()
+    assert lib.npn_abi_version() == 100
+    assert lib.npn_status_string(0) == b"ok"
+    for code in range(1, 7):
+        assert lib.npn_status_string(code) not in (b"ok", b"unknown status")
+    assert lib.npn_status_string(99) == b"unknown status"
+
+
+def test_size_queries():
+    import npn_native
+    q = npn_native.query
+    assert q("npn_gqa_tail_verify_workspace_size", 16, 8, 24, 4, 32776) > 0
+    assert q("npn_gqa_tail_verify_workspace_size", 16, 8, 24, 4, 4) == 0        # s_max < T
+    assert q("npn_gqa_tail_verify_workspace_size", 1, 9, 24, 4, 1024) == 0      # 54 rows > 48
+    assert q("npn_accept_workspace_size", 32, 7, 151936) > 0
+    assert q("npn_accept_workspace_size", 32, 0, 151936) == 0
+    assert q("npn_fp8_matmul_workspace_size", 8, 5120, 17408) >= 0
+    assert q("npn_fp8_matmul_workspace_size", 8, 100, 17408) == 0
+
+
+def test_ops_register_and_propagate_shapes():
+    import npn_ops  # noqa: F401
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    B, T, Hk, Hv, D = 2, 8, 16, 48, 128
+    QKV = (2 * Hk + Hv) * D
+    with FakeTensorMode():
+        f32, bf = torch.float32, torch.bfloat16
+        st = torch.empty(B * Hv * D, D, dtype=f32)
+        args = (torch.empty(B * T * QKV, dtype=bf), torch.empty(B * QKV, 3, dtype=bf),
+                torch.empty(QKV, 4), torch.empty(QKV), torch.empty(B * T * Hv),
+                torch.empty(B * T * Hv), torch.empty(B * T * Hv, D, dtype=bf), torch.empty(Hv),
+                torch.empty(Hv), torch.empty(D))
+        ck, out = torch.ops.deltanet.verify_batched(st, *args)
+        assert ck.shape == (B * T * Hv * D, D) and out.shape == (B * T * Hv, D)
+        y = torch.ops.fp8.matmul(torch.empty(64, 5120, dtype=bf),
+                                 torch.empty(5120, 17408, dtype=torch.int8), torch.empty(17408, 1))
+        assert y.shape == (64, 17408) and y.dtype == bf
+        q = torch.empty(B, T, 24, 256, dtype=bf)
+        o = torch.ops.gqa.tail_verify(q, q, torch.empty(256), torch.empty(B, T, 64),
+                                      torch.empty(B, T, 64), torch.empty(B, 4, 100, 256, dtype=bf),
+                                      torch.empty(B, 4, 100, 256, dtype=bf),
+                                      torch.empty(B, dtype=torch.int32))
+        assert o.shape == q.shape
+        acc, ids = torch.ops.spec.accept_greedy(torch.empty(B, T, 1000),
+                                                torch.empty(B, T - 1, dtype=torch.int64))
+        assert acc.shape == (B,) and ids.shape == (B, T)
+
+
+def test_ops_refuse_cpu_tensors():
+    """No CPU fallback: the ops are registered for HIP devices only."""
+    import npn_ops  # noqa: F401
+    x = torch.zeros(4, 64, dtype=torch.bfloat16)
+    w = torch.zeros(64, 64, dtype=torch.int8)
+    with pytest.raises((NotImplementedError, RuntimeError)):
+        torch.ops.fp8.matmul(x, w, torch.ones(64, 1))
+
+
+def test_rope_tables_match_oracle():
+    """The step's table generator (torch fp32, as the reference's _init_rope) and the
+    oracle's agree: inv_freq to 1 fp32 ulp, cos/sin tightly where position * ulp is small."""
+    import numpy as np
+    from oracle.gqa import rope_cos_sin
+    from spec_verify_step import rope_tables
+    pos = torch.arange(0, 2048, 7).reshape(1, -1)
+    c, s = rope_tables(pos)
+    rc, rs = rope_cos_sin(pos.numpy())
+    np.testing.assert_allclose(c.numpy(), rc, rtol=0, atol=2e-4)
+    np.testing.assert_allclose(s.numpy(), rs, rtol=0, atol=2e-4)
+    inv_t = 1.0 / (1e7 ** (torch.arange(0, 64, 2).float() / 64))
+    inv_o = (1.0 / (1e7 ** (np.arange(0, 64, 2) / 64.0))).astype(np.float32)
+    ulps = np.abs(inv_t.numpy().view(np.int32) - inv_o.view(np.int32))
+    assert ulps.max() <= 1

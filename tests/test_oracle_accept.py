@@ -1,0 +1,157 @@
+"""CPU pinning of oracle/accept.py.
+
+Greedy: argmax_first against torch.argmax on the tie/ownership cases of
+contrib/qwen3.6-35b-a3b/kernels/tests/test_decode_sharded_lm_cpu.py:29-46 and NaN rows;
+accept_greedy on constructed draft sequences.
+
+Rejection sampling (no reference vectors exist; pinned against the mathematics):
+- expfix: E(0) = 2^32, monotone, within max(2 quanta, 2^-21 relative) of floor(2^32 exp(x)),
+  0 below -32;
+- the exact distribution of the first emitted token implied by the integer contract
+  (acceptance probabilities counted over all 2^24 uniforms, residual picked by counting
+  uniforms per token) equals p = E^p / Z^p within 2^-22 (Leviathan et al. 2023, Thm 1);
+- _inverse_cdf selects the right token on both sides of every boundary uniform;
+- a chi-square test of the full accept_rejection output against p;
+- p == q accepts every draft; q(x) > 0 = p(x) always rejects and resamples from the
+  positive part of p - q.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import accept as oa
+
+U = 1 << 24
+
+
+def test_argmax_ties_and_ownership():
+    generator = torch.Generator().manual_seed(20260717)
+    logits = torch.randn(37, 256, generator=generator)
+    for rank in range(8):
+        logits[rank, rank * 32 + 11] = 100 + rank
+    logits[8, 7] = 200
+    logits[8, 13] = 200
+    logits[9, 63] = 300
+    logits[9, 192] = 300
+    logits[10] = 0
+    assert np.array_equal(oa.argmax_first(logits.numpy()), logits.argmax(-1).numpy())
+
+
+def test_argmax_nan_first():
+    x = torch.randn(3, 50)
+    x[0, 7] = float("nan")
+    x[0, 30] = float("nan")
+    x[1, 49] = float("nan")
+    assert np.array_equal(oa.argmax_first(x.numpy()), x.argmax(-1).numpy())
+
+
+def test_accept_greedy_cases():
+    t = torch.randn(3, 5, 100).numpy()
+    tid = t.argmax(-1)
+    d = tid[:, :4].copy()
+    d[1, 2] = (d[1, 2] + 1) % 100      # mismatch at position 2
+    d[2, 0] = (d[2, 0] + 1) % 100      # immediate mismatch
+    acc, out = oa.accept_greedy(t, d)
+    assert acc.tolist() == [4, 2, 0]
+    assert out[0].tolist() == tid[0].tolist()
+    assert out[1].tolist() == tid[1, :3].tolist() + [-1, -1]
+    assert out[2].tolist() == [tid[2, 0], -1, -1, -1, -1]
+
+
+def test_expfix_properties():
+    x = np.sort(-np.random.default_rng(0).exponential(4.0, 100000).astype(np.float32))
+    E = oa.expfix(x)
+    assert oa.expfix(np.float32([0.0]))[0] == 1 << 32
+    assert np.all(np.diff(E.astype(np.int64)) >= 0)                    # monotone in x
+    ref = np.floor(np.exp(x.astype(np.float64)) * 2.0 ** 32)
+    # within 2 quanta (2^-31 absolute) or 2^-21 relative, whichever is larger
+    assert np.all(np.abs(E - ref) <= np.maximum(2.0, ref * 2.0 ** -21))
+    assert np.all(oa.expfix(np.float32([-32.0, -40.0, -1e30])) == 0)
+
+
+def _first_token_distribution(t_row, d_row):
+    """Exact P(first emitted token = v) for K = 1 under the integer contract, with the draft
+    token drawn from the contract's own q = E^q / Z^q."""
+    Ep, Zp, _ = oa.row_weights(t_row)
+    Eq, Zq, _ = oa.row_weights(d_row)
+    V = len(Ep)
+    p_acc = np.zeros(V)
+    for x in range(V):
+        if Eq[x] == 0:
+            p_acc[x] = 1.0
+            continue
+        n = (int(Ep[x]) * Zq * U) // (int(Eq[x]) * Zp) + 1               # U*Eq*Zp <= 2^24*Ep*Zq
+        p_acc[x] = min(U, n) / U
+    q = np.array([int(e) for e in Eq], dtype=object) / Zq
+    reject = float(sum(q[x] * (1 - p_acc[x]) for x in range(V)))
+    R = [max(0, int(ep) * Zq - int(eq) * Zp) for ep, eq in zip(Ep, Eq)]
+    S = sum(R)
+    frac = np.zeros(V)
+    if S:
+        c_prev = 0
+        for v, r in enumerate(R):
+            c = c_prev + r
+            lo = -(-(c_prev * U) // S)            # smallest U_s with 2^24 * c_prev <= U_s * S ... picks v
+            hi = -(-(c * U) // S)
+            frac[v] = (min(hi, U) - min(lo, U)) / U
+            if r and lo < U:                      # boundary uniforms select v / the token before
+                assert oa._inverse_cdf(R, lo) == v
+                if lo > 0:
+                    assert oa._inverse_cdf(R, lo - 1) < v
+            c_prev = c
+    dist = np.array([float(q[v]) * p_acc[v] for v in range(V)]) + reject * frac
+    p = np.array([int(e) for e in Ep], dtype=np.float64) / Zp
+    return dist, p
+
+
+@pytest.mark.parametrize("seed,V", [(0, 5), (1, 17), (2, 40), (3, 3)])
+def test_exact_output_distribution_is_p(seed, V):
+    rng = np.random.default_rng(seed)
+    t = (rng.standard_normal(V) * 2).astype(np.float32)
+    d = (0.8 * t + 0.6 * rng.standard_normal(V) * 2).astype(np.float32)
+    dist, p = _first_token_distribution(t, d)
+    assert abs(dist.sum() - 1.0) < 2.0 ** -20
+    assert np.max(np.abs(dist - p)) < 2.0 ** -22
+
+
+def test_chi_square_full_function():
+    rng = np.random.default_rng(11)
+    V, N = 8, 20000
+    t_row = rng.standard_normal(V).astype(np.float32)
+    d_row = (0.5 * t_row + rng.standard_normal(V)).astype(np.float32)
+    q = np.exp(d_row - d_row.max()); q /= q.sum()
+    target = np.broadcast_to(np.stack([t_row, t_row]), (N, 2, V)).copy()
+    draft = np.broadcast_to(d_row, (N, 1, V)).copy()
+    ids = rng.choice(V, size=(N, 1), p=q)
+    u = rng.random((N, 1)).astype(np.float32)
+    us = rng.random(N).astype(np.float32)
+    _, out = oa.accept_rejection(target, draft, ids, u, us)
+    counts = np.bincount(out[:, 0], minlength=V)
+    p = np.exp(t_row - t_row.max()); p /= p.sum()
+    chi2 = float(((counts - N * p) ** 2 / (N * p)).sum())
+    assert chi2 < 24.3      # chi-square, 7 degrees of freedom, p = 0.001
+
+
+def test_equal_distributions_always_accept():
+    rng = np.random.default_rng(4)
+    t = rng.standard_normal((6, 4, 30)).astype(np.float32)
+    ids = rng.integers(0, 30, (6, 3))
+    u = (1 - 2.0 ** -24) * np.ones((6, 3), np.float32)    # largest uniform
+    acc, out = oa.accept_rejection(t, t[:, :3].copy(), ids, u, rng.random(6).astype(np.float32))
+    assert (acc == 3).all() and np.array_equal(out[:, :3], ids)
+
+
+def test_zero_target_mass_always_rejects():
+    rng = np.random.default_rng(5)
+    V = 12
+    t = rng.standard_normal((4, 2, V)).astype(np.float32)
+    d = t[:, :1].copy()
+    x = 3
+    t[:, 0, x] = -1e4                                         # p(x) = 0 under the contract
+    u = np.full((4, 1), 2.0 ** -24, np.float32)               # smallest positive uniform
+    acc, out = oa.accept_rejection(t, d, np.full((4, 1), x), u, rng.random(4).astype(np.float32))
+    assert (acc == 0).all()
+    Ep, Zp, _ = oa.row_weights(t[0, 0])
+    Eq, Zq, _ = oa.row_weights(d[0, 0])
+    positive = [int(ep) * Zq > int(eq) * Zp for ep, eq in zip(Ep, Eq)]
+    assert all(positive[v] for v in out[:, 0]) and x not in out[:, 0]

@@ -9,16 +9,21 @@
 // Verify tail (T tokens x grp q-heads per kv head = R query rows per (b, kv head)):
 //  1. qprep: q' per row, scaled by log2(e)/16 and split into bf16 hi + lo parts
 //     (hi = bf16(q'), lo = bf16(q' - hi)), so the bf16 MFMA sees q' to ~16 mantissa bits.
-//  2. attn: split-KV. One workgroup per (chunk of 512 keys, b, kv head), one wave per
-//     16-row tile of the R rows; the chunk streams through LDS in 32-key K/V tiles:
+//  2. attn: split-KV over a balanced partition. The (b, kv head) pairs' 32-key steps
+//     are laid end to end (prefix sums from a one-block plan kernel) and cut into
+//     kAttnWG equal ranges, one per workgroup, so every workgroup streams the same
+//     number of K/V bytes whatever the kv_len spread; a range may cover the end of one
+//     pair and the start of the next. One wave per 16-row tile of the R rows; each
+//     pair segment streams through LDS in 32-key K/V tiles:
 //       S^T[32 keys x 16] = K Q'^T  (K rows from LDS as MFMA A operands, q' hi/lo held in
 //                                   VGPRs as B operands)              v_mfma_f32_16x16x32_bf16
 //       online softmax per row in fp32 (exp2), causal limit kv_len + t per row
 //       O^T[256 x 16] += V^T P^T    (V tile read back transposed with ds_read_b64_tr_b16;
 //                                   P hi/lo in bf16, taken directly from the S^T
 //                                   accumulator registers)
-//     Each wave writes its rows' (m, l, O) partial for the chunk.
-//  3. merge: log-sum-exp merge of the chunk partials, * sigmoid(gate) -> bf16.
+//     Each wave writes its rows' (m, l, O) partial per pair segment, into slot w + p
+//     (workgroup w, pair p: unique, as a workgroup's pairs are consecutive).
+//  3. merge: log-sum-exp merge of a pair's segment partials, * sigmoid(gate) -> bf16.
 //
 // HBM layout: cache [B][Hkv][s_max][256] bf16, each (b, kv head) a contiguous block of
 // rows; query/gate/out [B][T][Hq][256]; query row r of (b, g) is token r / grp,
@@ -33,7 +38,8 @@ constexpr float kEps = 1e-6f;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegBig = -1.0e30f;   // finite "no key yet" running max (avoids inf - inf)
 
-constexpr int CH = 512;               // keys per workgroup (split-KV chunk)
+constexpr int kAttnWG = 512;          // attention workgroups (2 per CU on a 256-CU part)
+constexpr float kRescaleLog2 = 8.0f;  // exponent base moves only when a row max grows > 2^8
 constexpr int KS = 32;                // keys per step
 
 typedef __bf16 bf16x8 __attribute__((__vector_size__(8 * sizeof(__bf16))));
@@ -114,196 +120,350 @@ __global__ __launch_bounds__(256) void gqa_qprep_kernel(QPrepArgs a) {
 // 2. split-KV attention over one 512-key chunk of one (b, kv head).
 //    Workgroup = NRT waves; wave w owns query rows 16w..16w+15 (its q' hi/lo lives in
 //    VGPRs as MFMA B operands) and all waves share each 32-key K/V tile, which is DMA'd
-//    from HBM straight into LDS (global_load_lds_dwordx4), double-buffered.
-//    Tile rows keep their 16-byte chunks XOR-swizzled (K: kswz, V: vswz) so the MFMA
-//    operand reads of 16 rows at one column spread over the LDS banks.
+//    from HBM straight into LDS (global_load_lds_dwordx4) through an NST-stage ring.
+//
+//    LDS tile layout: one DMA instruction (64 lanes x 16 B) moves cache rows 2k and 2k+1
+//    into "block" k, interleaved by 16-byte chunk: lane l carries row 2k + (l & 1), chunk
+//    l >> 1, so chunk c of row r sits at block(r >> 1) + (2c + (r & 1)) * 16. Blocks are
+//    1024 B plus a pad (K: 32 B, V: 64 B). With that layout
+//      - every DMA source is the wave-uniform address of row 2k plus a per-lane constant
+//        ((l & 1) * 512 + (l >> 1) * 16), and
+//      - every MFMA operand read is one per-lane base plus an immediate offset,
+//    and the reads spread over the LDS banks: 16 K rows at one column land on 16 distinct
+//    16-byte bank groups (pad 32), and the transposed V reads of 4 rows x 64 B per 16-lane
+//    group on 4 distinct 64-byte groups (pad 64).
 struct AttnArgs {
   const uint16_t* qhi;
   const uint16_t* qlo;
   const uint16_t* cache_k;
   const uint16_t* cache_v;
   const int32_t* kv_len;
-  float* part_o;   // [B*Hkv][nch][R][DH]
-  float* part_ml;  // [B*Hkv][nch][R][2]
-  int Hkv, s_max, T, grp, nch;
+  const int32_t* pstart;  // [P + 1] first step of each pair; pstart[P] = total steps
+  float* part_o;          // [kAttnWG + P][R][DH]
+  float* part_ml;         // [kAttnWG + P][R][2]
+  int Hkv, s_max, T, grp, npairs;
 };
 
-__device__ __forceinline__ int kswz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
-__device__ __forceinline__ int vswz(int r) { return (r & 7) << 1; }
+// Steps of pair p = (b, kv head): ceil(kend_b / KS), kend_b = min(kv_len[b] + T, s_max).
+__device__ __forceinline__ int pair_kend(const int32_t* kv_len, int b, int T, int s_max) {
+  const int L = kv_len[b] > 0 ? kv_len[b] : 0;
+  return L + T < s_max ? L + T : s_max;
+}
 
-template <int NRT>
-__global__ __launch_bounds__(NRT * 64, 2) void gqa_attn_kernel(AttnArgs a) {
+// Workgroup w's step range is [w * S / kAttnWG, (w + 1) * S / kAttnWG).
+__device__ __forceinline__ int wg_first_step(int w, int S) {
+  return (int)((int64_t)w * S / kAttnWG);
+}
+
+// One-block plan: pstart[p] = sum of the steps of pairs before p (exclusive scan).
+__global__ __launch_bounds__(1024) void gqa_plan_kernel(const int32_t* kv_len, int32_t* pstart,
+                                                        int P, int Hkv, int T, int s_max) {
+  __shared__ int part[1024];
+  const int t = threadIdx.x;
+  const int per = (P + 1023) / 1024;
+  const int p0 = min(P, t * per), p1 = min(P, p0 + per);
+  int sum = 0;
+  for (int p = p0; p < p1; ++p) sum += (pair_kend(kv_len, p / Hkv, T, s_max) + KS - 1) / KS;
+  part[t] = sum;
+  __syncthreads();
+  for (int off = 1; off < 1024; off <<= 1) {  // inclusive Hillis-Steele scan
+    const int v = t >= off ? part[t - off] : 0;
+    __syncthreads();
+    part[t] += v;
+    __syncthreads();
+  }
+  int run = part[t] - sum;
+  for (int p = p0; p < p1; ++p) {
+    pstart[p] = run;
+    run += (pair_kend(kv_len, p / Hkv, T, s_max) + KS - 1) / KS;
+  }
+  if (t == 1023) pstart[P] = part[1023];
+}
+
+// Largest p in [0, P) with pstart[p] <= x (pstart is strictly increasing, pstart[0] = 0):
+// 64-way search, one sample per lane per round. Wave-uniform result.
+__device__ __forceinline__ int find_pair(const int32_t* pstart, int P, int x, int lane) {
+  int lo = 0, n = P;
+  while (n > 1) {
+    const int stride = (n + 63) / 64;
+    const int idx = lo + lane * stride;
+    const bool le = idx < lo + n && pstart[idx] <= x;
+    const int t = __popcll(__builtin_amdgcn_ballot_w64(le)) - 1;  // last lane with le
+    const int nlo = lo + t * stride;
+    n = min(stride, lo + n - nlo);
+    lo = nlo;
+  }
+  return __builtin_amdgcn_readfirstlane(lo);
+}
+
+constexpr int KBLK = 1024 + 32;            // bytes per 2-row block of the K tile
+constexpr int VBLK = 1024 + 64;            // ... of the V tile
+constexpr int KTILE = (KS / 2) * KBLK;     // 16896
+constexpr int VTILE = (KS / 2) * VBLK;     // 17408
+constexpr int STAGE = KTILE + VTILE + 1024;  // + one block of slack for padded DMA slots
+
+// Reductions over the 4 lane groups (lanes i, i+16, i+32, i+48) that hold one query row,
+// with gfx950's cross-row swaps instead of LDS permutes: after permlane32_swap(x, x) the
+// pair holds (x[l & 31], x[(l & 31) + 32]); after permlane16_swap(y, y) it holds the two
+// 16-lane rows of y's 32-lane half.
+__device__ __forceinline__ float max_over_groups(float x) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float sum_over_groups(float x) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+template <int NRT, int NST>  // NST: K/V ring stages
+__global__ __launch_bounds__(NRT * 64, NST <= 2 ? 2 : 1) void gqa_attn_kernel(AttnArgs a) {
   constexpr int R = NRT * 16;
-  constexpr int TILE = KS * DH * 2;  // bytes of one 32-key K or V tile
-  const int c = blockIdx.x;
-  const int bg = blockIdx.y;
-  const int b = bg / a.Hkv;
-  const int L = a.kv_len[b] > 0 ? a.kv_len[b] : 0;
-  const int kend = L + a.T < a.s_max ? L + a.T : a.s_max;  // rows [0, kend) are read
-  const int c0 = c * CH;
-  if (c0 >= kend) return;
+  constexpr int DPW = (KS + NRT - 1) / NRT;  // DMA instructions per wave per step
+  const int wg = blockIdx.x;
+  const int S = a.pstart[a.npairs];
+  int x = wg_first_step(wg, S);
+  const int x_end = wg_first_step(wg + 1, S);
+  if (x >= x_end) return;
 
-  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int i = lane & 15, G = lane >> 4;
   const int row = w * 16 + i;  // this lane's query row (B-operand column / C column)
 
-  __shared__ __attribute__((aligned(16))) uint8_t smem[2][2][TILE];  // [buffer][K|V]
+  __shared__ __attribute__((aligned(16))) uint8_t smem[NST * STAGE];
 
-  const uint16_t* kb = a.cache_k + (size_t)bg * a.s_max * DH;
-  const uint16_t* vb = a.cache_v + (size_t)bg * a.s_max * DH;
-  const int steps = min(CH / KS, (kend - c0 + KS - 1) / KS);
-
-  // DMA of step s's K and V tiles into buffer s&1: 32 instructions of 1 KiB (2 rows each),
-  // spread over the NRT waves.
-  auto dma = [&](int s) {
-    const int k0 = c0 + s * KS;
-    for (int j = w; j < 2 * (KS / 2); j += NRT) {
-      const int isv = j >= KS / 2;
-      const int it = isv ? j - KS / 2 : j;
-      const int r = 2 * it + (lane >> 5);
-      const int q = lane & 31;
-      int key = k0 + r;
-      key = key < kend ? key : kend - 1;
-      const int sq = q ^ (isv ? vswz(r) : kswz(r));
-      const uint16_t* src = (isv ? vb : kb) + (size_t)key * DH + sq * 8;
-      npn::lds_dma16(src, &smem[s & 1][isv][it * 2 * DH * 2]);
-    }
-  };
-  dma(0);
-
-  // q' hi/lo of this lane's row as B operands: dims 32*ks + 8*G .. +7.
-  u32x4 qh[8], ql[8];
-  {
-    const size_t qo = ((size_t)bg * R + row) * DH + 8 * G;
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
-      qh[ks] = *reinterpret_cast<const u32x4*>(a.qhi + qo + 32 * ks);
-      ql[ks] = *reinterpret_cast<const u32x4*>(a.qlo + qo + 32 * ks);
-    }
-  }
-  const int lim = row < a.T * a.grp ? L + row / a.grp : kend - 1;  // last key this row sees
-
-  float m_run = kNegBig, l_run = 0.f;
-  f32x4 acc[16];
-#pragma unroll
-  for (int dt = 0; dt < 16; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  // Transposed V reads: this lane supplies rows 4G + (i>>2) (+16), dims 16*dt + 4*(i&3).
+  // Per-lane constants. DMA source offset within a 2-row block; LDS bases of the operand
+  // reads: K row i (+16 for the second key tile), chunk 4*ks + G; V (transposed reads)
+  // key rows 4G + (i>>2) (+16) of dims 16*dt + 4*(i&3) .. +3, i.e. chunk
+  // 2*dt + ((i&3)>>1), half (i&1).
+  const unsigned lane_src = (unsigned)((lane & 1) * DH * 2 + (lane >> 1) * 16);
   const int tr_row = 4 * G + (i >> 2);
-  const int tr_half = (i & 1) * 8;
-  const int tr_cq = (i & 3) >> 1;
+  const int k_base0 = (i >> 1) * KBLK + (2 * G + (i & 1)) * 16;
+  const int v_base0 = KTILE + (tr_row >> 1) * VBLK + (2 * ((i & 3) >> 1) + (tr_row & 1)) * 16 +
+                      (i & 1) * 8;
 
-  for (int s = 0; s < steps; ++s) {
-    const int k0 = c0 + s * KS;
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's DMA of step s landed
-    __builtin_amdgcn_s_barrier();                     // ... and every other wave's
-    asm volatile("" ::: "memory");
-    if (s + 1 < steps) dma(s + 1);                    // buffer (s+1)&1 is free again
-    const uint8_t* kt_lds = smem[s & 1][0];
-    const uint8_t* vt_lds = smem[s & 1][1];
+  int p = find_pair(a.pstart, a.npairs, x, lane);
+  while (x < x_end) {
+    const int pbeg = a.pstart[p];
+    const int s_lo = x - pbeg;
+    const int steps = min(x_end, (int)a.pstart[p + 1]) - x;
+    const int bg = p;
+    const int b = bg / a.Hkv;
+    const int L = a.kv_len[b] > 0 ? a.kv_len[b] : 0;
+    const int kend = pair_kend(a.kv_len, b, a.T, a.s_max);  // rows [0, kend) are read
+    const int c0 = s_lo * KS;
+    const uint8_t* kb = reinterpret_cast<const uint8_t*>(a.cache_k + (size_t)bg * a.s_max * DH);
+    const uint8_t* vb = reinterpret_cast<const uint8_t*>(a.cache_v + (size_t)bg * a.s_max * DH);
 
-    // S^T[32 keys x 16 rows] = K Q'^T
-    f32x4 st[2];
+    // Every wave has finished reading the previous segment's stages.
+    __builtin_amdgcn_s_barrier();
+
+    // DMA of step s's tiles into stage s % NST: slot j < 16 is K block j, 16 <= j < 32 is
+    // V block j - 16, DPW slots per wave; slots past 32 (NRT * DPW > 32) fill the slack.
+    // A step that reaches past kend (a pair's last) clamps its rows to kend - 1, so V rows
+    // the mask removes still hold finite cache data.
+    auto dma = [&](int s) {
+      const int k0 = c0 + s * KS;
+      uint8_t* st = smem + (s % NST) * STAGE;
+      const bool tail = k0 + KS > kend;
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-      st[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
-      const int r = 16 * kt + i;
+      for (int q = 0; q < DPW; ++q) {
+        const int j = w + NRT * q;  // wave-uniform slot
+        const bool isv = j >= KS / 2;
+        const int blk = (isv ? j - KS / 2 : j) & (KS / 2 - 1);
+        uint8_t* dst = j < KS ? st + (isv ? KTILE + blk * VBLK : blk * KBLK) : st + KTILE + VTILE;
+        const uint8_t* src = isv ? vb : kb;
+        if (!tail) {
+          npn::lds_dma16_soff(src + (size_t)(k0 + 2 * blk) * DH * 2, lane_src, dst);
+        } else {
+          const int key = min(k0 + 2 * blk + (lane & 1), kend - 1);
+          npn::lds_dma16_soff(src, (unsigned)key * DH * 2 + (unsigned)(lane >> 1) * 16, dst);
+        }
+      }
+    };
+    // q' hi/lo of this lane's row as B operands: dims 32*ks + 8*G .. +7. Loaded by inline
+    // asm ahead of the K/V DMAs, so the loop's own vmcnt wait for step 0 covers them (a
+    // compiler-tracked load would make the compiler wait for every DMA issued after it).
+    u32x4 qh[8], ql[8];
+    {
+      const size_t qo = ((size_t)bg * R + row) * DH + 8 * G;
 #pragma unroll
       for (int ks = 0; ks < 8; ++ks) {
-        const int pos = (4 * ks + G) ^ kswz(r);
-        const bf16x8 ka = as_bf16x8(*reinterpret_cast<const u32x4*>(kt_lds + r * DH * 2 + pos * 16));
-        st[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, as_bf16x8(qh[ks]), st[kt], 0, 0, 0);
-        st[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, as_bf16x8(ql[ks]), st[kt], 0, 0, 0);
+        asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(qh[ks]) : "v"(a.qhi + qo + 32 * ks)
+                     : "memory");
+        asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(ql[ks]) : "v"(a.qlo + qo + 32 * ks)
+                     : "memory");
       }
     }
+    for (int s = 0; s < NST - 1 && s < steps; ++s) dma(s);
 
-    // causal mask + online softmax (base 2); P hi/lo become the B operands of P.V.
-    float mx = -INFINITY;
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int key = k0 + 16 * kt + 4 * G + r;
-        if (key > lim) st[kt][r] = -INFINITY;
-        mx = fmaxf(mx, st[kt][r]);
-      }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float mnew = fmaxf(m_run, mx);
-    const float corr = exp2f(m_run - mnew);
-    m_run = mnew;
-    bf16x8 ph, pl;
-    float psum = 0.f;
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float p = exp2f(st[kt][r] - mnew);
-        psum += p;
-        const __bf16 h = (__bf16)p;
-        ph[kt * 4 + r] = h;
-        pl[kt * 4 + r] = (__bf16)(p - (float)h);
-      }
-    l_run = l_run * corr + psum;
+    const int lim = row < a.T * a.grp ? L + row / a.grp : kend - 1;  // last key this row sees
 
-    // O^T[256 x 16 rows] += V^T P^T
+    float m_run = kNegBig, l_run = 0.f;
+    f32x4 acc[16];
 #pragma unroll
-    for (int dt = 0; dt < 16; ++dt) {
-      const int q = 2 * dt + tr_cq;
-      const uint8_t* p1 = vt_lds + tr_row * DH * 2 + ((q ^ vswz(tr_row)) * 16) + tr_half;
-      const uint8_t* p2 = vt_lds + (tr_row + 16) * DH * 2 + ((q ^ vswz(tr_row + 16)) * 16) + tr_half;
-      const bf16x8 va = pack8(lds_tr16(p1), lds_tr16(p2));
-      acc[dt] *= corr;
-      acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, ph, acc[dt], 0, 0, 0);
-      acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pl, acc[dt], 0, 0, 0);
+    for (int dt = 0; dt < 16; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    for (int s = 0; s < steps; ++s) {
+      const int k0 = c0 + s * KS;
+      // This wave's DMA of step s has landed once at most the DMAs of the steps after it
+      // stay in flight: steps up to s + NST - 2 are issued here (vmcnt holds 6 bits; a
+      // smaller count only waits longer).
+      if (NST >= 4 && s + 2 < steps)
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * DPW < 63 ? 2 * DPW : 63) : "memory");
+      else if (NST >= 3 && s + 1 < steps)
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DPW < 63 ? DPW : 63) : "memory");
+      else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __builtin_amdgcn_s_barrier();  // ... and every other wave's; stage of step s-1 is free
+      asm volatile("" ::: "memory");
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) {  // q' registers are read only after that wait
+        asm volatile("" : "+v"(qh[ks]));
+        asm volatile("" : "+v"(ql[ks]));
+      }
+      if (s + NST - 1 < steps) dma(s + NST - 1);
+      const uint8_t* stage = smem + (s % NST) * STAGE;
+      const uint8_t* kp = stage + k_base0;
+      const uint8_t* vp = stage + v_base0;
+
+      // S^T[32 keys x 16 rows] = K Q'^T. All 16 K fragments are read first so their LDS
+      // latencies overlap; the two key tiles' accumulation chains alternate.
+      u32x4 kf[2][8];
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks)
+          kf[kt][ks] = *reinterpret_cast<const u32x4*>(kp + kt * (KS / 4) * KBLK + ks * 128);
+      f32x4 st[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) {
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+          st[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kf[kt][ks]),
+                                                           as_bf16x8(qh[ks]), st[kt], 0, 0, 0);
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+          st[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kf[kt][ks]),
+                                                           as_bf16x8(ql[ks]), st[kt], 0, 0, 0);
+      }
+      // Keep the 16 K reads ahead of the 32 MFMAs (the scheduler would otherwise pair each
+      // read with its MFMAs and expose the LDS latency 8 times); V fragments then reuse
+      // the K fragments' registers.
+      __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 32, 0);
+      __builtin_amdgcn_sched_barrier(0);
+
+      // V^T fragments of all 16 dim tiles, read before the softmax so their latency
+      // overlaps it.
+      bf16x8 vf[16];
+#pragma unroll
+      for (int dt = 0; dt < 16; ++dt)
+        vf[dt] = pack8(lds_tr16(vp + dt * 64), lds_tr16(vp + dt * 64 + (KS / 4) * VBLK));
+
+      // causal mask (only a step that reaches past the first query row's limit L needs
+      // one) + online softmax (base 2); P hi/lo become the B operands of P.V.
+      if (k0 + KS - 1 > L) {
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (k0 + 16 * kt + 4 * G + r > lim) st[kt][r] = -INFINITY;
+      }
+      float mx = fmaxf(fmaxf(fmaxf(st[0][0], st[0][1]), fmaxf(st[0][2], st[0][3])),
+                       fmaxf(fmaxf(st[1][0], st[1][1]), fmaxf(st[1][2], st[1][3])));
+      mx = max_over_groups(mx);
+      // The exponent base m_run moves only when a row's max exceeds it by more than 2^8,
+      // so p = 2^(s - m_run) <= 256 and most steps skip rescaling O; O / l does not depend
+      // on the base. The branch is wave-uniform.
+      const bool grow = mx > m_run + kRescaleLog2;
+      if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+        const float mnew = grow ? mx : m_run;
+        const float corr = exp2f(m_run - mnew);
+        m_run = mnew;
+        l_run *= corr;
+#pragma unroll
+        for (int dt = 0; dt < 16; ++dt) acc[dt] *= corr;
+      }
+      bf16x8 ph, pl;
+      float psum = 0.f;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float pv = exp2f(st[kt][r] - m_run);
+          psum += pv;
+          const __bf16 h = (__bf16)pv;
+          ph[kt * 4 + r] = h;
+          pl[kt * 4 + r] = (__bf16)(pv - (float)h);
+        }
+      l_run += psum;
+
+      // O^T[256 x 16 rows] += V^T P^T
+#pragma unroll
+      for (int dt = 0; dt < 16; ++dt)
+        acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[dt], ph, acc[dt], 0, 0, 0);
+#pragma unroll
+      for (int dt = 0; dt < 16; ++dt)
+        acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[dt], pl, acc[dt], 0, 0, 0);
     }
-  }
 
-  // Row sum over the 4 lane groups, then this wave's 16 rows of the chunk partial.
-  l_run += __shfl_xor(l_run, 16, 64);
-  l_run += __shfl_xor(l_run, 32, 64);
-  float* po = a.part_o + (((size_t)bg * a.nch + c) * R + row) * DH;
+    // Row sum over the 4 lane groups, then this wave's 16 rows of the segment partial.
+    l_run = sum_over_groups(l_run);
+    const size_t slot = (size_t)wg + p;
+    float* po = a.part_o + (slot * R + row) * DH;
 #pragma unroll
-  for (int dt = 0; dt < 16; ++dt) *reinterpret_cast<f32x4*>(po + 16 * dt + 4 * G) = acc[dt];
-  if (G == 0) {
-    float* pml = a.part_ml + (((size_t)bg * a.nch + c) * R + row) * 2;
-    pml[0] = m_run;
-    pml[1] = l_run;
+    for (int dt = 0; dt < 16; ++dt) *reinterpret_cast<f32x4*>(po + 16 * dt + 4 * G) = acc[dt];
+    if (G == 0) {
+      float* pml = a.part_ml + (slot * R + row) * 2;
+      pml[0] = m_run;
+      pml[1] = l_run;
+    }
+    x += steps;
+    ++p;
   }
 }
 
 // ---------------------------------------------------------------------------------------
-// 3. merge chunk partials, apply sigmoid(gate), write bf16. One 64-thread block per
-//    (query row, b, kv head); lane l owns output dims 4l..4l+3 (float4 partial reads).
+// 3. merge a pair's segment partials, apply sigmoid(gate), write bf16. One 64-thread block
+//    per (query row, pair); lane l owns output dims 4l..4l+3 (float4 partial reads). The
+//    workgroups that covered pair p are w(first step) .. w(last step), with
+//    w(x) = ((x + 1) * kAttnWG - 1) / S; a workgroup with an empty range in between (only
+//    when S < kAttnWG) wrote nothing and is skipped.
 struct MergeArgs {
   const float* part_o;
   const float* part_ml;
-  const int32_t* kv_len;
+  const int32_t* pstart;
   const uint16_t* gate;
   uint16_t* out;
-  int T, Hq, Hkv, R, nch, s_max;
+  int T, Hq, Hkv, R, npairs;
 };
 
 __global__ __launch_bounds__(64) void gqa_merge_kernel(MergeArgs a) {
   const int r = blockIdx.x;
-  const int bg = blockIdx.y;
-  const int b = bg / a.Hkv, g = bg - b * a.Hkv;
+  const int pr = blockIdx.y;
+  const int b = pr / a.Hkv, g = pr - b * a.Hkv;
   const int grp = a.Hq / a.Hkv;
   const int lane = threadIdx.x;
-  const int L = a.kv_len[b] > 0 ? a.kv_len[b] : 0;
-  const int kend = L + a.T < a.s_max ? L + a.T : a.s_max;
-  const int nc = (kend + CH - 1) / CH;
-  const float* pml = a.part_ml + ((size_t)bg * a.nch * a.R + r) * 2;
-  const float* po = a.part_o + ((size_t)bg * a.nch * a.R + r) * DH + 4 * lane;
-  const size_t cstride_ml = (size_t)a.R * 2, cstride_o = (size_t)a.R * DH;
+  const int S = a.pstart[a.npairs];
+  const int x0 = a.pstart[pr], x1 = a.pstart[pr + 1] - 1;
+  const int w0 = (int)(((int64_t)(x0 + 1) * kAttnWG - 1) / S);
+  const int w1 = (int)(((int64_t)(x1 + 1) * kAttnWG - 1) / S);
+  const size_t stride_ml = (size_t)a.R * 2, stride_o = (size_t)a.R * DH;
+  const float* pml = a.part_ml + ((size_t)(w0 + pr) * a.R + r) * 2;
+  const float* po = a.part_o + ((size_t)(w0 + pr) * a.R + r) * DH + 4 * lane;
   float M = kNegBig;
-  for (int c = 0; c < nc; ++c) M = fmaxf(M, pml[c * cstride_ml]);
+  for (int w = w0; w <= w1; ++w)
+    if (wg_first_step(w, S) < wg_first_step(w + 1, S)) M = fmaxf(M, pml[(w - w0) * stride_ml]);
   float l = 0.f;
   f32x4 o = {0.f, 0.f, 0.f, 0.f};
-  for (int c = 0; c < nc; ++c) {
-    const float f = exp2f(pml[c * cstride_ml] - M);
-    l += f * pml[c * cstride_ml + 1];
-    o += f * *reinterpret_cast<const f32x4*>(po + c * cstride_o);
+  for (int w = w0; w <= w1; ++w) {
+    if (wg_first_step(w, S) == wg_first_step(w + 1, S)) continue;
+    const float f = exp2f(pml[(w - w0) * stride_ml] - M);
+    l += f * pml[(w - w0) * stride_ml + 1];
+    o += f * *reinterpret_cast<const f32x4*>(po + (w - w0) * stride_o);
   }
   const int t = r / grp, qh = g * grp + (r - t * grp);
   const size_t oi = (((size_t)b * a.T + t) * a.Hq + qh) * DH + 4 * lane;
@@ -461,27 +621,32 @@ __global__ __launch_bounds__(256) void gqa_tail_kernel(const float* __restrict__
 }
 
 struct VerifyPlan {
-  int grp, R, nrt, nch;
-  size_t q_bytes, po_bytes, pml_bytes, total;
+  int grp, R, nrt, P;
+  size_t q_bytes, po_bytes, pml_bytes, ps_bytes, total;
 };
 
-VerifyPlan plan(int B, int T, int Hq, int Hkv, int s_max) {
+VerifyPlan plan(int B, int T, int Hq, int Hkv) {
   VerifyPlan p{};
   p.grp = Hq / Hkv;
   p.nrt = (T * p.grp + 15) / 16;
   p.R = p.nrt * 16;
-  p.nch = (s_max + CH - 1) / CH;
+  p.P = B * Hkv;
+  const size_t slots = (size_t)kAttnWG + p.P;
   auto up = [](size_t x) { return (x + 255) & ~size_t(255); };
-  p.q_bytes = up((size_t)B * Hkv * p.R * DH * 2);
-  p.po_bytes = up((size_t)B * Hkv * p.nch * p.R * DH * 4);
-  p.pml_bytes = up((size_t)B * Hkv * p.nch * p.R * 2 * 4);
-  p.total = 2 * p.q_bytes + p.po_bytes + p.pml_bytes;
+  p.q_bytes = up((size_t)p.P * p.R * DH * 2);
+  p.po_bytes = up(slots * p.R * DH * 4);
+  p.pml_bytes = up(slots * p.R * 2 * 4);
+  p.ps_bytes = up((size_t)(p.P + 1) * 4);
+  p.total = 2 * p.q_bytes + p.po_bytes + p.pml_bytes + p.ps_bytes;
   return p;
 }
 
 bool verify_shape_ok(int B, int T, int Hq, int Hkv, int s_max) {
-  return B >= 1 && B <= 65536 && T >= 1 && Hkv >= 1 && Hq >= Hkv && Hq % Hkv == 0 &&
-         T * (Hq / Hkv) <= 48 && s_max >= T && s_max <= (1 << 24);
+  // s_max <= 2^23 keeps cache row offsets in 32 bits; the total step count in int32.
+  // B * Hkv is the merge grid's y extent (<= 65535).
+  return B >= 1 && (int64_t)B * Hkv <= 65535 && T >= 1 && Hkv >= 1 && Hq >= Hkv && Hq % Hkv == 0 &&
+         T * (Hq / Hkv) <= 48 && s_max >= T && s_max <= (1 << 23) &&
+         (int64_t)B * Hkv * ((s_max + KS - 1) / KS) < ((int64_t)1 << 31);
 }
 
 }  // namespace
@@ -489,7 +654,7 @@ bool verify_shape_ok(int B, int T, int Hq, int Hkv, int s_max) {
 extern "C" size_t npn_gqa_tail_verify_workspace_size(int B, int T, int q_heads, int kv_heads,
                                                      int s_max) {
   if (!verify_shape_ok(B, T, q_heads, kv_heads, s_max)) return 0;
-  return plan(B, T, q_heads, kv_heads, s_max).total;
+  return plan(B, T, q_heads, kv_heads).total;
 }
 
 extern "C" int npn_gqa_tail_verify(const uint16_t* query, const uint16_t* gate,
@@ -503,7 +668,7 @@ extern "C" int npn_gqa_tail_verify(const uint16_t* query, const uint16_t* gate,
   NPN_REQUIRE(verify_shape_ok(B, T, q_heads, kv_heads, s_max), NPN_ERR_SHAPE);
   NPN_REQUIRE(NPN_ALIGNED16(cache_k) && NPN_ALIGNED16(cache_v) && NPN_ALIGNED16(workspace),
               NPN_ERR_ALIGN);
-  const VerifyPlan p = plan(B, T, q_heads, kv_heads, s_max);
+  const VerifyPlan p = plan(B, T, q_heads, kv_heads);
   NPN_REQUIRE(workspace != nullptr && workspace_bytes >= p.total, NPN_ERR_WORKSPACE);
   hipStream_t s = static_cast<hipStream_t>(stream);
   uint8_t* ws = static_cast<uint8_t*>(workspace);
@@ -511,19 +676,23 @@ extern "C" int npn_gqa_tail_verify(const uint16_t* query, const uint16_t* gate,
   uint16_t* qlo = reinterpret_cast<uint16_t*>(ws + p.q_bytes);
   float* po = reinterpret_cast<float*>(ws + 2 * p.q_bytes);
   float* pml = reinterpret_cast<float*>(ws + 2 * p.q_bytes + p.po_bytes);
+  int32_t* pstart = reinterpret_cast<int32_t*>(ws + 2 * p.q_bytes + p.po_bytes + p.pml_bytes);
+
+  hipLaunchKernelGGL(gqa_plan_kernel, dim3(1), dim3(1024), 0, s, kv_len, pstart, p.P, kv_heads,
+                     T, s_max);
 
   QPrepArgs qa{query, q_norm, cos, sin, qhi, qlo, B, T, q_heads, kv_heads, p.R};
   const int rows = B * kv_heads * p.R;
   hipLaunchKernelGGL(gqa_qprep_kernel, dim3((rows + 3) / 4), dim3(256), 0, s, qa);
 
-  AttnArgs aa{qhi, qlo, cache_k, cache_v, kv_len, po, pml, kv_heads, s_max, T, p.grp, p.nch};
-  const dim3 grid(p.nch, B * kv_heads);
-  if (p.nrt == 1) hipLaunchKernelGGL(gqa_attn_kernel<1>, grid, dim3(64), 0, s, aa);
-  else if (p.nrt == 2) hipLaunchKernelGGL(gqa_attn_kernel<2>, grid, dim3(128), 0, s, aa);
-  else hipLaunchKernelGGL(gqa_attn_kernel<3>, grid, dim3(192), 0, s, aa);
+  AttnArgs aa{qhi, qlo, cache_k, cache_v, kv_len, pstart, po, pml, kv_heads, s_max, T, p.grp, p.P};
+  const dim3 grid(kAttnWG);
+  if (p.nrt == 1) hipLaunchKernelGGL((gqa_attn_kernel<1, 2>), grid, dim3(64), 0, s, aa);
+  else if (p.nrt == 2) hipLaunchKernelGGL((gqa_attn_kernel<2, 2>), grid, dim3(128), 0, s, aa);
+  else hipLaunchKernelGGL((gqa_attn_kernel<3, 2>), grid, dim3(192), 0, s, aa);
 
-  MergeArgs ma{po, pml, kv_len, gate, out, T, q_heads, kv_heads, p.R, p.nch, s_max};
-  hipLaunchKernelGGL(gqa_merge_kernel, dim3(T * p.grp, B * kv_heads), dim3(64), 0, s, ma);
+  MergeArgs ma{po, pml, pstart, gate, out, T, q_heads, kv_heads, p.R, p.P};
+  hipLaunchKernelGGL(gqa_merge_kernel, dim3(T * p.grp, p.P), dim3(64), 0, s, ma);
   return npn_launch_status();
 }
 

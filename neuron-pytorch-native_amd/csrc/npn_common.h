@@ -62,6 +62,17 @@ __device__ __forceinline__ void lds_dma16(const void* g, const void* lds_base) {
                : "memory", "m0");
 }
 
+// Same DMA with a wave-uniform global base (SGPR pair) and a 32-bit per-lane byte offset,
+// which keeps one VGPR per lane live instead of a 64-bit address.
+__device__ __forceinline__ void lds_dma16_soff(const void* sbase, unsigned voff,
+                                               const void* lds_base) {
+  const unsigned base = __builtin_amdgcn_readfirstlane(
+      (unsigned)(uintptr_t)(__attribute__((address_space(3))) const void*)lds_base);
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase),
+               "s"(base)
+               : "memory", "m0");
+}
+
 }  // namespace npn
 
 // ---- host-side checks ------------------------------------------------------------------

@@ -40,7 +40,39 @@ def parse():
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--per-op", action="store_true", help="print per-op timings to stderr")
+    p.add_argument("--copy-calibration", action="store_true",
+                   help="only run a plain 1 GiB device copy 5 times (scales HBM byte counters)")
     return p.parse_args()
+
+
+COPY_BYTES = 1 << 30
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic.txt")
+
+
+def copy_calibration():
+    """A plain device-to-device copy of COPY_BYTES, the reference for FETCH_SIZE / WRITE_SIZE."""
+    import torch
+    src = torch.empty(COPY_BYTES // 4, dtype=torch.int32, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": COPY_BYTES, "launches": 5}))
+
+
+def measured_traffic(op):
+    """HBM bytes per launch of an op's kernels from the committed counter summary, or None.
+    Lines read: 'traffic <op> <bytes>' (FETCH_SIZE + WRITE_SIZE per launch, each scaled by
+    the plain-copy calibration)."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                parts = line.split()
+                if len(parts) == 3 and parts[0] == "traffic" and parts[1] == op:
+                    return int(float(parts[2]))
+    except OSError:
+        pass
+    return None
 
 
 def kv_lengths(seed):
@@ -110,6 +142,9 @@ def cpu_baseline(model, x, logits, sample_b=0):
 
 def main():
     args = parse()
+    if args.copy_calibration:
+        copy_calibration()
+        return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (got --gpus {args.gpus}); the verify step is "
               f"measured on a single MI355X", file=sys.stderr)
@@ -163,6 +198,7 @@ def main():
         achieved = units / mean_s / 1e9
         roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None}
+    roof["traffic"] = measured_traffic(dom)
     roof["kernel"] = dom
     roof["mean_launch_ms"] = round(ops[dom]["mean_ms"], 4)
     roof["units_per_launch"] = units

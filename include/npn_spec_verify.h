@@ -115,13 +115,16 @@ int npn_gqa_tail(const float* query, const float* gate, const float* q_norm, con
 size_t npn_gqa_tail_verify_workspace_size(int B, int T, int q_heads, int kv_heads, int s_max);
 
 /* torch.ops.gqa.tail_verify -- new op: the gqa::tail math (gqa_tail_ops.py:14-26)
- * for T verify tokens per sequence over a bf16 KV cache, split over KV chunks.
+ * for T verify tokens per sequence over a bf16 KV cache (split-KV: the
+ * sequences' 32-key steps are divided evenly over a fixed set of workgroups,
+ * then a log-sum-exp merge).
  *   query, gate [B, T, Hq, 256] bf16   q_norm [256] f32
  *   cos, sin    [B, T, 64] f32 (RoPE of each query row's position)
  *   cache_k/v   [B, Hkv, s_max, 256] bf16, rows [0, kv_len[b]+T) valid
  *   kv_len      [B] int32, cache rows before the T verify rows (kv_len+T <= s_max)
  * Row (b,t,h) uses kv head h/(Hq/Hkv) and attends rows [0, kv_len[b]+t].
- * Output: out [B, T, Hq, 256] bf16. Hq/Hkv * T <= 64. */
+ * Output: out [B, T, Hq, 256] bf16. Limits: Hq/Hkv * T <= 48, s_max <= 2^23,
+ * B * Hkv <= 65535. The workspace query returns 0 outside them. */
 int npn_gqa_tail_verify(const uint16_t* query, const uint16_t* gate, const float* q_norm,
                         const float* cos, const float* sin, const uint16_t* cache_k,
                         const uint16_t* cache_v, const int32_t* kv_len, uint16_t* out, int B,
@@ -172,9 +175,14 @@ int npn_accept_greedy(const float* target_logits, const int64_t* draft_ids, int3
                       size_t workspace_bytes, void* stream);
 
 /* torch.ops.spec.accept_rejection -- new op. Rejection sampling (Leviathan et
- * al. 2023, Alg. 1) under the library's integer softmax contract (see the
- * library design notes): bit-identical to its CPU restatement for the same
- * logits and uniforms.
+ * al. 2023, Alg. 1) under an integer softmax contract, so the result is
+ * bit-identical to a CPU restatement for the same logits and uniforms:
+ *   x_v = t_v*inv_temperature - max (fp32); E_v = floor(2^32 * exp_c(x_v)) with
+ *   exp_c a fixed fp32 Cody-Waite + degree-7 Taylor evaluation without FMA;
+ *   Z = sum E_v (exact); U = floor(u * 2^24).
+ *   Accept draft x iff U * Eq_x * Zp <= 2^24 * Ep_x * Zq. At the first rejection
+ *   sample from R_v = max(0, Ep_v*Zq - Eq_v*Zp) (bonus: R_v = Ep_v of row K):
+ *   the smallest v with 2^24 * sum_{w<=v} R_w > U_s * sum_w R_w.
  *   target_logits [B, K+1, V] f32, draft_logits [B, K, V] f32, draft_ids [B, K]
  *   int64, u_accept [B, K] f32 in [0,1), u_sample [B] f32 in [0,1),
  *   inv_temperature > 0 (logits are multiplied by it). */

@@ -113,6 +113,33 @@ def test_rollback_copy_and_index(ops):
     assert torch.equal(ck_copy, ck_idx) and torch.equal(out_copy, out_idx)
 
 
+def test_rollback_clamps_out_of_range(ops):
+    """accepted / state_index outside [0, T-1] act as their clamped values (the kernels
+    clamp on the device instead of reading out of bounds)."""
+    B, T, Hk, Hv = 4, 8, 4, 12
+    d = deltanet_inputs(B, T, Hk, Hv, seed=23)
+    f = deltanet_flat_device(d)
+    ckpt, _ = ops.deltanet.verify_batched(
+        f["state"], f["mixed_qkv"], f["conv_state"], f["conv_weight"], f["conv_bias"],
+        f["a_out"], f["b_out"], f["z"], f["A_log"], f["dt_bias"], f["norm_weight"])
+    wild = torch.tensor([-2, 9, 3, 100], dtype=torch.int32)
+    clamped = wild.clamp(0, T - 1)
+    s_w, c_w = ops.deltanet.rollback(ckpt, f["mixed_qkv"], f["conv_state"], wild.cuda())
+    s_c, c_c = ops.deltanet.rollback(ckpt, f["mixed_qkv"], f["conv_state"], clamped.cuda())
+    d2 = deltanet_inputs(B, T, Hk, Hv, seed=24)
+    f2 = deltanet_flat_device(d2)
+    args = (f2["mixed_qkv"], c_c, f2["conv_weight"], f2["conv_bias"], f2["a_out"],
+            f2["b_out"], f2["z"], f2["A_log"], f2["dt_bias"], f2["norm_weight"])
+    ck_w, out_w = ops.deltanet.verify_from_ckpt(ckpt, wild.cuda(), *args)
+    ck_c, out_c = ops.deltanet.verify_from_ckpt(ckpt, clamped.cuda(), *args)
+    torch.cuda.synchronize()
+    assert torch.equal(s_w, s_c) and torch.equal(c_w, c_c)
+    assert torch.equal(ck_w, ck_c) and torch.equal(out_w, out_c)
+    _, cs_ref = od.deltanet_rollback(np.zeros((B, T, 1, 1, 1)), bits(d["mixed_qkv"]),
+                                     bits(d["conv_state"]), clamped.numpy())
+    assert np.array_equal(bits(c_w).reshape(cs_ref.shape), cs_ref)
+
+
 def test_full_size_b32_sampled(ops):
     """B=32, T=8, 16/48 heads (921.7 MB of state traffic): every sequence is independent,
     so three sampled sequences are checked against the oracle run on their slices."""

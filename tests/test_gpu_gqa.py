@@ -65,6 +65,16 @@ def test_tail_verify_matches_oracle(ops, B, T, Hq, Hkv, kv_lens, s_max):
     assert_rel_close(_run_verify(ops, d), _oracle_verify(d), out_unit=BF16_U, name="tail_verify")
 
 
+def test_tail_verify_many_short_ragged_pairs(ops):
+    """160 (sequence, kv head) pairs with 0..300 cached rows: more 32-key steps than
+    attention workgroups, so workgroup ranges start and end inside pairs and one
+    workgroup covers several consecutive pairs."""
+    B = 40
+    kv = np.random.default_rng(41).integers(0, 301, size=B).tolist()
+    d = gqa_verify_inputs(B, 8, 24, 4, kv, 320, seed=41)
+    assert_rel_close(_run_verify(ops, d), _oracle_verify(d), out_unit=BF16_U, name="ragged")
+
+
 def test_tail_verify_full_width_long(ops):
     """Config-2-like: 24/4 heads, T=8, KV lengths 4096..8192 (oracle-affordable)."""
     d = gqa_verify_inputs(2, 8, 24, 4, [4096, 8000], 8200, seed=2)

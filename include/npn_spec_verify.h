@@ -192,6 +192,45 @@ int npn_accept_rejection(const float* target_logits, const float* draft_logits,
                          int64_t* out_ids, int B, int K, int V, void* workspace,
                          size_t workspace_bytes, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Inter-layer glue of the verify step (the decode loop of
+ * contrib/qwen3.6-27b/static_decode.py:533-542), each a single pass.
+ * ------------------------------------------------------------------------- */
+
+/* torch.ops.normfuse.rms_norm -- replaces the op registered at
+ * contrib/qwen3.6-27b/kernels/rms_norm_nki_ops.py:7-13 (rms_norm,
+ * static_decode.py:322-335) and fuses the residual add before it
+ * (normfuse::residual_rms_norm, new):
+ *   hidden_out = bf16(hidden_in + delta)            (skipped when delta == NULL)
+ *   normed     = bf16((1 + weight) * h * rsqrt(mean(h^2) + eps)), h = hidden_out
+ *   hidden_in/out, delta, normed [M, H] bf16; weight [H] f32. H % 8 == 0, H <= 16384.
+ *   hidden_out may equal hidden_in; with delta == NULL it may be NULL. */
+int npn_residual_rmsnorm(const uint16_t* hidden_in, const uint16_t* delta, const float* weight,
+                         uint16_t* hidden_out, uint16_t* normed, int M, int H, float eps,
+                         void* stream);
+
+/* torch.ops.glue.silu_mul -- new op: the SwiGLU of _mlp_layer (static_decode.py:951-963),
+ * out = bf16(bf16(silu(gate)) * up) for gate_up [M, 2I] bf16 = [gate | up]; out [M, I].
+ * I % 8 == 0. */
+int npn_silu_mul(const uint16_t* gate_up, uint16_t* out, int M, int I, void* stream);
+
+/* torch.ops.glue.deltanet_split -- new op: the slicing and casts of _deltanet_layer
+ * (static_decode.py:802-832) from one fused in-projection output:
+ *   proj [M, ld] bf16 rows [qkv_n | z_n | hv (a) | hv (b) | unused]
+ *   -> mixed_qkv [M, qkv_n] bf16, z [M, z_n] bf16, a_out, b_out [M, hv] f32.
+ * qkv_n, z_n, hv, ld multiples of 8. */
+int npn_deltanet_split(const uint16_t* proj, int ld, uint16_t* mixed_qkv, uint16_t* z,
+                       float* a_out, float* b_out, int M, int qkv_n, int z_n, int hv,
+                       void* stream);
+
+/* torch.ops.glue.gqa_split -- new op: the per-head split of _gqa_layer
+ * (static_decode.py:867-870, :880-890) from one fused q/k/v projection output:
+ *   proj [M, ld] bf16 rows [(query | gate) x q_heads | key x kv_heads | value x kv_heads],
+ *   each head_dim wide -> query, gate [M, q_heads, head_dim], key, value
+ *   [M, kv_heads, head_dim] bf16. head_dim, ld multiples of 8. */
+int npn_gqa_split(const uint16_t* proj, int ld, uint16_t* query, uint16_t* gate, uint16_t* key,
+                  uint16_t* value, int M, int q_heads, int kv_heads, int head_dim, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,236 @@
+// Inter-layer glue of the verify step, fused into single passes over HBM
+// (the decode loop contrib/qwen3.6-27b/static_decode.py:533-542):
+//   residual RMSNorm  hidden' = bf16(hidden + delta);  normed = bf16((1 + w) * hidden' *
+//                     rsqrt(mean(hidden'^2) + eps))          (rms_norm, static_decode.py:322-335)
+//   SwiGLU            y = bf16(bf16(silu(gate)) * up)         (_mlp_layer, static_decode.py:951-963;
+//                     gate, up and silu(gate) are bf16 tensors there, so two roundings)
+//   DeltaNet split    in-proj row [qkv | z | a | b | pad] -> mixed_qkv, z (bf16), a, b (f32)
+//                     (the slicing and casts of _deltanet_layer, static_decode.py:802-832)
+//   GQA split         q/k/v-proj row [(query | gate) per q head | key per kv head | value per
+//                     kv head] -> query, gate, key, value (_gqa_layer, static_decode.py:867-890)
+// All four move 16-byte chunks (8 bf16) per lane; widths must be multiples of 8.
+#include "npn_common.h"
+
+namespace {
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void unpack8(const u32x4 v, float (&f)[8]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    f[2 * j] = __uint_as_float(v[j] << 16);
+    f[2 * j + 1] = __uint_as_float(v[j] & 0xFFFF0000u);
+  }
+}
+
+__device__ __forceinline__ u32x4 pack8(const float (&f)[8]) {
+  u32x4 v;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    v[j] = (uint32_t)npn::f32_to_bf16(f[2 * j]) | ((uint32_t)npn::f32_to_bf16(f[2 * j + 1]) << 16);
+  return v;
+}
+
+// ---- residual + (1 + w) RMSNorm: one 128-thread workgroup per row; the row (<= 16 chunks of
+// 8 per thread, H <= 16384) stays in registers between the sum of squares and the scaling.
+constexpr int kNormThreads = 128;
+constexpr int kNormMaxChunks = 16;
+
+__global__ __launch_bounds__(kNormThreads) void residual_rmsnorm_kernel(
+    const uint16_t* h_in, const uint16_t* __restrict__ delta, const float* __restrict__ weight,
+    uint16_t* h_out, uint16_t* __restrict__ y, int H, float eps) {  // h_out may alias h_in
+  const int row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int nc = H / 8;
+  const size_t base = (size_t)row * H;
+  float x[kNormMaxChunks][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < kNormMaxChunks; ++k) {
+    const int c = tid + k * kNormThreads;
+    if (c < nc) {
+      unpack8(*reinterpret_cast<const u32x4*>(h_in + base + 8 * c), x[k]);
+      if (delta != nullptr) {
+        float d[8];
+        unpack8(*reinterpret_cast<const u32x4*>(delta + base + 8 * c), d);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x[k][j] = npn::bf16_to_f32(npn::f32_to_bf16(x[k][j] + d[j]));
+        *reinterpret_cast<u32x4*>(h_out + base + 8 * c) = pack8(x[k]);
+      } else if (h_out != h_in) {
+        *reinterpret_cast<u32x4*>(h_out + base + 8 * c) = pack8(x[k]);
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ss += x[k][j] * x[k][j];
+    }
+  }
+  __shared__ float part[kNormThreads / 64];
+  ss = npn::wave_sum(ss);
+  if ((tid & 63) == 0) part[tid >> 6] = ss;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int w = 0; w < kNormThreads / 64; ++w) tot += part[w];
+  const float r = rsqrtf(tot / (float)H + eps);
+#pragma unroll
+  for (int k = 0; k < kNormMaxChunks; ++k) {
+    const int c = tid + k * kNormThreads;
+    if (c < nc) {
+      const float4 w0 = *reinterpret_cast<const float4*>(weight + 8 * c);
+      const float4 w1 = *reinterpret_cast<const float4*>(weight + 8 * c + 4);
+      const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+      float o[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[j] = (1.0f + wv[j]) * (x[k][j] * r);
+      *reinterpret_cast<u32x4*>(y + base + 8 * c) = pack8(o);
+    }
+  }
+}
+
+// ---- SwiGLU: gu [M, 2I] = [gate | up] -> y [M, I]; one lane per 8 outputs (grid-stride).
+__global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restrict__ gu,
+                                                       uint16_t* __restrict__ y, int M, int I) {
+  const int cpr = I / 8;  // chunks per row
+  const size_t n = (size_t)M * cpr;
+  for (size_t c = (size_t)blockIdx.x * blockDim.x + threadIdx.x; c < n;
+       c += (size_t)gridDim.x * blockDim.x) {
+    const size_t m = c / cpr, j = c - m * cpr;
+    float g[8], u[8], o[8];
+    unpack8(*reinterpret_cast<const u32x4*>(gu + m * 2 * I + 8 * j), g);
+    unpack8(*reinterpret_cast<const u32x4*>(gu + m * 2 * I + I + 8 * j), u);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float s = npn::bf16_to_f32(npn::f32_to_bf16(npn::silu(g[k])));
+      o[k] = s * u[k];
+    }
+    *reinterpret_cast<u32x4*>(y + m * I + 8 * j) = pack8(o);
+  }
+}
+
+// ---- DeltaNet in-projection split. Row m of proj (stride ld): [qkv_n | z_n | hv | hv | ...].
+__global__ __launch_bounds__(256) void dn_split_kernel(const uint16_t* __restrict__ proj, int ld,
+                                                       uint16_t* __restrict__ mixed,
+                                                       uint16_t* __restrict__ z,
+                                                       float* __restrict__ a,
+                                                       float* __restrict__ b, int M, int qkv_n,
+                                                       int z_n, int hv) {
+  const int cq = qkv_n / 8, cz = z_n / 8, ch = hv / 8;
+  const int cpr = cq + cz + 2 * ch;
+  const size_t n = (size_t)M * cpr;
+  for (size_t c = (size_t)blockIdx.x * blockDim.x + threadIdx.x; c < n;
+       c += (size_t)gridDim.x * blockDim.x) {
+    const size_t m = c / cpr;
+    const int j = (int)(c - m * cpr);
+    const u32x4 v = *reinterpret_cast<const u32x4*>(proj + m * ld + 8 * (size_t)j);
+    if (j < cq) {
+      *reinterpret_cast<u32x4*>(mixed + m * qkv_n + 8 * j) = v;
+    } else if (j < cq + cz) {
+      *reinterpret_cast<u32x4*>(z + m * z_n + 8 * (j - cq)) = v;
+    } else {
+      const bool isb = j >= cq + cz + ch;
+      const int k = j - cq - cz - (isb ? ch : 0);
+      float f[8];
+      unpack8(v, f);
+      float* dst = (isb ? b : a) + m * hv + 8 * k;
+      *reinterpret_cast<float4*>(dst) = make_float4(f[0], f[1], f[2], f[3]);
+      *reinterpret_cast<float4*>(dst + 4) = make_float4(f[4], f[5], f[6], f[7]);
+    }
+  }
+}
+
+// ---- GQA projection split. Row m of proj (stride ld): query/gate interleaved per q head
+// (hd each), then key per kv head, then value per kv head.
+__global__ __launch_bounds__(256) void gqa_split_kernel(const uint16_t* __restrict__ proj, int ld,
+                                                        uint16_t* __restrict__ query,
+                                                        uint16_t* __restrict__ gate,
+                                                        uint16_t* __restrict__ key,
+                                                        uint16_t* __restrict__ value, int M,
+                                                        int hq, int hkv, int hd) {
+  const int ch = hd / 8;
+  const int cqg = 2 * hq * ch;  // query+gate chunks per row
+  const int ckv = hkv * ch;
+  const int cpr = cqg + 2 * ckv;
+  const size_t n = (size_t)M * cpr;
+  for (size_t c = (size_t)blockIdx.x * blockDim.x + threadIdx.x; c < n;
+       c += (size_t)gridDim.x * blockDim.x) {
+    const size_t m = c / cpr;
+    const int j = (int)(c - m * cpr);
+    const u32x4 v = *reinterpret_cast<const u32x4*>(proj + m * ld + 8 * (size_t)j);
+    uint16_t* dst;
+    if (j < cqg) {
+      const int h = j / (2 * ch), r = j - h * 2 * ch;
+      dst = (r < ch ? query : gate) + (m * hq + h) * hd + 8 * (r < ch ? r : r - ch);
+    } else if (j < cqg + ckv) {
+      dst = key + m * hkv * hd + 8 * (j - cqg);
+    } else {
+      dst = value + m * hkv * hd + 8 * (j - cqg - ckv);
+    }
+    *reinterpret_cast<u32x4*>(dst) = v;
+  }
+}
+
+int grid_for(size_t chunks) {
+  const size_t blocks = (chunks + 255) / 256;
+  return (int)(blocks < 4096 ? (blocks > 0 ? blocks : 1) : 4096);
+}
+
+}  // namespace
+
+extern "C" int npn_residual_rmsnorm(const uint16_t* hidden_in, const uint16_t* delta,
+                                    const float* weight, uint16_t* hidden_out,
+                                    uint16_t* normed, int M, int H, float eps, void* stream) {
+  NPN_REQUIRE(hidden_in && weight && normed && (delta == nullptr || hidden_out), NPN_ERR_NULL);
+  NPN_REQUIRE(M >= 1 && H >= 8 && H % 8 == 0 && H / 8 <= kNormThreads * kNormMaxChunks,
+              NPN_ERR_SHAPE);
+  NPN_REQUIRE(eps >= 0.0f, NPN_ERR_VALUE);
+  NPN_REQUIRE(NPN_ALIGNED16(hidden_in) && NPN_ALIGNED16(delta) && NPN_ALIGNED16(weight) &&
+                  NPN_ALIGNED16(hidden_out) && NPN_ALIGNED16(normed),
+              NPN_ERR_ALIGN);
+  uint16_t* hout = hidden_out ? hidden_out : const_cast<uint16_t*>(hidden_in);
+  hipLaunchKernelGGL(residual_rmsnorm_kernel, dim3(M), dim3(kNormThreads), 0,
+                     static_cast<hipStream_t>(stream), hidden_in, delta, weight, hout, normed, H,
+                     eps);
+  return npn_launch_status();
+}
+
+extern "C" int npn_silu_mul(const uint16_t* gate_up, uint16_t* out, int M, int I, void* stream) {
+  NPN_REQUIRE(gate_up && out, NPN_ERR_NULL);
+  NPN_REQUIRE(M >= 1 && I >= 8 && I % 8 == 0, NPN_ERR_SHAPE);
+  NPN_REQUIRE(NPN_ALIGNED16(gate_up) && NPN_ALIGNED16(out), NPN_ERR_ALIGN);
+  hipLaunchKernelGGL(silu_mul_kernel, dim3(grid_for((size_t)M * (I / 8))), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), gate_up, out, M, I);
+  return npn_launch_status();
+}
+
+extern "C" int npn_deltanet_split(const uint16_t* proj, int ld, uint16_t* mixed_qkv, uint16_t* z,
+                                  float* a_out, float* b_out, int M, int qkv_n, int z_n, int hv,
+                                  void* stream) {
+  NPN_REQUIRE(proj && mixed_qkv && z && a_out && b_out, NPN_ERR_NULL);
+  NPN_REQUIRE(M >= 1 && qkv_n % 8 == 0 && z_n % 8 == 0 && hv % 8 == 0 && qkv_n > 0 && z_n > 0 &&
+                  hv > 0 && ld % 8 == 0 && ld >= qkv_n + z_n + 2 * hv,
+              NPN_ERR_SHAPE);
+  NPN_REQUIRE(NPN_ALIGNED16(proj) && NPN_ALIGNED16(mixed_qkv) && NPN_ALIGNED16(z) &&
+                  NPN_ALIGNED16(a_out) && NPN_ALIGNED16(b_out),
+              NPN_ERR_ALIGN);
+  const size_t chunks = (size_t)M * ((qkv_n + z_n + 2 * hv) / 8);
+  hipLaunchKernelGGL(dn_split_kernel, dim3(grid_for(chunks)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), proj, ld, mixed_qkv, z, a_out, b_out, M,
+                     qkv_n, z_n, hv);
+  return npn_launch_status();
+}
+
+extern "C" int npn_gqa_split(const uint16_t* proj, int ld, uint16_t* query, uint16_t* gate,
+                             uint16_t* key, uint16_t* value, int M, int q_heads, int kv_heads,
+                             int head_dim, void* stream) {
+  NPN_REQUIRE(proj && query && gate && key && value, NPN_ERR_NULL);
+  NPN_REQUIRE(M >= 1 && q_heads >= 1 && kv_heads >= 1 && head_dim >= 8 && head_dim % 8 == 0 &&
+                  ld % 8 == 0 && ld >= 2 * (q_heads + kv_heads) * head_dim,
+              NPN_ERR_SHAPE);
+  NPN_REQUIRE(NPN_ALIGNED16(proj) && NPN_ALIGNED16(query) && NPN_ALIGNED16(gate) &&
+                  NPN_ALIGNED16(key) && NPN_ALIGNED16(value),
+              NPN_ERR_ALIGN);
+  const size_t chunks = (size_t)M * (2 * (q_heads + kv_heads) * head_dim / 8);
+  hipLaunchKernelGGL(gqa_split_kernel, dim3(grid_for(chunks)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), proj, ld, query, gate, key, value, M,
+                     q_heads, kv_heads, head_dim);
+  return npn_launch_status();
+}

@@ -5,6 +5,8 @@
   torch.ops.gqa.{tail, tail_verify, kv_append}
   torch.ops.fp8.matmul
   torch.ops.spec.{accept_greedy, accept_rejection}
+  torch.ops.normfuse.{rms_norm, residual_rms_norm}
+  torch.ops.glue.{silu_mul, deltanet_split, gqa_split}
 
 (The reference registers its ops by importing each *_ops module,
 contrib/qwen3.6-27b/static_decode.py:29-34; importing the modules one by one works
@@ -16,3 +18,5 @@ import deltanet_verify_ops  # noqa: F401
 import gqa_tail_ops  # noqa: F401
 import fp8_matmul_ops  # noqa: F401
 import spec_accept_ops  # noqa: F401
+import rms_norm_nki_ops  # noqa: F401
+import glue_ops  # noqa: F401

@@ -1,0 +1,58 @@
+"""torch.ops.normfuse.rms_norm on gfx950 -- drop-in for the op registered at
+contrib/qwen3.6-27b/kernels/rms_norm_nki_ops.py:7-13 (same name and schema):
+
+  normfuse::rms_norm(x [..., H] bf16, weight [H] f32) -> [..., H] bf16
+      = x * rsqrt(mean(x^2) + 1e-6) * (1 + weight)      (rms_norm, static_decode.py:322-335)
+
+plus the residual form the decode loop applies before every norm
+(contrib/qwen3.6-27b/static_decode.py:533-542), fused into the same pass:
+
+  normfuse::residual_rms_norm(hidden, delta, weight, eps) -> (hidden + delta, rms_norm(...))
+
+The reference op takes one token's [H] vector; this one takes any number of rows.
+"""
+import torch
+
+from npn_native import call, require, stream_of
+
+RMS_EPS = 1e-6
+
+
+def _rows(x):
+    H = x.shape[-1]
+    return x.numel() // H, H
+
+
+@torch.library.custom_op("normfuse::rms_norm", mutates_args=(), device_types="cuda")
+def rms_norm(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    M, H = _rows(x)
+    require(x, "x", torch.bfloat16)
+    require(weight, "weight", torch.float32, numel=H)
+    out = torch.empty_like(x)
+    call("npn_residual_rmsnorm", x, None, weight, None, out, M, H, RMS_EPS, stream_of(x))
+    return out
+
+
+@rms_norm.register_fake
+def _(x, weight):
+    return torch.empty_like(x)
+
+
+@torch.library.custom_op("normfuse::residual_rms_norm", mutates_args=(), device_types="cuda")
+def residual_rms_norm(hidden: torch.Tensor, delta: torch.Tensor, weight: torch.Tensor,
+                      eps: float = RMS_EPS) -> tuple[torch.Tensor, torch.Tensor]:
+    """(bf16(hidden + delta), bf16((1 + weight) * h * rsqrt(mean(h^2) + eps))), h = the sum."""
+    M, H = _rows(hidden)
+    require(hidden, "hidden", torch.bfloat16)
+    require(delta, "delta", torch.bfloat16, shape=tuple(hidden.shape))
+    require(weight, "weight", torch.float32, numel=H)
+    h_out = torch.empty_like(hidden)
+    normed = torch.empty_like(hidden)
+    call("npn_residual_rmsnorm", hidden, delta, weight, h_out, normed, M, H, float(eps),
+         stream_of(hidden))
+    return h_out, normed
+
+
+@residual_rms_norm.register_fake
+def _(hidden, delta, weight, eps=RMS_EPS):
+    return torch.empty_like(hidden), torch.empty_like(hidden)

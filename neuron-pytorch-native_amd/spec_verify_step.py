@@ -31,16 +31,8 @@ GQA_HQ, GQA_HKV, GQA_DH = 24, 4, 256
 GQA_QG = GQA_HQ * 2 * GQA_DH              # 12288 (query and gate interleaved per head)
 INTER = 17408
 ROPE_DIM, ROPE_THETA = 64, 1e7
-RMS_EPS = 1e-6
 DN_IN_N = DN_QKV + DN_VAL + 2 * DN_HV     # 16480 = qkv | z | a | b
 DN_IN_PAD = ((DN_IN_N + 63) // 64) * 64   # 16512 (the GEMM takes N % 64 == 0)
-
-
-def rms_norm_1p(x, w):
-    """(1 + w) * x * rsqrt(mean(x^2) + eps) in fp32, cast back (static_decode.py:322-335)."""
-    xf = x.float()
-    n = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + RMS_EPS)
-    return ((1.0 + w) * n).to(x.dtype)
 
 
 def rope_tables(positions):
@@ -147,17 +139,15 @@ class VerifySlice:
         self.prev_accepted = None
         self.timer = _untimed
 
-    # ---- layers --------------------------------------------------------------------------
-    def _deltanet(self, L, x):
+    # ---- layers: each takes the normed input and returns the residual delta -------------
+    def _deltanet(self, L, h):
         B, T = self.B, self.T
-        h = rms_norm_1p(x, L["in_norm"])
         proj = fp8_linear(h, L["in_proj"], self.timer, f"fp8.matmul[{B * T}x{HIDDEN}x{DN_IN_PAD}]")
-        mixed = proj[:, :DN_QKV].contiguous().reshape(-1)
-        z = proj[:, DN_QKV:DN_QKV + DN_VAL].contiguous().reshape(B * T * DN_HV, DN_D)
-        a = proj[:, DN_QKV + DN_VAL:DN_QKV + DN_VAL + DN_HV].float().contiguous().reshape(-1)
-        b = proj[:, DN_QKV + DN_VAL + DN_HV:DN_IN_N].float().contiguous().reshape(-1)
-        args = (mixed, L["conv_state"], L["conv_w"], L["conv_b"], a, b, z, L["A_log"],
-                L["dt_bias"], L["norm_w"])
+        mixed, z, a, b = self.timer("glue.deltanet_split", torch.ops.glue.deltanet_split, proj,
+                                    DN_QKV, DN_VAL, DN_HV)
+        mixed = mixed.reshape(-1)
+        args = (mixed, L["conv_state"], L["conv_w"], L["conv_b"], a.reshape(-1), b.reshape(-1),
+                z.reshape(B * T * DN_HV, DN_D), L["A_log"], L["dt_bias"], L["norm_w"])
         if L["ckpt"] is None:
             ckpt, out = self.timer("deltanet.verify", torch.ops.deltanet.verify_batched,
                                    L["state"], *args)
@@ -165,42 +155,65 @@ class VerifySlice:
             ckpt, out = self.timer("deltanet.verify", torch.ops.deltanet.verify_from_ckpt,
                                    L["ckpt"], self.prev_accepted, *args)
         L["pending"] = (ckpt, mixed)
-        return x + fp8_linear(out.reshape(B * T, DN_VAL), L["out_proj"], self.timer,
-                              f"fp8.matmul[{B * T}x{DN_VAL}x{HIDDEN}]")
+        return fp8_linear(out.reshape(B * T, DN_VAL), L["out_proj"], self.timer,
+                          f"fp8.matmul[{B * T}x{DN_VAL}x{HIDDEN}]")
 
-    def _gqa(self, L, x, cos, sin):
+    def _gqa(self, L, h, cos, sin):
         B, T = self.B, self.T
-        h = rms_norm_1p(x, L["in_norm"])
         proj = fp8_linear(h, L["qkv_proj"], self.timer,
                           f"fp8.matmul[{B * T}x{HIDDEN}x{GQA_QG + 2 * GQA_HKV * GQA_DH}]")
-        qg = proj[:, :GQA_QG].reshape(B, T, GQA_HQ, 2 * GQA_DH)
-        query = qg[..., :GQA_DH].contiguous()
-        gate = qg[..., GQA_DH:].contiguous()
-        kv = proj[:, GQA_QG:].reshape(B, T, 2, GQA_HKV, GQA_DH)
-        key = kv[:, :, 0].contiguous()
-        value = kv[:, :, 1].contiguous()
-        self.timer("gqa.kv_append", torch.ops.gqa.kv_append, key, value, L["k_norm"], cos, sin,
-                   L["cache_k"], L["cache_v"], self.kv_len)
+        query, gate, key, value = self.timer("glue.gqa_split", torch.ops.glue.gqa_split, proj,
+                                             GQA_HQ, GQA_HKV, GQA_DH)
+        query = query.reshape(B, T, GQA_HQ, GQA_DH)
+        gate = gate.reshape(B, T, GQA_HQ, GQA_DH)
+        self.timer("gqa.kv_append", torch.ops.gqa.kv_append, key.reshape(B, T, GQA_HKV, GQA_DH),
+                   value.reshape(B, T, GQA_HKV, GQA_DH), L["k_norm"], cos, sin, L["cache_k"],
+                   L["cache_v"], self.kv_len)
         attn = self.timer("gqa.tail_verify", torch.ops.gqa.tail_verify, query, gate, L["q_norm"],
                           cos, sin, L["cache_k"], L["cache_v"], self.kv_len)
-        return x + fp8_linear(attn.reshape(B * T, GQA_HQ * GQA_DH), L["o_proj"], self.timer,
-                              f"fp8.matmul[{B * T}x{GQA_HQ * GQA_DH}x{HIDDEN}]")
+        return fp8_linear(attn.reshape(B * T, GQA_HQ * GQA_DH), L["o_proj"], self.timer,
+                          f"fp8.matmul[{B * T}x{GQA_HQ * GQA_DH}x{HIDDEN}]")
 
-    def _mlp(self, L, x):
-        h = rms_norm_1p(x, L["post_norm"])
-        M = x.shape[0]
+    def _mlp(self, L, h):
+        M = h.shape[0]
         gu = fp8_linear(h, L["gate_up"], self.timer, f"fp8.matmul[{M}x{HIDDEN}x{2 * INTER}]")
-        act = (torch.nn.functional.silu(gu[:, :INTER].float()) * gu[:, INTER:].float()).to(torch.bfloat16)
-        return x + fp8_linear(act, L["down"], self.timer, f"fp8.matmul[{M}x{INTER}x{HIDDEN}]")
+        act = self.timer("glue.silu_mul", torch.ops.glue.silu_mul, gu)
+        return fp8_linear(act, L["down"], self.timer, f"fp8.matmul[{M}x{INTER}x{HIDDEN}]")
 
-    def forward(self, x):
-        """x [B*T, 5120] bf16 -> hidden after the slice (the verify positions' features)."""
-        pos = self.kv_len.long().unsqueeze(1) + torch.arange(self.T, device=x.device)
-        cos, sin = rope_tables(pos)
-        for L in self.layers:
-            x = self._deltanet(L, x) if L["kind"] == "D" else self._gqa(L, x, cos, sin)
-            x = self._mlp(L, x)
-        return x
+    def forward(self, x, cos=None, sin=None, trace=None):
+        """x [B*T, 5120] bf16 -> hidden after the slice (the verify positions' features).
+        Per layer, as the reference's decode loop (static_decode.py:533-542):
+          normed = rms_norm(hidden); hidden += layer(normed);
+          normed = rms_norm(hidden); hidden += mlp(normed)
+        with every residual add fused into the norm that follows it. If `trace` is a list,
+        the residual stream entering each sublayer (mixer, then MLP, per layer) and the final
+        hidden are appended to it."""
+        if cos is None:
+            pos = self.kv_len.long().unsqueeze(1) + torch.arange(self.T, device=x.device)
+            cos, sin = rope_tables(pos)
+        layers = self.layers
+        hidden = x
+        normed = self.timer("normfuse.rms_norm", torch.ops.normfuse.rms_norm, x,
+                            layers[0]["in_norm"])
+        for i, L in enumerate(layers):
+            if trace is not None:
+                trace.append(hidden)
+            d = self._deltanet(L, normed) if L["kind"] == "D" else self._gqa(L, normed, cos, sin)
+            hidden, normed = self.timer("normfuse.residual_rms_norm",
+                                        torch.ops.normfuse.residual_rms_norm, hidden, d,
+                                        L["post_norm"])
+            if trace is not None:
+                trace.append(hidden)
+            d = self._mlp(L, normed)
+            if i + 1 < len(layers):
+                hidden, normed = self.timer("normfuse.residual_rms_norm",
+                                            torch.ops.normfuse.residual_rms_norm, hidden, d,
+                                            layers[i + 1]["in_norm"])
+            else:
+                hidden = hidden + d
+        if trace is not None:
+            trace.append(hidden)
+        return hidden
 
     def accept_and_rollback(self, accepted):
         """Commit `accepted` drafts per sequence: DeltaNet continues from checkpoint
@@ -215,9 +228,10 @@ class VerifySlice:
         self.prev_accepted = accepted
         self.kv_len = self.kv_len + accepted + 1
 
-    def step(self, x, target_logits, draft_logits, draft_ids, u_accept, u_sample, greedy=False):
+    def step(self, x, target_logits, draft_logits, draft_ids, u_accept, u_sample, greedy=False,
+             trace=None):
         """One verify + accept + rollback step. Returns (hidden, accepted, out_ids)."""
-        h = self.forward(x)
+        h = self.forward(x, trace=trace)
         if greedy:
             accepted, out_ids = self.timer("spec.accept_greedy", torch.ops.spec.accept_greedy,
                                            target_logits, draft_ids)

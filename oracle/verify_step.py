@@ -10,7 +10,7 @@ norms and DeltaNet parameters as float32, the decode state (DeltaNet state [B,Hv
 and conv state bits [B,QKV,3]; GQA cache bits [B,Hkv,S,256]) and kv_len [B].
 
 Pinning: composition of pinned op oracles; the end-to-end GPU test compares the device
-step against it (tests/test_gpu_verify_step.py).
+step against it over two consecutive steps (tests/test_gpu_verify_step.py).
 """
 import numpy as np
 
@@ -35,9 +35,31 @@ def rms_norm_1p_bits(x_bits, w):
     return bf16((np.float32(1.0) + np.asarray(w, np.float32)) * n)
 
 
+FP8_WEIGHTS = ("in_proj", "out_proj", "qkv_proj", "o_proj", "gate_up", "down")
+
+
+def decode_weights(layers):
+    """Decode every fp8 weight of the layer dicts to float32 [K, N] once (in place). Every
+    e4m3fn value is exact in float32; a static model keeps them decoded across steps."""
+    for L in layers:
+        for nm in FP8_WEIGHTS:
+            if nm in L and L[nm][0].dtype != np.float32:
+                w, s = L[nm]
+                L[nm] = (of.DECODE_LUT[np.asarray(w).view(np.uint8)].astype(np.float32), s)
+    return layers
+
+
 def linear(x_bits, wq):
+    """bf16(x . W * scale). Raw fp8 bytes go through the pinned float64 oracle; decoded
+    float32 weights (decode_weights) use a float32 product, whose relative error
+    (about K * 2^-24 <= 1e-3 * 2^-9 for K <= 17408) is far below the bf16 rounding of the
+    output."""
     w, s = wq
-    return bf16(of.fp8_matmul(x_bits, w, np.asarray(s).reshape(-1)))
+    s = np.asarray(s, np.float32).reshape(1, -1)
+    if w.dtype == np.float32:
+        x = bf16_bits_to_f32(x_bits).astype(np.float32)
+        return bf16((x @ w) * s)
+    return bf16(of.fp8_matmul(x_bits, w, s.reshape(-1)))
 
 
 def add(a_bits, b_bits):
@@ -72,25 +94,43 @@ def gqa_layer(L, x, B, T, hq, hkv, kv_len, cos, sin):
 
 
 def mlp(L, x, inter):
+    """SwiGLU as _mlp_layer (static_decode.py:951-963): gate, up and silu(gate) are bf16
+    tensors, so silu(gate) is rounded to bf16 before the product."""
     h = rms_norm_1p_bits(x, L["post_norm"])
     gu = bf16_bits_to_f32(linear(h, L["gate_up"])).astype(np.float32)
     g, u = gu[:, :inter], gu[:, inter:]
-    act = bf16((g / (np.float32(1.0) + np.exp(-g))) * u)
+    s = bf16_bits_to_f32(bf16(g / (np.float32(1.0) + np.exp(-g)))).astype(np.float32)
+    act = bf16(s * u)
     return add(x, linear(act, L["down"]))
 
 
 def verify_step(layers, x_bits, kv_len, B, T, target, draft, draft_ids, u_accept, u_sample,
-                cos, sin, dn_heads=(16, 48), gqa_heads=(24, 4), inter=17408):
+                cos, sin, dn_heads=(16, 48), gqa_heads=(24, 4), inter=17408,
+                layer_inputs=None, layer_outputs=None):
     """One verify + accept + rollback step. Returns (hidden bits [B*T, H], accepted, out_ids);
     layer states are updated in place (DeltaNet state = ckpt[accepted], conv rolled back,
-    GQA caches written); kv_len is returned advanced as the 4th value."""
+    GQA caches written); kv_len is returned advanced as the 4th value.
+
+    layer_inputs (optional): the residual stream entering each sublayer (mixer, then MLP,
+    per layer), as bits; sublayer j then starts from layer_inputs[j] instead of sublayer
+    j-1's output (teacher forcing, so a comparison measures each sublayer's own error
+    instead of re-rounded differences carried through bf16 sublayers).
+    layer_outputs (optional list): each sublayer's output is appended."""
     x = np.asarray(x_bits, np.uint16)
+    j = 0
     for L in layers:
-        if L["kind"] == "D":
-            x = deltanet_layer(L, x, B, T, *dn_heads)
-        else:
-            x = gqa_layer(L, x, B, T, *gqa_heads, kv_len, cos, sin)
-        x = mlp(L, x, inter)
+        for part in ("mixer", "mlp"):
+            if layer_inputs is not None:
+                x = np.asarray(layer_inputs[j], np.uint16)
+            if part == "mlp":
+                x = mlp(L, x, inter)
+            elif L["kind"] == "D":
+                x = deltanet_layer(L, x, B, T, *dn_heads)
+            else:
+                x = gqa_layer(L, x, B, T, *gqa_heads, kv_len, cos, sin)
+            if layer_outputs is not None:
+                layer_outputs.append(x)
+            j += 1
     accepted, out_ids = oa.accept_rejection(target, draft, draft_ids, u_accept, u_sample, 1.0)
     for L in layers:
         if L["kind"] == "D":

@@ -22,7 +22,7 @@ def test_library_exports_every_declared_symbol():
     import npn_native
     lib = npn_native.lib()
     names = _declared()
-    assert len(names) >= 14
+    assert len(names) >= 18
     for n in names:
         assert hasattr(lib, n), f"{n} declared in the header but not exported"
     assert set(names) == set(npn_native.SIGNATURES)
@@ -76,6 +76,15 @@ def test_ops_register_and_propagate_shapes():
         acc, ids = torch.ops.spec.accept_greedy(torch.empty(B, T, 1000),
                                                 torch.empty(B, T - 1, dtype=torch.int64))
         assert acc.shape == (B,) and ids.shape == (B, T)
+        x = torch.empty(16, 5120, dtype=bf)
+        h2, nrm = torch.ops.normfuse.residual_rms_norm(x, x, torch.empty(5120))
+        assert h2.shape == nrm.shape == x.shape
+        assert torch.ops.normfuse.rms_norm(x, torch.empty(5120)).shape == x.shape
+        assert torch.ops.glue.silu_mul(torch.empty(16, 64, dtype=bf)).shape == (16, 32)
+        m, zz, a, b = torch.ops.glue.deltanet_split(torch.empty(16, 16512, dtype=bf), 10240, 6144, 48)
+        assert (m.shape, zz.shape, a.shape, a.dtype) == ((16, 10240), (16, 6144), (16, 48), f32)
+        q, gt, k, v = torch.ops.glue.gqa_split(torch.empty(16, 14336, dtype=bf), 24, 4, 256)
+        assert q.shape == gt.shape == (16, 24, 256) and k.shape == v.shape == (16, 4, 256)
 
 
 def test_ops_refuse_cpu_tensors():

@@ -179,23 +179,31 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemm_kernel(GemmArgs a) {
 
 // ---------------------------------------------------------------------------------------
 // Wide kernel for 64 < M <= 256 rows per pass (MFMA-bound: each weight byte feeds 2*M flops).
-// The grid is one workgroup per CU. Columns are split into 16-wide units spread evenly over
-// the workgroups (u0..u1, at most NTM units each), so every CU gets the same work up to one
+// The grid is one workgroup of 8 waves per CU. A single wave per SIMD issues independent
+// bf16 MFMAs at about 55 % of the SIMD's peak, two waves at about 83 % (measured on MI355X),
+// so each SIMD runs two waves. Columns are split into 16-wide units spread evenly over the
+// workgroups (u0..u1, at most 2*NH units each), so every CU gets the same work up to one
 // unit; workgroups are placed so logically adjacent column ranges share an XCD and its L2
-// (a range is a 128..144-byte segment of each weight row, so neighbours share lines).
+// (a range is a 128..160-byte segment of each weight row, so neighbours share lines).
 //
 // Data path, all global reads by LDS DMA (npn::lds_dma16, no VGPR staging) into a
 // 3-stage ring, two 64-k chunks ahead of the MFMAs:
-//   x chunk  [256 rows][64 k] bf16, 16-byte chunks XOR-swizzled by (row & 7)
-//   W chunk  [64 k][ncols] raw e4m3fn bytes (the [K, N] layout, one row segment per k)
-// Each of the 4 waves owns 64 rows: A operands come from the x tile (ds_read_b128), B
-// operands from the W tile with the 8-bit transposed read ds_read_b64_tr_b8 -- in each
-// 16-lane group, lane i gets byte (i & 7) of the 8-byte chunk supplied by lane 2j + (i >> 3)
-// as its j-th byte, so lanes 2j + h supply row k0 + 8G + j, columns 8h..8h+7, and lane i
-// receives column i's 8 consecutive k -- then 4 v_cvt_scalef32_pk_bf16_fp8 make the bf16
-// B operand.
+//   x chunk  [256 rows][64 k] bf16, 16-byte chunks XOR-swizzled by (row >> 1) & 7, so the
+//            16 rows of an A-operand read cover all 64 LDS banks once (row parity x chunk)
+//   W chunk  [64 k][16 * nup] raw e4m3fn bytes: each k row's nu 16-byte column units (the
+//            [K, N] layout, one row segment per k) padded to nup = nu | 1 units, so the 16
+//            rows of a transposed B read start on 16 distinct 4-bank groups (nup odd)
+// Wave w owns rows 64*(w & 3) .. +63 and column tiles NH*(w >> 2) .. +NH-1 of the
+// workgroup's units, so the x tile is loaded once per CU and each B tile is read and
+// converted by the four waves of its column half (one per row quarter). A operands come from
+// the x tile (ds_read_b128), B operands from the W tile with the 8-bit transposed read
+// ds_read_b64_tr_b8 -- in each 16-lane group, lane i gets byte (i & 7) of the 8-byte chunk
+// supplied by lane 2j + (i >> 3) as its j-th byte, so lanes 2j + h supply row k0 + 8G + j,
+// columns 8h..8h+7, and lane i receives column i's 8 consecutive k -- then 4
+// v_cvt_scalef32_pk_bf16_fp8 make the bf16 B operand.
 constexpr int KC = 64;          // k per pipeline chunk
 constexpr int WIDE_WG = 256;    // workgroups per pass (one per CU)
+constexpr int WIDE_THREADS = 512;
 constexpr int NSTAGE = 3;
 
 struct WideArgs {
@@ -213,14 +221,13 @@ __device__ __forceinline__ i32x2 lds_tr8(const uint8_t* p) {
   return __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) i32x2*)(p));
 }
 
-
-template <int NTM>
-__global__ __launch_bounds__(256, 1) void fp8_gemm_wide_kernel(WideArgs a) {
-  constexpr int XBYTES = 256 * KC * 2;                 // 32 KiB x stage
-  constexpr int WI = (KC * NTM + 255) / 256;           // W DMA instructions per thread per chunk
-  constexpr int WBYTES = WI * 256 * 16;                // W stage incl. slack for padded lanes
+template <int NH>  // column tiles per wave; a workgroup holds up to 2*NH units
+__global__ __launch_bounds__(WIDE_THREADS, 1) void fp8_gemm_wide_kernel(WideArgs a) {
+  constexpr int XBYTES = 256 * KC * 2;                          // 32 KiB x stage
+  constexpr int WI = (KC * (2 * NH + 1) + WIDE_THREADS - 1) / WIDE_THREADS;  // W DMA per thread
+  constexpr int WBYTES = WI * WIDE_THREADS * 16;                // W stage incl. slack
   constexpr int STAGE = XBYTES + WBYTES;
-  constexpr int XI = XBYTES / (256 * 16);              // x DMA instructions per thread (8)
+  constexpr int XI = XBYTES / (WIDE_THREADS * 16);              // x DMA per thread (4)
   __shared__ __attribute__((aligned(16))) uint8_t smem[NSTAGE * STAGE];
 
   const int nwg = gridDim.x;
@@ -234,51 +241,56 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_wide_kernel(WideArgs a) {
   const int nu = u1 - u0;
   if (nu <= 0) return;
   const int n0 = 16 * u0;
-  const int ncols = 16 * nu;
+  const int nup = nu | 1;          // W row stride in the stage, in 16-byte units (odd)
   const int nchunks = a.K / KC;
   const int c_lo = (int)((long)nchunks * sk / a.split_k);
   const int c_hi = (int)((long)nchunks * (sk + 1) / a.split_k);
   const int m_base = blockIdx.y * 256;
   const int tid = threadIdx.x;
-  const int wv = tid >> 6, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int wr = wv & 3, wc = wv >> 2;  // row quarter, column half
   const int i = lane & 15, G = lane >> 4;
   const int mlast = a.M - 1;
 
-  // DMA of chunk c into stage st: x rows (8 instructions / thread), then W rows.
+  // DMA of chunk c into stage st: x rows (XI instructions / thread), then W rows.
   auto issue = [&](int c, int st) {
     uint8_t* xs = smem + st * STAGE;
     uint8_t* ws = xs + XBYTES;
 #pragma unroll
     for (int q = 0; q < XI; ++q) {
-      const int f = q * 256 + tid;            // 16-byte slot in the x stage
+      const int f = q * WIDE_THREADS + tid;   // 16-byte slot in the x stage
       const int row = f >> 3, pos = f & 7;    // 8 slots per 128-byte row
       int m = m_base + row;
       m = m <= mlast ? m : mlast;
-      const uint16_t* src = a.x + (size_t)m * a.K + c * KC + 8 * (pos ^ (row & 7));
-      npn::lds_dma16(src, xs + q * 4096 + (tid & ~63) * 16);
+      const uint16_t* src = a.x + (size_t)m * a.K + c * KC + 8 * (pos ^ ((row >> 1) & 7));
+      npn::lds_dma16(src, xs + q * (WIDE_THREADS * 16) + (tid & ~63) * 16);
     }
 #pragma unroll
     for (int q = 0; q < WI; ++q) {
-      int f = q * 256 + tid;                  // 16-byte slot of the W stage
-      if (f >= KC * nu) f = 0;                // padded lanes re-read slot 0 into the slack
-      const int r = f / nu, cc = f - (f / nu) * nu;
+      int f = q * WIDE_THREADS + tid;         // 16-byte slot of the W stage
+      if (f >= KC * nup) f = 0;               // lanes past the stage re-read slot 0 (slack)
+      const int r = f / nup;
+      int cc = f - r * nup;
+      cc = cc < nu ? cc : 0;                  // row pad slot: re-read the row's first unit
       const uint8_t* src = a.w + (size_t)(c * KC + r) * a.N + n0 + 16 * cc;
-      npn::lds_dma16(src, ws + q * 4096 + (tid & ~63) * 16);
+      npn::lds_dma16(src, ws + q * (WIDE_THREADS * 16) + (tid & ~63) * 16);
     }
   };
 
-  f32x4 acc[4][NTM];
+  f32x4 acc[4][NH];
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-    for (int nt = 0; nt < NTM; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int nt = 0; nt < NH; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  // B-operand tr8 address parts: lane supplies row 8G + (i >> 1), column half (i & 1), of
+  // this wave's first column tile.
+  const int trow = 8 * G + (i >> 1);
+  const int tcol = 8 * (i & 1) + 16 * NH * wc;
+
+  // Ring: chunk c in stage (c - c_lo) % 3, issued two chunks ahead of its use.
   if (c_lo < c_hi) issue(c_lo, 0);
   if (c_lo + 1 < c_hi) issue(c_lo + 1, 1);
-
-  // B-operand tr8 address parts: lane supplies row 8G + (i >> 1), column half (i & 1).
-  const int trow = 8 * G + (i >> 1);
-  const int tcol = 8 * (i & 1);
 
   for (int c = c_lo; c < c_hi; ++c) {
     const int st = (c - c_lo) % NSTAGE;
@@ -292,48 +304,67 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_wide_kernel(WideArgs a) {
     if (c + 2 < c_hi) issue(c + 2, (c + 2 - c_lo) % NSTAGE);
     const uint8_t* xs = smem + st * STAGE;
     const uint8_t* ws = xs + XBYTES;
-    // Every workgroup runs NTM column tiles: tiles past its own nu read in-bounds LDS
-    // (the next rows / stage slack) and are never stored, and the workgroups with nu < NTM
-    // are not the ones that set the kernel's duration.
+    // Every wave runs NH column tiles: tiles past the workgroup's nu read in-bounds LDS
+    // (the next rows / stage slack) and are never stored.
+    // All A and B fragments of the chunk are read first; the B tiles of k-step 0 are
+    // converted, then k-step 0's MFMAs alternate with k-step 1's conversions, so the MFMA
+    // stream is not stalled behind a convert-then-use chain per tile.
+    bf16x8 aop[2][4];
+    i32x2 raw[2][NH];
 #pragma unroll
-    for (int ks = 0; ks < KC / 32; ++ks) {
-      bf16x8 aop[4];
+    for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) {
-        const int row = 64 * wv + 16 * mt + i;
-        const int pos = (4 * ks + G) ^ (row & 7);
-        aop[mt] = *reinterpret_cast<const bf16x8*>(xs + row * (KC * 2) + pos * 16);
+        const int row = 64 * wr + 16 * mt + i;
+        const int pos = (4 * ks + G) ^ ((row >> 1) & 7);
+        aop[ks][mt] = *reinterpret_cast<const bf16x8*>(xs + row * (KC * 2) + pos * 16);
       }
-      i32x2 raw[NTM];
-      const uint8_t* wrow = ws + (32 * ks + trow) * ncols + tcol;
+      const uint8_t* wrow = ws + (32 * ks + trow) * (16 * nup) + tcol;
 #pragma unroll
-      for (int nt = 0; nt < NTM; ++nt) raw[nt] = lds_tr8(wrow + 16 * nt);
+      for (int nt = 0; nt < NH; ++nt) raw[ks][nt] = lds_tr8(wrow + 16 * nt);
+    }
+    bf16x8 bop[2][NH];
 #pragma unroll
-      for (int nt = 0; nt < NTM; ++nt) {
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int nt = 0; nt < NH; ++nt) {
         u32x4 bw;
-        bw[0] = fp8x2_to_bf16x2<false>((uint32_t)raw[nt][0]);
-        bw[1] = fp8x2_to_bf16x2<true>((uint32_t)raw[nt][0]);
-        bw[2] = fp8x2_to_bf16x2<false>((uint32_t)raw[nt][1]);
-        bw[3] = fp8x2_to_bf16x2<true>((uint32_t)raw[nt][1]);
-        const bf16x8 bop = __builtin_bit_cast(bf16x8, bw);
+        bw[0] = fp8x2_to_bf16x2<false>((uint32_t)raw[ks][nt][0]);
+        bw[1] = fp8x2_to_bf16x2<true>((uint32_t)raw[ks][nt][0]);
+        bw[2] = fp8x2_to_bf16x2<false>((uint32_t)raw[ks][nt][1]);
+        bw[3] = fp8x2_to_bf16x2<true>((uint32_t)raw[ks][nt][1]);
+        bop[ks][nt] = __builtin_bit_cast(bf16x8, bw);
+      }
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int nt = 0; nt < NH; ++nt)
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt)
-          acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop[mt], bop, acc[mt][nt], 0, 0, 0);
-      }
+          acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop[ks][mt], bop[ks][nt],
+                                                                acc[mt][nt], 0, 0, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 2 * (4 + NH), 0);  // LDS reads
+    __builtin_amdgcn_sched_group_barrier(0x002, 4 * NH, 0);        // k-step 0 conversions
+#pragma unroll
+    for (int j = 0; j < 4 * NH; ++j) {                             // k-step 0 MFMAs with
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);           // k-step 1 conversions
+      __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);
     }
+    __builtin_amdgcn_sched_group_barrier(0x008, 4 * NH, 0);        // k-step 1 MFMAs
   }
 
-  // Epilogue: lane (i, G) holds rows 64wv + 16mt + 4G + r, column n0 + 16nt + i.
+  // Epilogue: lane (i, G) holds rows 64wr + 16mt + 4G + r, column n0 + 16(NH wc + nt) + i.
 #pragma unroll
-  for (int nt = 0; nt < NTM; ++nt) {
-    if (nt >= nu) continue;
-    const int col = n0 + 16 * nt + i;
+  for (int nt = 0; nt < NH; ++nt) {
+    const int unit = NH * wc + nt;
+    if (unit >= nu) continue;
+    const int col = n0 + 16 * unit + i;
     const float sc = a.scale[col];
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int m = m_base + 64 * wv + 16 * mt + 4 * G + r;
+        const int m = m_base + 64 * wr + 16 * mt + 4 * G + r;
         if (m >= a.M) continue;
         if (a.split_k == 1) a.out[(size_t)m * a.N + col] = npn::f32_to_bf16(acc[mt][nt][r] * sc);
         else a.partial[((size_t)sk * a.M + m) * a.N + col] = acc[mt][nt][r];
@@ -360,8 +391,8 @@ struct GemmPlan {
   int units, groups, ntm;
 };
 
-// Wide-kernel instantiations: most 16-column units one workgroup can hold.
-constexpr int kWideNT[] = {1, 2, 3, 5, 9};
+// Wide-kernel instantiations: column tiles per wave (a workgroup holds twice as many units).
+constexpr int kWideNH[] = {1, 2, 3, 5};
 
 // Wide-kernel split-K choice: modelled time = max(MFMA time at the balance efficiency of the
 // column split, HBM time of weights + split-K partials). MFMA at 60% of 2.5 PFLOP/s, HBM at
@@ -376,8 +407,8 @@ bool plan_wide(int M, int K, int N, GemmPlan& p) {
     const int groups = units < WIDE_WG / s ? units : WIDE_WG / s;
     const int need = (units + groups - 1) / groups;
     int ntm = 0;
-    for (int v : kWideNT)
-      if (v >= need) { ntm = v; break; }
+    for (int v : kWideNH)
+      if (2 * v >= need) { ntm = v; break; }
     if (ntm == 0) continue;
     const double eff = (double)units / groups / need;
     const double bytes = (double)K * N + (s > 1 ? 2.0 * s * M * (double)N * 4 : 0.0);
@@ -443,12 +474,12 @@ extern "C" int npn_fp8_matmul(const uint16_t* x, const int8_t* w, const float* s
                 static_cast<float*>(workspace), M, K, N, p.units, p.groups, p.split_k};
     const int nwg = ((p.groups * p.split_k + 7) / 8) * 8;  // multiple of 8 for the XCD map
     const dim3 grid(nwg, p.passes);
+    const dim3 block(WIDE_THREADS);
     switch (p.ntm) {
-      case 1: hipLaunchKernelGGL(fp8_gemm_wide_kernel<1>, grid, dim3(256), 0, s, wa); break;
-      case 2: hipLaunchKernelGGL(fp8_gemm_wide_kernel<2>, grid, dim3(256), 0, s, wa); break;
-      case 3: hipLaunchKernelGGL(fp8_gemm_wide_kernel<3>, grid, dim3(256), 0, s, wa); break;
-      case 5: hipLaunchKernelGGL(fp8_gemm_wide_kernel<5>, grid, dim3(256), 0, s, wa); break;
-      default: hipLaunchKernelGGL(fp8_gemm_wide_kernel<9>, grid, dim3(256), 0, s, wa); break;
+      case 1: hipLaunchKernelGGL(fp8_gemm_wide_kernel<1>, grid, block, 0, s, wa); break;
+      case 2: hipLaunchKernelGGL(fp8_gemm_wide_kernel<2>, grid, block, 0, s, wa); break;
+      case 3: hipLaunchKernelGGL(fp8_gemm_wide_kernel<3>, grid, block, 0, s, wa); break;
+      default: hipLaunchKernelGGL(fp8_gemm_wide_kernel<5>, grid, block, 0, s, wa); break;
     }
     if (p.split_k > 1) {
       const size_t total = (size_t)M * N;

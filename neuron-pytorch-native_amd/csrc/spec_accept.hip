@@ -25,9 +25,11 @@
 
 namespace {
 
-constexpr int CHK = 8192;      // vocabulary entries per chunk
+constexpr int CHK = 8192;      // vocabulary entries per chunk (logit passes)
 constexpr int THREADS = 256;   // CHK / THREADS = 32 entries per thread
 constexpr int PER_T = CHK / THREADS;
+constexpr int MCHK = 2048;     // entries per chunk of the residual mass / inverse-CDF pass
+constexpr int PER_M = MCHK / THREADS;  // 8 consecutive entries per thread
 
 typedef unsigned __int128 u128;
 
@@ -119,6 +121,34 @@ __device__ float block_max(float v, float* sh) {
   return m;
 }
 
+// ---- chunk visitor -----------------------------------------------------------------------
+// Calls f(v, x) for this thread's share of entries [v0, v0 + CHK) of a row (x = src[v]).
+// With vec4 (row 16-byte aligned, V % 4 == 0) the thread reads PER_T/4 float4s at
+// v0 + 4 * (j * THREADS + tid), else PER_T floats at v0 + j * THREADS + tid. Every caller
+// combines the visited values with an order-independent operation (max, exact integer
+// sums, or the total order of the argmax), so the assignment does not affect results.
+template <typename F>
+__device__ __forceinline__ void visit_chunk(const float* src, int v0, int V, bool vec4, F f) {
+  if (vec4) {
+#pragma unroll
+    for (int j = 0; j < PER_T / 4; ++j) {
+      const int v = v0 + 4 * (j * THREADS + (int)threadIdx.x);
+      if (v < V) {
+        const float4 x = *reinterpret_cast<const float4*>(src + v);
+        f(v, x.x);
+        f(v + 1, x.y);
+        f(v + 2, x.z);
+        f(v + 3, x.w);
+      }
+    }
+  } else {
+    for (int j = 0; j < PER_T; ++j) {
+      const int v = v0 + j * THREADS + (int)threadIdx.x;
+      if (v < V) f(v, src[v]);
+    }
+  }
+}
+
 // ---- greedy ------------------------------------------------------------------------------
 // (val, idx) order: NaN above every number (first NaN wins), then larger value, then
 // smaller index. A total order, so any merge order gives the same winner.
@@ -135,19 +165,15 @@ struct ArgPart {
 
 __global__ __launch_bounds__(THREADS) void argmax_chunk_kernel(const float* __restrict__ logits,
                                                                 ArgPart* __restrict__ part,
-                                                                int V, int nch) {
+                                                                int V, int nch, bool vec4) {
   const int row = blockIdx.y, c = blockIdx.x;
   const float* src = logits + (size_t)row * V;
   const int v0 = c * CHK;
   float bv = -INFINITY;
   int bi = 0x7FFFFFFF;
-  for (int j = 0; j < PER_T; ++j) {
-    const int v = v0 + j * THREADS + threadIdx.x;
-    if (v < V) {
-      const float x = src[v];
-      if (beats(x, v, bv, bi)) { bv = x; bi = v; }
-    }
-  }
+  visit_chunk(src, v0, V, vec4, [&](int v, float x) {
+    if (beats(x, v, bv, bi)) { bv = x; bi = v; }
+  });
   for (int off = 32; off > 0; off >>= 1) {
     const float ov = __shfl_xor(bv, off, 64);
     const int oi = __shfl_xor(bi, off, 64);
@@ -200,14 +226,16 @@ struct RejArgs {
   float inv_temp;
   int32_t* accepted;
   int64_t* out_ids;
-  int B, K, V, nch;
+  int B, K, V, nch, nchm;  // chunks of CHK (logit passes) and of MCHK (mass / pick)
+  bool vec4;          // logit rows 16-byte aligned and V % 4 == 0
   // workspace
   float* rmax;        // [rows][nch]   rows = B*(K+1) target rows, then B*K draft rows
   uint64_t* zsum;     // [rows][nch]
   uint64_t* ex;       // [rows]        E at the row's draft token (target/draft rows i < K)
   int32_t* dec_row;   // [B]           sampling row index (target row; draft row or -1)
   uint64_t* dec_z;    // [B][2]        Zp, Zq of the sampling rows
-  u128* cmass;        // [B][nch]
+  float* dec_m;       // [B][2]        row maxima of the sampling rows (scaled logits)
+  u128* cmass;        // [B][nchm]
 };
 
 __device__ __forceinline__ const float* row_ptr(const RejArgs& a, int row) {
@@ -237,10 +265,7 @@ __global__ __launch_bounds__(THREADS) void rej_max_kernel(RejArgs a) {
   const float* src = row_ptr(a, row);
   const int v0 = c * CHK;
   float m = -INFINITY;
-  for (int j = 0; j < PER_T; ++j) {
-    const int v = v0 + j * THREADS + threadIdx.x;
-    if (v < a.V) m = fmaxf(m, scaled(src[v], a.inv_temp));
-  }
+  visit_chunk(src, v0, a.V, a.vec4, [&](int, float x) { m = fmaxf(m, scaled(x, a.inv_temp)); });
   __shared__ float sh[THREADS / 64];
   m = block_max(m, sh);
   if (threadIdx.x == 0) a.rmax[(size_t)row * a.nch + c] = m;
@@ -258,10 +283,8 @@ __global__ __launch_bounds__(THREADS) void rej_sum_kernel(RejArgs a) {
   const float m = row_max(a, row);
   const int v0 = c * CHK;
   uint64_t z = 0;
-  for (int j = 0; j < PER_T; ++j) {
-    const int v = v0 + j * THREADS + threadIdx.x;
-    if (v < a.V) z += expfix(scaled(src[v], a.inv_temp) - m);
-  }
+  visit_chunk(src, v0, a.V, a.vec4,
+              [&](int, float x) { z += expfix(scaled(x, a.inv_temp) - m); });
   __shared__ uint64_t sh[THREADS / 64];
   z = block_sum_u64(z, sh);
   if (threadIdx.x == 0) {
@@ -271,41 +294,62 @@ __global__ __launch_bounds__(THREADS) void rej_sum_kernel(RejArgs a) {
   }
 }
 
-__device__ __forceinline__ uint64_t row_z(const RejArgs& a, int row) {
-  uint64_t z = 0;
-  for (int c = 0; c < a.nch; ++c) z += a.zsum[(size_t)row * a.nch + c];
-  return z;
-}
-
-// One thread per sequence: the K accept tests, then which rows to sample from.
-__global__ void rej_decide_kernel(RejArgs a) {
-  const int b = blockIdx.x * blockDim.x + threadIdx.x;
-  if (b >= a.B) return;
+// One workgroup per sequence: the Z sums of its 2K+1 rows (chunk partials added in LDS with
+// exact 64-bit atomics, so the order does not matter), the K accept tests, then which rows
+// to sample from, with their Z sums and maxima for the mass and pick kernels.
+__global__ __launch_bounds__(THREADS) void rej_decide_kernel(RejArgs a) {
+  const int b = blockIdx.x;
   const int K = a.K, T = K + 1;
   const int nt = a.B * T;
-  int acc = K;
-  uint64_t zp_s = 0, zq_s = 0;
-  for (int i = 0; i < K; ++i) {
-    const int rt = b * T + i, rd = nt + b * K + i;
-    const uint64_t zp = row_z(a, rt), zq = row_z(a, rd);
-    const uint64_t ep = a.ex[rt], eq = a.ex[rd];
-    const u128 lhs = (u128)uniform_fix(a.u_accept[(size_t)b * K + i]) * eq * zp;
-    const u128 rhs = ((u128)ep * zq) << 24;
-    if (lhs > rhs) {
-      acc = i;
-      zp_s = zp;
-      zq_s = zq;
-      break;
-    }
+  const int nrows = 2 * K + 1;  // local row r: target row r (r <= K), draft row r - T
+  __shared__ unsigned long long zs[2 * 64 + 1];
+  __shared__ int s_acc;
+  __shared__ float shm[THREADS / 64];
+  for (int r = threadIdx.x; r < nrows; r += THREADS) zs[r] = 0;
+  __syncthreads();
+  for (int p = threadIdx.x; p < nrows * a.nch; p += THREADS) {
+    const int r = p / a.nch, c = p - r * a.nch;
+    const int row = r <= K ? b * T + r : nt + b * K + (r - T);
+    atomicAdd(&zs[r], (unsigned long long)a.zsum[(size_t)row * a.nch + c]);
   }
-  if (acc == K) zp_s = row_z(a, b * T + K);
-  a.accepted[b] = acc;
-  a.dec_row[b] = acc;
-  a.dec_z[2 * b] = zp_s;
-  a.dec_z[2 * b + 1] = zq_s;
-  for (int t = 0; t < T; ++t) {
-    if (t < acc) a.out_ids[(size_t)b * T + t] = a.draft_ids[(size_t)b * K + t];
-    else if (t > acc) a.out_ids[(size_t)b * T + t] = -1;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int acc = K;
+    uint64_t zp_s = 0, zq_s = 0;
+    for (int i = 0; i < K; ++i) {
+      const int rt = b * T + i, rd = nt + b * K + i;
+      const uint64_t zp = zs[i], zq = zs[T + i];
+      const uint64_t ep = a.ex[rt], eq = a.ex[rd];
+      const u128 lhs = (u128)uniform_fix(a.u_accept[(size_t)b * K + i]) * eq * zp;
+      const u128 rhs = ((u128)ep * zq) << 24;
+      if (lhs > rhs) {
+        acc = i;
+        zp_s = zp;
+        zq_s = zq;
+        break;
+      }
+    }
+    if (acc == K) zp_s = zs[K];
+    a.accepted[b] = acc;
+    a.dec_row[b] = acc;
+    a.dec_z[2 * b] = zp_s;
+    a.dec_z[2 * b + 1] = zq_s;
+    for (int t = 0; t < T; ++t) {
+      if (t < acc) a.out_ids[(size_t)b * T + t] = a.draft_ids[(size_t)b * K + t];
+      else if (t > acc) a.out_ids[(size_t)b * T + t] = -1;
+    }
+    s_acc = acc;
+  }
+  __syncthreads();
+  const int acc = s_acc;
+  // maxima of the sampling rows (the draft row only after a rejection)
+  const int rows[2] = {b * T + acc, nt + b * K + acc};
+  for (int k = 0; k < (acc < K ? 2 : 1); ++k) {
+    float m = -INFINITY;
+    for (int c = threadIdx.x; c < a.nch; c += THREADS)
+      m = fmaxf(m, a.rmax[(size_t)rows[k] * a.nch + c]);
+    m = block_max(m, shm);
+    if (threadIdx.x == 0) a.dec_m[2 * b + k] = m;
   }
 }
 
@@ -323,13 +367,12 @@ __device__ __forceinline__ SampleRow sample_row(const RejArgs& a, int b) {
   SampleRow s;
   const int rt = b * T + acc;
   s.p = a.target + (size_t)rt * a.V;
-  s.mp = row_max(a, rt);
+  s.mp = a.dec_m[2 * b];
   s.zp = a.dec_z[2 * b];
   s.zq = a.dec_z[2 * b + 1];
   if (acc < K) {
-    const int rd = a.B * T + b * K + acc;
     s.q = a.draft + (size_t)(b * K + acc) * a.V;
-    s.mq = row_max(a, rd);
+    s.mq = a.dec_m[2 * b + 1];
   } else {
     s.q = nullptr;
     s.mq = 0.f;
@@ -337,81 +380,163 @@ __device__ __forceinline__ SampleRow sample_row(const RejArgs& a, int b) {
   return s;
 }
 
-__device__ __forceinline__ u128 weight(const SampleRow& s, int v, float inv_temp) {
-  const uint64_t ep = expfix(scaled(s.p[v], inv_temp) - s.mp);
+__device__ __forceinline__ u128 weight_of(const SampleRow& s, float pv, float qv,
+                                          float inv_temp) {
+  const uint64_t ep = expfix(scaled(pv, inv_temp) - s.mp);
   if (s.q == nullptr) return ep;
-  const uint64_t eq = expfix(scaled(s.q[v], inv_temp) - s.mq);
+  const uint64_t eq = expfix(scaled(qv, inv_temp) - s.mq);
   const u128 x = (u128)ep * s.zq, y = (u128)eq * s.zp;
   return x > y ? x - y : 0;
+}
+
+
+// This thread's PER_M consecutive sampling-row entries starting at v0 (p, and q after a
+// rejection), loaded once; entries at or past V read as p = q = -inf (weight 0 is not
+// used for them: callers stop at V).
+struct RunVals {
+  float p[PER_M], q[PER_M];
+};
+
+__device__ __forceinline__ RunVals load_run(const RejArgs& a, const SampleRow& s, int v0) {
+  RunVals r;
+  if (a.vec4 && v0 + PER_M <= a.V) {
+#pragma unroll
+    for (int j = 0; j < PER_M; j += 4) {
+      const float4 pv = *reinterpret_cast<const float4*>(s.p + v0 + j);
+      r.p[j] = pv.x; r.p[j + 1] = pv.y; r.p[j + 2] = pv.z; r.p[j + 3] = pv.w;
+      if (s.q != nullptr) {
+        const float4 qv = *reinterpret_cast<const float4*>(s.q + v0 + j);
+        r.q[j] = qv.x; r.q[j + 1] = qv.y; r.q[j + 2] = qv.z; r.q[j + 3] = qv.w;
+      } else {
+        r.q[j] = r.q[j + 1] = r.q[j + 2] = r.q[j + 3] = 0.f;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < PER_M; ++j) {
+      const int v = v0 + j;
+      r.p[j] = v < a.V ? s.p[v] : -INFINITY;
+      r.q[j] = (v < a.V && s.q != nullptr) ? s.q[v] : 0.f;
+    }
+  }
+  return r;
 }
 
 __global__ __launch_bounds__(THREADS) void rej_mass_kernel(RejArgs a) {
   const int b = blockIdx.y, c = blockIdx.x;
   const SampleRow s = sample_row(a, b);
-  const int v0 = c * CHK;
+  const int v0 = c * MCHK + (int)threadIdx.x * PER_M;
   u128 m = 0;
-  for (int j = 0; j < PER_T; ++j) {
-    const int v = v0 + j * THREADS + threadIdx.x;
-    if (v < a.V) m += weight(s, v, a.inv_temp);
+  if (v0 < a.V) {
+    const RunVals r = load_run(a, s, v0);
+#pragma unroll
+    for (int j = 0; j < PER_M; ++j)
+      if (v0 + j < a.V) m += weight_of(s, r.p[j], r.q[j], a.inv_temp);
   }
   __shared__ u128 sh[THREADS / 64];
   m = block_sum_u128(m, sh);
-  if (threadIdx.x == 0) a.cmass[(size_t)b * a.nch + c] = m;
+  if (threadIdx.x == 0) a.cmass[(size_t)b * a.nchm + c] = m;
 }
 
-// Inverse CDF: chunk by chunk on the chunk masses, then inside the chosen chunk with a
-// block-wide exclusive scan over per-thread runs of PER_T consecutive entries.
+// ---- 128-bit wave scans (exact integers) ---------------------------------------------------
+__device__ __forceinline__ u128 shfl_u128(u128 v, int src_lane) {
+  uint32_t w[4] = {(uint32_t)v, (uint32_t)(v >> 32), (uint32_t)(v >> 64), (uint32_t)(v >> 96)};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) w[k] = __shfl(w[k], src_lane, 64);
+  return ((u128)w[3] << 96) | ((u128)w[2] << 64) | ((u128)w[1] << 32) | w[0];
+}
+
+__device__ __forceinline__ u128 shfl_up_u128(u128 v, int d) {
+  uint32_t w[4] = {(uint32_t)v, (uint32_t)(v >> 32), (uint32_t)(v >> 64), (uint32_t)(v >> 96)};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) w[k] = __shfl_up(w[k], d, 64);
+  return ((u128)w[3] << 96) | ((u128)w[2] << 64) | ((u128)w[1] << 32) | w[0];
+}
+
+// Inclusive prefix sum over the 64 lanes of a wave.
+__device__ __forceinline__ u128 wave_incl_scan_u128(u128 v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const u128 o = shfl_up_u128(v, d);
+    if (lane >= d) v += o;
+  }
+  return v;
+}
+
+// Inverse CDF: the smallest v with 2^24 * C_v > U_s * S (C_v the inclusive prefix of the
+// sampling weights, S their total). Wave 0 finds the MCHK chunk whose inclusive mass
+// crosses the target (64 chunks per scan window, carry between windows); then each thread
+// sums its run of PER_M consecutive entries of that chunk (values held in registers), a
+// block-wide exclusive scan of the runs gives every thread its starting prefix, and the
+// thread whose run crosses reports the first crossing entry (atomicMin over the block).
 __global__ __launch_bounds__(THREADS) void rej_pick_kernel(RejArgs a) {
   const int b = blockIdx.x;
   const SampleRow s = sample_row(a, b);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   __shared__ int s_chunk;
   __shared__ u128 s_before;
   __shared__ u128 s_target;
-  __shared__ u128 s_run[THREADS];
+  __shared__ u128 s_wtot[THREADS / 64];
   __shared__ int s_tok;
-  if (threadIdx.x == 0) {
-    u128 total = 0;
-    for (int c = 0; c < a.nch; ++c) total += a.cmass[(size_t)b * a.nch + c];
-    const u128 target = (u128)uniform_fix(a.u_sample[b]) * total;  // need 2^24 * C > target
+  const u128* cm = a.cmass + (size_t)b * a.nchm;
+  if (w == 0) {
+    u128 tot = 0;
+    for (int c = lane; c < a.nchm; c += 64) tot += cm[c];
+    tot = wave_incl_scan_u128(tot);
+    tot = shfl_u128(tot, 63);
+    const u128 target = (u128)uniform_fix(a.u_sample[b]) * tot;  // need 2^24 * C > target
+    u128 carry = 0;
+    int chunk = a.nchm - 1;
     u128 before = 0;
-    int chunk = a.nch - 1;
-    for (int c = 0; c < a.nch; ++c) {
-      const u128 m = a.cmass[(size_t)b * a.nch + c];
-      if (((before + m) << 24) > target) { chunk = c; break; }
-      before += m;
+    bool found = false;
+    for (int c0 = 0; c0 < a.nchm && !found; c0 += 64) {
+      const int c = c0 + lane;
+      const u128 m = c < a.nchm ? cm[c] : 0;
+      const u128 incl = wave_incl_scan_u128(m) + carry;
+      const uint64_t hit = __builtin_amdgcn_ballot_w64(c < a.nchm && (incl << 24) > target);
+      if (hit != 0) {
+        const int l = __builtin_ctzll(hit);
+        chunk = c0 + l;
+        before = shfl_u128(incl - m, l);
+        found = true;
+      }
+      carry = shfl_u128(incl, 63);
     }
-    s_chunk = chunk;
-    s_before = before;
-    s_target = target;
-    s_tok = 0x7FFFFFFF;
+    if (lane == 0) {
+      s_chunk = chunk;
+      s_before = found ? before : carry;
+      s_target = target;
+      s_tok = 0x7FFFFFFF;
+    }
   }
   __syncthreads();
-  const int v0 = s_chunk * CHK + threadIdx.x * PER_T;
+  const int v0 = s_chunk * MCHK + (int)threadIdx.x * PER_M;
+  RunVals rv;
   u128 run = 0;
-  for (int j = 0; j < PER_T; ++j) {
-    const int v = v0 + j;
-    if (v < a.V) run += weight(s, v, a.inv_temp);
+  if (v0 < a.V) {
+    rv = load_run(a, s, v0);
+#pragma unroll
+    for (int j = 0; j < PER_M; ++j)
+      if (v0 + j < a.V) run += weight_of(s, rv.p[j], rv.q[j], a.inv_temp);
   }
-  s_run[threadIdx.x] = run;
+  const u128 incl = wave_incl_scan_u128(run);
+  if (lane == 63) s_wtot[w] = incl;
   __syncthreads();
-  if (threadIdx.x == 0) {  // sequential exclusive scan of the 256 run sums (exact integers)
-    u128 acc = s_before;
-    for (int t = 0; t < THREADS; ++t) {
-      const u128 r = s_run[t];
-      s_run[t] = acc;
-      acc += r;
-    }
-  }
-  __syncthreads();
-  u128 c = s_run[threadIdx.x];
-  for (int j = 0; j < PER_T; ++j) {
-    const int v = v0 + j;
-    if (v >= a.V) break;
-    const u128 wv = weight(s, v, a.inv_temp);
-    c += wv;
-    if (wv != 0 && (c << 24) > s_target) {
-      atomicMin(&s_tok, v);  // first crossing in this run; lowest v over the block
-      break;
+  u128 c = s_before + incl - run;
+  for (int k = 0; k < w; ++k) c += s_wtot[k];
+  const u128 target = s_target;
+  if (v0 < a.V && ((c + run) << 24) > target) {  // the crossing lies in this run or before
+#pragma unroll
+    for (int j = 0; j < PER_M; ++j) {
+      const int v = v0 + j;
+      if (v >= a.V) break;
+      const u128 wv = weight_of(s, rv.p[j], rv.q[j], a.inv_temp);
+      c += wv;
+      if (wv != 0 && (c << 24) > target) {
+        atomicMin(&s_tok, v);
+        break;
+      }
     }
   }
   __syncthreads();
@@ -422,7 +547,7 @@ __global__ __launch_bounds__(THREADS) void rej_pick_kernel(RejArgs a) {
 }
 
 struct WsLayout {
-  size_t rmax, zsum, ex, dec_row, dec_z, cmass, total;
+  size_t rmax, zsum, ex, dec_row, dec_z, dec_m, cmass, total;
 };
 
 WsLayout layout(int B, int K, int V) {
@@ -438,7 +563,8 @@ WsLayout layout(int B, int K, int V) {
   l.ex = o; o += up(rows * sizeof(uint64_t));
   l.dec_row = o; o += up((size_t)B * sizeof(int32_t));
   l.dec_z = o; o += up((size_t)B * 2 * sizeof(uint64_t));
-  l.cmass = o; o += up((size_t)B * nch * sizeof(u128));
+  l.dec_m = o; o += up((size_t)B * 2 * sizeof(float));
+  l.cmass = o; o += up((size_t)B * ((V + MCHK - 1) / MCHK) * sizeof(u128));
   l.total = o;
   return l;
 }
@@ -465,8 +591,9 @@ extern "C" int npn_accept_greedy(const float* target_logits, const int64_t* draf
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int nch = (V + CHK - 1) / CHK;
   ArgPart* part = reinterpret_cast<ArgPart*>(static_cast<uint8_t*>(workspace) + l.rmax);
+  const bool vec4 = V % 4 == 0 && NPN_ALIGNED16(target_logits);
   hipLaunchKernelGGL(argmax_chunk_kernel, dim3(nch, B * (K + 1)), dim3(THREADS), 0, s,
-                     target_logits, part, V, nch);
+                     target_logits, part, V, nch, vec4);
   hipLaunchKernelGGL(greedy_accept_kernel, dim3((B + 63) / 64), dim3(64), 0, s, part, draft_ids,
                      accepted, out_ids, B, K, nch);
   return npn_launch_status();
@@ -488,16 +615,18 @@ extern "C" int npn_accept_rejection(const float* target_logits, const float* dra
   hipStream_t s = static_cast<hipStream_t>(stream);
   uint8_t* ws = static_cast<uint8_t*>(workspace);
   const int nch = (V + CHK - 1) / CHK;
+  const bool vec4 = V % 4 == 0 && NPN_ALIGNED16(target_logits) && NPN_ALIGNED16(draft_logits);
   RejArgs a{target_logits, draft_logits, draft_ids, u_accept, u_sample, inv_temperature,
-            accepted, out_ids, B, K, V, nch,
+            accepted, out_ids, B, K, V, nch, (V + MCHK - 1) / MCHK, vec4,
             reinterpret_cast<float*>(ws + l.rmax), reinterpret_cast<uint64_t*>(ws + l.zsum),
             reinterpret_cast<uint64_t*>(ws + l.ex), reinterpret_cast<int32_t*>(ws + l.dec_row),
-            reinterpret_cast<uint64_t*>(ws + l.dec_z), reinterpret_cast<u128*>(ws + l.cmass)};
+            reinterpret_cast<uint64_t*>(ws + l.dec_z), reinterpret_cast<float*>(ws + l.dec_m),
+            reinterpret_cast<u128*>(ws + l.cmass)};
   const int rows = B * (2 * K + 1);
   hipLaunchKernelGGL(rej_max_kernel, dim3(nch, rows), dim3(THREADS), 0, s, a);
   hipLaunchKernelGGL(rej_sum_kernel, dim3(nch, rows), dim3(THREADS), 0, s, a);
-  hipLaunchKernelGGL(rej_decide_kernel, dim3((B + 63) / 64), dim3(64), 0, s, a);
-  hipLaunchKernelGGL(rej_mass_kernel, dim3(nch, B), dim3(THREADS), 0, s, a);
+  hipLaunchKernelGGL(rej_decide_kernel, dim3(B), dim3(THREADS), 0, s, a);
+  hipLaunchKernelGGL(rej_mass_kernel, dim3(a.nchm, B), dim3(THREADS), 0, s, a);
   hipLaunchKernelGGL(rej_pick_kernel, dim3(B), dim3(THREADS), 0, s, a);
   return npn_launch_status();
 }

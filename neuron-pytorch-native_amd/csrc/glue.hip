@@ -31,10 +31,11 @@ __device__ __forceinline__ u32x4 pack8(const float (&f)[8]) {
   return v;
 }
 
-// ---- residual + (1 + w) RMSNorm: one 128-thread workgroup per row; the row (<= 16 chunks of
+// ---- residual + (1 + w) RMSNorm: one 256-thread workgroup per row; the row (<= 8 chunks of
 // 8 per thread, H <= 16384) stays in registers between the sum of squares and the scaling.
-constexpr int kNormThreads = 128;
-constexpr int kNormMaxChunks = 16;
+// Every load of the row is issued before the first store (hidden_out may alias hidden_in).
+constexpr int kNormThreads = 256;
+constexpr int kNormMaxChunks = 8;
 
 __global__ __launch_bounds__(kNormThreads) void residual_rmsnorm_kernel(
     const uint16_t* h_in, const uint16_t* __restrict__ delta, const float* __restrict__ weight,
@@ -43,21 +44,30 @@ __global__ __launch_bounds__(kNormThreads) void residual_rmsnorm_kernel(
   const int tid = threadIdx.x;
   const int nc = H / 8;
   const size_t base = (size_t)row * H;
+  u32x4 hv[kNormMaxChunks], dv[kNormMaxChunks];
+#pragma unroll
+  for (int k = 0; k < kNormMaxChunks; ++k) {
+    const int c = tid + k * kNormThreads;
+    if (c < nc) {
+      hv[k] = *reinterpret_cast<const u32x4*>(h_in + base + 8 * c);
+      if (delta != nullptr) dv[k] = *reinterpret_cast<const u32x4*>(delta + base + 8 * c);
+    }
+  }
   float x[kNormMaxChunks][8];
   float ss = 0.f;
 #pragma unroll
   for (int k = 0; k < kNormMaxChunks; ++k) {
     const int c = tid + k * kNormThreads;
     if (c < nc) {
-      unpack8(*reinterpret_cast<const u32x4*>(h_in + base + 8 * c), x[k]);
+      unpack8(hv[k], x[k]);
       if (delta != nullptr) {
         float d[8];
-        unpack8(*reinterpret_cast<const u32x4*>(delta + base + 8 * c), d);
+        unpack8(dv[k], d);
 #pragma unroll
         for (int j = 0; j < 8; ++j) x[k][j] = npn::bf16_to_f32(npn::f32_to_bf16(x[k][j] + d[j]));
         *reinterpret_cast<u32x4*>(h_out + base + 8 * c) = pack8(x[k]);
       } else if (h_out != h_in) {
-        *reinterpret_cast<u32x4*>(h_out + base + 8 * c) = pack8(x[k]);
+        *reinterpret_cast<u32x4*>(h_out + base + 8 * c) = hv[k];
       }
 #pragma unroll
       for (int j = 0; j < 8; ++j) ss += x[k][j] * x[k][j];

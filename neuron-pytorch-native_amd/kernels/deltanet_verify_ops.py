@@ -12,6 +12,9 @@ the T = K+1 tokens of a speculative verify block:
       -> same; the initial state of sequence b is prev_ckpt[b, state_index[b]]
          (index-based rollback: the previous step's accepted checkpoint is read in
          place, no state copy)
+  deltanet::verify_from_ckpt_into(prev_ckpt, state_index, mixed_qkv, ..., ckpt_out)
+      -> out; as verify_from_ckpt, writing the checkpoints into the caller's ckpt_out
+         (persistent ping-pong buffers for a captured HIP graph of the step)
   deltanet::rollback(ckpt, mixed_qkv, conv_state, accepted)
       -> (state [B*Hv*128, 128] f32 = ckpt[b, accepted[b]],
           conv_state [B*QKV, 3] bf16 = last 3 of [conv_state || x_0..x_a])
@@ -54,8 +57,10 @@ def _check_common(mixed_qkv, conv_state, conv_weight, conv_bias, a_out, b_out, z
 
 
 def _verify(state, state_index, state_T, mixed_qkv, conv_state, conv_weight, conv_bias, a_out,
-            b_out, z, A_log, dt_bias, norm_weight, B, hk, hv, T):
-    ckpt = torch.empty((B * T * hv * K_DIM, V_DIM), dtype=torch.float32, device=mixed_qkv.device)
+            b_out, z, A_log, dt_bias, norm_weight, B, hk, hv, T, ckpt=None):
+    if ckpt is None:
+        ckpt = torch.empty((B * T * hv * K_DIM, V_DIM), dtype=torch.float32,
+                           device=mixed_qkv.device)
     out = torch.empty((B * T * hv, V_DIM), dtype=torch.bfloat16, device=mixed_qkv.device)
     call("npn_deltanet_verify", state, state_index, state_T, mixed_qkv, conv_state, conv_weight,
          conv_bias, a_out, b_out, z, A_log, dt_bias, norm_weight, ckpt, out, B, T, hk, hv,
@@ -128,6 +133,46 @@ def _(prev_ckpt, state_index, mixed_qkv, conv_state, conv_weight, conv_bias, a_o
     bt_hv = a_out.shape[0]
     return (prev_ckpt.new_empty((bt_hv * K_DIM, V_DIM)),
             prev_ckpt.new_empty((bt_hv, V_DIM), dtype=torch.bfloat16))
+
+
+@torch.library.custom_op("deltanet::verify_from_ckpt_into", mutates_args=("ckpt_out",),
+                         device_types="cuda")
+def deltanet_verify_from_ckpt_into(
+    prev_ckpt: torch.Tensor,
+    state_index: torch.Tensor,
+    mixed_qkv: torch.Tensor,
+    conv_state: torch.Tensor,
+    conv_weight: torch.Tensor,
+    conv_bias: torch.Tensor,
+    a_out: torch.Tensor,
+    b_out: torch.Tensor,
+    z: torch.Tensor,
+    A_log: torch.Tensor,
+    dt_bias: torch.Tensor,
+    norm_weight: torch.Tensor,
+    ckpt_out: torch.Tensor,      # [B*T*V_HEADS*K_DIM, V_DIM] f32, must not overlap prev_ckpt
+) -> torch.Tensor:
+    B = state_index.numel()
+    hk, hv, T = _check_common(mixed_qkv, conv_state, conv_weight, conv_bias, a_out, b_out, z,
+                              A_log, dt_bias, norm_weight, B)
+    require(state_index, "state_index", torch.int32, numel=B)
+    if prev_ckpt.shape[0] % (B * hv * K_DIM):
+        raise RuntimeError("prev_ckpt must hold B*Tp*Hv*128 rows")
+    Tp = prev_ckpt.shape[0] // (B * hv * K_DIM)
+    require(prev_ckpt, "prev_ckpt", torch.float32, shape=(B * Tp * hv * K_DIM, V_DIM))
+    require(ckpt_out, "ckpt_out", torch.float32, shape=(B * T * hv * K_DIM, V_DIM))
+    p0, p1 = prev_ckpt.data_ptr(), prev_ckpt.data_ptr() + prev_ckpt.numel() * 4
+    o0, o1 = ckpt_out.data_ptr(), ckpt_out.data_ptr() + ckpt_out.numel() * 4
+    if p0 < o1 and o0 < p1:
+        raise RuntimeError("ckpt_out must not overlap prev_ckpt")
+    return _verify(prev_ckpt, state_index, Tp, mixed_qkv, conv_state, conv_weight, conv_bias,
+                   a_out, b_out, z, A_log, dt_bias, norm_weight, B, hk, hv, T, ckpt=ckpt_out)[1]
+
+
+@deltanet_verify_from_ckpt_into.register_fake
+def _(prev_ckpt, state_index, mixed_qkv, conv_state, conv_weight, conv_bias, a_out, b_out, z,
+      A_log, dt_bias, norm_weight, ckpt_out):
+    return prev_ckpt.new_empty((a_out.shape[0], V_DIM), dtype=torch.bfloat16)
 
 
 @torch.library.custom_op("deltanet::rollback", mutates_args=(), device_types="cuda")

@@ -138,6 +138,9 @@ class VerifySlice:
         self.kv_len = torch.as_tensor(kv_lens, dtype=torch.int32, device=device).clone()
         self.prev_accepted = None
         self.timer = _untimed
+        self.persistent = False
+        self.parity = 0
+        self.graphs = None
 
     # ---- layers: each takes the normed input and returns the residual delta -------------
     def _deltanet(self, L, h):
@@ -148,7 +151,12 @@ class VerifySlice:
         mixed = mixed.reshape(-1)
         args = (mixed, L["conv_state"], L["conv_w"], L["conv_b"], a.reshape(-1), b.reshape(-1),
                 z.reshape(B * T * DN_HV, DN_D), L["A_log"], L["dt_bias"], L["norm_w"])
-        if L["ckpt"] is None:
+        if self.persistent:  # previous checkpoints in ckbuf[parity], new ones into the other
+            p = self.parity
+            ckpt = L["ckbuf"][1 - p]
+            out = self.timer("deltanet.verify", torch.ops.deltanet.verify_from_ckpt_into,
+                             L["ckbuf"][p], self.prev_accepted, *args, ckpt)
+        elif L["ckpt"] is None:
             ckpt, out = self.timer("deltanet.verify", torch.ops.deltanet.verify_batched,
                                    L["state"], *args)
         else:
@@ -221,12 +229,62 @@ class VerifySlice:
         for L in self.layers:
             if L["kind"] == "D":
                 ckpt, mixed = L.pop("pending")
-                L["conv_state"] = self.timer("deltanet.conv_rollback",
-                                             torch.ops.deltanet.conv_rollback, mixed,
-                                             L["conv_state"], accepted, DN_HV)
-                L["ckpt"] = ckpt
-        self.prev_accepted = accepted
-        self.kv_len = self.kv_len + accepted + 1
+                conv = self.timer("deltanet.conv_rollback", torch.ops.deltanet.conv_rollback,
+                                  mixed, L["conv_state"], accepted, DN_HV)
+                if self.persistent:
+                    L["conv_state"].copy_(conv)
+                else:
+                    L["conv_state"] = conv
+                    L["ckpt"] = ckpt
+        if self.persistent:
+            self.prev_accepted.copy_(accepted)
+            self.kv_len.add_(accepted + 1)
+            self.committed.add_(accepted + 1)
+            self.parity ^= 1
+        else:
+            self.prev_accepted = accepted
+            self.kv_len = self.kv_len + accepted + 1
+
+    # ---- fixed-address state and HIP graphs of the step -----------------------------------
+    def make_persistent(self):
+        """After at least one eager step: keep the decode state in fixed buffers updated in
+        place (conv windows, previous accepted lengths, KV lengths, a committed-token
+        counter) with two checkpoint buffers per DeltaNet layer used in turn -- each step
+        reads the previous step's checkpoints from one and writes its own into the other --
+        so that a step can be captured once per buffer parity and replayed."""
+        if self.prev_accepted is None:
+            raise RuntimeError("run one eager step before make_persistent()")
+        for L in self.layers:
+            if L["kind"] == "D":
+                L["ckbuf"] = [L.pop("ckpt"), None]
+                L["ckbuf"][1] = torch.empty_like(L["ckbuf"][0])
+        self.committed = torch.zeros(self.B, dtype=torch.int32, device=self.device)
+        self.parity = 0
+        self.persistent = True
+
+    def capture(self, x, target_logits, draft_logits, draft_ids, u_accept, u_sample,
+                greedy=False):
+        """Capture the step in two HIP graphs, one per checkpoint-buffer parity, on fixed
+        inputs (x and the logits/uniform tensors keep their addresses). Capturing runs
+        nothing: the parity flips twice and ends where the live state is."""
+        if not self.persistent:
+            self.make_persistent()
+        self.graphs, self.graph_outputs = [], []
+        for _ in range(2):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                outs = self.step(x, target_logits, draft_logits, draft_ids, u_accept, u_sample,
+                                 greedy=greedy)
+            self.graphs.append(g)
+            self.graph_outputs.append(outs)
+
+    def replay(self):
+        """One step by graph replay; returns that graph's (hidden, accepted, out_ids) tensors
+        (overwritten by the next replay of the same graph)."""
+        p = self.parity
+        self.graphs[p].replay()
+        self.parity ^= 1
+        return self.graph_outputs[p]
 
     def step(self, x, target_logits, draft_logits, draft_ids, u_accept, u_sample, greedy=False,
              trace=None):

@@ -25,17 +25,26 @@ def f64(t):
     return t.detach().cpu().double().numpy()
 
 
-def assert_rel_close(got, ref, tol=REL_TOL, out_unit=0.0, name="tensor"):
+def assert_rel_close(got, ref, tol=REL_TOL, out_unit=0.0, name="tensor", scale=None):
+    """`scale` (default |ref|) is the per-element magnitude the out_unit term applies to;
+    a sum whose operands are larger than the result passes their magnitude, since a
+    rounding flip in an operand moves the sum by the operand's ulp."""
     got = np.asarray(got, np.float64)
     ref = np.asarray(ref, np.float64)
     assert got.shape == ref.shape, f"{name}: shape {got.shape} vs {ref.shape}"
     assert np.all(np.isfinite(got)), f"{name}: non-finite values"
     nref = np.linalg.norm(ref)
     fro = np.linalg.norm(got - ref) / max(nref, 1e-30)
-    bound = tol * np.abs(ref).max() + out_unit * np.abs(ref)
-    worst = np.max(np.abs(got - ref) - bound)
+    mag = np.abs(ref) if scale is None else np.asarray(scale, np.float64)
+    bound = tol * np.abs(ref).max() + out_unit * mag
+    excess = np.abs(got - ref) - bound
+    worst = np.max(excess)
     assert fro <= tol, f"{name}: Frobenius relative error {fro:.3e} > {tol}"
-    assert worst <= 0, f"{name}: elementwise error exceeds bound by {worst:.3e}"
+    if worst > 0:
+        at = np.unravel_index(np.argmax(excess), excess.shape)
+        raise AssertionError(f"{name}: elementwise error exceeds bound by {worst:.3e} at "
+                             f"{tuple(int(i) for i in at)} (got {got[at]:.6g}, ref {ref[at]:.6g}, "
+                             f"magnitude {mag.reshape(excess.shape)[at] if mag.ndim else mag:.6g})")
     return fro
 
 

@@ -19,7 +19,9 @@ after rollback, conv windows and the appended cache rows within 2e-3 relative
 path, since a flip of any of them shifts what follows by up to an ulp (2^-7 relative at the
 bottom of a binade): conv windows are copies of one rounded projection output (ONE_ULP);
 sublayer outputs (projection, silu, product, down projection, residual sum) and appended key
-rows (projection, norm, RoPE) pass through up to four (CHAIN_ULPS = 4 ulps). A wiring mistake
+rows (projection, norm, RoPE) pass through up to four (CHAIN_ULPS = 4 ulps). For a sublayer
+output (input + delta) the ulps are taken of |input| + |delta|, the operands' magnitude,
+which is larger than the output's where the two cancel. A wiring mistake
 (wrong slice, weight or layout) shows as O(1) errors under either bar.
 Cache rows outside the appended ones keep their values from before the step.
 """
@@ -93,7 +95,12 @@ def test_two_steps_match_oracle(ops):
         assert np.array_equal(ids.cpu().numpy(), oids), tag
         assert np.array_equal(model.kv_len.cpu().numpy(), okv), tag
         for i, (got, ref) in enumerate(zip(trace[1:], outs)):
-            assert_rel_close(got.float().cpu().numpy(), bf16_bits_to_f32(ref), out_unit=CHAIN_ULPS,
+            # output = input + delta: the delta's ulp flips scale with |delta|, which exceeds
+            # |output| where the two cancel, so the ulp term uses |input| + |delta|
+            hin = trace[i].float().cpu().numpy().astype(np.float64)
+            ref = bf16_bits_to_f32(ref)
+            assert_rel_close(got.float().cpu().numpy(), ref, out_unit=CHAIN_ULPS,
+                             scale=np.abs(hin) + np.abs(ref - hin),
                              name=f"{tag} sublayer {i} output")
         for L, d in zip(model.layers, olayers):
             if L["kind"] == "D":

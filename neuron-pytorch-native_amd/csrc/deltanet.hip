@@ -18,7 +18,9 @@
 // v = j and keeps all 128 rows of it in VGPRs for the whole verify block, so the
 // column sums S^T k and S^T q are thread-local. Each checkpoint row is one
 // 256-byte coalesced store per wave. The only cross-thread reductions are the q/k
-// L2 norms (before the loop) and the output RMS norm (after it).
+// L2 norms (before the loop) and the output RMS norm (after it). The per-token q, k, v
+// and o vectors live in LDS, which keeps the kernel at 168 VGPRs: three waves per SIMD,
+// so B*Hv = 1536 workgroups (B = 32, Hv = 48) are resident at once on 256 CUs.
 #include "npn_common.h"
 
 namespace {
@@ -73,7 +75,7 @@ __device__ __forceinline__ void conv_channel(const uint16_t* __restrict__ cs,
 }
 
 template <int TMAX>
-__global__ __launch_bounds__(kThreads, 2) void dn_verify_kernel(DnArgs a) {
+__global__ __launch_bounds__(kThreads, 3) void dn_verify_kernel(DnArgs a) {
   const int b = blockIdx.x / a.Hv;
   const int h = blockIdx.x - b * a.Hv;
   const int tid = threadIdx.x;
@@ -84,9 +86,14 @@ __global__ __launch_bounds__(kThreads, 2) void dn_verify_kernel(DnArgs a) {
   const int QKV = (2 * a.Hk + a.Hv) * D;
   const size_t tile = (size_t)D * D;
 
+  // Per token: raw (un-normalised) conv outputs of q and k, which every thread reads in
+  // full; v and o, which only their own thread uses, are parked here too so that the
+  // 128-row state column is the only large live set (three waves per SIMD).
   __shared__ float s_q[TMAX][D];
   __shared__ float s_k[TMAX][D];
-  __shared__ float s_red[2][2 * TMAX];
+  __shared__ float s_v[TMAX][D];
+  __shared__ float s_o[TMAX][D];
+  __shared__ float s_rq[TMAX], s_rk[TMAX], s_ro[TMAX];
   __shared__ float s_decay[TMAX];
   __shared__ float s_beta[TMAX];
 
@@ -104,12 +111,20 @@ __global__ __launch_bounds__(kThreads, 2) void dn_verify_kernel(DnArgs a) {
   for (int k = 0; k < D; ++k) S[k] = S0[(size_t)k * D + tid];
 
   // Conv + SiLU for this thread's q, k (shared k-head) and v channels.
-  const uint16_t* xb = a.mixed_qkv + (size_t)b * T * QKV;
-  const uint16_t* csb = a.conv_state + (size_t)b * QKV * 3;
-  float qv[TMAX], kv[TMAX], vv[TMAX];
-  conv_channel<TMAX>(csb, xb, a.conv_weight, a.conv_bias, kh * D + tid, QKV, T, qv);
-  conv_channel<TMAX>(csb, xb, a.conv_weight, a.conv_bias, (a.Hk + kh) * D + tid, QKV, T, kv);
-  conv_channel<TMAX>(csb, xb, a.conv_weight, a.conv_bias, (2 * a.Hk + h) * D + tid, QKV, T, vv);
+  {
+    const uint16_t* xb = a.mixed_qkv + (size_t)b * T * QKV;
+    const uint16_t* csb = a.conv_state + (size_t)b * QKV * 3;
+    float y[TMAX];
+    conv_channel<TMAX>(csb, xb, a.conv_weight, a.conv_bias, kh * D + tid, QKV, T, y);
+#pragma unroll
+    for (int t = 0; t < TMAX; ++t) s_q[t][tid] = y[t];
+    conv_channel<TMAX>(csb, xb, a.conv_weight, a.conv_bias, (a.Hk + kh) * D + tid, QKV, T, y);
+#pragma unroll
+    for (int t = 0; t < TMAX; ++t) s_k[t][tid] = y[t];
+    conv_channel<TMAX>(csb, xb, a.conv_weight, a.conv_bias, (2 * a.Hk + h) * D + tid, QKV, T, y);
+#pragma unroll
+    for (int t = 0; t < TMAX; ++t) s_v[t][tid] = y[t];
+  }
 
   // Gates for every token (one thread per token).
   if (tid < T) {
@@ -118,54 +133,52 @@ __global__ __launch_bounds__(kThreads, 2) void dn_verify_kernel(DnArgs a) {
     s_decay[tid] = __expf(g);
     s_beta[tid] = npn::sigmoid(a.b_out[gi]);
   }
+  __syncthreads();
 
-  // L2 norms of q_t and k_t over the 128 channels of the k-head.
+  // L2 norms of q_t and k_t over the 128 channels of the k-head: wave w reduces the tokens
+  // t = w, w + 2, ...; the scales multiply the dot products and the update below.
+  const float qscale = 0.08838834764831845f;  // 1/sqrt(128)
 #pragma unroll
-  for (int t = 0; t < TMAX; ++t) {
-    const float sq = npn::wave_sum(qv[t] * qv[t]);
-    const float sk = npn::wave_sum(kv[t] * kv[t]);
+  for (int t = wid; t < TMAX; t += 2) {
+    const float q0 = s_q[t][lane], q1 = s_q[t][lane + 64];
+    const float k0 = s_k[t][lane], k1 = s_k[t][lane + 64];
+    const float sq = npn::wave_sum(q0 * q0 + q1 * q1);
+    const float sk = npn::wave_sum(k0 * k0 + k1 * k1);
     if (lane == 0) {
-      s_red[wid][2 * t] = sq;
-      s_red[wid][2 * t + 1] = sk;
+      s_rq[t] = rsqrtf(sq + kEps) * qscale;
+      s_rk[t] = rsqrtf(sk + kEps);
     }
   }
   __syncthreads();
-  const float qscale = 0.08838834764831845f;  // 1/sqrt(128)
-#pragma unroll
-  for (int t = 0; t < TMAX; ++t) {
-    const float sq = s_red[0][2 * t] + s_red[1][2 * t];
-    const float sk = s_red[0][2 * t + 1] + s_red[1][2 * t + 1];
-    s_q[t][tid] = qv[t] * rsqrtf(sq + kEps) * qscale;
-    s_k[t][tid] = kv[t] * rsqrtf(sk + kEps);
-  }
-  __syncthreads();
 
-  // Recurrence over the T tokens; checkpoint after each.
-  float o[TMAX];
+  // Recurrence over the T tokens; checkpoint after each. With k = rk * k_raw and
+  // q = rq * q_raw: S^T k = rk * (S^T k_raw), S += k_raw (rk * delta), o = rq * (S^T q_raw).
   float* ck = a.ckpt + ((size_t)b * T * a.Hv + h) * tile + tid;
 #pragma unroll
   for (int t = 0; t < TMAX; ++t) {
-    o[t] = 0.0f;
     if (t < T) {
       const float decay = s_decay[t];
-      const float beta = s_beta[t];
+      const float rk = s_rk[t];
       float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int k = 0; k < D; ++k) {
         S[k] *= decay;
         acc[k & 3] = fmaf(S[k], s_k[t][k], acc[k & 3]);
       }
-      const float delta = (vv[t] - ((acc[0] + acc[1]) + (acc[2] + acc[3]))) * beta;
-      // Re-read k_t from LDS below instead of keeping 128 copies live in VGPRs.
+      const float kS = ((acc[0] + acc[1]) + (acc[2] + acc[3])) * rk;
+      const float kd = (s_v[t][tid] - kS) * s_beta[t] * rk;
       asm volatile("" ::: "memory");
       float oc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int k = 0; k < D; ++k) {
-        S[k] = fmaf(s_k[t][k], delta, S[k]);
+        S[k] = fmaf(s_k[t][k], kd, S[k]);
         oc[k & 3] = fmaf(S[k], s_q[t][k], oc[k & 3]);
       }
-      o[t] = (oc[0] + oc[1]) + (oc[2] + oc[3]);
+      s_o[t][tid] = ((oc[0] + oc[1]) + (oc[2] + oc[3])) * s_rq[t];
       asm volatile("" ::: "memory");
+      // Nontemporal stores. Plain (write-allocating) stores make this kernel ~11% shorter,
+      // but part of the 805 MB then drains from the memory-side cache during the GEMMs
+      // that follow, and the whole step is ~1% slower (measured on MI355X).
       float* dst = ck + (size_t)t * a.Hv * tile;
 #pragma unroll
       for (int k = 0; k < D; ++k) __builtin_nontemporal_store(S[k], dst + (size_t)k * D);
@@ -175,19 +188,19 @@ __global__ __launch_bounds__(kThreads, 2) void dn_verify_kernel(DnArgs a) {
   // Gated RMSNorm of o_t over the 128 v columns.
   __syncthreads();
 #pragma unroll
-  for (int t = 0; t < TMAX; ++t) {
-    const float so = npn::wave_sum(o[t] * o[t]);
-    if (lane == 0) s_red[wid][t] = so;
+  for (int t = wid; t < TMAX; t += 2) {
+    const float o0 = s_o[t][lane], o1 = s_o[t][lane + 64];
+    const float so = npn::wave_sum(o0 * o0 + o1 * o1);
+    if (lane == 0) s_ro[t] = rsqrtf(so * (1.0f / D) + kEps);
   }
   __syncthreads();
   const float nw = a.norm_weight[tid];
 #pragma unroll
   for (int t = 0; t < TMAX; ++t) {
     if (t < T) {
-      const float var = (s_red[0][t] + s_red[1][t]) * (1.0f / D);
       const size_t oi = (((size_t)b * T + t) * a.Hv + h) * D + tid;
       const float zz = npn::bf16_to_f32(a.z[oi]);
-      a.out[oi] = npn::f32_to_bf16(o[t] * rsqrtf(var + kEps) * nw * npn::silu(zz));
+      a.out[oi] = npn::f32_to_bf16(s_o[t][tid] * s_ro[t] * nw * npn::silu(zz));
     }
   }
 }

@@ -392,28 +392,40 @@ struct GemmPlan {
 };
 
 // Wide-kernel instantiations: column tiles per wave (a workgroup holds twice as many units).
-constexpr int kWideNH[] = {1, 2, 3, 5};
+constexpr int kWideNH[] = {1, 2, 3, 4, 5, 6};
 
-// Wide-kernel split-K choice: modelled time = max(MFMA time at the balance efficiency of the
-// column split, HBM time of weights + split-K partials). MFMA at 60% of 2.5 PFLOP/s, HBM at
-// 5.5 TB/s: only the ratio of the two matters for the choice.
+// Wide-kernel plan: split-K factor s, column groups g (one workgroup per (group, split)),
+// column tiles per wave ntm. Modelled time, additive because the three do not overlap well
+// in this kernel (fitted to measurements at M = 256 on MI355X):
+//   x:        every workgroup streams its 256 x (K / s) activation block from L2 into LDS,
+//             at about 51 GB/s per CU when all CUs do so at once;
+//   MFMA:     a workgroup computes 2 * ntm 16-column tiles whether or not all are real
+//             columns, at about 2.07 PFLOP/s / 256 per CU (two waves per SIMD);
+//   split-K:  partials written by the GEMM and read by the reduction, about 4.5 TB/s while
+//             one split-K buffer stays under 48 MB, plus the reduction's launch.
+// For each s the smallest ntm whose group count ceil(units / (2 ntm)) fits in 256 / s
+// workgroups is taken: fewest padded tiles, and every workgroup's tiles nearly all real.
 bool plan_wide(int M, int K, int N, GemmPlan& p) {
   if (M <= 64 || K % KC != 0 || N % 16 != 0) return false;
   const int units = N / 16;
-  const double flops = 2.0 * M * (double)N * K;
+  const int passes = (M + 255) / 256;
   double best = 1e30;
-  for (int s = 1; s <= 4; s *= 2) {
+  for (int s = 1; s <= 8; s *= 2) {
     if (K / KC < 2 * s) break;
-    const int groups = units < WIDE_WG / s ? units : WIDE_WG / s;
-    const int need = (units + groups - 1) / groups;
-    int ntm = 0;
-    for (int v : kWideNH)
-      if (2 * v >= need) { ntm = v; break; }
+    const double part_bytes = (double)s * M * N * 4;
+    if (s > 1 && part_bytes > 48e6) break;
+    const int gmax = WIDE_WG / s;
+    int ntm = 0, groups = 0;
+    for (int v : kWideNH) {
+      const int g = (units + 2 * v - 1) / (2 * v);
+      if (g <= gmax) { ntm = v; groups = g; break; }
+    }
     if (ntm == 0) continue;
-    const double eff = (double)units / groups / need;
-    const double bytes = (double)K * N + (s > 1 ? 2.0 * s * M * (double)N * 4 : 0.0);
-    const double t = flops / (eff * 0.6 * 2.5e15) > bytes / 5.5e12 ? flops / (eff * 0.6 * 2.5e15)
-                                                                      : bytes / 5.5e12;
+    const double kk = (double)K / s;
+    const double t_x = kk * 512.0 / 51e9;
+    const double t_mfma = 2.0 * ntm * 16 * 256 * 2 * kk / (2.07e15 / WIDE_WG);
+    const double t_part = s > 1 ? 2.0 * part_bytes / 4.5e12 + 3e-6 : 0.0;
+    const double t = (t_x + t_mfma) * passes + t_part;
     if (t < best * 0.97) {
       best = t;
       p.wide = true;
@@ -424,7 +436,7 @@ bool plan_wide(int M, int K, int N, GemmPlan& p) {
     }
   }
   if (!p.wide) return false;
-  p.passes = (M + 255) / 256;
+  p.passes = passes;
   p.ws = p.split_k > 1 ? (size_t)p.split_k * M * N * sizeof(float) : 0;
   return true;
 }
@@ -479,7 +491,9 @@ extern "C" int npn_fp8_matmul(const uint16_t* x, const int8_t* w, const float* s
       case 1: hipLaunchKernelGGL(fp8_gemm_wide_kernel<1>, grid, block, 0, s, wa); break;
       case 2: hipLaunchKernelGGL(fp8_gemm_wide_kernel<2>, grid, block, 0, s, wa); break;
       case 3: hipLaunchKernelGGL(fp8_gemm_wide_kernel<3>, grid, block, 0, s, wa); break;
-      default: hipLaunchKernelGGL(fp8_gemm_wide_kernel<5>, grid, block, 0, s, wa); break;
+      case 4: hipLaunchKernelGGL(fp8_gemm_wide_kernel<4>, grid, block, 0, s, wa); break;
+      case 5: hipLaunchKernelGGL(fp8_gemm_wide_kernel<5>, grid, block, 0, s, wa); break;
+      default: hipLaunchKernelGGL(fp8_gemm_wide_kernel<6>, grid, block, 0, s, wa); break;
     }
     if (p.split_k > 1) {
       const size_t total = (size_t)M * N;

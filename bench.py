@@ -17,6 +17,7 @@ A step = layers + acceptance + rollback on inputs resident in HBM. Reported:
   python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu-baseline]
 """
 import argparse
+import gc
 import json
 import os
 import sys
@@ -173,13 +174,18 @@ def main():
     torch.manual_seed(args.seed)
     kv_lens = kv_lengths(args.seed)
     # cache rows: the warmup, the graph-timed steps and the per-op eager pass each append T
-    s_max = int(kv_lens.max()) + T * (2 * (args.warmup + args.steps) + 4)
+    s_max = int(kv_lens.max()) + T * (2 * (args.warmup + args.steps) + 6)
     model = VerifySlice(B, K, kv_lens, s_max, pattern="DDDG", seed=args.seed, device=dev)
     g = torch.Generator(device=dev).manual_seed(args.seed + 1)
     x = torch.randn(B * T, HIDDEN, generator=g, device=dev).to(torch.bfloat16)
     logits = synthetic_logits(B, K, V, args.seed + 2, dev)
     kv_start = model.kv_len.clone()
 
+    # Python's garbage collector stays off from here to the end of the per-op pass: a full
+    # collection (tens of ms) inside an op's event bracket drains the GPU queue and shows up
+    # as that op's time.
+    gc.collect()
+    gc.disable()
     # Warmup: eager steps (the first starts from the initial DeltaNet state); then the state
     # moves to fixed buffers and the step is captured as HIP graphs (two checkpoint-buffer
     # parities), replayed in the timed region.
@@ -205,7 +211,12 @@ def main():
     ms_per_step = elapsed * 1e3 / args.steps
 
     # Per-op launch times: HIP events around every op launch on the launch stream, over an
-    # eager pass of the same number of steps (same kernels and sizes as the replays).
+    # eager pass of the same number of steps (same kernels and sizes as the replays), after
+    # two untimed eager steps: the first eager allocations after the graph captures may call
+    # hipMalloc, which waits for the queued work inside an op's event bracket.
+    for _ in range(2):
+        model.step(x, *logits)
+    torch.cuda.synchronize()
     kv0 = float(model.kv_len.float().mean().item())
     timer = OpTimer()
     model.timer = timer
@@ -214,6 +225,7 @@ def main():
         model.step(x, *logits)
     torch.cuda.synchronize()
     model.timer = lambda name, fn, *a: fn(*a)
+    gc.enable()
     ops = timer.summary()
     # mean prior cache rows seen by the attention over the timed eager steps
     kv_mean_rows = kv0 + float(model.committed.float().mean().item()) * (args.steps - 1) / (2 * args.steps)

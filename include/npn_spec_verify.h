@@ -157,6 +157,18 @@ size_t npn_fp8_matmul_workspace_size(int M, int K, int N);
 int npn_fp8_matmul(const uint16_t* x, const int8_t* w, const float* scale, uint16_t* out, int M,
                    int K, int N, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Split-K factor S of the GEMM plan for these sizes (1: no split; 0: unsupported sizes). */
+int npn_fp8_matmul_split_k(int M, int K, int N);
+
+/* torch.ops.fp8.matmul_partials -- new op, no reference counterpart: the GEMM of
+ * npn_fp8_matmul without its reduction and scaling, for consumers that fuse them.
+ *   partial [S][M][N] f32, S = npn_fp8_matmul_split_k(M, K, N): the unscaled products of x
+ *   and w over S consecutive K ranges. npn_fp8_matmul's output is
+ *   bf16(scale * (partial[0] + ... + partial[S-1])), summed from 0 in that order.
+ * Shape rules as npn_fp8_matmul; no workspace. */
+int npn_fp8_matmul_partials(const uint16_t* x, const int8_t* w, float* partial, int M, int K,
+                            int N, void* stream);
+
 /* ---------------------------------------------------------------------------
  * Acceptance. T = K+1 verify positions per sequence, vocabulary V.
  * Outputs: accepted [B] int32 in [0, K]; out_ids [B, T] int64: accepted drafts,
@@ -230,6 +242,23 @@ int npn_deltanet_split(const uint16_t* proj, int ld, uint16_t* mixed_qkv, uint16
  *   [M, kv_heads, head_dim] bf16. head_dim, ld multiples of 8. */
 int npn_gqa_split(const uint16_t* proj, int ld, uint16_t* query, uint16_t* gate, uint16_t* key,
                   uint16_t* value, int M, int q_heads, int kv_heads, int head_dim, void* stream);
+
+/* The same three glue ops reading their input from npn_fp8_matmul_partials output instead
+ * of a bf16 projection (new ops: normfuse::residual_rms_norm_partials,
+ * glue::deltanet_split_partials, glue::gqa_split_partials). Input row m is
+ *   bf16(scale[n] * (partial[0][m][n] + ... + partial[split_k-1][m][n])),
+ * bit-identical to npn_fp8_matmul's output, so each result equals npn_fp8_matmul followed by
+ * the bf16 op. partial [split_k][M][ld] f32 (ld = H for the norm), scale [ld] f32,
+ * 1 <= split_k <= 64; other arguments as in the bf16 forms. */
+int npn_residual_rmsnorm_partials(const uint16_t* hidden_in, const float* partial, int split_k,
+                                  const float* scale, const float* weight, uint16_t* hidden_out,
+                                  uint16_t* normed, int M, int H, float eps, void* stream);
+int npn_deltanet_split_partials(const float* partial, int split_k, const float* scale, int ld,
+                                uint16_t* mixed_qkv, uint16_t* z, float* a_out, float* b_out,
+                                int M, int qkv_n, int z_n, int hv, void* stream);
+int npn_gqa_split_partials(const float* partial, int split_k, const float* scale, int ld,
+                           uint16_t* query, uint16_t* gate, uint16_t* key, uint16_t* value,
+                           int M, int q_heads, int kv_heads, int head_dim, void* stream);
 
 #ifdef __cplusplus
 }

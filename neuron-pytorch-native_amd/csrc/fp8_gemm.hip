@@ -69,9 +69,9 @@ struct GemmArgs {
   const uint16_t* x;
   const uint8_t* w;
   const float* scale;
-  uint16_t* out;     // used when split_k == 1
-  float* partial;    // [split_k][M][N] when split_k > 1
-  int M, K, N, split_k;
+  uint16_t* out;     // used when split_k == 1 and !to_partial
+  float* partial;    // [split_k][M][N] fp32, unscaled, when split_k > 1 or to_partial
+  int M, K, N, split_k, to_partial;
 };
 
 template <int MT>
@@ -147,7 +147,7 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemm_kernel(GemmArgs a) {
   if (w != 0) return;
 
   // Wave 0 holds the tile sum: lane (i, G) has rows 16mt + 4G + r, columns n0 + 4i + ct.
-  if (a.split_k == 1) {
+  if (a.split_k == 1 && !a.to_partial) {
     float sc[4];
 #pragma unroll
     for (int ct = 0; ct < 4; ++ct) sc[ct] = a.scale[n0 + 4 * i + ct];
@@ -211,8 +211,8 @@ struct WideArgs {
   const uint8_t* w;
   const float* scale;
   uint16_t* out;
-  float* partial;  // [split_k][M][N] when split_k > 1
-  int M, K, N, units, groups, split_k;
+  float* partial;  // [split_k][M][N] fp32, unscaled, when split_k > 1 or to_partial
+  int M, K, N, units, groups, split_k, to_partial;
 };
 
 typedef int i32x2 __attribute__((ext_vector_type(2)));
@@ -359,14 +359,16 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void fp8_gemm_wide_kernel(WideArgs
     const int unit = NH * wc + nt;
     if (unit >= nu) continue;
     const int col = n0 + 16 * unit + i;
-    const float sc = a.scale[col];
+    const bool to_bf16 = a.split_k == 1 && !a.to_partial;
+    // partial outputs are unscaled, and the scale pointer may then be NULL
+    const float sc = to_bf16 ? a.scale[col] : 0.0f;
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int m = m_base + 64 * wr + 16 * mt + 4 * G + r;
         if (m >= a.M) continue;
-        if (a.split_k == 1) a.out[(size_t)m * a.N + col] = npn::f32_to_bf16(acc[mt][nt][r] * sc);
+        if (to_bf16) a.out[(size_t)m * a.N + col] = npn::f32_to_bf16(acc[mt][nt][r] * sc);
         else a.partial[((size_t)sk * a.M + m) * a.N + col] = acc[mt][nt][r];
       }
   }
@@ -462,6 +464,44 @@ bool shape_ok(int M, int K, int N) {
          (long)K * N < (1L << 40);
 }
 
+// Launches the plan's GEMM kernel; with split-K (or to_partial) it writes fp32 partials
+// [split_k][M][N] to `partial` and, when `reduce`, the fixed-order reduction into `out`.
+int launch_gemm(const GemmPlan& p, const uint16_t* x, const int8_t* w, const float* scale,
+                uint16_t* out, float* partial, int M, int K, int N, int to_partial, bool reduce,
+                hipStream_t s) {
+  if (p.wide) {
+    WideArgs wa{x, reinterpret_cast<const uint8_t*>(w), scale, out, partial, M, K, N,
+                p.units, p.groups, p.split_k, to_partial};
+    const int nwg = ((p.groups * p.split_k + 7) / 8) * 8;  // multiple of 8 for the XCD map
+    const dim3 grid(nwg, p.passes);
+    const dim3 block(WIDE_THREADS);
+    switch (p.ntm) {
+      case 1: hipLaunchKernelGGL(fp8_gemm_wide_kernel<1>, grid, block, 0, s, wa); break;
+      case 2: hipLaunchKernelGGL(fp8_gemm_wide_kernel<2>, grid, block, 0, s, wa); break;
+      case 3: hipLaunchKernelGGL(fp8_gemm_wide_kernel<3>, grid, block, 0, s, wa); break;
+      case 4: hipLaunchKernelGGL(fp8_gemm_wide_kernel<4>, grid, block, 0, s, wa); break;
+      case 5: hipLaunchKernelGGL(fp8_gemm_wide_kernel<5>, grid, block, 0, s, wa); break;
+      default: hipLaunchKernelGGL(fp8_gemm_wide_kernel<6>, grid, block, 0, s, wa); break;
+    }
+  } else {
+    GemmArgs ga{x, reinterpret_cast<const uint8_t*>(w), scale, out, partial, M, K, N, p.split_k,
+                to_partial};
+    const dim3 grid(N / NW, p.split_k, p.passes);
+    switch (p.mt) {
+      case 1: hipLaunchKernelGGL(fp8_gemm_kernel<1>, grid, dim3(WAVES * 64), 0, s, ga); break;
+      case 2: hipLaunchKernelGGL(fp8_gemm_kernel<2>, grid, dim3(WAVES * 64), 0, s, ga); break;
+      case 4: hipLaunchKernelGGL(fp8_gemm_kernel<4>, grid, dim3(WAVES * 64), 0, s, ga); break;
+      default: hipLaunchKernelGGL(fp8_gemm_kernel<8>, grid, dim3(WAVES * 64), 0, s, ga); break;
+    }
+  }
+  if (reduce && p.split_k > 1) {
+    const size_t total = (size_t)M * N;
+    hipLaunchKernelGGL(fp8_splitk_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256),
+                       0, s, partial, scale, out, M, N, p.split_k);
+  }
+  return npn_launch_status();
+}
+
 }  // namespace
 
 extern "C" size_t npn_fp8_matmul_workspace_size(int M, int K, int N) {
@@ -480,42 +520,22 @@ extern "C" int npn_fp8_matmul(const uint16_t* x, const int8_t* w, const float* s
     NPN_REQUIRE(workspace != nullptr && workspace_bytes >= p.ws, NPN_ERR_WORKSPACE);
     NPN_REQUIRE(NPN_ALIGNED16(workspace), NPN_ERR_ALIGN);
   }
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  if (p.wide) {
-    WideArgs wa{x, reinterpret_cast<const uint8_t*>(w), scale, out,
-                static_cast<float*>(workspace), M, K, N, p.units, p.groups, p.split_k};
-    const int nwg = ((p.groups * p.split_k + 7) / 8) * 8;  // multiple of 8 for the XCD map
-    const dim3 grid(nwg, p.passes);
-    const dim3 block(WIDE_THREADS);
-    switch (p.ntm) {
-      case 1: hipLaunchKernelGGL(fp8_gemm_wide_kernel<1>, grid, block, 0, s, wa); break;
-      case 2: hipLaunchKernelGGL(fp8_gemm_wide_kernel<2>, grid, block, 0, s, wa); break;
-      case 3: hipLaunchKernelGGL(fp8_gemm_wide_kernel<3>, grid, block, 0, s, wa); break;
-      case 4: hipLaunchKernelGGL(fp8_gemm_wide_kernel<4>, grid, block, 0, s, wa); break;
-      case 5: hipLaunchKernelGGL(fp8_gemm_wide_kernel<5>, grid, block, 0, s, wa); break;
-      default: hipLaunchKernelGGL(fp8_gemm_wide_kernel<6>, grid, block, 0, s, wa); break;
-    }
-    if (p.split_k > 1) {
-      const size_t total = (size_t)M * N;
-      hipLaunchKernelGGL(fp8_splitk_reduce_kernel, dim3((unsigned)((total + 255) / 256)),
-                         dim3(256), 0, s, static_cast<const float*>(workspace), scale, out, M, N,
-                         p.split_k);
-    }
-    return npn_launch_status();
-  }
-  GemmArgs ga{x, reinterpret_cast<const uint8_t*>(w), scale, out,
-              static_cast<float*>(workspace), M, K, N, p.split_k};
-  const dim3 grid(N / NW, p.split_k, p.passes);
-  switch (p.mt) {
-    case 1: hipLaunchKernelGGL(fp8_gemm_kernel<1>, grid, dim3(WAVES * 64), 0, s, ga); break;
-    case 2: hipLaunchKernelGGL(fp8_gemm_kernel<2>, grid, dim3(WAVES * 64), 0, s, ga); break;
-    case 4: hipLaunchKernelGGL(fp8_gemm_kernel<4>, grid, dim3(WAVES * 64), 0, s, ga); break;
-    default: hipLaunchKernelGGL(fp8_gemm_kernel<8>, grid, dim3(WAVES * 64), 0, s, ga); break;
-  }
-  if (p.split_k > 1) {
-    const size_t total = (size_t)M * N;
-    hipLaunchKernelGGL(fp8_splitk_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256),
-                       0, s, static_cast<const float*>(workspace), scale, out, M, N, p.split_k);
-  }
-  return npn_launch_status();
+  return launch_gemm(p, x, w, scale, out, static_cast<float*>(workspace), M, K, N, 0, true,
+                     static_cast<hipStream_t>(stream));
+}
+
+extern "C" int npn_fp8_matmul_split_k(int M, int K, int N) {
+  if (!shape_ok(M, K, N)) return 0;
+  return plan(M, K, N).split_k;
+}
+
+extern "C" int npn_fp8_matmul_partials(const uint16_t* x, const int8_t* w, float* partial, int M,
+                                       int K, int N, void* stream) {
+  NPN_REQUIRE(x && w && partial, NPN_ERR_NULL);
+  NPN_REQUIRE(shape_ok(M, K, N), NPN_ERR_SHAPE);
+  NPN_REQUIRE(NPN_ALIGNED16(x) && NPN_ALIGNED16(w) && NPN_ALIGNED16(partial), NPN_ERR_ALIGN);
+  const GemmPlan p = plan(M, K, N);
+  // Neither kernel reads the scale or writes `out` when it writes partials.
+  return launch_gemm(p, x, w, nullptr, nullptr, partial, M, K, N, 1, false,
+                     static_cast<hipStream_t>(stream));
 }

@@ -9,6 +9,11 @@
 //   GQA split         q/k/v-proj row [(query | gate) per q head | key per kv head | value per
 //                     kv head] -> query, gate, key, value (_gqa_layer, static_decode.py:867-890)
 // All four move 16-byte chunks (8 bf16) per lane; widths must be multiples of 8.
+// The residual norm and the two splits also read their input straight from the fp32 split-K
+// partials of the projection GEMM that produces it (npn_fp8_matmul_partials): each 8-value
+// chunk is bf16(scale * (p_0 + p_1 + ... + p_{S-1})), summed from 0 in that order, which is
+// exactly what the GEMM's own reduction writes, so the results are bit-identical and the
+// reduction's launch and its bf16 round trip through HBM go away.
 #include "npn_common.h"
 
 namespace {
@@ -31,14 +36,45 @@ __device__ __forceinline__ u32x4 pack8(const float (&f)[8]) {
   return v;
 }
 
+// Input sources: 8 bf16 values of row m starting at column col (a multiple of 8).
+struct BfSrc {  // a bf16 matrix with row stride ld
+  const uint16_t* p;
+  int ld;
+  __device__ __forceinline__ u32x4 load(size_t m, int col) const {
+    return *reinterpret_cast<const u32x4*>(p + m * ld + col);
+  }
+};
+struct PartSrc {  // fp32 split-K partials [S][M][ld] and the per-column scale
+  const float* p;
+  const float* scale;
+  int ld, S;
+  size_t stride;  // M * ld
+  __device__ __forceinline__ u32x4 load(size_t m, int col) const {
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    const float* q = p + m * ld + col;
+    for (int s = 0; s < S; ++s) {
+      const float4 a = *reinterpret_cast<const float4*>(q + s * stride);
+      const float4 b = *reinterpret_cast<const float4*>(q + s * stride + 4);
+      acc[0] += a.x; acc[1] += a.y; acc[2] += a.z; acc[3] += a.w;
+      acc[4] += b.x; acc[5] += b.y; acc[6] += b.z; acc[7] += b.w;
+    }
+    const float4 s0 = *reinterpret_cast<const float4*>(scale + col);
+    const float4 s1 = *reinterpret_cast<const float4*>(scale + col + 4);
+    const float o[8] = {acc[0] * s0.x, acc[1] * s0.y, acc[2] * s0.z, acc[3] * s0.w,
+                        acc[4] * s1.x, acc[5] * s1.y, acc[6] * s1.z, acc[7] * s1.w};
+    return pack8(o);
+  }
+};
+
 // ---- residual + (1 + w) RMSNorm: one 256-thread workgroup per row; the row (<= 8 chunks of
 // 8 per thread, H <= 16384) stays in registers between the sum of squares and the scaling.
 // Every load of the row is issued before the first store (hidden_out may alias hidden_in).
 constexpr int kNormThreads = 256;
 constexpr int kNormMaxChunks = 8;
 
+template <class Src>
 __global__ __launch_bounds__(kNormThreads) void residual_rmsnorm_kernel(
-    const uint16_t* h_in, const uint16_t* __restrict__ delta, const float* __restrict__ weight,
+    const uint16_t* h_in, Src delta, bool has_delta, const float* __restrict__ weight,
     uint16_t* h_out, uint16_t* __restrict__ y, int H, float eps) {  // h_out may alias h_in
   const int row = blockIdx.x;
   const int tid = threadIdx.x;
@@ -50,7 +86,7 @@ __global__ __launch_bounds__(kNormThreads) void residual_rmsnorm_kernel(
     const int c = tid + k * kNormThreads;
     if (c < nc) {
       hv[k] = *reinterpret_cast<const u32x4*>(h_in + base + 8 * c);
-      if (delta != nullptr) dv[k] = *reinterpret_cast<const u32x4*>(delta + base + 8 * c);
+      if (has_delta) dv[k] = delta.load(row, 8 * c);
     }
   }
   float x[kNormMaxChunks][8];
@@ -60,7 +96,7 @@ __global__ __launch_bounds__(kNormThreads) void residual_rmsnorm_kernel(
     const int c = tid + k * kNormThreads;
     if (c < nc) {
       unpack8(hv[k], x[k]);
-      if (delta != nullptr) {
+      if (has_delta) {
         float d[8];
         unpack8(dv[k], d);
 #pragma unroll
@@ -117,7 +153,8 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restric
 }
 
 // ---- DeltaNet in-projection split. Row m of proj (stride ld): [qkv_n | z_n | hv | hv | ...].
-__global__ __launch_bounds__(256) void dn_split_kernel(const uint16_t* __restrict__ proj, int ld,
+template <class Src>
+__global__ __launch_bounds__(256) void dn_split_kernel(Src proj,
                                                        uint16_t* __restrict__ mixed,
                                                        uint16_t* __restrict__ z,
                                                        float* __restrict__ a,
@@ -130,7 +167,7 @@ __global__ __launch_bounds__(256) void dn_split_kernel(const uint16_t* __restric
        c += (size_t)gridDim.x * blockDim.x) {
     const size_t m = c / cpr;
     const int j = (int)(c - m * cpr);
-    const u32x4 v = *reinterpret_cast<const u32x4*>(proj + m * ld + 8 * (size_t)j);
+    const u32x4 v = proj.load(m, 8 * j);
     if (j < cq) {
       *reinterpret_cast<u32x4*>(mixed + m * qkv_n + 8 * j) = v;
     } else if (j < cq + cz) {
@@ -149,7 +186,8 @@ __global__ __launch_bounds__(256) void dn_split_kernel(const uint16_t* __restric
 
 // ---- GQA projection split. Row m of proj (stride ld): query/gate interleaved per q head
 // (hd each), then key per kv head, then value per kv head.
-__global__ __launch_bounds__(256) void gqa_split_kernel(const uint16_t* __restrict__ proj, int ld,
+template <class Src>
+__global__ __launch_bounds__(256) void gqa_split_kernel(Src proj,
                                                         uint16_t* __restrict__ query,
                                                         uint16_t* __restrict__ gate,
                                                         uint16_t* __restrict__ key,
@@ -164,7 +202,7 @@ __global__ __launch_bounds__(256) void gqa_split_kernel(const uint16_t* __restri
        c += (size_t)gridDim.x * blockDim.x) {
     const size_t m = c / cpr;
     const int j = (int)(c - m * cpr);
-    const u32x4 v = *reinterpret_cast<const u32x4*>(proj + m * ld + 8 * (size_t)j);
+    const u32x4 v = proj.load(m, 8 * j);
     uint16_t* dst;
     if (j < cqg) {
       const int h = j / (2 * ch), r = j - h * 2 * ch;
@@ -196,9 +234,29 @@ extern "C" int npn_residual_rmsnorm(const uint16_t* hidden_in, const uint16_t* d
                   NPN_ALIGNED16(hidden_out) && NPN_ALIGNED16(normed),
               NPN_ERR_ALIGN);
   uint16_t* hout = hidden_out ? hidden_out : const_cast<uint16_t*>(hidden_in);
-  hipLaunchKernelGGL(residual_rmsnorm_kernel, dim3(M), dim3(kNormThreads), 0,
-                     static_cast<hipStream_t>(stream), hidden_in, delta, weight, hout, normed, H,
-                     eps);
+  hipLaunchKernelGGL(residual_rmsnorm_kernel<BfSrc>, dim3(M), dim3(kNormThreads), 0,
+                     static_cast<hipStream_t>(stream), hidden_in, BfSrc{delta, H},
+                     delta != nullptr, weight, hout, normed, H, eps);
+  return npn_launch_status();
+}
+
+extern "C" int npn_residual_rmsnorm_partials(const uint16_t* hidden_in, const float* partial,
+                                             int split_k, const float* scale,
+                                             const float* weight, uint16_t* hidden_out,
+                                             uint16_t* normed, int M, int H, float eps,
+                                             void* stream) {
+  NPN_REQUIRE(hidden_in && partial && scale && weight && hidden_out && normed, NPN_ERR_NULL);
+  NPN_REQUIRE(M >= 1 && H >= 8 && H % 8 == 0 && H / 8 <= kNormThreads * kNormMaxChunks &&
+                  split_k >= 1 && split_k <= 64,
+              NPN_ERR_SHAPE);
+  NPN_REQUIRE(eps >= 0.0f, NPN_ERR_VALUE);
+  NPN_REQUIRE(NPN_ALIGNED16(hidden_in) && NPN_ALIGNED16(partial) && NPN_ALIGNED16(scale) &&
+                  NPN_ALIGNED16(weight) && NPN_ALIGNED16(hidden_out) && NPN_ALIGNED16(normed),
+              NPN_ERR_ALIGN);
+  const PartSrc src{partial, scale, H, split_k, (size_t)M * H};
+  hipLaunchKernelGGL(residual_rmsnorm_kernel<PartSrc>, dim3(M), dim3(kNormThreads), 0,
+                     static_cast<hipStream_t>(stream), hidden_in, src, true, weight, hidden_out,
+                     normed, H, eps);
   return npn_launch_status();
 }
 
@@ -222,9 +280,29 @@ extern "C" int npn_deltanet_split(const uint16_t* proj, int ld, uint16_t* mixed_
                   NPN_ALIGNED16(a_out) && NPN_ALIGNED16(b_out),
               NPN_ERR_ALIGN);
   const size_t chunks = (size_t)M * ((qkv_n + z_n + 2 * hv) / 8);
-  hipLaunchKernelGGL(dn_split_kernel, dim3(grid_for(chunks)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), proj, ld, mixed_qkv, z, a_out, b_out, M,
-                     qkv_n, z_n, hv);
+  hipLaunchKernelGGL(dn_split_kernel<BfSrc>, dim3(grid_for(chunks)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), BfSrc{proj, ld}, mixed_qkv, z, a_out,
+                     b_out, M, qkv_n, z_n, hv);
+  return npn_launch_status();
+}
+
+extern "C" int npn_deltanet_split_partials(const float* partial, int split_k, const float* scale,
+                                           int ld, uint16_t* mixed_qkv, uint16_t* z,
+                                           float* a_out, float* b_out, int M, int qkv_n, int z_n,
+                                           int hv, void* stream) {
+  NPN_REQUIRE(partial && scale && mixed_qkv && z && a_out && b_out, NPN_ERR_NULL);
+  NPN_REQUIRE(M >= 1 && qkv_n % 8 == 0 && z_n % 8 == 0 && hv % 8 == 0 && qkv_n > 0 && z_n > 0 &&
+                  hv > 0 && ld % 8 == 0 && ld >= qkv_n + z_n + 2 * hv && split_k >= 1 &&
+                  split_k <= 64,
+              NPN_ERR_SHAPE);
+  NPN_REQUIRE(NPN_ALIGNED16(partial) && NPN_ALIGNED16(scale) && NPN_ALIGNED16(mixed_qkv) &&
+                  NPN_ALIGNED16(z) && NPN_ALIGNED16(a_out) && NPN_ALIGNED16(b_out),
+              NPN_ERR_ALIGN);
+  const size_t chunks = (size_t)M * ((qkv_n + z_n + 2 * hv) / 8);
+  const PartSrc src{partial, scale, ld, split_k, (size_t)M * ld};
+  hipLaunchKernelGGL(dn_split_kernel<PartSrc>, dim3(grid_for(chunks)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), src, mixed_qkv, z, a_out, b_out, M, qkv_n,
+                     z_n, hv);
   return npn_launch_status();
 }
 
@@ -239,8 +317,28 @@ extern "C" int npn_gqa_split(const uint16_t* proj, int ld, uint16_t* query, uint
                   NPN_ALIGNED16(key) && NPN_ALIGNED16(value),
               NPN_ERR_ALIGN);
   const size_t chunks = (size_t)M * (2 * (q_heads + kv_heads) * head_dim / 8);
-  hipLaunchKernelGGL(gqa_split_kernel, dim3(grid_for(chunks)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), proj, ld, query, gate, key, value, M,
-                     q_heads, kv_heads, head_dim);
+  hipLaunchKernelGGL(gqa_split_kernel<BfSrc>, dim3(grid_for(chunks)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), BfSrc{proj, ld}, query, gate, key, value,
+                     M, q_heads, kv_heads, head_dim);
+  return npn_launch_status();
+}
+
+extern "C" int npn_gqa_split_partials(const float* partial, int split_k, const float* scale,
+                                      int ld, uint16_t* query, uint16_t* gate, uint16_t* key,
+                                      uint16_t* value, int M, int q_heads, int kv_heads,
+                                      int head_dim, void* stream) {
+  NPN_REQUIRE(partial && scale && query && gate && key && value, NPN_ERR_NULL);
+  NPN_REQUIRE(M >= 1 && q_heads >= 1 && kv_heads >= 1 && head_dim >= 8 && head_dim % 8 == 0 &&
+                  ld % 8 == 0 && ld >= 2 * (q_heads + kv_heads) * head_dim && split_k >= 1 &&
+                  split_k <= 64,
+              NPN_ERR_SHAPE);
+  NPN_REQUIRE(NPN_ALIGNED16(partial) && NPN_ALIGNED16(scale) && NPN_ALIGNED16(query) &&
+                  NPN_ALIGNED16(gate) && NPN_ALIGNED16(key) && NPN_ALIGNED16(value),
+              NPN_ERR_ALIGN);
+  const size_t chunks = (size_t)M * (2 * (q_heads + kv_heads) * head_dim / 8);
+  const PartSrc src{partial, scale, ld, split_k, (size_t)M * ld};
+  hipLaunchKernelGGL(gqa_split_kernel<PartSrc>, dim3(grid_for(chunks)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), src, query, gate, key, value, M, q_heads,
+                     kv_heads, head_dim);
   return npn_launch_status();
 }

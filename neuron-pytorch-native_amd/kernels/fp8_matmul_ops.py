@@ -43,6 +43,39 @@ def _(x, w_fp8_T_i8, scale):
     return x.new_empty((x.shape[0], w_fp8_T_i8.shape[1]))
 
 
+def split_k(M, K, N):
+    """Split-K factor of the GEMM plan for these sizes (1: the GEMM writes bf16 itself)."""
+    return query("npn_fp8_matmul_split_k", M, K, N)
+
+
+@torch.library.custom_op("fp8::matmul_partials", mutates_args=(), device_types="cuda")
+def fp8_matmul_partials(x: torch.Tensor, w_fp8_T_i8: torch.Tensor) -> torch.Tensor:
+    """New op: the GEMM of fp8::matmul without its reduction and scale, [S, M, N] f32 with
+    S = split_k(M, K, N); fp8::matmul(x, w, scale) == bf16(scale * partials.sum(0)) summed
+    in order. The *_partials glue ops consume it."""
+    M, K = x.shape
+    Kw, N = w_fp8_T_i8.shape
+    if Kw != K:
+        raise RuntimeError(f"x has K={K} but the weight has K={Kw}")
+    require(x, "x", torch.bfloat16, shape=(M, K))
+    if w_fp8_T_i8.dtype not in (torch.int8, torch.uint8, torch.float8_e4m3fn):
+        raise TypeError(f"w_fp8_T_i8 must hold fp8 bytes, got {w_fp8_T_i8.dtype}")
+    require(w_fp8_T_i8, "w_fp8_T_i8", w_fp8_T_i8.dtype, shape=(K, N))
+    S = split_k(M, K, N)
+    if S == 0:
+        raise RuntimeError(f"unsupported fp8 matmul shape M={M} K={K} N={N}")
+    out = torch.empty((S, M, N), dtype=torch.float32, device=x.device)
+    call("npn_fp8_matmul_partials", x, w_fp8_T_i8, out, M, K, N, stream_of(x))
+    return out
+
+
+@fp8_matmul_partials.register_fake
+def _(x, w_fp8_T_i8):
+    M, K = x.shape
+    N = w_fp8_T_i8.shape[1]
+    return x.new_empty((split_k(M, K, N), M, N), dtype=torch.float32)
+
+
 def fp8_linear(x, w_fp8_T_i8, scale):
     """x [..., K] bf16 -> [..., N], as the reference's fp8_linear
     (contrib/qwen3.6-27b/static_decode.py:307-319)."""

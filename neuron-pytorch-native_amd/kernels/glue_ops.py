@@ -9,6 +9,9 @@ torch elementwise kernels in the reference's decode layers):
   glue::gqa_split(proj [M, ld] bf16, q_heads, kv_heads, head_dim)
       -> query, gate [M, q_heads, head_dim], key, value [M, kv_heads, head_dim] bf16
       (_gqa_layer, static_decode.py:867-870, :880-890)
+  glue::deltanet_split_partials, glue::gqa_split_partials: the same, reading the projection
+      as fp8::matmul_partials output [S, M, ld] f32 plus its scale; bit-identical to
+      fp8::matmul followed by the bf16 form
 """
 import torch
 
@@ -71,3 +74,61 @@ def _(proj, q_heads, kv_heads, head_dim):
     M = proj.shape[0]
     return (proj.new_empty((M, q_heads, head_dim)), proj.new_empty((M, q_heads, head_dim)),
             proj.new_empty((M, kv_heads, head_dim)), proj.new_empty((M, kv_heads, head_dim)))
+
+
+def _partials(partials, scale, name="partials"):
+    if partials.dim() != 3:
+        raise RuntimeError(f"{name} must be [S, M, N], got {tuple(partials.shape)}")
+    S, M, ld = partials.shape
+    require(partials, name, torch.float32)
+    require(scale, "scale", torch.float32, numel=ld)
+    return S, M, ld
+
+
+@torch.library.custom_op("glue::deltanet_split_partials", mutates_args=(), device_types="cuda")
+def deltanet_split_partials(partials: torch.Tensor, scale: torch.Tensor, qkv_n: int, z_n: int,
+                            hv: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor,
+                                              torch.Tensor]:
+    S, M, ld = _partials(partials, scale)
+    bf = torch.bfloat16
+    mixed = torch.empty((M, qkv_n), dtype=bf, device=partials.device)
+    z = torch.empty((M, z_n), dtype=bf, device=partials.device)
+    a = torch.empty((M, hv), dtype=torch.float32, device=partials.device)
+    b = torch.empty((M, hv), dtype=torch.float32, device=partials.device)
+    call("npn_deltanet_split_partials", partials, S, scale, ld, mixed, z, a, b, M, qkv_n, z_n,
+         hv, stream_of(partials))
+    return mixed, z, a, b
+
+
+@deltanet_split_partials.register_fake
+def _(partials, scale, qkv_n, z_n, hv):
+    M = partials.shape[1]
+    bf = torch.bfloat16
+    return (partials.new_empty((M, qkv_n), dtype=bf), partials.new_empty((M, z_n), dtype=bf),
+            partials.new_empty((M, hv)), partials.new_empty((M, hv)))
+
+
+@torch.library.custom_op("glue::gqa_split_partials", mutates_args=(), device_types="cuda")
+def gqa_split_partials(partials: torch.Tensor, scale: torch.Tensor, q_heads: int, kv_heads: int,
+                       head_dim: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor,
+                                               torch.Tensor]:
+    S, M, ld = _partials(partials, scale)
+    bf = torch.bfloat16
+    dev = partials.device
+    query = torch.empty((M, q_heads, head_dim), dtype=bf, device=dev)
+    gate = torch.empty((M, q_heads, head_dim), dtype=bf, device=dev)
+    key = torch.empty((M, kv_heads, head_dim), dtype=bf, device=dev)
+    value = torch.empty((M, kv_heads, head_dim), dtype=bf, device=dev)
+    call("npn_gqa_split_partials", partials, S, scale, ld, query, gate, key, value, M, q_heads,
+         kv_heads, head_dim, stream_of(partials))
+    return query, gate, key, value
+
+
+@gqa_split_partials.register_fake
+def _(partials, scale, q_heads, kv_heads, head_dim):
+    M = partials.shape[1]
+    bf = torch.bfloat16
+    return (partials.new_empty((M, q_heads, head_dim), dtype=bf),
+            partials.new_empty((M, q_heads, head_dim), dtype=bf),
+            partials.new_empty((M, kv_heads, head_dim), dtype=bf),
+            partials.new_empty((M, kv_heads, head_dim), dtype=bf))

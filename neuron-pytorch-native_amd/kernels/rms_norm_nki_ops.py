@@ -8,6 +8,8 @@ plus the residual form the decode loop applies before every norm
 (contrib/qwen3.6-27b/static_decode.py:533-542), fused into the same pass:
 
   normfuse::residual_rms_norm(hidden, delta, weight, eps) -> (hidden + delta, rms_norm(...))
+  normfuse::residual_rms_norm_partials(hidden, partials, scale, weight, eps): the same with
+      delta taken from fp8::matmul_partials output (the GEMM reduction fused in)
 
 The reference op takes one token's [H] vector; this one takes any number of rows.
 """
@@ -55,4 +57,31 @@ def residual_rms_norm(hidden: torch.Tensor, delta: torch.Tensor, weight: torch.T
 
 @residual_rms_norm.register_fake
 def _(hidden, delta, weight, eps=RMS_EPS):
+    return torch.empty_like(hidden), torch.empty_like(hidden)
+
+
+@torch.library.custom_op("normfuse::residual_rms_norm_partials", mutates_args=(),
+                         device_types="cuda")
+def residual_rms_norm_partials(hidden: torch.Tensor, partials: torch.Tensor, scale: torch.Tensor,
+                               weight: torch.Tensor,
+                               eps: float = RMS_EPS) -> tuple[torch.Tensor, torch.Tensor]:
+    """residual_rms_norm with delta = bf16(scale * partials.sum(0)) (summed in order) taken
+    from fp8::matmul_partials output [S, M, H]: bit-identical to fp8::matmul followed by
+    residual_rms_norm."""
+    M, H = _rows(hidden)
+    require(hidden, "hidden", torch.bfloat16)
+    if partials.dim() != 3 or tuple(partials.shape[1:]) != (M, H):
+        raise RuntimeError(f"partials must be [S, {M}, {H}], got {tuple(partials.shape)}")
+    require(partials, "partials", torch.float32)
+    require(scale, "scale", torch.float32, numel=H)
+    require(weight, "weight", torch.float32, numel=H)
+    h_out = torch.empty_like(hidden)
+    normed = torch.empty_like(hidden)
+    call("npn_residual_rmsnorm_partials", hidden, partials, partials.shape[0], scale, weight,
+         h_out, normed, M, H, float(eps), stream_of(hidden))
+    return h_out, normed
+
+
+@residual_rms_norm_partials.register_fake
+def _(hidden, partials, scale, weight, eps=RMS_EPS):
     return torch.empty_like(hidden), torch.empty_like(hidden)

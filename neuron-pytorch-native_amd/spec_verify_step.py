@@ -22,6 +22,7 @@ import math
 import torch
 
 import npn_ops  # noqa: F401  (registers the torch.ops)
+from fp8_matmul_ops import split_k as fp8_split_k
 
 HIDDEN = 5120
 DN_HK, DN_HV, DN_D = 16, 48, 128
@@ -95,12 +96,24 @@ def fp8_linear(x, wq, timer=_untimed, name="fp8.matmul"):
     return timer(name, torch.ops.fp8.matmul, x, w, s)
 
 
+def fp8_project(x, wq, timer=_untimed, name="fp8.matmul", fuse=True):
+    """A projection whose consumer is a glue op with a *_partials form: when the GEMM plan
+    splits K, returns (fp32 partials, scale) for that consumer to reduce (bit-identical to
+    fp8.matmul's own reduction); otherwise the bf16 output."""
+    w, s = wq
+    if fuse and fp8_split_k(x.shape[0], x.shape[1], w.shape[1]) > 1:
+        return timer(name, torch.ops.fp8.matmul_partials, x, w), s
+    return timer(name, torch.ops.fp8.matmul, x, w, s)
+
+
 class VerifySlice:
     """Random-init slice of `pattern` layers ('D' DeltaNet, 'G' GQA) plus per-layer MLPs,
     with the decode state of B sequences."""
 
-    def __init__(self, B, K, kv_lens, s_max, pattern="DDDG", seed=0, device="cuda"):
+    def __init__(self, B, K, kv_lens, s_max, pattern="DDDG", seed=0, device="cuda",
+                 fuse_splitk=True):
         self.B, self.K, self.T = B, K, K + 1
+        self.fuse_splitk = fuse_splitk
         self.pattern = pattern
         self.device = device
         self.s_max = s_max
@@ -145,9 +158,15 @@ class VerifySlice:
     # ---- layers: each takes the normed input and returns the residual delta -------------
     def _deltanet(self, L, h):
         B, T = self.B, self.T
-        proj = fp8_linear(h, L["in_proj"], self.timer, f"fp8.matmul[{B * T}x{HIDDEN}x{DN_IN_PAD}]")
-        mixed, z, a, b = self.timer("glue.deltanet_split", torch.ops.glue.deltanet_split, proj,
-                                    DN_QKV, DN_VAL, DN_HV)
+        proj = fp8_project(h, L["in_proj"], self.timer, f"fp8.matmul[{B * T}x{HIDDEN}x{DN_IN_PAD}]",
+                           self.fuse_splitk)
+        if isinstance(proj, tuple):
+            mixed, z, a, b = self.timer("glue.deltanet_split",
+                                        torch.ops.glue.deltanet_split_partials, *proj, DN_QKV,
+                                        DN_VAL, DN_HV)
+        else:
+            mixed, z, a, b = self.timer("glue.deltanet_split", torch.ops.glue.deltanet_split,
+                                        proj, DN_QKV, DN_VAL, DN_HV)
         mixed = mixed.reshape(-1)
         args = (mixed, L["conv_state"], L["conv_w"], L["conv_b"], a.reshape(-1), b.reshape(-1),
                 z.reshape(B * T * DN_HV, DN_D), L["A_log"], L["dt_bias"], L["norm_w"])
@@ -163,15 +182,21 @@ class VerifySlice:
             ckpt, out = self.timer("deltanet.verify", torch.ops.deltanet.verify_from_ckpt,
                                    L["ckpt"], self.prev_accepted, *args)
         L["pending"] = (ckpt, mixed)
-        return fp8_linear(out.reshape(B * T, DN_VAL), L["out_proj"], self.timer,
-                          f"fp8.matmul[{B * T}x{DN_VAL}x{HIDDEN}]")
+        return fp8_project(out.reshape(B * T, DN_VAL), L["out_proj"], self.timer,
+                           f"fp8.matmul[{B * T}x{DN_VAL}x{HIDDEN}]", self.fuse_splitk)
 
     def _gqa(self, L, h, cos, sin):
         B, T = self.B, self.T
-        proj = fp8_linear(h, L["qkv_proj"], self.timer,
-                          f"fp8.matmul[{B * T}x{HIDDEN}x{GQA_QG + 2 * GQA_HKV * GQA_DH}]")
-        query, gate, key, value = self.timer("glue.gqa_split", torch.ops.glue.gqa_split, proj,
-                                             GQA_HQ, GQA_HKV, GQA_DH)
+        proj = fp8_project(h, L["qkv_proj"], self.timer,
+                           f"fp8.matmul[{B * T}x{HIDDEN}x{GQA_QG + 2 * GQA_HKV * GQA_DH}]",
+                           self.fuse_splitk)
+        if isinstance(proj, tuple):
+            query, gate, key, value = self.timer("glue.gqa_split",
+                                                 torch.ops.glue.gqa_split_partials, *proj,
+                                                 GQA_HQ, GQA_HKV, GQA_DH)
+        else:
+            query, gate, key, value = self.timer("glue.gqa_split", torch.ops.glue.gqa_split,
+                                                 proj, GQA_HQ, GQA_HKV, GQA_DH)
         query = query.reshape(B, T, GQA_HQ, GQA_DH)
         gate = gate.reshape(B, T, GQA_HQ, GQA_DH)
         self.timer("gqa.kv_append", torch.ops.gqa.kv_append, key.reshape(B, T, GQA_HKV, GQA_DH),
@@ -179,14 +204,23 @@ class VerifySlice:
                    L["cache_v"], self.kv_len)
         attn = self.timer("gqa.tail_verify", torch.ops.gqa.tail_verify, query, gate, L["q_norm"],
                           cos, sin, L["cache_k"], L["cache_v"], self.kv_len)
-        return fp8_linear(attn.reshape(B * T, GQA_HQ * GQA_DH), L["o_proj"], self.timer,
-                          f"fp8.matmul[{B * T}x{GQA_HQ * GQA_DH}x{HIDDEN}]")
+        return fp8_project(attn.reshape(B * T, GQA_HQ * GQA_DH), L["o_proj"], self.timer,
+                           f"fp8.matmul[{B * T}x{GQA_HQ * GQA_DH}x{HIDDEN}]", self.fuse_splitk)
 
-    def _mlp(self, L, h):
+    def _mlp(self, L, h, last=False):
         M = h.shape[0]
         gu = fp8_linear(h, L["gate_up"], self.timer, f"fp8.matmul[{M}x{HIDDEN}x{2 * INTER}]")
         act = self.timer("glue.silu_mul", torch.ops.glue.silu_mul, gu)
-        return fp8_linear(act, L["down"], self.timer, f"fp8.matmul[{M}x{INTER}x{HIDDEN}]")
+        return fp8_project(act, L["down"], self.timer, f"fp8.matmul[{M}x{INTER}x{HIDDEN}]",
+                           self.fuse_splitk and not last)
+
+    def _add_norm(self, hidden, d, weight):
+        """(hidden + d, its (1+w) RMSNorm); d is a bf16 delta or (partials, scale)."""
+        if isinstance(d, tuple):
+            return self.timer("normfuse.residual_rms_norm",
+                              torch.ops.normfuse.residual_rms_norm_partials, hidden, *d, weight)
+        return self.timer("normfuse.residual_rms_norm", torch.ops.normfuse.residual_rms_norm,
+                          hidden, d, weight)
 
     def forward(self, x, cos=None, sin=None, trace=None):
         """x [B*T, 5120] bf16 -> hidden after the slice (the verify positions' features).
@@ -207,16 +241,13 @@ class VerifySlice:
             if trace is not None:
                 trace.append(hidden)
             d = self._deltanet(L, normed) if L["kind"] == "D" else self._gqa(L, normed, cos, sin)
-            hidden, normed = self.timer("normfuse.residual_rms_norm",
-                                        torch.ops.normfuse.residual_rms_norm, hidden, d,
-                                        L["post_norm"])
+            hidden, normed = self._add_norm(hidden, d, L["post_norm"])
             if trace is not None:
                 trace.append(hidden)
-            d = self._mlp(L, normed)
-            if i + 1 < len(layers):
-                hidden, normed = self.timer("normfuse.residual_rms_norm",
-                                            torch.ops.normfuse.residual_rms_norm, hidden, d,
-                                            layers[i + 1]["in_norm"])
+            last = i + 1 == len(layers)
+            d = self._mlp(L, normed, last)
+            if not last:
+                hidden, normed = self._add_norm(hidden, d, layers[i + 1]["in_norm"])
             else:
                 hidden = hidden + d
         if trace is not None:

@@ -22,7 +22,7 @@ def test_library_exports_every_declared_symbol():
     import npn_native
     lib = npn_native.lib()
     names = _declared()
-    assert len(names) >= 18
+    assert len(names) >= 23
     for n in names:
         assert hasattr(lib, n), f"{n} declared in the header but not exported"
     assert set(names) == set(npn_native.SIGNATURES)
@@ -85,6 +85,32 @@ def test_ops_register_and_propagate_shapes():
         assert (m.shape, zz.shape, a.shape, a.dtype) == ((16, 10240), (16, 6144), (16, 48), f32)
         q, gt, k, v = torch.ops.glue.gqa_split(torch.empty(16, 14336, dtype=bf), 24, 4, 256)
         assert q.shape == gt.shape == (16, 24, 256) and k.shape == v.shape == (16, 4, 256)
+        p = torch.ops.fp8.matmul_partials(torch.empty(256, 17408, dtype=bf),
+                                          torch.empty(17408, 5120, dtype=torch.int8))
+        assert p.shape == (8, 256, 5120) and p.dtype == f32
+        h = torch.empty(256, 5120, dtype=bf)
+        h2, nrm = torch.ops.normfuse.residual_rms_norm_partials(h, p, torch.empty(5120),
+                                                                torch.empty(5120))
+        assert h2.shape == nrm.shape == h.shape and nrm.dtype == bf
+        m, zz, a, b = torch.ops.glue.deltanet_split_partials(torch.empty(2, 16, 16512),
+                                                             torch.empty(16512), 10240, 6144, 48)
+        assert (m.shape, m.dtype, zz.shape, a.shape, a.dtype) == ((16, 10240), bf, (16, 6144),
+                                                                  (16, 48), f32)
+        q, gt, k, v = torch.ops.glue.gqa_split_partials(torch.empty(2, 16, 14336),
+                                                        torch.empty(14336), 24, 4, 256)
+        assert q.shape == gt.shape == (16, 24, 256) and k.shape == v.shape == (16, 4, 256)
+        assert q.dtype == bf
+
+
+def test_fp8_split_k_plan():
+    """Split-K factors the GEMM plan picks at the verify step's M = 256 (host code only)."""
+    from npn_native import query
+    assert query("npn_fp8_matmul_split_k", 256, 17408, 5120) == 8
+    assert query("npn_fp8_matmul_split_k", 256, 6144, 5120) == 4
+    assert query("npn_fp8_matmul_split_k", 256, 5120, 16512) == 2
+    assert query("npn_fp8_matmul_split_k", 256, 5120, 14336) == 2
+    assert query("npn_fp8_matmul_split_k", 256, 5120, 34816) == 1
+    assert query("npn_fp8_matmul_split_k", 256, 100, 5120) == 0
 
 
 def test_ops_refuse_cpu_tensors():

@@ -249,7 +249,7 @@ int npn_gqa_split(const uint16_t* proj, int ld, uint16_t* query, uint16_t* gate,
  *   bf16(scale[n] * (partial[0][m][n] + ... + partial[split_k-1][m][n])),
  * bit-identical to npn_fp8_matmul's output, so each result equals npn_fp8_matmul followed by
  * the bf16 op. partial [split_k][M][ld] f32 (ld = H for the norm), scale [ld] f32,
- * 1 <= split_k <= 64; other arguments as in the bf16 forms. */
+ * 1 <= split_k <= 8; other arguments as in the bf16 forms. */
 int npn_residual_rmsnorm_partials(const uint16_t* hidden_in, const float* partial, int split_k,
                                   const float* scale, const float* weight, uint16_t* hidden_out,
                                   uint16_t* normed, int M, int H, float eps, void* stream);

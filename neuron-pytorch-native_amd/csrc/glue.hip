@@ -44,19 +44,32 @@ struct BfSrc {  // a bf16 matrix with row stride ld
     return *reinterpret_cast<const u32x4*>(p + m * ld + col);
   }
 };
-struct PartSrc {  // fp32 split-K partials [S][M][ld] and the per-column scale
+constexpr int kMaxSplit = 8;  // partial count the unrolled loads cover (the GEMM plan's max)
+
+struct PartSrc {  // fp32 split-K partials [S][M][ld] and the per-column scale, S <= kMaxSplit
   const float* p;
   const float* scale;
   int ld, S;
   size_t stride;  // M * ld
   __device__ __forceinline__ u32x4 load(size_t m, int col) const {
-    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    // All S partial loads are issued before the first add (unrolled, predicated), so one
+    // memory latency is paid per chunk rather than S.
     const float* q = p + m * ld + col;
-    for (int s = 0; s < S; ++s) {
-      const float4 a = *reinterpret_cast<const float4*>(q + s * stride);
-      const float4 b = *reinterpret_cast<const float4*>(q + s * stride + 4);
-      acc[0] += a.x; acc[1] += a.y; acc[2] += a.z; acc[3] += a.w;
-      acc[4] += b.x; acc[5] += b.y; acc[6] += b.z; acc[7] += b.w;
+    float4 a[kMaxSplit], b[kMaxSplit];
+#pragma unroll
+    for (int s = 0; s < kMaxSplit; ++s) {
+      if (s < S) {
+        a[s] = *reinterpret_cast<const float4*>(q + s * stride);
+        b[s] = *reinterpret_cast<const float4*>(q + s * stride + 4);
+      }
+    }
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < kMaxSplit; ++s) {
+      if (s < S) {
+        acc[0] += a[s].x; acc[1] += a[s].y; acc[2] += a[s].z; acc[3] += a[s].w;
+        acc[4] += b[s].x; acc[5] += b[s].y; acc[6] += b[s].z; acc[7] += b[s].w;
+      }
     }
     const float4 s0 = *reinterpret_cast<const float4*>(scale + col);
     const float4 s1 = *reinterpret_cast<const float4*>(scale + col + 4);
@@ -66,11 +79,13 @@ struct PartSrc {  // fp32 split-K partials [S][M][ld] and the per-column scale
   }
 };
 
-// ---- residual + (1 + w) RMSNorm: one 256-thread workgroup per row; the row (<= 8 chunks of
-// 8 per thread, H <= 16384) stays in registers between the sum of squares and the scaling.
+// ---- residual + (1 + w) RMSNorm: one 1024-thread workgroup per row; the row (<= 2 chunks of
+// 8 per thread, H <= 16384) stays in registers between the sum of squares and the scaling,
+// and with split-K partials (S row segments per chunk) many loads are in flight per row.
+// Both input forms use this one layout, so their sums of squares associate identically.
 // Every load of the row is issued before the first store (hidden_out may alias hidden_in).
-constexpr int kNormThreads = 256;
-constexpr int kNormMaxChunks = 8;
+constexpr int kNormThreads = 1024;
+constexpr int kNormMaxChunks = 2;
 
 template <class Src>
 __global__ __launch_bounds__(kNormThreads) void residual_rmsnorm_kernel(
@@ -247,7 +262,7 @@ extern "C" int npn_residual_rmsnorm_partials(const uint16_t* hidden_in, const fl
                                              void* stream) {
   NPN_REQUIRE(hidden_in && partial && scale && weight && hidden_out && normed, NPN_ERR_NULL);
   NPN_REQUIRE(M >= 1 && H >= 8 && H % 8 == 0 && H / 8 <= kNormThreads * kNormMaxChunks &&
-                  split_k >= 1 && split_k <= 64,
+                  split_k >= 1 && split_k <= kMaxSplit,
               NPN_ERR_SHAPE);
   NPN_REQUIRE(eps >= 0.0f, NPN_ERR_VALUE);
   NPN_REQUIRE(NPN_ALIGNED16(hidden_in) && NPN_ALIGNED16(partial) && NPN_ALIGNED16(scale) &&
@@ -293,7 +308,7 @@ extern "C" int npn_deltanet_split_partials(const float* partial, int split_k, co
   NPN_REQUIRE(partial && scale && mixed_qkv && z && a_out && b_out, NPN_ERR_NULL);
   NPN_REQUIRE(M >= 1 && qkv_n % 8 == 0 && z_n % 8 == 0 && hv % 8 == 0 && qkv_n > 0 && z_n > 0 &&
                   hv > 0 && ld % 8 == 0 && ld >= qkv_n + z_n + 2 * hv && split_k >= 1 &&
-                  split_k <= 64,
+                  split_k <= kMaxSplit,
               NPN_ERR_SHAPE);
   NPN_REQUIRE(NPN_ALIGNED16(partial) && NPN_ALIGNED16(scale) && NPN_ALIGNED16(mixed_qkv) &&
                   NPN_ALIGNED16(z) && NPN_ALIGNED16(a_out) && NPN_ALIGNED16(b_out),
@@ -330,7 +345,7 @@ extern "C" int npn_gqa_split_partials(const float* partial, int split_k, const f
   NPN_REQUIRE(partial && scale && query && gate && key && value, NPN_ERR_NULL);
   NPN_REQUIRE(M >= 1 && q_heads >= 1 && kv_heads >= 1 && head_dim >= 8 && head_dim % 8 == 0 &&
                   ld % 8 == 0 && ld >= 2 * (q_heads + kv_heads) * head_dim && split_k >= 1 &&
-                  split_k <= 64,
+                  split_k <= kMaxSplit,
               NPN_ERR_SHAPE);
   NPN_REQUIRE(NPN_ALIGNED16(partial) && NPN_ALIGNED16(scale) && NPN_ALIGNED16(query) &&
                   NPN_ALIGNED16(gate) && NPN_ALIGNED16(key) && NPN_ALIGNED16(value),

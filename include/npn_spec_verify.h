@@ -91,7 +91,8 @@ int npn_deltanet_verify(const float* state, const int32_t* state_index, int stat
  *   accepted [B] int32 in [0, T-1] (number of accepted drafts).
  *   state_out [B, Hv, 128, 128] f32 = ckpt[b, accepted[b]] (may be NULL to skip
  *   the copy when the next verify uses state_index instead);
- *   conv_state_out [B, QKV, 3] bf16 = last 3 columns of [conv_state || x_0..x_a].
+ *   conv_state_out [B, QKV, 3] bf16 = last 3 columns of [conv_state || x_0..x_a]
+ *   (conv_state_out may equal conv_state: the rollback then happens in place).
  * Out-of-range accepted values are clamped into [0, T-1] on the device. */
 int npn_deltanet_rollback(const float* ckpt, const uint16_t* mixed_qkv,
                           const uint16_t* conv_state, const int32_t* accepted,
@@ -259,6 +260,22 @@ int npn_deltanet_split_partials(const float* partial, int split_k, const float* 
 int npn_gqa_split_partials(const float* partial, int split_k, const float* scale, int ld,
                            uint16_t* query, uint16_t* gate, uint16_t* key, uint16_t* value,
                            int M, int q_heads, int kv_heads, int head_dim, void* stream);
+
+/* torch.ops.gqa.rope_rows -- new op: the RoPE rows of the T verify positions,
+ *   cos_out, sin_out [B, T, dim] f32 = table[kv_len[b] + t] for cos_table, sin_table
+ *   [positions, dim] f32 built once, as the reference indexes its _init_rope table
+ *   (static_decode.py:489-502). Positions past the table are clamped to its last row.
+ *   dim % 4 == 0. */
+int npn_rope_rows(const float* cos_table, const float* sin_table, int positions,
+                  const int32_t* kv_len, float* cos_out, float* sin_out, int B, int T, int dim,
+                  void* stream);
+
+/* torch.ops.spec.commit_ -- new op: the bookkeeping after acceptance, in place, for
+ * decode state kept at fixed addresses (HIP-graph replay):
+ *   prev_accepted[b] = accepted[b]; kv_len[b] += accepted[b] + 1;
+ *   committed[b] += accepted[b] + 1. Any of the three outputs may be NULL. */
+int npn_spec_commit(const int32_t* accepted, int32_t* prev_accepted, int32_t* kv_len,
+                    int32_t* committed, int B, void* stream);
 
 #ifdef __cplusplus
 }

@@ -207,10 +207,12 @@ __global__ __launch_bounds__(kThreads, 3) void dn_verify_kernel(DnArgs a) {
 
 // conv_out[b][c][0..2] = last 3 columns of [conv_state[b][c][0..2] || x_0..x_a], a = accepted[b]
 // (0 when accepted == nullptr: the single-token shift new_cs = conv_in[:, 1:]).
-__global__ void dn_conv_window_kernel(const uint16_t* __restrict__ conv_state,
+// conv_out may equal conv_state (in-place rollback): each thread owns one channel's three
+// entries and loads all of them before it stores.
+__global__ void dn_conv_window_kernel(const uint16_t* conv_state,
                                       const uint16_t* __restrict__ x,
                                       const int32_t* __restrict__ accepted,
-                                      uint16_t* __restrict__ conv_out, int B, int T, int QKV) {
+                                      uint16_t* conv_out, int B, int T, int QKV) {
   const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= (size_t)B * QKV) return;
   const int b = (int)(i / QKV);
@@ -219,11 +221,14 @@ __global__ void dn_conv_window_kernel(const uint16_t* __restrict__ conv_state,
   acc = acc < 0 ? 0 : (acc >= T ? T - 1 : acc);
   const uint16_t* cs = conv_state + ((size_t)b * QKV + c) * 3;
   uint16_t* dst = conv_out + ((size_t)b * QKV + c) * 3;
+  uint16_t v[3];
 #pragma unroll
   for (int j = 0; j < 3; ++j) {
     const int p = acc + 1 + j;  // position in [cs0, cs1, cs2, x0, x1, ...]
-    dst[j] = p < 3 ? cs[p] : x[((size_t)b * T + (p - 3)) * QKV + c];
+    v[j] = p < 3 ? cs[p] : x[((size_t)b * T + (p - 3)) * QKV + c];
   }
+#pragma unroll
+  for (int j = 0; j < 3; ++j) dst[j] = v[j];
 }
 
 // state_out[b] = ckpt[b][accepted[b]] (tile-contiguous copy, 16 bytes per thread).

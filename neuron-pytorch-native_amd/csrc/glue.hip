@@ -231,6 +231,43 @@ __global__ __launch_bounds__(256) void gqa_split_kernel(Src proj,
   }
 }
 
+// ---- RoPE rows of the verify positions: cos/sin [B, T, D] = table[kv_len[b] + t] for a
+// table [P, D] built once (the reference's _init_rope, static_decode.py:489-502); positions
+// past the table are clamped to its last row.
+__global__ __launch_bounds__(256) void rope_rows_kernel(const float* __restrict__ tcos,
+                                                        const float* __restrict__ tsin,
+                                                        const int32_t* __restrict__ kv_len,
+                                                        float* __restrict__ cos_out,
+                                                        float* __restrict__ sin_out, int B, int T,
+                                                        int D, int P) {
+  const int d4 = D / 4;
+  const size_t n = (size_t)B * T * d4;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * blockDim.x) {
+    const size_t bt = i / d4;
+    const int k = (int)(i - bt * d4);
+    const int b = (int)(bt / T), t = (int)(bt - (size_t)b * T);
+    long pos = (long)kv_len[b] + t;
+    pos = pos < 0 ? 0 : (pos >= P ? P - 1 : pos);
+    reinterpret_cast<float4*>(cos_out)[i] = reinterpret_cast<const float4*>(tcos + pos * D)[k];
+    reinterpret_cast<float4*>(sin_out)[i] = reinterpret_cast<const float4*>(tsin + pos * D)[k];
+  }
+}
+
+// ---- Commit of a verify step's acceptance to the per-sequence decode state (one lane per
+// sequence): prev_accepted = accepted; kv_len += accepted + 1; committed += accepted + 1.
+__global__ __launch_bounds__(256) void commit_kernel(const int32_t* __restrict__ accepted,
+                                                     int32_t* __restrict__ prev_accepted,
+                                                     int32_t* __restrict__ kv_len,
+                                                     int32_t* __restrict__ committed, int B) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= B) return;
+  const int a = accepted[b];
+  if (prev_accepted != nullptr) prev_accepted[b] = a;
+  if (kv_len != nullptr) kv_len[b] += a + 1;
+  if (committed != nullptr) committed[b] += a + 1;
+}
+
 int grid_for(size_t chunks) {
   const size_t blocks = (chunks + 255) / 256;
   return (int)(blocks < 4096 ? (blocks > 0 ? blocks : 1) : 4096);
@@ -355,5 +392,30 @@ extern "C" int npn_gqa_split_partials(const float* partial, int split_k, const f
   hipLaunchKernelGGL(gqa_split_kernel<PartSrc>, dim3(grid_for(chunks)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), src, query, gate, key, value, M, q_heads,
                      kv_heads, head_dim);
+  return npn_launch_status();
+}
+
+extern "C" int npn_rope_rows(const float* cos_table, const float* sin_table, int positions,
+                             const int32_t* kv_len, float* cos_out, float* sin_out, int B, int T,
+                             int dim, void* stream) {
+  NPN_REQUIRE(cos_table && sin_table && kv_len && cos_out && sin_out, NPN_ERR_NULL);
+  NPN_REQUIRE(B >= 1 && T >= 1 && dim >= 4 && dim % 4 == 0 && positions >= 1, NPN_ERR_SHAPE);
+  NPN_REQUIRE(NPN_ALIGNED16(cos_table) && NPN_ALIGNED16(sin_table) && NPN_ALIGNED16(cos_out) &&
+                  NPN_ALIGNED16(sin_out),
+              NPN_ERR_ALIGN);
+  const size_t n = (size_t)B * T * (dim / 4);
+  hipLaunchKernelGGL(rope_rows_kernel, dim3(grid_for(n)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), cos_table, sin_table, kv_len, cos_out,
+                     sin_out, B, T, dim, positions);
+  return npn_launch_status();
+}
+
+extern "C" int npn_spec_commit(const int32_t* accepted, int32_t* prev_accepted, int32_t* kv_len,
+                               int32_t* committed, int B, void* stream) {
+  NPN_REQUIRE(accepted != nullptr, NPN_ERR_NULL);
+  NPN_REQUIRE(B >= 1, NPN_ERR_SHAPE);
+  hipLaunchKernelGGL(commit_kernel, dim3((B + 255) / 256), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), accepted, prev_accepted, kv_len, committed,
+                     B);
   return npn_launch_status();
 }

@@ -232,3 +232,28 @@ def deltanet_conv_rollback(
 @deltanet_conv_rollback.register_fake
 def _(mixed_qkv, conv_state, accepted, v_heads):
     return torch.empty_like(conv_state)
+
+
+@torch.library.custom_op("deltanet::conv_rollback_", mutates_args=("conv_state",),
+                         device_types="cuda")
+def deltanet_conv_rollback_(
+    mixed_qkv: torch.Tensor,     # [B*T*QKV_DIM] bf16
+    conv_state: torch.Tensor,    # [B*QKV_DIM, 3] bf16, rolled back in place
+    accepted: torch.Tensor,      # [B] int32 in [0, T-1]
+    v_heads: int,
+) -> None:
+    """deltanet::conv_rollback writing the new window over conv_state (fixed addresses)."""
+    B = accepted.numel()
+    qkv = conv_state.shape[0] // B
+    T = mixed_qkv.numel() // (B * qkv)
+    hk, hv = heads_from_shapes(qkv, v_heads)
+    require(accepted, "accepted", torch.int32, numel=B)
+    require(mixed_qkv, "mixed_qkv", torch.bfloat16, numel=B * T * qkv)
+    require(conv_state, "conv_state", torch.bfloat16, shape=(B * qkv, 3))
+    call("npn_deltanet_rollback", None, mixed_qkv, conv_state, accepted, None, conv_state,
+         B, T, hk, hv, stream_of(conv_state))
+
+
+@deltanet_conv_rollback_.register_fake
+def _(mixed_qkv, conv_state, accepted, v_heads):
+    return None

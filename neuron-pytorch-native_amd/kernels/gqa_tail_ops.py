@@ -130,3 +130,27 @@ def gqa_kv_append(
 @gqa_kv_append.register_fake
 def _(key, value, k_norm, cos, sin, cache_k, cache_v, kv_len):
     return None
+
+
+@torch.library.custom_op("gqa::rope_rows", mutates_args=(), device_types="cuda")
+def rope_rows(cos_table: torch.Tensor, sin_table: torch.Tensor, kv_len: torch.Tensor,
+              T: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """New op: cos, sin [B, T, dim] f32 = rows kv_len[b] + t of tables [P, dim] built once
+    (the reference's _init_rope table, contrib/qwen3.6-27b/static_decode.py:489-502);
+    positions past the table are clamped to its last row."""
+    P, dim = cos_table.shape
+    B = kv_len.numel()
+    require(cos_table, "cos_table", torch.float32, shape=(P, dim))
+    require(sin_table, "sin_table", torch.float32, shape=(P, dim))
+    require(kv_len, "kv_len", torch.int32, numel=B)
+    cos = torch.empty((B, T, dim), dtype=torch.float32, device=cos_table.device)
+    sin = torch.empty_like(cos)
+    call("npn_rope_rows", cos_table, sin_table, P, kv_len, cos, sin, B, T, dim,
+         stream_of(cos_table))
+    return cos, sin
+
+
+@rope_rows.register_fake
+def _(cos_table, sin_table, kv_len, T):
+    shape = (kv_len.numel(), T, cos_table.shape[1])
+    return cos_table.new_empty(shape), cos_table.new_empty(shape)

@@ -43,6 +43,8 @@ SIGNATURES = {
     "npn_residual_rmsnorm_partials": (_I, [_P, _P, _I] + [_P] * 4 + [_I, _I, _F, _P]),
     "npn_deltanet_split_partials": (_I, [_P, _I, _P, _I] + [_P] * 4 + [_I] * 4 + [_P]),
     "npn_gqa_split_partials": (_I, [_P, _I, _P, _I] + [_P] * 4 + [_I] * 4 + [_P]),
+    "npn_rope_rows": (_I, [_P, _P, _I] + [_P] * 3 + [_I] * 3 + [_P]),
+    "npn_spec_commit": (_I, [_P] * 4 + [_I, _P]),
 }
 
 _lib = None

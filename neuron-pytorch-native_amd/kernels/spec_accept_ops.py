@@ -75,3 +75,21 @@ def _(target_logits, draft_logits, draft_ids, u_accept, u_sample, inv_temperatur
     B, T, _ = target_logits.shape
     return (target_logits.new_empty((B,), dtype=torch.int32),
             target_logits.new_empty((B, T), dtype=torch.int64))
+
+
+@torch.library.custom_op("spec::commit_", mutates_args=("prev_accepted", "kv_len", "committed"),
+                         device_types="cuda")
+def commit_(accepted: torch.Tensor, prev_accepted: torch.Tensor, kv_len: torch.Tensor,
+            committed: torch.Tensor) -> None:
+    """New op: after acceptance, in place: prev_accepted = accepted, kv_len += accepted + 1,
+    committed += accepted + 1 (all int32 [B]), for decode state at fixed addresses."""
+    B = accepted.numel()
+    for t, n in ((accepted, "accepted"), (prev_accepted, "prev_accepted"), (kv_len, "kv_len"),
+                 (committed, "committed")):
+        require(t, n, torch.int32, numel=B)
+    call("npn_spec_commit", accepted, prev_accepted, kv_len, committed, B, stream_of(accepted))
+
+
+@commit_.register_fake
+def _(accepted, prev_accepted, kv_len, committed):
+    return None

@@ -149,6 +149,9 @@ class VerifySlice:
                 L["cache_v"] = torch.randn(shape, generator=g, device=device).to(torch.bfloat16)
             self.layers.append(L)
         self.kv_len = torch.as_tensor(kv_lens, dtype=torch.int32, device=device).clone()
+        # RoPE table of every cache position, built once (the reference's _init_rope); each
+        # step gathers the rows of its T positions.
+        self.rope_cos, self.rope_sin = rope_tables(torch.arange(s_max, device=device))
         self.prev_accepted = None
         self.timer = _untimed
         self.persistent = False
@@ -231,8 +234,8 @@ class VerifySlice:
         the residual stream entering each sublayer (mixer, then MLP, per layer) and the final
         hidden are appended to it."""
         if cos is None:
-            pos = self.kv_len.long().unsqueeze(1) + torch.arange(self.T, device=x.device)
-            cos, sin = rope_tables(pos)
+            cos, sin = self.timer("gqa.rope_rows", torch.ops.gqa.rope_rows, self.rope_cos,
+                                  self.rope_sin, self.kv_len, self.T)
         layers = self.layers
         hidden = x
         normed = self.timer("normfuse.rms_norm", torch.ops.normfuse.rms_norm, x,
@@ -260,17 +263,17 @@ class VerifySlice:
         for L in self.layers:
             if L["kind"] == "D":
                 ckpt, mixed = L.pop("pending")
-                conv = self.timer("deltanet.conv_rollback", torch.ops.deltanet.conv_rollback,
-                                  mixed, L["conv_state"], accepted, DN_HV)
-                if self.persistent:
-                    L["conv_state"].copy_(conv)
+                if self.persistent:  # window rolled back over the fixed buffer
+                    self.timer("deltanet.conv_rollback", torch.ops.deltanet.conv_rollback_,
+                               mixed, L["conv_state"], accepted, DN_HV)
                 else:
-                    L["conv_state"] = conv
+                    L["conv_state"] = self.timer("deltanet.conv_rollback",
+                                                 torch.ops.deltanet.conv_rollback, mixed,
+                                                 L["conv_state"], accepted, DN_HV)
                     L["ckpt"] = ckpt
         if self.persistent:
-            self.prev_accepted.copy_(accepted)
-            self.kv_len.add_(accepted + 1)
-            self.committed.add_(accepted + 1)
+            self.timer("spec.commit", torch.ops.spec.commit_, accepted, self.prev_accepted,
+                       self.kv_len, self.committed)
             self.parity ^= 1
         else:
             self.prev_accepted = accepted

@@ -9,7 +9,9 @@ rewritten in place with new values (same addresses, different data), other GPU w
 the same stream, and the device is synchronised; after every step the outputs (hidden,
 accepted lengths, emitted ids) and the whole decode state (KV lengths, committed counters,
 conv windows, the checkpoint buffers, the caches) must be bit-identical, since every kernel
-on the path is deterministic (fixed-order reductions, integer atomics only).
+on the path is deterministic (fixed-order reductions, integer atomics only). A third slice
+that never moves to fixed buffers (new state tensors every step, out-of-place rollback)
+steps alongside and must give the same outputs as the persistent eager one.
 """
 import pytest
 import torch
@@ -51,13 +53,14 @@ def test_graph_replay_matches_eager(greedy):
     dev = "cuda"
     kv = [37, 300, 5, 129]
     s_max = max(kv) + (K + 1) * (STEPS + 4)
-    models = [VerifySlice(B, K, kv, s_max, pattern="DG", seed=11, device=dev) for _ in range(2)]
-    eager, graphed = models
+    models = [VerifySlice(B, K, kv, s_max, pattern="DG", seed=11, device=dev) for _ in range(3)]
+    eager, graphed, plain = models  # plain: never made persistent (new state tensors per step)
     g = torch.Generator(device=dev).manual_seed(5)
     x = torch.randn(B * (K + 1), HIDDEN, generator=g, device=dev).to(torch.bfloat16)
     logits = synthetic_logits(B, K, V, 6, dev)
     for m in models:
         m.step(x, *logits, greedy=greedy)
+    for m in (eager, graphed):
         m.make_persistent()
     graphed.capture(x, *logits, greedy=greedy)
     torch.cuda.synchronize()
@@ -70,7 +73,11 @@ def test_graph_replay_matches_eager(greedy):
         junk = (junk @ junk).sum()
         torch.cuda.synchronize()
         h_e, a_e, ids_e = eager.step(x, *logits, greedy=greedy)
+        h_p, a_p, ids_p = plain.step(x, *logits, greedy=greedy)
         torch.cuda.synchronize()
+        assert torch.equal(a_e, a_p) and torch.equal(ids_e, ids_p), f"step {step}: persistent"
+        assert torch.equal(h_e.view(torch.int16), h_p.view(torch.int16)), f"step {step}: hidden"
+        assert torch.equal(eager.kv_len, plain.kv_len)
         h_g, a_g, ids_g = graphed.replay()
         torch.cuda.synchronize()
         assert torch.equal(a_e, a_g), f"step {step}: accepted {a_e.tolist()} vs {a_g.tolist()}"

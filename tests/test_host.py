@@ -22,7 +22,7 @@ def test_library_exports_every_declared_symbol():
     import npn_native
     lib = npn_native.lib()
     names = _declared()
-    assert len(names) >= 23
+    assert len(names) >= 25
     for n in names:
         assert hasattr(lib, n), f"{n} declared in the header but not exported"
     assert set(names) == set(npn_native.SIGNATURES)
@@ -100,6 +100,9 @@ def test_ops_register_and_propagate_shapes():
                                                         torch.empty(14336), 24, 4, 256)
         assert q.shape == gt.shape == (16, 24, 256) and k.shape == v.shape == (16, 4, 256)
         assert q.dtype == bf
+        c, sn = torch.ops.gqa.rope_rows(torch.empty(100, 64), torch.empty(100, 64),
+                                        torch.empty(B, dtype=torch.int32), T)
+        assert c.shape == sn.shape == (B, T, 64) and c.dtype == f32
 
 
 def test_fp8_split_k_plan():

@@ -36,13 +36,16 @@ T = K + 1
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--per-op", action="store_true", help="print per-op timings to stderr")
     p.add_argument("--no-graph", action="store_true",
                    help="time eager steps instead of HIP graph replays of the step")
+    p.add_argument("--lm-head", action="store_true",
+                   help="time the LM head + greedy acceptance over the 27B vocabulary, fused "
+                        "(argmax in the GEMM epilogue) against logits + accept_greedy")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only run a plain 1 GiB device copy 5 times (scales HBM byte counters)")
     return p.parse_args()
@@ -157,10 +160,62 @@ def cpu_baseline(model, x, logits, budget_s=10.0):
                       f"weights decoded to float32 once before timing, BLAS on {cores} threads"}
 
 
+LM_VOCAB = 248320  # Qwen3.6-27B vocabulary (static_decode.py:107)
+
+
+def lm_head_bench(args):
+    """LM head [B*T, 5120] x [5120, 248320] fp8 + greedy acceptance: fused (row argmax in the
+    GEMM epilogue, no logits) vs the GEMM writing bf16 logits, a float cast and
+    accept_greedy. Two weight copies (2.5 GB) alternate so the weights come from HBM."""
+    import torch
+    from spec_verify_step import HIDDEN, random_fp8_linear
+    dev = "cuda"
+    g = torch.Generator(device=dev).manual_seed(args.seed)
+    ws = [random_fp8_linear(LM_VOCAB, HIDDEN, g, dev) for _ in range(2)]
+    x = torch.randn(B * T, HIDDEN, generator=g, device=dev).to(torch.bfloat16)
+    drafts = torch.randint(0, LM_VOCAB, (B, K), generator=g, device=dev)
+
+    def fused(i):
+        w, sc = ws[i % 2]
+        return torch.ops.spec.accept_greedy_fused(x, w, sc, drafts)
+
+    def unfused(i):
+        w, sc = ws[i % 2]
+        logits = torch.ops.fp8.matmul(x, w, sc).float().view(B, T, LM_VOCAB)
+        return torch.ops.spec.accept_greedy(logits, drafts)
+
+    res = {}
+    for name, fn in (("fused", fused), ("unfused", unfused)):
+        for i in range(args.warmup):
+            fn(i)
+        torch.cuda.synchronize()
+        s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s_ev.record()
+        for i in range(args.steps):
+            fn(i)
+        e_ev.record()
+        torch.cuda.synchronize()
+        res[name] = s_ev.elapsed_time(e_ev) / args.steps
+    a_f, o_f = fused(0)
+    a_u, o_u = unfused(0)
+    flops = 2.0 * B * T * HIDDEN * LM_VOCAB
+    print(json.dumps({
+        "workload": f"LM head [{B * T}x{HIDDEN}]x[{HIDDEN}x{LM_VOCAB}] fp8 + greedy acceptance, "
+                    f"B={B}, K={K}",
+        "fused_ms": round(res["fused"], 4), "unfused_ms": round(res["unfused"], 4),
+        "fused_tflops": round(flops / res["fused"] / 1e9, 1),
+        "weights_gb": round(HIDDEN * LM_VOCAB / 1e9, 3),
+        "identical": bool(torch.equal(a_f, a_u) and torch.equal(o_f, o_u)),
+        "steps": args.steps, "warmup": args.warmup}))
+
+
 def main():
     args = parse()
     if args.copy_calibration:
         copy_calibration()
+        return
+    if args.lm_head:
+        lm_head_bench(args)
         return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (got --gpus {args.gpus}); the verify step is "

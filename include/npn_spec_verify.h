@@ -158,6 +158,17 @@ size_t npn_fp8_matmul_workspace_size(int M, int K, int N);
 int npn_fp8_matmul(const uint16_t* x, const int8_t* w, const float* scale, uint16_t* out, int M,
                    int K, int N, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Row argmax of npn_fp8_matmul's output without writing it (an LM head's greedy decision,
+ * the reference takes logits.argmax(-1) of the bf16 LM-head output,
+ * contrib/qwen3.6-27b/static_decode.py:546, :1313). New op torch.ops.fp8.matmul_argmax.
+ * Writes parts [M][G] of {float value; int32 column}: per row and column group, the largest
+ * bf16((x . w) * scale) value and its column (NaN counts as the maximum; ties go to the lower
+ * column), G = npn_fp8_matmul_argmax_groups(M, K, N). npn_argmax_parts reduces them to ids,
+ * npn_accept_greedy_parts to a greedy acceptance. Shape rules as npn_fp8_matmul. */
+int npn_fp8_matmul_argmax_groups(int M, int K, int N);
+int npn_fp8_matmul_argmax(const uint16_t* x, const int8_t* w, const float* scale, void* parts,
+                          int M, int K, int N, void* stream);
+
 /* Split-K factor S of the GEMM plan for these sizes (1: no split; 0: unsupported sizes). */
 int npn_fp8_matmul_split_k(int M, int K, int N);
 
@@ -204,6 +215,18 @@ int npn_accept_rejection(const float* target_logits, const float* draft_logits,
                          const float* u_sample, float inv_temperature, int32_t* accepted,
                          int64_t* out_ids, int B, int K, int V, void* workspace,
                          size_t workspace_bytes, void* stream);
+
+/* ids [M] int64 (and values [M] f32 if non-NULL) = the best of each row's nparts partials,
+ * in column order, under the same rule. */
+int npn_argmax_parts(const void* parts, int nparts, int64_t* ids, float* values, int M,
+                     void* stream);
+
+/* torch.ops.spec.accept_greedy_fused -- new op: npn_accept_greedy with the target argmax taken
+ * from npn_fp8_matmul_argmax partials of the LM head over the B*(K+1) verify rows (row
+ * b*(K+1) + t), so no logits are written or read. Same outputs and rules as npn_accept_greedy;
+ * K + 1 <= 16. */
+int npn_accept_greedy_parts(const void* parts, int nparts, const int64_t* draft_ids,
+                            int32_t* accepted, int64_t* out_ids, int B, int K, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Inter-layer glue of the verify step (the decode loop of

@@ -32,6 +32,38 @@ typedef float f32x4 __attribute__((__vector_size__(4 * sizeof(float))));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2 __attribute__((__vector_size__(2 * sizeof(__bf16))));
 
+// Row argmax over the GEMM's bf16 outputs (the LM head's greedy decision without writing the
+// logits): per (row, column group) the largest bf16(acc * scale) and its column, NaN counting
+// as the maximum and ties going to the lower column (torch.argmax). Same 8-byte layout as the
+// acceptance kernels' per-chunk partials, which reduce and consume it.
+struct ArgPart {
+  float v;
+  int i;
+};
+
+__device__ __forceinline__ bool arg_beats(float bv, int bi, float av, int ai) {
+  const bool an = isnan(av), bn = isnan(bv);
+  if (an || bn) return bn && (!an || bi < ai);
+  return bv > av || (bv == av && bi < ai);
+}
+
+// (v, i) of the best of the 16 lanes of this lane's 16-lane group, in every lane of it.
+__device__ __forceinline__ void arg_merge16(float& v, int& i) {
+#pragma unroll
+  for (int off = 8; off > 0; off >>= 1) {
+    const float ov = __shfl_xor(v, off, 64);
+    const int oi = __shfl_xor(i, off, 64);
+    if (arg_beats(ov, oi, v, i)) {
+      v = ov;
+      i = oi;
+    }
+  }
+}
+
+__device__ __forceinline__ float bf16_round(float x) {
+  return npn::bf16_to_f32(npn::f32_to_bf16(x));
+}
+
 // Bytes 0-1 (HI = false) or 2-3 (HI = true) of w -> two bf16 (OCP e4m3fn decode, scale 1).
 template <bool HI>
 __device__ __forceinline__ uint32_t fp8x2_to_bf16x2(uint32_t w) {
@@ -72,6 +104,7 @@ struct GemmArgs {
   uint16_t* out;     // used when split_k == 1 and !to_partial
   float* partial;    // [split_k][M][N] fp32, unscaled, when split_k > 1 or to_partial
   int M, K, N, split_k, to_partial;
+  ArgPart* amax;     // row argmax partials [M][N / NW] instead of out (split_k == 1)
 };
 
 template <int MT>
@@ -147,6 +180,30 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemm_kernel(GemmArgs a) {
   if (w != 0) return;
 
   // Wave 0 holds the tile sum: lane (i, G) has rows 16mt + 4G + r, columns n0 + 4i + ct.
+  if (a.amax != nullptr) {
+    float sc[4];
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) sc[ct] = a.scale[n0 + 4 * i + ct];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float bv = -__builtin_inff();
+        int bi = 0x7FFFFFFF;
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct) {
+          const float v = bf16_round(acc[mt][ct][r] * sc[ct]);
+          if (arg_beats(v, n0 + 4 * i + ct, bv, bi)) {
+            bv = v;
+            bi = n0 + 4 * i + ct;
+          }
+        }
+        arg_merge16(bv, bi);
+        const int m = m_base + 16 * mt + 4 * G + r;
+        if (i == 0 && m < a.M) a.amax[(size_t)m * gridDim.x + blockIdx.x] = ArgPart{bv, bi};
+      }
+    return;
+  }
   if (a.split_k == 1 && !a.to_partial) {
     float sc[4];
 #pragma unroll
@@ -213,6 +270,7 @@ struct WideArgs {
   uint16_t* out;
   float* partial;  // [split_k][M][N] fp32, unscaled, when split_k > 1 or to_partial
   int M, K, N, units, groups, split_k, to_partial;
+  ArgPart* amax;   // row argmax partials [M][groups] instead of out (split_k == 1)
 };
 
 typedef int i32x2 __attribute__((ext_vector_type(2)));
@@ -354,6 +412,63 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void fp8_gemm_wide_kernel(WideArgs
   }
 
   // Epilogue: lane (i, G) holds rows 64wr + 16mt + 4G + r, column n0 + 16(NH wc + nt) + i.
+  if (a.amax != nullptr) {
+    float bv[4][4];
+    int bi[4][4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        bv[mt][r] = -__builtin_inff();
+        bi[mt][r] = 0x7FFFFFFF;
+      }
+#pragma unroll
+    for (int nt = 0; nt < NH; ++nt) {
+      const int unit = NH * wc + nt;
+      if (unit >= nu) continue;
+      const int col = n0 + 16 * unit + i;
+      const float sc = a.scale[col];
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float v = bf16_round(acc[mt][nt][r] * sc);
+          if (arg_beats(v, col, bv[mt][r], bi[mt][r])) {
+            bv[mt][r] = v;
+            bi[mt][r] = col;
+          }
+        }
+    }
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) arg_merge16(bv[mt][r], bi[mt][r]);
+    // The column half wc = 1 hands its per-row bests to wc = 0 through LDS (the stages are
+    // free once every wave has passed this barrier).
+    __syncthreads();
+    ArgPart* sh = reinterpret_cast<ArgPart*>(smem);
+    if (wc == 1 && i == 0) {
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sh[64 * wr + 16 * mt + 4 * G + r] = ArgPart{bv[mt][r], bi[mt][r]};
+    }
+    __syncthreads();
+    if (wc == 0 && i == 0) {
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = 64 * wr + 16 * mt + 4 * G + r;
+          ArgPart best{bv[mt][r], bi[mt][r]};
+          const ArgPart o = sh[row];
+          if (arg_beats(o.v, o.i, best.v, best.i)) best = o;
+          const int m = m_base + row;
+          if (m < a.M) a.amax[(size_t)m * a.groups + grp] = best;
+        }
+    }
+    return;
+  }
 #pragma unroll
   for (int nt = 0; nt < NH; ++nt) {
     const int unit = NH * wc + nt;
@@ -407,12 +522,14 @@ constexpr int kWideNH[] = {1, 2, 3, 4, 5, 6};
 //             one split-K buffer stays under 48 MB, plus the reduction's launch.
 // For each s the smallest ntm whose group count ceil(units / (2 ntm)) fits in 256 / s
 // workgroups is taken: fewest padded tiles, and every workgroup's tiles nearly all real.
-bool plan_wide(int M, int K, int N, GemmPlan& p) {
+// Wider N (an LM head's vocabulary) runs in rounds of 256 workgroups of the widest tiles,
+// without split-K. `no_split` (the argmax epilogue, which needs whole sums) keeps s = 1.
+bool plan_wide(int M, int K, int N, GemmPlan& p, bool no_split) {
   if (M <= 64 || K % KC != 0 || N % 16 != 0) return false;
   const int units = N / 16;
   const int passes = (M + 255) / 256;
   double best = 1e30;
-  for (int s = 1; s <= 8; s *= 2) {
+  for (int s = 1; s <= (no_split ? 1 : 8); s *= 2) {
     if (K / KC < 2 * s) break;
     const double part_bytes = (double)s * M * N * 4;
     if (s > 1 && part_bytes > 48e6) break;
@@ -422,12 +539,17 @@ bool plan_wide(int M, int K, int N, GemmPlan& p) {
       const int g = (units + 2 * v - 1) / (2 * v);
       if (g <= gmax) { ntm = v; groups = g; break; }
     }
-    if (ntm == 0) continue;
+    if (ntm == 0) {
+      if (s > 1) continue;
+      ntm = kWideNH[sizeof(kWideNH) / sizeof(kWideNH[0]) - 1];
+      groups = (units + 2 * ntm - 1) / (2 * ntm);
+    }
+    const int rounds = (groups * s + WIDE_WG - 1) / WIDE_WG;
     const double kk = (double)K / s;
     const double t_x = kk * 512.0 / 51e9;
     const double t_mfma = 2.0 * ntm * 16 * 256 * 2 * kk / (2.07e15 / WIDE_WG);
     const double t_part = s > 1 ? 2.0 * part_bytes / 4.5e12 + 3e-6 : 0.0;
-    const double t = (t_x + t_mfma) * passes + t_part;
+    const double t = (t_x + t_mfma) * passes * rounds + t_part;
     if (t < best * 0.97) {
       best = t;
       p.wide = true;
@@ -443,9 +565,9 @@ bool plan_wide(int M, int K, int N, GemmPlan& p) {
   return true;
 }
 
-GemmPlan plan(int M, int K, int N) {
+GemmPlan plan(int M, int K, int N, bool no_split = false) {
   GemmPlan p{};
-  if (plan_wide(M, K, N, p)) return p;
+  if (plan_wide(M, K, N, p, no_split)) return p;
   p = GemmPlan{};
   const int mtiles = (M + 15) / 16;
   p.mt = mtiles >= 8 ? 8 : (mtiles >= 4 ? 4 : (mtiles >= 2 ? 2 : 1));
@@ -453,7 +575,8 @@ GemmPlan plan(int M, int K, int N) {
   const int tiles = (N / NW) * p.passes;
   const int nks = K / KSTEP;
   p.split_k = 1;
-  while (tiles * p.split_k < 256 && p.split_k < 4 && nks >= 2 * p.split_k * 2 * WAVES)
+  while (!no_split && tiles * p.split_k < 256 && p.split_k < 4 &&
+         nks >= 2 * p.split_k * 2 * WAVES)
     p.split_k *= 2;
   p.ws = p.split_k > 1 ? (size_t)p.split_k * M * N * sizeof(float) : 0;
   return p;
@@ -468,10 +591,10 @@ bool shape_ok(int M, int K, int N) {
 // [split_k][M][N] to `partial` and, when `reduce`, the fixed-order reduction into `out`.
 int launch_gemm(const GemmPlan& p, const uint16_t* x, const int8_t* w, const float* scale,
                 uint16_t* out, float* partial, int M, int K, int N, int to_partial, bool reduce,
-                hipStream_t s) {
+                hipStream_t s, ArgPart* amax = nullptr) {
   if (p.wide) {
     WideArgs wa{x, reinterpret_cast<const uint8_t*>(w), scale, out, partial, M, K, N,
-                p.units, p.groups, p.split_k, to_partial};
+                p.units, p.groups, p.split_k, to_partial, amax};
     const int nwg = ((p.groups * p.split_k + 7) / 8) * 8;  // multiple of 8 for the XCD map
     const dim3 grid(nwg, p.passes);
     const dim3 block(WIDE_THREADS);
@@ -485,7 +608,7 @@ int launch_gemm(const GemmPlan& p, const uint16_t* x, const int8_t* w, const flo
     }
   } else {
     GemmArgs ga{x, reinterpret_cast<const uint8_t*>(w), scale, out, partial, M, K, N, p.split_k,
-                to_partial};
+                to_partial, amax};
     const dim3 grid(N / NW, p.split_k, p.passes);
     switch (p.mt) {
       case 1: hipLaunchKernelGGL(fp8_gemm_kernel<1>, grid, dim3(WAVES * 64), 0, s, ga); break;
@@ -538,4 +661,22 @@ extern "C" int npn_fp8_matmul_partials(const uint16_t* x, const int8_t* w, float
   // Neither kernel reads the scale or writes `out` when it writes partials.
   return launch_gemm(p, x, w, nullptr, nullptr, partial, M, K, N, 1, false,
                      static_cast<hipStream_t>(stream));
+}
+
+// Row argmax of out = bf16((x . w) * scale) without writing out: partials per (row, column
+// group) for the acceptance kernels to reduce.
+extern "C" int npn_fp8_matmul_argmax_groups(int M, int K, int N) {
+  if (!shape_ok(M, K, N)) return 0;
+  const GemmPlan p = plan(M, K, N, true);
+  return p.wide ? p.groups : N / NW;
+}
+
+extern "C" int npn_fp8_matmul_argmax(const uint16_t* x, const int8_t* w, const float* scale,
+                                     void* parts, int M, int K, int N, void* stream) {
+  NPN_REQUIRE(x && w && scale && parts, NPN_ERR_NULL);
+  NPN_REQUIRE(shape_ok(M, K, N), NPN_ERR_SHAPE);
+  NPN_REQUIRE(NPN_ALIGNED16(x) && NPN_ALIGNED16(w) && NPN_ALIGNED16(parts), NPN_ERR_ALIGN);
+  const GemmPlan p = plan(M, K, N, true);
+  return launch_gemm(p, x, w, scale, nullptr, nullptr, M, K, N, 0, false,
+                     static_cast<hipStream_t>(stream), static_cast<ArgPart*>(parts));
 }

@@ -216,6 +216,62 @@ __global__ void greedy_accept_kernel(const ArgPart* __restrict__ part,
   accepted[b] = a;
 }
 
+// Best of one row's nparts partials, in every lane of the calling wave: lanes take the
+// partials lane, lane + 64, ... (each lane keeps its first best), then a shuffle tree. The
+// rule (NaN max, lower index on ties) is order-independent, so this equals a serial scan.
+__device__ __forceinline__ ArgPart wave_best(const ArgPart* __restrict__ row, int nparts) {
+  const int lane = threadIdx.x & 63;
+  float bv = -INFINITY;
+  int bi = 0x7FFFFFFF;
+  for (int c = lane; c < nparts; c += 64) {
+    const ArgPart p = row[c];
+    if (beats(p.v, p.i, bv, bi)) { bv = p.v; bi = p.i; }
+  }
+  for (int off = 32; off > 0; off >>= 1) {
+    const float ov = __shfl_xor(bv, off, 64);
+    const int oi = __shfl_xor(bi, off, 64);
+    if (beats(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+  }
+  return ArgPart{bv, bi};
+}
+
+// Row argmax from per-row partials [M][nparts]: one wave per row.
+__global__ __launch_bounds__(256) void argmax_parts_kernel(const ArgPart* __restrict__ part,
+                                                           int nparts, int64_t* __restrict__ ids,
+                                                           float* __restrict__ values, int M) {
+  const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (m >= M) return;
+  const ArgPart best = wave_best(part + (size_t)m * nparts, nparts);
+  if ((threadIdx.x & 63) == 0) {
+    ids[m] = best.i;
+    if (values != nullptr) values[m] = best.v;
+  }
+}
+
+// Greedy acceptance from per-row partials: one workgroup per sequence, wave t reduces row
+// (b, t); then one lane applies the acceptance rule of greedy_accept_kernel.
+__global__ __launch_bounds__(1024) void greedy_accept_parts_kernel(
+    const ArgPart* __restrict__ part, int nparts, const int64_t* __restrict__ draft_ids,
+    int32_t* __restrict__ accepted, int64_t* __restrict__ out_ids, int K) {
+  const int b = blockIdx.x, T = K + 1;
+  const int w = threadIdx.x >> 6;
+  __shared__ int best_id[16];
+  const ArgPart best = wave_best(part + ((size_t)b * T + w) * nparts, nparts);
+  if ((threadIdx.x & 63) == 0) best_id[w] = best.i;
+  __syncthreads();
+  if (threadIdx.x != 0) return;
+  int a = K;
+  bool stopped = false;
+  for (int t = 0; t < T; ++t) {
+    out_ids[(size_t)b * T + t] = stopped ? -1 : best_id[t];
+    if (!stopped && t < K && draft_ids[(size_t)b * K + t] != (int64_t)best_id[t]) {
+      a = t;
+      stopped = true;
+    }
+  }
+  accepted[b] = a;
+}
+
 // ---- rejection sampling ------------------------------------------------------------------
 struct RejArgs {
   const float* target;   // [B][K+1][V]
@@ -628,5 +684,26 @@ extern "C" int npn_accept_rejection(const float* target_logits, const float* dra
   hipLaunchKernelGGL(rej_decide_kernel, dim3(B), dim3(THREADS), 0, s, a);
   hipLaunchKernelGGL(rej_mass_kernel, dim3(a.nchm, B), dim3(THREADS), 0, s, a);
   hipLaunchKernelGGL(rej_pick_kernel, dim3(B), dim3(THREADS), 0, s, a);
+  return npn_launch_status();
+}
+
+extern "C" int npn_accept_greedy_parts(const void* parts, int nparts, const int64_t* draft_ids,
+                                       int32_t* accepted, int64_t* out_ids, int B, int K,
+                                       void* stream) {
+  NPN_REQUIRE(parts && draft_ids && accepted && out_ids, NPN_ERR_NULL);
+  NPN_REQUIRE(B >= 1 && K >= 0 && K + 1 <= 16 && nparts >= 1, NPN_ERR_SHAPE);
+  hipLaunchKernelGGL(greedy_accept_parts_kernel, dim3(B), dim3(64 * (K + 1)), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const ArgPart*>(parts), nparts,
+                     draft_ids, accepted, out_ids, K);
+  return npn_launch_status();
+}
+
+extern "C" int npn_argmax_parts(const void* parts, int nparts, int64_t* ids, float* values,
+                                int M, void* stream) {
+  NPN_REQUIRE(parts && ids, NPN_ERR_NULL);
+  NPN_REQUIRE(M >= 1 && nparts >= 1, NPN_ERR_SHAPE);
+  hipLaunchKernelGGL(argmax_parts_kernel, dim3((M + 3) / 4), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const ArgPart*>(parts), nparts,
+                     ids, values, M);
   return npn_launch_status();
 }

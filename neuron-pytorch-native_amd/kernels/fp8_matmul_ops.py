@@ -76,6 +76,52 @@ def _(x, w_fp8_T_i8):
     return x.new_empty((split_k(M, K, N), M, N), dtype=torch.float32)
 
 
+def _check_gemm_args(x, w_fp8_T_i8):
+    M, K = x.shape
+    Kw, N = w_fp8_T_i8.shape
+    if Kw != K:
+        raise RuntimeError(f"x has K={K} but the weight has K={Kw}")
+    require(x, "x", torch.bfloat16, shape=(M, K))
+    if w_fp8_T_i8.dtype not in (torch.int8, torch.uint8, torch.float8_e4m3fn):
+        raise TypeError(f"w_fp8_T_i8 must hold fp8 bytes, got {w_fp8_T_i8.dtype}")
+    require(w_fp8_T_i8, "w_fp8_T_i8", w_fp8_T_i8.dtype, shape=(K, N))
+    return M, K, N
+
+
+def argmax_parts(x, w_fp8_T_i8, scale):
+    """Per-(row, column group) argmax partials of bf16((x . w) * scale), [M, G, 2] int32
+    (value bits, column), for npn_argmax_parts / npn_accept_greedy_parts."""
+    M, K, N = _check_gemm_args(x, w_fp8_T_i8)
+    require(scale, "scale", torch.float32, numel=N)
+    G = query("npn_fp8_matmul_argmax_groups", M, K, N)
+    if G == 0:
+        raise RuntimeError(f"unsupported fp8 matmul shape M={M} K={K} N={N}")
+    parts = torch.empty((M, G, 2), dtype=torch.int32, device=x.device)
+    call("npn_fp8_matmul_argmax", x, w_fp8_T_i8, scale, parts, M, K, N, stream_of(x))
+    return parts
+
+
+@torch.library.custom_op("fp8::matmul_argmax", mutates_args=(), device_types="cuda")
+def fp8_matmul_argmax(x: torch.Tensor, w_fp8_T_i8: torch.Tensor,
+                      scale: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """New op: (values f32 [M], ids int64 [M]) = max and argmax over each row of
+    fp8::matmul(x, w, scale) (bf16 values; NaN is the maximum; ties to the lower column),
+    without writing the [M, N] output -- the LM head's greedy decision
+    (contrib/qwen3.6-27b/static_decode.py:546, :1313)."""
+    parts = argmax_parts(x, w_fp8_T_i8, scale)
+    M, G = parts.shape[0], parts.shape[1]
+    ids = torch.empty(M, dtype=torch.int64, device=x.device)
+    values = torch.empty(M, dtype=torch.float32, device=x.device)
+    call("npn_argmax_parts", parts, G, ids, values, M, stream_of(x))
+    return values, ids
+
+
+@fp8_matmul_argmax.register_fake
+def _(x, w_fp8_T_i8, scale):
+    M = x.shape[0]
+    return x.new_empty((M,), dtype=torch.float32), x.new_empty((M,), dtype=torch.int64)
+
+
 def fp8_linear(x, w_fp8_T_i8, scale):
     """x [..., K] bf16 -> [..., N], as the reference's fp8_linear
     (contrib/qwen3.6-27b/static_decode.py:307-319)."""

@@ -93,3 +93,31 @@ def commit_(accepted: torch.Tensor, prev_accepted: torch.Tensor, kv_len: torch.T
 @commit_.register_fake
 def _(accepted, prev_accepted, kv_len, committed):
     return None
+
+
+@torch.library.custom_op("spec::accept_greedy_fused", mutates_args=(), device_types="cuda")
+def accept_greedy_fused(hidden: torch.Tensor, lm_head_w: torch.Tensor, lm_head_scale: torch.Tensor,
+                        draft_ids: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """New op: greedy acceptance straight from the LM head: hidden [B*(K+1), H] bf16 (the
+    final-normed verify rows, row b*(K+1) + t), lm_head_w [H, V] fp8 bytes, lm_head_scale
+    [V] f32, draft_ids [B, K] int64 -> (accepted [B] int32, out_ids [B, K+1] int64), the
+    same as accept_greedy(fp8::matmul(hidden, w, scale).float().view(B, K+1, V), draft_ids)
+    but without writing or reading the logits."""
+    from fp8_matmul_ops import argmax_parts
+    B, K = draft_ids.shape
+    require(draft_ids, "draft_ids", torch.int64, shape=(B, K))
+    if hidden.shape[0] != B * (K + 1):
+        raise RuntimeError(f"hidden must have B*(K+1) = {B * (K + 1)} rows, got {hidden.shape[0]}")
+    parts = argmax_parts(hidden, lm_head_w, lm_head_scale)
+    accepted = torch.empty(B, dtype=torch.int32, device=hidden.device)
+    out_ids = torch.empty((B, K + 1), dtype=torch.int64, device=hidden.device)
+    call("npn_accept_greedy_parts", parts, parts.shape[1], draft_ids, accepted, out_ids, B, K,
+         stream_of(hidden))
+    return accepted, out_ids
+
+
+@accept_greedy_fused.register_fake
+def _(hidden, lm_head_w, lm_head_scale, draft_ids):
+    B, K = draft_ids.shape
+    return (hidden.new_empty((B,), dtype=torch.int32),
+            hidden.new_empty((B, K + 1), dtype=torch.int64))

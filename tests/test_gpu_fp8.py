@@ -3,12 +3,16 @@ with fp32 accumulation, at the verify-step shapes (M = B*T in {8, 64, 256}, K = 
 N in {5120, 17408, 34816}) on sampled columns, the reference's per-rank decode shapes
 (contrib/qwen3.6-27b/kernels/tests/test_fp8_matmul.py:217-236, seed 0), split-K, M
 not a multiple of 16, and the OCP-only codes 0x78..0x7E (256..448).
+The oracle's product is rounded to bf16 as the op's output is, so what remains is the
+accumulation order (fp32 MFMA sums vs fp64): the 2e-3 bar, and elementwise one bf16 ulp
+where that order flips a rounding.
 """
 import numpy as np
 import pytest
 import torch
 
 from oracle import fp8 as of
+from oracle.numerics import round_to_bf16
 from _util import BF16_U, assert_rel_close, bits, fp8_weights
 
 pytestmark = pytest.mark.gpu
@@ -27,7 +31,7 @@ def _check(ops, M, K, N, seed, cols=None, fp8_max=448.0):
         got = got[:, sel]
     else:
         ref = of.fp8_matmul(bits(x), w.numpy(), scale.numpy())
-    assert_rel_close(got, ref, out_unit=BF16_U, name=f"fp8 M={M} K={K} N={N}")
+    assert_rel_close(got, round_to_bf16(ref), out_unit=BF16_U, name=f"fp8 M={M} K={K} N={N}")
 
 
 @pytest.mark.parametrize("M", [1, 8, 13, 64, 100, 256])
@@ -55,11 +59,11 @@ def test_ocp_only_codes(ops):
     codes = np.random.default_rng(0).integers(0x78, 0x7F, size=(K, N)).astype(np.uint8)
     codes[::3] |= 0x80
     w = torch.from_numpy(codes.view(np.int8))
-    x = torch.randn(4, K).to(torch.bfloat16)
+    x = torch.randn(4, K, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16)
     scale = torch.full((N,), 1.0 / 448.0)
     got = ops.fp8.matmul(x.cuda(), w.cuda(), scale.reshape(N, 1).cuda()).float().cpu().numpy()
     ref = of.fp8_matmul(bits(x), codes, scale.numpy())
-    assert_rel_close(got, ref, out_unit=BF16_U, name="ocp codes")
+    assert_rel_close(got, round_to_bf16(ref), out_unit=BF16_U, name="ocp codes")
 
 
 def test_rejects_bad_shapes(ops):

@@ -22,7 +22,7 @@ def test_library_exports_every_declared_symbol():
     import npn_native
     lib = npn_native.lib()
     names = _declared()
-    assert len(names) >= 25
+    assert len(names) >= 29
     for n in names:
         assert hasattr(lib, n), f"{n} declared in the header but not exported"
     assert set(names) == set(npn_native.SIGNATURES)
@@ -100,6 +100,15 @@ def test_ops_register_and_propagate_shapes():
                                                         torch.empty(14336), 24, 4, 256)
         assert q.shape == gt.shape == (16, 24, 256) and k.shape == v.shape == (16, 4, 256)
         assert q.dtype == bf
+        vals, ids = torch.ops.fp8.matmul_argmax(torch.empty(256, 5120, dtype=bf),
+                                                torch.empty(5120, 248320, dtype=torch.int8),
+                                                torch.empty(248320))
+        assert vals.shape == ids.shape == (256,) and ids.dtype == torch.int64
+        acc, oid = torch.ops.spec.accept_greedy_fused(torch.empty(B * T, 5120, dtype=bf),
+                                                      torch.empty(5120, 4096, dtype=torch.int8),
+                                                      torch.empty(4096),
+                                                      torch.empty(B, T - 1, dtype=torch.int64))
+        assert acc.shape == (B,) and oid.shape == (B, T)
         c, sn = torch.ops.gqa.rope_rows(torch.empty(100, 64), torch.empty(100, 64),
                                         torch.empty(B, dtype=torch.int32), T)
         assert c.shape == sn.shape == (B, T, 64) and c.dtype == f32
@@ -114,6 +123,9 @@ def test_fp8_split_k_plan():
     assert query("npn_fp8_matmul_split_k", 256, 5120, 14336) == 2
     assert query("npn_fp8_matmul_split_k", 256, 5120, 34816) == 1
     assert query("npn_fp8_matmul_split_k", 256, 100, 5120) == 0
+    # argmax mode never splits K; the LM head's vocabulary runs in rounds of 12-unit groups
+    assert query("npn_fp8_matmul_argmax_groups", 256, 5120, 248320) == 1294
+    assert query("npn_fp8_matmul_argmax_groups", 16, 5120, 248320) == 248320 // 64
 
 
 def test_ops_refuse_cpu_tensors():

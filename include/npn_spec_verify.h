@@ -201,15 +201,19 @@ int npn_accept_greedy(const float* target_logits, const int64_t* draft_ids, int3
 /* torch.ops.spec.accept_rejection -- new op. Rejection sampling (Leviathan et
  * al. 2023, Alg. 1) under an integer softmax contract, so the result is
  * bit-identical to a CPU restatement for the same logits and uniforms:
- *   x_v = t_v*inv_temperature - max (fp32); E_v = floor(2^32 * exp_c(x_v)) with
- *   exp_c a fixed fp32 Cody-Waite + degree-7 Taylor evaluation without FMA;
- *   Z = sum E_v (exact); U = floor(u * 2^24).
+ *   x_v = t_v*inv_temperature - max (fp32); E_v = floor(2^31 * exp_c(x_v)) with
+ *   exp_c a fixed fp32 Cody-Waite + degree-7 Taylor evaluation in fused
+ *   multiply-adds; Z = sum E_v (exact); U = floor(u * 2^24).
  *   Accept draft x iff U * Eq_x * Zp <= 2^24 * Ep_x * Zq. At the first rejection
  *   sample from R_v = max(0, Ep_v*Zq - Eq_v*Zp) (bonus: R_v = Ep_v of row K):
  *   the smallest v with 2^24 * sum_{w<=v} R_w > U_s * sum_w R_w.
  *   target_logits [B, K+1, V] f32, draft_logits [B, K, V] f32, draft_ids [B, K]
  *   int64, u_accept [B, K] f32 in [0,1), u_sample [B] f32 in [0,1),
- *   inv_temperature > 0 (logits are multiplied by it). */
+ *   inv_temperature > 0 (logits are multiplied by it), V <= 2^20.
+ * On return the workspace starts with every row's Z (uint64 [R]) and, at byte
+ * offset 8R rounded up to a multiple of 256, every row's max scaled logit m
+ * (float [R]); R = B*(2K+1) rows: target row (b, i) at b*(K+1)+i, then draft
+ * row (b, i) at B*(K+1) + b*K + i. */
 int npn_accept_rejection(const float* target_logits, const float* draft_logits,
                          const int64_t* draft_ids, const float* u_accept,
                          const float* u_sample, float inv_temperature, int32_t* accepted,

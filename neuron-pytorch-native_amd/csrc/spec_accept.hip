@@ -7,9 +7,10 @@
 //
 // Rejection sampling (Leviathan et al. 2023, Alg. 1) under an integer softmax contract
 // that this file and its CPU restatement evaluate with identical IEEE-754 operations:
-//   s_v = t_v * inv_temp (fp32); m = max_v s_v; E_v = floor(2^32 * exp_c(s_v - m)) where
-//   exp_c is a Cody-Waite reduction + degree-7 Taylor polynomial evaluated with separately
-//   rounded fp32 multiplies and adds (this file is compiled with -ffp-contract=off);
+//   s_v = t_v * inv_temp (fp32); m = max_v s_v; E_v = floor(2^31 * exp_c(s_v - m)) where
+//   exp_c is a Cody-Waite reduction + degree-7 Taylor polynomial evaluated with explicit
+//   fp32 fused multiply-adds (this file is compiled with -ffp-contract=off, so no other
+//   multiply and add is fused);
 //   Z = sum_v E_v in 64-bit integers (exact, so the reduction order does not matter).
 //   Accept draft x at position i iff U * Eq_x * Zp <= 2^24 * Ep_x * Zq (128-bit integers,
 //   U = floor(u * 2^24)). At the first rejection sample from R_v = max(0, Ep_v Zq - Eq_v Zp),
@@ -18,9 +19,9 @@
 //
 // Kernels (each over B sequences, T = K+1 positions, vocabulary split into 8192-wide chunks):
 //   greedy:    argmax partials per (row, chunk) -> per-sequence merge + accept
-//   rejection: row max partials -> E sums per (row, chunk) and E at the draft token ->
-//              per-sequence decision -> residual/bonus mass per (sequence, chunk) ->
-//              per-sequence inverse-CDF pick
+//   rejection: row max partials -> E sums per (row, chunk) added into each row's Z, and
+//              E at the draft token -> per-sequence decision -> residual/bonus mass per
+//              (sequence, chunk) -> per-sequence inverse-CDF pick
 #include "npn_common.h"
 
 namespace {
@@ -30,6 +31,7 @@ constexpr int THREADS = 256;   // CHK / THREADS = 32 entries per thread
 constexpr int PER_T = CHK / THREADS;
 constexpr int MCHK = 2048;     // entries per chunk of the residual mass / inverse-CDF pass
 constexpr int PER_M = MCHK / THREADS;  // 8 consecutive entries per thread
+constexpr int kRejMaxV = 1 << 20;  // largest vocabulary of the rejection path
 
 typedef unsigned __int128 u128;
 
@@ -37,34 +39,36 @@ typedef unsigned __int128 u128;
 constexpr float kL2E = 0x1.715476p+0f;        // log2(e) in fp32
 constexpr float kLn2Hi = 0x1.62ep-1f;         // ln2, low 12 mantissa bits cleared
 constexpr float kLn2Lo = 0x1.0bfbe8p-15f;     // ln2 - kLn2Hi in fp32
-constexpr float kC7 = 0x1.a01a02p-13f;        // 1/7!
-constexpr float kC6 = 0x1.6c16c2p-10f;        // 1/6!
-constexpr float kC5 = 0x1.111112p-7f;         // 1/5!
-constexpr float kC4 = 0x1.555556p-5f;         // 1/4!
-constexpr float kC3 = 0x1.555556p-3f;         // 1/3!
-constexpr float kXMin = -32.0f;               // below: 2^32 exp(x) < 1
+constexpr float kMagic = 0x1.8p+23f;          // 1.5 * 2^23: fma(x, kL2E, kMagic) rounds to an integer
+// Taylor coefficients 1/k! in fp32, scaled by 2^31 (exact), k = 7..0
+constexpr float kP7 = 0x1.a01a02p+18f;
+constexpr float kP6 = 0x1.6c16c2p+21f;
+constexpr float kP5 = 0x1.111112p+24f;
+constexpr float kP4 = 0x1.555556p+26f;
+constexpr float kP3 = 0x1.555556p+28f;
+constexpr float kP2 = 0x1p+30f;
+constexpr float kP1 = 0x1p+31f;               // 2^31 / 1! and 2^31 / 0!
+constexpr float kXMin = -32.0f;               // at and below: 2^31 exp(x) < 1
 
-__device__ __forceinline__ uint64_t expfix(float x) {
-#pragma clang fp contract(off)
-  if (!(x > kXMin)) return 0;
-  const float kf = floorf(x * kL2E + 0.5f);
-  float r = x - kf * kLn2Hi;
-  r = r - kf * kLn2Lo;
-  float p = kC7;
-  p = p * r + kC6;
-  p = p * r + kC5;
-  p = p * r + kC4;
-  p = p * r + kC3;
-  p = p * r + 0.5f;
-  p = p * r + 1.0f;
-  p = p * r + 1.0f;
-  const uint32_t bits = __float_as_uint(p);
-  const int e = (int)((bits >> 23) & 0xFFu);
-  const uint64_t m = (uint64_t)((bits & 0x7FFFFFu) | 0x800000u);
-  const int shift = e + (int)kf - 118;
-  if (shift >= 0) return m << shift;
-  const int rs = -shift;
-  return rs >= 64 ? 0 : (m >> rs);
+// E = floor(2^31 * exp_c(x)) for x <= 0 (NaN and x <= -32 give 0; E(0) = 2^31).
+// kf = t - kMagic is round(x * log2 e) as an exact fp32 integer, and t's bit pattern holds
+// kf in its low bits, so adding (bits(t) << 23) to p's pattern multiplies p by 2^kf exactly
+// (the exponent stays in the normal range: p >= 2^30 and kf >= -47). The conversion to
+// uint32 truncates, which is the floor of a value in [0, 2^31].
+__device__ __forceinline__ uint32_t expfix(float x) {
+  x = fmaxf(x, kXMin);
+  const float t = __builtin_fmaf(x, kL2E, kMagic);
+  const float kf = t - kMagic;
+  float r = __builtin_fmaf(-kf, kLn2Hi, x);
+  r = __builtin_fmaf(-kf, kLn2Lo, r);
+  float p = __builtin_fmaf(kP7, r, kP6);
+  p = __builtin_fmaf(p, r, kP5);
+  p = __builtin_fmaf(p, r, kP4);
+  p = __builtin_fmaf(p, r, kP3);
+  p = __builtin_fmaf(p, r, kP2);
+  p = __builtin_fmaf(p, r, kP1);
+  p = __builtin_fmaf(p, r, kP1);
+  return (uint32_t)__uint_as_float(__float_as_uint(p) + (__float_as_uint(t) << 23));
 }
 
 __device__ __forceinline__ float scaled(float v, float inv_temp) {
@@ -129,7 +133,20 @@ __device__ float block_max(float v, float* sh) {
 // sums, or the total order of the argmax), so the assignment does not affect results.
 template <typename F>
 __device__ __forceinline__ void visit_chunk(const float* src, int v0, int V, bool vec4, F f) {
-  if (vec4) {
+  if (vec4 && v0 + CHK <= V) {  // whole chunk in the row: all loads first, no guards
+    float4 x[PER_T / 4];
+#pragma unroll
+    for (int j = 0; j < PER_T / 4; ++j)
+      x[j] = *reinterpret_cast<const float4*>(src + v0 + 4 * (j * THREADS + (int)threadIdx.x));
+#pragma unroll
+    for (int j = 0; j < PER_T / 4; ++j) {
+      const int v = v0 + 4 * (j * THREADS + (int)threadIdx.x);
+      f(v, x[j].x);
+      f(v + 1, x[j].y);
+      f(v + 2, x[j].z);
+      f(v + 3, x[j].w);
+    }
+  } else if (vec4) {
 #pragma unroll
     for (int j = 0; j < PER_T / 4; ++j) {
       const int v = v0 + 4 * (j * THREADS + (int)threadIdx.x);
@@ -284,10 +301,11 @@ struct RejArgs {
   int64_t* out_ids;
   int B, K, V, nch, nchm;  // chunks of CHK (logit passes) and of MCHK (mass / pick)
   bool vec4;          // logit rows 16-byte aligned and V % 4 == 0
-  // workspace
-  float* rmax;        // [rows][nch]   rows = B*(K+1) target rows, then B*K draft rows
-  uint64_t* zsum;     // [rows][nch]
-  uint64_t* ex;       // [rows]        E at the row's draft token (target/draft rows i < K)
+  // workspace (rows = B*(K+1) target rows, then B*K draft rows)
+  uint64_t* zrow;     // [rows]        Z of each row (chunk sums added atomically)
+  float* mrow;        // [rows]        max scaled logit of each row
+  uint32_t* ex;       // [rows]        E at the row's draft token (target/draft rows i < K)
+  float* rmax;        // [rows][nch]   chunk maxima
   int32_t* dec_row;   // [B]           sampling row index (target row; draft row or -1)
   uint64_t* dec_z;    // [B][2]        Zp, Zq of the sampling rows
   float* dec_m;       // [B][2]        row maxima of the sampling rows (scaled logits)
@@ -316,15 +334,18 @@ __device__ __forceinline__ int row_token(const RejArgs& a, int row) {
   return (int)x;
 }
 
-__global__ __launch_bounds__(THREADS) void rej_max_kernel(RejArgs a) {
-  const int row = blockIdx.y, c = blockIdx.x;
+// Chunk c of a row: its max scaled logit into the row's chunk maxima (and, from chunk 0,
+// a zero into the row's Z, which the sum pass adds into in a later launch).
+__device__ __forceinline__ void max_chunk(const RejArgs& a, int row, int c, float* sh) {
   const float* src = row_ptr(a, row);
   const int v0 = c * CHK;
   float m = -INFINITY;
   visit_chunk(src, v0, a.V, a.vec4, [&](int, float x) { m = fmaxf(m, scaled(x, a.inv_temp)); });
-  __shared__ float sh[THREADS / 64];
   m = block_max(m, sh);
-  if (threadIdx.x == 0) a.rmax[(size_t)row * a.nch + c] = m;
+  if (threadIdx.x == 0) {
+    a.rmax[(size_t)row * a.nch + c] = m;
+    if (c == 0) a.zrow[row] = 0;
+  }
 }
 
 __device__ __forceinline__ float row_max(const RejArgs& a, int row) {
@@ -333,79 +354,71 @@ __device__ __forceinline__ float row_max(const RejArgs& a, int row) {
   return m;
 }
 
-__global__ __launch_bounds__(THREADS) void rej_sum_kernel(RejArgs a) {
-  const int row = blockIdx.y, c = blockIdx.x;
+// Chunk c of a row: its E sum added into the row's Z (exact 64-bit atomics, so the order of
+// the chunks does not matter), the row max from chunk 0 and E at the draft token from the
+// chunk that holds it. kUnitTemp skips the multiply by inv_temp == 1 (x * 1 == x, NaN
+// stays NaN).
+template <bool kUnitTemp>
+__device__ __forceinline__ void sum_chunk(const RejArgs& a, int row, int c, uint64_t* sh) {
   const float* src = row_ptr(a, row);
   const float m = row_max(a, row);
+  const float it = a.inv_temp;
   const int v0 = c * CHK;
   uint64_t z = 0;
   visit_chunk(src, v0, a.V, a.vec4,
-              [&](int, float x) { z += expfix(scaled(x, a.inv_temp) - m); });
-  __shared__ uint64_t sh[THREADS / 64];
+              [&](int, float x) { z += expfix((kUnitTemp ? x : scaled(x, it)) - m); });
   z = block_sum_u64(z, sh);
   if (threadIdx.x == 0) {
-    a.zsum[(size_t)row * a.nch + c] = z;
+    atomicAdd(reinterpret_cast<unsigned long long*>(a.zrow + row), (unsigned long long)z);
+    if (c == 0) a.mrow[row] = m;
     const int x = row_token(a, row);
-    if (x >= v0 && x < v0 + CHK) a.ex[row] = expfix(scaled(src[x], a.inv_temp) - m);
+    if (x >= v0 && x < v0 + CHK) a.ex[row] = expfix(scaled(src[x], it) - m);
   }
 }
 
-// One workgroup per sequence: the Z sums of its 2K+1 rows (chunk partials added in LDS with
-// exact 64-bit atomics, so the order does not matter), the K accept tests, then which rows
-// to sample from, with their Z sums and maxima for the mass and pick kernels.
-__global__ __launch_bounds__(THREADS) void rej_decide_kernel(RejArgs a) {
-  const int b = blockIdx.x;
+// The logit passes: chunk maxima of every row, then E sums. The sum pass runs its rows and
+// chunks last-first, the reverse of the max pass's dispatch order, so the first chunks it
+// re-reads are the ones read last.
+__global__ __launch_bounds__(THREADS) void rej_max_kernel(RejArgs a) {
+  __shared__ float sh[THREADS / 64];
+  max_chunk(a, (int)blockIdx.y, (int)blockIdx.x, sh);
+}
+
+template <bool kUnitTemp>
+__global__ __launch_bounds__(THREADS) void rej_sum_kernel(RejArgs a) {
+  __shared__ uint64_t sh[THREADS / 64];
+  sum_chunk<kUnitTemp>(a, (int)(gridDim.y - 1 - blockIdx.y), (int)(gridDim.x - 1 - blockIdx.x),
+                       sh);
+}
+
+// One wave per sequence: lane i < K runs the accept test of draft position i (all tests at
+// once; the first failing lane is the rejection), then lane 0 records which rows to sample
+// from, with their Z sums and maxima for the mass and pick kernels.
+__global__ __launch_bounds__(64) void rej_decide_kernel(RejArgs a) {
+  const int b = blockIdx.x, i = threadIdx.x;
   const int K = a.K, T = K + 1;
   const int nt = a.B * T;
-  const int nrows = 2 * K + 1;  // local row r: target row r (r <= K), draft row r - T
-  __shared__ unsigned long long zs[2 * 64 + 1];
-  __shared__ int s_acc;
-  __shared__ float shm[THREADS / 64];
-  for (int r = threadIdx.x; r < nrows; r += THREADS) zs[r] = 0;
-  __syncthreads();
-  for (int p = threadIdx.x; p < nrows * a.nch; p += THREADS) {
-    const int r = p / a.nch, c = p - r * a.nch;
-    const int row = r <= K ? b * T + r : nt + b * K + (r - T);
-    atomicAdd(&zs[r], (unsigned long long)a.zsum[(size_t)row * a.nch + c]);
+  bool reject = false;
+  if (i < K) {
+    const int rt = b * T + i, rd = nt + b * K + i;
+    const uint64_t ueq = (uint64_t)uniform_fix(a.u_accept[(size_t)b * K + i]) * a.ex[rd];
+    const u128 lhs = (u128)ueq * a.zrow[rt];                   // < 2^24 * 2^31 * 2^51
+    const u128 rhs = ((u128)a.ex[rt] * a.zrow[rd]) << 24;
+    reject = lhs > rhs;
   }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    int acc = K;
-    uint64_t zp_s = 0, zq_s = 0;
-    for (int i = 0; i < K; ++i) {
-      const int rt = b * T + i, rd = nt + b * K + i;
-      const uint64_t zp = zs[i], zq = zs[T + i];
-      const uint64_t ep = a.ex[rt], eq = a.ex[rd];
-      const u128 lhs = (u128)uniform_fix(a.u_accept[(size_t)b * K + i]) * eq * zp;
-      const u128 rhs = ((u128)ep * zq) << 24;
-      if (lhs > rhs) {
-        acc = i;
-        zp_s = zp;
-        zq_s = zq;
-        break;
-      }
-    }
-    if (acc == K) zp_s = zs[K];
+  const uint64_t rej = __builtin_amdgcn_ballot_w64(reject);
+  const int acc = rej ? __builtin_ctzll(rej) : K;
+  if (i == 0) {
     a.accepted[b] = acc;
     a.dec_row[b] = acc;
-    a.dec_z[2 * b] = zp_s;
-    a.dec_z[2 * b + 1] = zq_s;
-    for (int t = 0; t < T; ++t) {
-      if (t < acc) a.out_ids[(size_t)b * T + t] = a.draft_ids[(size_t)b * K + t];
-      else if (t > acc) a.out_ids[(size_t)b * T + t] = -1;
-    }
-    s_acc = acc;
+    a.dec_z[2 * b] = a.zrow[b * T + acc];
+    a.dec_z[2 * b + 1] = acc < K ? a.zrow[nt + b * K + acc] : 0;
+    a.dec_m[2 * b] = a.mrow[b * T + acc];  // maxima of the sampling rows
+    a.dec_m[2 * b + 1] = acc < K ? a.mrow[nt + b * K + acc] : 0.f;
   }
-  __syncthreads();
-  const int acc = s_acc;
-  // maxima of the sampling rows (the draft row only after a rejection)
-  const int rows[2] = {b * T + acc, nt + b * K + acc};
-  for (int k = 0; k < (acc < K ? 2 : 1); ++k) {
-    float m = -INFINITY;
-    for (int c = threadIdx.x; c < a.nch; c += THREADS)
-      m = fmaxf(m, a.rmax[(size_t)rows[k] * a.nch + c]);
-    m = block_max(m, shm);
-    if (threadIdx.x == 0) a.dec_m[2 * b + k] = m;
+  for (int t = i; t < T; t += 64) {
+    if (t < acc) a.out_ids[(size_t)b * T + t] = a.draft_ids[(size_t)b * K + t];
+    else if (t > acc) a.out_ids[(size_t)b * T + t] = -1;
   }
 }
 
@@ -438,9 +451,9 @@ __device__ __forceinline__ SampleRow sample_row(const RejArgs& a, int b) {
 
 __device__ __forceinline__ u128 weight_of(const SampleRow& s, float pv, float qv,
                                           float inv_temp) {
-  const uint64_t ep = expfix(scaled(pv, inv_temp) - s.mp);
+  const uint32_t ep = expfix(scaled(pv, inv_temp) - s.mp);
   if (s.q == nullptr) return ep;
-  const uint64_t eq = expfix(scaled(qv, inv_temp) - s.mq);
+  const uint32_t eq = expfix(scaled(qv, inv_temp) - s.mq);
   const u128 x = (u128)ep * s.zq, y = (u128)eq * s.zp;
   return x > y ? x - y : 0;
 }
@@ -602,8 +615,10 @@ __global__ __launch_bounds__(THREADS) void rej_pick_kernel(RejArgs a) {
   }
 }
 
+// The per-row Z sums come first and the row maxima second: the header documents both as
+// results that the rejection call leaves in the workspace.
 struct WsLayout {
-  size_t rmax, zsum, ex, dec_row, dec_z, dec_m, cmass, total;
+  size_t zrow, mrow, ex, rmax, dec_row, dec_z, dec_m, cmass, total;
 };
 
 WsLayout layout(int B, int K, int V) {
@@ -612,11 +627,12 @@ WsLayout layout(int B, int K, int V) {
   auto up = [](size_t x) { return (x + 255) & ~size_t(255); };
   WsLayout l{};
   size_t o = 0;
+  l.zrow = o; o += up(rows * sizeof(uint64_t));
+  l.mrow = o; o += up(rows * sizeof(float));
+  l.ex = o; o += up(rows * sizeof(uint32_t));
   l.rmax = o; o += up(rows * nch * sizeof(float) > (size_t)B * (K + 1) * nch * sizeof(ArgPart)
                           ? rows * nch * sizeof(float)
                           : (size_t)B * (K + 1) * nch * sizeof(ArgPart));
-  l.zsum = o; o += up(rows * nch * sizeof(uint64_t));
-  l.ex = o; o += up(rows * sizeof(uint64_t));
   l.dec_row = o; o += up((size_t)B * sizeof(int32_t));
   l.dec_z = o; o += up((size_t)B * 2 * sizeof(uint64_t));
   l.dec_m = o; o += up((size_t)B * 2 * sizeof(float));
@@ -664,6 +680,8 @@ extern "C" int npn_accept_rejection(const float* target_logits, const float* dra
                   out_ids,
               NPN_ERR_NULL);
   NPN_REQUIRE(shape_ok(B, K, V), NPN_ERR_SHAPE);
+  // Z <= V * 2^31, so 2^24 * sum R <= 2^24 * Zp * Zq stays below 2^128 for V <= 2^20
+  NPN_REQUIRE(V <= kRejMaxV, NPN_ERR_SHAPE);
   NPN_REQUIRE(inv_temperature > 0.0f && inv_temperature < 1e30f, NPN_ERR_VALUE);
   const WsLayout l = layout(B, K, V);
   NPN_REQUIRE(workspace != nullptr && workspace_bytes >= l.total, NPN_ERR_WORKSPACE);
@@ -674,14 +692,17 @@ extern "C" int npn_accept_rejection(const float* target_logits, const float* dra
   const bool vec4 = V % 4 == 0 && NPN_ALIGNED16(target_logits) && NPN_ALIGNED16(draft_logits);
   RejArgs a{target_logits, draft_logits, draft_ids, u_accept, u_sample, inv_temperature,
             accepted, out_ids, B, K, V, nch, (V + MCHK - 1) / MCHK, vec4,
-            reinterpret_cast<float*>(ws + l.rmax), reinterpret_cast<uint64_t*>(ws + l.zsum),
-            reinterpret_cast<uint64_t*>(ws + l.ex), reinterpret_cast<int32_t*>(ws + l.dec_row),
-            reinterpret_cast<uint64_t*>(ws + l.dec_z), reinterpret_cast<float*>(ws + l.dec_m),
-            reinterpret_cast<u128*>(ws + l.cmass)};
+            reinterpret_cast<uint64_t*>(ws + l.zrow), reinterpret_cast<float*>(ws + l.mrow),
+            reinterpret_cast<uint32_t*>(ws + l.ex), reinterpret_cast<float*>(ws + l.rmax),
+            reinterpret_cast<int32_t*>(ws + l.dec_row), reinterpret_cast<uint64_t*>(ws + l.dec_z),
+            reinterpret_cast<float*>(ws + l.dec_m), reinterpret_cast<u128*>(ws + l.cmass)};
   const int rows = B * (2 * K + 1);
   hipLaunchKernelGGL(rej_max_kernel, dim3(nch, rows), dim3(THREADS), 0, s, a);
-  hipLaunchKernelGGL(rej_sum_kernel, dim3(nch, rows), dim3(THREADS), 0, s, a);
-  hipLaunchKernelGGL(rej_decide_kernel, dim3(B), dim3(THREADS), 0, s, a);
+  if (inv_temperature == 1.0f)
+    hipLaunchKernelGGL(rej_sum_kernel<true>, dim3(nch, rows), dim3(THREADS), 0, s, a);
+  else
+    hipLaunchKernelGGL(rej_sum_kernel<false>, dim3(nch, rows), dim3(THREADS), 0, s, a);
+  hipLaunchKernelGGL(rej_decide_kernel, dim3(B), dim3(64), 0, s, a);
   hipLaunchKernelGGL(rej_mass_kernel, dim3(a.nchm, B), dim3(THREADS), 0, s, a);
   hipLaunchKernelGGL(rej_pick_kernel, dim3(B), dim3(THREADS), 0, s, a);
   return npn_launch_status();

@@ -20,69 +20,88 @@ and q(x) > 0 = p(x) (always reject, residual = p restricted to p > q)
 (tests/test_oracle_accept.py).
 
 Integer softmax contract (shared bit-for-bit with ``csrc/spec_accept.hip``):
-- s_v = t_v * inv_temp (fp32 multiply), m = max_v s_v, x_v = s_v - m (fp32).
-- E_v = floor(2^32 * exp_c(x_v)) as an integer, with exp_c the fp32
-  Cody-Waite reduction + degree-7 Taylor polynomial below, evaluated with
-  separately rounded fp32 multiplies and adds only (no fused multiply-add),
+- s_v = t_v * inv_temp (fp32 multiply), m = max_v s_v over the non-NaN s_v (-inf if
+  none), x_v = s_v - m (fp32); NaN x_v give E_v = 0.
+- E_v = floor(2^31 * exp_c(x_v)) as an integer below 2^31 + 1, with exp_c the fp32
+  Cody-Waite reduction + degree-7 Taylor polynomial below, evaluated with correctly
+  rounded fp32 fused multiply-adds (IEEE-754 fusedMultiplyAdd) and one fp32 subtraction,
   so every step is one IEEE-754 operation that CPU and GPU round identically.
 - Z = sum_v E_v in exact integer arithmetic (order-independent).
 - p(v) = E^p_v / Z_p, q(v) = E^q_v / Z_q. Uniforms u are read as
   U = floor(u * 2^24).
 - Accept draft x at position i iff U * E^q_x * Z_p <= 2^24 * E^p_x * Z_q
-  (integers up to 2^107).
+  (integers below 2^104).
 - At the first rejection sample from R_v = max(0, E^p_v Z_q - E^q_v Z_p); if all
   K drafts are accepted sample the bonus from R_v = E^p_v of row K. The token is
   the smallest v with 2^24 * sum_{w<=v} R_w > U_s * sum_w R_w.
 """
 import numpy as np
 
-# ---- exp_c: Cody-Waite range reduction + Taylor polynomial, fp32, no FMA -------------
+# ---- fp32 fused multiply-add --------------------------------------------------------
+
+def fma32(a, b, c):
+    """fp32 a*b + c with one rounding (IEEE-754 fusedMultiplyAdd, round to nearest even),
+    elementwise. a*b is exact in float64 (24 + 24 significant bits); the float64 sum is
+    rounded to odd (round to nearest, then the neighbour with an odd last bit when the
+    TwoSum error is nonzero), which makes its rounding to fp32 the correctly rounded result
+    since 53 >= 24 + 2 (Boldo & Melquiond, "Emulation of FMA and correctly rounded sums:
+    proved algorithms using rounding to odd", IEEE Trans. Computers 57(4), 2008)."""
+    a = np.asarray(a, np.float32).astype(np.float64)
+    b = np.asarray(b, np.float32).astype(np.float64)
+    c = np.asarray(c, np.float32).astype(np.float64)
+    p = a * b
+    s = p + c
+    bp = s - p
+    err = (p - (s - bp)) + (c - bp)                                  # s + err == p + c exactly
+    even = (s.view(np.int64) & 1) == 0
+    toward = np.nextafter(s, np.where(err > 0, np.inf, -np.inf))
+    return np.where((err != 0) & even, toward, s).astype(np.float32)
+
+
+# ---- exp_c: Cody-Waite range reduction + Taylor polynomial, fp32 with FMA ------------
 
 _F = np.float32
 L2E = _F(1.4426950408889634)                     # log2(e) rounded to fp32
 _LN2 = 0.6931471805599453
 LN2_HI = np.array([_LN2], np.float32).view(np.uint32) & np.uint32(0xFFFFF000)
 LN2_HI = LN2_HI.view(np.float32)[0]              # ln2 with the low 12 mantissa bits cleared
-LN2_LO = _F(_LN2 - float(LN2_HI))                # remainder, so n*LN2_HI is exact for |n| < 2^12
-# Taylor coefficients 1/k!, k = 7..2 (1/1! and 1/0! are the final two Horner steps).
-TAYLOR = [_F(1.0 / 5040.0), _F(1.0 / 720.0), _F(1.0 / 120.0), _F(1.0 / 24.0), _F(1.0 / 6.0), _F(0.5)]
-X_MIN = _F(-32.0)                                # below this 2^32*exp(x) < 1: E = 0
-FIX_BITS = 32                                    # E = floor(2^32 * exp(x))
+LN2_LO = _F(_LN2 - float(LN2_HI))                # remainder
+MAGIC = _F(1.5 * 2.0 ** 23)                      # fma(x, L2E, MAGIC) rounds x*L2E to an integer
+FIX_BITS = 31                                    # E = floor(2^31 * exp(x))
+# Taylor coefficients 1/k! rounded to fp32, k = 7..0, each scaled by 2^FIX_BITS (exact:
+# a power of two), so the polynomial evaluates 2^31 * exp(r) directly.
+TAYLOR = [_F(_F(1.0 / f) * _F(2.0 ** FIX_BITS)) for f in (5040.0, 720.0, 120.0, 24.0, 6.0, 2.0, 1.0, 1.0)]
+X_MIN = _F(-32.0)                                # at and below this 2^31*exp(x) < 1: E = 0
 U_BITS = 24                                      # U = floor(u * 2^24)
 
 
 def expfix(x):
-    """E = floor(2^32 * exp_c(x)) for fp32 x <= 0, as uint64 (elementwise).
+    """E = floor(2^31 * exp_c(x)) for fp32 x <= 0, as uint32 (elementwise).
 
-    Steps (all fp32, one rounding each):
-      kf = floor(x * L2E + 0.5); r = (x - kf*LN2_HI) - kf*LN2_LO
-      p  = ((((((c7 r + c6) r + c5) r + c4) r + c3) r + c2) r + 1) r + 1
-      E  = mantissa(p) shifted by exponent(p) + kf + 32 - 150 (integer shift, floor)
+    Steps (all fp32, one rounding each; fma = fused multiply-add):
+      x  = fmax(x, -32)                        (NaN -> -32)
+      t  = fma(x, L2E, 1.5*2^23); kf = t - 1.5*2^23    (kf = round(x*log2 e), exact integer)
+      r  = fma(-kf, LN2_HI, x); r = fma(-kf, LN2_LO, r)
+      p  = Horner with fma over the coefficients 2^31/k!, k = 7..0   (p ~ 2^31 exp(r))
+      E  = trunc(p * 2^kf), the scaling done exactly by adding kf to p's exponent field
+           (kf * 2^23 added to the bit pattern; the low bits of t's pattern hold kf)
     """
-    x = np.asarray(x, np.float32)
-    x = np.where(x < X_MIN, X_MIN, x).astype(np.float32)
-    kf = np.floor((x * L2E).astype(np.float32) + _F(0.5)).astype(np.float32)
-    r = (x - (kf * LN2_HI).astype(np.float32)).astype(np.float32)
-    r = (r - (kf * LN2_LO).astype(np.float32)).astype(np.float32)
+    x = np.fmax(np.asarray(x, np.float32), X_MIN).astype(np.float32)
+    t = fma32(x, L2E, MAGIC)
+    kf = (t - MAGIC).astype(np.float32)
+    r = fma32(-kf, LN2_HI, x)
+    r = fma32(-kf, LN2_LO, r)
     p = np.full_like(r, TAYLOR[0])
     for c in TAYLOR[1:]:
-        p = ((p * r).astype(np.float32) + c).astype(np.float32)
-    p = ((p * r).astype(np.float32) + _F(1.0)).astype(np.float32)
-    p = ((p * r).astype(np.float32) + _F(1.0)).astype(np.float32)
-    bits = p.view(np.uint32).astype(np.int64)
-    e = (bits >> 23) & 0xFF
-    m = (bits & 0x7FFFFF) | 0x800000
-    shift = e + kf.astype(np.int64) - 118                           # (e-127-23) + kf + 32
-    left = np.where(shift > 0, shift, 0)
-    right = np.where(shift < 0, np.minimum(-shift, 63), 0)
-    out = np.where(shift >= 0, m << left, m >> right).astype(np.uint64)
-    return np.where(x <= X_MIN, np.uint64(0), out).astype(np.uint64)
+        p = fma32(p, r, c)
+    bits = (p.view(np.uint32) + (t.view(np.uint32) << np.uint32(23))).astype(np.uint32)
+    return bits.view(np.float32).astype(np.uint32)
 
 
 def row_weights(logits_row, inv_temp=1.0):
-    """(E [V] uint64, Z python int, m fp32) for one logits row under the contract."""
+    """(E [V] uint32, Z python int, m fp32) for one logits row under the contract."""
     s = (np.asarray(logits_row, np.float32) * _F(inv_temp)).astype(np.float32)
-    m = s.max()
+    m = np.fmax.reduce(s, initial=_F(-np.inf))     # NaN entries are ignored (and get E = 0)
     E = expfix((s - m).astype(np.float32))
     return E, int(E.sum(dtype=np.uint64)), m
 

@@ -6,7 +6,9 @@ test_decode_sharded_lm_cpu.py:29-46 (forced winners, equal maxima inside and acr
 8192-wide chunks, all-zero rows) plus NaN rows; the single-layer workload (5 positions,
 V = 32000, draft = argmax with p = 0.5).
 Rejection: the verify workload's distributions (V = 151936, draft logits 0.8 t + 0.6 eps)
-and small vocabularies where rejection and residual sampling happen often.
+and small vocabularies where rejection and residual sampling happen often; every row's
+normaliser Z and maximum m (left in the workspace) bit-exact against the oracle's
+row_weights, with -inf and NaN logits and a partial last chunk.
 """
 import numpy as np
 import pytest
@@ -94,3 +96,35 @@ def test_rejection_equal_distributions_always_accept(ops):
     acc, out = _rejection(ops, target, target[:, :5].contiguous(), ids, u, us)
     assert (acc == 5).all()
     assert np.array_equal(out[:, :5], ids.numpy())
+
+
+@pytest.mark.parametrize("B,K,V,seed,inv_t", [(3, 2, 151936, 4, 1.0), (2, 3, 20001, 5, 0.7)])
+def test_rejection_row_sums_bit_exact(ops, B, K, V, seed, inv_t):
+    from npn_native import call, query, stream_of
+    target, draft, ids, u, us = _rejection_inputs(B, K, V, seed)
+    target[0, 0, 17] = float("-inf")
+    target[B - 1, K, V - 1] = float("nan")
+    draft[0, K - 1, :100] = float("-inf")
+    draft[B - 1, 0, 3] = float("nan")
+    t, d = target.cuda(), draft.cuda()
+    ws = torch.zeros(query("npn_accept_workspace_size", B, K, V), dtype=torch.uint8,
+                     device="cuda")
+    acc = torch.empty(B, dtype=torch.int32, device="cuda")
+    out = torch.empty((B, K + 1), dtype=torch.int64, device="cuda")
+    call("npn_accept_rejection", t, d, ids.cuda(), u.cuda(), us.cuda(), inv_t, acc, out,
+         B, K, V, ws, ws.numel(), stream_of(t))
+    torch.cuda.synchronize()
+    R = B * (2 * K + 1)
+    off = (8 * R + 255) // 256 * 256
+    z = ws[:8 * R].cpu().numpy().view(np.uint64)
+    m = ws[off:off + 4 * R].cpu().numpy().view(np.float32)
+    rows = [target[b, i].numpy() for b in range(B) for i in range(K + 1)]
+    rows += [draft[b, i].numpy() for b in range(B) for i in range(K)]
+    for r, logits in enumerate(rows):
+        _, Z, mr = oa.row_weights(logits, inv_t)
+        assert int(z[r]) == Z, f"row {r}: Z {int(z[r])} vs oracle {Z}"
+        assert m[r].view(np.uint32) == np.float32(mr).view(np.uint32), f"row {r}: max"
+    racc, rout = oa.accept_rejection(target.numpy(), draft.numpy(), ids.numpy(), u.numpy(),
+                                     us.numpy(), inv_t)
+    assert np.array_equal(acc.cpu().numpy(), racc)
+    assert np.array_equal(out.cpu().numpy(), rout)

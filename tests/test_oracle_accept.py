@@ -5,8 +5,11 @@ contrib/qwen3.6-35b-a3b/kernels/tests/test_decode_sharded_lm_cpu.py:29-46 and Na
 accept_greedy on constructed draft sequences.
 
 Rejection sampling (no reference vectors exist; pinned against the mathematics):
-- expfix: E(0) = 2^32, monotone, within max(2 quanta, 2^-21 relative) of floor(2^32 exp(x)),
-  0 below -32;
+- fma32 (the fp32 fused multiply-add the contract is written in): equal to the C library's
+  fmaf on random operands and on a constructed double-rounding case, where rounding the
+  float64 sum to nearest first gives the wrong fp32 result;
+- expfix: E(0) = 2^31, monotone, within max(2 quanta, 2^-21 relative) of floor(2^31 exp(x)),
+  0 at and below -32 and for -inf and NaN;
 - the exact distribution of the first emitted token implied by the integer contract
   (acceptance probabilities counted over all 2^24 uniforms, residual picked by counting
   uniforms per token) equals p = E^p / Z^p within 2^-22 (Leviathan et al. 2023, Thm 1);
@@ -58,15 +61,52 @@ def test_accept_greedy_cases():
     assert out[2].tolist() == [tid[2, 0], -1, -1, -1, -1]
 
 
+def _libm_fmaf():
+    import ctypes
+    import ctypes.util
+    libm = ctypes.CDLL(ctypes.util.find_library("m") or "libm.so.6")
+    f = libm.fmaf
+    f.restype = ctypes.c_float
+    f.argtypes = [ctypes.c_float] * 3
+    return f
+
+
+def test_fma32_matches_libm_fmaf():
+    fmaf = _libm_fmaf()
+    rng = np.random.default_rng(3)
+    a = (rng.standard_normal(4000) * 4.0 ** rng.integers(-6, 6, 4000)).astype(np.float32)
+    b = (rng.standard_normal(4000) * 4.0 ** rng.integers(-6, 6, 4000)).astype(np.float32)
+    c = (rng.standard_normal(4000) * 4.0 ** rng.integers(-6, 6, 4000)).astype(np.float32)
+    # operand ranges of the contract: x in [-32, 0] against log2(e), and Horner steps
+    x = -rng.uniform(0, 32, 4000).astype(np.float32)
+    a = np.concatenate([a, x, rng.uniform(-0.35, 0.35, 4000).astype(np.float32)])
+    b = np.concatenate([b, np.full(4000, oa.L2E), np.full(4000, oa.TAYLOR[2])])
+    c = np.concatenate([c, np.full(4000, oa.MAGIC), np.full(4000, oa.TAYLOR[3])])
+    got = oa.fma32(a, b, c)
+    ref = np.array([fmaf(float(p), float(q), float(r)) for p, q, r in zip(a, b, c)], np.float32)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    # 641 * 6700417 = 2^32 + 1: a*b = 2^-24 + 2^-56, so 1 + a*b lies just above the fp32
+    # midpoint 1 + 2^-24; the float64 sum rounds onto the midpoint and then to even (1.0)
+    a1, b1, one = np.float32(641 * 2.0 ** -28), np.float32(6700417 * 2.0 ** -28), np.float32(1)
+    assert np.float32(np.float64(a1) * np.float64(b1) + 1.0) == one
+    for s in (1.0, -1.0):
+        want = fmaf(float(s * a1), float(b1), float(s * one))
+        assert want == s * (1 + 2.0 ** -23)
+        assert oa.fma32(np.float32(s * a1), b1, np.float32(s * one)) == np.float32(want)
+
+
 def test_expfix_properties():
     x = np.sort(-np.random.default_rng(0).exponential(4.0, 100000).astype(np.float32))
     E = oa.expfix(x)
-    assert oa.expfix(np.float32([0.0]))[0] == 1 << 32
+    assert E.dtype == np.uint32
+    assert oa.expfix(np.float32([0.0, -0.0]))[0] == 1 << 31
     assert np.all(np.diff(E.astype(np.int64)) >= 0)                    # monotone in x
-    ref = np.floor(np.exp(x.astype(np.float64)) * 2.0 ** 32)
-    # within 2 quanta (2^-31 absolute) or 2^-21 relative, whichever is larger
+    ref = np.floor(np.exp(x.astype(np.float64)) * 2.0 ** 31)
+    # within 2 quanta (2^-30 absolute) or 2^-21 relative, whichever is larger
     assert np.all(np.abs(E - ref) <= np.maximum(2.0, ref * 2.0 ** -21))
-    assert np.all(oa.expfix(np.float32([-32.0, -40.0, -1e30])) == 0)
+    assert np.all(oa.expfix(np.float32([-32.0, -40.0, -1e30, -np.inf, np.nan])) == 0)
+    # the smallest nonzero E: 2^31 exp(x) >= 1 from x = -31 ln 2 = -21.487 on
+    assert oa.expfix(np.float32([-21.4]))[0] == 1 and oa.expfix(np.float32([-21.6]))[0] == 0
 
 
 def _first_token_distribution(t_row, d_row):

@@ -158,6 +158,21 @@ size_t npn_fp8_matmul_workspace_size(int M, int K, int N);
 int npn_fp8_matmul(const uint16_t* x, const int8_t* w, const float* scale, uint16_t* out, int M,
                    int K, int N, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Workspace bytes for npn_fp8_matmul_swiglu (0 when the SwiGLU is fused into the GEMM
+ * epilogue and nothing is needed). */
+size_t npn_fp8_matmul_swiglu_workspace_size(int M, int K, int N);
+
+/* torch.ops.fp8.matmul_swiglu -- new op: the MLP's gate/up projection and SwiGLU
+ * (contrib/qwen3.6-27b/static_decode.py:951-963) in one call.
+ *   w [K, N] = [gate | up] along N (N % 128 == 0), scale [N];
+ *   out [M, N/2] bf16 = bf16(bf16(silu(g)) * u), [g | u] = bf16((x . w) * scale),
+ * bit-identical to npn_fp8_matmul followed by npn_silu_mul. Shapes whose npn_fp8_matmul
+ * plan is the wide kernel without split-K (64 < M, wide N) apply the SwiGLU in its epilogue
+ * and never write [g | u]; others write [g | u] to the workspace. */
+int npn_fp8_matmul_swiglu(const uint16_t* x, const int8_t* w, const float* scale, uint16_t* out,
+                          int M, int K, int N, void* workspace, size_t workspace_bytes,
+                          void* stream);
+
 /* Row argmax of npn_fp8_matmul's output without writing it (an LM head's greedy decision,
  * the reference takes logits.argmax(-1) of the bf16 LM-head output,
  * contrib/qwen3.6-27b/static_decode.py:546, :1313). New op torch.ops.fp8.matmul_argmax.

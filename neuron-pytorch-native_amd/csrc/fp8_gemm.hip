@@ -271,6 +271,10 @@ struct WideArgs {
   float* partial;  // [split_k][M][N] fp32, unscaled, when split_k > 1 or to_partial
   int M, K, N, units, groups, split_k, to_partial;
   ArgPart* amax;   // row argmax partials [M][groups] instead of out (split_k == 1)
+  // SwiGLU epilogue (split_k == 1): W = [gate | up] along N; units counts gate units, each
+  // workgroup takes gate units u0..u1 (at most NH) and the up units N/2 columns to their
+  // right, wave column half 0 computing gate and 1 up; out [M, N/2] = bf16(bf16(silu(g)) * u)
+  int swiglu;
 };
 
 typedef int i32x2 __attribute__((ext_vector_type(2)));
@@ -299,7 +303,8 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void fp8_gemm_wide_kernel(WideArgs
   const int nu = u1 - u0;
   if (nu <= 0) return;
   const int n0 = 16 * u0;
-  const int nup = nu | 1;          // W row stride in the stage, in 16-byte units (odd)
+  // W row stride in the stage, in 16-byte units (odd); SwiGLU: NH gate slots, NH up slots
+  const int nup = a.swiglu ? 2 * NH + 1 : (nu | 1);
   const int nchunks = a.K / KC;
   const int c_lo = (int)((long)nchunks * sk / a.split_k);
   const int c_hi = (int)((long)nchunks * (sk + 1) / a.split_k);
@@ -328,9 +333,17 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void fp8_gemm_wide_kernel(WideArgs
       int f = q * WIDE_THREADS + tid;         // 16-byte slot of the W stage
       if (f >= KC * nup) f = 0;               // lanes past the stage re-read slot 0 (slack)
       const int r = f / nup;
-      int cc = f - r * nup;
-      cc = cc < nu ? cc : 0;                  // row pad slot: re-read the row's first unit
-      const uint8_t* src = a.w + (size_t)(c * KC + r) * a.N + n0 + 16 * cc;
+      const int cc = f - r * nup;
+      int col;
+      if (a.swiglu) {                         // slots [0, NH) gate, [NH, 2NH) up, 2NH pad
+        const int hsel = cc >= NH && cc < 2 * NH ? 1 : 0;
+        int uu = cc - NH * hsel;
+        uu = uu < nu ? uu : 0;                // unused or pad slot: re-read unit u0
+        col = n0 + 16 * uu + hsel * (a.N / 2);
+      } else {
+        col = n0 + 16 * (cc < nu ? cc : 0);   // row pad slot: re-read the row's first unit
+      }
+      const uint8_t* src = a.w + (size_t)(c * KC + r) * a.N + col;
       npn::lds_dma16(src, ws + q * (WIDE_THREADS * 16) + (tid & ~63) * 16);
     }
   };
@@ -412,6 +425,49 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void fp8_gemm_wide_kernel(WideArgs
   }
 
   // Epilogue: lane (i, G) holds rows 64wr + 16mt + 4G + r, column n0 + 16(NH wc + nt) + i.
+  if (a.swiglu) {
+    // Wave (wr, 1) holds up for exactly the rows and columns that wave (wr, 0) holds for gate,
+    // lane for lane. The two split the SwiGLU: (wr, 0) finishes row blocks mt = 0, 1 and
+    // (wr, 1) mt = 2, 3, each handing the other its bf16 values of the other's blocks through
+    // LDS (the stages are free once every wave has passed the first barrier), then applying
+    // the glue kernel's rounding.
+    const int I = a.N / 2;
+    __syncthreads();
+    uint16_t* slot = reinterpret_cast<uint16_t*>(smem) + (size_t)(wr * 64 + lane) * (16 * NH);
+#pragma unroll
+    for (int nt = 0; nt < NH; ++nt) {
+      if (nt >= nu) continue;
+      const float sc = a.scale[wc * I + n0 + 16 * nt + i];
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+        if ((mt >> 1) == wc) continue;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) slot[16 * nt + 4 * mt + r] = npn::f32_to_bf16(acc[mt][nt][r] * sc);
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int nt = 0; nt < NH; ++nt) {
+      if (nt >= nu) continue;
+      const int col = n0 + 16 * nt + i;
+      const float sc = a.scale[wc * I + col];
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+        if ((mt >> 1) != wc) continue;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = m_base + 64 * wr + 16 * mt + 4 * G + r;
+          if (m >= a.M) continue;
+          const float own = npn::bf16_to_f32(npn::f32_to_bf16(acc[mt][nt][r] * sc));
+          const float other = npn::bf16_to_f32(slot[16 * nt + 4 * mt + r]);
+          const float g = wc == 0 ? own : other, u = wc == 0 ? other : own;
+          const float sg = npn::bf16_to_f32(npn::f32_to_bf16(npn::silu(g)));
+          a.out[(size_t)m * I + col] = npn::f32_to_bf16(sg * u);
+        }
+      }
+    }
+    return;
+  }
   if (a.amax != nullptr) {
     float bv[4][4];
     int bi[4][4];
@@ -591,10 +647,12 @@ bool shape_ok(int M, int K, int N) {
 // [split_k][M][N] to `partial` and, when `reduce`, the fixed-order reduction into `out`.
 int launch_gemm(const GemmPlan& p, const uint16_t* x, const int8_t* w, const float* scale,
                 uint16_t* out, float* partial, int M, int K, int N, int to_partial, bool reduce,
-                hipStream_t s, ArgPart* amax = nullptr) {
+                hipStream_t s, ArgPart* amax = nullptr, bool swiglu = false) {
   if (p.wide) {
+    // SwiGLU: the same groups, each of at most ntm gate units (plus their up units)
     WideArgs wa{x, reinterpret_cast<const uint8_t*>(w), scale, out, partial, M, K, N,
-                p.units, p.groups, p.split_k, to_partial, amax};
+                swiglu ? p.units / 2 : p.units, p.groups, p.split_k, to_partial, amax,
+                swiglu ? 1 : 0};
     const int nwg = ((p.groups * p.split_k + 7) / 8) * 8;  // multiple of 8 for the XCD map
     const dim3 grid(nwg, p.passes);
     const dim3 block(WIDE_THREADS);
@@ -661,6 +719,43 @@ extern "C" int npn_fp8_matmul_partials(const uint16_t* x, const int8_t* w, float
   // Neither kernel reads the scale or writes `out` when it writes partials.
   return launch_gemm(p, x, w, nullptr, nullptr, partial, M, K, N, 1, false,
                      static_cast<hipStream_t>(stream));
+}
+
+// SwiGLU of the GEMM output: out [M, N/2] = bf16(bf16(silu(g)) * u), [g | u] = bf16((x . w) *
+// scale). Wide plans without split-K fuse it into the GEMM epilogue; other shapes write
+// [g | u] to the workspace and run the glue kernel.
+extern "C" int npn_silu_mul(const uint16_t* gate_up, uint16_t* out, int M, int I, void* stream);
+
+// The fused form takes npn_fp8_matmul's own plan (so the sums are the same) when that plan is
+// a wide one without split-K.
+static bool swiglu_fused(const GemmPlan& p) { return p.wide && p.split_k == 1 && p.units % 2 == 0; }
+
+extern "C" size_t npn_fp8_matmul_swiglu_workspace_size(int M, int K, int N) {
+  if (!shape_ok(M, K, N) || N % 128 != 0) return 0;
+  const GemmPlan p = plan(M, K, N);
+  if (swiglu_fused(p)) return 0;
+  return (((size_t)M * N * 2 + 255) & ~(size_t)255) + p.ws;
+}
+
+extern "C" int npn_fp8_matmul_swiglu(const uint16_t* x, const int8_t* w, const float* scale,
+                                     uint16_t* out, int M, int K, int N, void* workspace,
+                                     size_t workspace_bytes, void* stream) {
+  NPN_REQUIRE(x && w && scale && out, NPN_ERR_NULL);
+  NPN_REQUIRE(shape_ok(M, K, N) && N % 128 == 0, NPN_ERR_SHAPE);
+  NPN_REQUIRE(NPN_ALIGNED16(x) && NPN_ALIGNED16(w) && NPN_ALIGNED16(out), NPN_ERR_ALIGN);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const GemmPlan p = plan(M, K, N);
+  if (swiglu_fused(p))
+    return launch_gemm(p, x, w, scale, out, nullptr, M, K, N, 0, false, s, nullptr, true);
+  const size_t need = npn_fp8_matmul_swiglu_workspace_size(M, K, N);
+  NPN_REQUIRE(workspace != nullptr && workspace_bytes >= need, NPN_ERR_WORKSPACE);
+  NPN_REQUIRE(NPN_ALIGNED16(workspace), NPN_ERR_ALIGN);
+  uint16_t* gu = static_cast<uint16_t*>(workspace);
+  const size_t gu_bytes = ((size_t)M * N * 2 + 255) & ~(size_t)255;
+  float* part = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + gu_bytes);
+  const int st = launch_gemm(p, x, w, scale, gu, part, M, K, N, 0, true, s);
+  if (st != NPN_OK) return st;
+  return npn_silu_mul(gu, out, M, N / 2, stream);
 }
 
 // Row argmax of out = bf16((x . w) * scale) without writing out: partials per (row, column

@@ -122,6 +122,29 @@ def _(x, w_fp8_T_i8, scale):
     return x.new_empty((M,), dtype=torch.float32), x.new_empty((M,), dtype=torch.int64)
 
 
+@torch.library.custom_op("fp8::matmul_swiglu", mutates_args=(), device_types="cuda")
+def fp8_matmul_swiglu(x: torch.Tensor, w_fp8_T_i8: torch.Tensor,
+                      scale: torch.Tensor) -> torch.Tensor:
+    """New op: the MLP's gate/up projection and SwiGLU in one call
+    (contrib/qwen3.6-27b/static_decode.py:951-963). w = [gate | up] along N; returns
+    [M, N/2] bf16 = bf16(bf16(silu(g)) * u) for [g | u] = fp8::matmul(x, w, scale),
+    bit-identical to fp8::matmul followed by glue::silu_mul."""
+    M, K, N = _check_gemm_args(x, w_fp8_T_i8)
+    require(scale, "scale", torch.float32, numel=N)
+    if N % 128 != 0 or not (K % 64 == 0 and 1 <= M <= 4096):
+        raise RuntimeError(f"unsupported fp8 matmul_swiglu shape M={M} K={K} N={N}")
+    n_ws = query("npn_fp8_matmul_swiglu_workspace_size", M, K, N)
+    ws = torch.empty(max(n_ws, 1), dtype=torch.uint8, device=x.device)
+    out = torch.empty((M, N // 2), dtype=torch.bfloat16, device=x.device)
+    call("npn_fp8_matmul_swiglu", x, w_fp8_T_i8, scale, out, M, K, N, ws, n_ws, stream_of(x))
+    return out
+
+
+@fp8_matmul_swiglu.register_fake
+def _(x, w_fp8_T_i8, scale):
+    return x.new_empty((x.shape[0], w_fp8_T_i8.shape[1] // 2), dtype=torch.bfloat16)
+
+
 def fp8_linear(x, w_fp8_T_i8, scale):
     """x [..., K] bf16 -> [..., N], as the reference's fp8_linear
     (contrib/qwen3.6-27b/static_decode.py:307-319)."""

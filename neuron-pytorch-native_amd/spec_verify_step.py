@@ -111,9 +111,10 @@ class VerifySlice:
     with the decode state of B sequences."""
 
     def __init__(self, B, K, kv_lens, s_max, pattern="DDDG", seed=0, device="cuda",
-                 fuse_splitk=True):
+                 fuse_splitk=True, fuse_swiglu=True):
         self.B, self.K, self.T = B, K, K + 1
         self.fuse_splitk = fuse_splitk
+        self.fuse_swiglu = fuse_swiglu
         self.pattern = pattern
         self.device = device
         self.s_max = s_max
@@ -212,8 +213,13 @@ class VerifySlice:
 
     def _mlp(self, L, h, last=False):
         M = h.shape[0]
-        gu = fp8_linear(h, L["gate_up"], self.timer, f"fp8.matmul[{M}x{HIDDEN}x{2 * INTER}]")
-        act = self.timer("glue.silu_mul", torch.ops.glue.silu_mul, gu)
+        if self.fuse_swiglu:
+            w, sc = L["gate_up"]
+            act = self.timer(f"fp8.matmul_swiglu[{M}x{HIDDEN}x{2 * INTER}]",
+                             torch.ops.fp8.matmul_swiglu, h, w, sc)
+        else:
+            gu = fp8_linear(h, L["gate_up"], self.timer, f"fp8.matmul[{M}x{HIDDEN}x{2 * INTER}]")
+            act = self.timer("glue.silu_mul", torch.ops.glue.silu_mul, gu)
         return fp8_project(act, L["down"], self.timer, f"fp8.matmul[{M}x{INTER}x{HIDDEN}]",
                            self.fuse_splitk and not last)
 

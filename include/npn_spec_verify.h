@@ -99,6 +99,20 @@ int npn_deltanet_rollback(const float* ckpt, const uint16_t* mixed_qkv,
                           float* state_out, uint16_t* conv_state_out, int B, int T,
                           int k_heads, int v_heads, void* stream);
 
+/* torch.ops.deltanet.chunked_prefill -- replaces the op registered at
+ * contrib/qwen3.6-27b/kernels/deltanet_chunked_ops.py:26-42 (kernel
+ * deltanet_chunked_v2.py:46-105): the gated delta rule over a whole prompt of one
+ * sequence, in chunks. Rows are head-major (row h*S + t):
+ *   state [Hv*128, 128] f32; query, key [Hv*S, 128] f32 raw (L2-normalised inside as
+ *   x * rsqrt(sum x^2 + 1e-6), q also scaled by 1/sqrt(128)); value [Hv*S, 128] f32;
+ *   g, beta [Hv*S] f32 (log decay and update gate per token and head).
+ * Outputs: out [Hv*S, 128] f32 (the raw attention output, before the gated norm),
+ * new_state [Hv*128, 128] f32. Any S >= 1 (the reference kernel needs S % C == 0; a
+ * last partial chunk is handled as zero-gate padding here). */
+int npn_deltanet_chunked_prefill(const float* state, const float* query, const float* key,
+                                 const float* value, const float* g, const float* beta,
+                                 float* out, float* new_state, int v_heads, int S, void* stream);
+
 /* ---------------------------------------------------------------------------
  * GQA attention tail. Head dim 256, partial RoPE on dims [0, 64).
  * ------------------------------------------------------------------------- */

@@ -1,0 +1,90 @@
+"""GPU parity of deltanet::chunked_prefill (the chunked gated-DeltaNet prefill) against the
+oracle (oracle/deltanet_chunked.py, float64): out and new_state within the path's 2e-3
+relative bar, measured as Frobenius and elementwise (tests/_util.py).
+
+Cases: the reference test's heads (V_HEADS = 12 per core, contrib/qwen3.6-27b/kernels/tests/
+test_deltanet_chunked_v2.py:17-60, model gates), the 27B model's 48 v-heads, lengths that are
+and are not multiples of the chunk, a single token, the reference's chunk sizes in the [C, C]
+constants (16 and 64: the kernel chunks by 64 either way), identical pad rows (where the
+reference's doubling-product inverse blows up, test_doubling_pad_stability.py:1-19), and the
+HF vectors of tests/golden/deltanet_chunked_hf.npz.
+"""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from _util import assert_rel_close
+from oracle import deltanet_chunked as oc
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
+                      "deltanet_chunked_hf.npz")
+
+
+def _inputs(Hv, S, seed, pad_from=None):
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal((Hv * S, 128)).astype(np.float32)
+    k = rng.standard_normal((Hv * S, 128)).astype(np.float32)
+    v = rng.standard_normal((Hv * S, 128)).astype(np.float32)
+    A_log = rng.standard_normal(Hv)
+    dt = rng.standard_normal(Hv) * 0.1
+    a = rng.standard_normal((Hv, S))
+    g = (-np.exp(A_log)[:, None] * np.log1p(np.exp(a + dt[:, None]))).reshape(-1, 1)
+    beta = 1.0 / (1.0 + np.exp(-rng.standard_normal((Hv * S, 1))))
+    state = (rng.standard_normal((Hv * 128, 128)) * 0.05).astype(np.float32)
+    if pad_from is not None:
+        for arr in (q, k, v):
+            a3 = arr.reshape(Hv, S, 128)
+            a3[:, pad_from:] = a3[:, pad_from:pad_from + 1]
+        for arr in (g, beta):
+            a2 = arr.reshape(Hv, S)
+            a2[:, pad_from:] = a2[:, pad_from:pad_from + 1]
+    return state, q, k, v, g.astype(np.float32), beta.astype(np.float32)
+
+
+def _run(ops, args, C):
+    m = [torch.from_numpy(x).cuda() for x in oc.constants(C)]
+    t = [torch.from_numpy(np.ascontiguousarray(x)).cuda() for x in args]
+    out, ns = ops.deltanet.chunked_prefill(*t, *m)
+    torch.cuda.synchronize()
+    return out.cpu().numpy(), ns.cpu().numpy()
+
+
+@pytest.mark.parametrize("Hv,S,C,seed", [(12, 64, 64, 0), (12, 200, 16, 1), (48, 130, 64, 2),
+                                         (4, 1, 64, 3), (3, 1000, 64, 4), (2, 63, 16, 5)])
+def test_chunked_prefill_matches_oracle(ops, Hv, S, C, seed):
+    args = _inputs(Hv, S, seed)
+    out, ns = _run(ops, args, C)
+    ro, rs = oc.chunked_prefill(*args, 64)
+    assert_rel_close(out, ro, name="out")
+    assert_rel_close(ns, rs, name="new_state")
+
+
+def test_identical_pad_rows(ops):
+    args = _inputs(2, 192, 6, pad_from=15)
+    out, ns = _run(ops, args, 64)
+    assert np.all(np.isfinite(ns)) and np.all(np.isfinite(out))
+    ro, rs = oc.recurrent(*args)
+    assert_rel_close(out, ro, name="out")
+    assert_rel_close(ns, rs, name="new_state")
+
+
+def test_hf_vectors(ops):
+    z = np.load(GOLDEN)
+    for c in sorted({k.split("_")[0] for k in z.files}):
+        f = lambda n: z[f"{c}_{n}"]
+        out, ns = _run(ops, (f("state"), f("q"), f("k"), f("v"), f("g"), f("beta")), int(f("C")))
+        assert_rel_close(out, f("out"), name=f"{c} out")
+        assert_rel_close(ns, f("new_state"), name=f"{c} new_state")
+
+
+def test_rejects_bad_shapes(ops):
+    args = [torch.from_numpy(np.ascontiguousarray(x)).cuda() for x in _inputs(2, 10, 7)]
+    m = [torch.from_numpy(x).cuda() for x in oc.constants(16)]
+    with pytest.raises(RuntimeError):
+        ops.deltanet.chunked_prefill(args[0][:200], *args[1:], *m)       # state rows % 128
+    with pytest.raises(RuntimeError):
+        ops.deltanet.chunked_prefill(*args, m[0][:, :8], m[1], m[2])      # constants not [C, C]

@@ -108,10 +108,15 @@ int npn_deltanet_rollback(const float* ckpt, const uint16_t* mixed_qkv,
  *   g, beta [Hv*S] f32 (log decay and update gate per token and head).
  * Outputs: out [Hv*S, 128] f32 (the raw attention output, before the gated norm),
  * new_state [Hv*128, 128] f32. Any S >= 1 (the reference kernel needs S % C == 0; a
- * last partial chunk is handled as zero-gate padding here). */
+ * last partial chunk is handled as zero-gate padding here). The workspace holds the
+ * state-independent part of every chunk (T, the intra-chunk attention and the per-token
+ * scales), npn_deltanet_chunked_workspace_size bytes (about 33 KiB per head and 64 tokens);
+ * two kernels run on the stream. Sizes: 1 <= v_heads <= 65535, v_heads * S <= 2^26. */
+size_t npn_deltanet_chunked_workspace_size(int v_heads, int S);
 int npn_deltanet_chunked_prefill(const float* state, const float* query, const float* key,
                                  const float* value, const float* g, const float* beta,
-                                 float* out, float* new_state, int v_heads, int S, void* stream);
+                                 float* out, float* new_state, int v_heads, int S,
+                                 void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------
  * GQA attention tail. Head dim 256, partial RoPE on dims [0, 64).

@@ -16,6 +16,7 @@ reference kernel needs S % C == 0).
 import torch
 
 from npn_native import call, require, stream_of
+from npn_native import query as query_size
 
 D = 128
 
@@ -41,10 +42,14 @@ def chunked_prefill(state: torch.Tensor, query: torch.Tensor, key: torch.Tensor,
     for name, t in (("m_incl", m_incl), ("m_strict", m_strict), ("eye", eye)):
         if t.dim() != 2 or tuple(t.shape) != (C, C) or C < 1:
             raise RuntimeError(f"{name} must be [C, C], got {tuple(t.shape)}")
+    n_ws = query_size("npn_deltanet_chunked_workspace_size", Hv, S)
+    if n_ws == 0:
+        raise RuntimeError(f"unsupported chunked prefill size Hv={Hv} S={S}")
+    ws = torch.empty(n_ws, dtype=torch.uint8, device=state.device)
     out = torch.empty((Hv * S, D), dtype=torch.float32, device=state.device)
     new_state = torch.empty((Hv * D, D), dtype=torch.float32, device=state.device)
     call("npn_deltanet_chunked_prefill", state, query, key, value, g, beta, out, new_state,
-         Hv, S, stream_of(state))
+         Hv, S, ws, n_ws, stream_of(state))
     return out, new_state
 
 

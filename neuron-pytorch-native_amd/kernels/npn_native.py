@@ -51,7 +51,8 @@ SIGNATURES = {
     "npn_accept_greedy_parts": (_I, [_P, _I] + [_P] * 3 + [_I, _I, _P]),
     "npn_fp8_matmul_swiglu_workspace_size": (_Z, [_I] * 3),
     "npn_fp8_matmul_swiglu": (_I, [_P] * 4 + [_I] * 3 + [_P, _Z, _P]),
-    "npn_deltanet_chunked_prefill": (_I, [_P] * 8 + [_I, _I, _P]),
+    "npn_deltanet_chunked_workspace_size": (_Z, [_I, _I]),
+    "npn_deltanet_chunked_prefill": (_I, [_P] * 8 + [_I, _I, _P, _Z, _P]),
 }
 
 _lib = None

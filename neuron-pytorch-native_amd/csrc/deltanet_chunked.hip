@@ -64,17 +64,71 @@ __device__ __forceinline__ float4 ld4(const float* p) {
 __device__ __forceinline__ void st4(float* p, float4 v) { *reinterpret_cast<float4*>(p) = v; }
 __device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
 
+// Raw buffer reads: one instruction per float4 with a per-lane byte offset, and reads at or
+// past `bytes` (checked on the per-lane offset) return zeros, which pads a last partial chunk.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
+}
+__device__ __forceinline__ float4 bload4(rsrc_t r, int voff, int soff) {
+  return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+
 // acc += A (16 x K) B (K x 16) with pa = &A[c][0] and pb = &B^T[c][0] (k contiguous in both).
+// All operands are read before the first product, so one LDS latency is paid per tile.
 template <int K>
 __device__ __forceinline__ void tile16(f32x4& acc, const float* pa, const float* pb) {
   const int k0 = ((threadIdx.x >> 4) & 3) * (K / 4);
+  float4 a[K / 16], b[K / 16];
 #pragma unroll
   for (int u = 0; u < K / 16; ++u) {
-    const float4 a = ld4(pa + k0 + 4 * u), b = ld4(pb + k0 + 4 * u);
-    acc = mfma16(a.x, b.x, acc);
-    acc = mfma16(a.y, b.y, acc);
-    acc = mfma16(a.z, b.z, acc);
-    acc = mfma16(a.w, b.w, acc);
+    a[u] = ld4(pa + k0 + 4 * u);
+    b[u] = ld4(pb + k0 + 4 * u);
+  }
+  __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the products
+#pragma unroll
+  for (int u = 0; u < K / 16; ++u) {
+    acc = mfma16(a[u].x, b[u].x, acc);
+    acc = mfma16(a[u].y, b[u].y, acc);
+    acc = mfma16(a[u].z, b[u].z, acc);
+    acc = mfma16(a[u].w, b[u].w, acc);
+  }
+}
+
+// Two tiles, acc1 over K1 and acc2 over K2 (K1 <= K2): the operands of both are read first,
+// then the two accumulation chains run interleaved; pre(u) runs before the u-th group of
+// products (global reads issued there overlap the products).
+template <int K1, int K2, typename Pre>
+__device__ __forceinline__ void tile16x2(f32x4& acc1, const float* pa1, const float* pb1,
+                                         f32x4& acc2, const float* pa2, const float* pb2,
+                                         Pre&& pre) {
+  const int g = (threadIdx.x >> 4) & 3;
+  float4 a1[K1 / 16], b1[K1 / 16], a2[K2 / 16], b2[K2 / 16];
+#pragma unroll
+  for (int u = 0; u < K1 / 16; ++u) {
+    a1[u] = ld4(pa1 + g * (K1 / 4) + 4 * u);
+    b1[u] = ld4(pb1 + g * (K1 / 4) + 4 * u);
+  }
+#pragma unroll
+  for (int u = 0; u < K2 / 16; ++u) {
+    a2[u] = ld4(pa2 + g * (K2 / 4) + 4 * u);
+    b2[u] = ld4(pb2 + g * (K2 / 4) + 4 * u);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int u = 0; u < K2 / 16; ++u) {
+    pre(u);
+    __builtin_amdgcn_sched_barrier(0);
+    if (u < K1 / 16) {
+      acc1 = mfma16(a1[u].x, b1[u].x, acc1);
+      acc1 = mfma16(a1[u].y, b1[u].y, acc1);
+      acc1 = mfma16(a1[u].z, b1[u].z, acc1);
+      acc1 = mfma16(a1[u].w, b1[u].w, acc1);
+    }
+    acc2 = mfma16(a2[u].x, b2[u].x, acc2);
+    acc2 = mfma16(a2[u].y, b2[u].y, acc2);
+    acc2 = mfma16(a2[u].z, b2[u].z, acc2);
+    acc2 = mfma16(a2[u].w, b2[u].w, acc2);
   }
 }
 
@@ -313,8 +367,10 @@ struct ScanSmem {
 // {1, 2} (waves 2, 3), which balances the triangular products.
 
 // X = (raw k) S and O = (raw q) S for the wave's rows; Z = beta (v - sk1 X) into zT; O *= sq.
-template <int I1, int I2>
-__device__ __forceinline__ void scan_state_products(ScanSmem& sm, int J, f32x4& o1, f32x4& o2) {
+// pre(u) issues the u-th part of the next chunk's global reads between the products.
+template <int I1, int I2, typename Pre>
+__device__ __forceinline__ void scan_state_products(ScanSmem& sm, int J, f32x4& o1, f32x4& o2,
+                                                    Pre&& pre) {
   const int lane = threadIdx.x & 63, g4 = lane >> 4, c = lane & 15;
   f32x4 x1 = zero4(), x2 = zero4();
   o1 = zero4();
@@ -324,10 +380,20 @@ __device__ __forceinline__ void scan_state_products(ScanSmem& sm, int J, f32x4& 
   const float* pk2 = sm.k + (16 * I2 + c) * RS + 32 * g4;
   const float* pq1 = sm.q + (16 * I1 + c) * RS + 32 * g4;
   const float* pq2 = sm.q + (16 * I2 + c) * RS + 32 * g4;
+  // operands double-buffered: step u + 1 is read while step u's 16 products run
+  float4 nb = ld4(pb), nk1 = ld4(pk1), nk2 = ld4(pk2), nq1 = ld4(pq1), nq2 = ld4(pq2);
 #pragma unroll
   for (int u = 0; u < 8; ++u) {
-    const float4 b = ld4(pb + 4 * u), k1 = ld4(pk1 + 4 * u), k2 = ld4(pk2 + 4 * u),
-                 q1 = ld4(pq1 + 4 * u), q2 = ld4(pq2 + 4 * u);
+    const float4 b = nb, k1 = nk1, k2 = nk2, q1 = nq1, q2 = nq2;
+    if (u < 7) {
+      nb = ld4(pb + 4 * u + 4);
+      nk1 = ld4(pk1 + 4 * u + 4);
+      nk2 = ld4(pk2 + 4 * u + 4);
+      nq1 = ld4(pq1 + 4 * u + 4);
+      nq2 = ld4(pq2 + 4 * u + 4);
+    }
+    pre(u);
+    __builtin_amdgcn_sched_barrier(0);
     x1 = mfma16(k1.x, b.x, x1); x2 = mfma16(k2.x, b.x, x2);
     o1 = mfma16(q1.x, b.x, o1); o2 = mfma16(q2.x, b.x, o2);
     x1 = mfma16(k1.y, b.y, x1); x2 = mfma16(k2.y, b.y, x2);
@@ -354,33 +420,48 @@ __device__ __forceinline__ void scan_state_products(ScanSmem& sm, int J, f32x4& 
   }
 }
 
-// v_new rows of block I = T Z (K = 16 (I + 1): T is lower triangular) into vnT and vsT.
-template <int I>
-__device__ __forceinline__ void scan_vnew(ScanSmem& sm, int J) {
+// v_new rows of blocks I1 and I2 = T Z (K = 16 (I + 1): T is lower triangular) into vnT, vsT.
+template <int I1, int I2, typename Pre>
+__device__ __forceinline__ void scan_vnew(ScanSmem& sm, int J, Pre&& pre) {
   const int lane = threadIdx.x & 63, g4 = lane >> 4, c = lane & 15;
-  f32x4 acc = zero4();
-  tile16<16 * (I + 1)>(acc, sm.t + (16 * I + c) * MS, sm.zT + (16 * J + c) * MS);
-  const int i0 = 16 * I + 4 * g4, o = (16 * J + c) * MS + i0;
-  st4(sm.vnT + o, make_float4(acc[0], acc[1], acc[2], acc[3]));
-  st4(sm.vsT + o, make_float4(acc[0] * sm.sc[i0].z, acc[1] * sm.sc[i0 + 1].z,
-                              acc[2] * sm.sc[i0 + 2].z, acc[3] * sm.sc[i0 + 3].z));
+  f32x4 v1 = zero4(), v2 = zero4();
+  const float* zb = sm.zT + (16 * J + c) * MS;
+  tile16x2<16 * (I1 + 1), 16 * (I2 + 1)>(v1, sm.t + (16 * I1 + c) * MS, zb,
+                                         v2, sm.t + (16 * I2 + c) * MS, zb, pre);
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const f32x4& acc = p == 0 ? v1 : v2;
+    const int i0 = 16 * (p == 0 ? I1 : I2) + 4 * g4, o = (16 * J + c) * MS + i0;
+    st4(sm.vnT + o, make_float4(acc[0], acc[1], acc[2], acc[3]));
+    st4(sm.vsT + o, make_float4(acc[0] * sm.sc[i0].z, acc[1] * sm.sc[i0 + 1].z,
+                                acc[2] * sm.sc[i0 + 2].z, acc[3] * sm.sc[i0 + 3].z));
+  }
 }
 
-// out rows of block I = O + intra v_new, written where the token exists.
-template <int I>
-__device__ __forceinline__ void scan_out(ScanSmem& sm, float* orow, int J, f32x4 o, int nvalid) {
+// out rows of blocks I1 and I2 = O + intra v_new, written where the token exists.
+template <int I1, int I2, typename Pre>
+__device__ __forceinline__ void scan_out(ScanSmem& sm, float* orow, int J, f32x4 o1, f32x4 o2,
+                                         int nvalid, Pre&& pre) {
   const int lane = threadIdx.x & 63, g4 = lane >> 4, c = lane & 15;
-  tile16<16 * (I + 1)>(o, sm.in + (16 * I + c) * MS, sm.vnT + (16 * J + c) * MS);
+  const float* vb = sm.vnT + (16 * J + c) * MS;
+  tile16x2<16 * (I1 + 1), 16 * (I2 + 1)>(o1, sm.in + (16 * I1 + c) * MS, vb,
+                                         o2, sm.in + (16 * I2 + c) * MS, vb, pre);
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int i = 16 * I + 4 * g4 + r;
-    if (i < nvalid) orow[(size_t)i * D + 16 * J + c] = o[r];
+  for (int p = 0; p < 2; ++p) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = 16 * (p == 0 ? I1 : I2) + 4 * g4 + r;
+      if (i < nvalid) orow[(size_t)i * D + 16 * J + c] = p == 0 ? o1[r] : o2[r];
+    }
   }
 }
 
 // S'^T[col][kk] = e^tot S^T[col][kk] + sum_i (sk2 v_new)^T[col][i] k[i][kk], for the wave's
 // column half and the four 16-blocks of kk from P0; in place (each element is read and
-// written by one lane).
+// written by one lane). Group g takes the tokens i = 8 (s >> 1) + 4 (g & 1) + 2 (g >> 1) +
+// (s & 1) at step s, so the column reads of k by the two groups of a half-wave fall 4 rows
+// apart, in opposite halves of the LDS banks; the reads of 4 steps are issued while the
+// previous 4 steps' products run.
 __device__ __forceinline__ void scan_state_update(ScanSmem& sm, int J, int P0) {
   const int lane = threadIdx.x & 63, g4 = lane >> 4, c = lane & 15;
   const float et = sm.etot;
@@ -388,17 +469,34 @@ __device__ __forceinline__ void scan_state_update(ScanSmem& sm, int J, int P0) {
 #pragma unroll
   for (int p = 0; p < 4; ++p)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) s[p][r] = et * sm.sT[(16 * J + 4 * g4 + r) * RS + 16 * (P0 + p) + c];
-  const float* va = sm.vsT + (16 * J + c) * MS + 16 * g4;
+    for (int r = 0; r < 4; ++r) s[p][r] = sm.sT[(16 * J + 4 * g4 + r) * RS + 16 * (P0 + p) + c];
+  const int i0 = 4 * (g4 & 1) + 2 * (g4 >> 1);
+  const float* va = sm.vsT + (16 * J + c) * MS + i0;
+  const float* kc = sm.k + i0 * RS + 16 * P0 + c;
+  float ae[2][4], kb[2][4][4];
+  auto load = [&](int t, int b) {  // steps 4t .. 4t + 3: tokens 16t + i0 + {0, 1, 8, 9}
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const float4 av = ld4(va + 4 * u);
-    const float* kr = sm.k + (16 * g4 + 4 * u) * RS + 16 * P0 + c;
-    const float ae[4] = {av.x, av.y, av.z, av.w};
+    for (int h = 0; h < 2; ++h) {
+      const float2 av = *reinterpret_cast<const float2*>(va + 16 * t + 8 * h);
+      ae[b][2 * h] = av.x;
+      ae[b][2 * h + 1] = av.y;
+#pragma unroll
+      for (int e = 0; e < 2; ++e)
+#pragma unroll
+        for (int p = 0; p < 4; ++p) kb[b][2 * h + e][p] = kc[(16 * t + 8 * h + e) * RS + 16 * p];
+    }
+  };
+  load(0, 0);
+#pragma unroll
+  for (int p = 0; p < 4; ++p) s[p] *= et;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    if (t < 3) load(t + 1, (t + 1) & 1);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int e = 0; e < 4; ++e)
 #pragma unroll
-      for (int p = 0; p < 4; ++p) s[p] = mfma16(ae[e], kr[e * RS + 16 * p], s[p]);
+      for (int p = 0; p < 4; ++p) s[p] = mfma16(ae[t & 1][e], kb[t & 1][e][p], s[p]);
   }
 #pragma unroll
   for (int p = 0; p < 4; ++p)
@@ -423,93 +521,103 @@ __global__ __launch_bounds__(256, 1) void dn_chunk_scan_kernel(ScanArgs a) {
     const int kk = e >> 5, cc = e & 31;
     sm.sT[cc * RS + kk] = a.state[((size_t)h * D + kk) * D + c0 + cc];
   }
-  // The next chunk's inputs, loaded into registers while the current chunk computes: q, k rows
-  // (rows 8j + (tid >> 5), float4 column tid & 31), this block's v columns (row tid >> 2,
-  // columns 8 (tid & 3) .. +7), the record's T and intra (float4 tid + 256 j) and scales.
+  // The next chunk's inputs are read into registers while the current chunk computes, in
+  // parts issued between the products (reading a chunk's 104 KB at once stalls every wave on
+  // the memory pipeline), and each goes to LDS as soon as the current chunk is done with that
+  // buffer, which keeps the registers held short:
+  //   part 0..7    q rows 8j + (tid >> 5), float4 column tid & 31     issued in Pa, stored after Pb
+  //   part 8..9    this block's v: row tid >> 2, columns 8 (tid & 3)  issued in Pa, stored in Pc
+  //   part 10..13  T (float4 tid + 256 j)                              issued in Pa, stored in Pc
+  //   part 14      scales (wave lane = token) and e^tot                issued in Pa, stored in Pc
+  //                (e^tot at the next chunk's start: the state update reads the current one)
+  //   part 15..22  k rows, as q                                        issued in Pa, stored at start
+  //   part 23..26  intra (float4 tid + 256 j)                          issued in Pb, stored at start
+  // Rows past the end of the prompt read row 0 here and are zeroed when stored.
   float4 pq[8], pk[8], pv[2], pt[4], pi[4];
   float4 psc = make_float4(0.f, 0.f, 0.f, 0.f);
   float pet = 0.f;
-  auto fetch = [&](int ci) {
+  // Reads go through buffer descriptors based at the chunk's first row, sized to the end of
+  // the prompt, so rows past it read as zeros.
+  const int qk_off = (tid >> 5) * (D * 4) + (tid & 31) * 16;         // + 4096 j
+  const int v_off = (tid >> 2) * (D * 4) + (c0 + 8 * (tid & 3)) * 4;  // + 16 p
+  auto fetch_part = [&](int ci, int part) {
     const int t0 = ci * CH;
-    const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int i = 8 * j + (tid >> 5), c4 = tid & 31;
-      const bool ok = t0 + i < S;
-      const size_t r = ok ? row0 + t0 + i : row0;
-      const float4 qv = reinterpret_cast<const float4*>(a.q + r * D)[c4];
-      const float4 kv = reinterpret_cast<const float4*>(a.k + r * D)[c4];
-      pq[j] = ok ? qv : z4;
-      pk[j] = ok ? kv : z4;
-    }
-    {
-      const int i = tid >> 2;
-      const bool ok = t0 + i < S;
-      const size_t r = ok ? row0 + t0 + i : row0;
-      const float4* src = reinterpret_cast<const float4*>(a.v + r * D + c0 + 8 * (tid & 3));
-      const float4 v0 = src[0], v1 = src[1];
-      pv[0] = ok ? v0 : z4;
-      pv[1] = ok ? v1 : z4;
-    }
+    const int rest = (S - t0) * (D * 4);
     const float* rec = a.ws + ((size_t)h * a.nch + ci) * REC;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      pt[j] = reinterpret_cast<const float4*>(rec + REC_T)[tid + 256 * j];
-      pi[j] = reinterpret_cast<const float4*>(rec + REC_I)[tid + 256 * j];
-    }
-    if (wv == 0) {
-      psc = reinterpret_cast<const float4*>(rec + REC_SC)[lane];
+    if (part < 8) {
+      pq[part] = bload4(make_rsrc(a.q + (row0 + t0) * D, rest), qk_off + 4096 * part, 0);
+    } else if (part < 10) {
+      pv[part - 8] = bload4(make_rsrc(a.v + (row0 + t0) * D, rest), v_off + 16 * (part - 8), 0);
+    } else if (part < 14) {
+      pt[part - 10] = bload4(make_rsrc(rec, REC * 4), tid * 16, (REC_T + 1024 * (part - 10)) * 4);
+    } else if (part == 14) {
+      psc = bload4(make_rsrc(rec, REC * 4), lane * 16, REC_SC * 4);
       pet = rec[REC_ET];
+    } else if (part < 23) {
+      pk[part - 15] = bload4(make_rsrc(a.k + (row0 + t0) * D, rest), qk_off + 4096 * (part - 15), 0);
+    } else if (part < 27) {
+      pi[part - 23] = bload4(make_rsrc(rec, REC * 4), tid * 16, (REC_I + 1024 * (part - 23)) * 4);
     }
   };
-  fetch(0);
+  auto store_q = [&]() {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) st4(sm.q + (8 * j + (tid >> 5)) * RS + 4 * (tid & 31), pq[j]);
+  };
+  auto store_v_t_sc = [&]() {
+    float* zd = sm.zT + 8 * (tid & 3) * MS + (tid >> 2);
+    zd[0] = pv[0].x; zd[MS] = pv[0].y; zd[2 * MS] = pv[0].z; zd[3 * MS] = pv[0].w;
+    zd[4 * MS] = pv[1].x; zd[5 * MS] = pv[1].y; zd[6 * MS] = pv[1].z; zd[7 * MS] = pv[1].w;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int e = tid + 256 * j, r = e >> 4, c4 = e & 15;
+      st4(sm.t + r * MS + 4 * c4, pt[j]);
+    }
+    if (wv == 0) sm.sc[lane] = psc;
+  };
+#pragma unroll
+  for (int part = 0; part < 27; ++part) fetch_part(0, part);
+  store_q();
+  store_v_t_sc();
   f32x4 o1, o2;
   for (int ci = 0; ci < a.nch; ++ci) {
     const int t0 = ci * CH;
     __syncthreads();
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int i = 8 * j + (tid >> 5), c4 = tid & 31;
-      st4(sm.q + i * RS + 4 * c4, pq[j]);
-      st4(sm.k + i * RS + 4 * c4, pk[j]);
-    }
-    {
-      float* zd = sm.zT + 8 * (tid & 3) * MS + (tid >> 2);
-      zd[0] = pv[0].x; zd[MS] = pv[0].y; zd[2 * MS] = pv[0].z; zd[3 * MS] = pv[0].w;
-      zd[4 * MS] = pv[1].x; zd[5 * MS] = pv[1].y; zd[6 * MS] = pv[1].z; zd[7 * MS] = pv[1].w;
-    }
+    for (int j = 0; j < 8; ++j) st4(sm.k + (8 * j + (tid >> 5)) * RS + 4 * (tid & 31), pk[j]);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int e = tid + 256 * j, r = e >> 4, c4 = e & 15;
-      st4(sm.t + r * MS + 4 * c4, pt[j]);
       st4(sm.in + r * MS + 4 * c4, pi[j]);
     }
-    if (wv == 0) {
-      sm.sc[lane] = psc;
-      if (lane == 0) sm.etot = pet;
-    }
-    if (ci + 1 < a.nch) fetch(ci + 1);  // in flight during this chunk's work
+    if (wv == 0 && lane == 0) sm.etot = pet;
+    // the next chunk's reads (unconditional, so that no branch forces an early wait: the last
+    // chunk reads itself again, and its late stores only rewrite buffers it no longer reads)
+    const int nx = min(ci + 1, a.nch - 1);
+    auto pre_a = [&](int u) {
+#pragma unroll
+      for (int d = 0; d < 3; ++d)
+        if (3 * u + d < 23) fetch_part(nx, 3 * u + d);
+    };
+    auto pre_b = [&](int u) {
+      if (u < 2) {
+        fetch_part(nx, 23 + 2 * u);
+        fetch_part(nx, 24 + 2 * u);
+      }
+    };
     __syncthreads();
-    if (wv < 2) scan_state_products<0, 3>(sm, J, o1, o2);
-    else scan_state_products<1, 2>(sm, J, o1, o2);
+    if (wv < 2) scan_state_products<0, 3>(sm, J, o1, o2, pre_a);
+    else scan_state_products<1, 2>(sm, J, o1, o2, pre_a);
     __syncthreads();
-    if (wv < 2) {
-      scan_vnew<0>(sm, J);
-      scan_vnew<3>(sm, J);
-    } else {
-      scan_vnew<1>(sm, J);
-      scan_vnew<2>(sm, J);
-    }
+    if (wv < 2) scan_vnew<0, 3>(sm, J, pre_b);
+    else scan_vnew<1, 2>(sm, J, pre_b);
+    store_q();  // q of this chunk was last read in Pa
     __syncthreads();
     const int nvalid = min(CH, S - t0);
     float* orow = a.out + (row0 + t0) * D + c0;
-    if (wv < 2) {
-      scan_out<0>(sm, orow, J, o1, nvalid);
-      scan_out<3>(sm, orow, J, o2, nvalid);
-    } else {
-      scan_out<1>(sm, orow, J, o1, nvalid);
-      scan_out<2>(sm, orow, J, o2, nvalid);
-    }
+    auto no_pre = [](int) {};
+    if (wv < 2) scan_out<0, 3>(sm, orow, J, o1, o2, nvalid, no_pre);
+    else scan_out<1, 2>(sm, orow, J, o1, o2, nvalid, no_pre);
+    store_v_t_sc();  // v (then Z), T and the scales were last read in Pb
     scan_state_update(sm, J, 4 * (wv >> 1));
   }
   __syncthreads();
@@ -519,8 +627,10 @@ __global__ __launch_bounds__(256, 1) void dn_chunk_scan_kernel(ScanArgs a) {
   }
 }
 
+// S * 512 bytes must fit the 32-bit buffer offsets
 bool shape_ok(int v_heads, int S) {
-  return v_heads >= 1 && v_heads <= 65535 && S >= 1 && (long)v_heads * S <= (1L << 26);
+  return v_heads >= 1 && v_heads <= 65535 && S >= 1 && S <= (1 << 22) &&
+         (long)v_heads * S <= (1L << 26);
 }
 
 }  // namespace

@@ -46,6 +46,9 @@ def parse():
     p.add_argument("--lm-head", action="store_true",
                    help="time the LM head + greedy acceptance over the 27B vocabulary, fused "
                         "(argmax in the GEMM epilogue) against logits + accept_greedy")
+    p.add_argument("--prefill", action="store_true",
+                   help="time the chunked gated-DeltaNet prefill (deltanet::chunked_prefill) "
+                        "over the 27B layer's 48 v-heads x 4096 prompt tokens")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only run a plain 1 GiB device copy 5 times (scales HBM byte counters)")
     return p.parse_args()
@@ -209,8 +212,100 @@ def lm_head_bench(args):
         "steps": args.steps, "warmup": args.warmup}))
 
 
+PF_HEADS, PF_TOKENS, PF_CHUNK, PF_DIM = 48, 4096, 64, 128
+FP32_PEAK_TFLOPS = 157.3       # MI355X dense fp32 MFMA
+
+
+def prefill_flops_per_chunk(C=PF_CHUNK, d=PF_DIM):
+    """Algorithmic FLOPs of one chunk of one head in the chunked form: A (strictly lower) and
+    the intra attention (lower) over d, the unit-lower inverse by substitution, k S and q S,
+    v_new = T Z and intra v_new (lower), and the state update k^T v_new."""
+    strict, lower = C * (C - 1) // 2, C * (C + 1) // 2
+    inverse = sum((i - j - 1) for i in range(C) for j in range(i)) * 2
+    return (2 * d * strict + 2 * d * lower + inverse + 2 * 2 * C * d * d
+            + 2 * 2 * d * lower + 2 * C * d * d)
+
+
+def prefill_bench(args):
+    """deltanet::chunked_prefill on [48 * 4096, 128] fp32 q, k, v (the 27B layer's v-heads over
+    a 4096-token prompt, k already repeated to the v-heads), random inputs with the model's
+    gate ranges. One head is checked against the float64 oracle; the oracle is timed on a
+    bounded CPU sample (one head, 512 tokens)."""
+    import numpy as np
+    import torch
+    import npn_ops  # noqa: F401  (registers torch.ops.deltanet.chunked_prefill)
+    from oracle import deltanet_chunked as oc
+    dev = "cuda"
+    Hv, S = PF_HEADS, PF_TOKENS
+    g = torch.Generator(device=dev).manual_seed(args.seed)
+    st = torch.randn(Hv * PF_DIM, PF_DIM, generator=g, device=dev) * 0.05
+    q, k, v = (torch.randn(Hv * S, PF_DIM, generator=g, device=dev) for _ in range(3))
+    a_log = torch.randn(Hv, 1, generator=g, device=dev)
+    dt = torch.randn(Hv, 1, generator=g, device=dev) * 0.1
+    a_in = torch.randn(Hv, S, generator=g, device=dev)
+    gate = (-torch.exp(a_log) * torch.nn.functional.softplus(a_in + dt)).reshape(-1, 1)
+    beta = torch.sigmoid(torch.randn(Hv * S, 1, generator=g, device=dev))
+    consts = [torch.from_numpy(x).to(dev) for x in oc.constants(PF_CHUNK)]
+
+    def run():
+        return torch.ops.deltanet.chunked_prefill(st, q, k, v, gate, beta, *consts)
+
+    for _ in range(args.warmup):
+        run()
+    torch.cuda.synchronize()
+    s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s_ev.record()
+    for _ in range(args.steps):
+        run()
+    e_ev.record()
+    torch.cuda.synchronize()
+    ms = s_ev.elapsed_time(e_ev) / args.steps
+    out, new_state = run()
+    # parity on head 0 (float64 oracle, the op's 2e-3 relative bar)
+    h0 = slice(0, S)
+    args0 = [x.detach().cpu().numpy() for x in (st[:PF_DIM], q[h0], k[h0], v[h0], gate[h0],
+                                                beta[h0])]
+    o_ref, s_ref = oc.chunked_prefill(*args0, PF_CHUNK)
+    err = max(float(np.abs(out[h0].cpu().numpy() - o_ref).max() / np.abs(o_ref).max()),
+              float(np.abs(new_state[:PF_DIM].cpu().numpy() - s_ref).max()
+                    / np.abs(s_ref).max()))
+    nch = -(-S // PF_CHUNK)
+    flops = prefill_flops_per_chunk() * nch * Hv
+    achieved = flops / ms / 1e9
+    line = {
+        "metric": "chunked prefill prompt tokens/s (one DeltaNet layer, 48 v-heads)",
+        "value": round(S / ms * 1e3, 1), "unit": "tokens/s", "ms_per_call": round(ms, 4),
+        "higher_is_better": True, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": f"deltanet::chunked_prefill, {Hv} v-heads x {S} tokens, "
+                               f"head dim {PF_DIM}, chunk {PF_CHUNK}"},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": FP32_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / FP32_PEAK_TFLOPS, 4),
+                     "traffic": None, "scope": "both kernels of the op",
+                     "flop_per_chunk_head": prefill_flops_per_chunk()},
+        "max_rel_err_head0": err, "steps": args.steps, "warmup": args.warmup,
+    }
+    if not args.no_cpu_baseline:
+        n_tok = 512
+        t0 = time.perf_counter()
+        reps = 0
+        while True:
+            oc.chunked_prefill(*(x[:n_tok] if x.shape[0] == S else x for x in args0), PF_CHUNK)
+            reps += 1
+            if time.perf_counter() - t0 > 5.0:
+                break
+        cpu_s = (time.perf_counter() - t0) / reps
+        line["cpu_baseline"] = {
+            "value": round(n_tok / cpu_s / Hv, 2), "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"oracle/deltanet_chunked.py (numpy float64) on 1 head x {n_tok} tokens, "
+                      f"scaled to {Hv} heads"}
+    print(json.dumps(line))
+
+
 def main():
     args = parse()
+    if args.prefill:
+        prefill_bench(args)
+        return
     if args.copy_calibration:
         copy_calibration()
         return

@@ -148,6 +148,7 @@ struct PrepArgs {
   float* ws;
   int S;
   int nch;
+  int items;   // Hv * nch, item = h * nch + chunk
 };
 
 struct PrepSmem {
@@ -162,175 +163,193 @@ struct PrepSmem {
   float gcum[CH], bt[CH], rq[CH], rk[CH];
 };
 
+// Persistent: each workgroup takes items blockIdx.x, + gridDim.x, ..., with the next item's q, k
+// rows, g and beta read into registers while the current one computes.
 __global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(PrepArgs a) {
   __shared__ __attribute__((aligned(16))) PrepSmem sm;
-  const int ci = blockIdx.x, h = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g4 = lane >> 4, c = lane & 15;
-  const int S = a.S, t0 = ci * CH;
-  const size_t row0 = (size_t)h * S;
-  float* rec = a.ws + ((size_t)h * a.nch + ci) * REC;
-
-  // raw q, k rows (zero past the end of the prompt); g_cum by a wave scan
+  const int S = a.S;
+  // raw q, k rows 8j + (tid >> 5), float4 column tid & 31; g and beta of token lane (wave 0);
+  // reads past the end of the prompt return zeros
+  const int qk_off = (tid >> 5) * (D * 4) + (tid & 31) * 16;
+  float4 pq[8], pk[8];
+  float pg = 0.f, pb = 0.f;
+  auto fetch = [&](int item) {
+    const int h = item / a.nch, t0 = (item - h * a.nch) * CH;
+    const size_t r0 = (size_t)h * S + t0;
+    const int rest = S - t0;
+    const rsrc_t rq = make_rsrc(a.q + r0 * D, rest * D * 4);
+    const rsrc_t rk = make_rsrc(a.k + r0 * D, rest * D * 4);
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int i = 8 * j + (tid >> 5), c4 = tid & 31;
-    const bool ok = t0 + i < S;
-    const size_t r = ok ? row0 + t0 + i : row0;
-    const float4 qv = reinterpret_cast<const float4*>(a.q + r * D)[c4];
-    const float4 kv = reinterpret_cast<const float4*>(a.k + r * D)[c4];
-    const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
-    st4(sm.u.q + i * RS + 4 * c4, ok ? qv : z4);
-    st4(sm.k + i * RS + 4 * c4, ok ? kv : z4);
-  }
-  if (wv == 0) {
-    const bool ok = t0 + lane < S;
-    const size_t r = ok ? row0 + t0 + lane : row0;
-    const float gv = a.g[r], bv = a.beta[r];
-    float gi = ok ? gv : 0.f;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const float o = __shfl_up(gi, d, 64);
-      if (lane >= d) gi += o;
+    for (int j = 0; j < 8; ++j) {
+      pq[j] = bload4(rq, qk_off + 4096 * j, 0);
+      pk[j] = bload4(rk, qk_off + 4096 * j, 0);
     }
-    sm.gcum[lane] = gi;
-    sm.bt[lane] = ok ? bv : 0.f;
-  }
-  __syncthreads();
-  {  // row norms, 4 threads per row
-    const int i = tid >> 2, part = tid & 3;
-    const float* qp = sm.u.q + i * RS + 32 * part;
-    const float* kp = sm.k + i * RS + 32 * part;
-    float sq = 0.f, sk = 0.f;
-#pragma unroll
-    for (int j = 0; j < 32; j += 4) {
-      const float4 x = ld4(qp + j), y = ld4(kp + j);
-      sq += x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w;
-      sk += y.x * y.x + y.y * y.y + y.z * y.z + y.w * y.w;
+    if (wv == 0) {
+      pg = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                         make_rsrc(a.g + r0, rest * 4), lane * 4, 0, 0));
+      pb = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                         make_rsrc(a.beta + r0, rest * 4), lane * 4, 0, 0));
     }
-    sq += __shfl_xor(sq, 1, 64);
-    sq += __shfl_xor(sq, 2, 64);
-    sk += __shfl_xor(sk, 1, 64);
-    sk += __shfl_xor(sk, 2, 64);
-    if (part == 0) {
-      sm.rq[i] = rsqrtf(sq + kNormEps);
-      sm.rk[i] = rsqrtf(sk + kNormEps);
+  };
+  if (blockIdx.x < a.items) fetch(blockIdx.x);
+  for (int item = blockIdx.x; item < a.items; item += gridDim.x) {
+    const int h = item / a.nch, ci = item - h * a.nch;
+    float* rec = a.ws + ((size_t)h * a.nch + ci) * REC;
+    __syncthreads();  // the previous item is done with LDS
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      st4(sm.u.q + (8 * j + (tid >> 5)) * RS + 4 * (tid & 31), pq[j]);
+      st4(sm.k + (8 * j + (tid >> 5)) * RS + 4 * (tid & 31), pk[j]);
     }
-  }
-  __syncthreads();
-  if (wv == 0) {
-    const float gi = sm.gcum[lane], tot = sm.gcum[CH - 1], rk = sm.rk[lane];
-    st4(rec + REC_SC + 4 * lane, make_float4(sm.rq[lane] * kQScale * __expf(gi), rk * __expf(gi),
-                                             rk * __expf(tot - gi), sm.bt[lane]));
-    if (lane == 0) rec[REC_ET] = __expf(tot);
-  }
-  if (wv >= 2) {  // the blocks above the diagonal of T and intra are zero
-    const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int e = tid - 128; e < 6 * 64; e += 128) {
-      const int b = e >> 6, row = (e >> 2) & 15, c4 = e & 3;
-      const int I = b < 3 ? 0 : b < 5 ? 1 : 2, J = b < 3 ? b + 1 : b < 5 ? b - 1 : 3;
-      const int off = (16 * I + row) * CH + 16 * J + 4 * c4;
-      st4(rec + REC_T + off, z4);
-      st4(rec + REC_I + off, z4);
-    }
-  }
-  // intra[i][j] = (q_i . k_j) rq_i rk_j / sqrt(128) dm(i, j) for i >= j
-  for (int t = wv; t < 10; t += 4) {
-    int I, J;
-    lower_block(t, I, J);
-    f32x4 acc = zero4();
-    tile16<D>(acc, sm.u.q + (16 * I + c) * RS, sm.k + (16 * J + c) * RS);
-    const int j = 16 * J + c;
-    const float rkj = sm.rk[j], gj = sm.gcum[j];
+    if (wv == 0) {  // g_cum by a wave scan
+      float gi = pg;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int i = 16 * I + 4 * g4 + r;
-      rec[REC_I + i * CH + j] =
-          i >= j ? sm.rq[i] * kQScale * rkj * acc[r] * __expf(sm.gcum[i] - gj) : 0.f;
-    }
-  }
-  __syncthreads();  // the q rows are consumed: A and T take their place
-  // A[i][j] = -beta_i (k_i . k_j) rk_i rk_j dm(i, j) for i > j
-  for (int t = wv; t < 10; t += 4) {
-    int I, J;
-    lower_block(t, I, J);
-    f32x4 acc = zero4();
-    tile16<D>(acc, sm.k + (16 * I + c) * RS, sm.k + (16 * J + c) * RS);
-    const int j = 16 * J + c;
-    const float rkj = sm.rk[j], gj = sm.gcum[j];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int i = 16 * I + 4 * g4 + r;
-      sm.u.at.a[i * MS + j] =
-          i > j ? -sm.bt[i] * sm.rk[i] * rkj * acc[r] * __expf(sm.gcum[i] - gj) : 0.f;
-    }
-  }
-  __syncthreads();
-  if (wv == 0) {
-    // T's diagonal blocks by forward substitution, lane 16 b + j holding column j of block b:
-    // T_bb[i][j] = sum_{m < i} A_bb[i][m] T_bb[m][j] for i > j (A_bb is zero on and above
-    // its diagonal, so the row reads may run past m = i - 1)
-    const int b = g4, j = c;
-    const float* ab = sm.u.at.a + 16 * b * MS + 16 * b;
-    float col[16];
-#pragma unroll
-    for (int m = 0; m < 16; ++m) col[m] = m == j ? 1.f : 0.f;
-#pragma unroll
-    for (int i = 1; i < 16; ++i) {
-      float s0 = 0.f, s1 = 0.f;
-#pragma unroll
-      for (int m4 = 0; m4 < i; m4 += 4) {
-        const float4 av = ld4(ab + i * MS + m4);
-        s0 += av.x * col[m4] + av.z * col[m4 + 2];
-        s1 += av.y * col[m4 + 1] + av.w * col[m4 + 3];
+      for (int d = 1; d < 64; d <<= 1) {
+        const float o = __shfl_up(gi, d, 64);
+        if (lane >= d) gi += o;
       }
-      if (i > j) col[i] = s0 + s1;
+      sm.gcum[lane] = gi;
+      sm.bt[lane] = pb;
     }
+    fetch(min(item + (int)gridDim.x, a.items - 1));  // unconditional: no branch forces a wait
+    __syncthreads();
+    {  // row norms, 4 threads per row
+      const int i = tid >> 2, part = tid & 3;
+      const float* qp = sm.u.q + i * RS + 32 * part;
+      const float* kp = sm.k + i * RS + 32 * part;
+      float sq = 0.f, sk = 0.f;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      sm.u.at.t[(16 * b + i) * MS + 16 * b + j] = col[i];
-      rec[REC_T + (16 * b + i) * CH + 16 * b + j] = col[i];
-    }
-  }
-  __syncthreads();
-  if (wv < 3) {
-    // block column Jb = wave: T_IJ = T_II sum_{M = J}^{I - 1} A_IM T_MJ for I > J; each T_MJ
-    // stays in registers (acc layout) as the B operand of the next block row
-    const int Jb = wv;
-    const float* am = sm.u.at.a;
-    const float* tm = sm.u.at.t;
-    f32x4 tj[4];
-#pragma unroll
-    for (int M = 0; M < 3; ++M) {
-      tj[M] = zero4();
-      if (M == Jb) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) tj[M][r] = tm[(16 * M + 4 * g4 + r) * MS + 16 * M + c];
+      for (int j = 0; j < 32; j += 4) {
+        const float4 x = ld4(qp + j), y = ld4(kp + j);
+        sq += x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w;
+        sk += y.x * y.x + y.y * y.y + y.z * y.z + y.w * y.w;
+      }
+      sq += __shfl_xor(sq, 1, 64);
+      sq += __shfl_xor(sq, 2, 64);
+      sk += __shfl_xor(sk, 1, 64);
+      sk += __shfl_xor(sk, 2, 64);
+      if (part == 0) {
+        sm.rq[i] = rsqrtf(sq + kNormEps);
+        sm.rk[i] = rsqrtf(sk + kNormEps);
       }
     }
+    __syncthreads();
+    if (wv == 0) {
+      const float gi = sm.gcum[lane], tot = sm.gcum[CH - 1], rk = sm.rk[lane];
+      st4(rec + REC_SC + 4 * lane, make_float4(sm.rq[lane] * kQScale * __expf(gi), rk * __expf(gi),
+                                               rk * __expf(tot - gi), sm.bt[lane]));
+      if (lane == 0) rec[REC_ET] = __expf(tot);
+    }
+    if (wv >= 2) {  // the blocks above the diagonal of T and intra are zero
+      const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int e = tid - 128; e < 6 * 64; e += 128) {
+        const int b = e >> 6, row = (e >> 2) & 15, c4 = e & 3;
+        const int I = b < 3 ? 0 : b < 5 ? 1 : 2, J = b < 3 ? b + 1 : b < 5 ? b - 1 : 3;
+        const int off = (16 * I + row) * CH + 16 * J + 4 * c4;
+        st4(rec + REC_T + off, z4);
+        st4(rec + REC_I + off, z4);
+      }
+    }
+    // intra[i][j] = (q_i . k_j) rq_i rk_j / sqrt(128) dm(i, j) for i >= j
+    for (int t = wv; t < 10; t += 4) {
+      int I, J;
+      lower_block(t, I, J);
+      f32x4 acc = zero4();
+      tile16<D>(acc, sm.u.q + (16 * I + c) * RS, sm.k + (16 * J + c) * RS);
+      const int j = 16 * J + c;
+      const float rkj = sm.rk[j], gj = sm.gcum[j];
 #pragma unroll
-    for (int I = 1; I < 4; ++I) {
-      if (I <= Jb) continue;
-      f32x4 R = zero4();
+      for (int r = 0; r < 4; ++r) {
+        const int i = 16 * I + 4 * g4 + r;
+        rec[REC_I + i * CH + j] =
+            i >= j ? sm.rq[i] * kQScale * rkj * acc[r] * __expf(sm.gcum[i] - gj) : 0.f;
+      }
+    }
+    __syncthreads();  // the q rows are consumed: A and T take their place
+    // A[i][j] = -beta_i (k_i . k_j) rk_i rk_j dm(i, j) for i > j
+    for (int t = wv; t < 10; t += 4) {
+      int I, J;
+      lower_block(t, I, J);
+      f32x4 acc = zero4();
+      tile16<D>(acc, sm.k + (16 * I + c) * RS, sm.k + (16 * J + c) * RS);
+      const int j = 16 * J + c;
+      const float rkj = sm.rk[j], gj = sm.gcum[j];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = 16 * I + 4 * g4 + r;
+        sm.u.at.a[i * MS + j] =
+            i > j ? -sm.bt[i] * sm.rk[i] * rkj * acc[r] * __expf(sm.gcum[i] - gj) : 0.f;
+      }
+    }
+    __syncthreads();
+    if (wv == 0) {
+      // T's diagonal blocks by forward substitution, lane 16 b + j holding column j of block b:
+      // T_bb[i][j] = sum_{m < i} A_bb[i][m] T_bb[m][j] for i > j (A_bb is zero on and above
+      // its diagonal, so the row reads may run past m = i - 1)
+      const int b = g4, j = c;
+      const float* ab = sm.u.at.a + 16 * b * MS + 16 * b;
+      float col[16];
+#pragma unroll
+      for (int m = 0; m < 16; ++m) col[m] = m == j ? 1.f : 0.f;
+#pragma unroll
+      for (int i = 1; i < 16; ++i) {
+        float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+        for (int m4 = 0; m4 < i; m4 += 4) {
+          const float4 av = ld4(ab + i * MS + m4);
+          s0 += av.x * col[m4] + av.z * col[m4 + 2];
+          s1 += av.y * col[m4 + 1] + av.w * col[m4 + 3];
+        }
+        if (i > j) col[i] = s0 + s1;
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        sm.u.at.t[(16 * b + i) * MS + 16 * b + j] = col[i];
+        rec[REC_T + (16 * b + i) * CH + 16 * b + j] = col[i];
+      }
+    }
+    __syncthreads();
+    if (wv < 3) {
+      // block column Jb = wave: T_IJ = T_II sum_{M = J}^{I - 1} A_IM T_MJ for I > J; each T_MJ
+      // stays in registers (acc layout) as the B operand of the next block row
+      const int Jb = wv;
+      const float* am = sm.u.at.a;
+      const float* tm = sm.u.at.t;
+      f32x4 tj[4];
 #pragma unroll
       for (int M = 0; M < 3; ++M) {
-        if (M < Jb || M >= I) continue;
-        const float4 av = ld4(am + (16 * I + c) * MS + 16 * M + 4 * g4);
-        R = mfma16(av.x, tj[M][0], R);
-        R = mfma16(av.y, tj[M][1], R);
-        R = mfma16(av.z, tj[M][2], R);
-        R = mfma16(av.w, tj[M][3], R);
-      }
-      const float4 tv = ld4(tm + (16 * I + c) * MS + 16 * I + 4 * g4);
-      f32x4 X = zero4();
-      X = mfma16(tv.x, R[0], X);
-      X = mfma16(tv.y, R[1], X);
-      X = mfma16(tv.z, R[2], X);
-      X = mfma16(tv.w, R[3], X);
-      tj[I] = X;
+        tj[M] = zero4();
+        if (M == Jb) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) rec[REC_T + (16 * I + 4 * g4 + r) * CH + 16 * Jb + c] = X[r];
+          for (int r = 0; r < 4; ++r) tj[M][r] = tm[(16 * M + 4 * g4 + r) * MS + 16 * M + c];
+        }
+      }
+#pragma unroll
+      for (int I = 1; I < 4; ++I) {
+        if (I <= Jb) continue;
+        f32x4 R = zero4();
+#pragma unroll
+        for (int M = 0; M < 3; ++M) {
+          if (M < Jb || M >= I) continue;
+          const float4 av = ld4(am + (16 * I + c) * MS + 16 * M + 4 * g4);
+          R = mfma16(av.x, tj[M][0], R);
+          R = mfma16(av.y, tj[M][1], R);
+          R = mfma16(av.z, tj[M][2], R);
+          R = mfma16(av.w, tj[M][3], R);
+        }
+        const float4 tv = ld4(tm + (16 * I + c) * MS + 16 * I + 4 * g4);
+        f32x4 X = zero4();
+        X = mfma16(tv.x, R[0], X);
+        X = mfma16(tv.y, R[1], X);
+        X = mfma16(tv.z, R[2], X);
+        X = mfma16(tv.w, R[3], X);
+        tj[I] = X;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) rec[REC_T + (16 * I + 4 * g4 + r) * CH + 16 * Jb + c] = X[r];
+      }
     }
   }
 }
@@ -524,15 +543,14 @@ __global__ __launch_bounds__(256, 1) void dn_chunk_scan_kernel(ScanArgs a) {
   // The next chunk's inputs are read into registers while the current chunk computes, in
   // parts issued between the products (reading a chunk's 104 KB at once stalls every wave on
   // the memory pipeline), and each goes to LDS as soon as the current chunk is done with that
-  // buffer, which keeps the registers held short:
-  //   part 0..7    q rows 8j + (tid >> 5), float4 column tid & 31     issued in Pa, stored after Pb
-  //   part 8..9    this block's v: row tid >> 2, columns 8 (tid & 3)  issued in Pa, stored in Pc
-  //   part 10..13  T (float4 tid + 256 j)                              issued in Pa, stored in Pc
-  //   part 14      scales (wave lane = token) and e^tot                issued in Pa, stored in Pc
-  //                (e^tot at the next chunk's start: the state update reads the current one)
-  //   part 15..22  k rows, as q                                        issued in Pa, stored at start
-  //   part 23..26  intra (float4 tid + 256 j)                          issued in Pb, stored at start
-  // Rows past the end of the prompt read row 0 here and are zeroed when stored.
+  // buffer, which keeps the registers held short (issued in / stored in):
+  //   part 0..7    q rows 8j + (tid >> 5), float4 column tid & 31      Pa / Pb
+  //   part 8..9    this block's v: row tid >> 2, columns 8 (tid & 3)   Pa / Pc
+  //   part 10..13  T (float4 tid + 256 j)                               Pa / Pc
+  //   part 14      scales (wave lane = token) and e^tot                 Pa / Pc, and e^tot at the
+  //                next chunk's start (the state update reads the current one)
+  //   part 15..22  k rows, as q                                         Pa / next chunk's start
+  //   part 23..26  intra (float4 tid + 256 j)                           Pb / next chunk's start
   float4 pq[8], pk[8], pv[2], pt[4], pi[4];
   float4 psc = make_float4(0.f, 0.f, 0.f, 0.f);
   float pet = 0.f;
@@ -554,7 +572,8 @@ __global__ __launch_bounds__(256, 1) void dn_chunk_scan_kernel(ScanArgs a) {
       psc = bload4(make_rsrc(rec, REC * 4), lane * 16, REC_SC * 4);
       pet = rec[REC_ET];
     } else if (part < 23) {
-      pk[part - 15] = bload4(make_rsrc(a.k + (row0 + t0) * D, rest), qk_off + 4096 * (part - 15), 0);
+      pk[part - 15] =
+          bload4(make_rsrc(a.k + (row0 + t0) * D, rest), qk_off + 4096 * (part - 15), 0);
     } else if (part < 27) {
       pi[part - 23] = bload4(make_rsrc(rec, REC * 4), tid * 16, (REC_I + 1024 * (part - 23)) * 4);
     }
@@ -627,6 +646,8 @@ __global__ __launch_bounds__(256, 1) void dn_chunk_scan_kernel(ScanArgs a) {
   }
 }
 
+constexpr int kPrepGrid = 512;  // two prep workgroups per CU (70 KB of LDS each)
+
 // S * 512 bytes must fit the 32-bit buffer offsets
 bool shape_ok(int v_heads, int S) {
   return v_heads >= 1 && v_heads <= 65535 && S >= 1 && S <= (1 << 22) &&
@@ -656,8 +677,9 @@ extern "C" int npn_deltanet_chunked_prefill(const float* state, const float* que
   const int nch = (S + CH - 1) / CH;
   hipStream_t st = static_cast<hipStream_t>(stream);
   float* ws = static_cast<float*>(workspace);
-  hipLaunchKernelGGL(dn_chunk_prep_kernel, dim3(nch, v_heads), dim3(256), 0, st,
-                     PrepArgs{query, key, g, beta, ws, S, nch});
+  const int items = nch * v_heads;
+  hipLaunchKernelGGL(dn_chunk_prep_kernel, dim3(std::min(items, kPrepGrid)), dim3(256), 0, st,
+                     PrepArgs{query, key, g, beta, ws, S, nch, items});
   const int groups = (v_heads + 7) / 8;
   hipLaunchKernelGGL(dn_chunk_scan_kernel, dim3(groups * 8 * NCB), dim3(256), 0, st,
                      ScanArgs{state, query, key, value, ws, out, new_state, S, nch, v_heads});

@@ -48,6 +48,11 @@ def test_size_queries():
     assert q("npn_accept_workspace_size", 32, 0, 151936) == 0
     assert q("npn_fp8_matmul_workspace_size", 8, 5120, 17408) >= 0
     assert q("npn_fp8_matmul_workspace_size", 8, 100, 17408) == 0
+    # chunked prefill: one 34,048-byte record per (head, 64-token chunk), partial chunks count
+    assert q("npn_deltanet_chunked_workspace_size", 48, 4096) == 48 * 64 * 34048
+    assert q("npn_deltanet_chunked_workspace_size", 3, 65) == 3 * 2 * 34048
+    assert q("npn_deltanet_chunked_workspace_size", 0, 64) == 0
+    assert q("npn_deltanet_chunked_workspace_size", 1, (1 << 22) + 1) == 0     # 32-bit offsets
 
 
 def test_ops_register_and_propagate_shapes():

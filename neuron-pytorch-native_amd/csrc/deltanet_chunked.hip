@@ -95,43 +95,6 @@ __device__ __forceinline__ void tile16(f32x4& acc, const float* pa, const float*
   }
 }
 
-// Two tiles, acc1 over K1 and acc2 over K2 (K1 <= K2): the operands of both are read first,
-// then the two accumulation chains run interleaved; pre(u) runs before the u-th group of
-// products (global reads issued there overlap the products).
-template <int K1, int K2, typename Pre>
-__device__ __forceinline__ void tile16x2(f32x4& acc1, const float* pa1, const float* pb1,
-                                         f32x4& acc2, const float* pa2, const float* pb2,
-                                         Pre&& pre) {
-  const int g = (threadIdx.x >> 4) & 3;
-  float4 a1[K1 / 16], b1[K1 / 16], a2[K2 / 16], b2[K2 / 16];
-#pragma unroll
-  for (int u = 0; u < K1 / 16; ++u) {
-    a1[u] = ld4(pa1 + g * (K1 / 4) + 4 * u);
-    b1[u] = ld4(pb1 + g * (K1 / 4) + 4 * u);
-  }
-#pragma unroll
-  for (int u = 0; u < K2 / 16; ++u) {
-    a2[u] = ld4(pa2 + g * (K2 / 4) + 4 * u);
-    b2[u] = ld4(pb2 + g * (K2 / 4) + 4 * u);
-  }
-  __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int u = 0; u < K2 / 16; ++u) {
-    pre(u);
-    __builtin_amdgcn_sched_barrier(0);
-    if (u < K1 / 16) {
-      acc1 = mfma16(a1[u].x, b1[u].x, acc1);
-      acc1 = mfma16(a1[u].y, b1[u].y, acc1);
-      acc1 = mfma16(a1[u].z, b1[u].z, acc1);
-      acc1 = mfma16(a1[u].w, b1[u].w, acc1);
-    }
-    acc2 = mfma16(a2[u].x, b2[u].x, acc2);
-    acc2 = mfma16(a2[u].y, b2[u].y, acc2);
-    acc2 = mfma16(a2[u].z, b2[u].z, acc2);
-    acc2 = mfma16(a2[u].w, b2[u].w, acc2);
-  }
-}
-
 // The 10 lower 16 x 16 blocks (I >= J) of a 64 x 64 matrix, t = I (I + 1) / 2 + J.
 __device__ __forceinline__ void lower_block(int t, int& I, int& J) {
   I = t < 1 ? 0 : t < 3 ? 1 : t < 6 ? 2 : 3;
@@ -382,117 +345,109 @@ struct ScanSmem {
   float etot;
 };
 
-// Wave roles: column half J = wave & 1 and the row blocks {I1, I2} = {0, 3} (waves 0, 1) or
-// {1, 2} (waves 2, 3), which balances the triangular products.
+// Wave w of the 8 owns row block I of the chunk and column half J = w & 1 of the block's 32
+// state columns: I = 3 - ((w >> 1) & 1) for w < 4, (w >> 1) & 1 for w >= 4. Waves w and w + 4
+// share a SIMD, so each SIMD holds row blocks {3, 0} or {2, 1}: the triangular products
+// (T Z, intra v_new) are balanced per SIMD, and its two waves cover each other's waits. The
+// older wave, which wins the SIMD's issue arbitration, takes the longer triangular chain.
 
-// X = (raw k) S and O = (raw q) S for the wave's rows; Z = beta (v - sk1 X) into zT; O *= sq.
-// pre(u) issues the u-th part of the next chunk's global reads between the products.
-template <int I1, int I2, typename Pre>
-__device__ __forceinline__ void scan_state_products(ScanSmem& sm, int J, f32x4& o1, f32x4& o2,
+// Pa: X = (raw k) S and O = (raw q) S for rows of block I; Z = beta (v - sk1 X) into zT;
+// O *= sq. pre(u) issues part of the next chunk's reads between the products.
+template <typename Pre>
+__device__ __forceinline__ void scan_state_products(ScanSmem& sm, int I, int J, f32x4& o,
                                                     Pre&& pre) {
   const int lane = threadIdx.x & 63, g4 = lane >> 4, c = lane & 15;
-  f32x4 x1 = zero4(), x2 = zero4();
-  o1 = zero4();
-  o2 = zero4();
+  f32x4 x = zero4();
+  o = zero4();
   const float* pb = sm.sT + (16 * J + c) * RS + 32 * g4;
-  const float* pk1 = sm.k + (16 * I1 + c) * RS + 32 * g4;
-  const float* pk2 = sm.k + (16 * I2 + c) * RS + 32 * g4;
-  const float* pq1 = sm.q + (16 * I1 + c) * RS + 32 * g4;
-  const float* pq2 = sm.q + (16 * I2 + c) * RS + 32 * g4;
-  // operands double-buffered: step u + 1 is read while step u's 16 products run
-  float4 nb = ld4(pb), nk1 = ld4(pk1), nk2 = ld4(pk2), nq1 = ld4(pq1), nq2 = ld4(pq2);
+  const float* pk = sm.k + (16 * I + c) * RS + 32 * g4;
+  const float* pq = sm.q + (16 * I + c) * RS + 32 * g4;
+  // operands double-buffered: step u + 1 is read while step u's products run
+  float4 nb = ld4(pb), nk = ld4(pk), nq = ld4(pq);
 #pragma unroll
   for (int u = 0; u < 8; ++u) {
-    const float4 b = nb, k1 = nk1, k2 = nk2, q1 = nq1, q2 = nq2;
+    const float4 b = nb, kv = nk, qv = nq;
     if (u < 7) {
       nb = ld4(pb + 4 * u + 4);
-      nk1 = ld4(pk1 + 4 * u + 4);
-      nk2 = ld4(pk2 + 4 * u + 4);
-      nq1 = ld4(pq1 + 4 * u + 4);
-      nq2 = ld4(pq2 + 4 * u + 4);
+      nk = ld4(pk + 4 * u + 4);
+      nq = ld4(pq + 4 * u + 4);
     }
     pre(u);
     __builtin_amdgcn_sched_barrier(0);
-    x1 = mfma16(k1.x, b.x, x1); x2 = mfma16(k2.x, b.x, x2);
-    o1 = mfma16(q1.x, b.x, o1); o2 = mfma16(q2.x, b.x, o2);
-    x1 = mfma16(k1.y, b.y, x1); x2 = mfma16(k2.y, b.y, x2);
-    o1 = mfma16(q1.y, b.y, o1); o2 = mfma16(q2.y, b.y, o2);
-    x1 = mfma16(k1.z, b.z, x1); x2 = mfma16(k2.z, b.z, x2);
-    o1 = mfma16(q1.z, b.z, o1); o2 = mfma16(q2.z, b.z, o2);
-    x1 = mfma16(k1.w, b.w, x1); x2 = mfma16(k2.w, b.w, x2);
-    o1 = mfma16(q1.w, b.w, o1); o2 = mfma16(q2.w, b.w, o2);
+    x = mfma16(kv.x, b.x, x);
+    o = mfma16(qv.x, b.x, o);
+    x = mfma16(kv.y, b.y, x);
+    o = mfma16(qv.y, b.y, o);
+    x = mfma16(kv.z, b.z, x);
+    o = mfma16(qv.z, b.z, o);
+    x = mfma16(kv.w, b.w, x);
+    o = mfma16(qv.w, b.w, o);
   }
-#pragma unroll
-  for (int p = 0; p < 2; ++p) {
-    const int i0 = 16 * (p == 0 ? I1 : I2) + 4 * g4;
-    const f32x4& x = p == 0 ? x1 : x2;
-    f32x4& o = p == 0 ? o1 : o2;
-    float* zp = sm.zT + (16 * J + c) * MS + i0;
-    const float4 v = ld4(zp);
-    const float4 s0 = sm.sc[i0], s1 = sm.sc[i0 + 1], s2 = sm.sc[i0 + 2], s3 = sm.sc[i0 + 3];
-    st4(zp, make_float4(s0.w * (v.x - s0.y * x[0]), s1.w * (v.y - s1.y * x[1]),
-                        s2.w * (v.z - s2.y * x[2]), s3.w * (v.w - s3.y * x[3])));
-    o[0] *= s0.x;
-    o[1] *= s1.x;
-    o[2] *= s2.x;
-    o[3] *= s3.x;
+  const int i0 = 16 * I + 4 * g4;
+  float* zp = sm.zT + (16 * J + c) * MS + i0;
+  const float4 v = ld4(zp);
+  const float4 s0 = sm.sc[i0], s1 = sm.sc[i0 + 1], s2 = sm.sc[i0 + 2], s3 = sm.sc[i0 + 3];
+  st4(zp, make_float4(s0.w * (v.x - s0.y * x[0]), s1.w * (v.y - s1.y * x[1]),
+                      s2.w * (v.z - s2.y * x[2]), s3.w * (v.w - s3.y * x[3])));
+  o[0] *= s0.x;
+  o[1] *= s1.x;
+  o[2] *= s2.x;
+  o[3] *= s3.x;
+}
+
+// acc += A B over K = 16 (I + 1) (a triangular left factor): the wave-uniform I picks the
+// instance.
+__device__ __forceinline__ void tile16_tri(f32x4& acc, int I, const float* pa, const float* pb) {
+  switch (I) {
+    case 0: tile16<16>(acc, pa, pb); break;
+    case 1: tile16<32>(acc, pa, pb); break;
+    case 2: tile16<48>(acc, pa, pb); break;
+    default: tile16<64>(acc, pa, pb); break;
   }
 }
 
-// v_new rows of blocks I1 and I2 = T Z (K = 16 (I + 1): T is lower triangular) into vnT, vsT.
-template <int I1, int I2, typename Pre>
-__device__ __forceinline__ void scan_vnew(ScanSmem& sm, int J, Pre&& pre) {
+// Pb: v_new rows of block I = T Z into vnT and (scaled by sk2) vsT.
+__device__ __forceinline__ void scan_vnew(ScanSmem& sm, int I, int J) {
   const int lane = threadIdx.x & 63, g4 = lane >> 4, c = lane & 15;
-  f32x4 v1 = zero4(), v2 = zero4();
-  const float* zb = sm.zT + (16 * J + c) * MS;
-  tile16x2<16 * (I1 + 1), 16 * (I2 + 1)>(v1, sm.t + (16 * I1 + c) * MS, zb,
-                                         v2, sm.t + (16 * I2 + c) * MS, zb, pre);
-#pragma unroll
-  for (int p = 0; p < 2; ++p) {
-    const f32x4& acc = p == 0 ? v1 : v2;
-    const int i0 = 16 * (p == 0 ? I1 : I2) + 4 * g4, o = (16 * J + c) * MS + i0;
-    st4(sm.vnT + o, make_float4(acc[0], acc[1], acc[2], acc[3]));
-    st4(sm.vsT + o, make_float4(acc[0] * sm.sc[i0].z, acc[1] * sm.sc[i0 + 1].z,
-                                acc[2] * sm.sc[i0 + 2].z, acc[3] * sm.sc[i0 + 3].z));
-  }
+  f32x4 acc = zero4();
+  tile16_tri(acc, I, sm.t + (16 * I + c) * MS, sm.zT + (16 * J + c) * MS);
+  const int i0 = 16 * I + 4 * g4, o = (16 * J + c) * MS + i0;
+  st4(sm.vnT + o, make_float4(acc[0], acc[1], acc[2], acc[3]));
+  st4(sm.vsT + o, make_float4(acc[0] * sm.sc[i0].z, acc[1] * sm.sc[i0 + 1].z,
+                              acc[2] * sm.sc[i0 + 2].z, acc[3] * sm.sc[i0 + 3].z));
 }
 
-// out rows of blocks I1 and I2 = O + intra v_new, written where the token exists.
-template <int I1, int I2, typename Pre>
-__device__ __forceinline__ void scan_out(ScanSmem& sm, float* orow, int J, f32x4 o1, f32x4 o2,
-                                         int nvalid, Pre&& pre) {
+// Pc: out rows of block I = O + intra v_new, written where the token exists.
+__device__ __forceinline__ void scan_out(ScanSmem& sm, float* orow, int I, int J, f32x4 o,
+                                         int nvalid) {
   const int lane = threadIdx.x & 63, g4 = lane >> 4, c = lane & 15;
-  const float* vb = sm.vnT + (16 * J + c) * MS;
-  tile16x2<16 * (I1 + 1), 16 * (I2 + 1)>(o1, sm.in + (16 * I1 + c) * MS, vb,
-                                         o2, sm.in + (16 * I2 + c) * MS, vb, pre);
+  tile16_tri(o, I, sm.in + (16 * I + c) * MS, sm.vnT + (16 * J + c) * MS);
 #pragma unroll
-  for (int p = 0; p < 2; ++p) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int i = 16 * (p == 0 ? I1 : I2) + 4 * g4 + r;
-      if (i < nvalid) orow[(size_t)i * D + 16 * J + c] = p == 0 ? o1[r] : o2[r];
-    }
+  for (int r = 0; r < 4; ++r) {
+    const int i = 16 * I + 4 * g4 + r;
+    if (i < nvalid) orow[(size_t)i * D + 16 * J + c] = o[r];
   }
 }
 
 // S'^T[col][kk] = e^tot S^T[col][kk] + sum_i (sk2 v_new)^T[col][i] k[i][kk], for the wave's
-// column half and the four 16-blocks of kk from P0; in place (each element is read and
+// column half and the two 16-blocks of kk from P0; in place (each element is read and
 // written by one lane). Group g takes the tokens i = 8 (s >> 1) + 4 (g & 1) + 2 (g >> 1) +
 // (s & 1) at step s, so the column reads of k by the two groups of a half-wave fall 4 rows
 // apart, in opposite halves of the LDS banks; the reads of 4 steps are issued while the
 // previous 4 steps' products run.
 __device__ __forceinline__ void scan_state_update(ScanSmem& sm, int J, int P0) {
+  constexpr int NP = 2;
   const int lane = threadIdx.x & 63, g4 = lane >> 4, c = lane & 15;
   const float et = sm.etot;
-  f32x4 s[4];
+  f32x4 s[NP];
 #pragma unroll
-  for (int p = 0; p < 4; ++p)
+  for (int p = 0; p < NP; ++p)
 #pragma unroll
     for (int r = 0; r < 4; ++r) s[p][r] = sm.sT[(16 * J + 4 * g4 + r) * RS + 16 * (P0 + p) + c];
   const int i0 = 4 * (g4 & 1) + 2 * (g4 >> 1);
   const float* va = sm.vsT + (16 * J + c) * MS + i0;
   const float* kc = sm.k + i0 * RS + 16 * P0 + c;
-  float ae[2][4], kb[2][4][4];
+  float ae[2][4], kb[2][4][NP];
   auto load = [&](int t, int b) {  // steps 4t .. 4t + 3: tokens 16t + i0 + {0, 1, 8, 9}
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -502,12 +457,12 @@ __device__ __forceinline__ void scan_state_update(ScanSmem& sm, int J, int P0) {
 #pragma unroll
       for (int e = 0; e < 2; ++e)
 #pragma unroll
-        for (int p = 0; p < 4; ++p) kb[b][2 * h + e][p] = kc[(16 * t + 8 * h + e) * RS + 16 * p];
+        for (int p = 0; p < NP; ++p) kb[b][2 * h + e][p] = kc[(16 * t + 8 * h + e) * RS + 16 * p];
     }
   };
   load(0, 0);
 #pragma unroll
-  for (int p = 0; p < 4; ++p) s[p] *= et;
+  for (int p = 0; p < NP; ++p) s[p] *= et;
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
     if (t < 3) load(t + 1, (t + 1) & 1);
@@ -515,15 +470,17 @@ __device__ __forceinline__ void scan_state_update(ScanSmem& sm, int J, int P0) {
 #pragma unroll
     for (int e = 0; e < 4; ++e)
 #pragma unroll
-      for (int p = 0; p < 4; ++p) s[p] = mfma16(ae[t & 1][e], kb[t & 1][e][p], s[p]);
+      for (int p = 0; p < NP; ++p) s[p] = mfma16(ae[t & 1][e], kb[t & 1][e][p], s[p]);
   }
 #pragma unroll
-  for (int p = 0; p < 4; ++p)
+  for (int p = 0; p < NP; ++p)
 #pragma unroll
     for (int r = 0; r < 4; ++r) sm.sT[(16 * J + 4 * g4 + r) * RS + 16 * (P0 + p) + c] = s[p][r];
 }
 
-__global__ __launch_bounds__(256, 1) void dn_chunk_scan_kernel(ScanArgs a) {
+constexpr int kScanThreads = 512;
+
+__global__ __launch_bounds__(kScanThreads, 1) void dn_chunk_scan_kernel(ScanArgs a) {
   __shared__ __attribute__((aligned(16))) ScanSmem sm;
   // workgroup L runs on XCD L % 8: the 4 column blocks of head h all get XCD h % 8
   const int L = blockIdx.x, grp = L / (8 * NCB), rem = L % (8 * NCB);
@@ -532,11 +489,12 @@ __global__ __launch_bounds__(256, 1) void dn_chunk_scan_kernel(ScanArgs a) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int J = wv & 1;
+  const int I = wv < 4 ? 3 - ((wv >> 1) & 1) : (wv >> 1) & 1;
   const int S = a.S;
   const size_t row0 = (size_t)h * S;
   const int c0 = 32 * cb;
 
-  for (int e = tid; e < D * 32; e += 256) {
+  for (int e = tid; e < D * 32; e += kScanThreads) {
     const int kk = e >> 5, cc = e & 31;
     sm.sT[cc * RS + kk] = a.state[((size_t)h * D + kk) * D + c0 + cc];
   }
@@ -544,68 +502,70 @@ __global__ __launch_bounds__(256, 1) void dn_chunk_scan_kernel(ScanArgs a) {
   // parts issued between the products (reading a chunk's 104 KB at once stalls every wave on
   // the memory pipeline), and each goes to LDS as soon as the current chunk is done with that
   // buffer, which keeps the registers held short (issued in / stored in):
-  //   part 0..7    q rows 8j + (tid >> 5), float4 column tid & 31      Pa / Pb
-  //   part 8..9    this block's v: row tid >> 2, columns 8 (tid & 3)   Pa / Pc
-  //   part 10..13  T (float4 tid + 256 j)                               Pa / Pc
-  //   part 14      scales (wave lane = token) and e^tot                 Pa / Pc, and e^tot at the
+  //   part 0..3    q rows (tid >> 5) + 16 j, float4 column tid & 31    Pa / Pb
+  //   part 4       this block's v: row tid >> 3, columns 4 (tid & 7)    Pa / Pc
+  //   part 5..6    T (float4 tid + 512 j)                               Pa / Pc
+  //   part 7       scales (wave 0, lane = token) and e^tot              Pa / Pc, and e^tot at the
   //                next chunk's start (the state update reads the current one)
-  //   part 15..22  k rows, as q                                         Pa / next chunk's start
-  //   part 23..26  intra (float4 tid + 256 j)                           Pb / next chunk's start
-  float4 pq[8], pk[8], pv[2], pt[4], pi[4];
-  float4 psc = make_float4(0.f, 0.f, 0.f, 0.f);
-  float pet = 0.f;
+  //   part 8..11   k rows, as q                                         Pa / next chunk's start
+  //   part 12..13  intra (float4 tid + 512 j)                           Pb / next chunk's start
   // Reads go through buffer descriptors based at the chunk's first row, sized to the end of
   // the prompt, so rows past it read as zeros.
-  const int qk_off = (tid >> 5) * (D * 4) + (tid & 31) * 16;         // + 4096 j
-  const int v_off = (tid >> 2) * (D * 4) + (c0 + 8 * (tid & 3)) * 4;  // + 16 p
+  float4 pq[4], pk[4], pv, pt[2], pi[2];
+  float4 psc = make_float4(0.f, 0.f, 0.f, 0.f);
+  float pet = 0.f;
+  const int qk_off = (tid >> 5) * (D * 4) + (tid & 31) * 16;        // + 8192 j
+  const int v_off = (tid >> 3) * (D * 4) + (c0 + 4 * (tid & 7)) * 4;
   auto fetch_part = [&](int ci, int part) {
     const int t0 = ci * CH;
     const int rest = (S - t0) * (D * 4);
     const float* rec = a.ws + ((size_t)h * a.nch + ci) * REC;
-    if (part < 8) {
-      pq[part] = bload4(make_rsrc(a.q + (row0 + t0) * D, rest), qk_off + 4096 * part, 0);
-    } else if (part < 10) {
-      pv[part - 8] = bload4(make_rsrc(a.v + (row0 + t0) * D, rest), v_off + 16 * (part - 8), 0);
-    } else if (part < 14) {
-      pt[part - 10] = bload4(make_rsrc(rec, REC * 4), tid * 16, (REC_T + 1024 * (part - 10)) * 4);
-    } else if (part == 14) {
+    if (part < 4) {
+      pq[part] = bload4(make_rsrc(a.q + (row0 + t0) * D, rest), qk_off + 8192 * part, 0);
+    } else if (part == 4) {
+      pv = bload4(make_rsrc(a.v + (row0 + t0) * D, rest), v_off, 0);
+    } else if (part < 7) {
+      pt[part - 5] = bload4(make_rsrc(rec, REC * 4), tid * 16, (REC_T + 2048 * (part - 5)) * 4);
+    } else if (part == 7) {
       psc = bload4(make_rsrc(rec, REC * 4), lane * 16, REC_SC * 4);
       pet = rec[REC_ET];
-    } else if (part < 23) {
-      pk[part - 15] =
-          bload4(make_rsrc(a.k + (row0 + t0) * D, rest), qk_off + 4096 * (part - 15), 0);
-    } else if (part < 27) {
-      pi[part - 23] = bload4(make_rsrc(rec, REC * 4), tid * 16, (REC_I + 1024 * (part - 23)) * 4);
+    } else if (part < 12) {
+      pk[part - 8] = bload4(make_rsrc(a.k + (row0 + t0) * D, rest), qk_off + 8192 * (part - 8), 0);
+    } else if (part < 14) {
+      pi[part - 12] =
+          bload4(make_rsrc(rec, REC * 4), tid * 16, (REC_I + 2048 * (part - 12)) * 4);
     }
   };
   auto store_q = [&]() {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) st4(sm.q + (8 * j + (tid >> 5)) * RS + 4 * (tid & 31), pq[j]);
+    for (int j = 0; j < 4; ++j) st4(sm.q + ((tid >> 5) + 16 * j) * RS + 4 * (tid & 31), pq[j]);
   };
   auto store_v_t_sc = [&]() {
-    float* zd = sm.zT + 8 * (tid & 3) * MS + (tid >> 2);
-    zd[0] = pv[0].x; zd[MS] = pv[0].y; zd[2 * MS] = pv[0].z; zd[3 * MS] = pv[0].w;
-    zd[4 * MS] = pv[1].x; zd[5 * MS] = pv[1].y; zd[6 * MS] = pv[1].z; zd[7 * MS] = pv[1].w;
+    float* zd = sm.zT + 4 * (tid & 7) * MS + (tid >> 3);
+    zd[0] = pv.x;
+    zd[MS] = pv.y;
+    zd[2 * MS] = pv.z;
+    zd[3 * MS] = pv.w;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int e = tid + 256 * j, r = e >> 4, c4 = e & 15;
+    for (int j = 0; j < 2; ++j) {
+      const int e = tid + kScanThreads * j, r = e >> 4, c4 = e & 15;
       st4(sm.t + r * MS + 4 * c4, pt[j]);
     }
     if (wv == 0) sm.sc[lane] = psc;
   };
 #pragma unroll
-  for (int part = 0; part < 27; ++part) fetch_part(0, part);
+  for (int part = 0; part < 14; ++part) fetch_part(0, part);
   store_q();
   store_v_t_sc();
-  f32x4 o1, o2;
+  f32x4 o;
   for (int ci = 0; ci < a.nch; ++ci) {
     const int t0 = ci * CH;
     __syncthreads();
 #pragma unroll
-    for (int j = 0; j < 8; ++j) st4(sm.k + (8 * j + (tid >> 5)) * RS + 4 * (tid & 31), pk[j]);
+    for (int j = 0; j < 4; ++j) st4(sm.k + ((tid >> 5) + 16 * j) * RS + 4 * (tid & 31), pk[j]);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int e = tid + 256 * j, r = e >> 4, c4 = e & 15;
+    for (int j = 0; j < 2; ++j) {
+      const int e = tid + kScanThreads * j, r = e >> 4, c4 = e & 15;
       st4(sm.in + r * MS + 4 * c4, pi[j]);
     }
     if (wv == 0 && lane == 0) sm.etot = pet;
@@ -613,34 +573,23 @@ __global__ __launch_bounds__(256, 1) void dn_chunk_scan_kernel(ScanArgs a) {
     // chunk reads itself again, and its late stores only rewrite buffers it no longer reads)
     const int nx = min(ci + 1, a.nch - 1);
     auto pre_a = [&](int u) {
-#pragma unroll
-      for (int d = 0; d < 3; ++d)
-        if (3 * u + d < 23) fetch_part(nx, 3 * u + d);
-    };
-    auto pre_b = [&](int u) {
-      if (u < 2) {
-        fetch_part(nx, 23 + 2 * u);
-        fetch_part(nx, 24 + 2 * u);
-      }
+      fetch_part(nx, u);
+      if (u >= 4) fetch_part(nx, u + 4);
     };
     __syncthreads();
-    if (wv < 2) scan_state_products<0, 3>(sm, J, o1, o2, pre_a);
-    else scan_state_products<1, 2>(sm, J, o1, o2, pre_a);
+    scan_state_products(sm, I, J, o, pre_a);
     __syncthreads();
-    if (wv < 2) scan_vnew<0, 3>(sm, J, pre_b);
-    else scan_vnew<1, 2>(sm, J, pre_b);
+    fetch_part(nx, 12);
+    fetch_part(nx, 13);
+    scan_vnew(sm, I, J);
     store_q();  // q of this chunk was last read in Pa
     __syncthreads();
-    const int nvalid = min(CH, S - t0);
-    float* orow = a.out + (row0 + t0) * D + c0;
-    auto no_pre = [](int) {};
-    if (wv < 2) scan_out<0, 3>(sm, orow, J, o1, o2, nvalid, no_pre);
-    else scan_out<1, 2>(sm, orow, J, o1, o2, nvalid, no_pre);
+    scan_out(sm, a.out + (row0 + t0) * D + c0, I, J, o, min(CH, S - t0));
     store_v_t_sc();  // v (then Z), T and the scales were last read in Pb
-    scan_state_update(sm, J, 4 * (wv >> 1));
+    scan_state_update(sm, J, 2 * (wv >> 1));
   }
   __syncthreads();
-  for (int e = tid; e < D * 32; e += 256) {
+  for (int e = tid; e < D * 32; e += kScanThreads) {
     const int kk = e >> 5, cc = e & 31;
     a.new_state[((size_t)h * D + kk) * D + c0 + cc] = sm.sT[cc * RS + kk];
   }
@@ -681,7 +630,7 @@ extern "C" int npn_deltanet_chunked_prefill(const float* state, const float* que
   hipLaunchKernelGGL(dn_chunk_prep_kernel, dim3(std::min(items, kPrepGrid)), dim3(256), 0, st,
                      PrepArgs{query, key, g, beta, ws, S, nch, items});
   const int groups = (v_heads + 7) / 8;
-  hipLaunchKernelGGL(dn_chunk_scan_kernel, dim3(groups * 8 * NCB), dim3(256), 0, st,
+  hipLaunchKernelGGL(dn_chunk_scan_kernel, dim3(groups * 8 * NCB), dim3(kScanThreads), 0, st,
                      ScanArgs{state, query, key, value, ws, out, new_state, S, nch, v_heads});
   return npn_launch_status();
 }

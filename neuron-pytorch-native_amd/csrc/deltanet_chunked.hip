@@ -332,16 +332,57 @@ struct ScanArgs {
   int Hv;
 };
 
+// Split operands: x = hi + lo with hi = bf16(x), lo = bf16(x - hi), and a product of two
+// split values as hi*hi + hi*lo + lo*hi in bf16 MFMAs accumulating in fp32 (the dropped
+// lo*lo term and lo's rounding leave about 2^-16 relative per product).
+typedef __bf16 bf16x8 __attribute__((__vector_size__(8 * sizeof(__bf16))));
+typedef __bf16 bf16x4 __attribute__((__vector_size__(4 * sizeof(__bf16))));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+constexpr int RB = D + 8;    // LDS row stride (bf16) of the split q, k and S^T rows: 272 bytes
+constexpr int VB = CH + 8;   // ... of the split (sk2 v_new)^T rows: 144 bytes
+
+__device__ __forceinline__ f32x4 mfma3(bf16x8 ah, bf16x8 al, bf16x8 bh, bf16x8 bl, f32x4 c) {
+  c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, c, 0, 0, 0);
+  c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, c, 0, 0, 0);
+  c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, c, 0, 0, 0);
+  return c;
+}
+__device__ __forceinline__ void split4(float4 x, bf16x4& h, bf16x4& l) {
+  h[0] = (__bf16)x.x;
+  h[1] = (__bf16)x.y;
+  h[2] = (__bf16)x.z;
+  h[3] = (__bf16)x.w;
+  l[0] = (__bf16)(x.x - (float)h[0]);
+  l[1] = (__bf16)(x.y - (float)h[1]);
+  l[2] = (__bf16)(x.z - (float)h[2]);
+  l[3] = (__bf16)(x.w - (float)h[3]);
+}
+__device__ __forceinline__ bf16x8 ld8(const __bf16* p) {
+  return *reinterpret_cast<const bf16x8*>(p);
+}
+// ds_read_tr16_b64: in each group of 16 lanes, lane i addresses 4 consecutive 16-bit values
+// of row (i >> 2) of a 4 x 16 block (columns 4 (i & 3) .. + 3) and receives column i of the
+// block's 4 rows.
+__device__ __forceinline__ s16x4 lds_tr16(const __bf16* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(p));
+}
+__device__ __forceinline__ bf16x8 pack8(s16x4 a, s16x4 b) {
+  typedef short s16x8 __attribute__((ext_vector_type(8)));
+  const s16x8 v = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+  return __builtin_bit_cast(bf16x8, v);
+}
+
 struct ScanSmem {
-  float q[CH * RS];      // raw q rows of the chunk
-  float k[CH * RS];      // raw k rows
-  float t[CH * MS];      // T
-  float in[CH * MS];     // intra
-  float sT[32 * RS];     // the state block, transposed: [column][k index]
-  float zT[32 * MS];     // v^T of the chunk, then Z^T
-  float vnT[32 * MS];    // v_new^T
-  float vsT[32 * MS];    // (sk2 v_new)^T
-  float4 sc[CH];         // sq, sk1, sk2, beta
+  __bf16 qh[CH * RB], ql[CH * RB];    // q rows of the chunk, split
+  __bf16 kh[CH * RB], kl[CH * RB];    // k rows, split
+  __bf16 sh[32 * RB], sl[32 * RB];    // the state block transposed ([column][k index]), split
+  __bf16 vsh[32 * VB], vsl[32 * VB];  // (sk2 v_new)^T, split
+  float t[CH * MS];                   // T
+  float in[CH * MS];                  // intra
+  float zT[32 * MS];                  // v^T of the chunk, then Z^T
+  float vnT[32 * MS];                 // v_new^T
+  float4 sc[CH];                      // sq, sk1, sk2, beta
   float etot;
 };
 
@@ -350,38 +391,37 @@ struct ScanSmem {
 // share a SIMD, so each SIMD holds row blocks {3, 0} or {2, 1}: the triangular products
 // (T Z, intra v_new) are balanced per SIMD, and its two waves cover each other's waits. The
 // older wave, which wins the SIMD's issue arbitration, takes the longer triangular chain.
+// The wave also owns state tiles (J, P0) and (J, P0 + 1), P0 = 2 ((w >> 1) & 3), in fp32
+// registers for the whole prompt.
 
-// Pa: X = (raw k) S and O = (raw q) S for rows of block I; Z = beta (v - sk1 X) into zT;
-// O *= sq. pre(u) issues part of the next chunk's reads between the products.
+// Pa: X = (raw k) S and O = (raw q) S for rows of block I (split products over the 128 k
+// indices, step st covering 32 st + 8 g .. + 7 for lane group g); Z = beta (v - sk1 X) into
+// zT; O *= sq. pre(st) issues part of the next chunk's reads between the products.
 template <typename Pre>
 __device__ __forceinline__ void scan_state_products(ScanSmem& sm, int I, int J, f32x4& o,
                                                     Pre&& pre) {
   const int lane = threadIdx.x & 63, g4 = lane >> 4, c = lane & 15;
   f32x4 x = zero4();
   o = zero4();
-  const float* pb = sm.sT + (16 * J + c) * RS + 32 * g4;
-  const float* pk = sm.k + (16 * I + c) * RS + 32 * g4;
-  const float* pq = sm.q + (16 * I + c) * RS + 32 * g4;
-  // operands double-buffered: step u + 1 is read while step u's products run
-  float4 nb = ld4(pb), nk = ld4(pk), nq = ld4(pq);
+  const int ro = (16 * I + c) * RB + 8 * g4, so = (16 * J + c) * RB + 8 * g4;
+  bf16x8 nkh = ld8(sm.kh + ro), nkl = ld8(sm.kl + ro), nqh = ld8(sm.qh + ro),
+         nql = ld8(sm.ql + ro), nsh = ld8(sm.sh + so), nsl = ld8(sm.sl + so);
 #pragma unroll
-  for (int u = 0; u < 8; ++u) {
-    const float4 b = nb, kv = nk, qv = nq;
-    if (u < 7) {
-      nb = ld4(pb + 4 * u + 4);
-      nk = ld4(pk + 4 * u + 4);
-      nq = ld4(pq + 4 * u + 4);
+  for (int st = 0; st < 4; ++st) {
+    const bf16x8 kh = nkh, kl = nkl, qh = nqh, ql = nql, sh = nsh, sl = nsl;
+    if (st < 3) {
+      const int d = 32 * (st + 1);
+      nkh = ld8(sm.kh + ro + d);
+      nkl = ld8(sm.kl + ro + d);
+      nqh = ld8(sm.qh + ro + d);
+      nql = ld8(sm.ql + ro + d);
+      nsh = ld8(sm.sh + so + d);
+      nsl = ld8(sm.sl + so + d);
     }
-    pre(u);
+    pre(st);
     __builtin_amdgcn_sched_barrier(0);
-    x = mfma16(kv.x, b.x, x);
-    o = mfma16(qv.x, b.x, o);
-    x = mfma16(kv.y, b.y, x);
-    o = mfma16(qv.y, b.y, o);
-    x = mfma16(kv.z, b.z, x);
-    o = mfma16(qv.z, b.z, o);
-    x = mfma16(kv.w, b.w, x);
-    o = mfma16(qv.w, b.w, o);
+    x = mfma3(kh, kl, sh, sl, x);
+    o = mfma3(qh, ql, sh, sl, o);
   }
   const int i0 = 16 * I + 4 * g4;
   float* zp = sm.zT + (16 * J + c) * MS + i0;
@@ -406,15 +446,19 @@ __device__ __forceinline__ void tile16_tri(f32x4& acc, int I, const float* pa, c
   }
 }
 
-// Pb: v_new rows of block I = T Z into vnT and (scaled by sk2) vsT.
+// Pb: v_new rows of block I = T Z into vnT, and sk2 v_new split into vsh / vsl.
 __device__ __forceinline__ void scan_vnew(ScanSmem& sm, int I, int J) {
   const int lane = threadIdx.x & 63, g4 = lane >> 4, c = lane & 15;
   f32x4 acc = zero4();
   tile16_tri(acc, I, sm.t + (16 * I + c) * MS, sm.zT + (16 * J + c) * MS);
-  const int i0 = 16 * I + 4 * g4, o = (16 * J + c) * MS + i0;
-  st4(sm.vnT + o, make_float4(acc[0], acc[1], acc[2], acc[3]));
-  st4(sm.vsT + o, make_float4(acc[0] * sm.sc[i0].z, acc[1] * sm.sc[i0 + 1].z,
-                              acc[2] * sm.sc[i0 + 2].z, acc[3] * sm.sc[i0 + 3].z));
+  const int i0 = 16 * I + 4 * g4;
+  st4(sm.vnT + (16 * J + c) * MS + i0, make_float4(acc[0], acc[1], acc[2], acc[3]));
+  bf16x4 h, l;
+  split4(make_float4(acc[0] * sm.sc[i0].z, acc[1] * sm.sc[i0 + 1].z, acc[2] * sm.sc[i0 + 2].z,
+                     acc[3] * sm.sc[i0 + 3].z),
+         h, l);
+  *reinterpret_cast<bf16x4*>(sm.vsh + (16 * J + c) * VB + i0) = h;
+  *reinterpret_cast<bf16x4*>(sm.vsl + (16 * J + c) * VB + i0) = l;
 }
 
 // Pc: out rows of block I = O + intra v_new, written where the token exists.
@@ -429,53 +473,43 @@ __device__ __forceinline__ void scan_out(ScanSmem& sm, float* orow, int I, int J
   }
 }
 
-// S'^T[col][kk] = e^tot S^T[col][kk] + sum_i (sk2 v_new)^T[col][i] k[i][kk], for the wave's
-// column half and the two 16-blocks of kk from P0; in place (each element is read and
-// written by one lane). Group g takes the tokens i = 8 (s >> 1) + 4 (g & 1) + 2 (g >> 1) +
-// (s & 1) at step s, so the column reads of k by the two groups of a half-wave fall 4 rows
-// apart, in opposite halves of the LDS banks; the reads of 4 steps are issued while the
-// previous 4 steps' products run.
-__device__ __forceinline__ void scan_state_update(ScanSmem& sm, int J, int P0) {
-  constexpr int NP = 2;
+// The wave's state tiles (J, P0 + p), held in registers as S^T[16 J + 4 g + r][16 (P0 + p) + c]:
+// S'^T = e^tot S^T + (sk2 v_new)^T k over the 64 tokens (split products, step st covering
+// tokens 32 st + 8 g .. + 7: the A operand from vsh / vsl rows, the B operand k's token column
+// read transposed), then the split of S'^T to LDS for the next chunk's products.
+__device__ __forceinline__ void scan_state_update(ScanSmem& sm, int J, int P0, f32x4 (&s)[2]) {
   const int lane = threadIdx.x & 63, g4 = lane >> 4, c = lane & 15;
-  const float et = sm.etot;
-  f32x4 s[NP];
+  bf16x8 ah[2], al[2], bh[2][2], bl[2][2];
 #pragma unroll
-  for (int p = 0; p < NP; ++p)
+  for (int st = 0; st < 2; ++st) {
+    const int ao = (16 * J + c) * VB + 32 * st + 8 * g4;
+    ah[st] = ld8(sm.vsh + ao);
+    al[st] = ld8(sm.vsl + ao);
+    const int r0 = 32 * st + 8 * g4 + (c >> 2);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) s[p][r] = sm.sT[(16 * J + 4 * g4 + r) * RS + 16 * (P0 + p) + c];
-  const int i0 = 4 * (g4 & 1) + 2 * (g4 >> 1);
-  const float* va = sm.vsT + (16 * J + c) * MS + i0;
-  const float* kc = sm.k + i0 * RS + 16 * P0 + c;
-  float ae[2][4], kb[2][4][NP];
-  auto load = [&](int t, int b) {  // steps 4t .. 4t + 3: tokens 16t + i0 + {0, 1, 8, 9}
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const float2 av = *reinterpret_cast<const float2*>(va + 16 * t + 8 * h);
-      ae[b][2 * h] = av.x;
-      ae[b][2 * h + 1] = av.y;
-#pragma unroll
-      for (int e = 0; e < 2; ++e)
-#pragma unroll
-        for (int p = 0; p < NP; ++p) kb[b][2 * h + e][p] = kc[(16 * t + 8 * h + e) * RS + 16 * p];
+    for (int p = 0; p < 2; ++p) {
+      const int bo = r0 * RB + 16 * (P0 + p) + 4 * (c & 3);
+      bh[st][p] = pack8(lds_tr16(sm.kh + bo), lds_tr16(sm.kh + bo + 4 * RB));
+      bl[st][p] = pack8(lds_tr16(sm.kl + bo), lds_tr16(sm.kl + bo + 4 * RB));
     }
-  };
-  load(0, 0);
-#pragma unroll
-  for (int p = 0; p < NP; ++p) s[p] *= et;
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    if (t < 3) load(t + 1, (t + 1) & 1);
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-#pragma unroll
-      for (int p = 0; p < NP; ++p) s[p] = mfma16(ae[t & 1][e], kb[t & 1][e][p], s[p]);
   }
+  const float et = sm.etot;
 #pragma unroll
-  for (int p = 0; p < NP; ++p)
+  for (int p = 0; p < 2; ++p) s[p] *= et;
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) sm.sT[(16 * J + 4 * g4 + r) * RS + 16 * (P0 + p) + c] = s[p][r];
+  for (int st = 0; st < 2; ++st)
+#pragma unroll
+    for (int p = 0; p < 2; ++p) s[p] = mfma3(ah[st], al[st], bh[st][p], bl[st][p], s[p]);
+#pragma unroll
+  for (int p = 0; p < 2; ++p)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int o = (16 * J + 4 * g4 + r) * RB + 16 * (P0 + p) + c;
+      const __bf16 h = (__bf16)s[p][r];
+      sm.sh[o] = h;
+      sm.sl[o] = (__bf16)(s[p][r] - (float)h);
+    }
 }
 
 constexpr int kScanThreads = 512;
@@ -486,23 +520,35 @@ __global__ __launch_bounds__(kScanThreads, 1) void dn_chunk_scan_kernel(ScanArgs
   const int L = blockIdx.x, grp = L / (8 * NCB), rem = L % (8 * NCB);
   const int cb = rem >> 3, h = 8 * grp + (rem & 7);
   if (h >= a.Hv) return;
-  const int tid = threadIdx.x, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63, g4 = lane >> 4, c = lane & 15;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int J = wv & 1;
   const int I = wv < 4 ? 3 - ((wv >> 1) & 1) : (wv >> 1) & 1;
+  const int P0 = 2 * ((wv >> 1) & 3);
   const int S = a.S;
   const size_t row0 = (size_t)h * S;
   const int c0 = 32 * cb;
 
-  for (int e = tid; e < D * 32; e += kScanThreads) {
-    const int kk = e >> 5, cc = e & 31;
-    sm.sT[cc * RS + kk] = a.state[((size_t)h * D + kk) * D + c0 + cc];
+  // this wave's state tiles: S[16 (P0 + p) + c][c0 + 16 J + 4 g + r] in s[p][r], and their split
+  f32x4 s[2];
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const float4 v4 = *reinterpret_cast<const float4*>(
+        a.state + ((size_t)h * D + 16 * (P0 + p) + c) * D + c0 + 16 * J + 4 * g4);
+    s[p] = f32x4{v4.x, v4.y, v4.z, v4.w};
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int o = (16 * J + 4 * g4 + r) * RB + 16 * (P0 + p) + c;
+      const __bf16 hb = (__bf16)s[p][r];
+      sm.sh[o] = hb;
+      sm.sl[o] = (__bf16)(s[p][r] - (float)hb);
+    }
   }
   // The next chunk's inputs are read into registers while the current chunk computes, in
   // parts issued between the products (reading a chunk's 104 KB at once stalls every wave on
   // the memory pipeline), and each goes to LDS as soon as the current chunk is done with that
   // buffer, which keeps the registers held short (issued in / stored in):
-  //   part 0..3    q rows (tid >> 5) + 16 j, float4 column tid & 31    Pa / Pb
+  //   part 0..3    q rows (tid >> 5) + 16 j, float4 column tid & 31    Pa / Pb (split)
   //   part 4       this block's v: row tid >> 3, columns 4 (tid & 7)    Pa / Pc
   //   part 5..6    T (float4 tid + 512 j)                               Pa / Pc
   //   part 7       scales (wave 0, lane = token) and e^tot              Pa / Pc, and e^tot at the
@@ -530,15 +576,23 @@ __global__ __launch_bounds__(kScanThreads, 1) void dn_chunk_scan_kernel(ScanArgs
       psc = bload4(make_rsrc(rec, REC * 4), lane * 16, REC_SC * 4);
       pet = rec[REC_ET];
     } else if (part < 12) {
-      pk[part - 8] = bload4(make_rsrc(a.k + (row0 + t0) * D, rest), qk_off + 8192 * (part - 8), 0);
+      pk[part - 8] =
+          bload4(make_rsrc(a.k + (row0 + t0) * D, rest), qk_off + 8192 * (part - 8), 0);
     } else if (part < 14) {
       pi[part - 12] =
           bload4(make_rsrc(rec, REC * 4), tid * 16, (REC_I + 2048 * (part - 12)) * 4);
     }
   };
-  auto store_q = [&]() {
+  // q or k rows of the registers, split, to LDS
+  auto store_split = [&](const float4 (&src)[4], __bf16* hi, __bf16* lo) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) st4(sm.q + ((tid >> 5) + 16 * j) * RS + 4 * (tid & 31), pq[j]);
+    for (int j = 0; j < 4; ++j) {
+      const int o = ((tid >> 5) + 16 * j) * RB + 4 * (tid & 31);
+      bf16x4 hh, ll;
+      split4(src[j], hh, ll);
+      *reinterpret_cast<bf16x4*>(hi + o) = hh;
+      *reinterpret_cast<bf16x4*>(lo + o) = ll;
+    }
   };
   auto store_v_t_sc = [&]() {
     float* zd = sm.zT + 4 * (tid & 7) * MS + (tid >> 3);
@@ -555,14 +609,13 @@ __global__ __launch_bounds__(kScanThreads, 1) void dn_chunk_scan_kernel(ScanArgs
   };
 #pragma unroll
   for (int part = 0; part < 14; ++part) fetch_part(0, part);
-  store_q();
+  store_split(pq, sm.qh, sm.ql);
   store_v_t_sc();
   f32x4 o;
   for (int ci = 0; ci < a.nch; ++ci) {
     const int t0 = ci * CH;
     __syncthreads();
-#pragma unroll
-    for (int j = 0; j < 4; ++j) st4(sm.k + ((tid >> 5) + 16 * j) * RS + 4 * (tid & 31), pk[j]);
+    store_split(pk, sm.kh, sm.kl);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int e = tid + kScanThreads * j, r = e >> 4, c4 = e & 15;
@@ -572,9 +625,9 @@ __global__ __launch_bounds__(kScanThreads, 1) void dn_chunk_scan_kernel(ScanArgs
     // the next chunk's reads (unconditional, so that no branch forces an early wait: the last
     // chunk reads itself again, and its late stores only rewrite buffers it no longer reads)
     const int nx = min(ci + 1, a.nch - 1);
-    auto pre_a = [&](int u) {
-      fetch_part(nx, u);
-      if (u >= 4) fetch_part(nx, u + 4);
+    auto pre_a = [&](int st) {
+#pragma unroll
+      for (int d = 0; d < 3; ++d) fetch_part(nx, 3 * st + d);
     };
     __syncthreads();
     scan_state_products(sm, I, J, o, pre_a);
@@ -582,17 +635,16 @@ __global__ __launch_bounds__(kScanThreads, 1) void dn_chunk_scan_kernel(ScanArgs
     fetch_part(nx, 12);
     fetch_part(nx, 13);
     scan_vnew(sm, I, J);
-    store_q();  // q of this chunk was last read in Pa
+    store_split(pq, sm.qh, sm.ql);  // q of this chunk was last read in Pa
     __syncthreads();
     scan_out(sm, a.out + (row0 + t0) * D + c0, I, J, o, min(CH, S - t0));
     store_v_t_sc();  // v (then Z), T and the scales were last read in Pb
-    scan_state_update(sm, J, 2 * (wv >> 1));
+    scan_state_update(sm, J, P0, s);
   }
-  __syncthreads();
-  for (int e = tid; e < D * 32; e += kScanThreads) {
-    const int kk = e >> 5, cc = e & 31;
-    a.new_state[((size_t)h * D + kk) * D + c0 + cc] = sm.sT[cc * RS + kk];
-  }
+#pragma unroll
+  for (int p = 0; p < 2; ++p)
+    *reinterpret_cast<float4*>(a.new_state + ((size_t)h * D + 16 * (P0 + p) + c) * D + c0 +
+                               16 * J + 4 * g4) = make_float4(s[p][0], s[p][1], s[p][2], s[p][3]);
 }
 
 constexpr int kPrepGrid = 512;  // two prep workgroups per CU (70 KB of LDS each)

@@ -281,7 +281,10 @@ def prefill_bench(args):
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": FP32_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / FP32_PEAK_TFLOPS, 4),
                      "traffic": None, "scope": "both kernels of the op",
-                     "flop_per_chunk_head": prefill_flops_per_chunk()},
+                     "flop_per_chunk_head": prefill_flops_per_chunk(),
+                     "bf16_executed_frac": round(3 * achieved / BF16_PEAK_TFLOPS, 4)},
+        "products": "fp32 results; matrix products as split bf16 (hi*hi + hi*lo + lo*hi, fp32 "
+                    "accumulation), the triangular inverse in fp32",
         "max_rel_err_head0": err, "steps": args.steps, "warmup": args.warmup,
     }
     if not args.no_cpu_baseline:

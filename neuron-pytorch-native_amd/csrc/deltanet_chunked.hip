@@ -17,20 +17,25 @@
 // written).
 //
 // Two kernels:
-// - dn_chunk_prep_kernel, one workgroup per (chunk, head), all chunks at once: everything that
-//   does not depend on the state -- the per-token scales (row norms folded with e^g_cum), A,
-//   T and the intra-chunk attention -- into a workspace record per (head, chunk).
-// - dn_chunk_scan_kernel, one workgroup per (head, 32-column block of V), chunk after chunk:
-//   only the products with the state. The columns of the state evolve independently, so the
-//   4 blocks of a head run side by side, each holding its 128 x 32 block (transposed) in LDS.
-//   The 4 workgroups of a head are placed on one XCD so that they share its L2 for the
-//   head's q, k and records.
+// - dn_chunk_prep_kernel, persistent workgroups over all (head, chunk) items at once:
+//   everything that does not depend on the state -- the per-token scales (row norms folded
+//   with e^g_cum), A, T and the intra-chunk attention -- into a workspace record per item.
+// - dn_chunk_scan_kernel, one workgroup of 8 waves per (head, 32-column block of V), chunk
+//   after chunk: only the products with the state. The columns of the state evolve
+//   independently, so the 4 blocks of a head run side by side, each holding its 128 x 32
+//   block in registers (and its split in LDS). The 4 workgroups of a head are placed on one
+//   XCD so that they share its L2 for the head's q, k and records.
 //
-// All products are 16 x 16 fp32 MFMA tiles (v_mfma_f32_16x16x4f32: lane l = 16 g + c supplies
-// A[c][k] and B[k][c] for the k of its group g; acc[r] is D[4 g + r][c]). In a tile over K,
-// group g takes k in [g K/4, (g + 1) K/4), so each lane reads row c of A and row c of B^T four
-// values at a time (float4 LDS reads). In the blocked inverse the output of one product feeds
-// the next as its B operand directly, with k = 4 g + r at step r.
+// Products. Matrix products over the 128 k indices or the 64 tokens of a chunk take split
+// operands: x = hi + lo with hi = bf16(x), lo = bf16(x - hi), and a product of two split
+// values is hi*hi + hi*lo + lo*hi in bf16 MFMAs (v_mfma_f32_16x16x32_bf16) accumulating in fp32;
+// the dropped lo*lo term and lo's rounding leave about 2^-16 relative per product, and the
+// results stay within 2e-5 of the float64 rule after 64 chunks. In a 16 x 16 tile lane
+// l = 16 g + c supplies A[c][k] and B[k][c] for the 8 consecutive k of its group g per
+// instruction, so each lane reads 16-byte rows of A and of B^T; acc[r] is D[4 g + r][c]. The
+// triangular inverse stays in fp32 (v_mfma_f32_16x16x4f32 and VALU): in the blocked inverse
+// the output of one product feeds the next as its B operand directly, with k = 4 g + r at
+// step r.
 #include "npn_common.h"
 
 namespace {
@@ -38,14 +43,14 @@ namespace {
 constexpr int CH = 64;                  // tokens per chunk
 constexpr int D = 128;                  // k and v head dims
 constexpr int NCB = 4;                  // 32-column blocks of V per head
-constexpr int RS = D + 4;               // LDS row stride of q, k and S^T (float4 rows)
 constexpr int MS = CH + 4;              // LDS row stride of A, T, intra and the [32][64] blocks
 constexpr float kNormEps = 1e-6f;
 constexpr float kQScale = 0.08838834764831845f;  // 1/sqrt(128)
 
 // Workspace record per (head, chunk), in floats (a multiple of 64: 256-byte aligned records).
-constexpr int REC_T = 0;                 // T [64][64] row-major, zero above the diagonal
-constexpr int REC_I = CH * CH;           // intra [64][64], zero above the diagonal
+constexpr int REC_T = 0;                 // T [64][64] row-major, zero above the diagonal: bf16 hi
+                                         // then bf16 lo (T = hi + lo)
+constexpr int REC_I = CH * CH;           // intra [64][64], zero above the diagonal, split alike
 constexpr int REC_SC = 2 * CH * CH;      // [64] x {sq, sk1, sk2, beta}
 constexpr int REC_ET = REC_SC + 4 * CH;  // e^(sum of the chunk's g)
 constexpr int REC = REC_ET + 64;
@@ -73,264 +78,6 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void* base, int bytes) {
 __device__ __forceinline__ float4 bload4(rsrc_t r, int voff, int soff) {
   return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
 }
-
-// acc += A (16 x K) B (K x 16) with pa = &A[c][0] and pb = &B^T[c][0] (k contiguous in both).
-// All operands are read before the first product, so one LDS latency is paid per tile.
-template <int K>
-__device__ __forceinline__ void tile16(f32x4& acc, const float* pa, const float* pb) {
-  const int k0 = ((threadIdx.x >> 4) & 3) * (K / 4);
-  float4 a[K / 16], b[K / 16];
-#pragma unroll
-  for (int u = 0; u < K / 16; ++u) {
-    a[u] = ld4(pa + k0 + 4 * u);
-    b[u] = ld4(pb + k0 + 4 * u);
-  }
-  __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the products
-#pragma unroll
-  for (int u = 0; u < K / 16; ++u) {
-    acc = mfma16(a[u].x, b[u].x, acc);
-    acc = mfma16(a[u].y, b[u].y, acc);
-    acc = mfma16(a[u].z, b[u].z, acc);
-    acc = mfma16(a[u].w, b[u].w, acc);
-  }
-}
-
-// The 10 lower 16 x 16 blocks (I >= J) of a 64 x 64 matrix, t = I (I + 1) / 2 + J.
-__device__ __forceinline__ void lower_block(int t, int& I, int& J) {
-  I = t < 1 ? 0 : t < 3 ? 1 : t < 6 ? 2 : 3;
-  J = t - I * (I + 1) / 2;
-}
-
-// ---- stage 1: per (chunk, head), independent of the state -----------------------------------
-
-struct PrepArgs {
-  const float* q;
-  const float* k;
-  const float* g;
-  const float* beta;
-  float* ws;
-  int S;
-  int nch;
-  int items;   // Hv * nch, item = h * nch + chunk
-};
-
-struct PrepSmem {
-  union {
-    float q[CH * RS];                    // raw q rows, until the intra blocks are done
-    struct {
-      float a[CH * MS];                  // A
-      float t[CH * MS];                  // T's diagonal blocks
-    } at;
-  } u;
-  float k[CH * RS];                      // raw k rows
-  float gcum[CH], bt[CH], rq[CH], rk[CH];
-};
-
-// Persistent: each workgroup takes items blockIdx.x, + gridDim.x, ..., with the next item's q, k
-// rows, g and beta read into registers while the current one computes.
-__global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(PrepArgs a) {
-  __shared__ __attribute__((aligned(16))) PrepSmem sm;
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int g4 = lane >> 4, c = lane & 15;
-  const int S = a.S;
-  // raw q, k rows 8j + (tid >> 5), float4 column tid & 31; g and beta of token lane (wave 0);
-  // reads past the end of the prompt return zeros
-  const int qk_off = (tid >> 5) * (D * 4) + (tid & 31) * 16;
-  float4 pq[8], pk[8];
-  float pg = 0.f, pb = 0.f;
-  auto fetch = [&](int item) {
-    const int h = item / a.nch, t0 = (item - h * a.nch) * CH;
-    const size_t r0 = (size_t)h * S + t0;
-    const int rest = S - t0;
-    const rsrc_t rq = make_rsrc(a.q + r0 * D, rest * D * 4);
-    const rsrc_t rk = make_rsrc(a.k + r0 * D, rest * D * 4);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      pq[j] = bload4(rq, qk_off + 4096 * j, 0);
-      pk[j] = bload4(rk, qk_off + 4096 * j, 0);
-    }
-    if (wv == 0) {
-      pg = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                         make_rsrc(a.g + r0, rest * 4), lane * 4, 0, 0));
-      pb = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                         make_rsrc(a.beta + r0, rest * 4), lane * 4, 0, 0));
-    }
-  };
-  if (blockIdx.x < a.items) fetch(blockIdx.x);
-  for (int item = blockIdx.x; item < a.items; item += gridDim.x) {
-    const int h = item / a.nch, ci = item - h * a.nch;
-    float* rec = a.ws + ((size_t)h * a.nch + ci) * REC;
-    __syncthreads();  // the previous item is done with LDS
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      st4(sm.u.q + (8 * j + (tid >> 5)) * RS + 4 * (tid & 31), pq[j]);
-      st4(sm.k + (8 * j + (tid >> 5)) * RS + 4 * (tid & 31), pk[j]);
-    }
-    if (wv == 0) {  // g_cum by a wave scan
-      float gi = pg;
-#pragma unroll
-      for (int d = 1; d < 64; d <<= 1) {
-        const float o = __shfl_up(gi, d, 64);
-        if (lane >= d) gi += o;
-      }
-      sm.gcum[lane] = gi;
-      sm.bt[lane] = pb;
-    }
-    fetch(min(item + (int)gridDim.x, a.items - 1));  // unconditional: no branch forces a wait
-    __syncthreads();
-    {  // row norms, 4 threads per row
-      const int i = tid >> 2, part = tid & 3;
-      const float* qp = sm.u.q + i * RS + 32 * part;
-      const float* kp = sm.k + i * RS + 32 * part;
-      float sq = 0.f, sk = 0.f;
-#pragma unroll
-      for (int j = 0; j < 32; j += 4) {
-        const float4 x = ld4(qp + j), y = ld4(kp + j);
-        sq += x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w;
-        sk += y.x * y.x + y.y * y.y + y.z * y.z + y.w * y.w;
-      }
-      sq += __shfl_xor(sq, 1, 64);
-      sq += __shfl_xor(sq, 2, 64);
-      sk += __shfl_xor(sk, 1, 64);
-      sk += __shfl_xor(sk, 2, 64);
-      if (part == 0) {
-        sm.rq[i] = rsqrtf(sq + kNormEps);
-        sm.rk[i] = rsqrtf(sk + kNormEps);
-      }
-    }
-    __syncthreads();
-    if (wv == 0) {
-      const float gi = sm.gcum[lane], tot = sm.gcum[CH - 1], rk = sm.rk[lane];
-      st4(rec + REC_SC + 4 * lane, make_float4(sm.rq[lane] * kQScale * __expf(gi), rk * __expf(gi),
-                                               rk * __expf(tot - gi), sm.bt[lane]));
-      if (lane == 0) rec[REC_ET] = __expf(tot);
-    }
-    if (wv >= 2) {  // the blocks above the diagonal of T and intra are zero
-      const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
-      for (int e = tid - 128; e < 6 * 64; e += 128) {
-        const int b = e >> 6, row = (e >> 2) & 15, c4 = e & 3;
-        const int I = b < 3 ? 0 : b < 5 ? 1 : 2, J = b < 3 ? b + 1 : b < 5 ? b - 1 : 3;
-        const int off = (16 * I + row) * CH + 16 * J + 4 * c4;
-        st4(rec + REC_T + off, z4);
-        st4(rec + REC_I + off, z4);
-      }
-    }
-    // intra[i][j] = (q_i . k_j) rq_i rk_j / sqrt(128) dm(i, j) for i >= j
-    for (int t = wv; t < 10; t += 4) {
-      int I, J;
-      lower_block(t, I, J);
-      f32x4 acc = zero4();
-      tile16<D>(acc, sm.u.q + (16 * I + c) * RS, sm.k + (16 * J + c) * RS);
-      const int j = 16 * J + c;
-      const float rkj = sm.rk[j], gj = sm.gcum[j];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = 16 * I + 4 * g4 + r;
-        rec[REC_I + i * CH + j] =
-            i >= j ? sm.rq[i] * kQScale * rkj * acc[r] * __expf(sm.gcum[i] - gj) : 0.f;
-      }
-    }
-    __syncthreads();  // the q rows are consumed: A and T take their place
-    // A[i][j] = -beta_i (k_i . k_j) rk_i rk_j dm(i, j) for i > j
-    for (int t = wv; t < 10; t += 4) {
-      int I, J;
-      lower_block(t, I, J);
-      f32x4 acc = zero4();
-      tile16<D>(acc, sm.k + (16 * I + c) * RS, sm.k + (16 * J + c) * RS);
-      const int j = 16 * J + c;
-      const float rkj = sm.rk[j], gj = sm.gcum[j];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = 16 * I + 4 * g4 + r;
-        sm.u.at.a[i * MS + j] =
-            i > j ? -sm.bt[i] * sm.rk[i] * rkj * acc[r] * __expf(sm.gcum[i] - gj) : 0.f;
-      }
-    }
-    __syncthreads();
-    if (wv == 0) {
-      // T's diagonal blocks by forward substitution, lane 16 b + j holding column j of block b:
-      // T_bb[i][j] = sum_{m < i} A_bb[i][m] T_bb[m][j] for i > j (A_bb is zero on and above
-      // its diagonal, so the row reads may run past m = i - 1)
-      const int b = g4, j = c;
-      const float* ab = sm.u.at.a + 16 * b * MS + 16 * b;
-      float col[16];
-#pragma unroll
-      for (int m = 0; m < 16; ++m) col[m] = m == j ? 1.f : 0.f;
-#pragma unroll
-      for (int i = 1; i < 16; ++i) {
-        float s0 = 0.f, s1 = 0.f;
-#pragma unroll
-        for (int m4 = 0; m4 < i; m4 += 4) {
-          const float4 av = ld4(ab + i * MS + m4);
-          s0 += av.x * col[m4] + av.z * col[m4 + 2];
-          s1 += av.y * col[m4 + 1] + av.w * col[m4 + 3];
-        }
-        if (i > j) col[i] = s0 + s1;
-      }
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        sm.u.at.t[(16 * b + i) * MS + 16 * b + j] = col[i];
-        rec[REC_T + (16 * b + i) * CH + 16 * b + j] = col[i];
-      }
-    }
-    __syncthreads();
-    if (wv < 3) {
-      // block column Jb = wave: T_IJ = T_II sum_{M = J}^{I - 1} A_IM T_MJ for I > J; each T_MJ
-      // stays in registers (acc layout) as the B operand of the next block row
-      const int Jb = wv;
-      const float* am = sm.u.at.a;
-      const float* tm = sm.u.at.t;
-      f32x4 tj[4];
-#pragma unroll
-      for (int M = 0; M < 3; ++M) {
-        tj[M] = zero4();
-        if (M == Jb) {
-#pragma unroll
-          for (int r = 0; r < 4; ++r) tj[M][r] = tm[(16 * M + 4 * g4 + r) * MS + 16 * M + c];
-        }
-      }
-#pragma unroll
-      for (int I = 1; I < 4; ++I) {
-        if (I <= Jb) continue;
-        f32x4 R = zero4();
-#pragma unroll
-        for (int M = 0; M < 3; ++M) {
-          if (M < Jb || M >= I) continue;
-          const float4 av = ld4(am + (16 * I + c) * MS + 16 * M + 4 * g4);
-          R = mfma16(av.x, tj[M][0], R);
-          R = mfma16(av.y, tj[M][1], R);
-          R = mfma16(av.z, tj[M][2], R);
-          R = mfma16(av.w, tj[M][3], R);
-        }
-        const float4 tv = ld4(tm + (16 * I + c) * MS + 16 * I + 4 * g4);
-        f32x4 X = zero4();
-        X = mfma16(tv.x, R[0], X);
-        X = mfma16(tv.y, R[1], X);
-        X = mfma16(tv.z, R[2], X);
-        X = mfma16(tv.w, R[3], X);
-        tj[I] = X;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) rec[REC_T + (16 * I + 4 * g4 + r) * CH + 16 * Jb + c] = X[r];
-      }
-    }
-  }
-}
-
-// ---- stage 2: per (head, column block), chunk after chunk -----------------------------------
-
-struct ScanArgs {
-  const float* state;
-  const float* q;
-  const float* k;
-  const float* v;
-  const float* ws;
-  float* out;
-  float* new_state;
-  int S;
-  int nch;
-  int Hv;
-};
 
 // Split operands: x = hi + lo with hi = bf16(x), lo = bf16(x - hi), and a product of two
 // split values as hi*hi + hi*lo + lo*hi in bf16 MFMAs accumulating in fp32 (the dropped
@@ -373,15 +120,303 @@ __device__ __forceinline__ bf16x8 pack8(s16x4 a, s16x4 b) {
   return __builtin_bit_cast(bf16x8, v);
 }
 
+// The 10 lower 16 x 16 blocks (I >= J) of a 64 x 64 matrix, t = I (I + 1) / 2 + J.
+__device__ __forceinline__ void lower_block(int t, int& I, int& J) {
+  I = t < 1 ? 0 : t < 3 ? 1 : t < 6 ? 2 : 3;
+  J = t - I * (I + 1) / 2;
+}
+
+// ---- stage 1: per (chunk, head), independent of the state -----------------------------------
+
+struct PrepArgs {
+  const float* q;
+  const float* k;
+  const float* g;
+  const float* beta;
+  float* ws;
+  int S;
+  int nch;
+  int items;   // Hv * nch, item = h * nch + chunk
+};
+
+struct PrepSmem {
+  union {
+    struct {
+      __bf16 h[CH * RB], l[CH * RB];     // q rows split, until the intra blocks are done
+    } q;
+    struct {
+      float a[CH * MS];                  // A
+      float t[CH * MS];                  // T's diagonal blocks
+    } at;
+  } u;
+  __bf16 kh[CH * RB], kl[CH * RB];       // k rows split
+  float gcum[CH], bt[CH], rq[CH], rk[CH];
+};
+
+// A 16 x 16 block over the 128 k indices from split operands: ah = &A_hi[row c][8 g], al, and
+// bh / bl the same for B^T (rows of both are k-contiguous); step st covers k = 32 st + 8 g ..
+// + 7. Operands are read two steps at a time (32 VGPRs live).
+__device__ __forceinline__ f32x4 tile_split128(const __bf16* ah, const __bf16* al,
+                                               const __bf16* bh, const __bf16* bl) {
+  f32x4 acc = zero4();
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh) {
+    bf16x8 x[2][4];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int d = 64 * hh + 32 * u;
+      x[u][0] = ld8(ah + d);
+      x[u][1] = ld8(al + d);
+      x[u][2] = ld8(bh + d);
+      x[u][3] = ld8(bl + d);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) acc = mfma3(x[u][0], x[u][1], x[u][2], x[u][3], acc);
+  }
+  return acc;
+}
+
+// Persistent: each workgroup takes items blockIdx.x, + gridDim.x, ..., with the next item's q, k
+// rows, g and beta read into registers while the current one computes.
+__global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(PrepArgs a) {
+  __shared__ __attribute__((aligned(16))) PrepSmem sm;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g4 = lane >> 4, c = lane & 15;
+  const int S = a.S;
+  // raw q, k rows 8j + (tid >> 5), float4 column tid & 31; g and beta of token lane (wave 0);
+  // reads past the end of the prompt return zeros
+  const int qk_off = (tid >> 5) * (D * 4) + (tid & 31) * 16;
+  float4 pq[8], pk[8];
+  float pg = 0.f, pb = 0.f;
+  auto fetch = [&](int item) {
+    const int h = item / a.nch, t0 = (item - h * a.nch) * CH;
+    const size_t r0 = (size_t)h * S + t0;
+    const int rest = S - t0;
+    const rsrc_t rq = make_rsrc(a.q + r0 * D, rest * D * 4);
+    const rsrc_t rk = make_rsrc(a.k + r0 * D, rest * D * 4);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      pq[j] = bload4(rq, qk_off + 4096 * j, 0);
+      pk[j] = bload4(rk, qk_off + 4096 * j, 0);
+    }
+    if (wv == 0) {
+      pg = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                         make_rsrc(a.g + r0, rest * 4), lane * 4, 0, 0));
+      pb = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                         make_rsrc(a.beta + r0, rest * 4), lane * 4, 0, 0));
+    }
+  };
+  if (blockIdx.x < a.items) fetch(blockIdx.x);
+  for (int item = blockIdx.x; item < a.items; item += gridDim.x) {
+    const int h = item / a.nch, ci = item - h * a.nch;
+    float* rec = a.ws + ((size_t)h * a.nch + ci) * REC;
+    __bf16* rth = reinterpret_cast<__bf16*>(rec + REC_T);   // T hi [64][64], then lo
+    __bf16* rih = reinterpret_cast<__bf16*>(rec + REC_I);   // intra hi, then lo
+    __syncthreads();  // the previous item is done with LDS
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int o = (8 * j + (tid >> 5)) * RB + 4 * (tid & 31);
+      bf16x4 hh, ll;
+      split4(pq[j], hh, ll);
+      *reinterpret_cast<bf16x4*>(sm.u.q.h + o) = hh;
+      *reinterpret_cast<bf16x4*>(sm.u.q.l + o) = ll;
+      split4(pk[j], hh, ll);
+      *reinterpret_cast<bf16x4*>(sm.kh + o) = hh;
+      *reinterpret_cast<bf16x4*>(sm.kl + o) = ll;
+    }
+    if (wv == 0) {  // g_cum by a wave scan
+      float gi = pg;
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const float o = __shfl_up(gi, d, 64);
+        if (lane >= d) gi += o;
+      }
+      sm.gcum[lane] = gi;
+      sm.bt[lane] = pb;
+    }
+    fetch(min(item + (int)gridDim.x, a.items - 1));  // unconditional: no branch forces a wait
+    __syncthreads();
+    {  // row norms from the split rows (hi + lo is x to 2^-17), 4 threads per row
+      const int i = tid >> 2, part = tid & 3;
+      float sq = 0.f, sk = 0.f;
+#pragma unroll
+      for (int j = 0; j < 32; j += 8) {
+        const int o = i * RB + 32 * part + j;
+        const bf16x8 qh = ld8(sm.u.q.h + o), ql = ld8(sm.u.q.l + o), kh = ld8(sm.kh + o),
+                     kl = ld8(sm.kl + o);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float x = (float)qh[e] + (float)ql[e], y = (float)kh[e] + (float)kl[e];
+          sq += x * x;
+          sk += y * y;
+        }
+      }
+      sq += __shfl_xor(sq, 1, 64);
+      sq += __shfl_xor(sq, 2, 64);
+      sk += __shfl_xor(sk, 1, 64);
+      sk += __shfl_xor(sk, 2, 64);
+      if (part == 0) {
+        sm.rq[i] = rsqrtf(sq + kNormEps);
+        sm.rk[i] = rsqrtf(sk + kNormEps);
+      }
+    }
+    __syncthreads();
+    if (wv == 0) {
+      const float gi = sm.gcum[lane], tot = sm.gcum[CH - 1], rk = sm.rk[lane];
+      st4(rec + REC_SC + 4 * lane,
+          make_float4(sm.rq[lane] * kQScale * __expf(gi), rk * __expf(gi), rk * __expf(tot - gi),
+                      sm.bt[lane]));
+      if (lane == 0) rec[REC_ET] = __expf(tot);
+    }
+    if (wv >= 2) {  // the blocks above the diagonal of T and intra are zero (hi and lo)
+      const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int e = tid - 128; e < 2 * 6 * 32; e += 128) {
+        const int half = e / 192, f = e % 192, b = f >> 5, row = (f >> 1) & 15, c8 = f & 1;
+        const int I = b < 3 ? 0 : b < 5 ? 1 : 2, J = b < 3 ? b + 1 : b < 5 ? b - 1 : 3;
+        const int off = half * CH * CH + (16 * I + row) * CH + 16 * J + 8 * c8;
+        *reinterpret_cast<float4*>(rth + off) = z4;
+        *reinterpret_cast<float4*>(rih + off) = z4;
+      }
+    }
+    // intra[i][j] = (q_i . k_j) rq_i rk_j / sqrt(128) dm(i, j) for i >= j, written split
+    for (int t = wv; t < 10; t += 4) {
+      int I, J;
+      lower_block(t, I, J);
+      const int ao = (16 * I + c) * RB + 8 * g4, bo = (16 * J + c) * RB + 8 * g4;
+      const f32x4 acc = tile_split128(sm.u.q.h + ao, sm.u.q.l + ao, sm.kh + bo, sm.kl + bo);
+      const int j = 16 * J + c;
+      const float rkj = sm.rk[j], gj = sm.gcum[j];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = 16 * I + 4 * g4 + r;
+        const float x =
+            i >= j ? sm.rq[i] * kQScale * rkj * acc[r] * __expf(sm.gcum[i] - gj) : 0.f;
+        const __bf16 hb = (__bf16)x;
+        rih[i * CH + j] = hb;
+        rih[CH * CH + i * CH + j] = (__bf16)(x - (float)hb);
+      }
+    }
+    __syncthreads();  // the q rows are consumed: A and T take their place
+    // A[i][j] = -beta_i (k_i . k_j) rk_i rk_j dm(i, j) for i > j
+    for (int t = wv; t < 10; t += 4) {
+      int I, J;
+      lower_block(t, I, J);
+      const int ao = (16 * I + c) * RB + 8 * g4, bo = (16 * J + c) * RB + 8 * g4;
+      const f32x4 acc = tile_split128(sm.kh + ao, sm.kl + ao, sm.kh + bo, sm.kl + bo);
+      const int j = 16 * J + c;
+      const float rkj = sm.rk[j], gj = sm.gcum[j];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = 16 * I + 4 * g4 + r;
+        sm.u.at.a[i * MS + j] =
+            i > j ? -sm.bt[i] * sm.rk[i] * rkj * acc[r] * __expf(sm.gcum[i] - gj) : 0.f;
+      }
+    }
+    __syncthreads();
+    if (wv == 0) {
+      // T's diagonal blocks by forward substitution, lane 16 b + j holding column j of block b:
+      // T_bb[i][j] = sum_{m < i} A_bb[i][m] T_bb[m][j] for i > j (A_bb is zero on and above
+      // its diagonal, so the row reads may run past m = i - 1)
+      const int b = g4, j = c;
+      const float* ab = sm.u.at.a + 16 * b * MS + 16 * b;
+      float col[16];
+#pragma unroll
+      for (int m = 0; m < 16; ++m) col[m] = m == j ? 1.f : 0.f;
+#pragma unroll
+      for (int i = 1; i < 16; ++i) {
+        float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+        for (int m4 = 0; m4 < i; m4 += 4) {
+          const float4 av = ld4(ab + i * MS + m4);
+          s0 += av.x * col[m4] + av.z * col[m4 + 2];
+          s1 += av.y * col[m4 + 1] + av.w * col[m4 + 3];
+        }
+        if (i > j) col[i] = s0 + s1;
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        sm.u.at.t[(16 * b + i) * MS + 16 * b + j] = col[i];
+        const int o = (16 * b + i) * CH + 16 * b + j;
+        const __bf16 hb = (__bf16)col[i];
+        rth[o] = hb;
+        rth[CH * CH + o] = (__bf16)(col[i] - (float)hb);
+      }
+    }
+    __syncthreads();
+    if (wv < 3) {
+      // block column Jb = wave: T_IJ = T_II sum_{M = J}^{I - 1} A_IM T_MJ for I > J; each T_MJ
+      // stays in registers (acc layout) as the B operand of the next block row
+      const int Jb = wv;
+      const float* am = sm.u.at.a;
+      const float* tm = sm.u.at.t;
+      f32x4 tj[4];
+#pragma unroll
+      for (int M = 0; M < 3; ++M) {
+        tj[M] = zero4();
+        if (M == Jb) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) tj[M][r] = tm[(16 * M + 4 * g4 + r) * MS + 16 * M + c];
+        }
+      }
+#pragma unroll
+      for (int I = 1; I < 4; ++I) {
+        if (I <= Jb) continue;
+        f32x4 R = zero4();
+#pragma unroll
+        for (int M = 0; M < 3; ++M) {
+          if (M < Jb || M >= I) continue;
+          const float4 av = ld4(am + (16 * I + c) * MS + 16 * M + 4 * g4);
+          R = mfma16(av.x, tj[M][0], R);
+          R = mfma16(av.y, tj[M][1], R);
+          R = mfma16(av.z, tj[M][2], R);
+          R = mfma16(av.w, tj[M][3], R);
+        }
+        const float4 tv = ld4(tm + (16 * I + c) * MS + 16 * I + 4 * g4);
+        f32x4 X = zero4();
+        X = mfma16(tv.x, R[0], X);
+        X = mfma16(tv.y, R[1], X);
+        X = mfma16(tv.z, R[2], X);
+        X = mfma16(tv.w, R[3], X);
+        tj[I] = X;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int o = (16 * I + 4 * g4 + r) * CH + 16 * Jb + c;
+          const __bf16 hb = (__bf16)X[r];
+          rth[o] = hb;
+          rth[CH * CH + o] = (__bf16)(X[r] - (float)hb);
+        }
+      }
+    }
+  }
+}
+
+// ---- stage 2: per (head, column block), chunk after chunk -----------------------------------
+
+struct ScanArgs {
+  const float* state;
+  const float* q;
+  const float* k;
+  const float* v;
+  const float* ws;
+  float* out;
+  float* new_state;
+  int S;
+  int nch;
+  int Hv;
+};
+
 struct ScanSmem {
   __bf16 qh[CH * RB], ql[CH * RB];    // q rows of the chunk, split
   __bf16 kh[CH * RB], kl[CH * RB];    // k rows, split
   __bf16 sh[32 * RB], sl[32 * RB];    // the state block transposed ([column][k index]), split
+  __bf16 th[CH * VB], tl[CH * VB];    // T, split (as the record holds it)
+  __bf16 ih[CH * VB], il[CH * VB];    // intra, split
+  __bf16 zh[32 * VB], zl[32 * VB];    // Z^T, split
+  __bf16 nh[32 * VB], nl[32 * VB];    // v_new^T, split
   __bf16 vsh[32 * VB], vsl[32 * VB];  // (sk2 v_new)^T, split
-  float t[CH * MS];                   // T
-  float in[CH * MS];                  // intra
-  float zT[32 * MS];                  // v^T of the chunk, then Z^T
-  float vnT[32 * MS];                 // v_new^T
+  float vT[32 * MS];                  // v^T of the chunk (fp32)
   float4 sc[CH];                      // sq, sk1, sk2, beta
   float etot;
 };
@@ -395,8 +430,8 @@ struct ScanSmem {
 // registers for the whole prompt.
 
 // Pa: X = (raw k) S and O = (raw q) S for rows of block I (split products over the 128 k
-// indices, step st covering 32 st + 8 g .. + 7 for lane group g); Z = beta (v - sk1 X) into
-// zT; O *= sq. pre(st) issues part of the next chunk's reads between the products.
+// indices, step st covering 32 st + 8 g .. + 7 for lane group g); Z = beta (v - sk1 X), split
+// into zh / zl; O *= sq. pre(st) issues part of the next chunk's reads between the products.
 template <typename Pre>
 __device__ __forceinline__ void scan_state_products(ScanSmem& sm, int I, int J, f32x4& o,
                                                     Pre&& pre) {
@@ -424,48 +459,69 @@ __device__ __forceinline__ void scan_state_products(ScanSmem& sm, int I, int J, 
     o = mfma3(qh, ql, sh, sl, o);
   }
   const int i0 = 16 * I + 4 * g4;
-  float* zp = sm.zT + (16 * J + c) * MS + i0;
-  const float4 v = ld4(zp);
+  const float4 v = ld4(sm.vT + (16 * J + c) * MS + i0);
   const float4 s0 = sm.sc[i0], s1 = sm.sc[i0 + 1], s2 = sm.sc[i0 + 2], s3 = sm.sc[i0 + 3];
-  st4(zp, make_float4(s0.w * (v.x - s0.y * x[0]), s1.w * (v.y - s1.y * x[1]),
-                      s2.w * (v.z - s2.y * x[2]), s3.w * (v.w - s3.y * x[3])));
+  bf16x4 zh, zl;
+  split4(make_float4(s0.w * (v.x - s0.y * x[0]), s1.w * (v.y - s1.y * x[1]),
+                     s2.w * (v.z - s2.y * x[2]), s3.w * (v.w - s3.y * x[3])),
+         zh, zl);
+  *reinterpret_cast<bf16x4*>(sm.zh + (16 * J + c) * VB + i0) = zh;
+  *reinterpret_cast<bf16x4*>(sm.zl + (16 * J + c) * VB + i0) = zl;
   o[0] *= s0.x;
   o[1] *= s1.x;
   o[2] *= s2.x;
   o[3] *= s3.x;
 }
 
-// acc += A B over K = 16 (I + 1) (a triangular left factor): the wave-uniform I picks the
-// instance.
-__device__ __forceinline__ void tile16_tri(f32x4& acc, int I, const float* pa, const float* pb) {
-  switch (I) {
-    case 0: tile16<16>(acc, pa, pb); break;
-    case 1: tile16<32>(acc, pa, pb); break;
-    case 2: tile16<48>(acc, pa, pb); break;
-    default: tile16<64>(acc, pa, pb); break;
+// acc += A B with a lower-triangular left factor from split rows over the tokens below
+// 32 ceil((I + 1) / 2) (A is zero above its diagonal, so the rounding up adds zero products):
+// ah = &A_hi[16 I + c][8 g], bh = &B^T_hi[col c][8 g], step st covering tokens 32 st + 8 g ..
+// + 7.
+template <int NST>
+__device__ __forceinline__ void tile_split_tri(f32x4& acc, const __bf16* ah, const __bf16* al,
+                                               const __bf16* bh, const __bf16* bl) {
+  bf16x8 x[NST][4];
+#pragma unroll
+  for (int st = 0; st < NST; ++st) {
+    x[st][0] = ld8(ah + 32 * st);
+    x[st][1] = ld8(al + 32 * st);
+    x[st][2] = ld8(bh + 32 * st);
+    x[st][3] = ld8(bl + 32 * st);
   }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int st = 0; st < NST; ++st) acc = mfma3(x[st][0], x[st][1], x[st][2], x[st][3], acc);
+}
+__device__ __forceinline__ void tile_tri(f32x4& acc, int I, const __bf16* ah, const __bf16* al,
+                                         const __bf16* bh, const __bf16* bl) {
+  if (I < 2) tile_split_tri<1>(acc, ah, al, bh, bl);
+  else tile_split_tri<2>(acc, ah, al, bh, bl);
 }
 
-// Pb: v_new rows of block I = T Z into vnT, and sk2 v_new split into vsh / vsl.
+// Pb: v_new rows of block I = T Z, split into nh / nl, and sk2 v_new split into vsh / vsl.
 __device__ __forceinline__ void scan_vnew(ScanSmem& sm, int I, int J) {
   const int lane = threadIdx.x & 63, g4 = lane >> 4, c = lane & 15;
   f32x4 acc = zero4();
-  tile16_tri(acc, I, sm.t + (16 * I + c) * MS, sm.zT + (16 * J + c) * MS);
-  const int i0 = 16 * I + 4 * g4;
-  st4(sm.vnT + (16 * J + c) * MS + i0, make_float4(acc[0], acc[1], acc[2], acc[3]));
+  const int ao = (16 * I + c) * VB + 8 * g4, bo = (16 * J + c) * VB + 8 * g4;
+  tile_tri(acc, I, sm.th + ao, sm.tl + ao, sm.zh + bo, sm.zl + bo);
+  const int i0 = 16 * I + 4 * g4, o = (16 * J + c) * VB + i0;
   bf16x4 h, l;
+  split4(make_float4(acc[0], acc[1], acc[2], acc[3]), h, l);
+  *reinterpret_cast<bf16x4*>(sm.nh + o) = h;
+  *reinterpret_cast<bf16x4*>(sm.nl + o) = l;
   split4(make_float4(acc[0] * sm.sc[i0].z, acc[1] * sm.sc[i0 + 1].z, acc[2] * sm.sc[i0 + 2].z,
                      acc[3] * sm.sc[i0 + 3].z),
          h, l);
-  *reinterpret_cast<bf16x4*>(sm.vsh + (16 * J + c) * VB + i0) = h;
-  *reinterpret_cast<bf16x4*>(sm.vsl + (16 * J + c) * VB + i0) = l;
+  *reinterpret_cast<bf16x4*>(sm.vsh + o) = h;
+  *reinterpret_cast<bf16x4*>(sm.vsl + o) = l;
 }
 
 // Pc: out rows of block I = O + intra v_new, written where the token exists.
 __device__ __forceinline__ void scan_out(ScanSmem& sm, float* orow, int I, int J, f32x4 o,
                                          int nvalid) {
   const int lane = threadIdx.x & 63, g4 = lane >> 4, c = lane & 15;
-  tile16_tri(o, I, sm.in + (16 * I + c) * MS, sm.vnT + (16 * J + c) * MS);
+  const int ao = (16 * I + c) * VB + 8 * g4, bo = (16 * J + c) * VB + 8 * g4;
+  tile_tri(o, I, sm.ih + ao, sm.il + ao, sm.nh + bo, sm.nl + bo);
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int i = 16 * I + 4 * g4 + r;
@@ -550,11 +606,11 @@ __global__ __launch_bounds__(kScanThreads, 1) void dn_chunk_scan_kernel(ScanArgs
   // buffer, which keeps the registers held short (issued in / stored in):
   //   part 0..3    q rows (tid >> 5) + 16 j, float4 column tid & 31    Pa / Pb (split)
   //   part 4       this block's v: row tid >> 3, columns 4 (tid & 7)    Pa / Pc
-  //   part 5..6    T (float4 tid + 512 j)                               Pa / Pc
+  //   part 5..6    T hi, lo (16 bytes tid of each)                      Pa / Pc
   //   part 7       scales (wave 0, lane = token) and e^tot              Pa / Pc, and e^tot at the
   //                next chunk's start (the state update reads the current one)
   //   part 8..11   k rows, as q                                         Pa / next chunk's start
-  //   part 12..13  intra (float4 tid + 512 j)                           Pb / next chunk's start
+  //   part 12..13  intra hi, lo, as T                                   Pb / next chunk's start
   // Reads go through buffer descriptors based at the chunk's first row, sized to the end of
   // the prompt, so rows past it read as zeros.
   float4 pq[4], pk[4], pv, pt[2], pi[2];
@@ -594,17 +650,17 @@ __global__ __launch_bounds__(kScanThreads, 1) void dn_chunk_scan_kernel(ScanArgs
       *reinterpret_cast<bf16x4*>(lo + o) = ll;
     }
   };
+  // a split 64 x 64 record matrix: 16 bytes tid of the hi half and of the lo half (row tid >> 3,
+  // columns 8 (tid & 7) .. + 7)
+  const int m_off = (tid >> 3) * VB + 8 * (tid & 7);
   auto store_v_t_sc = [&]() {
-    float* zd = sm.zT + 4 * (tid & 7) * MS + (tid >> 3);
-    zd[0] = pv.x;
-    zd[MS] = pv.y;
-    zd[2 * MS] = pv.z;
-    zd[3 * MS] = pv.w;
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int e = tid + kScanThreads * j, r = e >> 4, c4 = e & 15;
-      st4(sm.t + r * MS + 4 * c4, pt[j]);
-    }
+    float* vd = sm.vT + 4 * (tid & 7) * MS + (tid >> 3);
+    vd[0] = pv.x;
+    vd[MS] = pv.y;
+    vd[2 * MS] = pv.z;
+    vd[3 * MS] = pv.w;
+    *reinterpret_cast<float4*>(sm.th + m_off) = pt[0];
+    *reinterpret_cast<float4*>(sm.tl + m_off) = pt[1];
     if (wv == 0) sm.sc[lane] = psc;
   };
 #pragma unroll
@@ -616,11 +672,8 @@ __global__ __launch_bounds__(kScanThreads, 1) void dn_chunk_scan_kernel(ScanArgs
     const int t0 = ci * CH;
     __syncthreads();
     store_split(pk, sm.kh, sm.kl);
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int e = tid + kScanThreads * j, r = e >> 4, c4 = e & 15;
-      st4(sm.in + r * MS + 4 * c4, pi[j]);
-    }
+    *reinterpret_cast<float4*>(sm.ih + m_off) = pi[0];
+    *reinterpret_cast<float4*>(sm.il + m_off) = pi[1];
     if (wv == 0 && lane == 0) sm.etot = pet;
     // the next chunk's reads (unconditional, so that no branch forces an early wait: the last
     // chunk reads itself again, and its late stores only rewrite buffers it no longer reads)
@@ -638,7 +691,7 @@ __global__ __launch_bounds__(kScanThreads, 1) void dn_chunk_scan_kernel(ScanArgs
     store_split(pq, sm.qh, sm.ql);  // q of this chunk was last read in Pa
     __syncthreads();
     scan_out(sm, a.out + (row0 + t0) * D + c0, I, J, o, min(CH, S - t0));
-    store_v_t_sc();  // v (then Z), T and the scales were last read in Pb
+    store_v_t_sc();  // v, T and the scales were last read in Pa / Pb
     scan_state_update(sm, J, P0, s);
   }
 #pragma unroll

@@ -3,7 +3,8 @@ oracle (oracle/deltanet_chunked.py, float64): out and new_state within the path'
 relative bar, measured as Frobenius and elementwise (tests/_util.py).
 
 Cases: the reference test's heads (V_HEADS = 12 per core, contrib/qwen3.6-27b/kernels/tests/
-test_deltanet_chunked_v2.py:17-60, model gates), the 27B model's 48 v-heads, lengths that are
+test_deltanet_chunked_v2.py:17-60, model gates), the 27B model's 48 v-heads (also at a 4096-token
+prompt, first and last head against the oracle at 1e-4), lengths that are
 and are not multiples of the chunk, a single token, the reference's chunk sizes in the [C, C]
 constants (16 and 64: the kernel chunks by 64 either way), identical pad rows (where the
 reference's doubling-product inverse blows up, test_doubling_pad_stability.py:1-19), and the
@@ -61,6 +62,33 @@ def test_chunked_prefill_matches_oracle(ops, Hv, S, C, seed):
     ro, rs = oc.chunked_prefill(*args, 64)
     assert_rel_close(out, ro, name="out")
     assert_rel_close(ns, rs, name="new_state")
+
+
+def test_full_size_heads_match_oracle(ops):
+    """The 27B layer's width at a 4096-token prompt (48 v-heads x 64 chunks): the first and the
+    last head against the float64 oracle, at the op's 2e-3 bar and at 1e-4 (the split bf16
+    products keep the result fp32-class over all 64 chunks)."""
+    Hv, S = 48, 4096
+    g = torch.Generator(device="cuda").manual_seed(11)
+    st = torch.randn(Hv * 128, 128, generator=g, device="cuda") * 0.05
+    q, k, v = (torch.randn(Hv * S, 128, generator=g, device="cuda") for _ in range(3))
+    a_log = torch.randn(Hv, 1, generator=g, device="cuda")
+    dt = torch.randn(Hv, 1, generator=g, device="cuda") * 0.1
+    a_in = torch.randn(Hv, S, generator=g, device="cuda")
+    gate = (-torch.exp(a_log) * torch.nn.functional.softplus(a_in + dt)).reshape(-1, 1)
+    beta = torch.sigmoid(torch.randn(Hv * S, 1, generator=g, device="cuda"))
+    m = [torch.from_numpy(x).cuda() for x in oc.constants(64)]
+    out, ns = ops.deltanet.chunked_prefill(st, q, k, v, gate, beta, *m)
+    torch.cuda.synchronize()
+    for h in (0, Hv - 1):
+        rows, srows = slice(h * S, (h + 1) * S), slice(h * 128, (h + 1) * 128)
+        args = [x[rows].cpu().numpy() for x in (q, k, v, gate, beta)]
+        ro, rs = oc.chunked_prefill(st[srows].cpu().numpy(), *args, 64)
+        o, s_ = out[rows].cpu().numpy(), ns[srows].cpu().numpy()
+        assert_rel_close(o, ro, name=f"head {h} out")
+        assert_rel_close(s_, rs, name=f"head {h} new_state")
+        assert np.abs(o - ro).max() <= 1e-4 * np.abs(ro).max(), f"head {h} out"
+        assert np.abs(s_ - rs).max() <= 1e-4 * np.abs(rs).max(), f"head {h} new_state"
 
 
 def test_identical_pad_rows(ops):

@@ -407,9 +407,18 @@ struct ScanArgs {
   int Hv;
 };
 
+// The scan's q and k rows: 128 bf16 (256 bytes) per row, 16-byte chunk m of row r stored at
+// chunk m ^ f(r), f(r) = 2 (r & 3) + ((r >> 2) & 1). Eight consecutive rows then put a chunk on
+// 8 distinct LDS bank groups (the row reads of the state products), and 4 rows from a
+// multiple of 4 put a pair of chunks on 8 distinct ones (the transposed column reads of the
+// state update); a plain padded stride serves one pattern or the other.
+__device__ __forceinline__ int qk_idx(int r, int e) {
+  return r * D + (((e >> 3) ^ (2 * (r & 3) + ((r >> 2) & 1))) << 3) + (e & 7);
+}
+
 struct ScanSmem {
-  __bf16 qh[CH * RB], ql[CH * RB];    // q rows of the chunk, split
-  __bf16 kh[CH * RB], kl[CH * RB];    // k rows, split
+  __bf16 qh[CH * D], ql[CH * D];      // q rows of the chunk, split (qk_idx layout)
+  __bf16 kh[CH * D], kl[CH * D];      // k rows, split (qk_idx layout)
   __bf16 sh[32 * RB], sl[32 * RB];    // the state block transposed ([column][k index]), split
   __bf16 th[CH * VB], tl[CH * VB];    // T, split (as the record holds it)
   __bf16 ih[CH * VB], il[CH * VB];    // intra, split
@@ -438,7 +447,8 @@ __device__ __forceinline__ void scan_state_products(ScanSmem& sm, int I, int J, 
   const int lane = threadIdx.x & 63, g4 = lane >> 4, c = lane & 15;
   f32x4 x = zero4();
   o = zero4();
-  const int ro = (16 * I + c) * RB + 8 * g4, so = (16 * J + c) * RB + 8 * g4;
+  const int rr = 16 * I + c, so = (16 * J + c) * RB + 8 * g4;
+  int ro = qk_idx(rr, 8 * g4);
   bf16x8 nkh = ld8(sm.kh + ro), nkl = ld8(sm.kl + ro), nqh = ld8(sm.qh + ro),
          nql = ld8(sm.ql + ro), nsh = ld8(sm.sh + so), nsl = ld8(sm.sl + so);
 #pragma unroll
@@ -446,10 +456,11 @@ __device__ __forceinline__ void scan_state_products(ScanSmem& sm, int I, int J, 
     const bf16x8 kh = nkh, kl = nkl, qh = nqh, ql = nql, sh = nsh, sl = nsl;
     if (st < 3) {
       const int d = 32 * (st + 1);
-      nkh = ld8(sm.kh + ro + d);
-      nkl = ld8(sm.kl + ro + d);
-      nqh = ld8(sm.qh + ro + d);
-      nql = ld8(sm.ql + ro + d);
+      ro = qk_idx(rr, d + 8 * g4);
+      nkh = ld8(sm.kh + ro);
+      nkl = ld8(sm.kl + ro);
+      nqh = ld8(sm.qh + ro);
+      nql = ld8(sm.ql + ro);
       nsh = ld8(sm.sh + so + d);
       nsl = ld8(sm.sl + so + d);
     }
@@ -544,9 +555,10 @@ __device__ __forceinline__ void scan_state_update(ScanSmem& sm, int J, int P0, f
     const int r0 = 32 * st + 8 * g4 + (c >> 2);
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
-      const int bo = r0 * RB + 16 * (P0 + p) + 4 * (c & 3);
-      bh[st][p] = pack8(lds_tr16(sm.kh + bo), lds_tr16(sm.kh + bo + 4 * RB));
-      bl[st][p] = pack8(lds_tr16(sm.kl + bo), lds_tr16(sm.kl + bo + 4 * RB));
+      const int e = 16 * (P0 + p) + 4 * (c & 3);
+      const int b0 = qk_idx(r0, e), b1 = qk_idx(r0 + 4, e);
+      bh[st][p] = pack8(lds_tr16(sm.kh + b0), lds_tr16(sm.kh + b1));
+      bl[st][p] = pack8(lds_tr16(sm.kl + b0), lds_tr16(sm.kl + b1));
     }
   }
   const float et = sm.etot;
@@ -643,7 +655,7 @@ __global__ __launch_bounds__(kScanThreads, 1) void dn_chunk_scan_kernel(ScanArgs
   auto store_split = [&](const float4 (&src)[4], __bf16* hi, __bf16* lo) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int o = ((tid >> 5) + 16 * j) * RB + 4 * (tid & 31);
+      const int o = qk_idx((tid >> 5) + 16 * j, 4 * (tid & 31));
       bf16x4 hh, ll;
       split4(src[j], hh, ll);
       *reinterpret_cast<bf16x4*>(hi + o) = hh;

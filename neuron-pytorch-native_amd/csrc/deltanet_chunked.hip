@@ -43,7 +43,7 @@ namespace {
 constexpr int CH = 64;                  // tokens per chunk
 constexpr int D = 128;                  // k and v head dims
 constexpr int NCB = 4;                  // 32-column blocks of V per head
-constexpr int MS = CH + 4;              // LDS row stride of A, T, intra and the [32][64] blocks
+constexpr int MS = CH + 4;              // LDS row stride of fp32 A, T (prep) and v^T (scan)
 constexpr float kNormEps = 1e-6f;
 constexpr float kQScale = 0.08838834764831845f;  // 1/sqrt(128)
 
@@ -86,8 +86,9 @@ typedef __bf16 bf16x8 __attribute__((__vector_size__(8 * sizeof(__bf16))));
 typedef __bf16 bf16x4 __attribute__((__vector_size__(4 * sizeof(__bf16))));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 
-constexpr int RB = D + 8;    // LDS row stride (bf16) of the split q, k and S^T rows: 272 bytes
-constexpr int VB = CH + 8;   // ... of the split (sk2 v_new)^T rows: 144 bytes
+constexpr int RB = D + 8;    // LDS row stride (bf16) of the split S^T rows (scan) and q, k rows
+                             // (prep): 272 bytes
+constexpr int VB = CH + 8;   // ... of the split 64-wide rows (T, intra, Z^T, v_new^T): 144 bytes
 
 __device__ __forceinline__ f32x4 mfma3(bf16x8 ah, bf16x8 al, bf16x8 bh, bf16x8 bl, f32x4 c) {
   c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, c, 0, 0, 0);

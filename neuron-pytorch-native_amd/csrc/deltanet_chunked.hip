@@ -191,7 +191,8 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(PrepArgs a) {
   const int qk_off = (tid >> 5) * (D * 4) + (tid & 31) * 16;
   float4 pq[8], pk[8];
   float pg = 0.f, pb = 0.f;
-  auto fetch = [&](int item) {
+  // half 0: rows 0..31 of q and k; half 1: rows 32..63, g and beta
+  auto fetch = [&](int item, int half) {
     const int h = item / a.nch, t0 = (item - h * a.nch) * CH;
     const size_t r0 = (size_t)h * S + t0;
     const int rest = S - t0;
@@ -199,17 +200,21 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(PrepArgs a) {
     const rsrc_t rk = make_rsrc(a.k + r0 * D, rest * D * 4);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
+      if ((j >> 2) != half) continue;
       pq[j] = bload4(rq, qk_off + 4096 * j, 0);
       pk[j] = bload4(rk, qk_off + 4096 * j, 0);
     }
-    if (wv == 0) {
+    if (half == 1 && wv == 0) {
       pg = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
                                          make_rsrc(a.g + r0, rest * 4), lane * 4, 0, 0));
       pb = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
                                          make_rsrc(a.beta + r0, rest * 4), lane * 4, 0, 0));
     }
   };
-  if (blockIdx.x < a.items) fetch(blockIdx.x);
+  if (blockIdx.x < a.items) {
+    fetch(blockIdx.x, 0);
+    fetch(blockIdx.x, 1);
+  }
   for (int item = blockIdx.x; item < a.items; item += gridDim.x) {
     const int h = item / a.nch, ci = item - h * a.nch;
     float* rec = a.ws + ((size_t)h * a.nch + ci) * REC;
@@ -237,7 +242,10 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(PrepArgs a) {
       sm.gcum[lane] = gi;
       sm.bt[lane] = pb;
     }
-    fetch(min(item + (int)gridDim.x, a.items - 1));  // unconditional: no branch forces a wait
+    // the next item's reads, in two halves (unconditional, so that no branch forces an early
+    // wait: the last item reads itself again)
+    const int nx = min(item + (int)gridDim.x, a.items - 1);
+    fetch(nx, 0);
     __syncthreads();
     {  // row norms from the split rows (hi + lo is x to 2^-17), 4 threads per row
       const int i = tid >> 2, part = tid & 3;
@@ -299,6 +307,7 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(PrepArgs a) {
         rih[CH * CH + i * CH + j] = (__bf16)(x - (float)hb);
       }
     }
+    fetch(nx, 1);
     __syncthreads();  // the q rows are consumed: A and T take their place
     // A[i][j] = -beta_i (k_i . k_j) rk_i rk_j dm(i, j) for i > j
     for (int t = wv; t < 10; t += 4) {

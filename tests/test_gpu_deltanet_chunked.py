@@ -4,7 +4,8 @@ relative bar, measured as Frobenius and elementwise (tests/_util.py).
 
 Cases: the reference test's heads (V_HEADS = 12 per core, contrib/qwen3.6-27b/kernels/tests/
 test_deltanet_chunked_v2.py:17-60, model gates), the 27B model's 48 v-heads (also at a 4096-token
-prompt, first and last head against the oracle at 1e-4), lengths that are
+prompt, first and last head against the oracle at 1e-4), a 16379-token prompt (256 chunks), the
+C entry point's workspace check, lengths that are
 and are not multiples of the chunk, a single token, the reference's chunk sizes in the [C, C]
 constants (16 and 64: the kernel chunks by 64 either way), identical pad rows (where the
 reference's doubling-product inverse blows up, test_doubling_pad_stability.py:1-19), and the
@@ -89,6 +90,38 @@ def test_full_size_heads_match_oracle(ops):
         assert_rel_close(s_, rs, name=f"head {h} new_state")
         assert np.abs(o - ro).max() <= 1e-4 * np.abs(ro).max(), f"head {h} out"
         assert np.abs(s_ - rs).max() <= 1e-4 * np.abs(rs).max(), f"head {h} new_state"
+
+
+def test_long_prompt_matches_oracle(ops):
+    """16384 tokens (256 chunks, with a partial last one) on 2 heads: the state carried through
+    the whole scan stays within 1e-4 of the float64 oracle."""
+    args = _inputs(2, 16384 - 5, 12)
+    out, ns = _run(ops, args, 64)
+    ro, rs = oc.chunked_prefill(*args, 64)
+    assert_rel_close(out, ro, name="out")
+    assert_rel_close(ns, rs, name="new_state")
+    assert np.abs(ns - rs).max() <= 1e-4 * np.abs(rs).max()
+
+
+def test_c_abi_rejects_small_workspace(ops):
+    """npn_deltanet_chunked_prefill checks its workspace before launching anything."""
+    import npn_native
+    Hv, S = 2, 130
+    t = [torch.from_numpy(np.ascontiguousarray(x)).cuda() for x in _inputs(Hv, S, 13)]
+    out = torch.empty(Hv * S, 128, device="cuda")
+    ns = torch.empty(Hv * 128, 128, device="cuda")
+    n_ws = npn_native.query("npn_deltanet_chunked_workspace_size", Hv, S)
+    assert n_ws == Hv * 3 * 34048
+    ws = torch.empty(n_ws, dtype=torch.uint8, device="cuda")
+    with pytest.raises(RuntimeError, match="status 4"):
+        npn_native.call("npn_deltanet_chunked_prefill", *t, out, ns, Hv, S, ws, n_ws - 16,
+                        npn_native.stream_of(out))
+    npn_native.call("npn_deltanet_chunked_prefill", *t, out, ns, Hv, S, ws, n_ws,
+                    npn_native.stream_of(out))
+    torch.cuda.synchronize()
+    ro, rs = oc.chunked_prefill(*[x.cpu().numpy() for x in t], 64)
+    assert_rel_close(out.cpu().numpy(), ro, name="out")
+    assert_rel_close(ns.cpu().numpy(), rs, name="new_state")
 
 
 def test_identical_pad_rows(ops):

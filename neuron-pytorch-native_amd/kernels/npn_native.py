@@ -86,7 +86,13 @@ def stream_of(t):
 
 
 def call(name, *args):
-    """Call an npn_* entry point; raise RuntimeError on a non-zero status."""
+    """Call an npn_* entry point; raise RuntimeError on a non-zero status.
+
+    Every tensor argument must sit on one device: the kernels dereference the raw pointers
+    on the device of the stream they are launched on."""
+    devices = {a.device for a in args if isinstance(a, torch.Tensor)}
+    if len(devices) > 1:
+        raise RuntimeError(f"{name}: tensor arguments span devices {sorted(map(str, devices))}")
     status = getattr(lib(), name)(*[_arg(a) for a in args])
     if status != 0:
         text = lib().npn_status_string(status).decode()

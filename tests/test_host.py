@@ -142,6 +142,14 @@ def test_ops_refuse_cpu_tensors():
         torch.ops.fp8.matmul(x, w, torch.ones(64, 1))
 
 
+def test_call_refuses_mixed_devices():
+    """The C-ABI takes raw pointers: tensors on two devices are refused before any call."""
+    import npn_native
+    a, b = torch.zeros(4), torch.zeros(4, device="meta")
+    with pytest.raises(RuntimeError, match="span devices"):
+        npn_native.call("npn_silu_mul", a, b, 1, 4, None)
+
+
 def test_rope_tables_match_oracle():
     """The step's table generator (torch fp32, as the reference's _init_rope) and the
     oracle's agree: inv_freq to 1 fp32 ulp, cos/sin tightly where position * ulp is small."""

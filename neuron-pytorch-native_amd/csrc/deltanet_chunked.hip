@@ -537,12 +537,55 @@ __device__ __forceinline__ void scan_vnew(ScanSmem& sm, int I, int J) {
   *reinterpret_cast<bf16x4*>(sm.vsl + o) = l;
 }
 
-// Pc: out rows of block I = O + intra v_new, written where the token exists.
-__device__ __forceinline__ void scan_out(ScanSmem& sm, float* orow, int I, int J, f32x4 o,
-                                         int nvalid) {
+// Operands that Pc takes from buffers the next chunk's inputs overwrite during Pc, read into
+// registers in Pb: the wave's intra rows (A of the output product, tokens 32 st + 8 g .. + 7;
+// blocks above the diagonal are zero), k's token columns for state tiles P0 + p (B of the
+// state update, read transposed) and e^tot.
+struct PcOps {
+  bf16x8 ih[2], il[2];
+  bf16x8 kh[2][2], kl[2][2];
+  float et;
+};
+__device__ __forceinline__ void scan_pc_loads(ScanSmem& sm, int I, int P0, PcOps& op) {
   const int lane = threadIdx.x & 63, g4 = lane >> 4, c = lane & 15;
-  const int ao = (16 * I + c) * VB + 8 * g4, bo = (16 * J + c) * VB + 8 * g4;
-  tile_tri(o, I, sm.ih + ao, sm.il + ao, sm.nh + bo, sm.nl + bo);
+  const int ao = (16 * I + c) * VB + 8 * g4;
+#pragma unroll
+  for (int st = 0; st < 2; ++st) {
+    op.ih[st] = ld8(sm.ih + ao + 32 * st);
+    op.il[st] = ld8(sm.il + ao + 32 * st);
+    const int r0 = 32 * st + 8 * g4 + (c >> 2);
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const int e = 16 * (P0 + p) + 4 * (c & 3);
+      const int b0 = qk_idx(r0, e), b1 = qk_idx(r0 + 4, e);
+      op.kh[st][p] = pack8(lds_tr16(sm.kh + b0), lds_tr16(sm.kh + b1));
+      op.kl[st][p] = pack8(lds_tr16(sm.kl + b0), lds_tr16(sm.kl + b1));
+    }
+  }
+  op.et = sm.etot;
+}
+
+// Pc: out rows of block I = O + intra v_new (over the tokens below 32 ceil((I + 1) / 2)),
+// written where the token exists.
+template <int NST>
+__device__ __forceinline__ void out_tile(ScanSmem& sm, int J, const PcOps& op, f32x4& o) {
+  const int lane = threadIdx.x & 63, g4 = lane >> 4, c = lane & 15;
+  const int bo = (16 * J + c) * VB + 8 * g4;
+  bf16x8 bh[NST], bl[NST];
+#pragma unroll
+  for (int st = 0; st < NST; ++st) {
+    bh[st] = ld8(sm.nh + bo + 32 * st);
+    bl[st] = ld8(sm.nl + bo + 32 * st);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int st = 0; st < NST; ++st) o = mfma3(op.ih[st], op.il[st], bh[st], bl[st], o);
+}
+__device__ __forceinline__ void scan_out(ScanSmem& sm, float* orow, int I, int J, f32x4 o,
+                                         int nvalid, const PcOps& op) {
+  const int lane = threadIdx.x & 63, g4 = lane >> 4, c = lane & 15;
+  if (I < 2) out_tile<1>(sm, J, op, o);
+  else out_tile<2>(sm, J, op, o);
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int i = 16 * I + 4 * g4 + r;
@@ -552,33 +595,25 @@ __device__ __forceinline__ void scan_out(ScanSmem& sm, float* orow, int I, int J
 
 // The wave's state tiles (J, P0 + p), held in registers as S^T[16 J + 4 g + r][16 (P0 + p) + c]:
 // S'^T = e^tot S^T + (sk2 v_new)^T k over the 64 tokens (split products, step st covering
-// tokens 32 st + 8 g .. + 7: the A operand from vsh / vsl rows, the B operand k's token column
-// read transposed), then the split of S'^T to LDS for the next chunk's products.
-__device__ __forceinline__ void scan_state_update(ScanSmem& sm, int J, int P0, f32x4 (&s)[2]) {
+// tokens 32 st + 8 g .. + 7: the A operand from vsh / vsl rows, the B operand k's token columns
+// from op), then the split of S'^T to LDS for the next chunk's products.
+__device__ __forceinline__ void scan_state_update(ScanSmem& sm, int J, int P0, f32x4 (&s)[2],
+                                                  const PcOps& op) {
   const int lane = threadIdx.x & 63, g4 = lane >> 4, c = lane & 15;
-  bf16x8 ah[2], al[2], bh[2][2], bl[2][2];
+  bf16x8 ah[2], al[2];
 #pragma unroll
   for (int st = 0; st < 2; ++st) {
     const int ao = (16 * J + c) * VB + 32 * st + 8 * g4;
     ah[st] = ld8(sm.vsh + ao);
     al[st] = ld8(sm.vsl + ao);
-    const int r0 = 32 * st + 8 * g4 + (c >> 2);
-#pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      const int e = 16 * (P0 + p) + 4 * (c & 3);
-      const int b0 = qk_idx(r0, e), b1 = qk_idx(r0 + 4, e);
-      bh[st][p] = pack8(lds_tr16(sm.kh + b0), lds_tr16(sm.kh + b1));
-      bl[st][p] = pack8(lds_tr16(sm.kl + b0), lds_tr16(sm.kl + b1));
-    }
   }
-  const float et = sm.etot;
 #pragma unroll
-  for (int p = 0; p < 2; ++p) s[p] *= et;
+  for (int p = 0; p < 2; ++p) s[p] *= op.et;
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int st = 0; st < 2; ++st)
 #pragma unroll
-    for (int p = 0; p < 2; ++p) s[p] = mfma3(ah[st], al[st], bh[st][p], bl[st][p], s[p]);
+    for (int p = 0; p < 2; ++p) s[p] = mfma3(ah[st], al[st], op.kh[st][p], op.kl[st][p], s[p]);
 #pragma unroll
   for (int p = 0; p < 2; ++p)
 #pragma unroll
@@ -629,10 +664,9 @@ __global__ __launch_bounds__(kScanThreads, 1) void dn_chunk_scan_kernel(ScanArgs
   //   part 0..3    q rows (tid >> 5) + 16 j, float4 column tid & 31    Pa / Pb (split)
   //   part 4       this block's v: row tid >> 3, columns 4 (tid & 7)    Pa / Pc
   //   part 5..6    T hi, lo (16 bytes tid of each)                      Pa / Pc
-  //   part 7       scales (wave 0, lane = token) and e^tot              Pa / Pc, and e^tot at the
-  //                next chunk's start (the state update reads the current one)
-  //   part 8..11   k rows, as q                                         Pa / next chunk's start
-  //   part 12..13  intra hi, lo, as T                                   Pb / next chunk's start
+  //   part 7       scales (wave 0, lane = token) and e^tot              Pa / Pc
+  //   part 8..11   k rows, as q                                         Pa / Pc (end)
+  //   part 12..13  intra hi, lo, as T                                   Pb / Pc (end)
   // Reads go through buffer descriptors based at the chunk's first row, sized to the end of
   // the prompt, so rows past it read as zeros.
   float4 pq[4], pk[4], pv, pt[2], pi[2];
@@ -685,18 +719,21 @@ __global__ __launch_bounds__(kScanThreads, 1) void dn_chunk_scan_kernel(ScanArgs
     *reinterpret_cast<float4*>(sm.tl + m_off) = pt[1];
     if (wv == 0) sm.sc[lane] = psc;
   };
-#pragma unroll
-  for (int part = 0; part < 14; ++part) fetch_part(0, part);
-  store_split(pq, sm.qh, sm.ql);
-  store_v_t_sc();
-  f32x4 o;
-  for (int ci = 0; ci < a.nch; ++ci) {
-    const int t0 = ci * CH;
-    __syncthreads();
+  auto store_k_intra = [&]() {
     store_split(pk, sm.kh, sm.kl);
     *reinterpret_cast<float4*>(sm.ih + m_off) = pi[0];
     *reinterpret_cast<float4*>(sm.il + m_off) = pi[1];
     if (wv == 0 && lane == 0) sm.etot = pet;
+  };
+#pragma unroll
+  for (int part = 0; part < 14; ++part) fetch_part(0, part);
+  store_split(pq, sm.qh, sm.ql);
+  store_v_t_sc();
+  store_k_intra();
+  f32x4 o;
+  PcOps op;
+  for (int ci = 0; ci < a.nch; ++ci) {
+    const int t0 = ci * CH;
     // the next chunk's reads (unconditional, so that no branch forces an early wait: the last
     // chunk reads itself again, and its late stores only rewrite buffers it no longer reads)
     const int nx = min(ci + 1, a.nch - 1);
@@ -707,14 +744,16 @@ __global__ __launch_bounds__(kScanThreads, 1) void dn_chunk_scan_kernel(ScanArgs
     __syncthreads();
     scan_state_products(sm, I, J, o, pre_a);
     __syncthreads();
+    scan_pc_loads(sm, I, P0, op);  // frees k, intra and e^tot for the next chunk's stores in Pc
     fetch_part(nx, 12);
     fetch_part(nx, 13);
     scan_vnew(sm, I, J);
     store_split(pq, sm.qh, sm.ql);  // q of this chunk was last read in Pa
     __syncthreads();
-    scan_out(sm, a.out + (row0 + t0) * D + c0, I, J, o, min(CH, S - t0));
+    scan_out(sm, a.out + (row0 + t0) * D + c0, I, J, o, min(CH, S - t0), op);
     store_v_t_sc();  // v, T and the scales were last read in Pa / Pb
-    scan_state_update(sm, J, P0, s);
+    scan_state_update(sm, J, P0, s, op);
+    store_k_intra();  // k, intra and e^tot of this chunk were last read in Pa / Pb
   }
 #pragma unroll
   for (int p = 0; p < 2; ++p)

@@ -524,15 +524,14 @@ __device__ __forceinline__ void scan_vnew(ScanSmem& sm, int I, int J) {
   const int lane = threadIdx.x & 63, g4 = lane >> 4, c = lane & 15;
   f32x4 acc = zero4();
   const int ao = (16 * I + c) * VB + 8 * g4, bo = (16 * J + c) * VB + 8 * g4;
-  tile_tri(acc, I, sm.th + ao, sm.tl + ao, sm.zh + bo, sm.zl + bo);
   const int i0 = 16 * I + 4 * g4, o = (16 * J + c) * VB + i0;
+  const float z0 = sm.sc[i0].z, z1 = sm.sc[i0 + 1].z, z2 = sm.sc[i0 + 2].z, z3 = sm.sc[i0 + 3].z;
+  tile_tri(acc, I, sm.th + ao, sm.tl + ao, sm.zh + bo, sm.zl + bo);
   bf16x4 h, l;
   split4(make_float4(acc[0], acc[1], acc[2], acc[3]), h, l);
   *reinterpret_cast<bf16x4*>(sm.nh + o) = h;
   *reinterpret_cast<bf16x4*>(sm.nl + o) = l;
-  split4(make_float4(acc[0] * sm.sc[i0].z, acc[1] * sm.sc[i0 + 1].z, acc[2] * sm.sc[i0 + 2].z,
-                     acc[3] * sm.sc[i0 + 3].z),
-         h, l);
+  split4(make_float4(acc[0] * z0, acc[1] * z1, acc[2] * z2, acc[3] * z3), h, l);
   *reinterpret_cast<bf16x4*>(sm.vsh + o) = h;
   *reinterpret_cast<bf16x4*>(sm.vsl + o) = l;
 }

@@ -164,6 +164,9 @@ def cpu_baseline(model, x, logits, budget_s=10.0):
 
 
 LM_VOCAB = 248320  # Qwen3.6-27B vocabulary (static_decode.py:107)
+# untimed calls per variant before its timed ones, at least: with 3 the shader clock has not
+# settled for the first variant (measured: fused 0.808 ms per call after 3, 0.772 after 64)
+LM_MIN_WARMUP = 64
 
 
 def lm_head_bench(args):
@@ -188,8 +191,9 @@ def lm_head_bench(args):
         return torch.ops.spec.accept_greedy(logits, drafts)
 
     res = {}
+    warmup = max(args.warmup, LM_MIN_WARMUP)
     for name, fn in (("fused", fused), ("unfused", unfused)):
-        for i in range(args.warmup):
+        for i in range(warmup):
             fn(i)
         torch.cuda.synchronize()
         s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -209,7 +213,7 @@ def lm_head_bench(args):
         "fused_tflops": round(flops / res["fused"] / 1e9, 1),
         "weights_gb": round(HIDDEN * LM_VOCAB / 1e9, 3),
         "identical": bool(torch.equal(a_f, a_u) and torch.equal(o_f, o_u)),
-        "steps": args.steps, "warmup": args.warmup}))
+        "steps": args.steps, "warmup": warmup}))
 
 
 PF_HEADS, PF_TOKENS, PF_CHUNK, PF_DIM = 48, 4096, 64, 128

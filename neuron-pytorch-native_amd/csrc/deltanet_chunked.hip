@@ -743,15 +743,17 @@ __global__ __launch_bounds__(kScanThreads, 1) void dn_chunk_scan_kernel(ScanArgs
     __syncthreads();
     scan_state_products(sm, I, J, o, pre_a);
     __syncthreads();
-    scan_pc_loads(sm, I, P0, op);  // frees k, intra and e^tot for the next chunk's stores in Pc
     fetch_part(nx, 12);
     fetch_part(nx, 13);
     scan_vnew(sm, I, J);
+    // after v_new's operand reads (a wave's LDS requests return in order): frees k, intra and
+    // e^tot for the next chunk's stores in Pc
+    scan_pc_loads(sm, I, P0, op);
     store_split(pq, sm.qh, sm.ql);  // q of this chunk was last read in Pa
     __syncthreads();
+    scan_state_update(sm, J, P0, s, op);  // first: the next chunk waits on its split of S
     scan_out(sm, a.out + (row0 + t0) * D + c0, I, J, o, min(CH, S - t0), op);
     store_v_t_sc();  // v, T and the scales were last read in Pa / Pb
-    scan_state_update(sm, J, P0, s, op);
     store_k_intra();  // k, intra and e^tot of this chunk were last read in Pa / Pb
   }
 #pragma unroll

@@ -445,8 +445,8 @@ struct ScanSmem {
 // share a SIMD, so each SIMD holds row blocks {3, 0} or {2, 1}: the triangular products
 // (T Z, intra v_new) are balanced per SIMD, and its two waves cover each other's waits. The
 // older wave, which wins the SIMD's issue arbitration, takes the longer triangular chain.
-// The wave also owns state tiles (J, P0) and (J, P0 + 1), P0 = 2 ((w >> 1) & 3), in fp32
-// registers for the whole prompt.
+// The wave also owns the state tiles S[16 (P0 + p) .. + 15][16 J .. + 15] of the block's 32
+// columns (p = 0, 1; P0 = 2 ((w >> 1) & 3)) in fp32 registers for the whole prompt.
 
 // Pa: X = (raw k) S and O = (raw q) S for rows of block I (split products over the 128 k
 // indices, step st covering 32 st + 8 g .. + 7 for lane group g); Z = beta (v - sk1 X), split
@@ -592,10 +592,11 @@ __device__ __forceinline__ void scan_out(ScanSmem& sm, float* orow, int I, int J
   }
 }
 
-// The wave's state tiles (J, P0 + p), held in registers as S^T[16 J + 4 g + r][16 (P0 + p) + c]:
-// S'^T = e^tot S^T + (sk2 v_new)^T k over the 64 tokens (split products, step st covering
-// tokens 32 st + 8 g .. + 7: the A operand from vsh / vsl rows, the B operand k's token columns
-// from op), then the split of S'^T to LDS for the next chunk's products.
+// The wave's state tiles (P0 + p, J), held in registers as S[16 (P0 + p) + 4 g + r][16 J + c]:
+// S' = e^tot S + k^T (sk2 v_new) over the 64 tokens (split products, step st covering tokens
+// 32 st + 8 g .. + 7: the A operand k's token columns from op, the B operand from vsh / vsl
+// rows), then the split of S' to LDS, where a lane's 4 values are consecutive k indices of one
+// S^T row (one 8-byte store per half and tile).
 __device__ __forceinline__ void scan_state_update(ScanSmem& sm, int J, int P0, f32x4 (&s)[2],
                                                   const PcOps& op) {
   const int lane = threadIdx.x & 63, g4 = lane >> 4, c = lane & 15;
@@ -612,16 +613,15 @@ __device__ __forceinline__ void scan_state_update(ScanSmem& sm, int J, int P0, f
 #pragma unroll
   for (int st = 0; st < 2; ++st)
 #pragma unroll
-    for (int p = 0; p < 2; ++p) s[p] = mfma3(ah[st], al[st], op.kh[st][p], op.kl[st][p], s[p]);
+    for (int p = 0; p < 2; ++p) s[p] = mfma3(op.kh[st][p], op.kl[st][p], ah[st], al[st], s[p]);
 #pragma unroll
-  for (int p = 0; p < 2; ++p)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int o = (16 * J + 4 * g4 + r) * RB + 16 * (P0 + p) + c;
-      const __bf16 h = (__bf16)s[p][r];
-      sm.sh[o] = h;
-      sm.sl[o] = (__bf16)(s[p][r] - (float)h);
-    }
+  for (int p = 0; p < 2; ++p) {
+    const int o = (16 * J + c) * RB + 16 * (P0 + p) + 4 * g4;
+    bf16x4 h, l;
+    split4(make_float4(s[p][0], s[p][1], s[p][2], s[p][3]), h, l);
+    *reinterpret_cast<bf16x4*>(sm.sh + o) = h;
+    *reinterpret_cast<bf16x4*>(sm.sl + o) = l;
+  }
 }
 
 constexpr int kScanThreads = 512;
@@ -641,20 +641,18 @@ __global__ __launch_bounds__(kScanThreads, 1) void dn_chunk_scan_kernel(ScanArgs
   const size_t row0 = (size_t)h * S;
   const int c0 = 32 * cb;
 
-  // this wave's state tiles: S[16 (P0 + p) + c][c0 + 16 J + 4 g + r] in s[p][r], and their split
+  // this wave's state tiles: S[16 (P0 + p) + 4 g + r][c0 + 16 J + c] in s[p][r], and their split
   f32x4 s[2];
 #pragma unroll
   for (int p = 0; p < 2; ++p) {
-    const float4 v4 = *reinterpret_cast<const float4*>(
-        a.state + ((size_t)h * D + 16 * (P0 + p) + c) * D + c0 + 16 * J + 4 * g4);
-    s[p] = f32x4{v4.x, v4.y, v4.z, v4.w};
+    const float* src = a.state + ((size_t)h * D + 16 * (P0 + p) + 4 * g4) * D + c0 + 16 * J + c;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int o = (16 * J + 4 * g4 + r) * RB + 16 * (P0 + p) + c;
-      const __bf16 hb = (__bf16)s[p][r];
-      sm.sh[o] = hb;
-      sm.sl[o] = (__bf16)(s[p][r] - (float)hb);
-    }
+    for (int r = 0; r < 4; ++r) s[p][r] = src[r * D];
+    const int o = (16 * J + c) * RB + 16 * (P0 + p) + 4 * g4;
+    bf16x4 hh, ll;
+    split4(make_float4(s[p][0], s[p][1], s[p][2], s[p][3]), hh, ll);
+    *reinterpret_cast<bf16x4*>(sm.sh + o) = hh;
+    *reinterpret_cast<bf16x4*>(sm.sl + o) = ll;
   }
   // The next chunk's inputs are read into registers while the current chunk computes, in
   // parts issued between the products (reading a chunk's 104 KB at once stalls every wave on
@@ -757,9 +755,11 @@ __global__ __launch_bounds__(kScanThreads, 1) void dn_chunk_scan_kernel(ScanArgs
     store_k_intra();  // k, intra and e^tot of this chunk were last read in Pa / Pb
   }
 #pragma unroll
-  for (int p = 0; p < 2; ++p)
-    *reinterpret_cast<float4*>(a.new_state + ((size_t)h * D + 16 * (P0 + p) + c) * D + c0 +
-                               16 * J + 4 * g4) = make_float4(s[p][0], s[p][1], s[p][2], s[p][3]);
+  for (int p = 0; p < 2; ++p) {
+    float* dst = a.new_state + ((size_t)h * D + 16 * (P0 + p) + 4 * g4) * D + c0 + 16 * J + c;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) dst[r * D] = s[p][r];
+  }
 }
 
 constexpr int kPrepGrid = 512;  // two prep workgroups per CU (70 KB of LDS each)

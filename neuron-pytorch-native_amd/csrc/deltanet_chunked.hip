@@ -43,7 +43,7 @@ namespace {
 constexpr int CH = 64;                  // tokens per chunk
 constexpr int D = 128;                  // k and v head dims
 constexpr int NCB = 4;                  // 32-column blocks of V per head
-constexpr int MS = CH + 4;              // LDS row stride of fp32 A, T (prep) and v^T (scan)
+constexpr int MS = CH + 4;              // LDS row stride of the prep's fp32 A and T
 constexpr float kNormEps = 1e-6f;
 constexpr float kQScale = 0.08838834764831845f;  // 1/sqrt(128)
 
@@ -426,16 +426,20 @@ __device__ __forceinline__ int qk_idx(int r, int e) {
   return r * D + (((e >> 3) ^ (2 * (r & 3) + ((r >> 2) & 1))) << 3) + (e & 7);
 }
 
+constexpr int VS = 32 + 4;   // LDS row stride (fp32) of the block's v rows: 144 bytes
+constexpr int ZB = 32 + 16;  // LDS row stride (bf16) of the split Z rows: 96 bytes, so that a
+                             // transposed read's 4 rows fall on distinct banks
+
 struct ScanSmem {
   __bf16 qh[CH * D], ql[CH * D];      // q rows of the chunk, split (qk_idx layout)
   __bf16 kh[CH * D], kl[CH * D];      // k rows, split (qk_idx layout)
   __bf16 sh[32 * RB], sl[32 * RB];    // the state block transposed ([column][k index]), split
   __bf16 th[CH * VB], tl[CH * VB];    // T, split (as the record holds it)
   __bf16 ih[CH * VB], il[CH * VB];    // intra, split
-  __bf16 zh[32 * VB], zl[32 * VB];    // Z^T, split
+  __bf16 zh[CH * ZB], zl[CH * ZB];    // Z rows ([token][column]), split
   __bf16 nh[32 * VB], nl[32 * VB];    // v_new^T, split
   __bf16 vsh[32 * VB], vsl[32 * VB];  // (sk2 v_new)^T, split
-  float vT[32 * MS];                  // v^T of the chunk (fp32)
+  float vr[CH * VS];                  // v rows of the chunk, the block's 32 columns (fp32)
   float4 sc[CH];                      // sq, sk1, sk2, beta
   float etot;
 };
@@ -449,8 +453,11 @@ struct ScanSmem {
 // columns (p = 0, 1; P0 = 2 ((w >> 1) & 3)) in fp32 registers for the whole prompt.
 
 // Pa: X = (raw k) S and O = (raw q) S for rows of block I (split products over the 128 k
-// indices, step st covering 32 st + 8 g .. + 7 for lane group g); Z = beta (v - sk1 X), split
-// into zh / zl; O *= sq. pre(st) issues part of the next chunk's reads between the products.
+// indices, step st covering 32 st + 8 g .. + 7 for lane group g), formed as transposed tiles
+// (S^T as the A operand) so that x[r], o[r] hold token 16 I + c, column 16 J + 4 g + r: a
+// lane's v row, scales, Z and out are then one 16-byte access each. Z = beta (v - sk1 X),
+// split into zh / zl; O *= sq. pre(st) issues part of the next chunk's reads between the
+// products.
 template <typename Pre>
 __device__ __forceinline__ void scan_state_products(ScanSmem& sm, int I, int J, f32x4& o,
                                                     Pre&& pre) {
@@ -476,57 +483,50 @@ __device__ __forceinline__ void scan_state_products(ScanSmem& sm, int I, int J, 
     }
     pre(st);
     __builtin_amdgcn_sched_barrier(0);
-    x = mfma3(kh, kl, sh, sl, x);
-    o = mfma3(qh, ql, sh, sl, o);
+    x = mfma3(sh, sl, kh, kl, x);
+    o = mfma3(sh, sl, qh, ql, o);
   }
-  const int i0 = 16 * I + 4 * g4;
-  const float4 v = ld4(sm.vT + (16 * J + c) * MS + i0);
-  const float4 s0 = sm.sc[i0], s1 = sm.sc[i0 + 1], s2 = sm.sc[i0 + 2], s3 = sm.sc[i0 + 3];
+  const int i = 16 * I + c, zo = i * ZB + 16 * J + 4 * g4;
+  const float4 v = ld4(sm.vr + i * VS + 16 * J + 4 * g4);
+  const float4 sc = sm.sc[i];
   bf16x4 zh, zl;
-  split4(make_float4(s0.w * (v.x - s0.y * x[0]), s1.w * (v.y - s1.y * x[1]),
-                     s2.w * (v.z - s2.y * x[2]), s3.w * (v.w - s3.y * x[3])),
+  split4(make_float4(sc.w * (v.x - sc.y * x[0]), sc.w * (v.y - sc.y * x[1]),
+                     sc.w * (v.z - sc.y * x[2]), sc.w * (v.w - sc.y * x[3])),
          zh, zl);
-  *reinterpret_cast<bf16x4*>(sm.zh + (16 * J + c) * VB + i0) = zh;
-  *reinterpret_cast<bf16x4*>(sm.zl + (16 * J + c) * VB + i0) = zl;
-  o[0] *= s0.x;
-  o[1] *= s1.x;
-  o[2] *= s2.x;
-  o[3] *= s3.x;
+  *reinterpret_cast<bf16x4*>(sm.zh + zo) = zh;
+  *reinterpret_cast<bf16x4*>(sm.zl + zo) = zl;
+  o *= sc.x;
 }
 
-// acc += A B with a lower-triangular left factor from split rows over the tokens below
-// 32 ceil((I + 1) / 2) (A is zero above its diagonal, so the rounding up adds zero products):
-// ah = &A_hi[16 I + c][8 g], bh = &B^T_hi[col c][8 g], step st covering tokens 32 st + 8 g ..
-// + 7.
+// acc += T Z for rows of block I over the tokens below 32 ceil((I + 1) / 2) (T is zero above
+// its diagonal, so the rounding up adds zero products), step st covering tokens 32 st + 8 g ..
+// + 7: T's rows as the A operand, Z's columns read transposed from its rows as the B operand.
 template <int NST>
-__device__ __forceinline__ void tile_split_tri(f32x4& acc, const __bf16* ah, const __bf16* al,
-                                               const __bf16* bh, const __bf16* bl) {
+__device__ __forceinline__ void tile_tz(f32x4& acc, ScanSmem& sm, int I, int J) {
+  const int lane = threadIdx.x & 63, g4 = lane >> 4, c = lane & 15;
+  const int ao = (16 * I + c) * VB + 8 * g4;
   bf16x8 x[NST][4];
 #pragma unroll
   for (int st = 0; st < NST; ++st) {
-    x[st][0] = ld8(ah + 32 * st);
-    x[st][1] = ld8(al + 32 * st);
-    x[st][2] = ld8(bh + 32 * st);
-    x[st][3] = ld8(bl + 32 * st);
+    x[st][0] = ld8(sm.th + ao + 32 * st);
+    x[st][1] = ld8(sm.tl + ao + 32 * st);
+    const int b0 = (32 * st + 8 * g4 + (c >> 2)) * ZB + 16 * J + 4 * (c & 3);
+    x[st][2] = pack8(lds_tr16(sm.zh + b0), lds_tr16(sm.zh + b0 + 4 * ZB));
+    x[st][3] = pack8(lds_tr16(sm.zl + b0), lds_tr16(sm.zl + b0 + 4 * ZB));
   }
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int st = 0; st < NST; ++st) acc = mfma3(x[st][0], x[st][1], x[st][2], x[st][3], acc);
-}
-__device__ __forceinline__ void tile_tri(f32x4& acc, int I, const __bf16* ah, const __bf16* al,
-                                         const __bf16* bh, const __bf16* bl) {
-  if (I < 2) tile_split_tri<1>(acc, ah, al, bh, bl);
-  else tile_split_tri<2>(acc, ah, al, bh, bl);
 }
 
 // Pb: v_new rows of block I = T Z, split into nh / nl, and sk2 v_new split into vsh / vsl.
 __device__ __forceinline__ void scan_vnew(ScanSmem& sm, int I, int J) {
   const int lane = threadIdx.x & 63, g4 = lane >> 4, c = lane & 15;
   f32x4 acc = zero4();
-  const int ao = (16 * I + c) * VB + 8 * g4, bo = (16 * J + c) * VB + 8 * g4;
   const int i0 = 16 * I + 4 * g4, o = (16 * J + c) * VB + i0;
   const float z0 = sm.sc[i0].z, z1 = sm.sc[i0 + 1].z, z2 = sm.sc[i0 + 2].z, z3 = sm.sc[i0 + 3].z;
-  tile_tri(acc, I, sm.th + ao, sm.tl + ao, sm.zh + bo, sm.zl + bo);
+  if (I < 2) tile_tz<1>(acc, sm, I, J);
+  else tile_tz<2>(acc, sm, I, J);
   bf16x4 h, l;
   split4(make_float4(acc[0], acc[1], acc[2], acc[3]), h, l);
   *reinterpret_cast<bf16x4*>(sm.nh + o) = h;
@@ -564,8 +564,9 @@ __device__ __forceinline__ void scan_pc_loads(ScanSmem& sm, int I, int P0, PcOps
   op.et = sm.etot;
 }
 
-// Pc: out rows of block I = O + intra v_new (over the tokens below 32 ceil((I + 1) / 2)),
-// written where the token exists.
+// Pc: out rows of block I = O + intra v_new (over the tokens below 32 ceil((I + 1) / 2)), a
+// transposed tile like O (v_new^T rows as the A operand, intra rows as the B operand), written
+// where the token exists.
 template <int NST>
 __device__ __forceinline__ void out_tile(ScanSmem& sm, int J, const PcOps& op, f32x4& o) {
   const int lane = threadIdx.x & 63, g4 = lane >> 4, c = lane & 15;
@@ -578,18 +579,17 @@ __device__ __forceinline__ void out_tile(ScanSmem& sm, int J, const PcOps& op, f
   }
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int st = 0; st < NST; ++st) o = mfma3(op.ih[st], op.il[st], bh[st], bl[st], o);
+  for (int st = 0; st < NST; ++st) o = mfma3(bh[st], bl[st], op.ih[st], op.il[st], o);
 }
 __device__ __forceinline__ void scan_out(ScanSmem& sm, float* orow, int I, int J, f32x4 o,
                                          int nvalid, const PcOps& op) {
   const int lane = threadIdx.x & 63, g4 = lane >> 4, c = lane & 15;
   if (I < 2) out_tile<1>(sm, J, op, o);
   else out_tile<2>(sm, J, op, o);
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int i = 16 * I + 4 * g4 + r;
-    if (i < nvalid) orow[(size_t)i * D + 16 * J + c] = o[r];
-  }
+  const int i = 16 * I + c;
+  if (i < nvalid)
+    *reinterpret_cast<float4*>(orow + (size_t)i * D + 16 * J + 4 * g4) =
+        make_float4(o[0], o[1], o[2], o[3]);
 }
 
 // The wave's state tiles (P0 + p, J), held in registers as S[16 (P0 + p) + 4 g + r][16 J + c]:
@@ -707,11 +707,7 @@ __global__ __launch_bounds__(kScanThreads, 1) void dn_chunk_scan_kernel(ScanArgs
   // columns 8 (tid & 7) .. + 7)
   const int m_off = (tid >> 3) * VB + 8 * (tid & 7);
   auto store_v_t_sc = [&]() {
-    float* vd = sm.vT + 4 * (tid & 7) * MS + (tid >> 3);
-    vd[0] = pv.x;
-    vd[MS] = pv.y;
-    vd[2 * MS] = pv.z;
-    vd[3 * MS] = pv.w;
+    *reinterpret_cast<float4*>(sm.vr + (tid >> 3) * VS + 4 * (tid & 7)) = pv;
     *reinterpret_cast<float4*>(sm.th + m_off) = pt[0];
     *reinterpret_cast<float4*>(sm.tl + m_off) = pt[1];
     if (wv == 0) sm.sc[lane] = psc;

@@ -211,7 +211,7 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep_kernel(PrepArgs a) {
                                          make_rsrc(a.beta + r0, rest * 4), lane * 4, 0, 0));
     }
   };
-  if (blockIdx.x < a.items) {
+  if ((int)blockIdx.x < a.items) {
     fetch(blockIdx.x, 0);
     fetch(blockIdx.x, 1);
   }

@@ -54,7 +54,10 @@ __device__ __forceinline__ float wave_max(float v) {
 // (global_load_lds_dwordx4; lds_base must be the same for the whole wave). Issued through
 // inline asm so the compiler does not add a conservative vmcnt(0) wait before later LDS
 // reads of other buffers: callers track completion themselves with s_waitcnt vmcnt(n)
-// and make it visible to the other waves with s_barrier.
+// and make it visible to the other waves with s_barrier. hipcc warns that m0 is a reserved
+// register and ignores it in the clobber list; the statement sets m0 itself, and in the
+// gfx950 code of the kernels that use it every instruction naming m0 is such an
+// `s_mov_b32 m0`, so no compiler-held value in m0 spans it.
 __device__ __forceinline__ void lds_dma16(const void* g, const void* lds_base) {
   const unsigned base = __builtin_amdgcn_readfirstlane(
       (unsigned)(uintptr_t)(__attribute__((address_space(3))) const void*)lds_base);

@@ -87,7 +87,7 @@ int npn_deltanet_verify(const float* state, const int32_t* state_index, int stat
                         uint16_t* out, int B, int T, int k_heads, int v_heads, void* stream);
 
 /* torch.ops.deltanet.rollback -- new op: roll back to the accepted prefix
- * (contrib/qwen3.6-27b/kernels/tests/test_deltanet_spec_verify_rollback.py:153-157).
+ * (contrib/qwen3.6-27b/kernels/tests/test_deltanet_spec_verify_rollback.py:64-68).
  *   accepted [B] int32 in [0, T-1] (number of accepted drafts).
  *   state_out [B, Hv, 128, 128] f32 = ckpt[b, accepted[b]] (may be NULL to skip
  *   the copy when the next verify uses state_index instead);
@@ -241,6 +241,9 @@ int npn_accept_greedy(const float* target_logits, const int64_t* draft_ids, int3
  *   Accept draft x iff U * Eq_x * Zp <= 2^24 * Ep_x * Zq. At the first rejection
  *   sample from R_v = max(0, Ep_v*Zq - Eq_v*Zp) (bonus: R_v = Ep_v of row K):
  *   the smallest v with 2^24 * sum_{w<=v} R_w > U_s * sum_w R_w.
+ *   A row with no finite entry relative to its maximum (all NaN or -inf, or a +inf
+ *   entry) has Z = 0 and passes the accept test; if the bonus row has no mass the
+ *   token is its argmax (NaN counts as the maximum, ties go to the lowest index).
  *   target_logits [B, K+1, V] f32, draft_logits [B, K, V] f32, draft_ids [B, K]
  *   int64, u_accept [B, K] f32 in [0,1), u_sample [B] f32 in [0,1),
  *   inv_temperature > 0 (logits are multiplied by it), V <= 2^20.

@@ -185,13 +185,16 @@ __global__ __launch_bounds__(kThreads, 3) void dn_verify_kernel(DnArgs a) {
     }
   }
 
-  // Gated RMSNorm of o_t over the 128 v columns.
+  // Gated RMSNorm of o_t over the 128 v columns (tokens t < T only: s_o[t] is written for
+  // those alone).
   __syncthreads();
 #pragma unroll
   for (int t = wid; t < TMAX; t += 2) {
-    const float o0 = s_o[t][lane], o1 = s_o[t][lane + 64];
-    const float so = npn::wave_sum(o0 * o0 + o1 * o1);
-    if (lane == 0) s_ro[t] = rsqrtf(so * (1.0f / D) + kEps);
+    if (t < T) {
+      const float o0 = s_o[t][lane], o1 = s_o[t][lane + 64];
+      const float so = npn::wave_sum(o0 * o0 + o1 * o1);
+      if (lane == 0) s_ro[t] = rsqrtf(so * (1.0f / D) + kEps);
+    }
   }
   __syncthreads();
   const float nw = a.norm_weight[tid];

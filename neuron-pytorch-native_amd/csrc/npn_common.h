@@ -54,15 +54,25 @@ __device__ __forceinline__ float wave_max(float v) {
 // (global_load_lds_dwordx4; lds_base must be the same for the whole wave). Issued through
 // inline asm so the compiler does not add a conservative vmcnt(0) wait before later LDS
 // reads of other buffers: callers track completion themselves with s_waitcnt vmcnt(n)
-// and make it visible to the other waves with s_barrier. hipcc warns that m0 is a reserved
-// register and ignores it in the clobber list; the statement sets m0 itself, and in the
-// gfx950 code of the kernels that use it every instruction naming m0 is such an
-// `s_mov_b32 m0`, so no compiler-held value in m0 spans it.
+// and make it visible to the other waves with s_barrier.
+// The DMA takes its LDS base from m0, a register the compiler reserves (it does not honour
+// m0 in a clobber list). The statement therefore leaves m0 as it found it: it copies m0 to a
+// scratch SGPR, sets the base, and restores m0 after the issue (the instruction reads m0
+// when it issues). GFX9 needs one wait state between an SALU write of m0 and an LDS DMA
+// that reads it, hence the s_nop.
 __device__ __forceinline__ void lds_dma16(const void* g, const void* lds_base) {
   const unsigned base = __builtin_amdgcn_readfirstlane(
       (unsigned)(uintptr_t)(__attribute__((address_space(3))) const void*)lds_base);
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(base)
-               : "memory", "m0");
+  unsigned saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(g), "s"(base)
+      : "memory");
 }
 
 // Same DMA with a wave-uniform global base (SGPR pair) and a 32-bit per-lane byte offset,
@@ -71,9 +81,16 @@ __device__ __forceinline__ void lds_dma16_soff(const void* sbase, unsigned voff,
                                                const void* lds_base) {
   const unsigned base = __builtin_amdgcn_readfirstlane(
       (unsigned)(uintptr_t)(__attribute__((address_space(3))) const void*)lds_base);
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase),
-               "s"(base)
-               : "memory", "m0");
+  unsigned saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %3\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, %2\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(voff), "s"(sbase), "s"(base)
+      : "memory");
 }
 
 }  // namespace npn

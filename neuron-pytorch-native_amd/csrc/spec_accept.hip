@@ -548,12 +548,15 @@ __global__ __launch_bounds__(THREADS) void rej_pick_kernel(RejArgs a) {
   __shared__ u128 s_target;
   __shared__ u128 s_wtot[THREADS / 64];
   __shared__ int s_tok;
+  __shared__ int s_empty;
+  __shared__ ArgPart s_best[THREADS / 64];
   const u128* cm = a.cmass + (size_t)b * a.nchm;
   if (w == 0) {
     u128 tot = 0;
     for (int c = lane; c < a.nchm; c += 64) tot += cm[c];
     tot = wave_incl_scan_u128(tot);
     tot = shfl_u128(tot, 63);
+    if (lane == 0) s_empty = tot == 0;
     const u128 target = (u128)uniform_fix(a.u_sample[b]) * tot;  // need 2^24 * C > target
     u128 carry = 0;
     int chunk = a.nchm - 1;
@@ -580,6 +583,30 @@ __global__ __launch_bounds__(THREADS) void rej_pick_kernel(RejArgs a) {
     }
   }
   __syncthreads();
+  if (s_empty) {
+    // No sampling mass: every E of the sampling row is 0, which happens only for a bonus row
+    // whose logits are all NaN or -inf or include +inf (a residual after a rejection always
+    // has mass). The token is then the row's greedy choice: its argmax, NaN counting as the
+    // maximum and ties going to the lowest index (the order of argmax_chunk_kernel).
+    float bv = -INFINITY;
+    int bi = 0x7FFFFFFF;
+    for (int v = (int)threadIdx.x; v < a.V; v += THREADS)
+      if (beats(s.p[v], v, bv, bi)) { bv = s.p[v]; bi = v; }
+    for (int off = 32; off > 0; off >>= 1) {
+      const float ov = __shfl_xor(bv, off, 64);
+      const int oi = __shfl_xor(bi, off, 64);
+      if (beats(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+    }
+    if (lane == 0) s_best[w] = ArgPart{bv, bi};
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      ArgPart best = s_best[0];
+      for (int k = 1; k < THREADS / 64; ++k)
+        if (beats(s_best[k].v, s_best[k].i, best.v, best.i)) best = s_best[k];
+      a.out_ids[(size_t)b * (a.K + 1) + a.dec_row[b]] = best.i;
+    }
+    return;
+  }
   const int v0 = s_chunk * MCHK + (int)threadIdx.x * PER_M;
   RunVals rv;
   u128 run = 0;

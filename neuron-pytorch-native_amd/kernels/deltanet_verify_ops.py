@@ -21,7 +21,7 @@ the T = K+1 tokens of a speculative verify block:
 
 ckpt[b, t] is the state after verify token t; with `accepted` drafts the
 sequence continues from ckpt[b, accepted] -- the reference's traj[k-1] with
-k = accepted + 1 (contrib/qwen3.6-27b/kernels/tests/test_deltanet_spec_verify_rollback.py:153-157).
+k = accepted + 1 (contrib/qwen3.6-27b/kernels/tests/test_deltanet_spec_verify_rollback.py:64-68).
 T is derived from a_out: T = a_out.numel() // (B*Hv).
 """
 import torch

@@ -34,6 +34,12 @@ Integer softmax contract (shared bit-for-bit with ``csrc/spec_accept.hip``):
 - At the first rejection sample from R_v = max(0, E^p_v Z_q - E^q_v Z_p); if all
   K drafts are accepted sample the bonus from R_v = E^p_v of row K. The token is
   the smallest v with 2^24 * sum_{w<=v} R_w > U_s * sum_w R_w.
+- Rows without mass: Z = 0 when no entry is finite relative to the maximum (all NaN or
+  -inf, or a +inf entry). Such a target or draft row passes the accept test (both sides
+  are 0). A residual after a rejection always has mass (sum_v (E^p_v Z_q - E^q_v Z_p) = 0
+  with a negative term at the rejected token), so only a bonus row can be empty; its token
+  is then the greedy one, argmax of the target row (NaN counts as the maximum, first index
+  on ties).
 """
 import numpy as np
 
@@ -153,7 +159,12 @@ def accept_rejection(target, draft, draft_ids, u_accept, u_sample, inv_temp=1.0)
         else:
             Ep, _, _ = row_weights(target[b, K], inv_temp)
             R = [int(e) for e in Ep.tolist()]
-        out[b, a] = _inverse_cdf(R, Us)
+        if sum(R) == 0:
+            # no sampling mass (only a bonus row whose logits are all NaN / -inf or hold +inf:
+            # every E is 0): the row's greedy token, NaN counting as the maximum
+            out[b, a] = int(argmax_first(target[b, a]))
+        else:
+            out[b, a] = _inverse_cdf(R, Us)
     return accepted, out
 
 

@@ -128,3 +128,31 @@ def test_rejection_row_sums_bit_exact(ops, B, K, V, seed, inv_t):
                                      us.numpy(), inv_t)
     assert np.array_equal(acc.cpu().numpy(), racc)
     assert np.array_equal(out.cpu().numpy(), rout)
+
+
+@pytest.mark.parametrize("V", [50, 151936])
+def test_rejection_empty_bonus_rows(ops, V):
+    """Bonus rows without mass (all NaN, all -inf, a +inf entry) emit the row's argmax, a
+    valid token id (NaN first, then +inf, ties to the lowest index), as the oracle does;
+    a row whose NaN entries sit among finite ones still samples by inverse CDF."""
+    B, K = 5, 3
+    g = torch.Generator().manual_seed(31)
+    target = torch.randn(B, K + 1, V, generator=g)
+    draft = target[:, :K].clone()                       # p == q: every draft accepted
+    ids = torch.randint(0, V, (B, K), generator=g)
+    u, us = torch.rand(B, K, generator=g), torch.rand(B, generator=g)
+    target[0, K] = float("nan")
+    target[1, K] = float("-inf")
+    target[2, K, V // 3] = float("inf")
+    target[2, K, V - 1] = float("inf")
+    target[3, K, 7] = float("nan")
+    target[3, K, V - 2] = float("nan")
+    target[4, K] = float("-inf")
+    target[4, K, V - 1] = float("nan")                  # NaN wins over -inf
+    acc, out = _rejection(ops, target, draft, ids, u, us)
+    racc, rout = oa.accept_rejection(target.numpy(), draft.numpy(), ids.numpy(), u.numpy(),
+                                     us.numpy())
+    assert (acc == K).all()
+    assert np.array_equal(acc, racc) and np.array_equal(out, rout)
+    assert out[0, K] == 0 and out[1, K] == 0 and out[2, K] == V // 3 and out[4, K] == V - 1
+    assert ((out[:, K] >= 0) & (out[:, K] < V)).all()

@@ -195,3 +195,51 @@ def test_zero_target_mass_always_rejects():
     Eq, Zq, _ = oa.row_weights(d[0, 0])
     positive = [int(ep) * Zq > int(eq) * Zp for ep, eq in zip(Ep, Eq)]
     assert all(positive[v] for v in out[:, 0]) and x not in out[:, 0]
+
+
+def _all_accepting_inputs(B, K, V, seed):
+    """Draft logits equal to the target's (p == q, so every draft is accepted, U < 2^24)."""
+    g = np.random.default_rng(seed)
+    target = g.standard_normal((B, K + 1, V)).astype(np.float32)
+    draft = target[:, :K].copy()
+    ids = g.integers(0, V, (B, K))
+    u = g.random((B, K)).astype(np.float32)
+    us = g.random(B).astype(np.float32)
+    return target, draft, ids, u, us
+
+
+def test_empty_bonus_row_takes_the_greedy_token():
+    """A bonus row with no mass (all NaN, all -inf, or holding +inf: every E is 0) has no
+    sampling distribution; the token is then the row's argmax as torch.argmax defines it
+    (first NaN, else first +inf, else index 0 of an all -inf row)."""
+    B, K, V = 4, 3, 50
+    target, draft, ids, u, us = _all_accepting_inputs(B, K, V, 11)
+    target[0, K] = np.nan                              # all NaN -> first NaN, index 0
+    target[1, K] = -np.inf                             # all -inf -> index 0
+    target[2, K, 17] = np.inf                          # +inf among finite values -> 17
+    target[2, K, 33] = np.inf
+    target[3, K, 5] = np.nan                           # NaN among finite values:
+    target[3, K, 9] = np.nan                           # m ignores it, mass stays > 0
+    for b in range(3):
+        assert oa.row_weights(target[b, K])[1] == 0
+    assert oa.row_weights(target[3, K])[1] > 0
+    acc, out = oa.accept_rejection(target, draft, ids, u, us)
+    assert (acc == K).all()
+    assert np.array_equal(out[:, :K], ids)
+    assert out[0, K] == 0 and out[1, K] == 0 and out[2, K] == 17
+    # a row with mass samples by inverse CDF and never picks a NaN entry (E = 0 there)
+    assert out[3, K] not in (5, 9)
+    assert out[3, K] == oa._inverse_cdf([int(e) for e in oa.row_weights(target[3, K])[0]],
+                                        oa.uniform_fix(us[3]))
+
+
+def test_empty_rows_pass_the_accept_test():
+    """Z = 0 in a target or a draft row makes both sides of the accept test 0."""
+    B, K, V = 2, 3, 40
+    target, draft, ids, u, us = _all_accepting_inputs(B, K, V, 12)
+    draft[0, 1] = np.nan                               # empty draft row at position 1
+    target[1, 0] = -np.inf                             # empty target row at position 0
+    draft[1, 0] = target[1, 0] + 0                     # keep q(x) = p(x) elsewhere
+    u[:] = np.float32(0.999)
+    acc, _ = oa.accept_rejection(target, draft, ids, u, us)
+    assert (acc == K).all()

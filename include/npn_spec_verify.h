@@ -34,7 +34,9 @@ typedef enum npn_status {
   NPN_ERR_ALIGN = 3,       /* a pointer is not 16-byte aligned */
   NPN_ERR_WORKSPACE = 4,   /* workspace missing or smaller than the size query returned */
   NPN_ERR_LAUNCH = 5,      /* the HIP runtime rejected a kernel launch */
-  NPN_ERR_VALUE = 6        /* an argument value is out of range (e.g. temperature) */
+  NPN_ERR_VALUE = 6,       /* an argument value is out of range (e.g. temperature) */
+  NPN_ERR_SCRATCH = 7      /* the problem needs more than a no-allocation entry point's
+                              fixed scratch */
 } npn_status;
 
 /* Human-readable text for a status code (static storage). */
@@ -256,6 +258,26 @@ int npn_accept_rejection(const float* target_logits, const float* draft_logits,
                          const float* u_sample, float inv_temperature, int32_t* accepted,
                          int64_t* out_ids, int B, int K, int V, void* workspace,
                          size_t workspace_bytes, void* stream);
+
+/* Bytes of the fixed per-GPU scratch behind npn_accept_rejection_noalloc (4 MiB). */
+#define NPN_ACCEPT_SCRATCH_BYTES (4u << 20)
+
+/* npn_accept_rejection without a workspace argument and without any allocation. No
+ * counterpart in the reference: for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). The workspace
+ * is a fixed device array of NPN_ACCEPT_SCRATCH_BYTES per GPU, held from the first call on
+ * that GPU until the process ends; problems whose npn_accept_workspace_size(B, K, V) exceeds
+ * it return NPN_ERR_SCRATCH (B = 32, K = 7, V = 151936 needs 84 KiB). Every call on a GPU
+ * uses that GPU's one array, so calls that overlap on one GPU (concurrent streams, or
+ * threads) race and must be serialised by the caller; each call writes every scratch word it
+ * reads, so nothing needs clearing between calls. The stream's device (the current device
+ * for the null stream) selects the array. Results are bit-identical to
+ * npn_accept_rejection; the scratch is not readable through this interface. */
+int npn_accept_rejection_noalloc(const float* target_logits, const float* draft_logits,
+                                 const int64_t* draft_ids, const float* u_accept,
+                                 const float* u_sample, float inv_temperature,
+                                 int32_t* accepted, int64_t* out_ids, int B, int K, int V,
+                                 void* stream);
 
 /* ids [M] int64 (and values [M] f32 if non-NULL) = the best of each row's nparts partials,
  * in column order, under the same rule. */

@@ -10,6 +10,8 @@ extern "C" const char* npn_status_string(int status) {
     case NPN_ERR_WORKSPACE: return "workspace missing or too small";
     case NPN_ERR_LAUNCH: return "the HIP runtime rejected a kernel launch";
     case NPN_ERR_VALUE: return "an argument value is out of range";
+    case NPN_ERR_SCRATCH:
+      return "the problem needs more than the no-allocation entry point's fixed scratch";
     default: return "unknown status";
   }
 }

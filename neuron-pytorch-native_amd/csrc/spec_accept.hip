@@ -24,6 +24,8 @@
 //              (sequence, chunk) -> per-sequence inverse-CDF pick
 #include "npn_common.h"
 
+#include <mutex>
+
 namespace {
 
 constexpr int CHK = 8192;      // vocabulary entries per chunk (logit passes)
@@ -698,11 +700,13 @@ extern "C" int npn_accept_greedy(const float* target_logits, const int64_t* draf
   return npn_launch_status();
 }
 
-extern "C" int npn_accept_rejection(const float* target_logits, const float* draft_logits,
-                                    const int64_t* draft_ids, const float* u_accept,
-                                    const float* u_sample, float inv_temperature,
-                                    int32_t* accepted, int64_t* out_ids, int B, int K, int V,
-                                    void* workspace, size_t workspace_bytes, void* stream) {
+namespace {
+
+// Argument checks shared by the rejection entry points (everything but the workspace).
+int rejection_args_ok(const float* target_logits, const float* draft_logits,
+                      const int64_t* draft_ids, const float* u_accept, const float* u_sample,
+                      float inv_temperature, const int32_t* accepted, const int64_t* out_ids,
+                      int B, int K, int V) {
   NPN_REQUIRE(target_logits && draft_logits && draft_ids && u_accept && u_sample && accepted &&
                   out_ids,
               NPN_ERR_NULL);
@@ -710,11 +714,16 @@ extern "C" int npn_accept_rejection(const float* target_logits, const float* dra
   // Z <= V * 2^31, so 2^24 * sum R <= 2^24 * Zp * Zq stays below 2^128 for V <= 2^20
   NPN_REQUIRE(V <= kRejMaxV, NPN_ERR_SHAPE);
   NPN_REQUIRE(inv_temperature > 0.0f && inv_temperature < 1e30f, NPN_ERR_VALUE);
+  return NPN_OK;
+}
+
+// The five rejection kernels on `stream`, with the workspace at `ws` (layout(B, K, V).total
+// bytes, 16-byte aligned, checked by the caller).
+int rejection_launch(const float* target_logits, const float* draft_logits,
+                     const int64_t* draft_ids, const float* u_accept, const float* u_sample,
+                     float inv_temperature, int32_t* accepted, int64_t* out_ids, int B, int K,
+                     int V, uint8_t* ws, hipStream_t s) {
   const WsLayout l = layout(B, K, V);
-  NPN_REQUIRE(workspace != nullptr && workspace_bytes >= l.total, NPN_ERR_WORKSPACE);
-  NPN_REQUIRE(NPN_ALIGNED16(workspace), NPN_ERR_ALIGN);
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  uint8_t* ws = static_cast<uint8_t*>(workspace);
   const int nch = (V + CHK - 1) / CHK;
   const bool vec4 = V % 4 == 0 && NPN_ALIGNED16(target_logits) && NPN_ALIGNED16(draft_logits);
   RejArgs a{target_logits, draft_logits, draft_ids, u_accept, u_sample, inv_temperature,
@@ -733,6 +742,79 @@ extern "C" int npn_accept_rejection(const float* target_logits, const float* dra
   hipLaunchKernelGGL(rej_mass_kernel, dim3(a.nchm, B), dim3(THREADS), 0, s, a);
   hipLaunchKernelGGL(rej_pick_kernel, dim3(B), dim3(THREADS), 0, s, a);
   return npn_launch_status();
+}
+
+// ---- no-allocation variant -------------------------------------------------------------------
+// The workspace of npn_accept_rejection_noalloc: a fixed device array. Each GPU holds its own
+// copy, at its own address, for the life of the process. In host code `scratch` names a host
+// stand-in, not device memory: kernels get the address hipGetSymbolAddress returns for the
+// device they run on (scratch_on_device), never the array's name.
+constexpr size_t kScratchBytes = (size_t)NPN_ACCEPT_SCRATCH_BYTES;
+__device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the device `stream` belongs to (the current device for the
+// null stream), looked up once per device with that device current.
+int scratch_on_device(hipStream_t stream, uint8_t** out) {
+  int cur = 0;
+  if (hipGetDevice(&cur) != hipSuccess) return NPN_ERR_LAUNCH;
+  int dev = cur;
+  if (stream != nullptr) {
+    hipDevice_t sd;
+    if (hipStreamGetDevice(stream, &sd) != hipSuccess) return NPN_ERR_LAUNCH;
+    dev = (int)sd;
+  }
+  NPN_REQUIRE(dev >= 0 && dev < kMaxDevices, NPN_ERR_VALUE);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    if (dev != cur && hipSetDevice(dev) != hipSuccess) return NPN_ERR_LAUNCH;
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (dev != cur) (void)hipSetDevice(cur);
+    if (e != hipSuccess || p == nullptr) return NPN_ERR_LAUNCH;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = static_cast<uint8_t*>(g_scratch_ptr[dev]);
+  return NPN_OK;
+}
+
+}  // namespace
+
+extern "C" int npn_accept_rejection(const float* target_logits, const float* draft_logits,
+                                    const int64_t* draft_ids, const float* u_accept,
+                                    const float* u_sample, float inv_temperature,
+                                    int32_t* accepted, int64_t* out_ids, int B, int K, int V,
+                                    void* workspace, size_t workspace_bytes, void* stream) {
+  const int st = rejection_args_ok(target_logits, draft_logits, draft_ids, u_accept, u_sample,
+                                   inv_temperature, accepted, out_ids, B, K, V);
+  if (st != NPN_OK) return st;
+  NPN_REQUIRE(workspace != nullptr && workspace_bytes >= layout(B, K, V).total,
+              NPN_ERR_WORKSPACE);
+  NPN_REQUIRE(NPN_ALIGNED16(workspace), NPN_ERR_ALIGN);
+  return rejection_launch(target_logits, draft_logits, draft_ids, u_accept, u_sample,
+                          inv_temperature, accepted, out_ids, B, K, V,
+                          static_cast<uint8_t*>(workspace), static_cast<hipStream_t>(stream));
+}
+
+extern "C" int npn_accept_rejection_noalloc(const float* target_logits,
+                                            const float* draft_logits,
+                                            const int64_t* draft_ids, const float* u_accept,
+                                            const float* u_sample, float inv_temperature,
+                                            int32_t* accepted, int64_t* out_ids, int B, int K,
+                                            int V, void* stream) {
+  const int st = rejection_args_ok(target_logits, draft_logits, draft_ids, u_accept, u_sample,
+                                   inv_temperature, accepted, out_ids, B, K, V);
+  if (st != NPN_OK) return st;
+  NPN_REQUIRE(layout(B, K, V).total <= kScratchBytes, NPN_ERR_SCRATCH);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  uint8_t* ws = nullptr;
+  const int sst = scratch_on_device(s, &ws);
+  if (sst != NPN_OK) return sst;
+  return rejection_launch(target_logits, draft_logits, draft_ids, u_accept, u_sample,
+                          inv_temperature, accepted, out_ids, B, K, V, ws, s);
 }
 
 extern "C" int npn_accept_greedy_parts(const void* parts, int nparts, const int64_t* draft_ids,

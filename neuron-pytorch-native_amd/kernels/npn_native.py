@@ -34,6 +34,7 @@ SIGNATURES = {
     "npn_accept_workspace_size": (_Z, [_I] * 3),
     "npn_accept_greedy": (_I, [_P] * 4 + [_I] * 3 + [_P, _Z, _P]),
     "npn_accept_rejection": (_I, [_P] * 5 + [_F] + [_P] * 2 + [_I] * 3 + [_P, _Z, _P]),
+    "npn_accept_rejection_noalloc": (_I, [_P] * 5 + [_F] + [_P] * 2 + [_I] * 3 + [_P]),
     "npn_residual_rmsnorm": (_I, [_P] * 5 + [_I, _I, _F, _P]),
     "npn_silu_mul": (_I, [_P, _P, _I, _I, _P]),
     "npn_deltanet_split": (_I, [_P, _I] + [_P] * 4 + [_I] * 4 + [_P]),

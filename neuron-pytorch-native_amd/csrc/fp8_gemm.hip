@@ -283,6 +283,26 @@ __device__ __forceinline__ i32x2 lds_tr8(const uint8_t* p) {
   return __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) i32x2*)(p));
 }
 
+// Rows [0, 256) of a staged bf16 tile (row stride rs elements; column j of the tile is output
+// column n0 + j, 16 nu columns per row) to out (row stride ld), as 16-byte pieces; rows at or
+// past M are skipped.
+__device__ __forceinline__ void store_staged_bf16(const uint16_t* st, int rs, uint16_t* out,
+                                                  int ld, int m_base, int M, int n0, int nu) {
+  const int pieces = 2 * nu;
+  for (int p = threadIdx.x; p < 256 * pieces; p += WIDE_THREADS) {
+    const int row = p / pieces, q = p - row * pieces;
+    const int m = m_base + row;
+    if (m < M)
+      *reinterpret_cast<uint4*>(out + (size_t)m * ld + n0 + 8 * q) =
+          *reinterpret_cast<const uint4*>(st + row * rs + 8 * q);
+  }
+}
+
+// Byte offset of the SwiGLU staging tile: past the gate/up exchange slots (4 row quarters x 64
+// lanes x 16 NH bf16), 16-byte aligned.
+template <int NH>
+constexpr int kSwigluStageOff = 4 * 64 * 16 * NH * 2;
+
 template <int NH>  // column tiles per wave; a workgroup holds up to 2*NH units
 __global__ __launch_bounds__(WIDE_THREADS, 1) void fp8_gemm_wide_kernel(WideArgs a) {
   constexpr int XBYTES = 256 * KC * 2;                          // 32 KiB x stage
@@ -291,6 +311,10 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void fp8_gemm_wide_kernel(WideArgs
   constexpr int STAGE = XBYTES + WBYTES;
   constexpr int XI = XBYTES / (WIDE_THREADS * 16);              // x DMA per thread (4)
   __shared__ __attribute__((aligned(16))) uint8_t smem[NSTAGE * STAGE];
+  static_assert(256 * (32 * NH + 8) * 2 <= NSTAGE * STAGE, "bf16 staging exceeds the LDS ring");
+  static_assert(128 * (32 * NH + 4) * 4 <= NSTAGE * STAGE, "fp32 staging exceeds the LDS ring");
+  static_assert(kSwigluStageOff<NH> + 256 * (16 * NH + 8) * 2 <= NSTAGE * STAGE,
+                "SwiGLU staging exceeds the LDS ring");
 
   const int nwg = gridDim.x;
   const int per_xcd = nwg / 8;
@@ -446,6 +470,10 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void fp8_gemm_wide_kernel(WideArgs
       }
     }
     __syncthreads();
+    // results go to a row-major staging tile past the exchange slots, then out in 16-byte
+    // pieces (a row's 32 nu contiguous bytes per workgroup)
+    constexpr int RSW = 16 * NH + 8;  // staged row stride in bf16 (16 bytes of padding)
+    uint16_t* st = reinterpret_cast<uint16_t*>(smem + kSwigluStageOff<NH>);
 #pragma unroll
     for (int nt = 0; nt < NH; ++nt) {
       if (nt >= nu) continue;
@@ -456,16 +484,17 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void fp8_gemm_wide_kernel(WideArgs
         if ((mt >> 1) != wc) continue;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int m = m_base + 64 * wr + 16 * mt + 4 * G + r;
-          if (m >= a.M) continue;
+          const int row = 64 * wr + 16 * mt + 4 * G + r;
           const float own = npn::bf16_to_f32(npn::f32_to_bf16(acc[mt][nt][r] * sc));
           const float other = npn::bf16_to_f32(slot[16 * nt + 4 * mt + r]);
           const float g = wc == 0 ? own : other, u = wc == 0 ? other : own;
           const float sg = npn::bf16_to_f32(npn::f32_to_bf16(npn::silu(g)));
-          a.out[(size_t)m * I + col] = npn::f32_to_bf16(sg * u);
+          st[row * RSW + 16 * nt + i] = npn::f32_to_bf16(sg * u);
         }
       }
     }
+    __syncthreads();
+    store_staged_bf16(st, RSW, a.out, I, m_base, a.M, n0, nu);
     return;
   }
   if (a.amax != nullptr) {
@@ -525,23 +554,57 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void fp8_gemm_wide_kernel(WideArgs
     }
     return;
   }
+  // Outputs are staged row-major in LDS (the ring is free once every wave has passed this
+  // barrier) and written in 16-byte pieces: 2-byte or 64-byte-run stores straight from the
+  // MFMA layout cost several times the bytes' time.
+  __syncthreads();
+  if (a.split_k == 1 && !a.to_partial) {
+    constexpr int RSW = 32 * NH + 8;  // staged row stride in bf16 (16 bytes of padding)
+    uint16_t* st = reinterpret_cast<uint16_t*>(smem);
 #pragma unroll
-  for (int nt = 0; nt < NH; ++nt) {
-    const int unit = NH * wc + nt;
-    if (unit >= nu) continue;
-    const int col = n0 + 16 * unit + i;
-    const bool to_bf16 = a.split_k == 1 && !a.to_partial;
-    // partial outputs are unscaled, and the scale pointer may then be NULL
-    const float sc = to_bf16 ? a.scale[col] : 0.0f;
+    for (int nt = 0; nt < NH; ++nt) {
+      const int unit = NH * wc + nt;
+      if (unit >= nu) continue;
+      const float sc = a.scale[n0 + 16 * unit + i];
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
+      for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = m_base + 64 * wr + 16 * mt + 4 * G + r;
-        if (m >= a.M) continue;
-        if (to_bf16) a.out[(size_t)m * a.N + col] = npn::f32_to_bf16(acc[mt][nt][r] * sc);
-        else a.partial[((size_t)sk * a.M + m) * a.N + col] = acc[mt][nt][r];
+        for (int r = 0; r < 4; ++r)
+          st[(64 * wr + 16 * mt + 4 * G + r) * RSW + 16 * unit + i] =
+              npn::f32_to_bf16(acc[mt][nt][r] * sc);
+    }
+    __syncthreads();
+    store_staged_bf16(st, RSW, a.out, a.N, m_base, a.M, n0, nu);
+    return;
+  }
+  // fp32 partials (unscaled; the scale pointer may then be NULL), staged 128 rows at a time
+  constexpr int RSF = 32 * NH + 4;  // staged row stride in floats (16 bytes of padding)
+  float* stf = reinterpret_cast<float*>(smem);
+  float* part = a.partial + (size_t)sk * a.M * a.N;
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+    if ((wr >> 1) == half) {
+#pragma unroll
+      for (int nt = 0; nt < NH; ++nt) {
+        const int unit = NH * wc + nt;
+        if (unit >= nu) continue;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            stf[(64 * (wr & 1) + 16 * mt + 4 * G + r) * RSF + 16 * unit + i] = acc[mt][nt][r];
       }
+    }
+    __syncthreads();
+    const int pieces = 4 * nu;  // 16-byte pieces per staged row
+    for (int p = tid; p < 128 * pieces; p += WIDE_THREADS) {
+      const int row = p / pieces, q = p - row * pieces;
+      const int m = m_base + 128 * half + row;
+      if (m < a.M)
+        *reinterpret_cast<float4*>(part + (size_t)m * a.N + n0 + 4 * q) =
+            *reinterpret_cast<const float4*>(stf + row * RSF + 4 * q);
+    }
+    __syncthreads();
   }
 }
 

@@ -9,8 +9,13 @@ Layer dicts hold numpy arrays: fp8 weights as ([K, N] uint8/int8 bytes, [N] f32 
 norms and DeltaNet parameters as float32, the decode state (DeltaNet state [B,Hv,128,128]
 and conv state bits [B,QKV,3]; GQA cache bits [B,Hkv,S,256]) and kv_len [B].
 
-Pinning: composition of pinned op oracles; the end-to-end GPU test compares the device
-step against it over two consecutive steps (tests/test_gpu_verify_step.py).
+Pinning: tests/test_oracle_layers.py checks deltanet_mixer, gqa_mixer, mlp_branch,
+rms_norm_1p_bits and the DeltaNet / KV state they leave against HF transformers' Qwen3.5
+decoder layers (tests/golden/layers_hf.npz, made by tests/golden/make_layer_fixture.py):
+against HF run with bf16 rounding at the harness's op boundaries to 2e-3 relative (most
+outputs bit-identical), against HF in float32 to the bf16 noise of those roundings, and with
+plausible mistakes planted in this oracle failing. The end-to-end GPU test compares the
+device step against it over two consecutive steps (tests/test_gpu_verify_step.py).
 """
 import numpy as np
 
@@ -67,6 +72,12 @@ def add(a_bits, b_bits):
 
 
 def deltanet_layer(L, x, B, T, hk, hv):
+    return add(x, deltanet_mixer(L, x, B, T, hk, hv))
+
+
+def deltanet_mixer(L, x, B, T, hk, hv):
+    """The DeltaNet sublayer's output before the residual add (out_proj output bits);
+    leaves (ckpt, mixed) in L["pending"] for the rollback."""
     h = rms_norm_1p_bits(x, L["in_norm"])
     proj = linear(h, L["in_proj"])
     qkv = (2 * hk + hv) * 128
@@ -78,10 +89,16 @@ def deltanet_layer(L, x, B, T, hk, hv):
     ckpt, out = od.deltanet_verify(L["state"], mixed, L["conv_state"], L["conv_w"], L["conv_b"],
                                    a, b, z, L["A_log"], L["dt_bias"], L["norm_w"], hk, hv)
     L["pending"] = (ckpt, mixed)
-    return add(x, linear(bf16(out.reshape(B * T, val)), L["out_proj"]))
+    return linear(bf16(out.reshape(B * T, val)), L["out_proj"])
 
 
 def gqa_layer(L, x, B, T, hq, hkv, kv_len, cos, sin):
+    return add(x, gqa_mixer(L, x, B, T, hq, hkv, kv_len, cos, sin))
+
+
+def gqa_mixer(L, x, B, T, hq, hkv, kv_len, cos, sin):
+    """The attention sublayer's output before the residual add (o_proj output bits); the T
+    key/value rows are written into L's cache at kv_len."""
     h = rms_norm_1p_bits(x, L["in_norm"])
     proj = linear(h, L["qkv_proj"])
     qg = proj[:, :hq * 512].reshape(B, T, hq, 512)
@@ -90,18 +107,22 @@ def gqa_layer(L, x, B, T, hq, hkv, kv_len, cos, sin):
     og.gqa_kv_append(kv[:, :, 0], kv[:, :, 1], L["k_norm"], cos, sin, L["cache_k"], L["cache_v"],
                      kv_len)
     attn = og.gqa_tail_verify(query, gate, L["q_norm"], cos, sin, L["cache_k"], L["cache_v"], kv_len)
-    return add(x, linear(bf16(attn.reshape(B * T, hq * 256)), L["o_proj"]))
+    return linear(bf16(attn.reshape(B * T, hq * 256)), L["o_proj"])
 
 
 def mlp(L, x, inter):
-    """SwiGLU as _mlp_layer (static_decode.py:951-963): gate, up and silu(gate) are bf16
-    tensors, so silu(gate) is rounded to bf16 before the product."""
+    return add(x, mlp_branch(L, x, inter))
+
+
+def mlp_branch(L, x, inter):
+    """SwiGLU as _mlp_layer (static_decode.py:951-963), before the residual add: gate, up
+    and silu(gate) are bf16 tensors, so silu(gate) is rounded to bf16 before the product."""
     h = rms_norm_1p_bits(x, L["post_norm"])
     gu = bf16_bits_to_f32(linear(h, L["gate_up"])).astype(np.float32)
     g, u = gu[:, :inter], gu[:, inter:]
     s = bf16_bits_to_f32(bf16(g / (np.float32(1.0) + np.exp(-g)))).astype(np.float32)
     act = bf16(s * u)
-    return add(x, linear(act, L["down"]))
+    return linear(act, L["down"])
 
 
 def verify_step(layers, x_bits, kv_len, B, T, target, draft, draft_ids, u_accept, u_sample,

@@ -1,0 +1,226 @@
+"""Pins the layer composition of oracle/verify_step.py (deltanet_mixer, gqa_mixer, mlp_branch,
+rms_norm_1p_bits, the residual adds, the DeltaNet state / conv window and KV rows they leave)
+against HF transformers' Qwen3.5 decoder layers (tests/golden/layers_hf.npz, written by
+tests/golden/make_layer_fixture.py): a DeltaNet layer and an attention layer with their MLPs,
+T = 8 verify tokens continuing a nonzero decode state, at reduced widths with the real head
+sizes.
+
+Two comparisons:
+- HF with bf16 rounding at the op boundaries of the reference's decode harness
+  (contrib/qwen3.6-27b/static_decode.py:322-335, :753-963): the oracle rounds at the same
+  points, so its outputs agree bit for bit up to rare one-ulp flips where float32 and float64
+  intermediates straddle a bf16 rounding boundary. Tolerance: 2e-3 relative (Frobenius) per
+  output and at least 99% of the bf16 values identical; the DeltaNet state to 1e-5.
+- HF in float32 throughout: the oracle's bf16 roundings (about 10 on each path, each
+  within 2^-9 relative) keep it within 6e-3 relative.
+Plausible mistakes planted in the oracle (each a monkeypatch on the CPU) must fail the first
+comparison.
+"""
+import os
+
+import numpy as np
+import pytest
+
+from oracle import deltanet as od
+from oracle import gqa as og
+from oracle import verify_step as vs
+from oracle.numerics import bf16_bits_to_f32 as b2f
+
+FIXTURE = os.path.join(os.path.dirname(__file__), "golden", "layers_hf.npz")
+HK, HV, HQ, HKV, INTER = 1, 3, 4, 2, 512
+CASES = ("b2p37", "b1p3")
+TOL_ROUNDED = 2e-3
+SAME_BITS = 0.99
+TOL_STATE = 1e-5
+TOL_FP32 = 6e-3
+
+
+@pytest.fixture(scope="module")
+def fx():
+    return dict(np.load(FIXTURE))
+
+
+def weights(fx, nm):
+    w = lambda k: fx[f"w/{nm}/{k}"]
+    L = {"in_norm": w("in_norm"), "post_norm": w("post_norm"),
+         "gate_up": (w("gate_up"), w("gate_up_scale")), "down": (w("down"), w("down_scale"))}
+    if nm == "dn":
+        L.update(kind="D", in_proj=(w("in_proj"), w("in_proj_scale")),
+                 out_proj=(w("out_proj"), w("out_proj_scale")), conv_w=w("conv_w"),
+                 conv_b=w("conv_b"), A_log=w("A_log"), dt_bias=w("dt_bias"), norm_w=w("norm_w"))
+    else:
+        L.update(kind="G", qkv_proj=(w("qkv_proj"), w("qkv_proj_scale")),
+                 o_proj=(w("o_proj"), w("o_proj_scale")), q_norm=w("q_norm"), k_norm=w("k_norm"))
+    return L
+
+
+def with_state(fx, case, L):
+    B, T, P = (int(v) for v in fx[f"{case}/shape"])
+    L = dict(L)
+    if L["kind"] == "D":
+        L["state"] = fx[f"{case}/S0"].astype(np.float64)
+        L["conv_state"] = fx[f"{case}/conv_state"].copy()
+    else:
+        ck = np.zeros((B, HKV, P + T, 256), np.uint16)
+        cv = np.zeros_like(ck)
+        ck[:, :, :P] = fx[f"{case}/cache_k"]
+        cv[:, :, :P] = fx[f"{case}/cache_v"]
+        L["cache_k"], L["cache_v"] = ck, cv
+    return L, B, T, P
+
+
+def rel(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / np.linalg.norm(b))
+
+
+def same(a, b):
+    return float(np.mean(np.asarray(a) == np.asarray(b)))
+
+
+def rounded_errors(fx, case, gate_up_swapped=False):
+    """Oracle vs HF with bf16 rounding at the harness's op boundaries, each sublayer fed the
+    HF run's own input (teacher forcing). Returns {name: (relative error, fraction of
+    identical bf16 values or None)}."""
+    r = lambda k: fx[f"{case}/r/{k}"]
+    D, B, T, P = with_state(fx, case, weights(fx, "dn"))
+    G, _, _, _ = with_state(fx, case, weights(fx, "at"))
+    if gate_up_swapped:
+        for L in (D, G):
+            c, s = L["gate_up"]
+            L["gate_up"] = (np.concatenate([c[:, INTER:], c[:, :INTER]], 1),
+                            np.concatenate([s[INTER:], s[:INTER]]))
+    x0 = fx[f"{case}/x0"]
+    out = {}
+    m = vs.deltanet_mixer(D, x0, B, T, HK, HV)
+    out["dn mixer"] = (rel(b2f(m), b2f(r("dn/mixer"))), same(m, r("dn/mixer")))
+    h = vs.add(x0, m)
+    out["dn residual"] = (rel(b2f(h), b2f(r("dn/mlp_in"))), same(h, r("dn/mlp_in")))
+    ckpt, mixed = D.pop("pending")
+    S, cs = od.deltanet_rollback(ckpt, mixed, D["conv_state"], np.full(B, T - 1))
+    out["dn state"] = (rel(S, r("S_final")), None)
+    out["dn conv window"] = (rel(b2f(cs), b2f(r("conv_final"))), same(cs, r("conv_final")))
+    o = vs.mlp_branch(D, r("dn/mlp_in"), INTER)
+    out["dn mlp"] = (rel(b2f(o), b2f(r("dn/mlp_out"))), same(o, r("dn/mlp_out")))
+    x1 = r("at/in")
+    m = vs.gqa_mixer(G, x1, B, T, HQ, HKV, np.full(B, P), fx[f"{case}/cos"], fx[f"{case}/sin"])
+    out["attn mixer"] = (rel(b2f(m), b2f(r("at/mixer"))), same(m, r("at/mixer")))
+    out["attn residual"] = (rel(b2f(vs.add(x1, m)), b2f(r("at/mlp_in"))),
+                            same(vs.add(x1, m), r("at/mlp_in")))
+    kn, vn = G["cache_k"][:, :, P:], G["cache_v"][:, :, P:]
+    out["k rows"] = (rel(b2f(kn), b2f(r("k_new"))), same(kn, r("k_new")))
+    out["v rows"] = (rel(b2f(vn), b2f(r("v_new"))), same(vn, r("v_new")))
+    o = vs.mlp_branch(G, r("at/mlp_in"), INTER)
+    out["attn mlp"] = (rel(b2f(o), b2f(r("at/mlp_out"))), same(o, r("at/mlp_out")))
+    return out
+
+
+def failures(errs):
+    bad = []
+    for k, (e, s) in errs.items():
+        tol = TOL_STATE if k == "dn state" else TOL_ROUNDED
+        if not e <= tol or (s is not None and s < SAME_BITS):
+            bad.append(f"{k}: rel {e:.3g}, identical {s}")
+    return bad
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_layers_match_hf_rounded_at_harness_boundaries(fx, case):
+    bad = failures(rounded_errors(fx, case))
+    assert not bad, bad
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_layers_match_hf_float32_to_bf16_noise(fx, case):
+    f = lambda k: fx[f"{case}/{k}"]
+    D, B, T, P = with_state(fx, case, weights(fx, "dn"))
+    G, _, _, _ = with_state(fx, case, weights(fx, "at"))
+    x0 = f("x0")
+    y0 = vs.mlp(D, vs.deltanet_layer(D, x0, B, T, HK, HV), INTER)
+    assert rel(b2f(y0), f("dn/out")) < TOL_FP32
+    # the mixer alone, measured against the mixer's own size (the residual add of x0 is
+    # left out: its bf16 rounding is as large as the mixer's contribution here)
+    ckpt, mixed = D.pop("pending")
+    S, cs = od.deltanet_rollback(ckpt, mixed, D["conv_state"], np.full(B, T - 1))
+    assert rel(S, f("S_final")) < TOL_FP32
+    assert rel(b2f(cs), f("conv_final")) < TOL_FP32
+    x1 = f("at/in")
+    y1 = vs.mlp(G, vs.gqa_layer(G, x1, B, T, HQ, HKV, np.full(B, P), f("cos"), f("sin")), INTER)
+    assert rel(b2f(y1), f("at/out")) < TOL_FP32
+    assert rel(b2f(G["cache_k"][:, :, P:]), f("k_new")) < TOL_FP32
+    assert rel(b2f(G["cache_v"][:, :, P:]), f("v_new")) < TOL_FP32
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_rope_table_matches_hf(fx, case):
+    B, T, P = (int(v) for v in fx[f"{case}/shape"])
+    cos, sin = og.rope_cos_sin(P + np.arange(T)[None].repeat(B, 0), theta=1e7)
+    np.testing.assert_allclose(cos, fx[f"{case}/cos"], rtol=0, atol=4e-6)
+    np.testing.assert_allclose(sin, fx[f"{case}/sin"], rtol=0, atol=4e-6)
+    wrong, _ = og.rope_cos_sin(P + np.arange(T)[None].repeat(B, 0), theta=1e6)
+    assert np.abs(wrong - fx[f"{case}/cos"]).max() > 1e-2
+
+
+# ---- planted mistakes: each must fail the rounded comparison --------------------------------
+
+def _norm_without_one(x_bits, w):
+    x = b2f(x_bits).astype(np.float32)
+    n = x / np.sqrt((x * x).mean(-1, keepdims=True) + np.float32(1e-6))
+    return vs.bf16(np.asarray(w, np.float32) * n)
+
+
+def _plant(monkeypatch, name):
+    if name == "norm scales by w, not 1 + w":
+        monkeypatch.setattr(vs, "rms_norm_1p_bits", _norm_without_one)
+    elif name == "DeltaNet a and b slices swapped":
+        f = od.deltanet_verify
+        monkeypatch.setattr(od, "deltanet_verify", lambda st, mx, cs, cw, cb, a, b, *r: f(st, mx, cs, cw, cb, b, a, *r))
+    elif name == "DeltaNet q and k swapped":
+        f = od._split_qkv
+        monkeypatch.setattr(od, "_split_qkv", lambda *a: (lambda q, k, v: (k, q, v))(*f(*a)))
+    elif name == "conv window shifted by one":
+        f = od.conv_window
+        monkeypatch.setattr(od, "conv_window", lambda cs, mx: f(np.roll(cs, 1, axis=-1), mx))
+    elif name == "dt_bias left out":
+        f = od.gates
+        monkeypatch.setattr(od, "gates", lambda a, b, A, dt: f(a, b, A, np.zeros_like(dt)))
+    elif name == "rotate_half sign flipped":
+        def rope_wrong(x, cos, sin):
+            x = np.asarray(x, np.float64)
+            r = x[..., :64]
+            out = x.copy()
+            out[..., :64] = r * cos + np.concatenate([r[..., 32:], -r[..., :32]], -1) * sin
+            return out
+        monkeypatch.setattr(og, "rope_partial", rope_wrong)
+    elif name == "query heads mapped to kv heads round-robin":
+        f = og.gqa_tail_verify
+        def rr(q, g, qn, c, s, ck, cv, kl):
+            idx = np.arange(HQ).reshape(HKV, HQ // HKV).T.reshape(-1)   # head h -> kv head h % HKV
+            out = f(q[:, :, idx], g[:, :, idx], qn, c, s, ck, cv, kl)
+            res = np.empty_like(out)
+            res[:, :, idx] = out
+            return res
+        monkeypatch.setattr(og, "gqa_tail_verify", rr)
+    elif name == "attention misses its own row":
+        f = og.gqa_tail_verify
+        monkeypatch.setattr(og, "gqa_tail_verify", lambda q, g, qn, c, s, ck, cv, kl: f(
+            q, g, qn, c, s, ck, cv, np.asarray(kl) - 1))
+    else:
+        raise AssertionError(name)
+
+
+PLANTED = ["norm scales by w, not 1 + w", "DeltaNet a and b slices swapped",
+           "DeltaNet q and k swapped", "conv window shifted by one", "dt_bias left out",
+           "rotate_half sign flipped", "query heads mapped to kv heads round-robin",
+           "attention misses its own row"]
+
+
+@pytest.mark.parametrize("name", PLANTED)
+def test_planted_mistake_fails(fx, monkeypatch, name):
+    _plant(monkeypatch, name)
+    assert failures(rounded_errors(fx, "b2p37")), f"planted mistake not detected: {name}"
+
+
+def test_planted_gate_up_swap_fails(fx):
+    assert failures(rounded_errors(fx, "b2p37", gate_up_swapped=True))

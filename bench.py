@@ -8,11 +8,18 @@ KV lengths U{4096..32768}, rejection-sampling acceptance at temperature 1 over
 [32, 8, 151936] target and [32, 7, 151936] draft logits (draft = 0.8 t + 0.6 eps),
 then rollback (DeltaNet checkpoint index, conv windows, KV lengths).
 
-A step = layers + acceptance + rollback on inputs resident in HBM. Reported:
+A step = layers + acceptance + rollback on inputs resident in HBM; consecutive steps use
+8 pre-generated logits / uniform sets in turn. Reported:
   value        committed tokens/s = sum_b (a_b + 1) / t_step
-  roofline     the dominant kernel's algorithmic bytes (or FLOPs) per launch over its
-               mean launch time (HIP events on the launch stream, over the timed steps)
-  cpu_baseline the CPU oracle (numpy) on one sampled sequence of the same step
+  roofline     the dominant kernel family by time per step (every FP8 GEMM shape is one
+               family) and its op with the most time: algorithmic bytes (or FLOPs) per
+               launch over the mean launch time (HIP events on the launch stream)
+  kernels      the same figures for every op of the step
+  parity       the numpy oracle on two sequences of the first step, from the same initial
+               state, teacher-forced: accepted lengths and ids bit-exact, sublayer outputs
+               and states within 2e-3 (the bench exits 1 if not)
+  cpu_baseline the batched torch float32 step (oracle/torch_step.py) on the whole first
+               step on the host's cores, with the CPU model and thread count
 
   python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu-baseline]
 """
@@ -31,6 +38,7 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
 B, K, V = 32, 7, 151936
 T = K + 1
+N_SETS = 8                     # logits / uniform sets the timed steps use in turn
 
 
 def parse():
@@ -90,7 +98,8 @@ def kv_lengths(seed):
 
 
 def algorithmic(name, kv_len_mean_rows):
-    """(bound, units per launch, unit) for an op name of the step."""
+    """(bound, units per launch, unit) for an op name of the step; (None, None, None) for
+    ops without a count (the glue: norms, splits, RoPE rows, rollback)."""
     if name == "deltanet.verify":
         per_seq = 48 * 128 * 128 * 4 * (1 + T) + T * 10240 * 2 + 2 * T * 48 * 4 \
             + 2 * T * 48 * 128 * 2 + 10240 * 3 * 2
@@ -101,66 +110,209 @@ def algorithmic(name, kv_len_mean_rows):
         return "hbm", kv + 3 * B * T * 24 * 256 * 2 + 2 * B * T * 64 * 4, "B"
     if name == "spec.accept_rejection":
         return "hbm", (B * (2 * K + 1) * V + 2 * B * V) * 4, "B"
-    if name.startswith("fp8.matmul["):
-        m, k, n = (int(v) for v in name[len("fp8.matmul["):-1].split("x"))
+    if name.startswith(("fp8.matmul[", "fp8.matmul_swiglu[")):
+        m, k, n = (int(v) for v in name[name.index("[") + 1:-1].split("x"))
         return "mfma", 2 * m * n * k, "FLOP"
     return None, None, None
 
 
-def cpu_baseline(model, x, logits, budget_s=10.0):
-    """Time the numpy oracle on whole sequences of the same step (same weights, KV lengths,
-    inputs and logits), one after another until about budget_s of CPU work (at least one).
-    The fp8 weights are decoded to float32 once, outside the timed region, as a CPU
-    implementation of a static model would keep them."""
+def family(name):
+    """Kernel family of an op: every FP8 projection shape is one family (one GEMM kernel
+    design at several shapes); the others are their own."""
+    return "fp8 GEMM" if name.startswith("fp8.") else name
+
+
+def rate(bound, units, seconds):
+    """(achieved, peak, unit) of `units` algorithmic bytes or FLOPs done in `seconds`."""
+    if bound == "mfma":
+        return units / seconds / 1e12, BF16_PEAK_TFLOPS, "TFLOP/s"
+    return units / seconds / 1e9, HBM_PEAK_GBS, "GB/s"
+
+
+def kernel_table(ops, steps, kv_mean_rows):
+    """Per-op rows, by time per step: launches per step, mean launch ms, and for priced ops
+    the achieved rate and its fraction of the roofline that bounds the op."""
+    rows = []
+    for k, v in sorted(ops.items(), key=lambda kv: -kv[1]["total_ms"]):
+        row = {"op": k, "per_step": v["launches"] // steps, "mean_ms": round(v["mean_ms"], 4),
+               "ms_per_step": round(v["total_ms"] / steps, 4)}
+        bound, units, _ = algorithmic(k, kv_mean_rows)
+        if bound is not None:
+            achieved, peak, unit = rate(bound, units, v["mean_ms"] * 1e-3)
+            row.update(bound=bound, achieved=round(achieved, 1), unit=unit,
+                       frac=round(achieved / peak, 4))
+        rows.append(row)
+    return rows
+
+
+def roofline(ops, steps, kv_mean_rows):
+    """The roofline object: the kernel family with the most time per step among priced ops,
+    and within it the op with the most time (its mean launch, the dominant kernel); the
+    family's aggregate rate beside it."""
+    priced = [k for k in ops if algorithmic(k, kv_mean_rows)[0] is not None]
+    fam_ms = {}
+    for k in priced:
+        fam_ms[family(k)] = fam_ms.get(family(k), 0.0) + ops[k]["total_ms"]
+    fam = max(fam_ms, key=fam_ms.get)
+    members = [k for k in priced if family(k) == fam]
+    dom = max(members, key=lambda k: ops[k]["total_ms"])
+    bound, units, _ = algorithmic(dom, kv_mean_rows)
+    achieved, peak, unit = rate(bound, units, ops[dom]["mean_ms"] * 1e-3)
+    digits = 2 if bound == "mfma" else 1
+    roof = {"bound": bound, "achieved": round(achieved, digits), "peak": peak, "unit": unit,
+            "frac": round(achieved / peak, 4), "traffic": measured_traffic(dom),
+            "kernel": dom, "mean_launch_ms": round(ops[dom]["mean_ms"], 4),
+            "units_per_launch": units}
+    roof["traffic_source"] = (
+        "profiles/hbm_traffic.txt: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE per dispatch, "
+        "scaled by a plain 1 GiB copy" if roof["traffic"] is not None else None)
+    fam_units = sum(algorithmic(k, kv_mean_rows)[1] * ops[k]["launches"] for k in members)
+    fa, _, _ = rate(bound, fam_units, fam_ms[fam] * 1e-3)
+    roof["family"] = {"name": fam, "ops": len(members),
+                      "ms_per_step": round(fam_ms[fam] / steps, 4),
+                      "achieved": round(fa, digits), "frac": round(fa / peak, 4)}
+    return roof
+
+
+def snapshot(model, kv_rows):
+    """The decode state on the host before the first step: DeltaNet states and conv windows,
+    and the first kv_rows rows of every cache."""
+    snap = []
+    for L in model.layers:
+        if L["kind"] == "D":
+            snap.append({"state": L["state"].cpu(), "conv_state": L["conv_state"].cpu()})
+        else:
+            snap.append({nm: L[nm][:, :, :kv_rows].cpu() for nm in ("cache_k", "cache_v")})
+    return snap
+
+
+def host_weights(model, decode):
+    """Per layer: the fp8 projections as decode(bytes) with their [N] scales, and the other
+    parameters as CPU tensors."""
+    out = []
+    for L in model.layers:
+        d = {"kind": L["kind"]}
+        for nm, v in L.items():
+            if nm in ("in_proj", "out_proj", "qkv_proj", "o_proj", "gate_up", "down"):
+                d[nm] = (decode(v[0].cpu()), v[1].cpu().reshape(-1))
+            elif nm in ("in_norm", "post_norm", "conv_w", "conv_b", "A_log", "dt_bias",
+                        "norm_w", "q_norm", "k_norm"):
+                d[nm] = v.cpu()
+        out.append(d)
+    return out
+
+
+def oracle_parity(model, snap, kv_start, inputs, trace, first, sample):
+    """The numpy oracle on sequences `sample` of the first step, from the same initial state
+    (snap), teacher-forced with the GPU's residual stream entering each sublayer (trace):
+    accepted lengths and token ids must be bit-identical, each sublayer output and the
+    rolled-back DeltaNet states within 2e-3 relative (Frobenius)."""
     import numpy as np
     import torch
     from oracle import verify_step as ovs
-    from oracle.gqa import rope_cos_sin
+    from oracle.numerics import bf16_bits_to_f32
     from spec_verify_step import DN_HV, DN_QKV
-    weights = []
-    for L in model.layers:
-        d = {"kind": L["kind"], "in_norm": L["in_norm"].cpu().numpy(),
-             "post_norm": L["post_norm"].cpu().numpy()}
-        for nm in ovs.FP8_WEIGHTS:
-            if nm in L:
-                d[nm] = (L[nm][0].cpu().numpy(), L[nm][1].cpu().numpy().reshape(-1))
-        weights.append(d)
-    ovs.decode_weights(weights)
-    total, tokens, done = 0.0, 0, []
-    for b in range(B):
-        L_b = int(model.kv_len[b].item())
+    from spec_verify_step import rope_tables
+
+    def bits(t):
+        return t.contiguous().view(torch.int16).numpy().view(np.uint16)
+
+    def rel(a, b):
+        return float(np.linalg.norm(np.asarray(a, np.float64) - b) / np.linalg.norm(b))
+
+    t0 = time.perf_counter()
+    ws = host_weights(model, lambda w: w.numpy())
+    sel = list(sample)
+    kv = kv_start.cpu().numpy()[sel]
+    layers = []
+    for w, sn in zip(ws, snap):
+        d = {k: (v[0], v[1].numpy()) if isinstance(v, tuple) else
+             (v.numpy() if torch.is_tensor(v) else v) for k, v in w.items()}
+        if w["kind"] == "D":
+            d["state"] = sn["state"].reshape(B, DN_HV, 128, 128)[sel].double().numpy()
+            d["conv_state"] = bits(sn["conv_state"].reshape(B, DN_QKV, 3)[sel]).copy()
+        else:
+            for nm in ("cache_k", "cache_v"):
+                d[nm] = bits(sn[nm][sel]).copy()
+        layers.append(d)
+    ovs.decode_weights(layers)
+    pos = torch.as_tensor(kv)[:, None] + torch.arange(T)
+    cos, sin = (t.numpy() for t in rope_tables(pos))
+    rows = lambda t: t.reshape(B, T, -1)[sel].reshape(len(sel) * T, -1)
+    tgt, drf, ids, u, us = (t.cpu().numpy()[sel] for t in inputs)
+    outs = []
+    _, acc, out_ids, _ = ovs.verify_step(layers, bits(rows(trace[0])), kv, len(sel), T, tgt, drf,
+                                         ids, u, us, cos, sin,
+                                         layer_inputs=[bits(rows(t)) for t in trace[:-1]],
+                                         layer_outputs=outs)
+    sub = max(rel(rows(g).float().numpy(), bf16_bits_to_f32(r)) for g, r in zip(trace[1:], outs))
+    st = max(rel(gs, d["state"]) for gs, d in zip(first["states"], (l for l in layers if l["kind"] == "D")))
+    exact = bool(np.array_equal(first["accepted"].numpy()[sel], acc)
+                 and np.array_equal(first["out_ids"].numpy()[sel], out_ids))
+    return {"sequences": sel, "kv_len": kv.tolist(), "accepted_and_ids_bit_exact": exact,
+            "max_sublayer_rel_err": float(f"{sub:.3e}"), "max_state_rel_err": float(f"{st:.3e}"),
+            "tolerance": 2e-3, "ok": exact and sub <= 2e-3 and st <= 2e-3,
+            "oracle": "oracle/verify_step.py (numpy), teacher-forced with the GPU's residual "
+                      "stream entering each sublayer",
+            "oracle_s": round(time.perf_counter() - t0, 1)}
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
+def cpu_baseline(model, snap, kv_start, x, inputs, first, budget_s=20.0):
+    """The batched torch CPU float32 step (oracle/torch_step.py) on the whole workload (all B
+    sequences, the same weights, initial state, inputs and logits as the first GPU step),
+    repeated from the same initial state until about budget_s (at most 3 runs). The fp8
+    weights are decoded to float32 once, before timing, as a CPU implementation of a static
+    model keeps them."""
+    import torch
+    from oracle import torch_step as ts
+    from spec_verify_step import rope_tables
+    ws = host_weights(model, ts.decode_fp8)
+    xc = x.cpu().float()
+    tgt, drf, ids, u, us = (t.cpu() for t in inputs)
+    kv0 = kv_start.cpu().long()
+    cos, sin = rope_tables(kv0[:, None] + torch.arange(T))
+    times = []
+    while True:
         layers = []
-        for L, w in zip(model.layers, weights):
+        for w, sn in zip(ws, snap):
             d = dict(w)
-            if L["kind"] == "D":
-                for nm in ("conv_w", "conv_b", "A_log", "dt_bias", "norm_w"):
-                    d[nm] = L[nm].cpu().numpy()
-                rng = np.random.default_rng(b)
-                d["state"] = rng.standard_normal((1, DN_HV, 128, 128)) * 0.02
-                d["conv_state"] = rng.integers(0, 1 << 15, (1, DN_QKV, 3)).astype(np.uint16) & 0x3FFF
+            if w["kind"] == "D":
+                d["state"] = sn["state"].reshape(B, -1, 128, 128).clone()
+                d["conv_state"] = sn["conv_state"].reshape(B, -1, 3).float()
             else:
-                d["q_norm"], d["k_norm"] = L["q_norm"].cpu().numpy(), L["k_norm"].cpu().numpy()
-                rows = L_b + T
-                for nm in ("cache_k", "cache_v"):
-                    d[nm] = L[nm][b:b + 1, :, :rows].contiguous().cpu().view(torch.int16).numpy().view(np.uint16)
+                d["cache_k"], d["cache_v"] = sn["cache_k"].clone(), sn["cache_v"].clone()
             layers.append(d)
-        xb = x[b * T:(b + 1) * T].cpu().view(torch.int16).numpy().view(np.uint16)
-        tgt, drf, ids, u, us = (t[b:b + 1].cpu().numpy() for t in logits)
-        cos, sin = rope_cos_sin(L_b + np.arange(T)[None, :])
+        kv = kv0.clone()
+        step = ts.TorchCpuStep(layers, B, T)
         t0 = time.perf_counter()
-        _, acc, _, _ = ovs.verify_step(layers, xb, np.array([L_b]), 1, T, tgt, drf, ids, u, us,
-                                       cos, sin)
-        total += time.perf_counter() - t0
-        tokens += int(acc[0]) + 1
-        done.append(L_b)
-        if total >= budget_s:
+        _, acc, out_ids = step.step(xc, kv, cos, sin, tgt, drf, ids, u, us)
+        times.append(time.perf_counter() - t0)
+        print(f"cpu baseline: step {len(times)} took {times[-1]:.1f} s", file=sys.stderr,
+              flush=True)
+        if sum(times) >= budget_s or len(times) >= 3:
             break
-    cores = len(os.sched_getaffinity(0))
-    return {"value": round(tokens / total, 4), "unit": "tokens/s", "cores": cores,
-            "kind": "port",
-            "sample": f"{len(done)} of {B} sequences (kv_len {', '.join(map(str, done))}) "
-                      f"through the same 4-layer step, {total:.1f} s; numpy oracle, fp8 "
-                      f"weights decoded to float32 once before timing, BLAS on {cores} threads"}
+    per_step = sum(times) / len(times)
+    tokens = int((acc.long() + 1).sum())
+    same = int(((acc == first["accepted"]) & (out_ids == first["out_ids"]).all(1)).sum())
+    threads = torch.get_num_threads()
+    return {"value": round(tokens / per_step, 2), "unit": "tokens/s", "cores": threads,
+            "kind": "port", "cpu": cpu_model(), "threads": threads,
+            "sample": f"the whole first step (all {B} sequences, {tokens} committed tokens) from "
+                      f"the same initial state and inputs, {len(times)} run(s), "
+                      f"{per_step:.2f} s per step; oracle/torch_step.py, batched torch float32 "
+                      f"on the CPU, fp8 weights decoded to float32 once before timing",
+            "decisions_equal_to_gpu": f"{same}/{B}"}
 
 
 LM_VOCAB = 248320  # Qwen3.6-27B vocabulary (static_decode.py:107)
@@ -327,9 +479,11 @@ def main():
         print(f"bench.py runs on one GPU only (got --gpus {args.gpus}); the verify step is "
               f"measured on a single MI355X", file=sys.stderr)
         sys.exit(2)
-    import numpy as np
     import torch
     from spec_verify_step import HIDDEN, OpTimer, VerifySlice, synthetic_logits
+
+    def note(msg):
+        print(msg, file=sys.stderr, flush=True)
 
     dev = "cuda"
     torch.manual_seed(args.seed)
@@ -339,27 +493,45 @@ def main():
     model = VerifySlice(B, K, kv_lens, s_max, pattern="DDDG", seed=args.seed, device=dev)
     g = torch.Generator(device=dev).manual_seed(args.seed + 1)
     x = torch.randn(B * T, HIDDEN, generator=g, device=dev).to(torch.bfloat16)
-    logits = synthetic_logits(B, K, V, args.seed + 2, dev)
+    # N_SETS pre-generated logits / draft / uniform sets, used in turn by consecutive steps
+    sets = [synthetic_logits(B, K, V, args.seed + 2 + i, dev) for i in range(N_SETS)]
     kv_start = model.kv_len.clone()
+    check = not args.no_cpu_baseline
+    snap = snapshot(model, int(kv_lens.max()) + T) if check else None
 
     # Python's garbage collector stays off from here to the end of the per-op pass: a full
     # collection (tens of ms) inside an op's event bracket drains the GPU queue and shows up
     # as that op's time.
     gc.collect()
     gc.disable()
-    # Warmup: eager steps (the first starts from the initial DeltaNet state); then the state
-    # moves to fixed buffers and the step is captured as HIP graphs (two checkpoint-buffer
-    # parities), replayed in the timed region.
-    model.step(x, *logits)
-    for _ in range(max(args.warmup - 1, 0)):
-        model.step(x, *logits)
+    # Warmup: eager steps (the first starts from the initial DeltaNet state and is the one
+    # checked against the CPU); then the state moves to fixed buffers and the step is
+    # captured as one HIP graph per input set, replayed in turn in the timed region.
+    trace = [] if check else None
+    _, acc0, ids0 = model.step(x, *sets[0], trace=trace)
+    first = None
+    if check:
+        sample = sorted({int(kv_start.argmin()), int(kv_start.argmax())})
+        ck = [L["ckpt"].reshape(B, T, -1, 128, 128) for L in model.layers if L["kind"] == "D"]
+        first = {"accepted": acc0.cpu(), "out_ids": ids0.cpu(), "trace": [t.cpu() for t in trace],
+                 "states": [torch.stack([c[b, int(acc0[b])] for b in sample]).double().cpu()
+                            .numpy() for c in ck]}
+        trace = None
+    for i in range(1, max(args.warmup, 1)):
+        model.step(x, *sets[i % N_SETS])
     model.make_persistent()
     use_graph = not args.no_graph
     if use_graph:
-        model.capture(x, *logits)
+        model.capture(x, sets)
         for _ in range(args.warmup):
             model.replay()
-    run = model.replay if use_graph else (lambda: model.step(x, *logits))
+    step_no = [0]
+
+    def eager():
+        model.step(x, *sets[step_no[0] % N_SETS])
+        step_no[0] += 1
+
+    run = model.replay if use_graph else eager
     torch.cuda.synchronize()
     model.committed.zero_()
     torch.cuda.synchronize()
@@ -370,64 +542,44 @@ def main():
     elapsed = time.perf_counter() - t0
     tokens = int(model.committed.sum().item())
     ms_per_step = elapsed * 1e3 / args.steps
+    note(f"timed {args.steps} steps: {ms_per_step:.4f} ms per step")
 
     # Per-op launch times: HIP events around every op launch on the launch stream, over an
-    # eager pass of the same number of steps (same kernels and sizes as the replays), after
-    # two untimed eager steps: the first eager allocations after the graph captures may call
-    # hipMalloc, which waits for the queued work inside an op's event bracket.
+    # eager pass of the same number of steps over the same input sets (same kernels and
+    # sizes as the replays), after two untimed eager steps: the first eager allocations after
+    # the graph captures may call hipMalloc, which waits for the queued work inside an op's
+    # event bracket.
     for _ in range(2):
-        model.step(x, *logits)
+        eager()
     torch.cuda.synchronize()
     kv0 = float(model.kv_len.float().mean().item())
     timer = OpTimer()
     model.timer = timer
     model.committed.zero_()
     for _ in range(args.steps):
-        model.step(x, *logits)
+        eager()
     torch.cuda.synchronize()
     model.timer = lambda name, fn, *a: fn(*a)
     gc.enable()
     ops = timer.summary()
     # mean prior cache rows seen by the attention over the timed eager steps
     kv_mean_rows = kv0 + float(model.committed.float().mean().item()) * (args.steps - 1) / (2 * args.steps)
-
-    # dominant kernel by total time in the timed steps
-    priced = [k for k in ops if algorithmic(k, kv_mean_rows)[0] is not None]
-    dom = max(priced, key=lambda k: ops[k]["total_ms"])
-    top = max(ops, key=lambda k: ops[k]["total_ms"])
-    if top != dom:
-        print(f"note: op {top} has the most time but no algorithmic byte/flop count; "
-              f"roofline reported for {dom}", file=sys.stderr)
-    bound, units, unit = algorithmic(dom, kv_mean_rows)
-    mean_s = ops[dom]["mean_ms"] * 1e-3
-    if bound == "mfma":
-        achieved = units / mean_s / 1e12
-        roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": BF16_PEAK_TFLOPS,
-                "unit": "TFLOP/s", "frac": round(achieved / BF16_PEAK_TFLOPS, 4), "traffic": None}
-    else:
-        achieved = units / mean_s / 1e9
-        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None}
-    roof["traffic"] = measured_traffic(dom)
-    roof["kernel"] = dom
-    roof["mean_launch_ms"] = round(ops[dom]["mean_ms"], 4)
-    roof["units_per_launch"] = units
-
+    table = kernel_table(ops, args.steps, kv_mean_rows)
+    roof = roofline(ops, args.steps, kv_mean_rows)
     if args.per_op:
-        for k, v in sorted(ops.items(), key=lambda kv: -kv[1]["total_ms"]):
-            bnd, u, un = algorithmic(k, kv_mean_rows)
-            rate = ""
-            if bnd == "hbm":
-                rate = f"{u / (v['mean_ms'] * 1e-3) / 1e9:8.1f} GB/s"
-            elif bnd == "mfma":
-                rate = f"{u / (v['mean_ms'] * 1e-3) / 1e12:8.1f} TFLOP/s"
-            print(f"{k:40s} x{v['launches'] // args.steps:2d}/step {v['mean_ms']:8.4f} ms "
-                  f"{v['total_ms'] / args.steps:8.4f} ms/step {rate}", file=sys.stderr)
+        for r in table:
+            rt = f"{r['achieved']:9.1f} {r['unit']} ({r['frac']:.3f})" if "frac" in r else ""
+            note(f"{r['op']:40s} x{r['per_step']:2d}/step {r['mean_ms']:8.4f} ms "
+                 f"{r['ms_per_step']:8.4f} ms/step {rt}")
 
-    cpu = None
-    if not args.no_cpu_baseline:
-        model.kv_len = kv_start
-        cpu = cpu_baseline(model, x, logits)
+    cpu = parity = None
+    if check:
+        model.graphs = model.graph_outputs = None   # release the graphs' memory pools
+        note("parity: numpy oracle on the shortest- and longest-cache sequences of the first step")
+        parity = oracle_parity(model, snap, kv_start, sets[0], first["trace"], first, sample)
+        note(f"parity: {parity}")
+        note("cpu baseline: batched torch float32 step on the host")
+        cpu = cpu_baseline(model, snap, kv_start, x, sets[0], first)
 
     line = {
         "metric": "verify-step tokens/s (B=32,K=7) + achieved HBM GB/s vs MI355X peak",
@@ -441,7 +593,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (random-init weights, N(0,1) activations and logits)",
+        "data": f"synthetic (random-init weights, N(0,1) activations; {N_SETS} logits / "
+                f"uniform sets used in turn by consecutive steps)",
         "config": {"workload": "EAGLE3 verify+accept+rollback, 4-layer Qwen3.6-27B-width slice "
                                "(3 gated-DeltaNet + 1 GQA, FP8 W8A16 projections), rejection "
                                "sampling at T=1",
@@ -449,13 +602,18 @@ def main():
                    "kv_len": "U{4096..32768}", "parallelism": "single GPU"},
         "verified_tokens_per_s": round(B * T * args.steps / elapsed, 1),
         "committed_per_seq": round(tokens / (B * args.steps), 3),
-        "timing": ("HIP graph replays of the whole step (two captured graphs, one per "
-                   "DeltaNet checkpoint-buffer parity)" if use_graph else "eager steps")
+        "timing": ("HIP graph replays of the whole step (one captured graph per input set, "
+                   "alternating DeltaNet checkpoint buffers)" if use_graph else "eager steps")
                   + "; per-op launch times from HIP events over an eager pass of as many steps",
         "roofline": roof,
+        "kernels": table,
         "cpu_baseline": cpu,
+        "parity": parity,
     }
-    print(json.dumps(line))
+    print(json.dumps(line), flush=True)
+    if parity is not None and not parity["ok"]:
+        note("parity check FAILED: the GPU step differs from the oracle")
+        sys.exit(1)
 
 
 if __name__ == "__main__":

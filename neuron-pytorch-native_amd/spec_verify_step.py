@@ -302,29 +302,36 @@ class VerifySlice:
         self.parity = 0
         self.persistent = True
 
-    def capture(self, x, target_logits, draft_logits, draft_ids, u_accept, u_sample,
-                greedy=False):
-        """Capture the step in two HIP graphs, one per checkpoint-buffer parity, on fixed
-        inputs (x and the logits/uniform tensors keep their addresses). Capturing runs
-        nothing: the parity flips twice and ends where the live state is."""
+    def capture(self, x, input_sets, greedy=False):
+        """Capture the step as one HIP graph per entry of `input_sets`, each a tuple
+        (target_logits, draft_logits, draft_ids, u_accept, u_sample) of tensors that keep
+        their addresses (as does x). Consecutive graphs use the two checkpoint buffers in
+        turn, so the number of sets must be even; replay() runs them in order, cyclically.
+        Capturing runs nothing: the parity flips once per graph and ends where it started."""
+        if len(input_sets) == 0 or len(input_sets) % 2:
+            raise ValueError("capture needs an even, nonzero number of input sets")
         if not self.persistent:
             self.make_persistent()
         self.graphs, self.graph_outputs = [], []
-        for _ in range(2):
+        self.graph_parity0 = self.parity
+        for inputs in input_sets:
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):
-                outs = self.step(x, target_logits, draft_logits, draft_ids, u_accept, u_sample,
-                                 greedy=greedy)
+                outs = self.step(x, *inputs, greedy=greedy)
             self.graphs.append(g)
             self.graph_outputs.append(outs)
+        self.next_graph = 0
 
     def replay(self):
         """One step by graph replay; returns that graph's (hidden, accepted, out_ids) tensors
         (overwritten by the next replay of the same graph)."""
-        p = self.parity
-        self.graphs[p].replay()
+        i = self.next_graph
+        if (self.graph_parity0 + i) % 2 != self.parity:
+            raise RuntimeError("graph replay out of step with the checkpoint-buffer parity")
+        self.graphs[i].replay()
         self.parity ^= 1
-        return self.graph_outputs[p]
+        self.next_graph = (i + 1) % len(self.graphs)
+        return self.graph_outputs[i]
 
     def step(self, x, target_logits, draft_logits, draft_ids, u_accept, u_sample, greedy=False,
              trace=None):

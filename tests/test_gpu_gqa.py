@@ -81,6 +81,13 @@ def test_tail_verify_full_width_long(ops):
     assert_rel_close(_run_verify(ops, d), _oracle_verify(d), out_unit=BF16_U, name="tail_verify")
 
 
+def test_tail_verify_full_width_longest(ops):
+    """24/4 heads, T=8, at the top of the verify workloads' KV range (32768 rows), next to
+    a sequence in the middle of it, in one launch."""
+    d = gqa_verify_inputs(2, 8, 24, 4, [32768 - 8, 17000], 32768, seed=5)
+    assert_rel_close(_run_verify(ops, d), _oracle_verify(d), out_unit=BF16_U, name="tail_verify")
+
+
 def test_kv_append_then_attend_equals_cloned_cache(ops):
     """Append-after-attention equivalence (contrib/qwen3.6-35b-a3b/kernels/tests/
     test_gqa_stateful_cache_cpu.py:9-40): rows written by kv_append match the oracle's

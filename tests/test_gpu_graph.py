@@ -4,7 +4,9 @@ VerifySlice.capture / replay) against the same step run eagerly.
 Two slices built from the same seed run side by side. Both take one eager step from the
 initial DeltaNet state and then move their decode state to fixed buffers
 (make_persistent). One keeps stepping eagerly; the other captures the step as two HIP graphs
-(one per checkpoint-buffer parity) and replays them. Before every step the inputs are
+(one per checkpoint-buffer parity) and replays them. A second test captures one graph per
+input set (four sets of logits and uniforms) and replays them in rotation against eager steps
+that consume the same sets in the same order. Before every step the inputs are
 rewritten in place with new values (same addresses, different data), other GPU work runs on
 the same stream, and the device is synchronised; after every step the outputs (hidden,
 accepted lengths, emitted ids) and the whole decode state (KV lengths, committed counters,
@@ -62,7 +64,7 @@ def test_graph_replay_matches_eager(greedy):
         m.step(x, *logits, greedy=greedy)
     for m in (eager, graphed):
         m.make_persistent()
-    graphed.capture(x, *logits, greedy=greedy)
+    graphed.capture(x, [logits, logits], greedy=greedy)
     torch.cuda.synchronize()
 
     gen = torch.Generator(device=dev).manual_seed(7)
@@ -93,3 +95,33 @@ def test_graph_replay_matches_eager(greedy):
             assert torch.equal(a, b), f"step {step}: state {name} differs"
     # the steps did commit tokens (the replays are not no-ops)
     assert int(graphed.committed.sum()) >= B * STEPS
+
+
+def test_graph_rotation_over_input_sets():
+    from spec_verify_step import HIDDEN, VerifySlice, synthetic_logits
+    dev = "cuda"
+    kv = [37, 300, 5, 129]
+    n_sets, steps = 4, 6
+    s_max = max(kv) + (K + 1) * (steps + 4)
+    eager, graphed = (VerifySlice(B, K, kv, s_max, pattern="DG", seed=12, device=dev)
+                      for _ in range(2))
+    g = torch.Generator(device=dev).manual_seed(8)
+    x = torch.randn(B * (K + 1), HIDDEN, generator=g, device=dev).to(torch.bfloat16)
+    sets = [synthetic_logits(B, K, V, 20 + i, dev) for i in range(n_sets)]
+    for m in (eager, graphed):
+        m.step(x, *sets[0])
+        m.make_persistent()
+    graphed.capture(x, sets)
+    with pytest.raises(ValueError):
+        VerifySlice(B, K, kv, s_max, pattern="DG", seed=12, device=dev).capture(x, sets[:3])
+    torch.cuda.synchronize()
+    accepted = set()
+    for step in range(steps):
+        h_e, a_e, ids_e = eager.step(x, *sets[step % n_sets])
+        h_g, a_g, ids_g = graphed.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(a_e, a_g) and torch.equal(ids_e, ids_g), f"step {step}"
+        assert torch.equal(h_e.view(torch.int16), h_g.view(torch.int16)), f"step {step}"
+        assert torch.equal(eager.kv_len, graphed.kv_len), f"step {step}"
+        accepted.add(tuple(a_g.tolist()))
+    assert len(accepted) > 1  # the sets differ, so do the accepted lengths

@@ -57,6 +57,9 @@ def parse():
     p.add_argument("--prefill", action="store_true",
                    help="time the chunked gated-DeltaNet prefill (deltanet::chunked_prefill) "
                         "over the 27B layer's 48 v-heads x 4096 prompt tokens")
+    p.add_argument("--config", type=int, choices=(1, 2, 3),
+                   help="one kernel at its workload's shapes: 1 DeltaNet verify at B = 1, 8, "
+                        "32; 2 GQA verify attention at B = 16; 3 the FP8 GEMM at nine shapes")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only run a plain 1 GiB device copy 5 times (scales HBM byte counters)")
     return p.parse_args()
@@ -97,17 +100,33 @@ def kv_lengths(seed):
     return np.random.default_rng(seed).integers(4096, 32769, size=B).astype(np.int32)
 
 
+def dn_verify_bytes(nseq, hv=48, hk=16, t=T):
+    """Algorithmic HBM bytes of one DeltaNet verify launch over nseq sequences: the fp32 state
+    read once and t checkpoints written, the bf16 projection rows (q, k, v channels, z) read
+    and the output written, the a / b gate inputs, the conv window read, and the per-layer
+    constants (conv weights and bias, A_log, dt_bias, norm weight)."""
+    qkv = (2 * hk + hv) * 128
+    per_seq = hv * 128 * 128 * 4 * (1 + t) + t * qkv * 2 + 2 * t * hv * 4 \
+        + 2 * t * hv * 128 * 2 + qkv * 3 * 2
+    shared = qkv * 4 * 4 + qkv * 4 + 2 * hv * 4 + 128 * 4
+    return nseq * per_seq + shared
+
+
+def gqa_verify_bytes(kv_lens, hq=24, hkv=4, t=T, dh=256):
+    """Algorithmic HBM bytes of one verify-attention launch: every sequence's K and V rows
+    [0, kv_len + t) read once (bf16), the query, gate and output rows, and the RoPE rows."""
+    rows = sum(int(k) + t for k in kv_lens)
+    nseq = len(kv_lens)
+    return rows * hkv * dh * 2 * 2 + 3 * nseq * t * hq * dh * 2 + 2 * nseq * t * 64 * 4
+
+
 def algorithmic(name, kv_len_mean_rows):
     """(bound, units per launch, unit) for an op name of the step; (None, None, None) for
     ops without a count (the glue: norms, splits, RoPE rows, rollback)."""
     if name == "deltanet.verify":
-        per_seq = 48 * 128 * 128 * 4 * (1 + T) + T * 10240 * 2 + 2 * T * 48 * 4 \
-            + 2 * T * 48 * 128 * 2 + 10240 * 3 * 2
-        shared = 10240 * 4 * 4 + 10240 * 4 + 2 * 48 * 4 + 128 * 4
-        return "hbm", B * per_seq + shared, "B"
+        return "hbm", dn_verify_bytes(B), "B"
     if name == "gqa.tail_verify":
-        kv = B * 4 * (kv_len_mean_rows + T) * 256 * 2 * 2
-        return "hbm", kv + 3 * B * T * 24 * 256 * 2 + 2 * B * T * 64 * 4, "B"
+        return "hbm", gqa_verify_bytes([kv_len_mean_rows] * B), "B"
     if name == "spec.accept_rejection":
         return "hbm", (B * (2 * K + 1) * V + 2 * B * V) * 4, "B"
     if name.startswith(("fp8.matmul[", "fp8.matmul_swiglu[")):
@@ -315,6 +334,159 @@ def cpu_baseline(model, snap, kv_start, x, inputs, first, budget_s=20.0):
             "decisions_equal_to_gpu": f"{same}/{B}"}
 
 
+CFG_MIN_WARMUP = 64      # untimed calls first, so the shader clock has settled
+
+
+def time_calls(fn, n, warmup, replays=5):
+    """Mean ms per call of fn(i), i = 0..n-1: after max(warmup, CFG_MIN_WARMUP) untimed
+    calls, the n calls are captured in one HIP graph and the graph is replayed `replays`
+    times between HIP events, so the figure is the GPU's time per call (launches included)
+    rather than the host's time to issue a call from Python."""
+    import torch
+    for i in range(max(warmup, CFG_MIN_WARMUP)):
+        fn(i)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(n):
+            fn(i)
+    g.replay()
+    torch.cuda.synchronize()
+    s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s_ev.record()
+    for _ in range(replays):
+        g.replay()
+    e_ev.record()
+    torch.cuda.synchronize()
+    return s_ev.elapsed_time(e_ev) / (n * replays)
+
+
+def hbm_row(nbytes, ms):
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"bytes": int(nbytes), "achieved": round(gbs, 1), "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+
+def config1_bench(args):
+    """Full-width DeltaNet verify (16 k / 48 v heads of 128, T = 8) at B = 1, 8, 32, as the
+    step runs it: deltanet::verify_from_ckpt_into reads each sequence's state from the previous
+    checkpoint buffer at its accepted index (U{0..7}) and writes the T new checkpoints into the
+    other buffer (the two alternate), then deltanet::conv_rollback_ rolls the conv windows
+    back. q, k, v channels are bf16 N(0,1) (L2-normalised in the kernel), beta = sigmoid(N(0,1)),
+    g = -softplus(N(0,1)) (A_log = dt_bias = 0), states fp32 N(0, 0.02)."""
+    import torch
+    import npn_ops  # noqa: F401
+    dev, Hk, Hv, D = "cuda", 16, 48, 128
+    QKV = (2 * Hk + Hv) * D
+    rows = []
+    for nb in (1, 8, 32):
+        g = torch.Generator(device=dev).manual_seed(args.seed + nb)
+        ck = [torch.randn(nb * T * Hv * D, D, generator=g, device=dev) * 0.02 for _ in range(2)]
+        mixed = torch.randn(nb * T * QKV, generator=g, device=dev).to(torch.bfloat16)
+        conv = torch.randn(nb * QKV, 3, generator=g, device=dev).to(torch.bfloat16)
+        cw = torch.randn(QKV, 4, generator=g, device=dev) * 0.5
+        cb = torch.randn(QKV, generator=g, device=dev) * 0.1
+        a_in = torch.randn(nb * T * Hv, generator=g, device=dev)
+        b_in = torch.randn(nb * T * Hv, generator=g, device=dev)
+        z = torch.randn(nb * T * Hv, D, generator=g, device=dev).to(torch.bfloat16)
+        zeros = torch.zeros(Hv, device=dev)
+        nw = torch.randn(D, generator=g, device=dev) * 0.1 + 1.0
+        acc = torch.randint(0, T, (nb,), generator=g, device=dev, dtype=torch.int32)
+
+        def verify(i):
+            return torch.ops.deltanet.verify_from_ckpt_into(
+                ck[i % 2], acc, mixed, conv, cw, cb, a_in, b_in, z, zeros, zeros, nw,
+                ck[1 - i % 2])
+
+        def rollback(i):
+            torch.ops.deltanet.conv_rollback_(mixed, conv, acc, Hv)
+
+        ms_v = time_calls(verify, args.steps, args.warmup)
+        ms_r = time_calls(rollback, args.steps, args.warmup)
+        row = {"B": nb, "workgroups": nb * Hv, "verify_ms": round(ms_v, 4),
+               "rollback_ms": round(ms_r, 4)}
+        row.update(hbm_row(dn_verify_bytes(nb), ms_v))
+        rows.append(row)
+        del ck
+    print(json.dumps({
+        "workload": "DeltaNet verify, 16 k / 48 v heads of 128, T = 8, state checkpoints per "
+                    "position, index rollback to U{0..7}",
+        "kernel": "deltanet.verify (dn_verify_kernel), conv rollback separately",
+        "bound": "hbm", "peak": HBM_PEAK_GBS, "rows": rows, "steps": args.steps,
+        "warmup": max(args.warmup, CFG_MIN_WARMUP)}))
+
+
+def config2_bench(args):
+    """GQA verify attention: B = 16, T = 8 causal query rows, 24 q / 4 kv heads of 256, partial
+    RoPE (64 dims, theta 1e7), bf16 N(0,1) KV cache with per-sequence lengths U{4096..32768}
+    in contiguous per-sequence blocks; bf16 output, fp32 softmax."""
+    import numpy as np
+    import torch
+    import npn_ops  # noqa: F401
+    from spec_verify_step import rope_tables
+    dev, nb, hq, hkv, dh = "cuda", 16, 24, 4, 256
+    kv = np.random.default_rng(args.seed).integers(4096, 32769, size=nb)
+    s_max = int(kv.max()) + T
+    g = torch.Generator(device=dev).manual_seed(args.seed)
+    q = torch.randn(nb, T, hq, dh, generator=g, device=dev).to(torch.bfloat16)
+    gate = torch.randn(nb, T, hq, dh, generator=g, device=dev).to(torch.bfloat16)
+    qn = torch.randn(dh, generator=g, device=dev) * 0.1
+    ck = torch.randn(nb, hkv, s_max, dh, generator=g, device=dev).to(torch.bfloat16)
+    cv = torch.randn(nb, hkv, s_max, dh, generator=g, device=dev).to(torch.bfloat16)
+    kvl = torch.as_tensor(kv, dtype=torch.int32, device=dev)
+    cos, sin = rope_tables(kvl.long()[:, None] + torch.arange(T, device=dev))
+
+    def attn(i):
+        return torch.ops.gqa.tail_verify(q, gate, qn, cos, sin, ck, cv, kvl)
+
+    ms = time_calls(attn, args.steps, args.warmup)
+    row = {"B": nb, "kv_len": kv.tolist(), "ms": round(ms, 4)}
+    row.update(hbm_row(gqa_verify_bytes(kv), ms))
+    print(json.dumps({
+        "workload": "GQA verify attention, B = 16, T = 8, 24 q / 4 kv heads of 256, kv "
+                    "U{4096..32768}", "kernel": "gqa.tail_verify", "bound": "hbm",
+        "peak": HBM_PEAK_GBS, "rows": [row], "steps": args.steps,
+        "warmup": max(args.warmup, CFG_MIN_WARMUP)}))
+
+
+def config3_bench(args):
+    """FP8 W8A16 GEMM (fp8::matmul, bf16 out) at M = B*T in {8, 64, 256}, K = 5120,
+    N in {5120, 17408, 34816}: e4m3 weights from N(0, 0.02) per-channel absmax-quantised
+    (clip +-448), fp32 per-channel scales, bf16 N(0,1) activations. Enough weight copies
+    (at least 2, over 600 MB in all) are used in turn that the weights come from HBM."""
+    import torch
+    import npn_ops  # noqa: F401
+    from spec_verify_step import random_fp8_linear
+    dev, Kd = "cuda", 5120
+    rows = []
+    for n in (5120, 17408, 34816):
+        g = torch.Generator(device=dev).manual_seed(args.seed + n)
+        copies = max(2, -(-600_000_000 // (Kd * n)))
+        ws = [random_fp8_linear(n, Kd, g, dev) for _ in range(copies)]
+        for m in (8, 64, 256):
+            x = torch.randn(m, Kd, generator=g, device=dev).to(torch.bfloat16)
+
+            def mm(i):
+                w, sc = ws[i % copies]
+                return torch.ops.fp8.matmul(x, w, sc)
+
+            ms = time_calls(mm, max(args.steps, 2 * copies), args.warmup)
+            flops = 2.0 * m * n * Kd
+            tf = flops / (ms * 1e-3) / 1e12
+            row = {"M": m, "K": Kd, "N": n, "ms": round(ms, 4), "tflops": round(tf, 1),
+                   "mfma_frac": round(tf / BF16_PEAK_TFLOPS, 4), "weight_copies": copies}
+            hb = hbm_row(Kd * n + n * 4 + m * Kd * 2 + m * n * 2, ms)
+            row.update({"hbm_gbs": hb["achieved"], "hbm_frac": hb["frac"],
+                        "bound": "hbm" if m <= 64 else "mfma"})
+            rows.append(row)
+        del ws
+    print(json.dumps({
+        "workload": "FP8 W8A16 GEMM, M in {8, 64, 256}, K = 5120, N in {5120, 17408, 34816}",
+        "kernel": "fp8.matmul", "peaks": {"hbm_gbs": HBM_PEAK_GBS,
+                                          "bf16_mfma_tflops": BF16_PEAK_TFLOPS},
+        "rows": rows, "steps": args.steps, "warmup": max(args.warmup, CFG_MIN_WARMUP)}))
+
+
 LM_VOCAB = 248320  # Qwen3.6-27B vocabulary (static_decode.py:107)
 # untimed calls per variant before its timed ones, at least: with 3 the shader clock has not
 # settled for the first variant (measured: fused 0.808 ms per call after 3, 0.772 after 64)
@@ -474,6 +646,9 @@ def main():
         return
     if args.lm_head:
         lm_head_bench(args)
+        return
+    if args.config:
+        (config1_bench, config2_bench, config3_bench)[args.config - 1](args)
         return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (got --gpus {args.gpus}); the verify step is "

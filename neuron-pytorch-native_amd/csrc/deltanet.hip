@@ -14,19 +14,14 @@
 // Checkpoints ckpt[b][t][h] use the same tile layout, so the T=1 checkpoint buffer is
 // exactly the reference's new_state.
 //
-// Work decomposition: one 128-thread workgroup per (b, h); thread j owns state column
-// v = j and keeps all 128 rows of it in VGPRs for the whole verify block, so the
-// column sums S^T k and S^T q are thread-local. Each checkpoint row is one
-// 256-byte coalesced store per wave. The only cross-thread reductions are the q/k
-// L2 norms (before the loop) and the output RMS norm (after it). The per-token q, k, v
-// and o vectors live in LDS, which keeps the kernel at 168 VGPRs: three waves per SIMD,
-// so B*Hv = 1536 workgroups (B = 32, Hv = 48) are resident at once on 256 CUs.
+// Work decomposition: one workgroup per (b, h) whose waves hold the head's 128 state columns
+// split into row parts (the verify kernel below); the workgroup size follows the batch, so
+// small batches still stream the states through many waves.
 #include "npn_common.h"
 
 namespace {
 
 constexpr int D = 128;
-constexpr int kThreads = 128;
 constexpr float kEps = 1e-6f;
 
 struct DnArgs {
@@ -74,21 +69,30 @@ __device__ __forceinline__ void conv_channel(const uint16_t* __restrict__ cs,
   }
 }
 
-template <int TMAX>
-__global__ __launch_bounds__(kThreads, 3) void dn_verify_kernel(DnArgs a) {
+// Verify kernel: one workgroup of 128 * P threads per (b, h). Wave w holds state columns
+// 64 (w & 1) .. + 63 and rows (w >> 1) * 128 / P .. + 128 / P of them in VGPRs for the whole
+// verify block, so a head's state streams through 2 P waves. The column sums S^T k and
+// S^T q of each token are added over the P row parts through LDS in part order; each
+// checkpoint row is one 256-byte coalesced store per wave; the q / k L2 norms (before the
+// loop) and the output RMS norm (after it) are wave reductions over the head's 128 channels.
+// The per-token q, k, v and o vectors live in LDS.
+template <int TMAX, int P>
+__global__ __launch_bounds__(128 * P) void dn_verify_kernel(DnArgs a) {
+  constexpr int R = D / P;             // state rows per thread
+  constexpr int NT = 128 * P;
   const int b = blockIdx.x / a.Hv;
   const int h = blockIdx.x - b * a.Hv;
   const int tid = threadIdx.x;
   const int lane = tid & (npn::kWave - 1);
   const int wid = tid >> 6;
+  const int c = (wid & 1) * 64 + lane;   // state column (v index)
+  const int part = wid >> 1;             // rows part * R .. part * R + R - 1
+  const int r0 = part * R;
   const int T = a.T;
   const int kh = h / (a.Hv / a.Hk);
   const int QKV = (2 * a.Hk + a.Hv) * D;
   const size_t tile = (size_t)D * D;
 
-  // Per token: raw (un-normalised) conv outputs of q and k, which every thread reads in
-  // full; v and o, which only their own thread uses, are parked here too so that the
-  // 128-row state column is the only large live set (three waves per SIMD).
   __shared__ float s_q[TMAX][D];
   __shared__ float s_k[TMAX][D];
   __shared__ float s_v[TMAX][D];
@@ -96,8 +100,8 @@ __global__ __launch_bounds__(kThreads, 3) void dn_verify_kernel(DnArgs a) {
   __shared__ float s_rq[TMAX], s_rk[TMAX], s_ro[TMAX];
   __shared__ float s_decay[TMAX];
   __shared__ float s_beta[TMAX];
+  __shared__ float s_red[2][P][D];
 
-  // Initial state column (issued first so the loads overlap the prologue).
   const float* S0;
   if (a.state_index != nullptr) {
     int idx = a.state_index[b];
@@ -106,27 +110,24 @@ __global__ __launch_bounds__(kThreads, 3) void dn_verify_kernel(DnArgs a) {
   } else {
     S0 = a.state + ((size_t)b * a.Hv + h) * tile;
   }
-  float S[D];
+  float S[R];
 #pragma unroll
-  for (int k = 0; k < D; ++k) S[k] = S0[(size_t)k * D + tid];
+  for (int r = 0; r < R; ++r) S[r] = S0[(size_t)(r0 + r) * D + c];
 
-  // Conv + SiLU for this thread's q, k (shared k-head) and v channels.
+  // Conv + SiLU of the head's q, k and v channels (3 * 128 channels over the workgroup).
   {
     const uint16_t* xb = a.mixed_qkv + (size_t)b * T * QKV;
     const uint16_t* csb = a.conv_state + (size_t)b * QKV * 3;
-    float y[TMAX];
-    conv_channel<TMAX>(csb, xb, a.conv_weight, a.conv_bias, kh * D + tid, QKV, T, y);
+    for (int ch = tid; ch < 3 * D; ch += NT) {
+      const int which = ch / D, i = ch - which * D;
+      const int chan = which == 0 ? kh * D + i : (which == 1 ? (a.Hk + kh) * D + i : (2 * a.Hk + h) * D + i);
+      float (*dst)[D] = which == 0 ? s_q : (which == 1 ? s_k : s_v);
+      float y[TMAX];
+      conv_channel<TMAX>(csb, xb, a.conv_weight, a.conv_bias, chan, QKV, T, y);
 #pragma unroll
-    for (int t = 0; t < TMAX; ++t) s_q[t][tid] = y[t];
-    conv_channel<TMAX>(csb, xb, a.conv_weight, a.conv_bias, (a.Hk + kh) * D + tid, QKV, T, y);
-#pragma unroll
-    for (int t = 0; t < TMAX; ++t) s_k[t][tid] = y[t];
-    conv_channel<TMAX>(csb, xb, a.conv_weight, a.conv_bias, (2 * a.Hk + h) * D + tid, QKV, T, y);
-#pragma unroll
-    for (int t = 0; t < TMAX; ++t) s_v[t][tid] = y[t];
+      for (int t = 0; t < TMAX; ++t) dst[t][i] = y[t];
+    }
   }
-
-  // Gates for every token (one thread per token).
   if (tid < T) {
     const size_t gi = ((size_t)b * T + tid) * a.Hv + h;
     const float g = -__expf(a.A_log[h]) * npn::softplus(a.a_out[gi] + a.dt_bias[h]);
@@ -135,11 +136,8 @@ __global__ __launch_bounds__(kThreads, 3) void dn_verify_kernel(DnArgs a) {
   }
   __syncthreads();
 
-  // L2 norms of q_t and k_t over the 128 channels of the k-head: wave w reduces the tokens
-  // t = w, w + 2, ...; the scales multiply the dot products and the update below.
   const float qscale = 0.08838834764831845f;  // 1/sqrt(128)
-#pragma unroll
-  for (int t = wid; t < TMAX; t += 2) {
+  for (int t = wid; t < TMAX; t += 2 * P) {
     const float q0 = s_q[t][lane], q1 = s_q[t][lane + 64];
     const float k0 = s_k[t][lane], k1 = s_k[t][lane + 64];
     const float sq = npn::wave_sum(q0 * q0 + q1 * q1);
@@ -151,9 +149,7 @@ __global__ __launch_bounds__(kThreads, 3) void dn_verify_kernel(DnArgs a) {
   }
   __syncthreads();
 
-  // Recurrence over the T tokens; checkpoint after each. With k = rk * k_raw and
-  // q = rq * q_raw: S^T k = rk * (S^T k_raw), S += k_raw (rk * delta), o = rq * (S^T q_raw).
-  float* ck = a.ckpt + ((size_t)b * T * a.Hv + h) * tile + tid;
+  float* ck = a.ckpt + ((size_t)b * T * a.Hv + h) * tile + (size_t)r0 * D + c;
 #pragma unroll
   for (int t = 0; t < TMAX; ++t) {
     if (t < T) {
@@ -161,35 +157,41 @@ __global__ __launch_bounds__(kThreads, 3) void dn_verify_kernel(DnArgs a) {
       const float rk = s_rk[t];
       float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int k = 0; k < D; ++k) {
-        S[k] *= decay;
-        acc[k & 3] = fmaf(S[k], s_k[t][k], acc[k & 3]);
+      for (int r = 0; r < R; ++r) {
+        S[r] *= decay;
+        acc[r & 3] = fmaf(S[r], s_k[t][r0 + r], acc[r & 3]);
       }
-      const float kS = ((acc[0] + acc[1]) + (acc[2] + acc[3])) * rk;
-      const float kd = (s_v[t][tid] - kS) * s_beta[t] * rk;
-      asm volatile("" ::: "memory");
+      s_red[0][part][c] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+      __syncthreads();
+      float kS = 0.f;
+#pragma unroll
+      for (int q = 0; q < P; ++q) kS += s_red[0][q][c];
+      const float kd = (s_v[t][c] - kS * rk) * s_beta[t] * rk;
       float oc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int k = 0; k < D; ++k) {
-        S[k] = fmaf(s_k[t][k], kd, S[k]);
-        oc[k & 3] = fmaf(S[k], s_q[t][k], oc[k & 3]);
+      for (int r = 0; r < R; ++r) {
+        S[r] = fmaf(s_k[t][r0 + r], kd, S[r]);
+        oc[r & 3] = fmaf(S[r], s_q[t][r0 + r], oc[r & 3]);
       }
-      s_o[t][tid] = ((oc[0] + oc[1]) + (oc[2] + oc[3])) * s_rq[t];
-      asm volatile("" ::: "memory");
-      // Nontemporal stores. Plain (write-allocating) stores make this kernel ~11% shorter,
-      // but part of the 805 MB then drains from the memory-side cache during the GEMMs
-      // that follow, and the whole step is ~1% slower (measured on MI355X).
+      s_red[1][part][c] = (oc[0] + oc[1]) + (oc[2] + oc[3]);
+      // Nontemporal stores: write-allocating ones leave part of the checkpoints to drain from
+      // the memory-side cache during the GEMMs that follow (the step measured ~1% slower).
       float* dst = ck + (size_t)t * a.Hv * tile;
 #pragma unroll
-      for (int k = 0; k < D; ++k) __builtin_nontemporal_store(S[k], dst + (size_t)k * D);
+      for (int r = 0; r < R; ++r) __builtin_nontemporal_store(S[r], dst + (size_t)r * D);
+      __syncthreads();
+      if (part == 0) {
+        float o = 0.f;
+#pragma unroll
+        for (int q = 0; q < P; ++q) o += s_red[1][q][c];
+        s_o[t][c] = o * s_rq[t];
+      }
     }
   }
 
-  // Gated RMSNorm of o_t over the 128 v columns (tokens t < T only: s_o[t] is written for
-  // those alone).
+  // Gated RMSNorm of o_t over the 128 v columns (tokens t < T only).
   __syncthreads();
-#pragma unroll
-  for (int t = wid; t < TMAX; t += 2) {
+  for (int t = wid; t < TMAX; t += 2 * P) {
     if (t < T) {
       const float o0 = s_o[t][lane], o1 = s_o[t][lane + 64];
       const float so = npn::wave_sum(o0 * o0 + o1 * o1);
@@ -197,14 +199,11 @@ __global__ __launch_bounds__(kThreads, 3) void dn_verify_kernel(DnArgs a) {
     }
   }
   __syncthreads();
-  const float nw = a.norm_weight[tid];
-#pragma unroll
-  for (int t = 0; t < TMAX; ++t) {
-    if (t < T) {
-      const size_t oi = (((size_t)b * T + t) * a.Hv + h) * D + tid;
-      const float zz = npn::bf16_to_f32(a.z[oi]);
-      a.out[oi] = npn::f32_to_bf16(s_o[t][tid] * s_ro[t] * nw * npn::silu(zz));
-    }
+  for (int idx = tid; idx < T * D; idx += NT) {
+    const int t = idx / D, cc = idx - t * D;
+    const size_t oi = (((size_t)b * T + t) * a.Hv + h) * D + cc;
+    const float zz = npn::bf16_to_f32(a.z[oi]);
+    a.out[oi] = npn::f32_to_bf16(s_o[t][cc] * s_ro[t] * a.norm_weight[cc] * npn::silu(zz));
   }
 }
 
@@ -254,9 +253,20 @@ int check_heads(int k_heads, int v_heads) {
   return NPN_OK;
 }
 
+// Row parts per state column, from a sweep on MI355X (16 k / 48 v heads, T = 8, P = 1, 2, 4,
+// 8): below 192 heads (B <= 3) eight parts (B = 1: 18.0 us against 31.8 us unsplit), below
+// 1536 four (B = 8: 47.0 us against 56.7 us), and two from there (B = 32: 168 us against
+// 183 us, 67 % of HBM peak).
+int row_parts(int heads) { return heads < 192 ? 8 : (heads < 1536 ? 4 : 2); }
+
 template <int TMAX>
 void launch_verify(const DnArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL(dn_verify_kernel<TMAX>, dim3(a.B * a.Hv), dim3(kThreads), 0, s, a);
+  const int heads = a.B * a.Hv;
+  switch (row_parts(heads)) {
+    case 2: hipLaunchKernelGGL((dn_verify_kernel<TMAX, 2>), dim3(heads), dim3(256), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((dn_verify_kernel<TMAX, 4>), dim3(heads), dim3(512), 0, s, a); break;
+    default: hipLaunchKernelGGL((dn_verify_kernel<TMAX, 8>), dim3(heads), dim3(1024), 0, s, a); break;
+  }
 }
 
 int verify_impl(const DnArgs& a, hipStream_t s) {

@@ -5,27 +5,20 @@
 // to [K, N] (N contiguous), bf16 activations, fp32 accumulation, per-output-channel scale
 // applied to the fp32 sum, then a bf16 cast.
 //
-// Mapping onto v_mfma_f32_16x16x32_bf16 (A = x tile 16 rows x 32 k, B = W tile 32 k x 16 n):
-// the B operand wants 8 consecutive k of one column per lane, but [K, N] stores a column
-// with stride N. Each lane therefore loads one dword = 4 adjacent columns from each of its
-// 8 k rows (W[k0 + 8G + j][n0 + 4i .. 4i+3], j = 0..7; 64-byte runs per row across the 16
-// lanes of a group), transposes the 8x4 byte block in registers with v_perm_b32, and
-// dequantises each column's 8 bytes to bf16 with v_cvt_scalef32_pk_bf16_fp8 (exact: every
-// e4m3fn value is a bf16 value). Column ct of the lane feeds MFMA number ct, whose output
-// column i is global column n0 + 4i + ct: a 64-column wave tile is 4 MFMAs with their
-// columns interleaved, and the epilogue writes 4 adjacent bf16 per lane and row.
-//
-// Work split: workgroup = 8 waves on one 64-column tile; the waves split K, their fp32
-// partials are summed in a fixed tree through LDS (deterministic), scaled and stored.
-// For narrow N, K is also split across workgroups (split_k); partials then go through an
-// fp32 workspace and a fixed-order reduction kernel. M is covered in passes of 16*MT rows.
+// Two kernels. Up to 64 rows per pass (the narrow kernel, HBM-bound) the weights go straight
+// from HBM into registers: v_mfma_f32_16x16x32_bf16's B operand wants 8 consecutive k of one
+// column per lane, but [K, N] stores a column with stride N, so each lane loads 16 adjacent
+// columns from each of its 8 k rows (256-byte runs per row across the 16 lanes of a group),
+// transposes each 8x4 byte quarter of that block in registers with v_perm_b32 and dequantises
+// each column's 8 bytes to bf16 with v_cvt_scalef32_pk_bf16_fp8 (exact: every e4m3fn value is
+// a bf16 value). Above 64 rows (the wide kernel, MFMA-bound) a workgroup stages W tiles in LDS
+// with direct global-to-LDS loads and reads the B operands back transposed
+// (ds_read_b64_tr_b8); details with each kernel below.
 #include "npn_common.h"
 
 namespace {
 
-constexpr int NW = 64;      // columns per workgroup tile
 constexpr int KSTEP = 32;   // k per MFMA
-constexpr int WAVES = 8;
 
 typedef __bf16 bf16x8 __attribute__((__vector_size__(8 * sizeof(__bf16))));
 typedef float f32x4 __attribute__((__vector_size__(4 * sizeof(float))));
@@ -104,133 +97,186 @@ struct GemmArgs {
   uint16_t* out;     // used when split_k == 1 and !to_partial
   float* partial;    // [split_k][M][N] fp32, unscaled, when split_k > 1 or to_partial
   int M, K, N, split_k, to_partial;
-  ArgPart* amax;     // row argmax partials [M][N / NW] instead of out (split_k == 1)
+  ArgPart* amax;     // row argmax partials [M][ceil(N / NT)] instead of out (split_k == 1)
 };
 
-template <int MT>
-__global__ __launch_bounds__(WAVES * 64) void fp8_gemm_kernel(GemmArgs a) {
-  constexpr int ROWS = 16 * MT;
-  const int n0 = blockIdx.x * NW;
+// ---------------------------------------------------------------------------------------
+// Narrow kernel for M <= 64 rows per pass (HBM-bound: each weight byte feeds 2*M flops).
+// The weights stream once from HBM, so what matters is how the reads meet the DRAM: consecutive
+// rows of W are N bytes apart, and a W row read in pieces of 64 contiguous bytes streams at
+// about 2.4 TB/s on MI355X, in pieces of 128 bytes at 4.1 TB/s and of 256 bytes at 4.8 TB/s,
+// whatever the bytes per lane (measured with a pure-load kernel, 178 MB of W, 544
+// workgroups). So a workgroup owns a 256-column tile: lane (i, G) loads 16 bytes (columns
+// n0 + 16 i .. + 15) from each of its 8 k rows 8 G + j, and each quarter of those bytes is
+// transposed in registers and dequantised into the B operands of 4 MFMAs (column ct of
+// quarter q feeds MFMA 4 q + ct, whose output column i is n0 + 16 i + 4 q + ct).
+// A workgroup is 4 waves = RB row blocks of 16 rows x (4 / RB) k parts; waves of one k part
+// read the same W bytes (served by the CU's L1), waves of one row block add their partial sums
+// in a fixed tree through LDS. For wide N, K is also split across workgroups (split_k);
+// partials then go through an fp32 workspace and a fixed-order reduction kernel.
+constexpr int NT = 256;     // columns per narrow tile
+constexpr int NWAVES = 4;   // waves per narrow workgroup
+
+template <int RB>
+__global__ __launch_bounds__(NWAVES * 64, 3) void fp8_gemm_kernel(GemmArgs a) {
+  constexpr int KP = NWAVES / RB;
+  constexpr int ROWS = 16 * RB;
+  const int n0 = blockIdx.x * NT;
   const int sk = blockIdx.y;
-  const int m_base = blockIdx.z * ROWS;
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int i = lane & 15, G = lane >> 4;
+  const int rb = w % RB, kp = w / RB;
+  const int m_base = blockIdx.z * ROWS + 16 * rb;
+  // This lane's 16 columns; N % 16 == 0, so they are all inside N or all past it (a last,
+  // partial tile): lanes past N read the tile's last 16 columns again and store nothing.
+  const int nc = n0 + 16 * i;
+  const bool col_ok = nc < a.N;
+  const uint8_t* wcol = a.w + (col_ok ? nc : a.N - 16);
+  // A operand row i of the row block (rows past M read row M - 1, zeroed after the load)
+  const int mrow = m_base + i;
+  const bool row_ok = mrow < a.M;
+  const uint16_t* xrow = a.x + (size_t)(row_ok ? mrow : a.M - 1) * a.K;
 
-  // k steps of this wave: split evenly over split_k * WAVES workers.
+  // k steps of this wave: split evenly over split_k * KP workers.
   const int nks = a.K / KSTEP;
-  const int worker = sk * WAVES + w;
-  const int workers = a.split_k * WAVES;
+  const int worker = sk * KP + kp;
+  const int workers = a.split_k * KP;
   const int ks_lo = (int)(((long)nks * worker) / workers);
   const int ks_hi = (int)(((long)nks * (worker + 1)) / workers);
 
-  f32x4 acc[MT][4];
+  f32x4 acc[16];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int ct = 0; ct < 4; ++ct) acc[mt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int c = 0; c < 16; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const uint8_t* wcol = a.w + n0 + 4 * i;
-  for (int ks = ks_lo; ks < ks_hi; ++ks) {
+  // Two register slots: the W bytes and x row of step ks + 1 load while step ks computes
+  // (a wave has two steps' loads in flight; one step is about a memory round trip of
+  // compute-free waiting otherwise). The loop is unrolled by two so the slots are fixed
+  // registers, and every load is unconditional -- a step past the range repeats the last
+  // one -- so the wait before a step counts only the one batch issued after it.
+  u32x4 wd[2][8], xd[2];
+  auto load = [&](int ks, u32x4 (&dw)[8], u32x4& dx) {
+    ks = ks < ks_hi ? ks : ks_hi - 1;
     const int k0 = ks * KSTEP + 8 * G;
-    uint32_t d[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j)
-      d[j] = *reinterpret_cast<const uint32_t*>(wcol + (size_t)(k0 + j) * a.N);
-    bf16x8 aop[MT];
+      dw[j] = *reinterpret_cast<const u32x4*>(wcol + (size_t)(k0 + j) * a.N);
+    dx = *reinterpret_cast<const u32x4*>(xrow + k0);
+  };
+  auto compute = [&](const u32x4 (&dw)[8], const u32x4& dx) {
+    const u32x4 zero = {0u, 0u, 0u, 0u};
+    const bf16x8 aop = __builtin_bit_cast(bf16x8, row_ok ? dx : zero);
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const int m = m_base + 16 * mt + i;
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if (m < a.M) v = *reinterpret_cast<const u32x4*>(a.x + (size_t)m * a.K + k0);
-      aop[mt] = __builtin_bit_cast(bf16x8, v);
-    }
-    bf16x8 bop[4];
-    transpose_dequant(d, bop);
+    for (int q = 0; q < 4; ++q) {
+      uint32_t dq[8];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+      for (int j = 0; j < 8; ++j) dq[j] = dw[j][q];
+      bf16x8 bop[4];
+      transpose_dequant(dq, bop);
 #pragma unroll
       for (int ct = 0; ct < 4; ++ct)
-        acc[mt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop[mt], bop[ct], acc[mt][ct], 0, 0, 0);
+        acc[4 * q + ct] =
+            __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop, bop[ct], acc[4 * q + ct], 0, 0, 0);
+    }
+  };
+  // sched_barrier(0) keeps each batch of loads ahead of the previous step's MFMAs (the
+  // scheduler would otherwise sink them below, leaving nothing in flight at the wait).
+  if (ks_lo < ks_hi) {
+    load(ks_lo, wd[0], xd[0]);
+    for (int ks = ks_lo; ks < ks_hi; ks += 2) {
+      load(ks + 1, wd[1], xd[1]);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(wd[0], xd[0]);
+      load(ks + 2, wd[0], xd[0]);
+      __builtin_amdgcn_sched_barrier(0);
+      if (ks + 1 < ks_hi) compute(wd[1], xd[1]);
+    }
   }
 
-  // Deterministic tree over the 8 waves: (w, w+4), (w, w+2), (w, w+1).
-  __shared__ __attribute__((aligned(16))) float red[4][ROWS * NW];
-  auto slot_off = [&](int mt, int ct, int r) { return (16 * mt + 4 * G + r) * NW + 4 * i + ct; };
+  // Deterministic tree over the k parts of each row block, one column quarter at a time:
+  // parts (p, p + KP/2), then (p, p + KP/4), ...
+  if constexpr (KP > 1) {
+    __shared__ __attribute__((aligned(16))) float red[(KP / 2) * RB][16 * 64];
+    auto slot_off = [&](int ct, int r) { return (4 * G + r) * 64 + 4 * i + ct; };
 #pragma unroll
-  for (int half = 4; half >= 1; half >>= 1) {
-    if (w >= half && w < 2 * half) {
+    for (int q = 0; q < 4; ++q) {
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
+      for (int half = KP / 2; half >= 1; half >>= 1) {
+        if (kp >= half && kp < 2 * half) {
 #pragma unroll
-        for (int ct = 0; ct < 4; ++ct)
+          for (int ct = 0; ct < 4; ++ct)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) red[w - half][slot_off(mt, ct, r)] = acc[mt][ct][r];
+            for (int r = 0; r < 4; ++r)
+              red[(kp - half) * RB + rb][slot_off(ct, r)] = acc[4 * q + ct][r];
+        }
+        __syncthreads();
+        if (kp < half) {
+#pragma unroll
+          for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              acc[4 * q + ct][r] += red[kp * RB + rb][slot_off(ct, r)];
+        }
+        __syncthreads();
+      }
     }
-    __syncthreads();
-    if (w < half) {
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int ct = 0; ct < 4; ++ct)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) acc[mt][ct][r] += red[w][slot_off(mt, ct, r)];
-    }
-    __syncthreads();
   }
-  if (w != 0) return;
+  if (kp != 0) return;
 
-  // Wave 0 holds the tile sum: lane (i, G) has rows 16mt + 4G + r, columns n0 + 4i + ct.
+  // Waves of k part 0 hold their row block's sums: lane (i, G) has rows m_base + 4 G + r and
+  // columns nc + c in acc[c][r].
   if (a.amax != nullptr) {
-    float sc[4];
+    float sc[16];
 #pragma unroll
-    for (int ct = 0; ct < 4; ++ct) sc[ct] = a.scale[n0 + 4 * i + ct];
+    for (int c = 0; c < 16; ++c) sc[c] = col_ok ? a.scale[nc + c] : 0.0f;
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+    for (int r = 0; r < 4; ++r) {
+      float bv = -__builtin_inff();
+      int bi = 0x7FFFFFFF;
+      if (col_ok) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float bv = -__builtin_inff();
-        int bi = 0x7FFFFFFF;
-#pragma unroll
-        for (int ct = 0; ct < 4; ++ct) {
-          const float v = bf16_round(acc[mt][ct][r] * sc[ct]);
-          if (arg_beats(v, n0 + 4 * i + ct, bv, bi)) {
+        for (int c = 0; c < 16; ++c) {
+          const float v = bf16_round(acc[c][r] * sc[c]);
+          if (arg_beats(v, nc + c, bv, bi)) {
             bv = v;
-            bi = n0 + 4 * i + ct;
+            bi = nc + c;
           }
         }
-        arg_merge16(bv, bi);
-        const int m = m_base + 16 * mt + 4 * G + r;
-        if (i == 0 && m < a.M) a.amax[(size_t)m * gridDim.x + blockIdx.x] = ArgPart{bv, bi};
       }
+      arg_merge16(bv, bi);
+      const int m = m_base + 4 * G + r;
+      if (i == 0 && m < a.M) a.amax[(size_t)m * gridDim.x + blockIdx.x] = ArgPart{bv, bi};
+    }
     return;
   }
+  if (!col_ok) return;
   if (a.split_k == 1 && !a.to_partial) {
-    float sc[4];
+    float sc[16];
 #pragma unroll
-    for (int ct = 0; ct < 4; ++ct) sc[ct] = a.scale[n0 + 4 * i + ct];
+    for (int c = 0; c < 16; ++c) sc[c] = a.scale[nc + c];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+    for (int r = 0; r < 4; ++r) {
+      const int m = m_base + 4 * G + r;
+      if (m >= a.M) continue;
+      uint32_t pk[8];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = m_base + 16 * mt + 4 * G + r;
-        if (m >= a.M) continue;
-        uint32_t lo = npn::f32_to_bf16(acc[mt][0][r] * sc[0]) |
-                      ((uint32_t)npn::f32_to_bf16(acc[mt][1][r] * sc[1]) << 16);
-        uint32_t hi = npn::f32_to_bf16(acc[mt][2][r] * sc[2]) |
-                      ((uint32_t)npn::f32_to_bf16(acc[mt][3][r] * sc[3]) << 16);
-        *reinterpret_cast<uint2*>(a.out + (size_t)m * a.N + n0 + 4 * i) = make_uint2(lo, hi);
-      }
+      for (int c = 0; c < 8; ++c)
+        pk[c] = npn::f32_to_bf16(acc[2 * c][r] * sc[2 * c]) |
+                ((uint32_t)npn::f32_to_bf16(acc[2 * c + 1][r] * sc[2 * c + 1]) << 16);
+      uint4* dst = reinterpret_cast<uint4*>(a.out + (size_t)m * a.N + nc);
+      dst[0] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+      dst[1] = make_uint4(pk[4], pk[5], pk[6], pk[7]);
+    }
   } else {
     float* part = a.partial + (size_t)sk * a.M * a.N;
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+    for (int r = 0; r < 4; ++r) {
+      const int m = m_base + 4 * G + r;
+      if (m >= a.M) continue;
+      float4* dst = reinterpret_cast<float4*>(part + (size_t)m * a.N + nc);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = m_base + 16 * mt + 4 * G + r;
-        if (m >= a.M) continue;
-        *reinterpret_cast<float4*>(part + (size_t)m * a.N + n0 + 4 * i) =
-            make_float4(acc[mt][0][r], acc[mt][1][r], acc[mt][2][r], acc[mt][3][r]);
-      }
+      for (int c = 0; c < 4; ++c)
+        dst[c] = make_float4(acc[4 * c][r], acc[4 * c + 1][r], acc[4 * c + 2][r], acc[4 * c + 3][r]);
+    }
   }
 }
 
@@ -688,14 +734,20 @@ GemmPlan plan(int M, int K, int N, bool no_split = false) {
   GemmPlan p{};
   if (plan_wide(M, K, N, p, no_split)) return p;
   p = GemmPlan{};
+  // Narrow plan: row blocks per pass (4 waves: RB row blocks x 4 / RB k parts), and a split-K
+  // factor: the largest power of two up to 8 that keeps the grid at or under 160 workgroups.
+  // Measured on MI355X at M = 8 and 64, K = 5120, N = 5120 / 17408 / 34816, the GEMM plus its
+  // reduction is fastest at 136 to 160 workgroups (N = 34816 unsplit, 17408 split in two,
+  // 5120 in eight); more workgroups only add partial traffic and HBM contention.
   const int mtiles = (M + 15) / 16;
-  p.mt = mtiles >= 8 ? 8 : (mtiles >= 4 ? 4 : (mtiles >= 2 ? 2 : 1));
+  p.mt = mtiles >= 4 ? 4 : (mtiles >= 2 ? 2 : 1);
   p.passes = (M + 16 * p.mt - 1) / (16 * p.mt);
-  const int tiles = (N / NW) * p.passes;
+  const int tiles = ((N + NT - 1) / NT) * p.passes;
+  const int kparts = NWAVES / p.mt;
   const int nks = K / KSTEP;
   p.split_k = 1;
-  while (!no_split && tiles * p.split_k < 256 && p.split_k < 4 &&
-         nks >= 2 * p.split_k * 2 * WAVES)
+  while (!no_split && p.split_k < 8 && tiles * p.split_k * 2 <= 160 &&
+         nks >= 2 * (2 * p.split_k) * kparts)
     p.split_k *= 2;
   p.ws = p.split_k > 1 ? (size_t)p.split_k * M * N * sizeof(float) : 0;
   return p;
@@ -730,12 +782,11 @@ int launch_gemm(const GemmPlan& p, const uint16_t* x, const int8_t* w, const flo
   } else {
     GemmArgs ga{x, reinterpret_cast<const uint8_t*>(w), scale, out, partial, M, K, N, p.split_k,
                 to_partial, amax};
-    const dim3 grid(N / NW, p.split_k, p.passes);
+    const dim3 grid((N + NT - 1) / NT, p.split_k, p.passes);
     switch (p.mt) {
-      case 1: hipLaunchKernelGGL(fp8_gemm_kernel<1>, grid, dim3(WAVES * 64), 0, s, ga); break;
-      case 2: hipLaunchKernelGGL(fp8_gemm_kernel<2>, grid, dim3(WAVES * 64), 0, s, ga); break;
-      case 4: hipLaunchKernelGGL(fp8_gemm_kernel<4>, grid, dim3(WAVES * 64), 0, s, ga); break;
-      default: hipLaunchKernelGGL(fp8_gemm_kernel<8>, grid, dim3(WAVES * 64), 0, s, ga); break;
+      case 1: hipLaunchKernelGGL(fp8_gemm_kernel<1>, grid, dim3(NWAVES * 64), 0, s, ga); break;
+      case 2: hipLaunchKernelGGL(fp8_gemm_kernel<2>, grid, dim3(NWAVES * 64), 0, s, ga); break;
+      default: hipLaunchKernelGGL(fp8_gemm_kernel<4>, grid, dim3(NWAVES * 64), 0, s, ga); break;
     }
   }
   if (reduce && p.split_k > 1) {
@@ -826,7 +877,7 @@ extern "C" int npn_fp8_matmul_swiglu(const uint16_t* x, const int8_t* w, const f
 extern "C" int npn_fp8_matmul_argmax_groups(int M, int K, int N) {
   if (!shape_ok(M, K, N)) return 0;
   const GemmPlan p = plan(M, K, N, true);
-  return p.wide ? p.groups : N / NW;
+  return p.wide ? p.groups : (N + NT - 1) / NT;
 }
 
 extern "C" int npn_fp8_matmul_argmax(const uint16_t* x, const int8_t* w, const float* scale,

@@ -154,6 +154,22 @@ def test_full_size_b32_sampled(ops):
         assert_rel_close(gout[b:b + 1], out, out_unit=BF16_U, name=f"out[b={b}]")
 
 
+@pytest.mark.parametrize("B,parts", [(8, 4), (16, 2), (1, 8)])
+def test_row_split_batches_sampled(ops, B, parts):
+    """Batches that run the row-split kernel (each state column's rows split over `parts`
+    wave pairs: B*Hv = 384 -> 4, 768 -> 2, 48 -> 8), full width, T = 8; sampled sequences
+    against the oracle."""
+    Hk, Hv, T = 16, 48, 8
+    d = deltanet_inputs(B, T, Hk, Hv, seed=40 + B)
+    gck, gout = _verify_gpu(ops, d)
+    for b in sorted({0, B // 2, B - 1}):
+        sl = {k: (v[b:b + 1] if k in ("state", "mixed_qkv", "conv_state", "a_out", "b_out", "z")
+                  else v) for k, v in d.items()}
+        ck, out = od.deltanet_verify(*deltanet_oracle_args(sl), Hk, Hv)
+        assert_rel_close(gck[b:b + 1], ck, name=f"ckpt[b={b}]")
+        assert_rel_close(gout[b:b + 1], out, out_unit=BF16_U, name=f"out[b={b}]")
+
+
 def test_rejects_bad_shapes(ops):
     d = deltanet_inputs(1, 2, 4, 12, seed=1)
     f = deltanet_flat_device(d)

@@ -53,7 +53,8 @@ def parse():
                    help="time eager steps instead of HIP graph replays of the step")
     p.add_argument("--lm-head", action="store_true",
                    help="time the LM head + greedy acceptance over the 27B vocabulary, fused "
-                        "(argmax in the GEMM epilogue) against logits + accept_greedy")
+                        "(argmax in the GEMM epilogue) against logits + accept_greedy, and the "
+                        "same for rejection sampling (row maxima in the epilogue)")
     p.add_argument("--prefill", action="store_true",
                    help="time the chunked gated-DeltaNet prefill (deltanet::chunked_prefill) "
                         "over the 27B layer's 48 v-heads x 4096 prompt tokens")
@@ -529,6 +530,37 @@ def lm_head_bench(args):
         res[name] = s_ev.elapsed_time(e_ev) / args.steps
     a_f, o_f = fused(0)
     a_u, o_u = unfused(0)
+
+    # Rejection sampling at temperature 1 over the same LM head: the fused op (GEMM writing
+    # bf16 logits and row-group maxima, sampling passes over bf16 target rows without a max
+    # pass over them) against the GEMM, a float cast and accept_rejection.
+    draft = torch.randn(B, K, LM_VOCAB, generator=g, device=dev)
+    rids = torch.randint(0, LM_VOCAB, (B, K), generator=g, device=dev)
+    u = torch.rand(B, K, generator=g, device=dev)
+    us = torch.rand(B, generator=g, device=dev)
+
+    def rej_fused(i):
+        w, sc = ws[i % 2]
+        return torch.ops.spec.accept_rejection_lm_head(x, w, sc, draft, rids, u, us, 1.0)[:2]
+
+    def rej_unfused(i):
+        w, sc = ws[i % 2]
+        logits = torch.ops.fp8.matmul(x, w, sc).float().view(B, T, LM_VOCAB)
+        return torch.ops.spec.accept_rejection(logits, draft, rids, u, us, 1.0)
+
+    for name, fn in (("rej_fused", rej_fused), ("rej_unfused", rej_unfused)):
+        for i in range(warmup):
+            fn(i)
+        torch.cuda.synchronize()
+        s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s_ev.record()
+        for i in range(args.steps):
+            fn(i)
+        e_ev.record()
+        torch.cuda.synchronize()
+        res[name] = s_ev.elapsed_time(e_ev) / args.steps
+    ra_f, ro_f = rej_fused(0)
+    ra_u, ro_u = rej_unfused(0)
     flops = 2.0 * B * T * HIDDEN * LM_VOCAB
     print(json.dumps({
         "workload": f"LM head [{B * T}x{HIDDEN}]x[{HIDDEN}x{LM_VOCAB}] fp8 + greedy acceptance, "
@@ -537,6 +569,11 @@ def lm_head_bench(args):
         "fused_tflops": round(flops / res["fused"] / 1e9, 1),
         "weights_gb": round(HIDDEN * LM_VOCAB / 1e9, 3),
         "identical": bool(torch.equal(a_f, a_u) and torch.equal(o_f, o_u)),
+        "rejection": {
+            "workload": "the same LM head + rejection sampling at temperature 1 against "
+                        f"[{B}, {K}, {LM_VOCAB}] fp32 draft logits",
+            "fused_ms": round(res["rej_fused"], 4), "unfused_ms": round(res["rej_unfused"], 4),
+            "identical": bool(torch.equal(ra_f, ra_u) and torch.equal(ro_f, ro_u))},
         "steps": args.steps, "warmup": warmup}))
 
 

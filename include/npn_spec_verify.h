@@ -205,6 +205,15 @@ int npn_fp8_matmul_argmax_groups(int M, int K, int N);
 int npn_fp8_matmul_argmax(const uint16_t* x, const int8_t* w, const float* scale, void* parts,
                           int M, int K, int N, void* stream);
 
+/* New op, no reference counterpart: out [M, N] bf16 = bf16((x . w) * scale) as
+ * npn_fp8_matmul, and gmax [M][G] f32 = per row and column group (the groups of
+ * npn_fp8_matmul_argmax, G = npn_fp8_matmul_argmax_groups(M, K, N)) the largest of the row's
+ * bf16 outputs in the group, NaN ignored (-inf if the group has none). The plan never splits
+ * K; out is bit-identical to npn_fp8_matmul's wherever that plan does not split either (the
+ * vocabulary-wide N of an LM head). Shape rules as npn_fp8_matmul. */
+int npn_fp8_matmul_rowmax(const uint16_t* x, const int8_t* w, const float* scale, uint16_t* out,
+                          float* gmax, int M, int K, int N, void* stream);
+
 /* Split-K factor S of the GEMM plan for these sizes (1: no split; 0: unsupported sizes). */
 int npn_fp8_matmul_split_k(int M, int K, int N);
 
@@ -290,6 +299,25 @@ int npn_argmax_parts(const void* parts, int nparts, int64_t* ids, float* values,
  * K + 1 <= 16. */
 int npn_accept_greedy_parts(const void* parts, int nparts, const int64_t* draft_ids,
                             int32_t* accepted, int64_t* out_ids, int B, int K, void* stream);
+
+/* torch.ops.spec.accept_rejection_lm_head -- new op: npn_accept_rejection with the target
+ * logits produced by the LM head in the same call. hidden [B*(K+1), H] bf16 (the final-normed
+ * verify rows, row b*(K+1) + t), lm_head_w [H, V] e4m3fn bytes, lm_head_scale [V] f32:
+ * target_logits [B*(K+1), V] bf16 is written (= npn_fp8_matmul_rowmax's out) together with
+ * its row-group maxima (in the workspace); the rejection passes read the target rows in bf16
+ * and take their maxima from the groups instead of a pass over them. accepted / out_ids equal
+ * npn_accept_rejection's on the fp32 cast of target_logits, bit for bit, with the same
+ * draft logits, ids, uniforms and inv_temperature (> 0). V % 64 == 0, H % 64 == 0, the other
+ * rules as npn_accept_rejection. Workspace: npn_accept_rejection_lm_head_workspace_size
+ * (0: unsupported sizes). */
+size_t npn_accept_rejection_lm_head_workspace_size(int B, int K, int H, int V);
+int npn_accept_rejection_lm_head(const uint16_t* hidden, const int8_t* lm_head_w,
+                                 const float* lm_head_scale, const float* draft_logits,
+                                 const int64_t* draft_ids, const float* u_accept,
+                                 const float* u_sample, float inv_temperature,
+                                 uint16_t* target_logits, int32_t* accepted, int64_t* out_ids,
+                                 int B, int K, int H, int V, void* workspace,
+                                 size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Inter-layer glue of the verify step (the decode loop of

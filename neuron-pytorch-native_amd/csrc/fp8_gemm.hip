@@ -98,6 +98,7 @@ struct GemmArgs {
   float* partial;    // [split_k][M][N] fp32, unscaled, when split_k > 1 or to_partial
   int M, K, N, split_k, to_partial;
   ArgPart* amax;     // row argmax partials [M][ceil(N / NT)] instead of out (split_k == 1)
+  float* gmax;       // with out: per-(row, tile) max of the bf16 outputs, NaN ignored
 };
 
 // ---------------------------------------------------------------------------------------
@@ -248,25 +249,36 @@ __global__ __launch_bounds__(NWAVES * 64, 3) void fp8_gemm_kernel(GemmArgs a) {
     }
     return;
   }
-  if (!col_ok) return;
   if (a.split_k == 1 && !a.to_partial) {
     float sc[16];
 #pragma unroll
-    for (int c = 0; c < 16; ++c) sc[c] = a.scale[nc + c];
+    for (int c = 0; c < 16; ++c) sc[c] = col_ok ? a.scale[nc + c] : 0.0f;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int m = m_base + 4 * G + r;
-      if (m >= a.M) continue;
       uint32_t pk[8];
+      float mx = -__builtin_inff();  // max of the row's bf16 outputs (fmaxf ignores NaN)
 #pragma unroll
-      for (int c = 0; c < 8; ++c)
-        pk[c] = npn::f32_to_bf16(acc[2 * c][r] * sc[2 * c]) |
-                ((uint32_t)npn::f32_to_bf16(acc[2 * c + 1][r] * sc[2 * c + 1]) << 16);
-      uint4* dst = reinterpret_cast<uint4*>(a.out + (size_t)m * a.N + nc);
-      dst[0] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
-      dst[1] = make_uint4(pk[4], pk[5], pk[6], pk[7]);
+      for (int c = 0; c < 8; ++c) {
+        const uint32_t lo = npn::f32_to_bf16(acc[2 * c][r] * sc[2 * c]);
+        const uint32_t hi = npn::f32_to_bf16(acc[2 * c + 1][r] * sc[2 * c + 1]);
+        pk[c] = lo | (hi << 16);
+        mx = fmaxf(mx, fmaxf(npn::bf16_to_f32(lo), npn::bf16_to_f32(hi)));
+      }
+      if (col_ok && m < a.M) {
+        uint4* dst = reinterpret_cast<uint4*>(a.out + (size_t)m * a.N + nc);
+        dst[0] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+        dst[1] = make_uint4(pk[4], pk[5], pk[6], pk[7]);
+      }
+      if (a.gmax != nullptr) {  // the 16 lanes of a group share the row; lanes past N add -inf
+        if (!col_ok) mx = -__builtin_inff();
+#pragma unroll
+        for (int off = 8; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+        if (i == 0 && m < a.M) a.gmax[(size_t)m * gridDim.x + blockIdx.x] = mx;
+      }
     }
   } else {
+    if (!col_ok) return;
     float* part = a.partial + (size_t)sk * a.M * a.N;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -317,6 +329,7 @@ struct WideArgs {
   float* partial;  // [split_k][M][N] fp32, unscaled, when split_k > 1 or to_partial
   int M, K, N, units, groups, split_k, to_partial;
   ArgPart* amax;   // row argmax partials [M][groups] instead of out (split_k == 1)
+  float* gmax;     // with out: per-(row, group) max of the bf16 outputs, NaN ignored
   // SwiGLU epilogue (split_k == 1): W = [gate | up] along N; units counts gate units, each
   // workgroup takes gate units u0..u1 (at most NH) and the up units N/2 columns to their
   // right, wave column half 0 computing gate and 1 up; out [M, N/2] = bf16(bf16(silu(g)) * u)
@@ -346,6 +359,23 @@ __device__ __forceinline__ void store_staged_bf16(const uint16_t* st, int rs, ui
 
 // Byte offset of the SwiGLU staging tile: past the gate/up exchange slots (4 row quarters x 64
 // lanes x 16 NH bf16), 16-byte aligned.
+// Per-row max of a staged bf16 tile (256 rows of 16 nu values, row stride rs), NaN ignored
+// (fmaxf), into gmax[m][grp] (stride ld): two threads per row, alternating 16-byte pieces.
+__device__ __forceinline__ void staged_row_max(const uint16_t* st, int rs, float* gmax, int ld,
+                                               int grp, int m_base, int M, int nu) {
+  const int row = threadIdx.x >> 1, half = threadIdx.x & 1;
+  float mx = -__builtin_inff();
+  for (int q = half; q < 2 * nu; q += 2) {
+    const uint4 v = *reinterpret_cast<const uint4*>(st + row * rs + 8 * q);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      mx = fmaxf(mx, fmaxf(npn::bf16_to_f32(w[k] & 0xFFFFu), npn::bf16_to_f32(w[k] >> 16)));
+  }
+  mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
+  if (half == 0 && m_base + row < M) gmax[(size_t)(m_base + row) * ld + grp] = mx;
+}
+
 template <int NH>
 constexpr int kSwigluStageOff = 4 * 64 * 16 * NH * 2;
 
@@ -621,6 +651,7 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void fp8_gemm_wide_kernel(WideArgs
     }
     __syncthreads();
     store_staged_bf16(st, RSW, a.out, a.N, m_base, a.M, n0, nu);
+    if (a.gmax != nullptr) staged_row_max(st, RSW, a.gmax, a.groups, grp, m_base, a.M, nu);
     return;
   }
   // fp32 partials (unscaled; the scale pointer may then be NULL), staged 128 rows at a time
@@ -762,11 +793,12 @@ bool shape_ok(int M, int K, int N) {
 // [split_k][M][N] to `partial` and, when `reduce`, the fixed-order reduction into `out`.
 int launch_gemm(const GemmPlan& p, const uint16_t* x, const int8_t* w, const float* scale,
                 uint16_t* out, float* partial, int M, int K, int N, int to_partial, bool reduce,
-                hipStream_t s, ArgPart* amax = nullptr, bool swiglu = false) {
+                hipStream_t s, ArgPart* amax = nullptr, bool swiglu = false,
+                float* gmax = nullptr) {
   if (p.wide) {
     // SwiGLU: the same groups, each of at most ntm gate units (plus their up units)
     WideArgs wa{x, reinterpret_cast<const uint8_t*>(w), scale, out, partial, M, K, N,
-                swiglu ? p.units / 2 : p.units, p.groups, p.split_k, to_partial, amax,
+                swiglu ? p.units / 2 : p.units, p.groups, p.split_k, to_partial, amax, gmax,
                 swiglu ? 1 : 0};
     const int nwg = ((p.groups * p.split_k + 7) / 8) * 8;  // multiple of 8 for the XCD map
     const dim3 grid(nwg, p.passes);
@@ -781,7 +813,7 @@ int launch_gemm(const GemmPlan& p, const uint16_t* x, const int8_t* w, const flo
     }
   } else {
     GemmArgs ga{x, reinterpret_cast<const uint8_t*>(w), scale, out, partial, M, K, N, p.split_k,
-                to_partial, amax};
+                to_partial, amax, gmax};
     const dim3 grid((N + NT - 1) / NT, p.split_k, p.passes);
     switch (p.mt) {
       case 1: hipLaunchKernelGGL(fp8_gemm_kernel<1>, grid, dim3(NWAVES * 64), 0, s, ga); break;
@@ -888,4 +920,20 @@ extern "C" int npn_fp8_matmul_argmax(const uint16_t* x, const int8_t* w, const f
   const GemmPlan p = plan(M, K, N, true);
   return launch_gemm(p, x, w, scale, nullptr, nullptr, M, K, N, 0, false,
                      static_cast<hipStream_t>(stream), static_cast<ArgPart*>(parts));
+}
+
+// out = bf16((x . w) * scale) and, per (row, column group) of the argmax plan
+// (npn_fp8_matmul_argmax_groups groups), the max of the row's bf16 outputs in the group with
+// NaN ignored (-inf if none): the row maxima the rejection-sampling passes would otherwise
+// read the logits for. The plan never splits K, so out equals npn_fp8_matmul's whenever
+// that plan does not split either (true for vocabulary-wide N).
+extern "C" int npn_fp8_matmul_rowmax(const uint16_t* x, const int8_t* w, const float* scale,
+                                     uint16_t* out, float* gmax, int M, int K, int N,
+                                     void* stream) {
+  NPN_REQUIRE(x && w && scale && out && gmax, NPN_ERR_NULL);
+  NPN_REQUIRE(shape_ok(M, K, N), NPN_ERR_SHAPE);
+  NPN_REQUIRE(NPN_ALIGNED16(x) && NPN_ALIGNED16(w) && NPN_ALIGNED16(out), NPN_ERR_ALIGN);
+  const GemmPlan p = plan(M, K, N, true);
+  return launch_gemm(p, x, w, scale, out, nullptr, M, K, N, 0, false,
+                     static_cast<hipStream_t>(stream), nullptr, false, gmax);
 }

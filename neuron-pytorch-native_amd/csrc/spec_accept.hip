@@ -168,6 +168,42 @@ __device__ __forceinline__ void visit_chunk(const float* src, int v0, int V, boo
   }
 }
 
+// The same over a bf16 row (the LM head's logits): with vec (row 16-byte aligned, V % 8 == 0)
+// the thread reads PER_T/8 16-byte pieces of 8 entries at v0 + 8 * (j * THREADS + tid).
+template <typename F>
+__device__ __forceinline__ void visit_chunk(const uint16_t* src, int v0, int V, bool vec, F f) {
+  auto unpack = [&](int v, uint4 x) {
+    const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      f(v + 2 * k, npn::bf16_to_f32(w[k] & 0xFFFFu));
+      f(v + 2 * k + 1, npn::bf16_to_f32(w[k] >> 16));
+    }
+  };
+  if (vec && v0 + CHK <= V) {
+    uint4 x[PER_T / 8];
+#pragma unroll
+    for (int j = 0; j < PER_T / 8; ++j)
+      x[j] = *reinterpret_cast<const uint4*>(src + v0 + 8 * (j * THREADS + (int)threadIdx.x));
+#pragma unroll
+    for (int j = 0; j < PER_T / 8; ++j) unpack(v0 + 8 * (j * THREADS + (int)threadIdx.x), x[j]);
+  } else if (vec) {
+#pragma unroll
+    for (int j = 0; j < PER_T / 8; ++j) {
+      const int v = v0 + 8 * (j * THREADS + (int)threadIdx.x);
+      if (v < V) unpack(v, *reinterpret_cast<const uint4*>(src + v));
+    }
+  } else {
+    for (int j = 0; j < PER_T; ++j) {
+      const int v = v0 + j * THREADS + (int)threadIdx.x;
+      if (v < V) f(v, npn::bf16_to_f32(src[v]));
+    }
+  }
+}
+
+__device__ __forceinline__ float elem(const float* p, int v) { return p[v]; }
+__device__ __forceinline__ float elem(const uint16_t* p, int v) { return npn::bf16_to_f32(p[v]); }
+
 // ---- greedy ------------------------------------------------------------------------------
 // (val, idx) order: NaN above every number (first NaN wins), then larger value, then
 // smaller index. A total order, so any merge order gives the same winner.
@@ -293,7 +329,7 @@ __global__ __launch_bounds__(1024) void greedy_accept_parts_kernel(
 
 // ---- rejection sampling ------------------------------------------------------------------
 struct RejArgs {
-  const float* target;   // [B][K+1][V]
+  const void* target;    // [B][K+1][V] fp32, or bf16 (the LM head's logits)
   const float* draft;    // [B][K][V]
   const int64_t* draft_ids;
   const float* u_accept;
@@ -312,11 +348,13 @@ struct RejArgs {
   uint64_t* dec_z;    // [B][2]        Zp, Zq of the sampling rows
   float* dec_m;       // [B][2]        row maxima of the sampling rows (scaled logits)
   u128* cmass;        // [B][nchm]
+  const float* tgmax; // or null: [B*(K+1)][ngmax] group maxima of the target rows (NaN ignored)
+  int ngmax;
 };
 
-__device__ __forceinline__ const float* row_ptr(const RejArgs& a, int row) {
-  const int nt = a.B * (a.K + 1);
-  return row < nt ? a.target + (size_t)row * a.V : a.draft + (size_t)(row - nt) * a.V;
+template <typename TT>
+__device__ __forceinline__ const TT* target_row(const RejArgs& a, int row) {
+  return static_cast<const TT*>(a.target) + (size_t)row * a.V;
 }
 
 // Draft token whose E this row reports, or -1 (bonus rows).
@@ -338,8 +376,9 @@ __device__ __forceinline__ int row_token(const RejArgs& a, int row) {
 
 // Chunk c of a row: its max scaled logit into the row's chunk maxima (and, from chunk 0,
 // a zero into the row's Z, which the sum pass adds into in a later launch).
-__device__ __forceinline__ void max_chunk(const RejArgs& a, int row, int c, float* sh) {
-  const float* src = row_ptr(a, row);
+template <typename E>
+__device__ __forceinline__ void max_chunk(const RejArgs& a, const E* src, int row, int c,
+                                          float* sh) {
   const int v0 = c * CHK;
   float m = -INFINITY;
   visit_chunk(src, v0, a.V, a.vec4, [&](int, float x) { m = fmaxf(m, scaled(x, a.inv_temp)); });
@@ -360,9 +399,9 @@ __device__ __forceinline__ float row_max(const RejArgs& a, int row) {
 // the chunks does not matter), the row max from chunk 0 and E at the draft token from the
 // chunk that holds it. kUnitTemp skips the multiply by inv_temp == 1 (x * 1 == x, NaN
 // stays NaN).
-template <bool kUnitTemp>
-__device__ __forceinline__ void sum_chunk(const RejArgs& a, int row, int c, uint64_t* sh) {
-  const float* src = row_ptr(a, row);
+template <bool kUnitTemp, typename E>
+__device__ __forceinline__ void sum_chunk(const RejArgs& a, const E* src, int row, int c,
+                                          uint64_t* sh) {
   const float m = row_max(a, row);
   const float it = a.inv_temp;
   const int v0 = c * CHK;
@@ -374,23 +413,53 @@ __device__ __forceinline__ void sum_chunk(const RejArgs& a, int row, int c, uint
     atomicAdd(reinterpret_cast<unsigned long long*>(a.zrow + row), (unsigned long long)z);
     if (c == 0) a.mrow[row] = m;
     const int x = row_token(a, row);
-    if (x >= v0 && x < v0 + CHK) a.ex[row] = expfix(scaled(src[x], it) - m);
+    if (x >= v0 && x < v0 + CHK) a.ex[row] = expfix(scaled(elem(src, x), it) - m);
   }
 }
 
 // The logit passes: chunk maxima of every row, then E sums. The sum pass runs its rows and
 // chunks last-first, the reverse of the max pass's dispatch order, so the first chunks it
 // re-reads are the ones read last.
-__global__ __launch_bounds__(THREADS) void rej_max_kernel(RejArgs a) {
-  __shared__ float sh[THREADS / 64];
-  max_chunk(a, (int)blockIdx.y, (int)blockIdx.x, sh);
+// With group maxima of the target rows (the LM head's epilogue), a target row's max is the
+// max of its groups, scaled: for inv_temp > 0, scaled(max t) == max scaled(t) (rounding is
+// monotone), so the value is the one the max pass would find, without reading the row.
+__device__ __forceinline__ void max_from_groups(const RejArgs& a, int row, int c, float* sh) {
+  if (c != 0) {
+    if (threadIdx.x == 0) a.rmax[(size_t)row * a.nch + c] = -INFINITY;
+    return;
+  }
+  float m = -INFINITY;
+  for (int g = (int)threadIdx.x; g < a.ngmax; g += THREADS)
+    m = fmaxf(m, a.tgmax[(size_t)row * a.ngmax + g]);
+  m = block_max(m, sh);
+  if (threadIdx.x == 0) {
+    a.rmax[(size_t)row * a.nch] = scaled(m, a.inv_temp);
+    a.zrow[row] = 0;
+  }
 }
 
-template <bool kUnitTemp>
+template <typename TT>
+__global__ __launch_bounds__(THREADS) void rej_max_kernel(RejArgs a) {
+  __shared__ float sh[THREADS / 64];
+  const int row = (int)blockIdx.y, c = (int)blockIdx.x;
+  const int nt = a.B * (a.K + 1);
+  if (row >= nt)
+    max_chunk(a, a.draft + (size_t)(row - nt) * a.V, row, c, sh);
+  else if (a.tgmax != nullptr)
+    max_from_groups(a, row, c, sh);
+  else
+    max_chunk(a, target_row<TT>(a, row), row, c, sh);
+}
+
+template <bool kUnitTemp, typename TT>
 __global__ __launch_bounds__(THREADS) void rej_sum_kernel(RejArgs a) {
   __shared__ uint64_t sh[THREADS / 64];
-  sum_chunk<kUnitTemp>(a, (int)(gridDim.y - 1 - blockIdx.y), (int)(gridDim.x - 1 - blockIdx.x),
-                       sh);
+  const int row = (int)(gridDim.y - 1 - blockIdx.y), c = (int)(gridDim.x - 1 - blockIdx.x);
+  const int nt = a.B * (a.K + 1);
+  if (row >= nt)
+    sum_chunk<kUnitTemp>(a, a.draft + (size_t)(row - nt) * a.V, row, c, sh);
+  else
+    sum_chunk<kUnitTemp>(a, target_row<TT>(a, row), row, c, sh);
 }
 
 // One wave per sequence: lane i < K runs the accept test of draft position i (all tests at
@@ -425,19 +494,21 @@ __global__ __launch_bounds__(64) void rej_decide_kernel(RejArgs a) {
 }
 
 // Sampling weight of vocabulary entry v for sequence b (residual or bonus).
+template <typename TT>
 struct SampleRow {
-  const float* p;
+  const TT* p;
   const float* q;  // nullptr for the bonus row
   float mp, mq;
   uint64_t zp, zq;
 };
 
-__device__ __forceinline__ SampleRow sample_row(const RejArgs& a, int b) {
+template <typename TT>
+__device__ __forceinline__ SampleRow<TT> sample_row(const RejArgs& a, int b) {
   const int K = a.K, T = K + 1;
   const int acc = a.dec_row[b];
-  SampleRow s;
+  SampleRow<TT> s;
   const int rt = b * T + acc;
-  s.p = a.target + (size_t)rt * a.V;
+  s.p = target_row<TT>(a, rt);
   s.mp = a.dec_m[2 * b];
   s.zp = a.dec_z[2 * b];
   s.zq = a.dec_z[2 * b + 1];
@@ -451,7 +522,8 @@ __device__ __forceinline__ SampleRow sample_row(const RejArgs& a, int b) {
   return s;
 }
 
-__device__ __forceinline__ u128 weight_of(const SampleRow& s, float pv, float qv,
+template <typename TT>
+__device__ __forceinline__ u128 weight_of(const SampleRow<TT>& s, float pv, float qv,
                                           float inv_temp) {
   const uint32_t ep = expfix(scaled(pv, inv_temp) - s.mp);
   if (s.q == nullptr) return ep;
@@ -468,13 +540,32 @@ struct RunVals {
   float p[PER_M], q[PER_M];
 };
 
-__device__ __forceinline__ RunVals load_run(const RejArgs& a, const SampleRow& s, int v0) {
+__device__ __forceinline__ void load_p(const float* p, int v0, float (&dst)[PER_M]) {
+#pragma unroll
+  for (int j = 0; j < PER_M; j += 4) {
+    const float4 pv = *reinterpret_cast<const float4*>(p + v0 + j);
+    dst[j] = pv.x; dst[j + 1] = pv.y; dst[j + 2] = pv.z; dst[j + 3] = pv.w;
+  }
+}
+
+__device__ __forceinline__ void load_p(const uint16_t* p, int v0, float (&dst)[PER_M]) {
+  static_assert(PER_M == 8, "one 16-byte piece of bf16 per run");
+  const uint4 x = *reinterpret_cast<const uint4*>(p + v0);
+  const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    dst[2 * k] = npn::bf16_to_f32(w[k] & 0xFFFFu);
+    dst[2 * k + 1] = npn::bf16_to_f32(w[k] >> 16);
+  }
+}
+
+template <typename TT>
+__device__ __forceinline__ RunVals load_run(const RejArgs& a, const SampleRow<TT>& s, int v0) {
   RunVals r;
   if (a.vec4 && v0 + PER_M <= a.V) {
+    load_p(s.p, v0, r.p);
 #pragma unroll
     for (int j = 0; j < PER_M; j += 4) {
-      const float4 pv = *reinterpret_cast<const float4*>(s.p + v0 + j);
-      r.p[j] = pv.x; r.p[j + 1] = pv.y; r.p[j + 2] = pv.z; r.p[j + 3] = pv.w;
       if (s.q != nullptr) {
         const float4 qv = *reinterpret_cast<const float4*>(s.q + v0 + j);
         r.q[j] = qv.x; r.q[j + 1] = qv.y; r.q[j + 2] = qv.z; r.q[j + 3] = qv.w;
@@ -486,16 +577,17 @@ __device__ __forceinline__ RunVals load_run(const RejArgs& a, const SampleRow& s
 #pragma unroll
     for (int j = 0; j < PER_M; ++j) {
       const int v = v0 + j;
-      r.p[j] = v < a.V ? s.p[v] : -INFINITY;
+      r.p[j] = v < a.V ? elem(s.p, v) : -INFINITY;
       r.q[j] = (v < a.V && s.q != nullptr) ? s.q[v] : 0.f;
     }
   }
   return r;
 }
 
+template <typename TT>
 __global__ __launch_bounds__(THREADS) void rej_mass_kernel(RejArgs a) {
   const int b = blockIdx.y, c = blockIdx.x;
-  const SampleRow s = sample_row(a, b);
+  const SampleRow<TT> s = sample_row<TT>(a, b);
   const int v0 = c * MCHK + (int)threadIdx.x * PER_M;
   u128 m = 0;
   if (v0 < a.V) {
@@ -541,9 +633,10 @@ __device__ __forceinline__ u128 wave_incl_scan_u128(u128 v) {
 // sums its run of PER_M consecutive entries of that chunk (values held in registers), a
 // block-wide exclusive scan of the runs gives every thread its starting prefix, and the
 // thread whose run crosses reports the first crossing entry (atomicMin over the block).
+template <typename TT>
 __global__ __launch_bounds__(THREADS) void rej_pick_kernel(RejArgs a) {
   const int b = blockIdx.x;
-  const SampleRow s = sample_row(a, b);
+  const SampleRow<TT> s = sample_row<TT>(a, b);
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   __shared__ int s_chunk;
   __shared__ u128 s_before;
@@ -592,8 +685,10 @@ __global__ __launch_bounds__(THREADS) void rej_pick_kernel(RejArgs a) {
     // maximum and ties going to the lowest index (the order of argmax_chunk_kernel).
     float bv = -INFINITY;
     int bi = 0x7FFFFFFF;
-    for (int v = (int)threadIdx.x; v < a.V; v += THREADS)
-      if (beats(s.p[v], v, bv, bi)) { bv = s.p[v]; bi = v; }
+    for (int v = (int)threadIdx.x; v < a.V; v += THREADS) {
+      const float pv = elem(s.p, v);
+      if (beats(pv, v, bv, bi)) { bv = pv; bi = v; }
+    }
     for (int off = 32; off > 0; off >>= 1) {
       const float ov = __shfl_xor(bv, off, 64);
       const int oi = __shfl_xor(bi, off, 64);
@@ -719,28 +814,35 @@ int rejection_args_ok(const float* target_logits, const float* draft_logits,
 
 // The five rejection kernels on `stream`, with the workspace at `ws` (layout(B, K, V).total
 // bytes, 16-byte aligned, checked by the caller).
-int rejection_launch(const float* target_logits, const float* draft_logits,
+// TT is the target rows' element type: float, or bf16 bits (uint16_t) for the LM-head form,
+// which passes the target rows' group maxima (tgmax, ngmax per row) so the max pass skips them.
+template <typename TT>
+int rejection_launch(const TT* target_logits, const float* draft_logits,
                      const int64_t* draft_ids, const float* u_accept, const float* u_sample,
                      float inv_temperature, int32_t* accepted, int64_t* out_ids, int B, int K,
-                     int V, uint8_t* ws, hipStream_t s) {
+                     int V, uint8_t* ws, hipStream_t s, const float* tgmax = nullptr,
+                     int ngmax = 0) {
   const WsLayout l = layout(B, K, V);
   const int nch = (V + CHK - 1) / CHK;
-  const bool vec4 = V % 4 == 0 && NPN_ALIGNED16(target_logits) && NPN_ALIGNED16(draft_logits);
+  // 16-byte pieces of whole rows: V % 8 for bf16 target rows (and V % 4 for the fp32 ones)
+  const bool vec4 = V % (sizeof(TT) == 2 ? 8 : 4) == 0 && NPN_ALIGNED16(target_logits) &&
+                    NPN_ALIGNED16(draft_logits);
   RejArgs a{target_logits, draft_logits, draft_ids, u_accept, u_sample, inv_temperature,
             accepted, out_ids, B, K, V, nch, (V + MCHK - 1) / MCHK, vec4,
             reinterpret_cast<uint64_t*>(ws + l.zrow), reinterpret_cast<float*>(ws + l.mrow),
             reinterpret_cast<uint32_t*>(ws + l.ex), reinterpret_cast<float*>(ws + l.rmax),
             reinterpret_cast<int32_t*>(ws + l.dec_row), reinterpret_cast<uint64_t*>(ws + l.dec_z),
-            reinterpret_cast<float*>(ws + l.dec_m), reinterpret_cast<u128*>(ws + l.cmass)};
+            reinterpret_cast<float*>(ws + l.dec_m), reinterpret_cast<u128*>(ws + l.cmass),
+            tgmax, ngmax};
   const int rows = B * (2 * K + 1);
-  hipLaunchKernelGGL(rej_max_kernel, dim3(nch, rows), dim3(THREADS), 0, s, a);
+  hipLaunchKernelGGL(rej_max_kernel<TT>, dim3(nch, rows), dim3(THREADS), 0, s, a);
   if (inv_temperature == 1.0f)
-    hipLaunchKernelGGL(rej_sum_kernel<true>, dim3(nch, rows), dim3(THREADS), 0, s, a);
+    hipLaunchKernelGGL((rej_sum_kernel<true, TT>), dim3(nch, rows), dim3(THREADS), 0, s, a);
   else
-    hipLaunchKernelGGL(rej_sum_kernel<false>, dim3(nch, rows), dim3(THREADS), 0, s, a);
+    hipLaunchKernelGGL((rej_sum_kernel<false, TT>), dim3(nch, rows), dim3(THREADS), 0, s, a);
   hipLaunchKernelGGL(rej_decide_kernel, dim3(B), dim3(64), 0, s, a);
-  hipLaunchKernelGGL(rej_mass_kernel, dim3(a.nchm, B), dim3(THREADS), 0, s, a);
-  hipLaunchKernelGGL(rej_pick_kernel, dim3(B), dim3(THREADS), 0, s, a);
+  hipLaunchKernelGGL(rej_mass_kernel<TT>, dim3(a.nchm, B), dim3(THREADS), 0, s, a);
+  hipLaunchKernelGGL(rej_pick_kernel<TT>, dim3(B), dim3(THREADS), 0, s, a);
   return npn_launch_status();
 }
 
@@ -836,4 +938,51 @@ extern "C" int npn_argmax_parts(const void* parts, int nparts, int64_t* ids, flo
                      static_cast<hipStream_t>(stream), static_cast<const ArgPart*>(parts), nparts,
                      ids, values, M);
   return npn_launch_status();
+}
+
+// ---- rejection sampling straight from the LM head --------------------------------------------
+// The LM head's GEMM writes the target logits in bf16 and, in its epilogue, each row's maxima
+// per column group; the rejection passes then read the target rows in bf16 (half the bytes)
+// and skip them in the max pass. The decisions equal npn_accept_rejection's on the same
+// logits cast to fp32 (every step of the contract sees the same values).
+namespace {
+
+size_t lm_head_gmax_bytes(int M, int G) { return ((size_t)M * G * sizeof(float) + 255) & ~(size_t)255; }
+
+}  // namespace
+
+extern "C" size_t npn_accept_rejection_lm_head_workspace_size(int B, int K, int H, int V) {
+  if (!shape_ok(B, K, V) || V > kRejMaxV) return 0;
+  const int G = npn_fp8_matmul_argmax_groups(B * (K + 1), H, V);
+  if (G <= 0) return 0;
+  return layout(B, K, V).total + lm_head_gmax_bytes(B * (K + 1), G);
+}
+
+extern "C" int npn_accept_rejection_lm_head(const uint16_t* hidden, const int8_t* lm_head_w,
+                                            const float* lm_head_scale,
+                                            const float* draft_logits, const int64_t* draft_ids,
+                                            const float* u_accept, const float* u_sample,
+                                            float inv_temperature, uint16_t* target_logits,
+                                            int32_t* accepted, int64_t* out_ids, int B, int K,
+                                            int H, int V, void* workspace,
+                                            size_t workspace_bytes, void* stream) {
+  NPN_REQUIRE(hidden && lm_head_w && lm_head_scale, NPN_ERR_NULL);
+  const int st = rejection_args_ok(reinterpret_cast<const float*>(target_logits), draft_logits,
+                                   draft_ids, u_accept, u_sample, inv_temperature, accepted,
+                                   out_ids, B, K, V);
+  if (st != NPN_OK) return st;
+  const int M = B * (K + 1);
+  const int G = npn_fp8_matmul_argmax_groups(M, H, V);
+  NPN_REQUIRE(G > 0, NPN_ERR_SHAPE);
+  const size_t need = npn_accept_rejection_lm_head_workspace_size(B, K, H, V);
+  NPN_REQUIRE(workspace != nullptr && workspace_bytes >= need, NPN_ERR_WORKSPACE);
+  NPN_REQUIRE(NPN_ALIGNED16(workspace), NPN_ERR_ALIGN);
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  float* gmax = reinterpret_cast<float*>(ws + layout(B, K, V).total);
+  const int gst = npn_fp8_matmul_rowmax(hidden, lm_head_w, lm_head_scale, target_logits, gmax, M,
+                                        H, V, stream);
+  if (gst != NPN_OK) return gst;
+  return rejection_launch(static_cast<const uint16_t*>(target_logits), draft_logits, draft_ids,
+                          u_accept, u_sample, inv_temperature, accepted, out_ids, B, K, V, ws,
+                          static_cast<hipStream_t>(stream), gmax, G);
 }

@@ -52,6 +52,9 @@ SIGNATURES = {
     "npn_accept_greedy_parts": (_I, [_P, _I] + [_P] * 3 + [_I, _I, _P]),
     "npn_fp8_matmul_swiglu_workspace_size": (_Z, [_I] * 3),
     "npn_fp8_matmul_swiglu": (_I, [_P] * 4 + [_I] * 3 + [_P, _Z, _P]),
+    "npn_fp8_matmul_rowmax": (_I, [_P] * 5 + [_I] * 3 + [_P]),
+    "npn_accept_rejection_lm_head_workspace_size": (_Z, [_I] * 4),
+    "npn_accept_rejection_lm_head": (_I, [_P] * 7 + [_F] + [_P] * 3 + [_I] * 4 + [_P, _Z, _P]),
     "npn_deltanet_chunked_workspace_size": (_Z, [_I, _I]),
     "npn_deltanet_chunked_prefill": (_I, [_P] * 8 + [_I, _I, _P, _Z, _P]),
 }

@@ -9,6 +9,11 @@ contrib/qwen3.6-27b/static_decode.py:1313).
                          inv_temperature: float = 1.0)
       -> (accepted [B] int32, out_ids [B, K+1] int64)
 
+  spec::accept_rejection_lm_head(hidden [B*(K+1), H] bf16, lm_head_w [H, V] fp8 bytes,
+                                 lm_head_scale [V] f32, draft_logits, draft_ids, u_accept,
+                                 u_sample, inv_temperature)
+      -> (accepted, out_ids, target_logits [B, K+1, V] bf16)
+
 accepted[b] is the number of accepted drafts (0..K); out_ids[b] holds those drafts,
 then the correction (or bonus) token, then -1. Rejection sampling follows Leviathan
 et al. 2023 (Alg. 1) under the library's integer softmax contract, so its decisions
@@ -121,3 +126,51 @@ def _(hidden, lm_head_w, lm_head_scale, draft_ids):
     B, K = draft_ids.shape
     return (hidden.new_empty((B,), dtype=torch.int32),
             hidden.new_empty((B, K + 1), dtype=torch.int64))
+
+
+@torch.library.custom_op("spec::accept_rejection_lm_head", mutates_args=(), device_types="cuda")
+def accept_rejection_lm_head(hidden: torch.Tensor, lm_head_w: torch.Tensor,
+                             lm_head_scale: torch.Tensor, draft_logits: torch.Tensor,
+                             draft_ids: torch.Tensor, u_accept: torch.Tensor,
+                             u_sample: torch.Tensor, inv_temperature: float = 1.0
+                             ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """New op: rejection sampling with the target logits made by the LM head in the same
+    call: hidden [B*(K+1), H] bf16 (row b*(K+1) + t), lm_head_w [H, V] e4m3fn bytes,
+    lm_head_scale [V] f32 -> (accepted [B] int32, out_ids [B, K+1] int64, target_logits
+    [B, K+1, V] bf16). The GEMM's epilogue also gives each row's maxima per column group,
+    so the sampling passes read the target rows once less and in bf16. Equal, bit for bit,
+    to accept_rejection(fp8::matmul(hidden, w, scale).float().view(B, K+1, V), ...) wherever
+    fp8::matmul's plan does not split K (vocabulary-wide V)."""
+    B, K, V = draft_logits.shape
+    T = K + 1
+    require(hidden, "hidden", torch.bfloat16)
+    if hidden.dim() != 2 or hidden.shape[0] != B * T:
+        raise RuntimeError(f"hidden must be [B*(K+1), H] = [{B * T}, H], got {tuple(hidden.shape)}")
+    H = hidden.shape[1]
+    require(lm_head_w, "lm_head_w", torch.int8, shape=(H, V))
+    require(lm_head_scale, "lm_head_scale", torch.float32, numel=V)
+    require(draft_logits, "draft_logits", torch.float32, shape=(B, K, V))
+    require(draft_ids, "draft_ids", torch.int64, shape=(B, K))
+    require(u_accept, "u_accept", torch.float32, shape=(B, K))
+    require(u_sample, "u_sample", torch.float32, numel=B)
+    if not inv_temperature > 0.0:
+        raise ValueError("inv_temperature must be > 0")
+    n = query("npn_accept_rejection_lm_head_workspace_size", B, K, H, V)
+    if n == 0:
+        raise RuntimeError(f"unsupported sizes B={B} K={K} H={H} V={V}")
+    ws = torch.empty(n, dtype=torch.uint8, device=hidden.device)
+    logits = torch.empty((B, T, V), dtype=torch.bfloat16, device=hidden.device)
+    accepted = torch.empty(B, dtype=torch.int32, device=hidden.device)
+    out_ids = torch.empty((B, T), dtype=torch.int64, device=hidden.device)
+    call("npn_accept_rejection_lm_head", hidden, lm_head_w, lm_head_scale, draft_logits,
+         draft_ids, u_accept, u_sample, float(inv_temperature), logits, accepted, out_ids, B, K,
+         H, V, ws, ws.numel(), stream_of(hidden))
+    return accepted, out_ids, logits
+
+
+@accept_rejection_lm_head.register_fake
+def _(hidden, lm_head_w, lm_head_scale, draft_logits, draft_ids, u_accept, u_sample,
+      inv_temperature=1.0):
+    B, K, V = draft_logits.shape
+    return (hidden.new_empty(B, dtype=torch.int32), hidden.new_empty((B, K + 1), dtype=torch.int64),
+            hidden.new_empty((B, K + 1, V), dtype=torch.bfloat16))

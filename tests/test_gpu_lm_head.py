@@ -10,7 +10,13 @@ Bars:
   - against the oracle (fp64 product, bf16 rounding, first-index argmax) at a small size: the
     chosen logit is within one bf16 ulp of the oracle's maximum, and the ids agree wherever
     the oracle's top two are more than two ulps apart;
-  - accept_greedy_fused == accept_greedy over the materialised logits, bit-exact.
+  - accept_greedy_fused == accept_greedy over the materialised logits, bit-exact;
+  - the row-max epilogue (npn_fp8_matmul_rowmax): its logits bit-identical to fp8::matmul's,
+    and the max over its row-group maxima equal to each row's max with NaN ignored, including
+    rows made ±inf and NaN by an infinite activation;
+  - accept_rejection_lm_head == accept_rejection over the fp32 cast of the same logits,
+    bit-exact (accepted lengths, ids and the logits it returns), at the 27B verify batch
+    (M = 256, wide kernel) and a small one (M = 64, narrow kernel), temperature 1 and 1/0.7.
 """
 import numpy as np
 import pytest
@@ -86,3 +92,61 @@ def test_accept_greedy_fused(ops):
     torch.cuda.synchronize()
     assert torch.equal(acc_f, acc_r) and torch.equal(ids_f, ids_r)
     assert acc_f.tolist() == [min(b, K) for b in range(B)]
+
+
+def _rowmax(x, w, sc):
+    from npn_native import call, query, stream_of
+    M, K = x.shape
+    N = w.shape[1]
+    G = query("npn_fp8_matmul_argmax_groups", M, K, N)
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    gmax = torch.empty((M, G), dtype=torch.float32, device=x.device)
+    call("npn_fp8_matmul_rowmax", x, w, sc, out, gmax, M, K, N, stream_of(x))
+    return out, gmax
+
+
+@pytest.mark.parametrize("M,K,N", [(256, 5120, 151936), (40, 5120, 248320), (13, 128, 1024)])
+def test_matmul_rowmax(ops, M, K, N):
+    """Shapes where fp8::matmul's own plan does not split K either (so its sums are the
+    same); the host plan tests pin which shapes split."""
+    g = torch.Generator(device="cuda").manual_seed(M + 3 * N)
+    x = torch.randn(M, K, generator=g, device="cuda").to(torch.bfloat16)
+    w, sc = _gpu_weights(K, N, M + 7)
+    # row 0: x[0, 0] = +inf, with W row 0 zero on columns 0..99 -> those logits NaN (inf * 0),
+    # the others +-inf; row 1: -inf the same way
+    x[0, 0] = float("inf")
+    x[1, 0] = float("-inf")
+    w[0, :100] = 0
+    out, gmax = _rowmax(x, w, sc)
+    ref = ops.fp8.matmul(x, w, sc)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+    rf = ref.float()
+    want = torch.where(torch.isnan(rf), torch.full_like(rf, float("-inf")), rf).amax(1)
+    assert torch.equal(gmax.amax(1), want)
+    assert torch.isnan(rf[0, :100]).all() and want[0] == float("inf")
+
+
+@pytest.mark.parametrize("B,V,inv_t", [(32, 151936, 1.0), (8, 151936, 1.0 / 0.7),
+                                       (32, 248320, 1.0)])
+def test_accept_rejection_lm_head(ops, B, V, inv_t):
+    K, H = 7, 5120
+    T = K + 1
+    g = torch.Generator(device="cuda").manual_seed(B + V)
+    hid = torch.randn(B * T, H, generator=g, device="cuda").to(torch.bfloat16)
+    w, sc = _gpu_weights(H, V, B + 11)
+    logits = ops.fp8.matmul(hid, w, sc).float().view(B, T, V)
+    draft = 0.8 * logits[:, :K] + 0.6 * torch.randn(B, K, V, generator=g, device="cuda")
+    ids = torch.multinomial(torch.softmax(draft * inv_t, -1).reshape(B * K, V), 1,
+                            generator=g).reshape(B, K)
+    u = torch.rand(B, K, generator=g, device="cuda")
+    us = torch.rand(B, generator=g, device="cuda")
+    acc_f, ids_f, lg = ops.spec.accept_rejection_lm_head(hid, w, sc, draft.contiguous(), ids, u,
+                                                         us, inv_t)
+    acc_r, ids_r = ops.spec.accept_rejection(logits.contiguous(), draft.contiguous(), ids, u, us,
+                                             inv_t)
+    torch.cuda.synchronize()
+    assert torch.equal(lg.float(), logits)
+    assert torch.equal(acc_f, acc_r), (acc_f.tolist(), acc_r.tolist())
+    assert torch.equal(ids_f, ids_r)
+    assert 0 < acc_f.float().mean() < K  # neither all accepted nor all rejected

@@ -5,15 +5,14 @@
 // to [K, N] (N contiguous), bf16 activations, fp32 accumulation, per-output-channel scale
 // applied to the fp32 sum, then a bf16 cast.
 //
-// Two kernels. Up to 64 rows per pass (the narrow kernel, HBM-bound) the weights go straight
-// from HBM into registers: v_mfma_f32_16x16x32_bf16's B operand wants 8 consecutive k of one
-// column per lane, but [K, N] stores a column with stride N, so each lane loads 16 adjacent
-// columns from each of its 8 k rows (256-byte runs per row across the 16 lanes of a group),
-// transposes each 8x4 byte quarter of that block in registers with v_perm_b32 and dequantises
-// each column's 8 bytes to bf16 with v_cvt_scalef32_pk_bf16_fp8 (exact: every e4m3fn value is
-// a bf16 value). Above 64 rows (the wide kernel, MFMA-bound) a workgroup stages W tiles in LDS
-// with direct global-to-LDS loads and reads the B operands back transposed
-// (ds_read_b64_tr_b8); details with each kernel below.
+// Two kernels, both staging W tiles in LDS with direct global-to-LDS loads.
+// v_mfma_f32_16x16x32_bf16's B operand wants 8 consecutive k of one column per lane, but
+// [K, N] stores a column with stride N. Up to 64 rows (the narrow kernel, HBM-bound) each lane
+// reads 4 to 16 adjacent columns from each of its 8 k rows out of LDS, transposes each 8x4
+// byte quarter in registers with v_perm_b32 and dequantises each column's 8 bytes to bf16
+// with v_cvt_scalef32_pk_bf16_fp8 (exact: every e4m3fn value is a bf16 value). Above 64 rows
+// (the wide kernel, MFMA-bound) the B operands are read back transposed (ds_read_b64_tr_b8)
+// and converted the same way; details with each kernel below.
 #include "npn_common.h"
 
 namespace {
@@ -97,145 +96,153 @@ struct GemmArgs {
   uint16_t* out;     // used when split_k == 1 and !to_partial
   float* partial;    // [split_k][M][N] fp32, unscaled, when split_k > 1 or to_partial
   int M, K, N, split_k, to_partial;
-  ArgPart* amax;     // row argmax partials [M][ceil(N / NT)] instead of out (split_k == 1)
-  float* gmax;       // with out: per-(row, tile) max of the bf16 outputs, NaN ignored
+  ArgPart* amax;     // row argmax partials [M][column groups] instead of out (split_k == 1)
+  float* gmax;       // with out: per-(row, column group) max of the bf16 outputs, NaN ignored
 };
 
 // ---------------------------------------------------------------------------------------
-// Narrow kernel for M <= 64 rows per pass (HBM-bound: each weight byte feeds 2*M flops).
+// Narrow kernel for M <= 64 rows (HBM-bound: each weight byte feeds 2*M flops).
 // The weights stream once from HBM, so what matters is how the reads meet the DRAM: consecutive
 // rows of W are N bytes apart, and a W row read in pieces of 64 contiguous bytes streams at
 // about 2.4 TB/s on MI355X, in pieces of 128 bytes at 4.1 TB/s and of 256 bytes at 4.8 TB/s,
 // whatever the bytes per lane (measured with a pure-load kernel, 178 MB of W, 544
-// workgroups). So a workgroup owns a 256-column tile: lane (i, G) loads 16 bytes (columns
-// n0 + 16 i .. + 15) from each of its 8 k rows 8 G + j, and each quarter of those bytes is
-// transposed in registers and dequantised into the B operands of 4 MFMAs (column ct of
-// quarter q feeds MFMA 4 q + ct, whose output column i is n0 + 16 i + 4 q + ct).
-// A workgroup is 4 waves = RB row blocks of 16 rows x (4 / RB) k parts; waves of one k part
-// read the same W bytes (served by the CU's L1), waves of one row block add their partial sums
-// in a fixed tree through LDS. For wide N, K is also split across workgroups (split_k);
-// partials then go through an fp32 workspace and a fixed-order reduction kernel.
+// workgroups). So a workgroup owns a 256-column tile, and each k step's W tile (32 rows x
+// 256 columns, 256-byte row runs) and x rows (16 RB rows x 32 k) move HBM -> LDS by direct
+// loads (global_load_lds_dwordx4), NS stages deep: every W byte is fetched once per
+// workgroup, whatever its number of row blocks, and NS - 1 tiles are in flight. The NWV waves
+// split the tile by rows and columns with no k split: RB row blocks of 16 rows x CH = NWV / RB
+// column slices of 256 / CH columns; lane (i, G) reads CB = 16 / CH bytes (columns) from each
+// of its 8 k rows 8 G + j out of LDS, and each 4-column quarter is transposed and dequantised
+// in registers into the B operands of 4 MFMAs (column ct of quarter q feeds MFMA 4 q + ct).
+// Each wave issues the same DMA instructions for every tile (steps past the range repeat the
+// last one), so a constant vmcnt per wave names "this tile landed"; an s_barrier then
+// publishes it. For wide N, K is also split across workgroups (split_k); partials then go
+// through an fp32 workspace and a fixed-order reduction kernel.
 constexpr int NT = 256;     // columns per narrow tile
-constexpr int NWAVES = 4;   // waves per narrow workgroup
 
-template <int RB>
-__global__ __launch_bounds__(NWAVES * 64, 3) void fp8_gemm_kernel(GemmArgs a) {
-  constexpr int KP = NWAVES / RB;
-  constexpr int ROWS = 16 * RB;
+template <int RB, int NS, int NWV>
+__global__ __launch_bounds__(NWV * 64, 1) void fp8_gemm_narrow_kernel(GemmArgs a) {
+  constexpr int NTH = NWV * 64;
+  constexpr int CH = NWV / RB;               // column slices
+  constexpr int CB = 16 / CH;                // columns (bytes) per lane
+  static_assert(CB >= 4 && CB <= 16, "4 to 16 columns per lane");
+  constexpr int WST = 32 * NT;               // W stage bytes
+  constexpr int XST = 16 * RB * 64;          // x stage bytes (rows x 32 k bf16)
+  constexpr int STAGE = WST + XST;
+  constexpr int WQ = WST / 16 / NTH;         // W DMA instructions (16 bytes) per thread
+  constexpr int XW = XST / 16 / 64;          // waves that move x, one 16-byte DMA per lane
+  static_assert(WQ * 16 * NTH == WST && XW * 64 * 16 == XST && XW <= NWV,
+                "whole DMA instructions per stage");
+  __shared__ __attribute__((aligned(16))) uint8_t smem[NS * STAGE];
+
   const int n0 = blockIdx.x * NT;
   const int sk = blockIdx.y;
-  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int m_pass = blockIdx.z * 16 * RB;
+  const int tid = threadIdx.x;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int i = lane & 15, G = lane >> 4;
-  const int rb = w % RB, kp = w / RB;
-  const int m_base = blockIdx.z * ROWS + 16 * rb;
-  // This lane's 16 columns; N % 16 == 0, so they are all inside N or all past it (a last,
-  // partial tile): lanes past N read the tile's last 16 columns again and store nothing.
-  const int nc = n0 + 16 * i;
-  const bool col_ok = nc < a.N;
-  const uint8_t* wcol = a.w + (col_ok ? nc : a.N - 16);
-  // A operand row i of the row block (rows past M read row M - 1, zeroed after the load)
-  const int mrow = m_base + i;
-  const bool row_ok = mrow < a.M;
-  const uint16_t* xrow = a.x + (size_t)(row_ok ? mrow : a.M - 1) * a.K;
-
-  // k steps of this wave: split evenly over split_k * KP workers.
+  const int rb = w / CH, ch = w - rb * CH;
   const int nks = a.K / KSTEP;
-  const int worker = sk * KP + kp;
-  const int workers = a.split_k * KP;
-  const int ks_lo = (int)(((long)nks * worker) / workers);
-  const int ks_hi = (int)(((long)nks * (worker + 1)) / workers);
+  const int ks_lo = (int)(((long)nks * sk) / a.split_k);
+  const int ks_hi = (int)(((long)nks * (sk + 1)) / a.split_k);
+  const int ntile = ks_hi - ks_lo;
 
-  f32x4 acc[16];
+  // DMA of k step ks into stage st: W rows (2 x 16 bytes per thread), then x rows.
+  auto issue = [&](int ks, int st) {
+    uint8_t* ws = smem + st * STAGE;
+    uint8_t* xs = ws + WST;
+    const int k0 = ks * KSTEP;
 #pragma unroll
-  for (int c = 0; c < 16; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  // Two register slots: the W bytes and x row of step ks + 1 load while step ks computes
-  // (a wave has two steps' loads in flight; one step is about a memory round trip of
-  // compute-free waiting otherwise). The loop is unrolled by two so the slots are fixed
-  // registers, and every load is unconditional -- a step past the range repeats the last
-  // one -- so the wait before a step counts only the one batch issued after it.
-  u32x4 wd[2][8], xd[2];
-  auto load = [&](int ks, u32x4 (&dw)[8], u32x4& dx) {
-    ks = ks < ks_hi ? ks : ks_hi - 1;
-    const int k0 = ks * KSTEP + 8 * G;
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-      dw[j] = *reinterpret_cast<const u32x4*>(wcol + (size_t)(k0 + j) * a.N);
-    dx = *reinterpret_cast<const u32x4*>(xrow + k0);
-  };
-  auto compute = [&](const u32x4 (&dw)[8], const u32x4& dx) {
-    const u32x4 zero = {0u, 0u, 0u, 0u};
-    const bf16x8 aop = __builtin_bit_cast(bf16x8, row_ok ? dx : zero);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      uint32_t dq[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) dq[j] = dw[j][q];
-      bf16x8 bop[4];
-      transpose_dequant(dq, bop);
-#pragma unroll
-      for (int ct = 0; ct < 4; ++ct)
-        acc[4 * q + ct] =
-            __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop, bop[ct], acc[4 * q + ct], 0, 0, 0);
+    for (int q = 0; q < WQ; ++q) {
+      const int s = q * NTH + tid;                    // 16-byte slot of the W stage
+      const int row = s >> 4;
+      int col = n0 + 16 * (s & 15);
+      col = col < a.N ? col : a.N - 16;               // a partial last tile re-reads valid bytes
+      npn::lds_dma16(a.w + (size_t)(k0 + row) * a.N + col, ws + q * (NTH * 16) + (tid & ~63) * 16);
+    }
+    if (w < XW) {                                     // 16-byte slots, 4 per 64-byte row
+      const int s = w * 64 + lane;
+      int m = m_pass + (s >> 2);
+      m = m < a.M ? m : a.M - 1;
+      npn::lds_dma16(a.x + (size_t)m * a.K + k0 + 8 * (s & 3), xs + w * 1024);
     }
   };
-  // sched_barrier(0) keeps each batch of loads ahead of the previous step's MFMAs (the
-  // scheduler would otherwise sink them below, leaving nothing in flight at the wait).
-  if (ks_lo < ks_hi) {
-    load(ks_lo, wd[0], xd[0]);
-    for (int ks = ks_lo; ks < ks_hi; ks += 2) {
-      load(ks + 1, wd[1], xd[1]);
-      __builtin_amdgcn_sched_barrier(0);
-      compute(wd[0], xd[0]);
-      load(ks + 2, wd[0], xd[0]);
-      __builtin_amdgcn_sched_barrier(0);
-      if (ks + 1 < ks_hi) compute(wd[1], xd[1]);
-    }
-  }
 
-  // Deterministic tree over the k parts of each row block, one column quarter at a time:
-  // parts (p, p + KP/2), then (p, p + KP/4), ...
-  if constexpr (KP > 1) {
-    __shared__ __attribute__((aligned(16))) float red[(KP / 2) * RB][16 * 64];
-    auto slot_off = [&](int ct, int r) { return (4 * G + r) * 64 + 4 * i + ct; };
+  f32x4 acc[CB];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+  for (int c = 0; c < CB; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int mrow = m_pass + 16 * rb + i;              // A operand row of this lane
+  const bool row_ok = mrow < a.M;
+  const int lcol = ch * 16 * CB + CB * i;             // the lane's first column in the tile
+
+  if (ntile > 0) {
 #pragma unroll
-      for (int half = KP / 2; half >= 1; half >>= 1) {
-        if (kp >= half && kp < 2 * half) {
+    for (int p = 0; p < NS - 1; ++p) issue(ks_lo + (p < ntile ? p : ntile - 1), p);
+    for (int t = 0; t < ntile; ++t) {
+      // tiles t + 1 .. t + NS - 2 were issued after tile t: wait for the rest, then publish
+      if (w < XW)
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NS - 2) * (WQ + 1)) : "memory");
+      else
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NS - 2) * WQ) : "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      const int tn = t + NS - 1;                      // into the stage tile t - 1 used
+      issue(ks_lo + (tn < ntile ? tn : ntile - 1), tn % NS);
+      const uint8_t* ws = smem + (t % NS) * STAGE;
+      const uint8_t* xs = ws + WST;
+      const u32x4 xv = *reinterpret_cast<const u32x4*>(xs + (16 * rb + i) * 64 + 16 * G);
+      const u32x4 zero = {0u, 0u, 0u, 0u};
+      const bf16x8 aop = __builtin_bit_cast(bf16x8, row_ok ? xv : zero);
+      uint32_t d[8][CB / 4];
 #pragma unroll
-          for (int ct = 0; ct < 4; ++ct)
+      for (int j = 0; j < 8; ++j) {
+        const uint8_t* src = ws + (8 * G + j) * NT + lcol;
+        if constexpr (CB == 16) {
+          const u32x4 v = *reinterpret_cast<const u32x4*>(src);
 #pragma unroll
-            for (int r = 0; r < 4; ++r)
-              red[(kp - half) * RB + rb][slot_off(ct, r)] = acc[4 * q + ct][r];
+          for (int q = 0; q < 4; ++q) d[j][q] = v[q];
+        } else if constexpr (CB == 8) {
+          const uint2 v = *reinterpret_cast<const uint2*>(src);
+          d[j][0] = v.x;
+          d[j][1] = v.y;
+        } else {
+          d[j][0] = *reinterpret_cast<const uint32_t*>(src);
         }
-        __syncthreads();
-        if (kp < half) {
+      }
 #pragma unroll
-          for (int ct = 0; ct < 4; ++ct)
+      for (int q = 0; q < CB / 4; ++q) {
+        uint32_t dq[8];
 #pragma unroll
-            for (int r = 0; r < 4; ++r)
-              acc[4 * q + ct][r] += red[kp * RB + rb][slot_off(ct, r)];
-        }
-        __syncthreads();
+        for (int j = 0; j < 8; ++j) dq[j] = d[j][q];
+        bf16x8 bop[4];
+        transpose_dequant(dq, bop);
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct)
+          acc[4 * q + ct] =
+              __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop, bop[ct], acc[4 * q + ct], 0, 0, 0);
       }
     }
   }
-  if (kp != 0) return;
+  // the repeats issued past the range must land before the workgroup's LDS is released
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-  // Waves of k part 0 hold their row block's sums: lane (i, G) has rows m_base + 4 G + r and
-  // columns nc + c in acc[c][r].
+  // Lane (i, G) holds rows m_pass + 16 rb + 4 G + r and columns nc + c in acc[c][r]; its
+  // group for the row maxima is the (tile, column slice) pair.
+  const int nc = n0 + lcol;
+  const bool col_ok = nc < a.N;
+  const int groups = gridDim.x * CH;
+  const int grp = blockIdx.x * CH + ch;
   if (a.amax != nullptr) {
-    float sc[16];
+    float sc[CB];
 #pragma unroll
-    for (int c = 0; c < 16; ++c) sc[c] = col_ok ? a.scale[nc + c] : 0.0f;
+    for (int c = 0; c < CB; ++c) sc[c] = col_ok ? a.scale[nc + c] : 0.0f;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       float bv = -__builtin_inff();
       int bi = 0x7FFFFFFF;
       if (col_ok) {
 #pragma unroll
-        for (int c = 0; c < 16; ++c) {
+        for (int c = 0; c < CB; ++c) {
           const float v = bf16_round(acc[c][r] * sc[c]);
           if (arg_beats(v, nc + c, bv, bi)) {
             bv = v;
@@ -244,37 +251,43 @@ __global__ __launch_bounds__(NWAVES * 64, 3) void fp8_gemm_kernel(GemmArgs a) {
         }
       }
       arg_merge16(bv, bi);
-      const int m = m_base + 4 * G + r;
-      if (i == 0 && m < a.M) a.amax[(size_t)m * gridDim.x + blockIdx.x] = ArgPart{bv, bi};
+      const int m = m_pass + 16 * rb + 4 * G + r;
+      if (i == 0 && m < a.M) a.amax[(size_t)m * groups + grp] = ArgPart{bv, bi};
     }
     return;
   }
   if (a.split_k == 1 && !a.to_partial) {
-    float sc[16];
+    float sc[CB];
 #pragma unroll
-    for (int c = 0; c < 16; ++c) sc[c] = col_ok ? a.scale[nc + c] : 0.0f;
+    for (int c = 0; c < CB; ++c) sc[c] = col_ok ? a.scale[nc + c] : 0.0f;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int m = m_base + 4 * G + r;
-      uint32_t pk[8];
+      const int m = m_pass + 16 * rb + 4 * G + r;
+      uint32_t pk[CB / 2];
       float mx = -__builtin_inff();  // max of the row's bf16 outputs (fmaxf ignores NaN)
 #pragma unroll
-      for (int c = 0; c < 8; ++c) {
+      for (int c = 0; c < CB / 2; ++c) {
         const uint32_t lo = npn::f32_to_bf16(acc[2 * c][r] * sc[2 * c]);
         const uint32_t hi = npn::f32_to_bf16(acc[2 * c + 1][r] * sc[2 * c + 1]);
         pk[c] = lo | (hi << 16);
         mx = fmaxf(mx, fmaxf(npn::bf16_to_f32(lo), npn::bf16_to_f32(hi)));
       }
       if (col_ok && m < a.M) {
-        uint4* dst = reinterpret_cast<uint4*>(a.out + (size_t)m * a.N + nc);
-        dst[0] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
-        dst[1] = make_uint4(pk[4], pk[5], pk[6], pk[7]);
+        uint16_t* dst = a.out + (size_t)m * a.N + nc;
+        if constexpr (CB == 16) {
+          reinterpret_cast<uint4*>(dst)[0] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+          reinterpret_cast<uint4*>(dst)[1] = make_uint4(pk[4], pk[5], pk[6], pk[7]);
+        } else if constexpr (CB == 8) {
+          *reinterpret_cast<uint4*>(dst) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+        } else {
+          *reinterpret_cast<uint2*>(dst) = make_uint2(pk[0], pk[1]);
+        }
       }
       if (a.gmax != nullptr) {  // the 16 lanes of a group share the row; lanes past N add -inf
         if (!col_ok) mx = -__builtin_inff();
 #pragma unroll
         for (int off = 8; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-        if (i == 0 && m < a.M) a.gmax[(size_t)m * gridDim.x + blockIdx.x] = mx;
+        if (i == 0 && m < a.M) a.gmax[(size_t)m * groups + grp] = mx;
       }
     }
   } else {
@@ -282,11 +295,11 @@ __global__ __launch_bounds__(NWAVES * 64, 3) void fp8_gemm_kernel(GemmArgs a) {
     float* part = a.partial + (size_t)sk * a.M * a.N;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int m = m_base + 4 * G + r;
+      const int m = m_pass + 16 * rb + 4 * G + r;
       if (m >= a.M) continue;
       float4* dst = reinterpret_cast<float4*>(part + (size_t)m * a.N + nc);
 #pragma unroll
-      for (int c = 0; c < 4; ++c)
+      for (int c = 0; c < CB / 4; ++c)
         dst[c] = make_float4(acc[4 * c][r], acc[4 * c + 1][r], acc[4 * c + 2][r], acc[4 * c + 3][r]);
     }
   }
@@ -765,24 +778,28 @@ GemmPlan plan(int M, int K, int N, bool no_split = false) {
   GemmPlan p{};
   if (plan_wide(M, K, N, p, no_split)) return p;
   p = GemmPlan{};
-  // Narrow plan: row blocks per pass (4 waves: RB row blocks x 4 / RB k parts), and a split-K
-  // factor: the largest power of two up to 8 that keeps the grid at or under 160 workgroups.
-  // Measured on MI355X at M = 8 and 64, K = 5120, N = 5120 / 17408 / 34816, the GEMM plus its
-  // reduction is fastest at 136 to 160 workgroups (N = 34816 unsplit, 17408 split in two,
-  // 5120 in eight); more workgroups only add partial traffic and HBM contention.
+  // Narrow plan: one pass of RB = 1, 2 or 4 row blocks (M <= 64), and a split-K factor: the
+  // largest power of two up to 8 whose grid stays at or under 576 workgroups with at least
+  // 8 k steps each. Measured on MI355X at M = 8, 32 and 64, K = 5120, N = 5120 / 17408 /
+  // 34816 (GEMM plus reduction, weights rotated through 600 MB): one workgroup per CU keeps
+  // only NS - 1 tiles in flight and reaches about 21 GB/s per CU, so the split that engages
+  // every CU wins (N = 34816 split 4: 0.092 -> 0.070 ms at M = 64) until the partial traffic
+  // outgrows it.
   const int mtiles = (M + 15) / 16;
-  p.mt = mtiles >= 4 ? 4 : (mtiles >= 2 ? 2 : 1);
+  p.mt = mtiles >= 3 ? 4 : mtiles;
   p.passes = (M + 16 * p.mt - 1) / (16 * p.mt);
   const int tiles = ((N + NT - 1) / NT) * p.passes;
-  const int kparts = NWAVES / p.mt;
   const int nks = K / KSTEP;
   p.split_k = 1;
-  while (!no_split && p.split_k < 8 && tiles * p.split_k * 2 <= 160 &&
-         nks >= 2 * (2 * p.split_k) * kparts)
+  while (!no_split && p.split_k < 8 && tiles * p.split_k * 2 <= 576 && nks >= 16 * p.split_k)
     p.split_k *= 2;
   p.ws = p.split_k > 1 ? (size_t)p.split_k * M * N * sizeof(float) : 0;
   return p;
 }
+
+// Column slices per narrow tile (the kernel's CH = waves / row blocks): its row-maximum and
+// argmax groups are (tile, slice) pairs.
+int narrow_slices(int mt) { return mt == 1 ? 4 : (mt == 2 ? 4 : 2); }
 
 bool shape_ok(int M, int K, int N) {
   return M >= 1 && M <= 4096 && K >= 64 && K % 64 == 0 && N >= 64 && N % 64 == 0 &&
@@ -816,9 +833,9 @@ int launch_gemm(const GemmPlan& p, const uint16_t* x, const int8_t* w, const flo
                 to_partial, amax, gmax};
     const dim3 grid((N + NT - 1) / NT, p.split_k, p.passes);
     switch (p.mt) {
-      case 1: hipLaunchKernelGGL(fp8_gemm_kernel<1>, grid, dim3(NWAVES * 64), 0, s, ga); break;
-      case 2: hipLaunchKernelGGL(fp8_gemm_kernel<2>, grid, dim3(NWAVES * 64), 0, s, ga); break;
-      default: hipLaunchKernelGGL(fp8_gemm_kernel<4>, grid, dim3(NWAVES * 64), 0, s, ga); break;
+      case 1: hipLaunchKernelGGL((fp8_gemm_narrow_kernel<1, 4, 4>), grid, dim3(256), 0, s, ga); break;
+      case 2: hipLaunchKernelGGL((fp8_gemm_narrow_kernel<2, 4, 8>), grid, dim3(512), 0, s, ga); break;
+      default: hipLaunchKernelGGL((fp8_gemm_narrow_kernel<4, 4, 8>), grid, dim3(512), 0, s, ga); break;
     }
   }
   if (reduce && p.split_k > 1) {
@@ -909,7 +926,7 @@ extern "C" int npn_fp8_matmul_swiglu(const uint16_t* x, const int8_t* w, const f
 extern "C" int npn_fp8_matmul_argmax_groups(int M, int K, int N) {
   if (!shape_ok(M, K, N)) return 0;
   const GemmPlan p = plan(M, K, N, true);
-  return p.wide ? p.groups : (N + NT - 1) / NT;
+  return p.wide ? p.groups : ((N + NT - 1) / NT) * narrow_slices(p.mt);
 }
 
 extern "C" int npn_fp8_matmul_argmax(const uint16_t* x, const int8_t* w, const float* scale,

@@ -100,7 +100,7 @@ __global__ __launch_bounds__(128 * P) void dn_verify_kernel(DnArgs a) {
   __shared__ float s_rq[TMAX], s_rk[TMAX], s_ro[TMAX];
   __shared__ float s_decay[TMAX];
   __shared__ float s_beta[TMAX];
-  __shared__ float s_red[2][P][D];
+  __shared__ float s_red[2][2][P][D];  // [S^T k | S^T q][token parity][row part][column]
 
   const float* S0;
   if (a.state_index != nullptr) {
@@ -149,6 +149,16 @@ __global__ __launch_bounds__(128 * P) void dn_verify_kernel(DnArgs a) {
   }
   __syncthreads();
 
+  // o of token t from its P row-part sums (threads of part 0), in part order
+  auto o_reduce = [&](int t) {
+    float pr[P];
+#pragma unroll
+    for (int q = 0; q < P; ++q) pr[q] = s_red[1][t & 1][q][c];
+    float o = 0.f;
+#pragma unroll
+    for (int q = 0; q < P; ++q) o += pr[q];
+    s_o[t][c] = o * s_rq[t];
+  };
   float* ck = a.ckpt + ((size_t)b * T * a.Hv + h) * tile + (size_t)r0 * D + c;
 #pragma unroll
   for (int t = 0; t < TMAX; ++t) {
@@ -161,11 +171,18 @@ __global__ __launch_bounds__(128 * P) void dn_verify_kernel(DnArgs a) {
         S[r] *= decay;
         acc[r & 3] = fmaf(S[r], s_k[t][r0 + r], acc[r & 3]);
       }
-      s_red[0][part][c] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+      s_red[0][t & 1][part][c] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+      // One barrier per token: it publishes token t's S^T k sums and token t - 1's S^T q
+      // sums (each kind double-buffered by token parity, so token t + 1 writes the other
+      // half while this token's halves are still being read).
       __syncthreads();
+      if (t > 0 && part == 0) o_reduce(t - 1);
+      float pr[P];
+#pragma unroll
+      for (int q = 0; q < P; ++q) pr[q] = s_red[0][t & 1][q][c];
       float kS = 0.f;
 #pragma unroll
-      for (int q = 0; q < P; ++q) kS += s_red[0][q][c];
+      for (int q = 0; q < P; ++q) kS += pr[q];
       const float kd = (s_v[t][c] - kS * rk) * s_beta[t] * rk;
       float oc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -173,21 +190,16 @@ __global__ __launch_bounds__(128 * P) void dn_verify_kernel(DnArgs a) {
         S[r] = fmaf(s_k[t][r0 + r], kd, S[r]);
         oc[r & 3] = fmaf(S[r], s_q[t][r0 + r], oc[r & 3]);
       }
-      s_red[1][part][c] = (oc[0] + oc[1]) + (oc[2] + oc[3]);
+      s_red[1][t & 1][part][c] = (oc[0] + oc[1]) + (oc[2] + oc[3]);
       // Nontemporal stores: write-allocating ones leave part of the checkpoints to drain from
       // the memory-side cache during the GEMMs that follow (the step measured ~1% slower).
       float* dst = ck + (size_t)t * a.Hv * tile;
 #pragma unroll
       for (int r = 0; r < R; ++r) __builtin_nontemporal_store(S[r], dst + (size_t)r * D);
-      __syncthreads();
-      if (part == 0) {
-        float o = 0.f;
-#pragma unroll
-        for (int q = 0; q < P; ++q) o += s_red[1][q][c];
-        s_o[t][c] = o * s_rq[t];
-      }
     }
   }
+  __syncthreads();
+  if (part == 0) o_reduce(T - 1);
 
   // Gated RMSNorm of o_t over the 128 v columns (tokens t < T only).
   __syncthreads();

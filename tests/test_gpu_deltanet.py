@@ -154,10 +154,10 @@ def test_full_size_b32_sampled(ops):
         assert_rel_close(gout[b:b + 1], out, out_unit=BF16_U, name=f"out[b={b}]")
 
 
-@pytest.mark.parametrize("B,parts", [(8, 4), (16, 2), (1, 8)])
+@pytest.mark.parametrize("B,parts", [(8, 4), (16, 2), (1, 8), (3, 8)])
 def test_row_split_batches_sampled(ops, B, parts):
     """Batches that run the row-split kernel (each state column's rows split over `parts`
-    wave pairs: B*Hv = 384 -> 4, 768 -> 2, 48 -> 8), full width, T = 8; sampled sequences
+    wave pairs: B*Hv = 384 -> 4, 768 -> 2, 48 and 144 -> 8), full width, T = 8; sampled sequences
     against the oracle."""
     Hk, Hv, T = 16, 48, 8
     d = deltanet_inputs(B, T, Hk, Hv, seed=40 + B)

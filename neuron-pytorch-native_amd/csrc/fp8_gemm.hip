@@ -114,11 +114,25 @@ struct GemmArgs {
 // column slices of 256 / CH columns; lane (i, G) reads CB = 16 / CH bytes (columns) from each
 // of its 8 k rows 8 G + j out of LDS, and each 4-column quarter is transposed and dequantised
 // in registers into the B operands of 4 MFMAs (column ct of quarter q feeds MFMA 4 q + ct).
-// Each wave issues the same DMA instructions for every tile (steps past the range repeat the
-// last one), so a constant vmcnt per wave names "this tile landed"; an s_barrier then
+// Each wave issues the same DMA instructions for every tile, so a vmcnt of (tiles issued
+// after tile t) x (this wave's DMAs per tile) names "tile t landed"; an s_barrier then
 // publishes it. For wide N, K is also split across workgroups (split_k); partials then go
 // through an fp32 workspace and a fixed-order reduction kernel.
 constexpr int NT = 256;     // columns per narrow tile
+
+// s_waitcnt vmcnt(pend * DPT) for a wave-uniform pend in [0, C] (the count is an immediate).
+template <int C, int DPT>
+__device__ __forceinline__ void wait_tiles(int pend) {
+  if constexpr (C > 0) {
+    if (pend >= C) {
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(C * DPT) : "memory");
+      return;
+    }
+    wait_tiles<C - 1, DPT>(pend);
+  } else {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  }
+}
 
 template <int RB, int NS, int NWV>
 __global__ __launch_bounds__(NWV * 64, 1) void fp8_gemm_narrow_kernel(GemmArgs a) {
@@ -177,17 +191,19 @@ __global__ __launch_bounds__(NWV * 64, 1) void fp8_gemm_narrow_kernel(GemmArgs a
 
   if (ntile > 0) {
 #pragma unroll
-    for (int p = 0; p < NS - 1; ++p) issue(ks_lo + (p < ntile ? p : ntile - 1), p);
+    for (int p = 0; p < NS - 1; ++p)
+      if (p < ntile) issue(ks_lo + p, p);
     for (int t = 0; t < ntile; ++t) {
-      // tiles t + 1 .. t + NS - 2 were issued after tile t: wait for the rest, then publish
-      if (w < XW)
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NS - 2) * (WQ + 1)) : "memory");
-      else
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NS - 2) * WQ) : "memory");
+      // Tiles t + 1 .. min(t + NS - 2, ntile - 1) were issued after tile t: wait until at
+      // most their DMAs are outstanding (this wave's count per tile is WQ, plus one x DMA
+      // for waves w < XW), then publish tile t.
+      const int pend = min(ntile - 1 - t, NS - 2);
+      if (w < XW) wait_tiles<NS - 2, WQ + 1>(pend);
+      else wait_tiles<NS - 2, WQ>(pend);
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
       const int tn = t + NS - 1;                      // into the stage tile t - 1 used
-      issue(ks_lo + (tn < ntile ? tn : ntile - 1), tn % NS);
+      if (tn < ntile) issue(ks_lo + tn, tn % NS);
       const uint8_t* ws = smem + (t % NS) * STAGE;
       const uint8_t* xs = ws + WST;
       const u32x4 xv = *reinterpret_cast<const u32x4*>(xs + (16 * rb + i) * 64 + 16 * G);
@@ -223,8 +239,7 @@ __global__ __launch_bounds__(NWV * 64, 1) void fp8_gemm_narrow_kernel(GemmArgs a
       }
     }
   }
-  // the repeats issued past the range must land before the workgroup's LDS is released
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  // (every DMA has landed: the last tile waited with vmcnt(0))
 
   // Lane (i, G) holds rows m_pass + 16 rb + 4 G + r and columns nc + c in acc[c][r]; its
   // group for the row maxima is the (tile, column slice) pair.
@@ -779,19 +794,21 @@ GemmPlan plan(int M, int K, int N, bool no_split = false) {
   if (plan_wide(M, K, N, p, no_split)) return p;
   p = GemmPlan{};
   // Narrow plan: one pass of RB = 1, 2 or 4 row blocks (M <= 64), and a split-K factor: the
-  // largest power of two up to 8 whose grid stays at or under 576 workgroups with at least
-  // 8 k steps each. Measured on MI355X at M = 8, 32 and 64, K = 5120, N = 5120 / 17408 /
-  // 34816 (GEMM plus reduction, weights rotated through 600 MB): one workgroup per CU keeps
-  // only NS - 1 tiles in flight and reaches about 21 GB/s per CU, so the split that engages
-  // every CU wins (N = 34816 split 4: 0.092 -> 0.070 ms at M = 64) until the partial traffic
-  // outgrows it.
+  // largest power of two up to 8 whose grid stays at or under 576 workgroups (1152 up to 16
+  // rows, whose partials are small) with at least 8 k steps each. Measured on MI355X at
+  // M = 8, 32 and 64, K = 5120, N = 5120 / 17408 / 34816 (GEMM plus reduction, weights
+  // rotated through 600 MB): one workgroup per CU keeps only NS - 1 tiles in flight and
+  // reaches about 21 GB/s per CU, so the split that engages every CU wins (N = 34816 split
+  // 4: 0.092 -> 0.070 ms at M = 64; split 8: 0.043 -> 0.040 ms at M = 8) until the partial
+  // traffic outgrows it.
   const int mtiles = (M + 15) / 16;
   p.mt = mtiles >= 3 ? 4 : mtiles;
   p.passes = (M + 16 * p.mt - 1) / (16 * p.mt);
   const int tiles = ((N + NT - 1) / NT) * p.passes;
   const int nks = K / KSTEP;
+  const int max_wg = M <= 16 ? 1152 : 576;
   p.split_k = 1;
-  while (!no_split && p.split_k < 8 && tiles * p.split_k * 2 <= 576 && nks >= 16 * p.split_k)
+  while (!no_split && p.split_k < 8 && tiles * p.split_k * 2 <= max_wg && nks >= 16 * p.split_k)
     p.split_k *= 2;
   p.ws = p.split_k > 1 ? (size_t)p.split_k * M * N * sizeof(float) : 0;
   return p;

@@ -39,6 +39,13 @@ def test_small_n(ops, M):
     _check(ops, M, 5120, 512, seed=M)
 
 
+@pytest.mark.parametrize("M,N", [(8, 320), (40, 576), (64, 1088), (1, 64), (16, 1344)])
+def test_partial_last_tile(ops, M, N):
+    """N not a multiple of the narrow kernel's 256-column tile: the last tile's W reads past
+    N are clamped and its columns past N never stored (K = 1024 also splits K in two)."""
+    _check(ops, M, 1024, N, seed=N + M)
+
+
 @pytest.mark.parametrize("M,N", [(8, 5120), (64, 17408), (256, 34816)])
 def test_verify_shapes_sampled(ops, M, N):
     rng = np.random.default_rng(M)

@@ -37,7 +37,7 @@ def _gpu_weights(K, N, seed):
 
 
 @pytest.mark.parametrize("M,K,N", [(256, 5120, 248320), (40, 5120, 248320), (256, 1024, 4096),
-                                   (13, 512, 1024)])
+                                   (13, 512, 1024), (13, 256, 320), (40, 256, 832)])
 def test_matmul_argmax_equals_torch_argmax(ops, M, K, N):
     g = torch.Generator(device="cuda").manual_seed(M + N)
     x = torch.randn(M, K, generator=g, device="cuda").to(torch.bfloat16)
@@ -105,7 +105,8 @@ def _rowmax(x, w, sc):
     return out, gmax
 
 
-@pytest.mark.parametrize("M,K,N", [(256, 5120, 151936), (40, 5120, 248320), (13, 128, 1024)])
+@pytest.mark.parametrize("M,K,N", [(256, 5120, 151936), (40, 5120, 248320), (13, 128, 1024),
+                                   (13, 128, 320), (40, 256, 832)])
 def test_matmul_rowmax(ops, M, K, N):
     """Shapes where fp8::matmul's own plan does not split K either (so its sums are the
     same); the host plan tests pin which shapes split."""

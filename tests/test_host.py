@@ -131,12 +131,15 @@ def test_fp8_split_k_plan():
     # argmax mode never splits K; the LM head's vocabulary runs in rounds of 12-unit groups
     assert query("npn_fp8_matmul_argmax_groups", 256, 5120, 248320) == 1294
     # below 65 rows: 256-column tiles of 4 column slices (2 at 33..64 rows), and the grid
-    # kept at or under 576 workgroups
+    # kept at or under 576 workgroups (1152 up to 16 rows)
     assert query("npn_fp8_matmul_argmax_groups", 16, 5120, 248320) == 248320 // 64
     assert query("npn_fp8_matmul_argmax_groups", 32, 5120, 248320) == 248320 // 64
     assert query("npn_fp8_matmul_argmax_groups", 40, 5120, 248320) == 248320 // 128
+    assert query("npn_fp8_matmul_split_k", 8, 5120, 34816) == 8         # up to 1152 at M <= 16
+    assert query("npn_fp8_matmul_split_k", 16, 5120, 34816) == 8
     for m in (8, 32, 64):
-        assert query("npn_fp8_matmul_split_k", m, 5120, 34816) == 4     # 136 tiles
+        if m > 16:
+            assert query("npn_fp8_matmul_split_k", m, 5120, 34816) == 4  # 136 tiles
         assert query("npn_fp8_matmul_split_k", m, 5120, 17408) == 8     # 68 tiles
         assert query("npn_fp8_matmul_split_k", m, 5120, 5120) == 8      # 20 tiles
         assert query("npn_fp8_matmul_split_k", m, 17408, 5120) == 8

@@ -98,6 +98,7 @@ struct GemmArgs {
   int M, K, N, split_k, to_partial;
   ArgPart* amax;     // row argmax partials [M][column groups] instead of out (split_k == 1)
   float* gmax;       // with out: per-(row, column group) max of the bf16 outputs, NaN ignored
+  int sk_wg;         // narrow kernel, > 0: stream-K over this many workgroups (split_k slots)
 };
 
 // ---------------------------------------------------------------------------------------
@@ -149,47 +150,38 @@ __global__ __launch_bounds__(NWV * 64, 1) void fp8_gemm_narrow_kernel(GemmArgs a
                 "whole DMA instructions per stage");
   __shared__ __attribute__((aligned(16))) uint8_t smem[NS * STAGE];
 
-  const int n0 = blockIdx.x * NT;
-  const int sk = blockIdx.y;
   const int m_pass = blockIdx.z * 16 * RB;
   const int tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int i = lane & 15, G = lane >> 4;
   const int rb = w / CH, ch = w - rb * CH;
   const int nks = a.K / KSTEP;
-  const int ks_lo = (int)(((long)nks * sk) / a.split_k);
-  const int ks_hi = (int)(((long)nks * (sk + 1)) / a.split_k);
-  const int ntile = ks_hi - ks_lo;
-
-  // DMA of k step ks into stage st: W rows (2 x 16 bytes per thread), then x rows.
-  auto issue = [&](int ks, int st) {
-    uint8_t* ws = smem + st * STAGE;
-    uint8_t* xs = ws + WST;
-    const int k0 = ks * KSTEP;
-#pragma unroll
-    for (int q = 0; q < WQ; ++q) {
-      const int s = q * NTH + tid;                    // 16-byte slot of the W stage
-      const int row = s >> 4;
-      int col = n0 + 16 * (s & 15);
-      col = col < a.N ? col : a.N - 16;               // a partial last tile re-reads valid bytes
-      npn::lds_dma16(a.w + (size_t)(k0 + row) * a.N + col, ws + q * (NTH * 16) + (tid & ~63) * 16);
-    }
-    if (w < XW) {                                     // 16-byte slots, 4 per 64-byte row
-      const int s = w * 64 + lane;
-      int m = m_pass + (s >> 2);
-      m = m < a.M ? m : a.M - 1;
-      npn::lds_dma16(a.x + (size_t)m * a.K + k0 + 8 * (s & 3), xs + w * 1024);
-    }
-  };
-
-  f32x4 acc[CB];
-#pragma unroll
-  for (int c = 0; c < CB; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
   const int mrow = m_pass + 16 * rb + i;              // A operand row of this lane
   const bool row_ok = mrow < a.M;
   const int lcol = ch * 16 * CB + CB * i;             // the lane's first column in the tile
 
-  if (ntile > 0) {
+  // k steps ks_lo .. ks_lo + ntile - 1 of the tile at column n0, summed into acc.
+  auto run = [&](int n0, int ks_lo, int ntile, f32x4 (&acc)[CB]) {
+    // DMA of k step ks into stage st: W rows (WQ x 16 bytes per thread), then x rows.
+    auto issue = [&](int ks, int st) {
+      uint8_t* ws = smem + st * STAGE;
+      uint8_t* xs = ws + WST;
+      const int k0 = ks * KSTEP;
+#pragma unroll
+      for (int q = 0; q < WQ; ++q) {
+        const int s = q * NTH + tid;                  // 16-byte slot of the W stage
+        const int row = s >> 4;
+        int col = n0 + 16 * (s & 15);
+        col = col < a.N ? col : a.N - 16;             // a partial last tile re-reads valid bytes
+        npn::lds_dma16(a.w + (size_t)(k0 + row) * a.N + col, ws + q * (NTH * 16) + (tid & ~63) * 16);
+      }
+      if (w < XW) {                                   // 16-byte slots, 4 per 64-byte row
+        const int s = w * 64 + lane;
+        int m = m_pass + (s >> 2);
+        m = m < a.M ? m : a.M - 1;
+        npn::lds_dma16(a.x + (size_t)m * a.K + k0 + 8 * (s & 3), xs + w * 1024);
+      }
+    };
 #pragma unroll
     for (int p = 0; p < NS - 1; ++p)
       if (p < ntile) issue(ks_lo + p, p);
@@ -238,8 +230,66 @@ __global__ __launch_bounds__(NWV * 64, 1) void fp8_gemm_narrow_kernel(GemmArgs a
               __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop, bop[ct], acc[4 * q + ct], 0, 0, 0);
       }
     }
+    // (every DMA has landed: the last tile waited with vmcnt(0))
+  };
+
+  // fp32 sums (unscaled) of this lane's rows and columns of the tile at n0 into partial
+  // slot `slot` ([split_k][M][N]); zero sums when `zero`.
+  auto store_partial = [&](int slot, int n0, const f32x4 (&acc)[CB], bool zero) {
+    const int nc = n0 + lcol;
+    if (nc >= a.N) return;
+    float* part = a.partial + (size_t)slot * a.M * a.N;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = m_pass + 16 * rb + 4 * G + r;
+      if (m >= a.M) continue;
+      float4* dst = reinterpret_cast<float4*>(part + (size_t)m * a.N + nc);
+#pragma unroll
+      for (int c = 0; c < CB / 4; ++c)
+        dst[c] = zero ? make_float4(0.f, 0.f, 0.f, 0.f)
+                      : make_float4(acc[4 * c][r], acc[4 * c + 1][r], acc[4 * c + 2][r],
+                                    acc[4 * c + 3][r]);
+    }
+  };
+
+  if (a.sk_wg > 0) {
+    // Stream-K: the tiles' k steps laid end to end (U units), workgroup wg taking units
+    // [wg U / W, (wg + 1) U / W). A tile's units are covered by workgroups wfirst .. wlast
+    // (closed form: the workgroup that holds unit x is ((x + 1) W - 1) / U); workgroup wg
+    // writes its sums of tile t to slot wg - wfirst, and wlast zeroes the slots past the
+    // tile's last, so every tile's split_k slots add to its full sum in slot order.
+    const long U = (long)((a.N + NT - 1) / NT) * nks;
+    const long W = a.sk_wg;
+    const long wg = blockIdx.x;
+    const long u0 = wg * U / W, u1 = (wg + 1) * U / W;
+    for (long t = u0 / nks; t * nks < u1; ++t) {
+      const long tb = t * nks;
+      const int lo = (int)(u0 > tb ? u0 - tb : 0);
+      const int hi = (int)(u1 - tb < nks ? u1 - tb : nks);
+      const int wfirst = (int)(((tb + 1) * W - 1) / U);
+      const int wlast = (int)(((tb + nks) * W - 1) / U);
+      f32x4 acc[CB];
+#pragma unroll
+      for (int c = 0; c < CB; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+      __syncthreads();  // every wave is done with the ring's previous segment
+      run((int)t * NT, lo, hi - lo, acc);
+      store_partial((int)wg - wfirst, (int)t * NT, acc, false);
+      if (wg == wlast)
+        for (int sl = wlast - wfirst + 1; sl < a.split_k; ++sl)
+          store_partial(sl, (int)t * NT, acc, true);
+    }
+    return;
   }
-  // (every DMA has landed: the last tile waited with vmcnt(0))
+
+  const int n0 = blockIdx.x * NT;
+  const int sk = blockIdx.y;
+  const int ks_lo = (int)(((long)nks * sk) / a.split_k);
+  const int ks_hi = (int)(((long)nks * (sk + 1)) / a.split_k);
+  f32x4 acc[CB];
+#pragma unroll
+  for (int c = 0; c < CB; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+  run(n0, ks_lo, ks_hi - ks_lo, acc);
+
 
   // Lane (i, G) holds rows m_pass + 16 rb + 4 G + r and columns nc + c in acc[c][r]; its
   // group for the row maxima is the (tile, column slice) pair.
@@ -306,17 +356,7 @@ __global__ __launch_bounds__(NWV * 64, 1) void fp8_gemm_narrow_kernel(GemmArgs a
       }
     }
   } else {
-    if (!col_ok) return;
-    float* part = a.partial + (size_t)sk * a.M * a.N;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int m = m_pass + 16 * rb + 4 * G + r;
-      if (m >= a.M) continue;
-      float4* dst = reinterpret_cast<float4*>(part + (size_t)m * a.N + nc);
-#pragma unroll
-      for (int c = 0; c < CB / 4; ++c)
-        dst[c] = make_float4(acc[4 * c][r], acc[4 * c + 1][r], acc[4 * c + 2][r], acc[4 * c + 3][r]);
-    }
+    store_partial(sk, n0, acc, false);
   }
 }
 
@@ -730,6 +770,7 @@ struct GemmPlan {
   size_t ws;
   bool wide;
   int units, groups, ntm;
+  int sk_wg;  // narrow: stream-K workgroups (0: a tiles x split_k grid)
 };
 
 // Wide-kernel instantiations: column tiles per wave (a workgroup holds twice as many units).
@@ -810,6 +851,27 @@ GemmPlan plan(int M, int K, int N, bool no_split = false) {
   p.split_k = 1;
   while (!no_split && p.split_k < 8 && tiles * p.split_k * 2 <= max_wg && nks >= 16 * p.split_k)
     p.split_k *= 2;
+  // Stream-K where the tiles x split grid cannot fill the CUs evenly (136 tiles x 4 = 544
+  // workgroups leave 32 CUs with three while the rest run two): up to 512 workgroups (two per
+  // CU) share the tiles' k steps equally, at least 8 each, with at most 8 partial slots per
+  // tile (so at most 7 workgroups' shares per tile). Measured on MI355X, M = 64, K = 5120: a
+  // 512-workgroup grid (N = 32768, split 4) streams W at 3.3 TB/s, the 544 of N = 34816 at
+  // 2.9 TB/s.
+  if (!no_split && p.passes == 1 && tiles < 256) {
+    const long W = 7L * tiles < 512 ? 7L * tiles : 512;
+    const long U = (long)tiles * nks;
+    if (W > 384 && U >= 8 * W) {
+      int slots = 0;
+      for (long t = 0; t < tiles; ++t) {
+        const long wfirst = ((t * nks + 1) * W - 1) / U, wlast = (((t + 1) * nks) * W - 1) / U;
+        slots = (int)(wlast - wfirst + 1) > slots ? (int)(wlast - wfirst + 1) : slots;
+      }
+      if (slots >= 2 && slots <= 8) {
+        p.sk_wg = (int)W;
+        p.split_k = slots;
+      }
+    }
+  }
   p.ws = p.split_k > 1 ? (size_t)p.split_k * M * N * sizeof(float) : 0;
   return p;
 }
@@ -847,8 +909,8 @@ int launch_gemm(const GemmPlan& p, const uint16_t* x, const int8_t* w, const flo
     }
   } else {
     GemmArgs ga{x, reinterpret_cast<const uint8_t*>(w), scale, out, partial, M, K, N, p.split_k,
-                to_partial, amax, gmax};
-    const dim3 grid((N + NT - 1) / NT, p.split_k, p.passes);
+                to_partial, amax, gmax, p.sk_wg};
+    const dim3 grid = p.sk_wg > 0 ? dim3(p.sk_wg, 1, 1) : dim3((N + NT - 1) / NT, p.split_k, p.passes);
     switch (p.mt) {
       case 1: hipLaunchKernelGGL((fp8_gemm_narrow_kernel<1, 4, 4>), grid, dim3(256), 0, s, ga); break;
       case 2: hipLaunchKernelGGL((fp8_gemm_narrow_kernel<2, 4, 8>), grid, dim3(512), 0, s, ga); break;

@@ -46,6 +46,15 @@ def test_partial_last_tile(ops, M, N):
     _check(ops, M, 1024, N, seed=N + M)
 
 
+@pytest.mark.parametrize("M,K,N", [(8, 1024, 34816), (40, 2048, 17408), (64, 2048, 14336)])
+def test_stream_k(ops, M, K, N):
+    """Narrow shapes planned as stream-K (each workgroup an equal run of the tiles' k steps,
+    a tile's partial sums in up to 8 slots, unused slots zeroed), every column checked."""
+    import npn_native
+    assert npn_native.query("npn_fp8_matmul_split_k", M, K, N) in (5, 7)
+    _check(ops, M, K, N, seed=K + N)
+
+
 @pytest.mark.parametrize("M,N", [(8, 5120), (64, 17408), (256, 34816)])
 def test_verify_shapes_sampled(ops, M, N):
     rng = np.random.default_rng(M)

@@ -135,14 +135,15 @@ def test_fp8_split_k_plan():
     assert query("npn_fp8_matmul_argmax_groups", 16, 5120, 248320) == 248320 // 64
     assert query("npn_fp8_matmul_argmax_groups", 32, 5120, 248320) == 248320 // 64
     assert query("npn_fp8_matmul_argmax_groups", 40, 5120, 248320) == 248320 // 128
-    assert query("npn_fp8_matmul_split_k", 8, 5120, 34816) == 8         # up to 1152 at M <= 16
-    assert query("npn_fp8_matmul_split_k", 16, 5120, 34816) == 8
     for m in (8, 32, 64):
-        if m > 16:
-            assert query("npn_fp8_matmul_split_k", m, 5120, 34816) == 4  # 136 tiles
-        assert query("npn_fp8_matmul_split_k", m, 5120, 17408) == 8     # 68 tiles
-        assert query("npn_fp8_matmul_split_k", m, 5120, 5120) == 8      # 20 tiles
+        # stream-K (partial slots per tile): 136 tiles over 512 workgroups, 68 over 476
+        assert query("npn_fp8_matmul_split_k", m, 5120, 34816) == 5
+        assert query("npn_fp8_matmul_split_k", m, 5120, 17408) == 7
+        assert query("npn_fp8_matmul_split_k", m, 5120, 14336) == 7
+        # a tiles x split grid: 20 tiles split 8
+        assert query("npn_fp8_matmul_split_k", m, 5120, 5120) == 8
         assert query("npn_fp8_matmul_split_k", m, 17408, 5120) == 8
+    assert query("npn_fp8_matmul_workspace_size", 64, 5120, 34816) == 5 * 64 * 34816 * 4
     assert query("npn_fp8_matmul_split_k", 8, 256, 1024) == 1           # 8 k steps
     assert query("npn_fp8_matmul_split_k", 8, 512, 1024) == 2
 

@@ -39,6 +39,7 @@ def _state(m):
 def _fill_inputs(x, logits, gen):
     from spec_verify_step import HIDDEN
     target, draft, ids, u, us = logits
+    B = ids.shape[0]
     x.copy_(torch.randn(x.shape[0], HIDDEN, generator=gen, device=x.device).to(torch.bfloat16))
     target.copy_(torch.randn(target.shape, generator=gen, device=x.device))
     draft.copy_(0.8 * target[:, :K] + 0.6 * torch.randn(draft.shape, generator=gen,
@@ -49,11 +50,14 @@ def _fill_inputs(x, logits, gen):
     us.copy_(torch.rand(us.shape, generator=gen, device=x.device))
 
 
-@pytest.mark.parametrize("greedy", [False, True])
-def test_graph_replay_matches_eager(greedy):
+@pytest.mark.parametrize("greedy,nseq", [(False, 4), (True, 4), (False, 1), (False, 9)])
+def test_graph_replay_matches_eager(greedy, nseq):
+    """nseq sequences: 4 (M = 32, narrow GEMMs, stream-K at the gate/up width), 1 (M = 8),
+    9 (M = 72, the wide GEMM kernel with most of its 256 rows past M)."""
     from spec_verify_step import HIDDEN, VerifySlice, synthetic_logits
     dev = "cuda"
-    kv = [37, 300, 5, 129]
+    B = nseq
+    kv = [37, 300, 5, 129, 64, 1000, 2, 17, 511][:B]
     s_max = max(kv) + (K + 1) * (STEPS + 4)
     models = [VerifySlice(B, K, kv, s_max, pattern="DG", seed=11, device=dev) for _ in range(3)]
     eager, graphed, plain = models  # plain: never made persistent (new state tensors per step)

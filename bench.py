@@ -47,6 +47,9 @@ def parse():
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--batch", type=int, default=32,
+                   help="sequences per step (the workload's B = 32; other values are side runs "
+                        "of the same step, labelled with their B)")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--per-op", action="store_true", help="print per-op timings to stderr")
     p.add_argument("--no-graph", action="store_true",
@@ -691,6 +694,11 @@ def main():
         print(f"bench.py runs on one GPU only (got --gpus {args.gpus}); the verify step is "
               f"measured on a single MI355X", file=sys.stderr)
         sys.exit(2)
+    global B
+    if not 1 <= args.batch <= 256:
+        print(f"--batch must be in [1, 256] (got {args.batch})", file=sys.stderr)
+        sys.exit(2)
+    B = args.batch
     import torch
     from spec_verify_step import HIDDEN, OpTimer, VerifySlice, synthetic_logits
 
@@ -794,7 +802,7 @@ def main():
         cpu = cpu_baseline(model, snap, kv_start, x, sets[0], first)
 
     line = {
-        "metric": "verify-step tokens/s (B=32,K=7) + achieved HBM GB/s vs MI355X peak",
+        "metric": f"verify-step tokens/s (B={B},K={K}) + achieved HBM GB/s vs MI355X peak",
         "value": round(tokens / elapsed, 1),
         "unit": "tokens/s",
         "n_gpus": 1,

@@ -11,7 +11,8 @@
 //     (hi = bf16(q'), lo = bf16(q' - hi)), so the bf16 MFMA sees q' to ~16 mantissa bits.
 //  2. attn: split-KV over a balanced partition. The (b, kv head) pairs' 32-key steps
 //     are laid end to end (prefix sums from a one-block plan kernel) and cut into
-//     kAttnWG equal ranges, one per workgroup, so every workgroup streams the same
+//     W = min(kAttnWG, S / 16) equal ranges (S steps in all), one per workgroup of the
+//     kAttnWG launched (the rest exit at once), so every workgroup streams the same
 //     number of K/V bytes whatever the kv_len spread; a range may cover the end of one
 //     pair and the start of the next. One wave per 16-row tile of the R rows; each
 //     pair segment streams through LDS in 32-key K/V tiles:
@@ -150,9 +151,19 @@ __device__ __forceinline__ int pair_kend(const int32_t* kv_len, int b, int T, in
   return L + T < s_max ? L + T : s_max;
 }
 
-// Workgroup w's step range is [w * S / kAttnWG, (w + 1) * S / kAttnWG).
+// Workgroups that take part for S steps in all: kAttnWG, or fewer when that would leave a
+// workgroup under kMinSteps steps (small batches), so a workgroup's fixed costs (its q' rows,
+// its partial rows, the ring's fill) stay small against its key stream and a pair's
+// partials stay few for the merge.
+constexpr int kMinSteps = 16;
+__device__ __forceinline__ int attn_wgs(int S) {
+  const int w = S / kMinSteps;
+  return w < 1 ? 1 : (w > kAttnWG ? kAttnWG : w);
+}
+
+// Workgroup w's step range is [w * S / W, (w + 1) * S / W), W = attn_wgs(S).
 __device__ __forceinline__ int wg_first_step(int w, int S) {
-  return (int)((int64_t)w * S / kAttnWG);
+  return (int)((int64_t)w * S / attn_wgs(S));
 }
 
 // One-block plan: pstart[p] = sum of the steps of pairs before p (exclusive scan).
@@ -225,6 +236,7 @@ __global__ __launch_bounds__(NRT * 64, NST <= 2 ? 2 : 1) void gqa_attn_kernel(At
   constexpr int DPW = (KS + NRT - 1) / NRT;  // DMA instructions per wave per step
   const int wg = blockIdx.x;
   const int S = a.pstart[a.npairs];
+  if (wg >= attn_wgs(S)) return;
   int x = wg_first_step(wg, S);
   const int x_end = wg_first_step(wg + 1, S);
   if (x >= x_end) return;
@@ -427,11 +439,13 @@ __global__ __launch_bounds__(NRT * 64, NST <= 2 ? 2 : 1) void gqa_attn_kernel(At
 }
 
 // ---------------------------------------------------------------------------------------
-// 3. merge a pair's segment partials, apply sigmoid(gate), write bf16. One 64-thread block
-//    per (query row, pair); lane l owns output dims 4l..4l+3 (float4 partial reads). The
-//    workgroups that covered pair p are w(first step) .. w(last step), with
-//    w(x) = ((x + 1) * kAttnWG - 1) / S; a workgroup with an empty range in between (only
-//    when S < kAttnWG) wrote nothing and is skipped.
+// 3. merge a pair's segment partials, apply sigmoid(gate), write bf16. One 256-thread block
+//    per (query row, pair); lane l of every wave owns output dims 4l..4l+3 (float4 partial
+//    reads). The workgroups that covered pair p are w(first step) .. w(last step), with
+//    w(x) = ((x + 1) * W - 1) / S, W = attn_wgs(S). Wave q merges segments q, q + 4, ... of
+//    the pair (loads issued four segments at a time), and wave 0 then merges the four
+//    waves' (m, l, O) in wave order: a small batch's pairs have tens of segments each, which
+//    one wave walking them in turn paid for in memory latency.
 struct MergeArgs {
   const float* part_o;
   const float* part_ml;
@@ -441,39 +455,83 @@ struct MergeArgs {
   int T, Hq, Hkv, R, npairs;
 };
 
-__global__ __launch_bounds__(64) void gqa_merge_kernel(MergeArgs a) {
+__global__ __launch_bounds__(256) void gqa_merge_kernel(MergeArgs a) {
   const int r = blockIdx.x;
   const int pr = blockIdx.y;
   const int b = pr / a.Hkv, g = pr - b * a.Hkv;
   const int grp = a.Hq / a.Hkv;
-  const int lane = threadIdx.x;
+  const int q = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int S = a.pstart[a.npairs];
+  const int64_t W = attn_wgs(S);
   const int x0 = a.pstart[pr], x1 = a.pstart[pr + 1] - 1;
-  const int w0 = (int)(((int64_t)(x0 + 1) * kAttnWG - 1) / S);
-  const int w1 = (int)(((int64_t)(x1 + 1) * kAttnWG - 1) / S);
+  const int w0 = (int)(((int64_t)(x0 + 1) * W - 1) / S);
+  const int w1 = (int)(((int64_t)(x1 + 1) * W - 1) / S);
   const size_t stride_ml = (size_t)a.R * 2, stride_o = (size_t)a.R * DH;
   const float* pml = a.part_ml + ((size_t)(w0 + pr) * a.R + r) * 2;
   const float* po = a.part_o + ((size_t)(w0 + pr) * a.R + r) * DH + 4 * lane;
+  auto live = [&](int w) { return w <= w1 && wg_first_step(w, S) < wg_first_step(w + 1, S); };
+  // this wave's segments w0 + q + 4 j: their maximum, then their rescaled sums
   float M = kNegBig;
-  for (int w = w0; w <= w1; ++w)
-    if (wg_first_step(w, S) < wg_first_step(w + 1, S)) M = fmaxf(M, pml[(w - w0) * stride_ml]);
+  for (int base = w0 + q; base <= w1; base += 16) {
+    float mv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int w = base + 4 * j;
+      mv[j] = live(w) ? pml[(w - w0) * stride_ml] : kNegBig;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) M = fmaxf(M, mv[j]);
+  }
   float l = 0.f;
   f32x4 o = {0.f, 0.f, 0.f, 0.f};
-  for (int w = w0; w <= w1; ++w) {
-    if (wg_first_step(w, S) == wg_first_step(w + 1, S)) continue;
-    const float f = exp2f(pml[(w - w0) * stride_ml] - M);
-    l += f * pml[(w - w0) * stride_ml + 1];
-    o += f * *reinterpret_cast<const f32x4*>(po + (w - w0) * stride_o);
+  for (int base = w0 + q; base <= w1; base += 16) {
+    float mv[4], lv[4];
+    f32x4 ov[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int w = base + 4 * j;
+      const bool ok = live(w);
+      mv[j] = ok ? pml[(w - w0) * stride_ml] : kNegBig;
+      lv[j] = ok ? pml[(w - w0) * stride_ml + 1] : 0.f;
+      ov[j] = ok ? *reinterpret_cast<const f32x4*>(po + (w - w0) * stride_o)
+                 : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float f = exp2f(mv[j] - M);
+      l += f * lv[j];
+      o += f * ov[j];
+    }
+  }
+  __shared__ float s_ml[4][2];
+  __shared__ f32x4 s_o[4][64];
+  if (lane == 0) {
+    s_ml[q][0] = M;
+    s_ml[q][1] = l;
+  }
+  s_o[q][lane] = o;
+  __syncthreads();
+  if (q != 0) return;
+  float Mt = s_ml[0][0];
+#pragma unroll
+  for (int k = 1; k < 4; ++k) Mt = fmaxf(Mt, s_ml[k][0]);
+  float lt = 0.f;
+  f32x4 ot = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const float f = exp2f(s_ml[k][0] - Mt);
+    lt += f * s_ml[k][1];
+    ot += f * s_o[k][lane];
   }
   const int t = r / grp, qh = g * grp + (r - t * grp);
   const size_t oi = (((size_t)b * a.T + t) * a.Hq + qh) * DH + 4 * lane;
-  const float inv = 1.0f / l;
+  const float inv = 1.0f / lt;
   uint32_t w[2];
   for (int j = 0; j < 2; ++j) {
     const float g0 = npn::sigmoid(npn::bf16_to_f32(a.gate[oi + 2 * j]));
     const float g1 = npn::sigmoid(npn::bf16_to_f32(a.gate[oi + 2 * j + 1]));
-    w[j] = npn::f32_to_bf16(o[2 * j] * inv * g0) |
-           ((uint32_t)npn::f32_to_bf16(o[2 * j + 1] * inv * g1) << 16);
+    w[j] = npn::f32_to_bf16(ot[2 * j] * inv * g0) |
+           ((uint32_t)npn::f32_to_bf16(ot[2 * j + 1] * inv * g1) << 16);
   }
   *reinterpret_cast<uint2*>(a.out + oi) = make_uint2(w[0], w[1]);
 }
@@ -692,7 +750,7 @@ extern "C" int npn_gqa_tail_verify(const uint16_t* query, const uint16_t* gate,
   else hipLaunchKernelGGL((gqa_attn_kernel<3, 2>), grid, dim3(192), 0, s, aa);
 
   MergeArgs ma{po, pml, pstart, gate, out, T, q_heads, kv_heads, p.R, p.P};
-  hipLaunchKernelGGL(gqa_merge_kernel, dim3(T * p.grp, p.P), dim3(64), 0, s, ma);
+  hipLaunchKernelGGL(gqa_merge_kernel, dim3(T * p.grp, p.P), dim3(256), 0, s, ma);
   return npn_launch_status();
 }
 

@@ -835,8 +835,9 @@ GemmPlan plan(int M, int K, int N, bool no_split = false) {
   if (plan_wide(M, K, N, p, no_split)) return p;
   p = GemmPlan{};
   // Narrow plan: one pass of RB = 1, 2 or 4 row blocks (M <= 64), and a split-K factor: the
-  // largest power of two up to 8 whose grid stays at or under 576 workgroups (1152 up to 16
-  // rows, whose partials are small) with at least 8 k steps each. Measured on MI355X at
+  // largest power of two up to 8 whose grid stays at or under 576 workgroups (up to 16 and
+  // 1152 workgroups for at most 16 rows, whose partials are small) with at least 8 k steps
+  // each. Measured on MI355X at
   // M = 8, 32 and 64, K = 5120, N = 5120 / 17408 / 34816 (GEMM plus reduction, weights
   // rotated through 600 MB): one workgroup per CU keeps only NS - 1 tiles in flight and
   // reaches about 21 GB/s per CU, so the split that engages every CU wins (N = 34816 split
@@ -848,8 +849,10 @@ GemmPlan plan(int M, int K, int N, bool no_split = false) {
   const int tiles = ((N + NT - 1) / NT) * p.passes;
   const int nks = K / KSTEP;
   const int max_wg = M <= 16 ? 1152 : 576;
+  const int max_split = M <= 16 ? 16 : 8;
   p.split_k = 1;
-  while (!no_split && p.split_k < 8 && tiles * p.split_k * 2 <= max_wg && nks >= 16 * p.split_k)
+  while (!no_split && p.split_k < max_split && tiles * p.split_k * 2 <= max_wg &&
+         nks >= 16 * p.split_k)
     p.split_k *= 2;
   // Stream-K where the tiles x split grid cannot fill the CUs evenly (136 tiles x 4 = 544
   // workgroups leave 32 CUs with three while the rest run two): up to 512 workgroups (two per

@@ -44,7 +44,8 @@ struct BfSrc {  // a bf16 matrix with row stride ld
     return *reinterpret_cast<const u32x4*>(p + m * ld + col);
   }
 };
-constexpr int kMaxSplit = 8;  // partial count the unrolled loads cover (the GEMM plan's max)
+constexpr int kMaxSplit = 16;  // the GEMM plan's largest split-K factor
+constexpr int kSplitBatch = 8;  // partials loaded per batch (unrolled)
 
 struct PartSrc {  // fp32 split-K partials [S][M][ld] and the per-column scale, S <= kMaxSplit
   const float* p;
@@ -52,23 +53,26 @@ struct PartSrc {  // fp32 split-K partials [S][M][ld] and the per-column scale, 
   int ld, S;
   size_t stride;  // M * ld
   __device__ __forceinline__ u32x4 load(size_t m, int col) const {
-    // All S partial loads are issued before the first add (unrolled, predicated), so one
-    // memory latency is paid per chunk rather than S.
+    // The partials are added in order s = 0 .. S-1 (as the GEMM's own reduction does); the
+    // loads of each batch of 8 are issued before its first add (unrolled, predicated), so
+    // one memory latency is paid per batch rather than per partial.
     const float* q = p + m * ld + col;
-    float4 a[kMaxSplit], b[kMaxSplit];
-#pragma unroll
-    for (int s = 0; s < kMaxSplit; ++s) {
-      if (s < S) {
-        a[s] = *reinterpret_cast<const float4*>(q + s * stride);
-        b[s] = *reinterpret_cast<const float4*>(q + s * stride + 4);
-      }
-    }
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < S; s0 += kSplitBatch) {
+      float4 a[kSplitBatch], b[kSplitBatch];
 #pragma unroll
-    for (int s = 0; s < kMaxSplit; ++s) {
-      if (s < S) {
-        acc[0] += a[s].x; acc[1] += a[s].y; acc[2] += a[s].z; acc[3] += a[s].w;
-        acc[4] += b[s].x; acc[5] += b[s].y; acc[6] += b[s].z; acc[7] += b[s].w;
+      for (int j = 0; j < kSplitBatch; ++j) {
+        if (s0 + j < S) {
+          a[j] = *reinterpret_cast<const float4*>(q + (s0 + j) * stride);
+          b[j] = *reinterpret_cast<const float4*>(q + (s0 + j) * stride + 4);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < kSplitBatch; ++j) {
+        if (s0 + j < S) {
+          acc[0] += a[j].x; acc[1] += a[j].y; acc[2] += a[j].z; acc[3] += a[j].w;
+          acc[4] += b[j].x; acc[5] += b[j].y; acc[6] += b[j].z; acc[7] += b[j].w;
+        }
       }
     }
     const float4 s0 = *reinterpret_cast<const float4*>(scale + col);

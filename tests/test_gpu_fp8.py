@@ -55,6 +55,14 @@ def test_stream_k(ops, M, K, N):
     _check(ops, M, K, N, seed=K + N)
 
 
+@pytest.mark.parametrize("M,K,N", [(8, 17408, 5120), (16, 6144, 4608)])
+def test_split_16(ops, M, K, N):
+    """At most 16 rows with few 256-column tiles: split-K 16, every column checked."""
+    import npn_native
+    assert npn_native.query("npn_fp8_matmul_split_k", M, K, N) == 16
+    _check(ops, M, K, N, seed=K + N)
+
+
 @pytest.mark.parametrize("M,N", [(8, 5120), (64, 17408), (256, 34816)])
 def test_verify_shapes_sampled(ops, M, N):
     rng = np.random.default_rng(M)

@@ -34,10 +34,11 @@ def _reduce_in_order(p, sc):
     return (acc * sc.reshape(1, -1)).to(torch.bfloat16)
 
 
-@pytest.mark.parametrize("K,N,S", [(17408, 5120, 8), (6144, 5120, 4), (5120, 16512, 2),
-                                   (5120, 14336, 2), (5120, 34816, 1)])
-def test_partials_reduce_to_matmul(ops, K, N, S):
-    M = 256
+@pytest.mark.parametrize("M,K,N,S", [(256, 17408, 5120, 8), (256, 6144, 5120, 4),
+                                     (256, 5120, 16512, 2), (256, 5120, 14336, 2),
+                                     (256, 5120, 34816, 1), (8, 17408, 5120, 16),
+                                     (64, 5120, 34816, 5)])
+def test_partials_reduce_to_matmul(ops, M, K, N, S):
     x, w, sc = _inputs(M, K, N, K + N)
     p = ops.fp8.matmul_partials(x, w)
     ref = ops.fp8.matmul(x, w, sc)
@@ -46,9 +47,10 @@ def test_partials_reduce_to_matmul(ops, K, N, S):
     assert torch.equal(_bits(_reduce_in_order(p, sc)), _bits(ref))
 
 
-@pytest.mark.parametrize("K", [17408, 6144])
-def test_residual_rms_norm_partials(ops, K):
-    M, H = 256, 5120
+@pytest.mark.parametrize("M,K", [(256, 17408), (256, 6144), (8, 17408), (13, 6144)])
+def test_residual_rms_norm_partials(ops, M, K):
+    """M = 8 and 13 run the narrow plan's split 16 (two batches of partial loads)."""
+    H = 5120
     x, w, sc = _inputs(M, K, H, K)
     g = torch.Generator(device="cuda").manual_seed(7)
     hid = (torch.randn(M, H, generator=g, device="cuda") * 2).to(torch.bfloat16)

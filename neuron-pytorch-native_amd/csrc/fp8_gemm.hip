@@ -765,6 +765,29 @@ __global__ void fp8_splitk_reduce_kernel(const float* __restrict__ partial,
   out[idx] = npn::f32_to_bf16(s * scale[idx % N]);
 }
 
+// SwiGLU of split-K partials of W = [gate | up] (N = 2 I): out[m][j] =
+// bf16(bf16(silu(g)) * u), g and u the bf16 outputs bf16(scale * sum_s partial[s]) of columns
+// j and I + j (the reduction above, then the glue kernel's SwiGLU rounding).
+__global__ void fp8_splitk_swiglu_kernel(const float* __restrict__ partial,
+                                         const float* __restrict__ scale,
+                                         uint16_t* __restrict__ out, int M, int N, int split_k) {
+  const int I = N / 2;
+  const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (size_t)M * I) return;
+  const size_t m = idx / I, j = idx - m * I;
+  const size_t total = (size_t)M * N;
+  const float* pg = partial + m * N + j;
+  float g = 0.f, u = 0.f;
+  for (int k = 0; k < split_k; ++k) {
+    g += pg[(size_t)k * total];
+    u += pg[(size_t)k * total + I];
+  }
+  const float gb = npn::bf16_to_f32(npn::f32_to_bf16(g * scale[j]));
+  const float ub = npn::bf16_to_f32(npn::f32_to_bf16(u * scale[I + j]));
+  const float sb = npn::bf16_to_f32(npn::f32_to_bf16(npn::silu(gb)));
+  out[idx] = npn::f32_to_bf16(sb * ub);
+}
+
 struct GemmPlan {
   int mt, passes, split_k;
   size_t ws;
@@ -998,6 +1021,14 @@ extern "C" int npn_fp8_matmul_swiglu(const uint16_t* x, const int8_t* w, const f
   uint16_t* gu = static_cast<uint16_t*>(workspace);
   const size_t gu_bytes = ((size_t)M * N * 2 + 255) & ~(size_t)255;
   float* part = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + gu_bytes);
+  if (p.split_k > 1) {  // the reduction and the SwiGLU in one pass over the partials
+    const int st = launch_gemm(p, x, w, scale, nullptr, part, M, K, N, 0, false, s);
+    if (st != NPN_OK) return st;
+    const size_t n = (size_t)M * (N / 2);
+    hipLaunchKernelGGL(fp8_splitk_swiglu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                       s, part, scale, out, M, N, p.split_k);
+    return npn_launch_status();
+  }
   const int st = launch_gemm(p, x, w, scale, gu, part, M, K, N, 0, true, s);
   if (st != NPN_OK) return st;
   return npn_silu_mul(gu, out, M, N / 2, stream);

@@ -31,8 +31,13 @@ def _bits(t):
 
 @pytest.mark.parametrize("M,K,N,fused", [
     (256, 5120, 34816, True), (100, 1024, 34816, True), (200, 2048, 26624, True),
-    (65, 640, 34816, True), (100, 1024, 4096, False), (48, 1024, 2048, False)])
+    (65, 640, 34816, True), (100, 1024, 4096, False), (48, 1024, 2048, False),
+    (8, 5120, 34816, False), (64, 2048, 34816, False), (8, 5120, 4096, False),
+    (16, 256, 1024, False)])
 def test_swiglu_fused_equals_unfused(ops, M, K, N, fused):
+    """Unfused shapes take the GEMM's partials through one reduce + SwiGLU kernel when the
+    plan splits K (stream-K at N = 34816, split 16 at M = 8, N = 4096) and the plain GEMM +
+    glue SwiGLU when it does not (K = 256)."""
     from npn_native import query
     # which path the shape takes: the fused epilogue needs no workspace
     assert (query("npn_fp8_matmul_swiglu_workspace_size", M, K, N) == 0) == fused

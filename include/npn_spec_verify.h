@@ -68,6 +68,31 @@ int npn_deltanet_full_batched(const float* state, const uint16_t* mixed_qkv,
                               uint16_t* new_conv_state, uint16_t* out, int B, int k_heads,
                               int v_heads, void* stream);
 
+/* torch.ops.deltanet.full_fp8 -- replaces the op registered at
+ * contrib/qwen3.6-27b/kernels/deltanet_full_fp8_ops.py:7-32 (kernel deltanet_full_fp8.py;
+ * called by the decode harness at B = 1 with fp8 weights, static_decode.py:784-797): the four
+ * fp8 W8A16 in-projections of one decode token folded into deltanet::full.
+ *   x [hidden] bf16 (one token of one sequence)
+ *   qkv_w [hidden, QKV], z_w [hidden, Hv*128], a_w, b_w [hidden, Hv]: e4m3fn bytes, [K, N]
+ *   qkv_s [QKV], z_s [Hv*128], a_s, b_s [Hv]: f32 per-output-channel scales
+ *   mixed_qkv = bf16((x . qkv_w) * qkv_s), z = bf16((x . z_w) * z_s),
+ *   a_out = (x . a_w) * a_s, b_out = (x . b_w) * b_s in f32 (not rounded), fp32 accumulation;
+ * then the token step of npn_deltanet_full_batched with B = 1 (same state, conv and parameter
+ * arguments, same outputs; new_conv_state must not overlap conv_state). mixed_qkv and z are
+ * bit-identical to npn_fp8_matmul's outputs. hidden % 64 == 0; workspace of
+ * npn_deltanet_full_fp8_workspace_size(hidden, k_heads, v_heads) bytes (0: unsupported sizes),
+ * 16-byte aligned. Four launches: the qkv and z GEMMs (split-K partials), one kernel that
+ * reduces them, shifts the conv window and computes a_out and b_out, then the token step. */
+size_t npn_deltanet_full_fp8_workspace_size(int hidden, int k_heads, int v_heads);
+int npn_deltanet_full_fp8(const uint16_t* x, const float* state, const uint16_t* conv_state,
+                          const float* conv_weight, const float* conv_bias, const float* A_log,
+                          const float* dt_bias, const float* norm_weight, const int8_t* qkv_w,
+                          const float* qkv_s, const int8_t* z_w, const float* z_s,
+                          const int8_t* a_w, const float* a_s, const int8_t* b_w,
+                          const float* b_s, float* new_state, uint16_t* new_conv_state,
+                          uint16_t* out, int hidden, int k_heads, int v_heads, void* workspace,
+                          size_t workspace_bytes, void* stream);
+
 /* torch.ops.deltanet.verify_batched -- new op (no reference counterpart; it runs
  * the token step of deltanet_full_batched_ops.py:22-41 over T = K+1 verify
  * tokens and keeps every intermediate state, the trajectory of
@@ -364,7 +389,7 @@ int npn_gqa_split(const uint16_t* proj, int ld, uint16_t* query, uint16_t* gate,
  *   bf16(scale[n] * (partial[0][m][n] + ... + partial[split_k-1][m][n])),
  * bit-identical to npn_fp8_matmul's output, so each result equals npn_fp8_matmul followed by
  * the bf16 op. partial [split_k][M][ld] f32 (ld = H for the norm), scale [ld] f32,
- * 1 <= split_k <= 8; other arguments as in the bf16 forms. */
+ * 1 <= split_k <= 16; other arguments as in the bf16 forms. */
 int npn_residual_rmsnorm_partials(const uint16_t* hidden_in, const float* partial, int split_k,
                                   const float* scale, const float* weight, uint16_t* hidden_out,
                                   uint16_t* normed, int M, int H, float eps, void* stream);

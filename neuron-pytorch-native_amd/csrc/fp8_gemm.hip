@@ -951,6 +951,112 @@ int launch_gemm(const GemmPlan& p, const uint16_t* x, const int8_t* w, const flo
   return npn_launch_status();
 }
 
+// The end of deltanet::full_fp8's in-projections, in one launch after the two GEMMs:
+//  - blocks [0, nq): the qkv GEMM's split-K partials reduced in slot order and scaled into
+//    bf16 mixed_qkv (the values npn_fp8_matmul writes; a sum of one slot is that slot), and the
+//    new conv window [conv_state[:, 1:] | mixed_qkv];
+//  - blocks [nq, nq + nz): the same reduction for z;
+//  - the last 2 * hv blocks: the thin in_proj_a / in_proj_b projections in float32, column n
+//    of matrix j per block: out_j[n] = (sum_k x[k] * W_j[k][n]) * scale_j[n], W_j [K, hv]
+//    e4m3fn bytes (rows hv bytes apart: the two matrices are a few hundred KB, read once from
+//    HBM and then from L2). Thread t adds k = t, t + 256, ... in order, then the wave sums
+//    (fixed butterfly) and the four waves in order: the same bits every run.
+struct InprojFinishArgs {
+  const float* pq;          // [sq][qkv] partials of x . qkv_w
+  const float* qs;
+  uint16_t* mixed;
+  const uint16_t* conv_in;  // [qkv][3]
+  uint16_t* conv_out;
+  const float* pz;          // [sz][zn] partials of x . z_w
+  const float* zs;
+  uint16_t* z;
+  const uint16_t* x;
+  const uint8_t* wa;
+  const float* sa;
+  float* a;
+  const uint8_t* wb;
+  const float* sb;
+  float* b;
+  int sq, qkv, sz, zn, K, hv;
+};
+
+__global__ __launch_bounds__(256) void dn_fp8_inproj_finish_kernel(InprojFinishArgs p) {
+  const int nq = (p.qkv + 255) / 256, nz = (p.zn + 255) / 256;
+  const int blk = blockIdx.x;
+  if (blk < nq + nz) {
+    const bool isq = blk < nq;
+    const int n = isq ? p.qkv : p.zn;
+    const int i = (isq ? blk : blk - nq) * 256 + threadIdx.x;
+    if (i >= n) return;
+    const float* P = isq ? p.pq : p.pz;
+    const int S = isq ? p.sq : p.sz;
+    float acc = P[i];
+    for (int k = 1; k < S; ++k) acc += P[(size_t)k * n + i];
+    const uint16_t v = npn::f32_to_bf16(acc * (isq ? p.qs : p.zs)[i]);
+    if (isq) {
+      p.mixed[i] = v;
+      p.conv_out[3 * i] = p.conv_in[3 * i + 1];
+      p.conv_out[3 * i + 1] = p.conv_in[3 * i + 2];
+      p.conv_out[3 * i + 2] = v;
+    } else {
+      p.z[i] = v;
+    }
+    return;
+  }
+  const int j = (blk - nq - nz) / p.hv, col = (blk - nq - nz) - j * p.hv;
+  const uint8_t* w = j ? p.wb : p.wa;
+  // U loads per thread in flight at once (one batch for HIDDEN = 5120); indices past K are
+  // clamped to K - 1 so the loads need no branch, and their products are not added
+  constexpr int U = 20;
+  float acc = 0.f;
+  for (int k0 = threadIdx.x; k0 < p.K; k0 += 256 * U) {
+    float xv[U], wv[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int k = min(k0 + 256 * u, p.K - 1);
+      xv[u] = npn::bf16_to_f32(p.x[k]);
+      wv[u] = npn::bf16lo(fp8x2_to_bf16x2<false>(w[(size_t)k * p.hv + col]));
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (k0 + 256 * u < p.K) acc += xv[u] * wv[u];
+  }
+  acc = npn::wave_sum(acc);
+  __shared__ float part[4];
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const float sc = (j ? p.sb : p.sa)[col];
+    (j ? p.b : p.a)[col] = (((part[0] + part[1]) + part[2]) + part[3]) * sc;
+  }
+}
+
+// Workspace of npn_deltanet_full_fp8, 256-byte aligned regions: mixed_qkv [QKV] bf16, z
+// [Hv * 128] bf16, a_out and b_out [Hv] f32, then the split-K partials of the qkv and z GEMMs
+// ([S][N] f32 each, S from the GEMM plan for one row).
+struct FullFp8Layout {
+  size_t z, a, b, pq, pz, total;
+  int sq, sz;
+};
+
+FullFp8Layout full_fp8_layout(int H, int qkv, int hv) {
+  auto up = [](size_t n) { return (n + 255) & ~(size_t)255; };
+  FullFp8Layout l;
+  l.sq = plan(1, H, qkv).split_k;
+  l.sz = plan(1, H, hv * 128).split_k;
+  l.z = up((size_t)qkv * 2);
+  l.a = l.z + up((size_t)hv * 128 * 2);
+  l.b = l.a + up((size_t)hv * 4);
+  l.pq = l.b + up((size_t)hv * 4);
+  l.pz = l.pq + up((size_t)l.sq * qkv * 4);
+  l.total = l.pz + up((size_t)l.sz * hv * 128 * 4);
+  return l;
+}
+
+bool full_fp8_heads_ok(int k_heads, int v_heads) {
+  return k_heads > 0 && v_heads > 0 && v_heads % k_heads == 0 && v_heads <= 4096;
+}
+
 }  // namespace
 
 extern "C" size_t npn_fp8_matmul_workspace_size(int M, int K, int N) {
@@ -1066,4 +1172,59 @@ extern "C" int npn_fp8_matmul_rowmax(const uint16_t* x, const int8_t* w, const f
   const GemmPlan p = plan(M, K, N, true);
   return launch_gemm(p, x, w, scale, out, nullptr, M, K, N, 0, false,
                      static_cast<hipStream_t>(stream), nullptr, false, gmax);
+}
+
+// deltanet::full_fp8: the four in-projections of one decode token, then the token step of
+// deltanet::full on their outputs. Four launches: the qkv and z GEMMs writing split-K partials
+// (the plans of npn_fp8_matmul for one row), the finishing kernel above (mixed_qkv and z as
+// npn_fp8_matmul's bf16 outputs, the new conv window, a_out and b_out in float32, not rounded),
+// and the DeltaNet token step (npn_deltanet_verify with T = 1).
+extern "C" size_t npn_deltanet_full_fp8_workspace_size(int hidden, int k_heads, int v_heads) {
+  if (!full_fp8_heads_ok(k_heads, v_heads)) return 0;
+  const int qkv = (2 * k_heads + v_heads) * 128;
+  if (!shape_ok(1, hidden, qkv)) return 0;
+  return full_fp8_layout(hidden, qkv, v_heads).total;
+}
+
+extern "C" int npn_deltanet_full_fp8(
+    const uint16_t* x, const float* state, const uint16_t* conv_state, const float* conv_weight,
+    const float* conv_bias, const float* A_log, const float* dt_bias, const float* norm_weight,
+    const int8_t* qkv_w, const float* qkv_s, const int8_t* z_w, const float* z_s,
+    const int8_t* a_w, const float* a_s, const int8_t* b_w, const float* b_s, float* new_state,
+    uint16_t* new_conv_state, uint16_t* out, int hidden, int k_heads, int v_heads,
+    void* workspace, size_t workspace_bytes, void* stream) {
+  NPN_REQUIRE(x && state && conv_state && conv_weight && conv_bias && A_log && dt_bias &&
+                  norm_weight && qkv_w && qkv_s && z_w && z_s && a_w && a_s && b_w && b_s &&
+                  new_state && new_conv_state && out,
+              NPN_ERR_NULL);
+  NPN_REQUIRE(full_fp8_heads_ok(k_heads, v_heads), NPN_ERR_SHAPE);
+  const int qkv = (2 * k_heads + v_heads) * 128, zn = v_heads * 128;
+  NPN_REQUIRE(shape_ok(1, hidden, qkv), NPN_ERR_SHAPE);
+  NPN_REQUIRE(NPN_ALIGNED16(x) && NPN_ALIGNED16(qkv_w) && NPN_ALIGNED16(z_w), NPN_ERR_ALIGN);
+  // the new conv window is written before the token step reads the old one
+  NPN_REQUIRE(new_conv_state != conv_state, NPN_ERR_VALUE);
+  const FullFp8Layout l = full_fp8_layout(hidden, qkv, v_heads);
+  NPN_REQUIRE(workspace != nullptr && workspace_bytes >= l.total, NPN_ERR_WORKSPACE);
+  NPN_REQUIRE(NPN_ALIGNED16(workspace), NPN_ERR_ALIGN);
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  float* pq = reinterpret_cast<float*>(ws + l.pq);
+  float* pz = reinterpret_cast<float*>(ws + l.pz);
+  int st = launch_gemm(plan(1, hidden, qkv), x, qkv_w, nullptr, nullptr, pq, 1, hidden, qkv, 1,
+                       false, s);
+  if (st != NPN_OK) return st;
+  st = launch_gemm(plan(1, hidden, zn), x, z_w, nullptr, nullptr, pz, 1, hidden, zn, 1, false, s);
+  if (st != NPN_OK) return st;
+  InprojFinishArgs fa{pq, qkv_s, reinterpret_cast<uint16_t*>(ws), conv_state, new_conv_state,
+                      pz, z_s, reinterpret_cast<uint16_t*>(ws + l.z), x,
+                      reinterpret_cast<const uint8_t*>(a_w), a_s, reinterpret_cast<float*>(ws + l.a),
+                      reinterpret_cast<const uint8_t*>(b_w), b_s, reinterpret_cast<float*>(ws + l.b),
+                      l.sq, qkv, l.sz, zn, hidden, v_heads};
+  const int blocks = (qkv + 255) / 256 + (zn + 255) / 256 + 2 * v_heads;
+  hipLaunchKernelGGL(dn_fp8_inproj_finish_kernel, dim3(blocks), dim3(256), 0, s, fa);
+  st = npn_launch_status();
+  if (st != NPN_OK) return st;
+  return npn_deltanet_verify(state, nullptr, 0, fa.mixed, conv_state, conv_weight, conv_bias,
+                             fa.a, fa.b, fa.z, A_log, dt_bias, norm_weight, new_state, out, 1, 1,
+                             k_heads, v_heads, stream);
 }

@@ -57,6 +57,8 @@ SIGNATURES = {
     "npn_accept_rejection_lm_head": (_I, [_P] * 7 + [_F] + [_P] * 3 + [_I] * 4 + [_P, _Z, _P]),
     "npn_deltanet_chunked_workspace_size": (_Z, [_I, _I]),
     "npn_deltanet_chunked_prefill": (_I, [_P] * 8 + [_I, _I, _P, _Z, _P]),
+    "npn_deltanet_full_fp8_workspace_size": (_Z, [_I] * 3),
+    "npn_deltanet_full_fp8": (_I, [_P] * 19 + [_I] * 3 + [_P, _Z, _P]),
 }
 
 _lib = None

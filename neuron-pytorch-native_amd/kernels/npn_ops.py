@@ -1,7 +1,7 @@
 """Import every op module once, registering all torch.ops of the library:
 
-  torch.ops.deltanet.{full, full_batched, verify_batched, verify_from_ckpt, rollback,
-                      conv_rollback, chunked_prefill}
+  torch.ops.deltanet.{full, full_batched, full_fp8, verify_batched, verify_from_ckpt,
+                      rollback, conv_rollback, chunked_prefill}
   torch.ops.gqa.{tail, tail_verify, kv_append}
   torch.ops.fp8.{matmul, matmul_partials, matmul_argmax, matmul_swiglu}
   torch.ops.spec.{accept_greedy, accept_rejection}
@@ -14,6 +14,7 @@ the same way here.)
 """
 import deltanet_full_ops  # noqa: F401
 import deltanet_full_batched_ops  # noqa: F401
+import deltanet_full_fp8_ops  # noqa: F401
 import deltanet_verify_ops  # noqa: F401
 import deltanet_chunked_ops  # noqa: F401
 import gqa_tail_ops  # noqa: F401

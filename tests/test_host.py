@@ -31,7 +31,7 @@ def test_library_exports_every_declared_symbol():
 def test_status_strings_and_version():
     import npn_native
     lib = npn_native.lib()
-    assert lib.npn_abi_version() == 100
+    assert lib.npn_abi_version() == 101
     assert lib.npn_status_string(0) == b"ok"
     for code in range(1, 7):
         assert lib.npn_status_string(code) not in (b"ok", b"unknown status")
@@ -53,6 +53,13 @@ def test_size_queries():
     assert q("npn_deltanet_chunked_workspace_size", 3, 65) == 3 * 2 * 34048
     assert q("npn_deltanet_chunked_workspace_size", 0, 64) == 0
     assert q("npn_deltanet_chunked_workspace_size", 1, (1 << 22) + 1) == 0     # 32-bit offsets
+    # full_fp8: mixed_qkv and z (bf16), a and b (f32), each 256-byte aligned, then the split-K
+    # partials [S][N] f32 of the qkv and z GEMMs
+    fixed = 10240 * 2 + 6144 * 2 + 256 + 256
+    parts = sum(q("npn_fp8_matmul_split_k", 1, 5120, n) * n * 4 for n in (10240, 6144))
+    assert q("npn_deltanet_full_fp8_workspace_size", 5120, 16, 48) == fixed + parts
+    assert q("npn_deltanet_full_fp8_workspace_size", 5100, 16, 48) == 0        # hidden % 64
+    assert q("npn_deltanet_full_fp8_workspace_size", 5120, 5, 48) == 0         # Hv % Hk
 
 
 def test_ops_register_and_propagate_shapes():
@@ -117,6 +124,16 @@ def test_ops_register_and_propagate_shapes():
         c, sn = torch.ops.gqa.rope_rows(torch.empty(100, 64), torch.empty(100, 64),
                                         torch.empty(B, dtype=torch.int32), T)
         assert c.shape == sn.shape == (B, T, 64) and c.dtype == f32
+        i8 = torch.int8
+        ns, nc, g = torch.ops.deltanet.full_fp8(
+            torch.empty(1, 5120, dtype=bf), torch.empty(Hv * D, D), torch.empty(QKV, 3, dtype=bf),
+            torch.empty(QKV, 4), torch.empty(QKV), torch.empty(Hv), torch.empty(Hv),
+            torch.empty(D), torch.empty(5120, QKV, dtype=i8), torch.empty(QKV, 1),
+            torch.empty(5120, Hv * D, dtype=i8), torch.empty(Hv * D, 1),
+            torch.empty(5120, Hv, dtype=i8), torch.empty(Hv, 1), torch.empty(5120, Hv, dtype=i8),
+            torch.empty(Hv, 1))
+        assert ns.shape == (Hv * D, D) and nc.shape == (QKV, 3) and g.shape == (Hv, D)
+        assert g.dtype == bf and nc.dtype == bf
 
 
 def test_fp8_split_k_plan():

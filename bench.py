@@ -64,6 +64,9 @@ def parse():
     p.add_argument("--config", type=int, choices=(1, 2, 3),
                    help="one kernel at its workload's shapes: 1 DeltaNet verify at B = 1, 8, "
                         "32; 2 GQA verify attention at B = 16; 3 the FP8 GEMM at nine shapes")
+    p.add_argument("--full-fp8", action="store_true",
+                   help="time deltanet::full_fp8 (one decode token, fp8 in-projections) at the "
+                        "reference's per-rank heads (4/12) and full width (16/48)")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only run a plain 1 GiB device copy 5 times (scales HBM byte counters)")
     return p.parse_args()
@@ -420,6 +423,69 @@ def config1_bench(args):
         "warmup": max(args.warmup, CFG_MIN_WARMUP)}))
 
 
+def full_fp8_bytes(hk, hv, hidden=5120, d=128):
+    """Algorithmic bytes of one deltanet::full_fp8 call: the four fp8 weight matrices and their
+    scales, x, the state in and out, the conv window in and out, the conv weight and bias,
+    A_log, dt_bias, norm weight and the bf16 output."""
+    qkv, zn = (2 * hk + hv) * d, hv * d
+    n = qkv + zn + 2 * hv
+    return (hidden * n + 4 * n + 2 * hidden + 2 * hv * d * d * 4 + qkv * 3 * 2 * 2
+            + qkv * 5 * 4 + 2 * hv * 4 + d * 4 + hv * d * 2)
+
+
+def full_fp8_bench(args):
+    """deltanet::full_fp8: one decode token of one sequence through the four fp8
+    in-projections (HIDDEN 5120 -> qkv, z, a, b) and the DeltaNet token step, at the
+    reference's per-rank heads (4 k / 12 v) and full width (16 / 48). Weights are e4m3 codes
+    of N(0, 0.02) quantised per channel (clip +-448), x bf16 N(0,1), states fp32 N(0, 0.1);
+    four copies of the weights and states are used in turn (360 MB at full width, above the
+    256 MB memory-side cache), so the weights come from HBM."""
+    import torch
+    import npn_ops  # noqa: F401
+    dev, H, D = "cuda", 5120, 128
+    rows = []
+    for hk, hv in ((4, 12), (16, 48)):
+        qkv = (2 * hk + hv) * D
+        g = torch.Generator(device=dev).manual_seed(args.seed + hv)
+
+        def weights(n):
+            w = (torch.randn(n, H, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+            sc = w.abs().amax(-1).float().clamp_min(1e-12) / 448.0
+            q = (w * (1.0 / sc).to(torch.bfloat16)[:, None]).clamp(-448, 448)
+            return q.to(torch.float8_e4m3fn).view(torch.int8).t().contiguous(), sc.reshape(n, 1)
+
+        shared = [torch.randn(1, H, generator=g, device=dev).to(torch.bfloat16),
+                  None,
+                  torch.randn(qkv, 3, generator=g, device=dev).to(torch.bfloat16),
+                  torch.randn(qkv, 4, generator=g, device=dev) * 0.5,
+                  torch.randn(qkv, generator=g, device=dev) * 0.1,
+                  torch.randn(hv, generator=g, device=dev) * 0.5,
+                  torch.randn(hv, generator=g, device=dev),
+                  torch.randn(D, generator=g, device=dev) * 0.1 + 1.0]
+        sets = []
+        for _ in range(4):
+            a = list(shared)
+            a[1] = torch.randn(hv * D, D, generator=g, device=dev) * 0.1
+            for n in (qkv, hv * D, hv, hv):
+                a += list(weights(n))
+            sets.append(a)
+
+        def call(i):
+            return torch.ops.deltanet.full_fp8(*sets[i % 4])
+
+        ms = time_calls(call, args.steps, args.warmup)
+        row = {"k_heads": hk, "v_heads": hv, "ms": round(ms, 4)}
+        row.update(hbm_row(full_fp8_bytes(hk, hv), ms))
+        rows.append(row)
+        del sets
+    print(json.dumps({
+        "workload": "deltanet::full_fp8, one decode token of one sequence, HIDDEN 5120, fp8 "
+                    "in-projections (qkv, z, a, b) + DeltaNet token step",
+        "kernel": "deltanet.full_fp8 (two narrow fp8 GEMMs, dn_fp8_inproj_finish_kernel, "
+                  "dn_verify_kernel)", "bound": "hbm", "peak": HBM_PEAK_GBS, "rows": rows,
+        "steps": args.steps, "warmup": max(args.warmup, CFG_MIN_WARMUP)}))
+
+
 def config2_bench(args):
     """GQA verify attention: B = 16, T = 8 causal query rows, 24 q / 4 kv heads of 256, partial
     RoPE (64 dims, theta 1e7), bf16 N(0,1) KV cache with per-sequence lengths U{4096..32768}
@@ -686,6 +752,9 @@ def main():
         return
     if args.lm_head:
         lm_head_bench(args)
+        return
+    if args.full_fp8:
+        full_fp8_bench(args)
         return
     if args.config:
         (config1_bench, config2_bench, config3_bench)[args.config - 1](args)

@@ -63,7 +63,8 @@ __device__ __forceinline__ s16x4 lds_tr16(const uint8_t* p) {
 
 // ---------------------------------------------------------------------------------------
 // 1. q' = rope((1+w) * rmsnorm(q)) * log2(e)/16, split into bf16 hi/lo.
-//    One wave per padded query row (b, g, r); lane l owns dims 4l..4l+3.
+//    One wave per padded query row (b, g, r); lane l owns dims 4l..4l+3. Block 0 of the same
+//    launch writes the split-KV plan instead (pstart, below), which the attention reads.
 struct QPrepArgs {
   const uint16_t* query;
   const float* q_norm;
@@ -71,11 +72,45 @@ struct QPrepArgs {
   const float* sin;
   uint16_t* qhi;   // [B][Hkv][R][DH]
   uint16_t* qlo;
-  int B, T, Hq, Hkv, R;
+  const int32_t* kv_len;
+  int32_t* pstart;  // [P + 1]
+  int B, T, Hq, Hkv, R, P, s_max;
 };
 
+__device__ __forceinline__ int pair_kend(const int32_t* kv_len, int b, int T, int s_max);
+
+// The plan: pstart[p] = sum of the steps of pairs before p (exclusive scan over one block of
+// 256 threads), pstart[P] = all steps.
+__device__ void plan_block(const int32_t* kv_len, int32_t* pstart, int P, int Hkv, int T,
+                           int s_max) {
+  __shared__ int part[256];
+  const int t = threadIdx.x;
+  const int per = (P + 255) / 256;
+  const int p0 = min(P, t * per), p1 = min(P, p0 + per);
+  int sum = 0;
+  for (int p = p0; p < p1; ++p) sum += (pair_kend(kv_len, p / Hkv, T, s_max) + KS - 1) / KS;
+  part[t] = sum;
+  __syncthreads();
+  for (int off = 1; off < 256; off <<= 1) {  // inclusive Hillis-Steele scan
+    const int v = t >= off ? part[t - off] : 0;
+    __syncthreads();
+    part[t] += v;
+    __syncthreads();
+  }
+  int run = part[t] - sum;
+  for (int p = p0; p < p1; ++p) {
+    pstart[p] = run;
+    run += (pair_kend(kv_len, p / Hkv, T, s_max) + KS - 1) / KS;
+  }
+  if (t == 255) pstart[P] = part[255];
+}
+
 __global__ __launch_bounds__(256) void gqa_qprep_kernel(QPrepArgs a) {
-  const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (blockIdx.x == 0) {
+    plan_block(a.kv_len, a.pstart, a.P, a.Hkv, a.T, a.s_max);
+    return;
+  }
+  const int wave = (blockIdx.x - 1) * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int grp = a.Hq / a.Hkv;
   if (wave >= a.B * a.Hkv * a.R) return;
@@ -164,31 +199,6 @@ __device__ __forceinline__ int attn_wgs(int S) {
 // Workgroup w's step range is [w * S / W, (w + 1) * S / W), W = attn_wgs(S).
 __device__ __forceinline__ int wg_first_step(int w, int S) {
   return (int)((int64_t)w * S / attn_wgs(S));
-}
-
-// One-block plan: pstart[p] = sum of the steps of pairs before p (exclusive scan).
-__global__ __launch_bounds__(1024) void gqa_plan_kernel(const int32_t* kv_len, int32_t* pstart,
-                                                        int P, int Hkv, int T, int s_max) {
-  __shared__ int part[1024];
-  const int t = threadIdx.x;
-  const int per = (P + 1023) / 1024;
-  const int p0 = min(P, t * per), p1 = min(P, p0 + per);
-  int sum = 0;
-  for (int p = p0; p < p1; ++p) sum += (pair_kend(kv_len, p / Hkv, T, s_max) + KS - 1) / KS;
-  part[t] = sum;
-  __syncthreads();
-  for (int off = 1; off < 1024; off <<= 1) {  // inclusive Hillis-Steele scan
-    const int v = t >= off ? part[t - off] : 0;
-    __syncthreads();
-    part[t] += v;
-    __syncthreads();
-  }
-  int run = part[t] - sum;
-  for (int p = p0; p < p1; ++p) {
-    pstart[p] = run;
-    run += (pair_kend(kv_len, p / Hkv, T, s_max) + KS - 1) / KS;
-  }
-  if (t == 1023) pstart[P] = part[1023];
 }
 
 // Largest p in [0, P) with pstart[p] <= x (pstart is strictly increasing, pstart[0] = 0):
@@ -736,12 +746,10 @@ extern "C" int npn_gqa_tail_verify(const uint16_t* query, const uint16_t* gate,
   float* pml = reinterpret_cast<float*>(ws + 2 * p.q_bytes + p.po_bytes);
   int32_t* pstart = reinterpret_cast<int32_t*>(ws + 2 * p.q_bytes + p.po_bytes + p.pml_bytes);
 
-  hipLaunchKernelGGL(gqa_plan_kernel, dim3(1), dim3(1024), 0, s, kv_len, pstart, p.P, kv_heads,
-                     T, s_max);
-
-  QPrepArgs qa{query, q_norm, cos, sin, qhi, qlo, B, T, q_heads, kv_heads, p.R};
+  QPrepArgs qa{query, q_norm, cos, sin, qhi, qlo, kv_len, pstart, B, T, q_heads, kv_heads, p.R,
+               p.P, s_max};
   const int rows = B * kv_heads * p.R;
-  hipLaunchKernelGGL(gqa_qprep_kernel, dim3((rows + 3) / 4), dim3(256), 0, s, qa);
+  hipLaunchKernelGGL(gqa_qprep_kernel, dim3(1 + (rows + 3) / 4), dim3(256), 0, s, qa);
 
   AttnArgs aa{qhi, qlo, cache_k, cache_v, kv_len, pstart, po, pml, kv_heads, s_max, T, p.grp, p.P};
   const dim3 grid(kAttnWG);

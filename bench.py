@@ -134,6 +134,8 @@ def algorithmic(name, kv_len_mean_rows):
         return "hbm", dn_verify_bytes(B), "B"
     if name == "gqa.tail_verify":
         return "hbm", gqa_verify_bytes([kv_len_mean_rows] * B), "B"
+    if name == "gqa.tail_verify_append":  # + the new K/V rows read and written to the cache
+        return "hbm", gqa_verify_bytes([kv_len_mean_rows] * B) + 4 * B * T * 4 * 256 * 2, "B"
     if name == "spec.accept_rejection":
         return "hbm", (B * (2 * K + 1) * V + 2 * B * V) * 4, "B"
     if name.startswith(("fp8.matmul[", "fp8.matmul_swiglu[")):

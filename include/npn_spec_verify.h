@@ -188,6 +188,25 @@ int npn_gqa_kv_append(const uint16_t* key, const uint16_t* value, const float* k
                       const int32_t* kv_len, int B, int T, int kv_heads, int s_max,
                       void* stream);
 
+/* torch.ops.gqa.tail_verify_append -- new op: the whole k-side and attention of
+ * _gqa_layer (contrib/qwen3.6-27b/static_decode.py:880-931) in the verify tail's
+ * launches: npn_gqa_kv_append followed by npn_gqa_tail_verify, with the RoPE rows read
+ * from the position tables (the reference's _init_rope, static_decode.py:489-502) at
+ * row kv_len[b] + t clamped to [0, positions) -- the rows npn_rope_rows gathers. The
+ * append runs in the query-prep launch, so this is two launches fewer than
+ * npn_rope_rows + npn_gqa_kv_append + npn_gqa_tail_verify, whose results (out and the
+ * appended cache rows) it equals bit for bit.
+ *   key, value [B, T, Hkv, 256] bf16; k_norm [256] f32;
+ *   cos_table, sin_table [positions, 64] f32 (16-byte aligned);
+ *   other arguments, limits and workspace (npn_gqa_tail_verify_workspace_size) as
+ *   npn_gqa_tail_verify; cache_k/v are written at rows kv_len[b]+t < s_max. */
+int npn_gqa_tail_verify_append(const uint16_t* query, const uint16_t* gate, const uint16_t* key,
+                               const uint16_t* value, const float* q_norm, const float* k_norm,
+                               const float* cos_table, const float* sin_table, int positions,
+                               uint16_t* cache_k, uint16_t* cache_v, const int32_t* kv_len,
+                               uint16_t* out, int B, int T, int q_heads, int kv_heads, int s_max,
+                               void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---------------------------------------------------------------------------
  * FP8 W8A16 GEMM.
  * ------------------------------------------------------------------------- */

@@ -9,6 +9,9 @@
 // Verify tail (T tokens x grp q-heads per kv head = R query rows per (b, kv head)):
 //  1. qprep: q' per row, scaled by log2(e)/16 and split into bf16 hi + lo parts
 //     (hi = bf16(q'), lo = bf16(q' - hi)), so the bf16 MFMA sees q' to ~16 mantissa bits.
+//     Block 0 of the same launch writes the split-KV plan; with the fused append
+//     (npn_gqa_tail_verify_append) further blocks append the T new K/V rows to the cache,
+//     and the RoPE rows come straight from the position table.
 //  2. attn: split-KV over a balanced partition. The (b, kv head) pairs' 32-key steps
 //     are laid end to end (prefix sums from a one-block plan kernel) and cut into
 //     W = min(kAttnWG, S / 16) equal ranges (S steps in all), one per workgroup of the
@@ -62,19 +65,89 @@ __device__ __forceinline__ s16x4 lds_tr16(const uint8_t* p) {
 }
 
 // ---------------------------------------------------------------------------------------
+// RoPE rows of verify position (b, t): the caller's [B, T, 64] rows, or with a table [P, 64]
+// (the reference's _init_rope table, contrib/qwen3.6-27b/static_decode.py:489-502) its row
+// kv_len[b] + t clamped to [0, P), the rows gqa::rope_rows would gather.
+struct RopeSrc {
+  const float* cos;   // [B, T, 64], or the table [P, 64] when P > 0
+  const float* sin;
+  int P;
+};
+
+__device__ __forceinline__ size_t rope_row(const RopeSrc& r, const int32_t* kv_len, int b, int t,
+                                           int T) {
+  if (r.P <= 0) return ((size_t)b * T + t) * ROPE;
+  long pos = (long)kv_len[b] + t;
+  pos = pos < 0 ? 0 : (pos >= r.P ? r.P - 1 : pos);
+  return (size_t)pos * ROPE;
+}
+
+// ---------------------------------------------------------------------------------------
+// KV append: cache row kv_len[b]+t of head g <- bf16(rope(bf16(rmsnorm_1p(key)))), value copy.
+// One wave per (b, t, g); lane l owns dims 4l..4l+3.
+struct AppendArgs {
+  const uint16_t* key;
+  const uint16_t* value;
+  const float* k_norm;
+  RopeSrc rope;
+  uint16_t* cache_k;
+  uint16_t* cache_v;
+  const int32_t* kv_len;
+  int B, T, Hkv, s_max;
+};
+
+__device__ __forceinline__ void kv_append_wave(const AppendArgs& a, int wave, int lane) {
+  if (wave >= a.B * a.T * a.Hkv) return;
+  const int g = wave % a.Hkv;
+  const int bt = wave / a.Hkv;
+  const int b = bt / a.T, t = bt - b * a.T;
+  const int pos = a.kv_len[b] + t;
+  if (pos < 0 || pos >= a.s_max) return;
+  const uint16_t* src = a.key + (size_t)wave * DH + 4 * lane;
+  float x[4];
+  float ss = 0.f;
+  for (int j = 0; j < 4; ++j) {
+    x[j] = npn::bf16_to_f32(src[j]);
+    ss += x[j] * x[j];
+  }
+  ss = npn::wave_sum(ss);
+  const float rn = rsqrtf(ss * (1.0f / DH) + kEps);
+  for (int j = 0; j < 4; ++j)
+    x[j] = npn::bf16_to_f32(npn::f32_to_bf16((1.0f + a.k_norm[4 * lane + j]) * (x[j] * rn)));
+  float y[4];
+  for (int j = 0; j < 4; ++j) y[j] = __shfl_xor(x[j], 8, 64);
+  if (lane < ROPE / 4) {
+    const size_t ro = rope_row(a.rope, a.kv_len, b, t, a.T) + 4 * lane;
+    const float* cs = a.rope.cos + ro;
+    const float* sn = a.rope.sin + ro;
+    const float sign = lane < ROPE / 8 ? -1.0f : 1.0f;
+    for (int j = 0; j < 4; ++j) x[j] = x[j] * cs[j] + sign * y[j] * sn[j];
+  }
+  const size_t row = (((size_t)b * a.Hkv + g) * a.s_max + pos) * DH + 4 * lane;
+  for (int j = 0; j < 4; ++j) a.cache_k[row + j] = npn::f32_to_bf16(x[j]);
+  const uint16_t* vs = a.value + (size_t)wave * DH + 4 * lane;
+  for (int j = 0; j < 4; ++j) a.cache_v[row + j] = vs[j];
+}
+
+__global__ __launch_bounds__(256) void gqa_kv_append_kernel(AppendArgs a) {
+  kv_append_wave(a, blockIdx.x * 4 + (threadIdx.x >> 6), threadIdx.x & 63);
+}
+
+// ---------------------------------------------------------------------------------------
 // 1. q' = rope((1+w) * rmsnorm(q)) * log2(e)/16, split into bf16 hi/lo.
 //    One wave per padded query row (b, g, r); lane l owns dims 4l..4l+3. Block 0 of the same
 //    launch writes the split-KV plan instead (pstart, below), which the attention reads.
 struct QPrepArgs {
   const uint16_t* query;
   const float* q_norm;
-  const float* cos;
-  const float* sin;
+  RopeSrc rope;
   uint16_t* qhi;   // [B][Hkv][R][DH]
   uint16_t* qlo;
   const int32_t* kv_len;
   int32_t* pstart;  // [P + 1]
   int B, T, Hq, Hkv, R, P, s_max;
+  int qblocks;      // blocks 1..qblocks prepare q'; any blocks after them append the new
+  AppendArgs app;   // K/V rows to the cache (app.key != nullptr), one wave per row
 };
 
 __device__ __forceinline__ int pair_kend(const int32_t* kv_len, int b, int T, int s_max);
@@ -110,6 +183,10 @@ __global__ __launch_bounds__(256) void gqa_qprep_kernel(QPrepArgs a) {
     plan_block(a.kv_len, a.pstart, a.P, a.Hkv, a.T, a.s_max);
     return;
   }
+  if ((int)blockIdx.x > a.qblocks) {
+    kv_append_wave(a.app, (blockIdx.x - 1 - a.qblocks) * 4 + (threadIdx.x >> 6), threadIdx.x & 63);
+    return;
+  }
   const int wave = (blockIdx.x - 1) * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int grp = a.Hq / a.Hkv;
@@ -138,8 +215,9 @@ __global__ __launch_bounds__(256) void gqa_qprep_kernel(QPrepArgs a) {
   float y[4];
   for (int j = 0; j < 4; ++j) y[j] = __shfl_xor(x[j], 8, 64);
   if (lane < ROPE / 4) {
-    const float* cs = a.cos + ((size_t)b * a.T + t) * ROPE + 4 * lane;
-    const float* sn = a.sin + ((size_t)b * a.T + t) * ROPE + 4 * lane;
+    const size_t ro = rope_row(a.rope, a.kv_len, b, t, a.T) + 4 * lane;
+    const float* cs = a.rope.cos + ro;
+    const float* sn = a.rope.sin + ro;
     const float sign = lane < ROPE / 8 ? -1.0f : 1.0f;  // rotate_half = cat(-x[32:], x[:32])
     for (int j = 0; j < 4; ++j) x[j] = x[j] * cs[j] + sign * y[j] * sn[j];
   }
@@ -547,55 +625,6 @@ __global__ __launch_bounds__(256) void gqa_merge_kernel(MergeArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------
-// KV append: cache row kv_len[b]+t of head g <- bf16(rope(bf16(rmsnorm_1p(key)))), value copy.
-// One wave per (b, t, g); lane l owns dims 4l..4l+3.
-struct AppendArgs {
-  const uint16_t* key;
-  const uint16_t* value;
-  const float* k_norm;
-  const float* cos;
-  const float* sin;
-  uint16_t* cache_k;
-  uint16_t* cache_v;
-  const int32_t* kv_len;
-  int B, T, Hkv, s_max;
-};
-
-__global__ __launch_bounds__(256) void gqa_kv_append_kernel(AppendArgs a) {
-  const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (wave >= a.B * a.T * a.Hkv) return;
-  const int g = wave % a.Hkv;
-  const int bt = wave / a.Hkv;
-  const int b = bt / a.T, t = bt - b * a.T;
-  const int pos = a.kv_len[b] + t;
-  if (pos < 0 || pos >= a.s_max) return;
-  const uint16_t* src = a.key + (size_t)wave * DH + 4 * lane;
-  float x[4];
-  float ss = 0.f;
-  for (int j = 0; j < 4; ++j) {
-    x[j] = npn::bf16_to_f32(src[j]);
-    ss += x[j] * x[j];
-  }
-  ss = npn::wave_sum(ss);
-  const float rn = rsqrtf(ss * (1.0f / DH) + kEps);
-  for (int j = 0; j < 4; ++j)
-    x[j] = npn::bf16_to_f32(npn::f32_to_bf16((1.0f + a.k_norm[4 * lane + j]) * (x[j] * rn)));
-  float y[4];
-  for (int j = 0; j < 4; ++j) y[j] = __shfl_xor(x[j], 8, 64);
-  if (lane < ROPE / 4) {
-    const float* cs = a.cos + ((size_t)b * a.T + t) * ROPE + 4 * lane;
-    const float* sn = a.sin + ((size_t)b * a.T + t) * ROPE + 4 * lane;
-    const float sign = lane < ROPE / 8 ? -1.0f : 1.0f;
-    for (int j = 0; j < 4; ++j) x[j] = x[j] * cs[j] + sign * y[j] * sn[j];
-  }
-  const size_t row = (((size_t)b * a.Hkv + g) * a.s_max + pos) * DH + 4 * lane;
-  for (int j = 0; j < 4; ++j) a.cache_k[row + j] = npn::f32_to_bf16(x[j]);
-  const uint16_t* vs = a.value + (size_t)wave * DH + 4 * lane;
-  for (int j = 0; j < 4; ++j) a.cache_v[row + j] = vs[j];
-}
-
-// ---------------------------------------------------------------------------------------
 // Decode tail of the reference op (fp32 cache, one kv head, mask shared over the batch).
 // One 256-thread block per sequence b handles its Hq rows; keys in blocks of 64, online
 // softmax in fp32. Wave w scores keys w, w+4, ...: lane l holds dims 4l..4l+3.
@@ -725,13 +754,15 @@ extern "C" size_t npn_gqa_tail_verify_workspace_size(int B, int T, int q_heads, 
   return plan(B, T, q_heads, kv_heads).total;
 }
 
-extern "C" int npn_gqa_tail_verify(const uint16_t* query, const uint16_t* gate,
-                                   const float* q_norm, const float* cos, const float* sin,
-                                   const uint16_t* cache_k, const uint16_t* cache_v,
-                                   const int32_t* kv_len, uint16_t* out, int B, int T,
-                                   int q_heads, int kv_heads, int s_max, void* workspace,
-                                   size_t workspace_bytes, void* stream) {
-  NPN_REQUIRE(query && gate && q_norm && cos && sin && cache_k && cache_v && kv_len && out,
+// The verify tail's launches; with app.key set the query-prep launch also appends the new
+// K/V rows (the attention launch that follows reads them).
+static int tail_verify_launch(const uint16_t* query, const uint16_t* gate, const float* q_norm,
+                              RopeSrc rope, const AppendArgs& app, const uint16_t* cache_k,
+                              const uint16_t* cache_v, const int32_t* kv_len, uint16_t* out,
+                              int B, int T, int q_heads, int kv_heads, int s_max, void* workspace,
+                              size_t workspace_bytes, void* stream) {
+  NPN_REQUIRE(query && gate && q_norm && rope.cos && rope.sin && cache_k && cache_v && kv_len &&
+                  out,
               NPN_ERR_NULL);
   NPN_REQUIRE(verify_shape_ok(B, T, q_heads, kv_heads, s_max), NPN_ERR_SHAPE);
   NPN_REQUIRE(NPN_ALIGNED16(cache_k) && NPN_ALIGNED16(cache_v) && NPN_ALIGNED16(workspace),
@@ -746,10 +777,12 @@ extern "C" int npn_gqa_tail_verify(const uint16_t* query, const uint16_t* gate,
   float* pml = reinterpret_cast<float*>(ws + 2 * p.q_bytes + p.po_bytes);
   int32_t* pstart = reinterpret_cast<int32_t*>(ws + 2 * p.q_bytes + p.po_bytes + p.pml_bytes);
 
-  QPrepArgs qa{query, q_norm, cos, sin, qhi, qlo, kv_len, pstart, B, T, q_heads, kv_heads, p.R,
-               p.P, s_max};
   const int rows = B * kv_heads * p.R;
-  hipLaunchKernelGGL(gqa_qprep_kernel, dim3(1 + (rows + 3) / 4), dim3(256), 0, s, qa);
+  const int qblocks = (rows + 3) / 4;
+  QPrepArgs qa{query, q_norm, rope, qhi, qlo, kv_len, pstart, B, T, q_heads, kv_heads, p.R,
+               p.P, s_max, qblocks, app};
+  const int ablocks = app.key != nullptr ? (B * T * kv_heads + 3) / 4 : 0;
+  hipLaunchKernelGGL(gqa_qprep_kernel, dim3(1 + qblocks + ablocks), dim3(256), 0, s, qa);
 
   AttnArgs aa{qhi, qlo, cache_k, cache_v, kv_len, pstart, po, pml, kv_heads, s_max, T, p.grp, p.P};
   const dim3 grid(kAttnWG);
@@ -762,13 +795,43 @@ extern "C" int npn_gqa_tail_verify(const uint16_t* query, const uint16_t* gate,
   return npn_launch_status();
 }
 
+extern "C" int npn_gqa_tail_verify(const uint16_t* query, const uint16_t* gate,
+                                   const float* q_norm, const float* cos, const float* sin,
+                                   const uint16_t* cache_k, const uint16_t* cache_v,
+                                   const int32_t* kv_len, uint16_t* out, int B, int T,
+                                   int q_heads, int kv_heads, int s_max, void* workspace,
+                                   size_t workspace_bytes, void* stream) {
+  AppendArgs none{};
+  return tail_verify_launch(query, gate, q_norm, RopeSrc{cos, sin, 0}, none, cache_k, cache_v,
+                            kv_len, out, B, T, q_heads, kv_heads, s_max, workspace,
+                            workspace_bytes, stream);
+}
+
+extern "C" int npn_gqa_tail_verify_append(const uint16_t* query, const uint16_t* gate,
+                                          const uint16_t* key, const uint16_t* value,
+                                          const float* q_norm, const float* k_norm,
+                                          const float* cos_table, const float* sin_table,
+                                          int positions, uint16_t* cache_k, uint16_t* cache_v,
+                                          const int32_t* kv_len, uint16_t* out, int B, int T,
+                                          int q_heads, int kv_heads, int s_max, void* workspace,
+                                          size_t workspace_bytes, void* stream) {
+  NPN_REQUIRE(key && value && k_norm, NPN_ERR_NULL);
+  NPN_REQUIRE(positions >= 1, NPN_ERR_SHAPE);
+  NPN_REQUIRE(NPN_ALIGNED16(cos_table) && NPN_ALIGNED16(sin_table), NPN_ERR_ALIGN);
+  const RopeSrc rope{cos_table, sin_table, positions};
+  const AppendArgs app{key, value, k_norm, rope, cache_k, cache_v, kv_len, B, T, kv_heads, s_max};
+  return tail_verify_launch(query, gate, q_norm, rope, app, cache_k, cache_v, kv_len, out, B, T,
+                            q_heads, kv_heads, s_max, workspace, workspace_bytes, stream);
+}
+
 extern "C" int npn_gqa_kv_append(const uint16_t* key, const uint16_t* value, const float* k_norm,
                                  const float* cos, const float* sin, uint16_t* cache_k,
                                  uint16_t* cache_v, const int32_t* kv_len, int B, int T,
                                  int kv_heads, int s_max, void* stream) {
   NPN_REQUIRE(key && value && k_norm && cos && sin && cache_k && cache_v && kv_len, NPN_ERR_NULL);
   NPN_REQUIRE(B >= 1 && T >= 1 && kv_heads >= 1 && s_max >= T, NPN_ERR_SHAPE);
-  AppendArgs aa{key, value, k_norm, cos, sin, cache_k, cache_v, kv_len, B, T, kv_heads, s_max};
+  AppendArgs aa{key, value, k_norm, RopeSrc{cos, sin, 0}, cache_k, cache_v, kv_len, B, T,
+                kv_heads, s_max};
   const int waves = B * T * kv_heads;
   hipLaunchKernelGGL(gqa_kv_append_kernel, dim3((waves + 3) / 4), dim3(256), 0,
                      static_cast<hipStream_t>(stream), aa);

@@ -16,6 +16,12 @@ New ops for the T-token verify step (same conventions, bf16 KV cache):
                  cos [B,T,64] f32, sin [B,T,64] f32, cache_k, cache_v, kv_len [B] int32)
       -> (), writes rows kv_len[b]+t of both caches in place (the k-side RMSNorm +
       partial RoPE + cache write of _gqa_layer, contrib/qwen3.6-27b/static_decode.py:880-910).
+  gqa::tail_verify_append(query, gate, key, value, q_norm, k_norm,
+                          cos_table [P,64] f32, sin_table [P,64] f32, cache_k, cache_v, kv_len)
+      -> out [B,T,Hq,256] bf16: kv_append then tail_verify in the tail's own launches (the
+      append rides in the query-prep launch), with the RoPE rows read from the position
+      tables at kv_len[b] + t (clamped to the table) as rope_rows gathers them; equal bit
+      for bit to rope_rows + kv_append + tail_verify.
 """
 import torch
 
@@ -130,6 +136,50 @@ def gqa_kv_append(
 @gqa_kv_append.register_fake
 def _(key, value, k_norm, cos, sin, cache_k, cache_v, kv_len):
     return None
+
+
+@torch.library.custom_op("gqa::tail_verify_append", mutates_args=("cache_k", "cache_v"),
+                         device_types="cuda")
+def gqa_tail_verify_append(
+    query: torch.Tensor,      # [B, T, Hq, 256] bf16
+    gate: torch.Tensor,       # [B, T, Hq, 256] bf16
+    key: torch.Tensor,        # [B, T, Hkv, 256] bf16 (k projection, pre-norm)
+    value: torch.Tensor,      # [B, T, Hkv, 256] bf16
+    q_norm: torch.Tensor,     # [256] f32
+    k_norm: torch.Tensor,     # [256] f32
+    cos_table: torch.Tensor,  # [P, 64] f32
+    sin_table: torch.Tensor,  # [P, 64] f32
+    cache_k: torch.Tensor,    # [B, Hkv, S, 256] bf16 (rows kv_len[b]+t written in place)
+    cache_v: torch.Tensor,    # [B, Hkv, S, 256] bf16 (rows kv_len[b]+t written in place)
+    kv_len: torch.Tensor,     # [B] int32
+) -> torch.Tensor:
+    B, T, hq, dh = query.shape
+    hkv, s_max = cache_k.shape[1], cache_k.shape[2]
+    P = cos_table.shape[0]
+    if dh != HEAD_DIM:
+        raise RuntimeError(f"head dim must be {HEAD_DIM}")
+    require(query, "query", torch.bfloat16)
+    require(gate, "gate", torch.bfloat16, shape=query.shape)
+    require(key, "key", torch.bfloat16, shape=(B, T, hkv, HEAD_DIM))
+    require(value, "value", torch.bfloat16, shape=(B, T, hkv, HEAD_DIM))
+    require(q_norm, "q_norm", torch.float32, numel=HEAD_DIM)
+    require(k_norm, "k_norm", torch.float32, numel=HEAD_DIM)
+    require(cos_table, "cos_table", torch.float32, shape=(P, ROPE_DIM))
+    require(sin_table, "sin_table", torch.float32, shape=(P, ROPE_DIM))
+    require(cache_k, "cache_k", torch.bfloat16, shape=(B, hkv, s_max, HEAD_DIM))
+    require(cache_v, "cache_v", torch.bfloat16, shape=(B, hkv, s_max, HEAD_DIM))
+    require(kv_len, "kv_len", torch.int32, numel=B)
+    ws = tail_verify_workspace(B, T, hq, hkv, s_max, query.device)
+    out = torch.empty_like(query)
+    call("npn_gqa_tail_verify_append", query, gate, key, value, q_norm, k_norm, cos_table,
+         sin_table, P, cache_k, cache_v, kv_len, out, B, T, hq, hkv, s_max, ws, ws.numel(),
+         stream_of(query))
+    return out
+
+
+@gqa_tail_verify_append.register_fake
+def _(query, gate, key, value, q_norm, k_norm, cos_table, sin_table, cache_k, cache_v, kv_len):
+    return torch.empty_like(query)
 
 
 @torch.library.custom_op("gqa::rope_rows", mutates_args=(), device_types="cuda")

@@ -29,6 +29,7 @@ SIGNATURES = {
     "npn_gqa_tail_verify_workspace_size": (_Z, [_I] * 5),
     "npn_gqa_tail_verify": (_I, [_P] * 9 + [_I] * 5 + [_P, _Z, _P]),
     "npn_gqa_kv_append": (_I, [_P] * 8 + [_I] * 4 + [_P]),
+    "npn_gqa_tail_verify_append": (_I, [_P] * 8 + [_I] + [_P] * 4 + [_I] * 5 + [_P, _Z, _P]),
     "npn_fp8_matmul_workspace_size": (_Z, [_I] * 3),
     "npn_fp8_matmul": (_I, [_P] * 4 + [_I] * 3 + [_P, _Z, _P]),
     "npn_accept_workspace_size": (_Z, [_I] * 3),

@@ -7,7 +7,8 @@ per sequence instead of one:
 
   x [B*T, 5120] --(per layer)--> input RMSNorm(1+w)
       DeltaNet layer: fp8 in-proj [qkv | z | a | b] -> deltanet::verify_from_ckpt -> fp8 out-proj
-      GQA layer:      fp8 [q+gate | k | v] -> gqa::kv_append -> gqa::tail_verify -> fp8 o-proj
+      GQA layer:      fp8 [q+gate | k | v] -> gqa::tail_verify_append (k norm + RoPE + KV
+                      append in the attention's query-prep launch) -> fp8 o-proj
     -> residual -> post RMSNorm(1+w) -> fp8 gate/up -> SiLU * up -> fp8 down -> residual
   logits -> spec::accept_rejection (or accept_greedy)
   rollback: DeltaNet state = checkpoint[accepted] (read in place by the next step),
@@ -111,10 +112,11 @@ class VerifySlice:
     with the decode state of B sequences."""
 
     def __init__(self, B, K, kv_lens, s_max, pattern="DDDG", seed=0, device="cuda",
-                 fuse_splitk=True, fuse_swiglu=True):
+                 fuse_splitk=True, fuse_swiglu=True, fuse_gqa=True):
         self.B, self.K, self.T = B, K, K + 1
         self.fuse_splitk = fuse_splitk
         self.fuse_swiglu = fuse_swiglu
+        self.fuse_gqa = fuse_gqa
         self.pattern = pattern
         self.device = device
         self.s_max = s_max
@@ -203,11 +205,17 @@ class VerifySlice:
                                                  proj, GQA_HQ, GQA_HKV, GQA_DH)
         query = query.reshape(B, T, GQA_HQ, GQA_DH)
         gate = gate.reshape(B, T, GQA_HQ, GQA_DH)
-        self.timer("gqa.kv_append", torch.ops.gqa.kv_append, key.reshape(B, T, GQA_HKV, GQA_DH),
-                   value.reshape(B, T, GQA_HKV, GQA_DH), L["k_norm"], cos, sin, L["cache_k"],
-                   L["cache_v"], self.kv_len)
-        attn = self.timer("gqa.tail_verify", torch.ops.gqa.tail_verify, query, gate, L["q_norm"],
-                          cos, sin, L["cache_k"], L["cache_v"], self.kv_len)
+        key = key.reshape(B, T, GQA_HKV, GQA_DH)
+        value = value.reshape(B, T, GQA_HKV, GQA_DH)
+        if cos is None:  # append, RoPE rows from the tables and attention in one op
+            attn = self.timer("gqa.tail_verify_append", torch.ops.gqa.tail_verify_append,
+                              query, gate, key, value, L["q_norm"], L["k_norm"], self.rope_cos,
+                              self.rope_sin, L["cache_k"], L["cache_v"], self.kv_len)
+        else:
+            self.timer("gqa.kv_append", torch.ops.gqa.kv_append, key, value, L["k_norm"], cos,
+                       sin, L["cache_k"], L["cache_v"], self.kv_len)
+            attn = self.timer("gqa.tail_verify", torch.ops.gqa.tail_verify, query, gate,
+                              L["q_norm"], cos, sin, L["cache_k"], L["cache_v"], self.kv_len)
         return fp8_project(attn.reshape(B * T, GQA_HQ * GQA_DH), L["o_proj"], self.timer,
                            f"fp8.matmul[{B * T}x{GQA_HQ * GQA_DH}x{HIDDEN}]", self.fuse_splitk)
 
@@ -236,10 +244,12 @@ class VerifySlice:
         Per layer, as the reference's decode loop (static_decode.py:533-542):
           normed = rms_norm(hidden); hidden += layer(normed);
           normed = rms_norm(hidden); hidden += mlp(normed)
-        with every residual add fused into the norm that follows it. If `trace` is a list,
+        with every residual add fused into the norm that follows it. Explicit cos/sin rows
+        (or fuse_gqa=False) select the separate rope_rows / kv_append / tail_verify ops,
+        whose results the fused op equals bit for bit. If `trace` is a list,
         the residual stream entering each sublayer (mixer, then MLP, per layer) and the final
         hidden are appended to it."""
-        if cos is None:
+        if cos is None and not self.fuse_gqa and "G" in self.pattern:
             cos, sin = self.timer("gqa.rope_rows", torch.ops.gqa.rope_rows, self.rope_cos,
                                   self.rope_sin, self.kv_len, self.T)
         layers = self.layers

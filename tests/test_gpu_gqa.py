@@ -112,3 +112,33 @@ def test_kv_append_then_attend_equals_cloned_cache(ops):
     diff = np.abs(gk.astype(np.int32) - rk.astype(np.int32))
     assert diff.max() <= 1, f"kv_append key rows differ by {diff.max()} bf16 ulps"
     assert (diff > 0).mean() < 0.01
+
+
+@pytest.mark.parametrize("P", [600, 310])
+def test_tail_verify_append_equals_separate_ops(ops, P):
+    """gqa::tail_verify_append (append in the query-prep launch, RoPE rows from the position
+    tables) against rope_rows + kv_append + tail_verify: output and both caches bit for bit,
+    with kv_len 0, one mid-cache and one ending at s_max, and (P = 310) positions past the
+    table clamped to its last row as rope_rows clamps them."""
+    from oracle.gqa import rope_cos_sin
+    B, T, Hq, Hkv, s_max = 3, 8, 24, 4, 600
+    g = torch.Generator().manual_seed(21)
+    kv_len = torch.tensor([0, 300, s_max - T], dtype=torch.int32)
+    d = gqa_verify_inputs(B, T, Hq, Hkv, kv_len.numpy(), s_max, seed=22)
+    key = torch.randn(B, T, Hkv, 256, generator=g).to(torch.bfloat16).cuda()
+    value = torch.randn(B, T, Hkv, 256, generator=g).to(torch.bfloat16).cuda()
+    k_norm = (torch.randn(256, generator=g) * 0.1).cuda()
+    tc, ts = rope_cos_sin(np.arange(P)[:, None], theta=1e7)
+    tc = torch.from_numpy(tc.reshape(P, 64)).cuda()
+    ts = torch.from_numpy(ts.reshape(P, 64)).cuda()
+    q, gate, qn = d["query"].cuda(), d["gate"].cuda(), d["q_norm"].cuda()
+    kvl = kv_len.cuda()
+    ck1, cv1 = d["cache_k"].cuda(), d["cache_v"].cuda()
+    ck2, cv2 = ck1.clone(), cv1.clone()
+    cos, sin = ops.gqa.rope_rows(tc, ts, kvl, T)
+    ops.gqa.kv_append(key, value, k_norm, cos, sin, ck1, cv1, kvl)
+    ref = ops.gqa.tail_verify(q, gate, qn, cos, sin, ck1, cv1, kvl)
+    out = ops.gqa.tail_verify_append(q, gate, key, value, qn, k_norm, tc, ts, ck2, cv2, kvl)
+    torch.cuda.synchronize()
+    assert torch.equal(ck2, ck1) and torch.equal(cv2, cv1)
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))

@@ -91,11 +91,14 @@ def test_gqa_split_partials(ops):
 
 
 def test_step_fused_equals_unfused(ops):
-    """A whole verify step with the reductions fused is bit-identical to one without."""
+    """A whole verify step with the split-K reductions fused into their consumers and the KV
+    append + RoPE rows fused into the attention's launches is bit-identical to one with
+    neither."""
     from spec_verify_step import HIDDEN, VerifySlice, synthetic_logits
     kv = [37, 300, 5, 129]
     B, K = 4, 7
-    models = [VerifySlice(B, K, kv, 400, pattern="DG", seed=5, device="cuda", fuse_splitk=f)
+    models = [VerifySlice(B, K, kv, 400, pattern="DG", seed=5, device="cuda", fuse_splitk=f,
+                          fuse_gqa=f)
               for f in (True, False)]
     g = torch.Generator(device="cuda").manual_seed(3)
     x = torch.randn(B * (K + 1), HIDDEN, generator=g, device="cuda").to(torch.bfloat16)

@@ -435,6 +435,18 @@ int npn_rope_rows(const float* cos_table, const float* sin_table, int positions,
 int npn_spec_commit(const int32_t* accepted, int32_t* prev_accepted, int32_t* kv_len,
                     int32_t* committed, int B, void* stream);
 
+/* torch.ops.deltanet.rollback_commit_ -- new op: the whole bookkeeping after acceptance in
+ * one launch, for decode state at fixed addresses: every DeltaNet layer's conv window rolled
+ * back in place (npn_deltanet_rollback with conv_state_out == conv_state and no state copy)
+ * and npn_spec_commit. Same results as those calls; 1 launch instead of layers + 1.
+ *   mixed_qkv, conv_state: host arrays of `layers` (0..8) device pointers, layer l's
+ *   [B, T, QKV] bf16 verify inputs and its [B, QKV, 3] bf16 window (rolled back in place);
+ *   accepted [B] int32; prev_accepted, kv_len, committed [B] int32 (each may be NULL). */
+int npn_deltanet_rollback_commit(const uint16_t* const* mixed_qkv, uint16_t* const* conv_state,
+                                 int layers, const int32_t* accepted, int32_t* prev_accepted,
+                                 int32_t* kv_len, int32_t* committed, int B, int T, int k_heads,
+                                 int v_heads, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -223,12 +223,9 @@ __global__ __launch_bounds__(128 * P) void dn_verify_kernel(DnArgs a) {
 // (0 when accepted == nullptr: the single-token shift new_cs = conv_in[:, 1:]).
 // conv_out may equal conv_state (in-place rollback): each thread owns one channel's three
 // entries and loads all of them before it stores.
-__global__ void dn_conv_window_kernel(const uint16_t* conv_state,
-                                      const uint16_t* __restrict__ x,
-                                      const int32_t* __restrict__ accepted,
-                                      uint16_t* conv_out, int B, int T, int QKV) {
-  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= (size_t)B * QKV) return;
+__device__ __forceinline__ void conv_window_at(const uint16_t* conv_state, const uint16_t* x,
+                                               const int32_t* accepted, uint16_t* conv_out,
+                                               int T, int QKV, size_t i) {
   const int b = (int)(i / QKV);
   const int c = (int)(i - (size_t)b * QKV);
   int acc = accepted ? accepted[b] : 0;
@@ -243,6 +240,48 @@ __global__ void dn_conv_window_kernel(const uint16_t* conv_state,
   }
 #pragma unroll
   for (int j = 0; j < 3; ++j) dst[j] = v[j];
+}
+
+__global__ void dn_conv_window_kernel(const uint16_t* conv_state,
+                                      const uint16_t* __restrict__ x,
+                                      const int32_t* __restrict__ accepted,
+                                      uint16_t* conv_out, int B, int T, int QKV) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (size_t)B * QKV) return;
+  conv_window_at(conv_state, x, accepted, conv_out, T, QKV, i);
+}
+
+// The bookkeeping after acceptance in one launch: every DeltaNet layer's conv window rolled
+// back in place (as dn_conv_window_kernel), and, in the last block, the per-sequence commit
+// prev_accepted = accepted, kv_len += accepted + 1, committed += accepted + 1 (null pointers
+// skipped). The two parts touch disjoint memory and only read `accepted`.
+constexpr int kMaxRollbackLayers = 8;
+struct RollbackCommitArgs {
+  const uint16_t* mixed[kMaxRollbackLayers];
+  uint16_t* conv[kMaxRollbackLayers];
+  const int32_t* accepted;
+  int32_t* prev_accepted;
+  int32_t* kv_len;
+  int32_t* committed;
+  size_t per_layer;  // B * QKV windows per layer
+  unsigned conv_blocks;
+  int layers, B, T, QKV;
+};
+
+__global__ __launch_bounds__(256) void dn_rollback_commit_kernel(RollbackCommitArgs a) {
+  if (blockIdx.x == a.conv_blocks) {
+    for (int b = threadIdx.x; b < a.B; b += blockDim.x) {
+      const int acc = a.accepted[b];
+      if (a.prev_accepted != nullptr) a.prev_accepted[b] = acc;
+      if (a.kv_len != nullptr) a.kv_len[b] += acc + 1;
+      if (a.committed != nullptr) a.committed[b] += acc + 1;
+    }
+    return;
+  }
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (size_t)a.layers * a.per_layer) return;
+  const int l = (int)(i / a.per_layer);
+  conv_window_at(a.conv[l], a.mixed[l], a.accepted, a.conv[l], a.T, a.QKV, i - l * a.per_layer);
 }
 
 // state_out[b] = ckpt[b][accepted[b]] (tile-contiguous copy, 16 bytes per thread).
@@ -355,5 +394,37 @@ extern "C" int npn_deltanet_rollback(const float* ckpt, const uint16_t* mixed_qk
   const size_t n = (size_t)B * QKV;
   hipLaunchKernelGGL(dn_conv_window_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
                      conv_state, mixed_qkv, accepted, conv_state_out, B, T, QKV);
+  return npn_launch_status();
+}
+
+extern "C" int npn_deltanet_rollback_commit(const uint16_t* const* mixed_qkv,
+                                            uint16_t* const* conv_state, int layers,
+                                            const int32_t* accepted, int32_t* prev_accepted,
+                                            int32_t* kv_len, int32_t* committed, int B, int T,
+                                            int k_heads, int v_heads, void* stream) {
+  NPN_REQUIRE(accepted != nullptr && (layers == 0 || (mixed_qkv && conv_state)), NPN_ERR_NULL);
+  NPN_REQUIRE(layers >= 0 && layers <= kMaxRollbackLayers && B >= 1 && B <= 65536 && T >= 1 &&
+                  T <= 16,
+              NPN_ERR_SHAPE);
+  int st = check_heads(k_heads, v_heads);
+  if (st != NPN_OK) return st;
+  RollbackCommitArgs a{};
+  for (int l = 0; l < layers; ++l) {
+    NPN_REQUIRE(mixed_qkv[l] != nullptr && conv_state[l] != nullptr, NPN_ERR_NULL);
+    a.mixed[l] = mixed_qkv[l];
+    a.conv[l] = conv_state[l];
+  }
+  a.accepted = accepted;
+  a.prev_accepted = prev_accepted;
+  a.kv_len = kv_len;
+  a.committed = committed;
+  a.layers = layers;
+  a.B = B;
+  a.T = T;
+  a.QKV = (2 * k_heads + v_heads) * D;
+  a.per_layer = (size_t)B * a.QKV;
+  a.conv_blocks = (unsigned)(((size_t)layers * a.per_layer + 255) / 256);
+  hipLaunchKernelGGL(dn_rollback_commit_kernel, dim3(a.conv_blocks + 1), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), a);
   return npn_launch_status();
 }

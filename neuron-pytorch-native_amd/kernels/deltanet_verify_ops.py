@@ -24,6 +24,8 @@ sequence continues from ckpt[b, accepted] -- the reference's traj[k-1] with
 k = accepted + 1 (contrib/qwen3.6-27b/kernels/tests/test_deltanet_spec_verify_rollback.py:64-68).
 T is derived from a_out: T = a_out.numel() // (B*Hv).
 """
+import ctypes
+
 import torch
 
 from npn_native import call, require, stream_of
@@ -256,4 +258,44 @@ def deltanet_conv_rollback_(
 
 @deltanet_conv_rollback_.register_fake
 def _(mixed_qkv, conv_state, accepted, v_heads):
+    return None
+
+
+@torch.library.custom_op("deltanet::rollback_commit_",
+                         mutates_args=("conv_states", "prev_accepted", "kv_len", "committed"),
+                         device_types="cuda")
+def deltanet_rollback_commit_(
+    mixed_qkvs: list[torch.Tensor],   # per DeltaNet layer: [B*T*QKV_DIM] bf16
+    conv_states: list[torch.Tensor],  # per DeltaNet layer: [B*QKV_DIM, 3] bf16, in place
+    accepted: torch.Tensor,           # [B] int32 in [0, T-1]
+    prev_accepted: torch.Tensor,      # [B] int32, set to accepted
+    kv_len: torch.Tensor,             # [B] int32, += accepted + 1
+    committed: torch.Tensor,          # [B] int32, += accepted + 1
+    v_heads: int,
+) -> None:
+    """deltanet::conv_rollback_ over every layer plus spec::commit_, in one launch."""
+    B = accepted.numel()
+    if len(mixed_qkvs) != len(conv_states) or len(conv_states) > 8:
+        raise RuntimeError("rollback_commit_: one mixed_qkv per conv_state, at most 8 layers")
+    for t, n in ((accepted, "accepted"), (prev_accepted, "prev_accepted"), (kv_len, "kv_len"),
+                 (committed, "committed")):
+        require(t, n, torch.int32, numel=B)
+    hk, hv, T = 1, v_heads, 1
+    for mixed, conv in zip(mixed_qkvs, conv_states):
+        qkv = conv.shape[0] // B
+        T = mixed.numel() // (B * qkv)
+        hk, hv = heads_from_shapes(qkv, v_heads)
+        require(mixed, "mixed_qkv", torch.bfloat16, numel=B * T * qkv)
+        require(conv, "conv_state", torch.bfloat16, shape=(B * qkv, 3))
+    if len({(m.numel(), c.shape) for m, c in zip(mixed_qkvs, conv_states)}) > 1:
+        raise RuntimeError("rollback_commit_: every layer must have the same shapes")
+    n = len(conv_states)
+    mp = (ctypes.c_void_p * max(n, 1))(*[m.data_ptr() for m in mixed_qkvs])
+    cp = (ctypes.c_void_p * max(n, 1))(*[c.data_ptr() for c in conv_states])
+    call("npn_deltanet_rollback_commit", mp, cp, n, accepted, prev_accepted, kv_len, committed,
+         B, T, hk, hv, stream_of(accepted))
+
+
+@deltanet_rollback_commit_.register_fake
+def _(mixed_qkvs, conv_states, accepted, prev_accepted, kv_len, committed, v_heads):
     return None

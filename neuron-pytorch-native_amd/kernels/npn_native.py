@@ -47,6 +47,7 @@ SIGNATURES = {
     "npn_gqa_split_partials": (_I, [_P, _I, _P, _I] + [_P] * 4 + [_I] * 4 + [_P]),
     "npn_rope_rows": (_I, [_P, _P, _I] + [_P] * 3 + [_I] * 3 + [_P]),
     "npn_spec_commit": (_I, [_P] * 4 + [_I, _P]),
+    "npn_deltanet_rollback_commit": (_I, [_P, _P, _I] + [_P] * 4 + [_I] * 4 + [_P]),
     "npn_fp8_matmul_argmax_groups": (_I, [_I] * 3),
     "npn_fp8_matmul_argmax": (_I, [_P] * 4 + [_I] * 3 + [_P]),
     "npn_argmax_parts": (_I, [_P, _I, _P, _P, _I, _P]),

@@ -112,11 +112,11 @@ class VerifySlice:
     with the decode state of B sequences."""
 
     def __init__(self, B, K, kv_lens, s_max, pattern="DDDG", seed=0, device="cuda",
-                 fuse_splitk=True, fuse_swiglu=True, fuse_gqa=True):
+                 fuse_splitk=True, fuse_swiglu=True, fuse_launches=True):
         self.B, self.K, self.T = B, K, K + 1
         self.fuse_splitk = fuse_splitk
         self.fuse_swiglu = fuse_swiglu
-        self.fuse_gqa = fuse_gqa
+        self.fuse_launches = fuse_launches
         self.pattern = pattern
         self.device = device
         self.s_max = s_max
@@ -245,11 +245,11 @@ class VerifySlice:
           normed = rms_norm(hidden); hidden += layer(normed);
           normed = rms_norm(hidden); hidden += mlp(normed)
         with every residual add fused into the norm that follows it. Explicit cos/sin rows
-        (or fuse_gqa=False) select the separate rope_rows / kv_append / tail_verify ops,
+        (or fuse_launches=False) select the separate rope_rows / kv_append / tail_verify ops,
         whose results the fused op equals bit for bit. If `trace` is a list,
         the residual stream entering each sublayer (mixer, then MLP, per layer) and the final
         hidden are appended to it."""
-        if cos is None and not self.fuse_gqa and "G" in self.pattern:
+        if cos is None and not self.fuse_launches and "G" in self.pattern:
             cos, sin = self.timer("gqa.rope_rows", torch.ops.gqa.rope_rows, self.rope_cos,
                                   self.rope_sin, self.kv_len, self.T)
         layers = self.layers
@@ -275,7 +275,17 @@ class VerifySlice:
 
     def accept_and_rollback(self, accepted):
         """Commit `accepted` drafts per sequence: DeltaNet continues from checkpoint
-        [accepted] (in place, next step), conv windows roll back, KV lengths advance."""
+        [accepted] (in place, next step), conv windows roll back, KV lengths advance. With
+        state at fixed addresses and fuse_launches, the conv rollbacks of every DeltaNet layer
+        and the commit are one launch (deltanet::rollback_commit_)."""
+        if self.persistent and self.fuse_launches:
+            dn = [L for L in self.layers if L["kind"] == "D"]
+            pend = [L.pop("pending") for L in dn]
+            self.timer("deltanet.rollback_commit", torch.ops.deltanet.rollback_commit_,
+                       [m for _, m in pend], [L["conv_state"] for L in dn], accepted,
+                       self.prev_accepted, self.kv_len, self.committed, DN_HV)
+            self.parity ^= 1
+            return
         for L in self.layers:
             if L["kind"] == "D":
                 ckpt, mixed = L.pop("pending")

@@ -98,7 +98,7 @@ def test_step_fused_equals_unfused(ops):
     kv = [37, 300, 5, 129]
     B, K = 4, 7
     models = [VerifySlice(B, K, kv, 400, pattern="DG", seed=5, device="cuda", fuse_splitk=f,
-                          fuse_gqa=f)
+                          fuse_launches=f)
               for f in (True, False)]
     g = torch.Generator(device="cuda").manual_seed(3)
     x = torch.randn(B * (K + 1), HIDDEN, generator=g, device="cuda").to(torch.bfloat16)

@@ -47,3 +47,30 @@ def test_commit(ops):
     assert prev.tolist() == [0, 7, 3, 1]
     assert kv.tolist() == [11, 28, 34, 42]
     assert com.tolist() == [2, 10, 7, 6]
+
+
+@pytest.mark.parametrize("layers", [0, 1, 3])
+def test_rollback_commit_equals_separate_ops(ops, layers):
+    """deltanet::rollback_commit_ (every layer's conv window in place + the commit, one
+    launch) against conv_rollback_ per layer and commit_, bit for bit, with accepted values
+    out of range on both sides (clamped for the windows, added as given by the commit)."""
+    B, T, QKV = 5, 8, 10240
+    g = torch.Generator(device="cuda").manual_seed(7 + layers)
+    mixed = [torch.randn(B * T * QKV, generator=g, device="cuda").to(torch.bfloat16)
+             for _ in range(layers)]
+    conv = [torch.randn(B * QKV, 3, generator=g, device="cuda").to(torch.bfloat16)
+            for _ in range(layers)]
+    acc = torch.tensor([0, 7, 3, -2, 9], dtype=torch.int32, device="cuda")
+    state = [torch.tensor(v, dtype=torch.int32, device="cuda")
+             for v in ([1, 2, 3, 4, 5], [100, 200, 300, 400, 500], [0, 0, 7, 7, 9])]
+    ref_conv = [c.clone() for c in conv]
+    ref_state = [s.clone() for s in state]
+    for m, c in zip(mixed, ref_conv):
+        ops.deltanet.conv_rollback_(m, c, acc, 48)
+    ops.spec.commit_(acc, *ref_state)
+    ops.deltanet.rollback_commit_(mixed, conv, acc, *state, 48)
+    torch.cuda.synchronize()
+    for c, r in zip(conv, ref_conv):
+        assert torch.equal(c.view(torch.int16), r.view(torch.int16))
+    for s, r in zip(state, ref_state):
+        assert torch.equal(s, r)

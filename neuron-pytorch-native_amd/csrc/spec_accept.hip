@@ -20,8 +20,8 @@
 // Kernels (each over B sequences, T = K+1 positions, vocabulary split into 8192-wide chunks):
 //   greedy:    argmax partials per (row, chunk) -> per-sequence merge + accept
 //   rejection: row max partials -> E sums per (row, chunk) added into each row's Z, and
-//              E at the draft token -> per-sequence decision -> residual/bonus mass per
-//              (sequence, chunk) -> per-sequence inverse-CDF pick
+//              E at the draft token -> residual/bonus mass per (sequence, chunk), each block
+//              making its sequence's decision first -> per-sequence inverse-CDF pick
 #include "npn_common.h"
 
 #include <mutex>
@@ -462,11 +462,12 @@ __global__ __launch_bounds__(THREADS) void rej_sum_kernel(RejArgs a) {
     sum_chunk<kUnitTemp>(a, target_row<TT>(a, row), row, c, sh);
 }
 
-// One wave per sequence: lane i < K runs the accept test of draft position i (all tests at
-// once; the first failing lane is the rejection), then lane 0 records which rows to sample
-// from, with their Z sums and maxima for the mass and pick kernels.
-__global__ __launch_bounds__(64) void rej_decide_kernel(RejArgs a) {
-  const int b = blockIdx.x, i = threadIdx.x;
+// The decision for sequence b, by one wave: lane i < K runs the accept test of draft position
+// i (all tests at once; the first failing lane is the rejection). Returns the accepted count
+// in every lane; with `record`, also writes accepted, the emitted draft ids (-1 past the
+// sampled position) and which rows to sample from, with their Z sums and maxima, for the pick
+// kernel.
+__device__ __forceinline__ int decide_wave(const RejArgs& a, int b, int i, bool record) {
   const int K = a.K, T = K + 1;
   const int nt = a.B * T;
   bool reject = false;
@@ -479,18 +480,21 @@ __global__ __launch_bounds__(64) void rej_decide_kernel(RejArgs a) {
   }
   const uint64_t rej = __builtin_amdgcn_ballot_w64(reject);
   const int acc = rej ? __builtin_ctzll(rej) : K;
-  if (i == 0) {
-    a.accepted[b] = acc;
-    a.dec_row[b] = acc;
-    a.dec_z[2 * b] = a.zrow[b * T + acc];
-    a.dec_z[2 * b + 1] = acc < K ? a.zrow[nt + b * K + acc] : 0;
-    a.dec_m[2 * b] = a.mrow[b * T + acc];  // maxima of the sampling rows
-    a.dec_m[2 * b + 1] = acc < K ? a.mrow[nt + b * K + acc] : 0.f;
+  if (record) {
+    if (i == 0) {
+      a.accepted[b] = acc;
+      a.dec_row[b] = acc;
+      a.dec_z[2 * b] = a.zrow[b * T + acc];
+      a.dec_z[2 * b + 1] = acc < K ? a.zrow[nt + b * K + acc] : 0;
+      a.dec_m[2 * b] = a.mrow[b * T + acc];  // maxima of the sampling rows
+      a.dec_m[2 * b + 1] = acc < K ? a.mrow[nt + b * K + acc] : 0.f;
+    }
+    for (int t = i; t < T; t += 64) {
+      if (t < acc) a.out_ids[(size_t)b * T + t] = a.draft_ids[(size_t)b * K + t];
+      else if (t > acc) a.out_ids[(size_t)b * T + t] = -1;
+    }
   }
-  for (int t = i; t < T; t += 64) {
-    if (t < acc) a.out_ids[(size_t)b * T + t] = a.draft_ids[(size_t)b * K + t];
-    else if (t > acc) a.out_ids[(size_t)b * T + t] = -1;
-  }
+  return acc;
 }
 
 // Sampling weight of vocabulary entry v for sequence b (residual or bonus).
@@ -518,6 +522,27 @@ __device__ __forceinline__ SampleRow<TT> sample_row(const RejArgs& a, int b) {
   } else {
     s.q = nullptr;
     s.mq = 0.f;
+  }
+  return s;
+}
+
+// The same rows from the row statistics, for a block that has just made the decision.
+template <typename TT>
+__device__ __forceinline__ SampleRow<TT> sample_row_at(const RejArgs& a, int b, int acc) {
+  const int K = a.K, T = K + 1;
+  const int nt = a.B * T;
+  SampleRow<TT> s;
+  s.p = target_row<TT>(a, b * T + acc);
+  s.mp = a.mrow[b * T + acc];
+  s.zp = a.zrow[b * T + acc];
+  if (acc < K) {
+    s.q = a.draft + (size_t)(b * K + acc) * a.V;
+    s.mq = a.mrow[nt + b * K + acc];
+    s.zq = a.zrow[nt + b * K + acc];
+  } else {
+    s.q = nullptr;
+    s.mq = 0.f;
+    s.zq = 0;
   }
   return s;
 }
@@ -584,10 +609,19 @@ __device__ __forceinline__ RunVals load_run(const RejArgs& a, const SampleRow<TT
   return r;
 }
 
+// Residual (or bonus) mass of sequence b's chunk c. Wave 0 of every block makes the
+// sequence's decision (a few integer products), and chunk 0's block records it for the pick
+// kernel, so the decision takes no launch of its own.
 template <typename TT>
 __global__ __launch_bounds__(THREADS) void rej_mass_kernel(RejArgs a) {
   const int b = blockIdx.y, c = blockIdx.x;
-  const SampleRow<TT> s = sample_row<TT>(a, b);
+  __shared__ int s_acc;
+  if (threadIdx.x < 64) {
+    const int acc = decide_wave(a, b, (int)threadIdx.x, c == 0);
+    if (threadIdx.x == 0) s_acc = acc;
+  }
+  __syncthreads();
+  const SampleRow<TT> s = sample_row_at<TT>(a, b, s_acc);
   const int v0 = c * MCHK + (int)threadIdx.x * PER_M;
   u128 m = 0;
   if (v0 < a.V) {
@@ -840,7 +874,6 @@ int rejection_launch(const TT* target_logits, const float* draft_logits,
     hipLaunchKernelGGL((rej_sum_kernel<true, TT>), dim3(nch, rows), dim3(THREADS), 0, s, a);
   else
     hipLaunchKernelGGL((rej_sum_kernel<false, TT>), dim3(nch, rows), dim3(THREADS), 0, s, a);
-  hipLaunchKernelGGL(rej_decide_kernel, dim3(B), dim3(64), 0, s, a);
   hipLaunchKernelGGL(rej_mass_kernel<TT>, dim3(a.nchm, B), dim3(THREADS), 0, s, a);
   hipLaunchKernelGGL(rej_pick_kernel<TT>, dim3(B), dim3(THREADS), 0, s, a);
   return npn_launch_status();

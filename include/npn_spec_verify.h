@@ -289,23 +289,29 @@ int npn_accept_greedy(const float* target_logits, const int64_t* draft_ids, int3
 
 /* torch.ops.spec.accept_rejection -- new op. Rejection sampling (Leviathan et
  * al. 2023, Alg. 1) under an integer softmax contract, so the result is
- * bit-identical to a CPU restatement for the same logits and uniforms:
- *   x_v = t_v*inv_temperature - max (fp32); E_v = floor(2^31 * exp_c(x_v)) with
- *   exp_c a fixed fp32 Cody-Waite + degree-7 Taylor evaluation in fused
- *   multiply-adds; Z = sum E_v (exact); U = floor(u * 2^24).
- *   Accept draft x iff U * Eq_x * Zp <= 2^24 * Ep_x * Zq. At the first rejection
- *   sample from R_v = max(0, Ep_v*Zq - Eq_v*Zp) (bonus: R_v = Ep_v of row K):
- *   the smallest v with 2^24 * sum_{w<=v} R_w > U_s * sum_w R_w.
+ * bit-identical to a CPU restatement for the same logits and uniforms, and every
+ * sum comes from one pass over the logits:
+ *   s_v = t_v*inv_temperature (fp32); the vocabulary is cut into chunks of 8192;
+ *   m_c = max of chunk c's non-NaN s_v, M = max_c m_c; E_v = floor(2^31 *
+ *   exp_c(s_v - m_c)), F_c = floor(2^31 * exp_c(m_c - M)) with exp_c a fixed fp32
+ *   Cody-Waite + degree-7 Taylor evaluation in fused multiply-adds; the weight of v
+ *   is W_v = E_v * F_c and Z = sum_v W_v (exact integers); U = floor(u * 2^24).
+ *   Accept draft x iff U * Wq_x * Zp <= 2^24 * Wp_x * Zq. At the first rejection
+ *   sample from R_v = max(0, Wp_v*Zq - Wq_v*Zp) (bonus: R_v = Wp_v of row K):
+ *   the smallest v with 2^24 * sum_{w<=v} R_w > U_s * sum_w R_w (exact to 2^192).
  *   A row with no finite entry relative to its maximum (all NaN or -inf, or a +inf
  *   entry) has Z = 0 and passes the accept test; if the bonus row has no mass the
  *   token is its argmax (NaN counts as the maximum, ties go to the lowest index).
  *   target_logits [B, K+1, V] f32, draft_logits [B, K, V] f32, draft_ids [B, K]
  *   int64, u_accept [B, K] f32 in [0,1), u_sample [B] f32 in [0,1),
  *   inv_temperature > 0 (logits are multiplied by it), V <= 2^20.
- * On return the workspace starts with every row's Z (uint64 [R]) and, at byte
- * offset 8R rounded up to a multiple of 256, every row's max scaled logit m
- * (float [R]); R = B*(2K+1) rows: target row (b, i) at b*(K+1)+i, then draft
- * row (b, i) at B*(K+1) + b*K + i. */
+ * Four launches: the one logit pass (per row and chunk: m_c, the sum of E, E at the draft
+ * token), the row totals and the decision (one workgroup per sequence), the residual mass
+ * per 2048-entry chunk, the inverse CDF.
+ * On return the workspace starts with every row's Z (unsigned 128-bit, low 64-bit word
+ * first [R]) and, at byte offset 16R rounded up to a multiple of 256, every row's max
+ * scaled logit M (float [R]); R = B*(2K+1) rows: target row (b, i) at b*(K+1)+i, then
+ * draft row (b, i) at B*(K+1) + b*K + i. */
 int npn_accept_rejection(const float* target_logits, const float* draft_logits,
                          const int64_t* draft_ids, const float* u_accept,
                          const float* u_sample, float inv_temperature, int32_t* accepted,
@@ -320,7 +326,7 @@ int npn_accept_rejection(const float* target_logits, const float* draft_logits,
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). The workspace
  * is a fixed device array of NPN_ACCEPT_SCRATCH_BYTES per GPU, held from the first call on
  * that GPU until the process ends; problems whose npn_accept_workspace_size(B, K, V) exceeds
- * it return NPN_ERR_SCRATCH (B = 32, K = 7, V = 151936 needs 84 KiB). Every call on a GPU
+ * it return NPN_ERR_SCRATCH (B = 32, K = 7, V = 151936 needs 179 KiB). Every call on a GPU
  * uses that GPU's one array, so calls that overlap on one GPU (concurrent streams, or
  * threads) race and must be serialised by the caller; each call writes every scratch word it
  * reads, so nothing needs clearing between calls. The stream's device (the current device
@@ -347,9 +353,8 @@ int npn_accept_greedy_parts(const void* parts, int nparts, const int64_t* draft_
 /* torch.ops.spec.accept_rejection_lm_head -- new op: npn_accept_rejection with the target
  * logits produced by the LM head in the same call. hidden [B*(K+1), H] bf16 (the final-normed
  * verify rows, row b*(K+1) + t), lm_head_w [H, V] e4m3fn bytes, lm_head_scale [V] f32:
- * target_logits [B*(K+1), V] bf16 is written (= npn_fp8_matmul_rowmax's out) together with
- * its row-group maxima (in the workspace); the rejection passes read the target rows in bf16
- * and take their maxima from the groups instead of a pass over them. accepted / out_ids equal
+ * target_logits [B*(K+1), V] bf16 is written (= npn_fp8_matmul's out), and the rejection
+ * pass reads the target rows in bf16 (half the bytes of fp32 rows). accepted / out_ids equal
  * npn_accept_rejection's on the fp32 cast of target_logits, bit for bit, with the same
  * draft logits, ids, uniforms and inv_temperature (> 0). V % 64 == 0, H % 64 == 0, the other
  * rules as npn_accept_rejection. Workspace: npn_accept_rejection_lm_head_workspace_size

@@ -19,9 +19,9 @@
 //
 // Kernels (each over B sequences, T = K+1 positions, vocabulary split into 8192-wide chunks):
 //   greedy:    argmax partials per (row, chunk) -> per-sequence merge + accept
-//   rejection: row max partials -> E sums per (row, chunk) added into each row's Z, and
-//              E at the draft token -> residual/bonus mass per (sequence, chunk), each block
-//              making its sequence's decision first -> per-sequence inverse-CDF pick
+//   rejection: one pass per (row, chunk): the chunk maximum, the sum of E and E at the draft
+//              token -> per-sequence row totals and decision -> residual/bonus mass per
+//              (sequence, chunk) -> per-sequence inverse-CDF pick
 #include "npn_common.h"
 
 #include <mutex>
@@ -328,6 +328,61 @@ __global__ __launch_bounds__(1024) void greedy_accept_parts_kernel(
 }
 
 // ---- rejection sampling ------------------------------------------------------------------
+// 192-bit unsigned integers (three 64-bit limbs, little end first) for the exact products of
+// the contract: W (< 2^63) times Z (< 2^80), times a 24-bit uniform or shift.
+struct u192 {
+  uint64_t w0, w1, w2;
+};
+
+__device__ __forceinline__ u192 u192_from(u128 x) { return u192{(uint64_t)x, (uint64_t)(x >> 64), 0}; }
+
+__device__ __forceinline__ u192 add192(u192 a, u192 b) {
+  const u128 s0 = (u128)a.w0 + b.w0;
+  const u128 s1 = (u128)a.w1 + b.w1 + (uint64_t)(s0 >> 64);
+  return u192{(uint64_t)s0, (uint64_t)s1, a.w2 + b.w2 + (uint64_t)(s1 >> 64)};
+}
+
+__device__ __forceinline__ u192 sub192(u192 a, u192 b) {  // a >= b
+  const uint64_t b0 = a.w0 < b.w0;
+  const u128 d1 = (u128)a.w1 - b.w1 - b0;
+  const uint64_t b1 = (uint64_t)(d1 >> 64) != 0;  // borrow out of limb 1
+  return u192{a.w0 - b.w0, (uint64_t)d1, a.w2 - b.w2 - b1};
+}
+
+__device__ __forceinline__ bool gt192(u192 a, u192 b) {
+  if (a.w2 != b.w2) return a.w2 > b.w2;
+  if (a.w1 != b.w1) return a.w1 > b.w1;
+  return a.w0 > b.w0;
+}
+
+__device__ __forceinline__ bool is_zero192(u192 a) { return (a.w0 | a.w1 | a.w2) == 0; }
+
+// x * y for x < 2^64 and y < 2^128, exact (< 2^192).
+__device__ __forceinline__ u192 mul64x128(uint64_t x, u128 y) {
+  const u128 lo = (u128)x * (uint64_t)y;
+  const u128 hi = (u128)x * (uint64_t)(y >> 64);
+  const u128 mid = (lo >> 64) + (uint64_t)hi;
+  return u192{(uint64_t)lo, (uint64_t)mid, (uint64_t)(hi >> 64) + (uint64_t)(mid >> 64)};
+}
+
+// x * m for x < 2^128 and m < 2^32, exact (< 2^160).
+__device__ __forceinline__ u192 mul128x32(u128 x, uint32_t m) {
+  const u128 p0 = (u128)(uint64_t)x * m;
+  const u128 p1 = (u128)(uint64_t)(x >> 64) * m + (uint64_t)(p0 >> 64);
+  return u192{(uint64_t)p0, (uint64_t)p1, (uint64_t)(p1 >> 64)};
+}
+
+// a * m for m < 2^32 (exact while the product stays below 2^192).
+__device__ __forceinline__ u192 mul192x32(u192 a, uint32_t m) {
+  const u128 p0 = (u128)a.w0 * m;
+  const u128 p1 = (u128)a.w1 * m + (uint64_t)(p0 >> 64);
+  return u192{(uint64_t)p0, (uint64_t)p1, a.w2 * m + (uint64_t)(p1 >> 64)};
+}
+
+__device__ __forceinline__ u192 shl24_192(u192 a) {
+  return u192{a.w0 << 24, (a.w1 << 24) | (a.w0 >> 40), (a.w2 << 24) | (a.w1 >> 40)};
+}
+
 struct RejArgs {
   const void* target;    // [B][K+1][V] fp32, or bf16 (the LM head's logits)
   const float* draft;    // [B][K][V]
@@ -337,19 +392,18 @@ struct RejArgs {
   float inv_temp;
   int32_t* accepted;
   int64_t* out_ids;
-  int B, K, V, nch, nchm;  // chunks of CHK (logit passes) and of MCHK (mass / pick)
-  bool vec4;          // logit rows 16-byte aligned and V % 4 == 0
+  int B, K, V, nch, nchm;  // chunks of CHK (logit pass) and of MCHK (mass / pick)
+  bool vec4;          // logit rows 16-byte aligned and V % 4 == 0 (V % 8 for bf16 rows)
   // workspace (rows = B*(K+1) target rows, then B*K draft rows)
-  uint64_t* zrow;     // [rows]        Z of each row (chunk sums added atomically)
-  float* mrow;        // [rows]        max scaled logit of each row
+  u128* zrow;         // [rows]        Z of each row
+  float* mrow;        // [rows]        row maximum M (scaled logits)
   uint32_t* ex;       // [rows]        E at the row's draft token (target/draft rows i < K)
-  float* rmax;        // [rows][nch]   chunk maxima
-  int32_t* dec_row;   // [B]           sampling row index (target row; draft row or -1)
-  uint64_t* dec_z;    // [B][2]        Zp, Zq of the sampling rows
-  float* dec_m;       // [B][2]        row maxima of the sampling rows (scaled logits)
-  u128* cmass;        // [B][nchm]
-  const float* tgmax; // or null: [B*(K+1)][ngmax] group maxima of the target rows (NaN ignored)
-  int ngmax;
+  float* rmax;        // [rows][nch]   chunk maxima m_c
+  uint64_t* rsum;     // [rows][nch]   chunk sums S_c
+  int32_t* dec_row;   // [B]           sampling position (target row; draft row or none)
+  u128* dec_z;        // [B][2]        Zp, Zq of the sampling rows
+  float* dec_m;       // [B][2]        row maxima of the sampling rows
+  u192* cmass;        // [B][nchm]
 };
 
 template <typename TT>
@@ -374,189 +428,152 @@ __device__ __forceinline__ int row_token(const RejArgs& a, int row) {
   return (int)x;
 }
 
-// Chunk c of a row: its max scaled logit into the row's chunk maxima (and, from chunk 0,
-// a zero into the row's Z, which the sum pass adds into in a later launch).
-template <typename E>
-__device__ __forceinline__ void max_chunk(const RejArgs& a, const E* src, int row, int c,
-                                          float* sh) {
-  const int v0 = c * CHK;
-  float m = -INFINITY;
-  visit_chunk(src, v0, a.V, a.vec4, [&](int, float x) { m = fmaxf(m, scaled(x, a.inv_temp)); });
-  m = block_max(m, sh);
-  if (threadIdx.x == 0) {
-    a.rmax[(size_t)row * a.nch + c] = m;
-    if (c == 0) a.zrow[row] = 0;
+// This thread's entries of chunk [v0, v0 + CHK) of a row, in registers, scaled (NaN for
+// entries past V: the maximum ignores them and they get E = 0). Same entry assignment as
+// visit_chunk; the sums are exact, so the assignment does not affect results.
+template <bool kUnitTemp>
+__device__ __forceinline__ void load_chunk(const float* src, int v0, int V, bool vec4,
+                                           float inv_temp, float (&x)[PER_T]) {
+  if (vec4 && v0 + CHK <= V) {
+#pragma unroll
+    for (int j = 0; j < PER_T / 4; ++j) {
+      const float4 f =
+          *reinterpret_cast<const float4*>(src + v0 + 4 * (j * THREADS + (int)threadIdx.x));
+      x[4 * j] = f.x; x[4 * j + 1] = f.y; x[4 * j + 2] = f.z; x[4 * j + 3] = f.w;
+    }
+  } else if (vec4) {
+#pragma unroll
+    for (int j = 0; j < PER_T / 4; ++j) {
+      const int v = v0 + 4 * (j * THREADS + (int)threadIdx.x);
+      float4 f = make_float4(NAN, NAN, NAN, NAN);
+      if (v < V) f = *reinterpret_cast<const float4*>(src + v);
+      x[4 * j] = f.x; x[4 * j + 1] = f.y; x[4 * j + 2] = f.z; x[4 * j + 3] = f.w;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < PER_T; ++j) {
+      const int v = v0 + j * THREADS + (int)threadIdx.x;
+      x[j] = v < V ? src[v] : NAN;
+    }
+  }
+  if (!kUnitTemp) {
+#pragma unroll
+    for (int j = 0; j < PER_T; ++j) x[j] = scaled(x[j], inv_temp);
   }
 }
 
-__device__ __forceinline__ float row_max(const RejArgs& a, int row) {
-  float m = a.rmax[(size_t)row * a.nch];
-  for (int c = 1; c < a.nch; ++c) m = fmaxf(m, a.rmax[(size_t)row * a.nch + c]);
-  return m;
-}
-
-// Chunk c of a row: its E sum added into the row's Z (exact 64-bit atomics, so the order of
-// the chunks does not matter), the row max from chunk 0 and E at the draft token from the
-// chunk that holds it. kUnitTemp skips the multiply by inv_temp == 1 (x * 1 == x, NaN
-// stays NaN).
-template <bool kUnitTemp, typename E>
-__device__ __forceinline__ void sum_chunk(const RejArgs& a, const E* src, int row, int c,
-                                          uint64_t* sh) {
-  const float m = row_max(a, row);
-  const float it = a.inv_temp;
-  const int v0 = c * CHK;
-  uint64_t z = 0;
-  visit_chunk(src, v0, a.V, a.vec4,
-              [&](int, float x) { z += expfix((kUnitTemp ? x : scaled(x, it)) - m); });
-  z = block_sum_u64(z, sh);
-  if (threadIdx.x == 0) {
-    atomicAdd(reinterpret_cast<unsigned long long*>(a.zrow + row), (unsigned long long)z);
-    if (c == 0) a.mrow[row] = m;
-    const int x = row_token(a, row);
-    if (x >= v0 && x < v0 + CHK) a.ex[row] = expfix(scaled(elem(src, x), it) - m);
+template <bool kUnitTemp>
+__device__ __forceinline__ void load_chunk(const uint16_t* src, int v0, int V, bool vec,
+                                           float inv_temp, float (&x)[PER_T]) {
+  if (vec) {
+#pragma unroll
+    for (int j = 0; j < PER_T / 8; ++j) {
+      const int v = v0 + 8 * (j * THREADS + (int)threadIdx.x);
+      uint4 q = make_uint4(0x7FC07FC0u, 0x7FC07FC0u, 0x7FC07FC0u, 0x7FC07FC0u);  // bf16 NaNs
+      if (v < V) q = *reinterpret_cast<const uint4*>(src + v);
+      const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        x[8 * j + 2 * k] = npn::bf16_to_f32(w[k] & 0xFFFFu);
+        x[8 * j + 2 * k + 1] = npn::bf16_to_f32(w[k] >> 16);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < PER_T; ++j) {
+      const int v = v0 + j * THREADS + (int)threadIdx.x;
+      x[j] = v < V ? npn::bf16_to_f32(src[v]) : NAN;
+    }
+  }
+  if (!kUnitTemp) {
+#pragma unroll
+    for (int j = 0; j < PER_T; ++j) x[j] = scaled(x[j], inv_temp);
   }
 }
 
-// The logit passes: chunk maxima of every row, then E sums. The sum pass runs its rows and
-// chunks last-first, the reverse of the max pass's dispatch order, so the first chunks it
-// re-reads are the ones read last.
-// With group maxima of the target rows (the LM head's epilogue), a target row's max is the
-// max of its groups, scaled: for inv_temp > 0, scaled(max t) == max scaled(t) (rounding is
-// monotone), so the value is the one the max pass would find, without reading the row.
-__device__ __forceinline__ void max_from_groups(const RejArgs& a, int row, int c, float* sh) {
-  if (c != 0) {
-    if (threadIdx.x == 0) a.rmax[(size_t)row * a.nch + c] = -INFINITY;
-    return;
-  }
-  float m = -INFINITY;
-  for (int g = (int)threadIdx.x; g < a.ngmax; g += THREADS)
-    m = fmaxf(m, a.tgmax[(size_t)row * a.ngmax + g]);
-  m = block_max(m, sh);
-  if (threadIdx.x == 0) {
-    a.rmax[(size_t)row * a.nch] = scaled(m, a.inv_temp);
-    a.zrow[row] = 0;
-  }
-}
-
-template <typename TT>
-__global__ __launch_bounds__(THREADS) void rej_max_kernel(RejArgs a) {
-  __shared__ float sh[THREADS / 64];
+// The one logit pass: chunk c of a row, read once into registers; its maximum m_c, then
+// S_c = sum of E_v = expfix(s_v - m_c), and E at the row's draft token if it lies here.
+// kUnitTemp skips the multiply by inv_temp == 1 (x * 1 == x, NaN stays NaN).
+template <bool kUnitTemp, typename TT>
+__global__ __launch_bounds__(THREADS) void rej_scan_kernel(RejArgs a) {
+  __shared__ float shm[THREADS / 64];
+  __shared__ uint64_t shs[THREADS / 64];
   const int row = (int)blockIdx.y, c = (int)blockIdx.x;
   const int nt = a.B * (a.K + 1);
+  const int v0 = c * CHK;
+  float x[PER_T];
   if (row >= nt)
-    max_chunk(a, a.draft + (size_t)(row - nt) * a.V, row, c, sh);
-  else if (a.tgmax != nullptr)
-    max_from_groups(a, row, c, sh);
+    load_chunk<kUnitTemp>(a.draft + (size_t)(row - nt) * a.V, v0, a.V, a.vec4, a.inv_temp, x);
   else
-    max_chunk(a, target_row<TT>(a, row), row, c, sh);
-}
-
-template <bool kUnitTemp, typename TT>
-__global__ __launch_bounds__(THREADS) void rej_sum_kernel(RejArgs a) {
-  __shared__ uint64_t sh[THREADS / 64];
-  const int row = (int)(gridDim.y - 1 - blockIdx.y), c = (int)(gridDim.x - 1 - blockIdx.x);
-  const int nt = a.B * (a.K + 1);
-  if (row >= nt)
-    sum_chunk<kUnitTemp>(a, a.draft + (size_t)(row - nt) * a.V, row, c, sh);
-  else
-    sum_chunk<kUnitTemp>(a, target_row<TT>(a, row), row, c, sh);
-}
-
-// The decision for sequence b, by one wave: lane i < K runs the accept test of draft position
-// i (all tests at once; the first failing lane is the rejection). Returns the accepted count
-// in every lane; with `record`, also writes accepted, the emitted draft ids (-1 past the
-// sampled position) and which rows to sample from, with their Z sums and maxima, for the pick
-// kernel.
-__device__ __forceinline__ int decide_wave(const RejArgs& a, int b, int i, bool record) {
-  const int K = a.K, T = K + 1;
-  const int nt = a.B * T;
-  bool reject = false;
-  if (i < K) {
-    const int rt = b * T + i, rd = nt + b * K + i;
-    const uint64_t ueq = (uint64_t)uniform_fix(a.u_accept[(size_t)b * K + i]) * a.ex[rd];
-    const u128 lhs = (u128)ueq * a.zrow[rt];                   // < 2^24 * 2^31 * 2^51
-    const u128 rhs = ((u128)a.ex[rt] * a.zrow[rd]) << 24;
-    reject = lhs > rhs;
-  }
-  const uint64_t rej = __builtin_amdgcn_ballot_w64(reject);
-  const int acc = rej ? __builtin_ctzll(rej) : K;
-  if (record) {
-    if (i == 0) {
-      a.accepted[b] = acc;
-      a.dec_row[b] = acc;
-      a.dec_z[2 * b] = a.zrow[b * T + acc];
-      a.dec_z[2 * b + 1] = acc < K ? a.zrow[nt + b * K + acc] : 0;
-      a.dec_m[2 * b] = a.mrow[b * T + acc];  // maxima of the sampling rows
-      a.dec_m[2 * b + 1] = acc < K ? a.mrow[nt + b * K + acc] : 0.f;
-    }
-    for (int t = i; t < T; t += 64) {
-      if (t < acc) a.out_ids[(size_t)b * T + t] = a.draft_ids[(size_t)b * K + t];
-      else if (t > acc) a.out_ids[(size_t)b * T + t] = -1;
+    load_chunk<kUnitTemp>(target_row<TT>(a, row), v0, a.V, a.vec4, a.inv_temp, x);
+  float m = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < PER_T; ++j) m = fmaxf(m, x[j]);
+  m = block_max(m, shm);
+  uint64_t z = 0;
+#pragma unroll
+  for (int j = 0; j < PER_T; ++j) z += expfix(x[j] - m);
+  z = block_sum_u64(z, shs);
+  if (threadIdx.x == 0) {
+    a.rmax[(size_t)row * a.nch + c] = m;
+    a.rsum[(size_t)row * a.nch + c] = z;
+    const int tok = row_token(a, row);
+    if (tok >= v0 && tok < v0 + CHK) {
+      const float xt = row >= nt ? a.draft[(size_t)(row - nt) * a.V + tok]
+                                 : elem(target_row<TT>(a, row), tok);
+      a.ex[row] = expfix(scaled(xt, a.inv_temp) - m);
     }
   }
-  return acc;
 }
 
-// Sampling weight of vocabulary entry v for sequence b (residual or bonus).
+// Sampling weight of vocabulary entry v for sequence b (residual or bonus), in one MCHK chunk
+// (inside one CHK chunk c, whose m_c and F_c are fixed per call). After a rejection the
+// residual W^p Zq - W^q Zp = E^p (F^p Zq) - E^q (F^q Zp): the two bracketed products
+// (< 2^111) are formed once per call, so each entry costs two 32 x 128-bit products.
 template <typename TT>
 struct SampleRow {
   const TT* p;
   const float* q;  // nullptr for the bonus row
-  float mp, mq;
-  uint64_t zp, zq;
+  float mp, mq;    // chunk maxima of the chunk being weighed
+  uint64_t fp;     // F^p_c (the bonus weight is E^p F^p_c)
+  u128 gp, gq;     // F^p_c Zq and F^q_c Zp
 };
 
+// The sampling rows of sequence b at position acc (the first rejection, or K: bonus), with
+// row maxima Mp, Mq and totals Zp, Zq, positioned at the CHK chunk c.
 template <typename TT>
-__device__ __forceinline__ SampleRow<TT> sample_row(const RejArgs& a, int b) {
-  const int K = a.K, T = K + 1;
-  const int acc = a.dec_row[b];
-  SampleRow<TT> s;
-  const int rt = b * T + acc;
-  s.p = target_row<TT>(a, rt);
-  s.mp = a.dec_m[2 * b];
-  s.zp = a.dec_z[2 * b];
-  s.zq = a.dec_z[2 * b + 1];
-  if (acc < K) {
-    s.q = a.draft + (size_t)(b * K + acc) * a.V;
-    s.mq = a.dec_m[2 * b + 1];
-  } else {
-    s.q = nullptr;
-    s.mq = 0.f;
-  }
-  return s;
-}
-
-// The same rows from the row statistics, for a block that has just made the decision.
-template <typename TT>
-__device__ __forceinline__ SampleRow<TT> sample_row_at(const RejArgs& a, int b, int acc) {
+__device__ __forceinline__ SampleRow<TT> sample_row(const RejArgs& a, int b, int acc, float Mp,
+                                                    float Mq, u128 zp, u128 zq, int c) {
   const int K = a.K, T = K + 1;
   const int nt = a.B * T;
   SampleRow<TT> s;
-  s.p = target_row<TT>(a, b * T + acc);
-  s.mp = a.mrow[b * T + acc];
-  s.zp = a.zrow[b * T + acc];
+  const int rp = b * T + acc;
+  s.p = target_row<TT>(a, rp);
+  s.mp = a.rmax[(size_t)rp * a.nch + c];
+  s.fp = expfix(s.mp - Mp);
+  s.gp = (u128)s.fp * zq;
   if (acc < K) {
+    const int rq = nt + b * K + acc;
     s.q = a.draft + (size_t)(b * K + acc) * a.V;
-    s.mq = a.mrow[nt + b * K + acc];
-    s.zq = a.zrow[nt + b * K + acc];
+    s.mq = a.rmax[(size_t)rq * a.nch + c];
+    s.gq = (u128)expfix(s.mq - Mq) * zp;
   } else {
     s.q = nullptr;
     s.mq = 0.f;
-    s.zq = 0;
+    s.gq = 0;
   }
   return s;
 }
 
 template <typename TT>
-__device__ __forceinline__ u128 weight_of(const SampleRow<TT>& s, float pv, float qv,
+__device__ __forceinline__ u192 weight_of(const SampleRow<TT>& s, float pv, float qv,
                                           float inv_temp) {
   const uint32_t ep = expfix(scaled(pv, inv_temp) - s.mp);
-  if (s.q == nullptr) return ep;
+  if (s.q == nullptr) return u192{(uint64_t)ep * s.fp, 0, 0};
   const uint32_t eq = expfix(scaled(qv, inv_temp) - s.mq);
-  const u128 x = (u128)ep * s.zq, y = (u128)eq * s.zp;
-  return x > y ? x - y : 0;
+  const u192 x = mul128x32(s.gp, ep), y = mul128x32(s.gq, eq);
+  return gt192(x, y) ? sub192(x, y) : u192{0, 0, 0};
 }
-
 
 // This thread's PER_M consecutive sampling-row entries starting at v0 (p, and q after a
 // rejection), loaded once; entries at or past V read as p = q = -inf (weight 0 is not
@@ -609,56 +626,144 @@ __device__ __forceinline__ RunVals load_run(const RejArgs& a, const SampleRow<TT
   return r;
 }
 
-// Residual (or bonus) mass of sequence b's chunk c. Wave 0 of every block makes the
-// sequence's decision (a few integer products), and chunk 0's block records it for the pick
-// kernel, so the decision takes no launch of its own.
+// ---- 192-bit wave and block sums and scans -----------------------------------------------
+__device__ __forceinline__ u192 shfl_u192(u192 v, int src_lane) {
+  uint32_t w[6] = {(uint32_t)v.w0, (uint32_t)(v.w0 >> 32), (uint32_t)v.w1,
+                   (uint32_t)(v.w1 >> 32), (uint32_t)v.w2, (uint32_t)(v.w2 >> 32)};
+#pragma unroll
+  for (int k = 0; k < 6; ++k) w[k] = __shfl(w[k], src_lane, 64);
+  return u192{((uint64_t)w[1] << 32) | w[0], ((uint64_t)w[3] << 32) | w[2],
+              ((uint64_t)w[5] << 32) | w[4]};
+}
+
+__device__ __forceinline__ u192 shfl_up_u192(u192 v, int d) {
+  uint32_t w[6] = {(uint32_t)v.w0, (uint32_t)(v.w0 >> 32), (uint32_t)v.w1,
+                   (uint32_t)(v.w1 >> 32), (uint32_t)v.w2, (uint32_t)(v.w2 >> 32)};
+#pragma unroll
+  for (int k = 0; k < 6; ++k) w[k] = __shfl_up(w[k], d, 64);
+  return u192{((uint64_t)w[1] << 32) | w[0], ((uint64_t)w[3] << 32) | w[2],
+              ((uint64_t)w[5] << 32) | w[4]};
+}
+
+__device__ __forceinline__ u192 shfl_xor_u192(u192 v, int m) {
+  uint32_t w[6] = {(uint32_t)v.w0, (uint32_t)(v.w0 >> 32), (uint32_t)v.w1,
+                   (uint32_t)(v.w1 >> 32), (uint32_t)v.w2, (uint32_t)(v.w2 >> 32)};
+#pragma unroll
+  for (int k = 0; k < 6; ++k) w[k] = __shfl_xor(w[k], m, 64);
+  return u192{((uint64_t)w[1] << 32) | w[0], ((uint64_t)w[3] << 32) | w[2],
+              ((uint64_t)w[5] << 32) | w[4]};
+}
+
+// Inclusive prefix sum over the 64 lanes of a wave.
+__device__ __forceinline__ u192 wave_incl_scan_u192(u192 v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const u192 o = shfl_up_u192(v, d);
+    if (lane >= d) v = add192(v, o);
+  }
+  return v;
+}
+
+__device__ u192 block_sum_u192(u192 v, u192* sh) {
+  for (int off = 32; off > 0; off >>= 1) v = add192(v, shfl_xor_u192(v, off));
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (lane == 0) sh[w] = v;
+  __syncthreads();
+  u192 s{0, 0, 0};
+  for (int i = 0; i < (int)(blockDim.x >> 6); ++i) s = add192(s, sh[i]);
+  __syncthreads();
+  return s;
+}
+
+// ---- decision + residual mass -------------------------------------------------------------
+constexpr int kMaxRowsPerSeq = 2 * 64 + 1;  // 2K+1 rows of a sequence (K <= 64)
+
+__device__ __forceinline__ u128 wave_sum_u128(u128 v) {
+  for (int off = 32; off > 0; off >>= 1) {
+    const uint64_t lo = shfl_xor_u64((uint64_t)v, off);
+    const uint64_t hi = shfl_xor_u64((uint64_t)(v >> 64), off);
+    v += ((u128)hi << 64) | lo;
+  }
+  return v;
+}
+
+// One workgroup per sequence. Its waves take the sequence's 2K+1 rows (target rows j <= K,
+// then draft rows), each row's chunks spread over the lanes: M = max_c m_c,
+// Z = sum_c F_c * S_c with F_c = expfix(m_c - M), and the weight W = E * F_c of the row's
+// draft token; Z and M go to the workspace. Then lane i < K of wave 0 runs the accept test
+// of draft position i (all tests at once; the first failing lane is the rejection), and the
+// decision, the emitted draft ids and the sampling rows' Z and M are recorded.
+__global__ __launch_bounds__(1024) void rej_decide_kernel(RejArgs a) {
+  const int b = blockIdx.x;
+  const int K = a.K, T = K + 1;
+  const int nt = a.B * T;
+  const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = blockDim.x >> 6;
+  __shared__ u128 s_z[kMaxRowsPerSeq];
+  __shared__ float s_m[kMaxRowsPerSeq];
+  __shared__ uint64_t s_w[kMaxRowsPerSeq];
+  for (int j = wv; j < T + K; j += nw) {
+    const int row = j < T ? b * T + j : nt + b * K + (j - T);
+    const float* rm = a.rmax + (size_t)row * a.nch;
+    const uint64_t* rs = a.rsum + (size_t)row * a.nch;
+    float M = -INFINITY;
+    for (int c = lane; c < a.nch; c += 64) M = fmaxf(M, rm[c]);
+    M = npn::wave_max(M);
+    u128 z = 0;
+    for (int c = lane; c < a.nch; c += 64) z += (u128)rs[c] * expfix(rm[c] - M);
+    z = wave_sum_u128(z);
+    if (lane == 0) {
+      const int tok = row_token(a, row);
+      s_z[j] = z;
+      s_m[j] = M;
+      s_w[j] = tok < 0 ? 0 : (uint64_t)a.ex[row] * expfix(rm[tok / CHK] - M);
+      a.zrow[row] = z;
+      a.mrow[row] = M;
+    }
+  }
+  __syncthreads();
+  if (wv != 0) return;
+  bool reject = false;
+  if (lane < K) {
+    const uint32_t U = uniform_fix(a.u_accept[(size_t)b * K + lane]);
+    const u192 lhs = mul192x32(mul64x128(s_w[T + lane], s_z[lane]), U);
+    const u192 rhs = shl24_192(mul64x128(s_w[lane], s_z[T + lane]));
+    reject = gt192(lhs, rhs);
+  }
+  const uint64_t rej = __builtin_amdgcn_ballot_w64(reject);
+  const int acc = rej ? __builtin_ctzll(rej) : K;
+  if (lane == 0) {
+    a.accepted[b] = acc;
+    a.dec_row[b] = acc;
+    a.dec_z[2 * b] = s_z[acc];
+    a.dec_z[2 * b + 1] = acc < K ? s_z[T + acc] : 0;
+    a.dec_m[2 * b] = s_m[acc];  // maxima of the sampling rows
+    a.dec_m[2 * b + 1] = acc < K ? s_m[T + acc] : 0.f;
+  }
+  for (int t = lane; t < T; t += 64) {
+    if (t < acc) a.out_ids[(size_t)b * T + t] = a.draft_ids[(size_t)b * K + t];
+    else if (t > acc) a.out_ids[(size_t)b * T + t] = -1;
+  }
+}
+
+// Residual (or bonus) mass of sequence b's MCHK chunk c.
 template <typename TT>
 __global__ __launch_bounds__(THREADS) void rej_mass_kernel(RejArgs a) {
   const int b = blockIdx.y, c = blockIdx.x;
-  __shared__ int s_acc;
-  if (threadIdx.x < 64) {
-    const int acc = decide_wave(a, b, (int)threadIdx.x, c == 0);
-    if (threadIdx.x == 0) s_acc = acc;
-  }
-  __syncthreads();
-  const SampleRow<TT> s = sample_row_at<TT>(a, b, s_acc);
+  const int acc = a.dec_row[b];
+  const SampleRow<TT> s = sample_row<TT>(a, b, acc, a.dec_m[2 * b], a.dec_m[2 * b + 1],
+                                         a.dec_z[2 * b], a.dec_z[2 * b + 1], (c * MCHK) / CHK);
   const int v0 = c * MCHK + (int)threadIdx.x * PER_M;
-  u128 m = 0;
+  u192 m{0, 0, 0};
   if (v0 < a.V) {
     const RunVals r = load_run(a, s, v0);
 #pragma unroll
     for (int j = 0; j < PER_M; ++j)
-      if (v0 + j < a.V) m += weight_of(s, r.p[j], r.q[j], a.inv_temp);
+      if (v0 + j < a.V) m = add192(m, weight_of(s, r.p[j], r.q[j], a.inv_temp));
   }
-  __shared__ u128 sh[THREADS / 64];
-  m = block_sum_u128(m, sh);
+  __shared__ u192 sh[THREADS / 64];
+  m = block_sum_u192(m, sh);
   if (threadIdx.x == 0) a.cmass[(size_t)b * a.nchm + c] = m;
-}
-
-// ---- 128-bit wave scans (exact integers) ---------------------------------------------------
-__device__ __forceinline__ u128 shfl_u128(u128 v, int src_lane) {
-  uint32_t w[4] = {(uint32_t)v, (uint32_t)(v >> 32), (uint32_t)(v >> 64), (uint32_t)(v >> 96)};
-#pragma unroll
-  for (int k = 0; k < 4; ++k) w[k] = __shfl(w[k], src_lane, 64);
-  return ((u128)w[3] << 96) | ((u128)w[2] << 64) | ((u128)w[1] << 32) | w[0];
-}
-
-__device__ __forceinline__ u128 shfl_up_u128(u128 v, int d) {
-  uint32_t w[4] = {(uint32_t)v, (uint32_t)(v >> 32), (uint32_t)(v >> 64), (uint32_t)(v >> 96)};
-#pragma unroll
-  for (int k = 0; k < 4; ++k) w[k] = __shfl_up(w[k], d, 64);
-  return ((u128)w[3] << 96) | ((u128)w[2] << 64) | ((u128)w[1] << 32) | w[0];
-}
-
-// Inclusive prefix sum over the 64 lanes of a wave.
-__device__ __forceinline__ u128 wave_incl_scan_u128(u128 v) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const u128 o = shfl_up_u128(v, d);
-    if (lane >= d) v += o;
-  }
-  return v;
 }
 
 // Inverse CDF: the smallest v with 2^24 * C_v > U_s * S (C_v the inclusive prefix of the
@@ -670,39 +775,40 @@ __device__ __forceinline__ u128 wave_incl_scan_u128(u128 v) {
 template <typename TT>
 __global__ __launch_bounds__(THREADS) void rej_pick_kernel(RejArgs a) {
   const int b = blockIdx.x;
-  const SampleRow<TT> s = sample_row<TT>(a, b);
+  const int K = a.K, T = K + 1;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   __shared__ int s_chunk;
-  __shared__ u128 s_before;
-  __shared__ u128 s_target;
-  __shared__ u128 s_wtot[THREADS / 64];
+  __shared__ u192 s_before;
+  __shared__ u192 s_target;
+  __shared__ u192 s_wtot[THREADS / 64];
   __shared__ int s_tok;
   __shared__ int s_empty;
   __shared__ ArgPart s_best[THREADS / 64];
-  const u128* cm = a.cmass + (size_t)b * a.nchm;
+  const u192* cm = a.cmass + (size_t)b * a.nchm;
   if (w == 0) {
-    u128 tot = 0;
-    for (int c = lane; c < a.nchm; c += 64) tot += cm[c];
-    tot = wave_incl_scan_u128(tot);
-    tot = shfl_u128(tot, 63);
-    if (lane == 0) s_empty = tot == 0;
-    const u128 target = (u128)uniform_fix(a.u_sample[b]) * tot;  // need 2^24 * C > target
-    u128 carry = 0;
+    u192 tot{0, 0, 0};
+    for (int c = lane; c < a.nchm; c += 64) tot = add192(tot, cm[c]);
+    tot = wave_incl_scan_u192(tot);
+    tot = shfl_u192(tot, 63);
+    if (lane == 0) s_empty = is_zero192(tot);
+    const u192 target = mul192x32(tot, uniform_fix(a.u_sample[b]));  // need 2^24 C > target
+    u192 carry{0, 0, 0};
     int chunk = a.nchm - 1;
-    u128 before = 0;
+    u192 before{0, 0, 0};
     bool found = false;
     for (int c0 = 0; c0 < a.nchm && !found; c0 += 64) {
       const int c = c0 + lane;
-      const u128 m = c < a.nchm ? cm[c] : 0;
-      const u128 incl = wave_incl_scan_u128(m) + carry;
-      const uint64_t hit = __builtin_amdgcn_ballot_w64(c < a.nchm && (incl << 24) > target);
+      const u192 m = c < a.nchm ? cm[c] : u192{0, 0, 0};
+      const u192 incl = add192(wave_incl_scan_u192(m), carry);
+      const uint64_t hit =
+          __builtin_amdgcn_ballot_w64(c < a.nchm && gt192(shl24_192(incl), target));
       if (hit != 0) {
         const int l = __builtin_ctzll(hit);
         chunk = c0 + l;
-        before = shfl_u128(incl - m, l);
+        before = shfl_u192(sub192(incl, m), l);
         found = true;
       }
-      carry = shfl_u128(incl, 63);
+      carry = shfl_u192(incl, 63);
     }
     if (lane == 0) {
       s_chunk = chunk;
@@ -712,15 +818,18 @@ __global__ __launch_bounds__(THREADS) void rej_pick_kernel(RejArgs a) {
     }
   }
   __syncthreads();
+  const int acc = a.dec_row[b];
   if (s_empty) {
-    // No sampling mass: every E of the sampling row is 0, which happens only for a bonus row
-    // whose logits are all NaN or -inf or include +inf (a residual after a rejection always
-    // has mass). The token is then the row's greedy choice: its argmax, NaN counting as the
-    // maximum and ties going to the lowest index (the order of argmax_chunk_kernel).
+    // No sampling mass: every weight of the sampling row is 0, which happens only for a
+    // bonus row whose logits are all NaN or -inf or include +inf (a residual after a
+    // rejection always has mass). The token is then the row's greedy choice: its argmax,
+    // NaN counting as the maximum and ties going to the lowest index (the order of
+    // argmax_chunk_kernel).
+    const TT* p = target_row<TT>(a, b * T + acc);
     float bv = -INFINITY;
     int bi = 0x7FFFFFFF;
     for (int v = (int)threadIdx.x; v < a.V; v += THREADS) {
-      const float pv = elem(s.p, v);
+      const float pv = elem(p, v);
       if (beats(pv, v, bv, bi)) { bv = pv; bi = v; }
     }
     for (int off = 32; off > 0; off >>= 1) {
@@ -734,49 +843,50 @@ __global__ __launch_bounds__(THREADS) void rej_pick_kernel(RejArgs a) {
       ArgPart best = s_best[0];
       for (int k = 1; k < THREADS / 64; ++k)
         if (beats(s_best[k].v, s_best[k].i, best.v, best.i)) best = s_best[k];
-      a.out_ids[(size_t)b * (a.K + 1) + a.dec_row[b]] = best.i;
+      a.out_ids[(size_t)b * T + acc] = best.i;
     }
     return;
   }
-  const int v0 = s_chunk * MCHK + (int)threadIdx.x * PER_M;
+  const int chunk = s_chunk;
+  const SampleRow<TT> s = sample_row<TT>(a, b, acc, a.dec_m[2 * b], a.dec_m[2 * b + 1],
+                                         a.dec_z[2 * b], a.dec_z[2 * b + 1],
+                                         (chunk * MCHK) / CHK);
+  const int v0 = chunk * MCHK + (int)threadIdx.x * PER_M;
   RunVals rv;
-  u128 run = 0;
+  u192 run{0, 0, 0};
   if (v0 < a.V) {
     rv = load_run(a, s, v0);
 #pragma unroll
     for (int j = 0; j < PER_M; ++j)
-      if (v0 + j < a.V) run += weight_of(s, rv.p[j], rv.q[j], a.inv_temp);
+      if (v0 + j < a.V) run = add192(run, weight_of(s, rv.p[j], rv.q[j], a.inv_temp));
   }
-  const u128 incl = wave_incl_scan_u128(run);
+  const u192 incl = wave_incl_scan_u192(run);
   if (lane == 63) s_wtot[w] = incl;
   __syncthreads();
-  u128 c = s_before + incl - run;
-  for (int k = 0; k < w; ++k) c += s_wtot[k];
-  const u128 target = s_target;
-  if (v0 < a.V && ((c + run) << 24) > target) {  // the crossing lies in this run or before
+  u192 c = add192(s_before, sub192(incl, run));
+  for (int k = 0; k < w; ++k) c = add192(c, s_wtot[k]);
+  const u192 target = s_target;
+  if (v0 < a.V && gt192(shl24_192(add192(c, run)), target)) {  // the crossing is in this run
 #pragma unroll
     for (int j = 0; j < PER_M; ++j) {
       const int v = v0 + j;
       if (v >= a.V) break;
-      const u128 wv = weight_of(s, rv.p[j], rv.q[j], a.inv_temp);
-      c += wv;
-      if (wv != 0 && (c << 24) > target) {
+      const u192 wv = weight_of(s, rv.p[j], rv.q[j], a.inv_temp);
+      c = add192(c, wv);
+      if (!is_zero192(wv) && gt192(shl24_192(c), target)) {
         atomicMin(&s_tok, v);
         break;
       }
     }
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    const int T = a.K + 1;
-    a.out_ids[(size_t)b * T + a.dec_row[b]] = s_tok;
-  }
+  if (threadIdx.x == 0) a.out_ids[(size_t)b * T + acc] = s_tok;
 }
 
 // The per-row Z sums come first and the row maxima second: the header documents both as
 // results that the rejection call leaves in the workspace.
 struct WsLayout {
-  size_t zrow, mrow, ex, rmax, dec_row, dec_z, dec_m, cmass, total;
+  size_t zrow, mrow, ex, rmax, rsum, dec_row, dec_z, dec_m, cmass, total;
 };
 
 WsLayout layout(int B, int K, int V) {
@@ -785,16 +895,18 @@ WsLayout layout(int B, int K, int V) {
   auto up = [](size_t x) { return (x + 255) & ~size_t(255); };
   WsLayout l{};
   size_t o = 0;
-  l.zrow = o; o += up(rows * sizeof(uint64_t));
+  l.zrow = o; o += up(rows * sizeof(u128));
   l.mrow = o; o += up(rows * sizeof(float));
   l.ex = o; o += up(rows * sizeof(uint32_t));
+  // chunk maxima; the greedy path's argmax partials share the region
   l.rmax = o; o += up(rows * nch * sizeof(float) > (size_t)B * (K + 1) * nch * sizeof(ArgPart)
                           ? rows * nch * sizeof(float)
                           : (size_t)B * (K + 1) * nch * sizeof(ArgPart));
+  l.rsum = o; o += up(rows * nch * sizeof(uint64_t));
   l.dec_row = o; o += up((size_t)B * sizeof(int32_t));
-  l.dec_z = o; o += up((size_t)B * 2 * sizeof(uint64_t));
+  l.dec_z = o; o += up((size_t)B * 2 * sizeof(u128));
   l.dec_m = o; o += up((size_t)B * 2 * sizeof(float));
-  l.cmass = o; o += up((size_t)B * ((V + MCHK - 1) / MCHK) * sizeof(u128));
+  l.cmass = o; o += up((size_t)B * ((V + MCHK - 1) / MCHK) * sizeof(u192));
   l.total = o;
   return l;
 }
@@ -840,22 +952,23 @@ int rejection_args_ok(const float* target_logits, const float* draft_logits,
                   out_ids,
               NPN_ERR_NULL);
   NPN_REQUIRE(shape_ok(B, K, V), NPN_ERR_SHAPE);
-  // Z <= V * 2^31, so 2^24 * sum R <= 2^24 * Zp * Zq stays below 2^128 for V <= 2^20
+  // Z < 2^80 and every residual sum below 2^162 for V <= 2^20, so the contract's products
+  // stay below 2^192
   NPN_REQUIRE(V <= kRejMaxV, NPN_ERR_SHAPE);
   NPN_REQUIRE(inv_temperature > 0.0f && inv_temperature < 1e30f, NPN_ERR_VALUE);
   return NPN_OK;
 }
 
-// The five rejection kernels on `stream`, with the workspace at `ws` (layout(B, K, V).total
-// bytes, 16-byte aligned, checked by the caller).
-// TT is the target rows' element type: float, or bf16 bits (uint16_t) for the LM-head form,
-// which passes the target rows' group maxima (tgmax, ngmax per row) so the max pass skips them.
+// The four rejection kernels on `stream` (one logit pass, row totals + decision, residual
+// mass, pick),
+// with the workspace at `ws` (layout(B, K, V).total bytes, 16-byte aligned, checked by the
+// caller). TT is the target rows' element type: float, or bf16 bits (uint16_t) for the
+// LM-head form.
 template <typename TT>
 int rejection_launch(const TT* target_logits, const float* draft_logits,
                      const int64_t* draft_ids, const float* u_accept, const float* u_sample,
                      float inv_temperature, int32_t* accepted, int64_t* out_ids, int B, int K,
-                     int V, uint8_t* ws, hipStream_t s, const float* tgmax = nullptr,
-                     int ngmax = 0) {
+                     int V, uint8_t* ws, hipStream_t s) {
   const WsLayout l = layout(B, K, V);
   const int nch = (V + CHK - 1) / CHK;
   // 16-byte pieces of whole rows: V % 8 for bf16 target rows (and V % 4 for the fp32 ones)
@@ -863,17 +976,18 @@ int rejection_launch(const TT* target_logits, const float* draft_logits,
                     NPN_ALIGNED16(draft_logits);
   RejArgs a{target_logits, draft_logits, draft_ids, u_accept, u_sample, inv_temperature,
             accepted, out_ids, B, K, V, nch, (V + MCHK - 1) / MCHK, vec4,
-            reinterpret_cast<uint64_t*>(ws + l.zrow), reinterpret_cast<float*>(ws + l.mrow),
+            reinterpret_cast<u128*>(ws + l.zrow), reinterpret_cast<float*>(ws + l.mrow),
             reinterpret_cast<uint32_t*>(ws + l.ex), reinterpret_cast<float*>(ws + l.rmax),
-            reinterpret_cast<int32_t*>(ws + l.dec_row), reinterpret_cast<uint64_t*>(ws + l.dec_z),
-            reinterpret_cast<float*>(ws + l.dec_m), reinterpret_cast<u128*>(ws + l.cmass),
-            tgmax, ngmax};
+            reinterpret_cast<uint64_t*>(ws + l.rsum), reinterpret_cast<int32_t*>(ws + l.dec_row),
+            reinterpret_cast<u128*>(ws + l.dec_z), reinterpret_cast<float*>(ws + l.dec_m),
+            reinterpret_cast<u192*>(ws + l.cmass)};
   const int rows = B * (2 * K + 1);
-  hipLaunchKernelGGL(rej_max_kernel<TT>, dim3(nch, rows), dim3(THREADS), 0, s, a);
   if (inv_temperature == 1.0f)
-    hipLaunchKernelGGL((rej_sum_kernel<true, TT>), dim3(nch, rows), dim3(THREADS), 0, s, a);
+    hipLaunchKernelGGL((rej_scan_kernel<true, TT>), dim3(nch, rows), dim3(THREADS), 0, s, a);
   else
-    hipLaunchKernelGGL((rej_sum_kernel<false, TT>), dim3(nch, rows), dim3(THREADS), 0, s, a);
+    hipLaunchKernelGGL((rej_scan_kernel<false, TT>), dim3(nch, rows), dim3(THREADS), 0, s, a);
+  const int dthreads = 64 * (2 * K + 1 < 16 ? 2 * K + 1 : 16);
+  hipLaunchKernelGGL(rej_decide_kernel, dim3(B), dim3(dthreads), 0, s, a);
   hipLaunchKernelGGL(rej_mass_kernel<TT>, dim3(a.nchm, B), dim3(THREADS), 0, s, a);
   hipLaunchKernelGGL(rej_pick_kernel<TT>, dim3(B), dim3(THREADS), 0, s, a);
   return npn_launch_status();
@@ -974,21 +1088,19 @@ extern "C" int npn_argmax_parts(const void* parts, int nparts, int64_t* ids, flo
 }
 
 // ---- rejection sampling straight from the LM head --------------------------------------------
-// The LM head's GEMM writes the target logits in bf16 and, in its epilogue, each row's maxima
-// per column group; the rejection passes then read the target rows in bf16 (half the bytes)
-// and skip them in the max pass. The decisions equal npn_accept_rejection's on the same
-// logits cast to fp32 (every step of the contract sees the same values).
+// The LM head's GEMM writes the target logits in bf16; the rejection pass then reads the
+// target rows in bf16 (half the bytes). The decisions equal npn_accept_rejection's on the
+// same logits cast to fp32 (every step of the contract sees the same values).
 namespace {
 
-size_t lm_head_gmax_bytes(int M, int G) { return ((size_t)M * G * sizeof(float) + 255) & ~(size_t)255; }
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 }  // namespace
 
 extern "C" size_t npn_accept_rejection_lm_head_workspace_size(int B, int K, int H, int V) {
   if (!shape_ok(B, K, V) || V > kRejMaxV) return 0;
-  const int G = npn_fp8_matmul_argmax_groups(B * (K + 1), H, V);
-  if (G <= 0) return 0;
-  return layout(B, K, V).total + lm_head_gmax_bytes(B * (K + 1), G);
+  if (npn_fp8_matmul_argmax_groups(B * (K + 1), H, V) <= 0) return 0;  // GEMM shape rules
+  return align256(layout(B, K, V).total) + npn_fp8_matmul_workspace_size(B * (K + 1), H, V);
 }
 
 extern "C" int npn_accept_rejection_lm_head(const uint16_t* hidden, const int8_t* lm_head_w,
@@ -1005,17 +1117,16 @@ extern "C" int npn_accept_rejection_lm_head(const uint16_t* hidden, const int8_t
                                    out_ids, B, K, V);
   if (st != NPN_OK) return st;
   const int M = B * (K + 1);
-  const int G = npn_fp8_matmul_argmax_groups(M, H, V);
-  NPN_REQUIRE(G > 0, NPN_ERR_SHAPE);
   const size_t need = npn_accept_rejection_lm_head_workspace_size(B, K, H, V);
+  NPN_REQUIRE(need > 0, NPN_ERR_SHAPE);
   NPN_REQUIRE(workspace != nullptr && workspace_bytes >= need, NPN_ERR_WORKSPACE);
   NPN_REQUIRE(NPN_ALIGNED16(workspace), NPN_ERR_ALIGN);
   uint8_t* ws = static_cast<uint8_t*>(workspace);
-  float* gmax = reinterpret_cast<float*>(ws + layout(B, K, V).total);
-  const int gst = npn_fp8_matmul_rowmax(hidden, lm_head_w, lm_head_scale, target_logits, gmax, M,
-                                        H, V, stream);
+  const size_t gemm_off = align256(layout(B, K, V).total);
+  const int gst = npn_fp8_matmul(hidden, lm_head_w, lm_head_scale, target_logits, M, H, V,
+                                 ws + gemm_off, need - gemm_off, stream);
   if (gst != NPN_OK) return gst;
   return rejection_launch(static_cast<const uint16_t*>(target_logits), draft_logits, draft_ids,
                           u_accept, u_sample, inv_temperature, accepted, out_ids, B, K, V, ws,
-                          static_cast<hipStream_t>(stream), gmax, G);
+                          static_cast<hipStream_t>(stream));
 }

@@ -16,7 +16,8 @@ contrib/qwen3.6-27b/static_decode.py:1313).
 
 accepted[b] is the number of accepted drafts (0..K); out_ids[b] holds those drafts,
 then the correction (or bonus) token, then -1. Rejection sampling follows Leviathan
-et al. 2023 (Alg. 1) under the library's integer softmax contract, so its decisions
+et al. 2023 (Alg. 1) under the library's integer softmax contract (chunk-relative exponentials
+with exact chunk factors, so one pass over the logits gives every sum), so its decisions
 are bit-identical to the CPU restatement for the same logits and uniforms.
 """
 import torch
@@ -137,10 +138,8 @@ def accept_rejection_lm_head(hidden: torch.Tensor, lm_head_w: torch.Tensor,
     """New op: rejection sampling with the target logits made by the LM head in the same
     call: hidden [B*(K+1), H] bf16 (row b*(K+1) + t), lm_head_w [H, V] e4m3fn bytes,
     lm_head_scale [V] f32 -> (accepted [B] int32, out_ids [B, K+1] int64, target_logits
-    [B, K+1, V] bf16). The GEMM's epilogue also gives each row's maxima per column group,
-    so the sampling passes read the target rows once less and in bf16. Equal, bit for bit,
-    to accept_rejection(fp8::matmul(hidden, w, scale).float().view(B, K+1, V), ...) wherever
-    fp8::matmul's plan does not split K (vocabulary-wide V)."""
+    [B, K+1, V] bf16). The sampling pass reads the target rows once, in bf16. Equal, bit for
+    bit, to accept_rejection(fp8::matmul(hidden, w, scale).float().view(B, K+1, V), ...)."""
     B, K, V = draft_logits.shape
     T = K + 1
     require(hidden, "hidden", torch.bfloat16)

@@ -19,24 +19,30 @@ test that emitted tokens follow p, and the special cases p == q (always accept)
 and q(x) > 0 = p(x) (always reject, residual = p restricted to p > q)
 (tests/test_oracle_accept.py).
 
-Integer softmax contract (shared bit-for-bit with ``csrc/spec_accept.hip``):
-- s_v = t_v * inv_temp (fp32 multiply), m = max_v s_v over the non-NaN s_v (-inf if
-  none), x_v = s_v - m (fp32); NaN x_v give E_v = 0.
-- E_v = floor(2^31 * exp_c(x_v)) as an integer below 2^31 + 1, with exp_c the fp32
+Integer softmax contract (shared bit-for-bit with ``csrc/spec_accept.hip``), built so
+that one pass over the logits gives every sum (each vocabulary chunk's values are
+referred to the chunk's own maximum, and chunks to the row maximum by exact factors):
+- s_v = t_v * inv_temp (fp32 multiply). The vocabulary is cut into chunks of CHUNK = 8192
+  entries; m_c = max of the non-NaN s_v of chunk c (-inf if none), M = max_c m_c.
+- E_v = floor(2^31 * exp_c(s_v - m_c)) for v in chunk c (fp32 subtraction; NaN gives 0),
+  F_c = floor(2^31 * exp_c(m_c - M)), both below 2^31 + 1, with exp_c the fp32
   Cody-Waite reduction + degree-7 Taylor polynomial below, evaluated with correctly
-  rounded fp32 fused multiply-adds (IEEE-754 fusedMultiplyAdd) and one fp32 subtraction,
-  so every step is one IEEE-754 operation that CPU and GPU round identically.
-- Z = sum_v E_v in exact integer arithmetic (order-independent).
-- p(v) = E^p_v / Z_p, q(v) = E^q_v / Z_q. Uniforms u are read as
-  U = floor(u * 2^24).
-- Accept draft x at position i iff U * E^q_x * Z_p <= 2^24 * E^p_x * Z_q
-  (integers below 2^104).
-- At the first rejection sample from R_v = max(0, E^p_v Z_q - E^q_v Z_p); if all
-  K drafts are accepted sample the bonus from R_v = E^p_v of row K. The token is
-  the smallest v with 2^24 * sum_{w<=v} R_w > U_s * sum_w R_w.
+  rounded fp32 fused multiply-adds (IEEE-754 fusedMultiplyAdd), so every step is one
+  IEEE-754 operation that CPU and GPU round identically.
+- The weight of v is W_v = E_v * F_c (an integer below 2^62 + 1) and the row's total is
+  Z = sum_v W_v = sum_c F_c * S_c with S_c = sum_{v in c} E_v, in exact integers
+  (order-independent; Z < 2^80 for V <= 2^20). W_v / Z approximates softmax(s)_v to about
+  2^-30 relative for every entry within 21 of its chunk maximum whose chunk maximum is
+  within 21 of M.
+- p(v) = W^p_v / Z_p, q(v) = W^q_v / Z_q. Uniforms u are read as U = floor(u * 2^24).
+- Accept draft x at position i iff U * W^q_x * Z_p <= 2^24 * W^p_x * Z_q
+  (integers below 2^166).
+- At the first rejection sample from R_v = max(0, W^p_v Z_q - W^q_v Z_p); if all
+  K drafts are accepted sample the bonus from R_v = W^p_v of row K. The token is
+  the smallest v with 2^24 * sum_{w<=v} R_w > U_s * sum_w R_w (integers below 2^184).
 - Rows without mass: Z = 0 when no entry is finite relative to the maximum (all NaN or
   -inf, or a +inf entry). Such a target or draft row passes the accept test (both sides
-  are 0). A residual after a rejection always has mass (sum_v (E^p_v Z_q - E^q_v Z_p) = 0
+  are 0). A residual after a rejection always has mass (sum_v (W^p_v Z_q - W^q_v Z_p) = 0
   with a negative term at the rejected token), so only a bonus row can be empty; its token
   is then the greedy one, argmax of the target row (NaN counts as the maximum, first index
   on ties).
@@ -104,12 +110,34 @@ def expfix(x):
     return bits.view(np.float32).astype(np.uint32)
 
 
-def row_weights(logits_row, inv_temp=1.0):
-    """(E [V] uint32, Z python int, m fp32) for one logits row under the contract."""
+CHUNK = 8192                                     # vocabulary entries per chunk
+
+
+def row_chunks(logits_row, inv_temp=1.0):
+    """(s fp32 [V], m [nch] fp32 chunk maxima, S [nch] python ints, E [V] uint32) of one row."""
     s = (np.asarray(logits_row, np.float32) * _F(inv_temp)).astype(np.float32)
-    m = np.fmax.reduce(s, initial=_F(-np.inf))     # NaN entries are ignored (and get E = 0)
-    E = expfix((s - m).astype(np.float32))
-    return E, int(E.sum(dtype=np.uint64)), m
+    V = s.shape[0]
+    nch = (V + CHUNK - 1) // CHUNK
+    m = np.empty(nch, np.float32)
+    E = np.empty(V, np.uint32)
+    S = []
+    for c in range(nch):
+        seg = s[c * CHUNK:(c + 1) * CHUNK]
+        m[c] = np.fmax.reduce(seg, initial=_F(-np.inf))   # NaN entries are ignored
+        E[c * CHUNK:(c + 1) * CHUNK] = expfix((seg - m[c]).astype(np.float32))
+        S.append(int(E[c * CHUNK:(c + 1) * CHUNK].sum(dtype=np.uint64)))
+    return s, m, S, E
+
+
+def row_weights(logits_row, inv_temp=1.0):
+    """(W [V] uint64, Z python int, M fp32) for one logits row under the contract:
+    W_v = E_v * F_c (below 2^62 + 1, exact in uint64), Z = sum_c F_c * S_c, M the row max."""
+    _, m, S, E = row_chunks(logits_row, inv_temp)
+    M = np.fmax.reduce(m, initial=_F(-np.inf))
+    F = expfix((m - M).astype(np.float32))
+    Z = sum(int(f) * sc for f, sc in zip(F.tolist(), S))
+    W = E.astype(np.uint64) * np.repeat(F.astype(np.uint64), CHUNK)[:E.shape[0]]
+    return W, Z, M
 
 
 def uniform_fix(u):
@@ -155,10 +183,10 @@ def accept_rejection(target, draft, draft_ids, u_accept, u_sample, inv_temp=1.0)
         if a < K:
             Ep, Zp, _ = row_weights(target[b, a], inv_temp)
             Eq, Zq, _ = row_weights(draft[b, a], inv_temp)
-            R = [max(0, int(ep) * Zq - int(eq) * Zp) for ep, eq in zip(Ep.tolist(), Eq.tolist())]
+            R = [max(0, ep * Zq - eq * Zp) for ep, eq in zip(Ep.tolist(), Eq.tolist())]
         else:
             Ep, _, _ = row_weights(target[b, K], inv_temp)
-            R = [int(e) for e in Ep.tolist()]
+            R = Ep.tolist()
         if sum(R) == 0:
             # no sampling mass (only a bonus row whose logits are all NaN / -inf or hold +inf:
             # every E is 0): the row's greedy token, NaN counting as the maximum

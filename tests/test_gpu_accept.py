@@ -115,8 +115,9 @@ def test_rejection_row_sums_bit_exact(ops, B, K, V, seed, inv_t):
          B, K, V, ws, ws.numel(), stream_of(t))
     torch.cuda.synchronize()
     R = B * (2 * K + 1)
-    off = (8 * R + 255) // 256 * 256
-    z = ws[:8 * R].cpu().numpy().view(np.uint64)
+    off = (16 * R + 255) // 256 * 256
+    zw = ws[:16 * R].cpu().numpy().view(np.uint64).reshape(R, 2)   # u128, low word first
+    z = [int(lo) | (int(hi) << 64) for lo, hi in zw]
     m = ws[off:off + 4 * R].cpu().numpy().view(np.float32)
     rows = [target[b, i].numpy() for b in range(B) for i in range(K + 1)]
     rows += [draft[b, i].numpy() for b in range(B) for i in range(K)]

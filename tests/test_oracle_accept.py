@@ -243,3 +243,57 @@ def test_empty_rows_pass_the_accept_test():
     u[:] = np.float32(0.999)
     acc, _ = oa.accept_rejection(target, draft, ids, u, us)
     assert (acc == K).all()
+
+
+def test_multichunk_weights_follow_softmax():
+    """With several 8192-entry chunks whose maxima differ (the row maximum in chunk 2, one
+    chunk 40 below it), the contract's p = W / Z equals float64 softmax(s) to the contract's
+    precision (2^-19 relative + 2^-29 absolute), Z is exactly the sum of the weights, the top chunk's weights are E * 2^31, and
+    the far chunk gets weight 0. A factor taken against the wrong maximum, or a chunk left out
+    of Z, moves p by orders of magnitude more than the bound."""
+    rng = np.random.default_rng(5)
+    C = oa.CHUNK
+    V = 4 * C + 1000
+    t = rng.normal(0.0, 2.0, V).astype(np.float32)
+    t[C:2 * C] -= 6.0            # chunk 1 below the others
+    t[2 * C:3 * C] += 3.0        # the row maximum lives in chunk 2
+    t[3 * C:4 * C] -= 40.0       # a chunk whose factor is 0
+    for inv_t in (1.0, 0.7):
+        W, Z, M = oa.row_weights(t, inv_t)
+        assert Z == int(W.astype(object).sum())
+        s = (t * np.float32(inv_t)).astype(np.float32).astype(np.float64)
+        ref = np.exp(s - s.max())
+        ref /= ref.sum()
+        p = np.array([int(w) / Z for w in W.tolist()])
+        # each factor is exp to ~2^-21 relative plus one unit of flooring: |dp| is at most
+        # about 2^-20 p + 2^31 / Z, with Z >= 2^62 (the row maximum's own weight)
+        assert np.all(np.abs(p - ref) <= 2.0 ** -19 * ref + 2.0 ** -29)
+        assert np.all(W[3 * C:4 * C] == 0)
+        _, m, S, E = oa.row_chunks(t, inv_t)
+        assert M == m.max() and np.argmax(m) == 2
+        top = W[2 * C:3 * C]
+        assert np.array_equal(top, E[2 * C:3 * C].astype(np.uint64) << np.uint64(31))
+
+
+def test_multichunk_p_equals_q_accepts_and_residual_is_valid():
+    """Rows spanning several chunks: p == q always accepts; a rejection samples a token with
+    p > q (the residual's support)."""
+    rng = np.random.default_rng(6)
+    V, K = 2 * oa.CHUNK + 300, 3
+    t = rng.normal(0, 1.5, (2, K + 1, V)).astype(np.float32)
+    ids = rng.integers(0, V, (2, K))
+    u = rng.random((2, K)).astype(np.float32)
+    us = rng.random(2).astype(np.float32)
+    acc, _ = oa.accept_rejection(t, t[:, :K].copy(), ids, u, us)
+    assert (acc == K).all()
+    d = t[:, :K].copy()
+    d[:, :, :oa.CHUNK] += 4.0                       # q puts its mass on chunk 0
+    ids[:] = 5                                      # drafts from the region q favours
+    acc, out = oa.accept_rejection(t, d, ids, np.full((2, K), 0.999, np.float32), us)
+    for b in range(2):
+        a = int(acc[b])
+        if a < K:
+            Wp, Zp, _ = oa.row_weights(t[b, a])
+            Wq, Zq, _ = oa.row_weights(d[b, a])
+            x = int(out[b, a])
+            assert int(Wp[x]) * Zq > int(Wq[x]) * Zp

@@ -171,7 +171,8 @@ size_t npn_gqa_tail_verify_workspace_size(int B, int T, int q_heads, int kv_head
  *   kv_len      [B] int32, cache rows before the T verify rows (kv_len+T <= s_max)
  * Row (b,t,h) uses kv head h/(Hq/Hkv) and attends rows [0, kv_len[b]+t].
  * Output: out [B, T, Hq, 256] bf16. Limits: Hq/Hkv * T <= 48, s_max <= 2^23,
- * B * Hkv <= 65535. The workspace query returns 0 outside them. */
+ * B * Hkv <= 65535. The workspace query returns 0 outside them. gate, out, the
+ * caches and the workspace must be 16-byte aligned. */
 int npn_gqa_tail_verify(const uint16_t* query, const uint16_t* gate, const float* q_norm,
                         const float* cos, const float* sin, const uint16_t* cache_k,
                         const uint16_t* cache_v, const int32_t* kv_len, uint16_t* out, int B,

@@ -558,9 +558,30 @@ __global__ __launch_bounds__(256) void gqa_merge_kernel(MergeArgs a) {
   const float* pml = a.part_ml + ((size_t)(w0 + pr) * a.R + r) * 2;
   const float* po = a.part_o + ((size_t)(w0 + pr) * a.R + r) * DH + 4 * lane;
   auto live = [&](int w) { return w <= w1 && wg_first_step(w, S) < wg_first_step(w + 1, S); };
-  // this wave's segments w0 + q + 4 j: their maximum, then their rescaled sums
+  const int t = r / grp, qh = g * grp + (r - t * grp);
+  const size_t oi = (((size_t)b * a.T + t) * a.Hq + qh) * DH + 4 * lane;
+  // The gate is needed only by wave 0's output, after the merge: its load is issued first.
+  uint2 gate_bits = make_uint2(0u, 0u);
+  if (q == 0) gate_bits = *reinterpret_cast<const uint2*>(a.gate + oi);
+  // This wave's segments w0 + q + 4 j: their maximum, then their rescaled sums. The first
+  // batch of four (all of a pair's segments whenever it has at most 16) is loaded once and
+  // kept in registers for both passes: one round trip to memory instead of two, with the
+  // same arithmetic.
+  float mv0[4], lv0[4];
+  f32x4 ov0[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int w = w0 + q + 4 * j;
+    const bool ok = live(w);
+    mv0[j] = ok ? pml[(w - w0) * stride_ml] : kNegBig;
+    lv0[j] = ok ? pml[(w - w0) * stride_ml + 1] : 0.f;
+    ov0[j] = ok ? *reinterpret_cast<const f32x4*>(po + (w - w0) * stride_o)
+                : f32x4{0.f, 0.f, 0.f, 0.f};
+  }
   float M = kNegBig;
-  for (int base = w0 + q; base <= w1; base += 16) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) M = fmaxf(M, mv0[j]);
+  for (int base = w0 + q + 16; base <= w1; base += 16) {
     float mv[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -572,7 +593,13 @@ __global__ __launch_bounds__(256) void gqa_merge_kernel(MergeArgs a) {
   }
   float l = 0.f;
   f32x4 o = {0.f, 0.f, 0.f, 0.f};
-  for (int base = w0 + q; base <= w1; base += 16) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float f = exp2f(mv0[j] - M);
+    l += f * lv0[j];
+    o += f * ov0[j];
+  }
+  for (int base = w0 + q + 16; base <= w1; base += 16) {
     float mv[4], lv[4];
     f32x4 ov[4];
 #pragma unroll
@@ -611,13 +638,12 @@ __global__ __launch_bounds__(256) void gqa_merge_kernel(MergeArgs a) {
     lt += f * s_ml[k][1];
     ot += f * s_o[k][lane];
   }
-  const int t = r / grp, qh = g * grp + (r - t * grp);
-  const size_t oi = (((size_t)b * a.T + t) * a.Hq + qh) * DH + 4 * lane;
   const float inv = 1.0f / lt;
+  const uint32_t gw[2] = {gate_bits.x, gate_bits.y};
   uint32_t w[2];
   for (int j = 0; j < 2; ++j) {
-    const float g0 = npn::sigmoid(npn::bf16_to_f32(a.gate[oi + 2 * j]));
-    const float g1 = npn::sigmoid(npn::bf16_to_f32(a.gate[oi + 2 * j + 1]));
+    const float g0 = npn::sigmoid(npn::bf16_to_f32((uint16_t)(gw[j] & 0xFFFFu)));
+    const float g1 = npn::sigmoid(npn::bf16_to_f32((uint16_t)(gw[j] >> 16)));
     w[j] = npn::f32_to_bf16(ot[2 * j] * inv * g0) |
            ((uint32_t)npn::f32_to_bf16(ot[2 * j + 1] * inv * g1) << 16);
   }
@@ -765,7 +791,8 @@ static int tail_verify_launch(const uint16_t* query, const uint16_t* gate, const
                   out,
               NPN_ERR_NULL);
   NPN_REQUIRE(verify_shape_ok(B, T, q_heads, kv_heads, s_max), NPN_ERR_SHAPE);
-  NPN_REQUIRE(NPN_ALIGNED16(cache_k) && NPN_ALIGNED16(cache_v) && NPN_ALIGNED16(workspace),
+  NPN_REQUIRE(NPN_ALIGNED16(cache_k) && NPN_ALIGNED16(cache_v) && NPN_ALIGNED16(workspace) &&
+                  NPN_ALIGNED16(gate) && NPN_ALIGNED16(out),
               NPN_ERR_ALIGN);
   const VerifyPlan p = plan(B, T, q_heads, kv_heads);
   NPN_REQUIRE(workspace != nullptr && workspace_bytes >= p.total, NPN_ERR_WORKSPACE);

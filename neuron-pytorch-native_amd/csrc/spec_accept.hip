@@ -785,6 +785,11 @@ __global__ __launch_bounds__(THREADS) void rej_pick_kernel(RejArgs a) {
   __shared__ int s_empty;
   __shared__ ArgPart s_best[THREADS / 64];
   const u192* cm = a.cmass + (size_t)b * a.nchm;
+  // The sampling row's decision values do not depend on the chunk: their loads are issued
+  // before the chunk search, so they are in registers when it ends.
+  const int acc = a.dec_row[b];
+  const float dmp = a.dec_m[2 * b], dmq = a.dec_m[2 * b + 1];
+  const u128 dzp = a.dec_z[2 * b], dzq = a.dec_z[2 * b + 1];
   if (w == 0) {
     u192 tot{0, 0, 0};
     for (int c = lane; c < a.nchm; c += 64) tot = add192(tot, cm[c]);
@@ -818,7 +823,6 @@ __global__ __launch_bounds__(THREADS) void rej_pick_kernel(RejArgs a) {
     }
   }
   __syncthreads();
-  const int acc = a.dec_row[b];
   if (s_empty) {
     // No sampling mass: every weight of the sampling row is 0, which happens only for a
     // bonus row whose logits are all NaN or -inf or include +inf (a residual after a
@@ -848,9 +852,7 @@ __global__ __launch_bounds__(THREADS) void rej_pick_kernel(RejArgs a) {
     return;
   }
   const int chunk = s_chunk;
-  const SampleRow<TT> s = sample_row<TT>(a, b, acc, a.dec_m[2 * b], a.dec_m[2 * b + 1],
-                                         a.dec_z[2 * b], a.dec_z[2 * b + 1],
-                                         (chunk * MCHK) / CHK);
+  const SampleRow<TT> s = sample_row<TT>(a, b, acc, dmp, dmq, dzp, dzq, (chunk * MCHK) / CHK);
   const int v0 = chunk * MCHK + (int)threadIdx.x * PER_M;
   RunVals rv;
   u192 run{0, 0, 0};

@@ -418,6 +418,14 @@ int npn_gqa_split(const uint16_t* proj, int ld, uint16_t* query, uint16_t* gate,
 int npn_residual_rmsnorm_partials(const uint16_t* hidden_in, const float* partial, int split_k,
                                   const float* scale, const float* weight, uint16_t* hidden_out,
                                   uint16_t* normed, int M, int H, float eps, void* stream);
+/* torch.ops.normfuse.residual_add_partials -- new op: the residual add that ends the
+ * layer stack (static_decode.py:533-542, the last layer's hidden += mlp(normed)) with the
+ * MLP's down-projection taken as split-K partials: hidden_out = bf16(hidden_in + delta),
+ * delta as above, equal to npn_fp8_matmul followed by a bf16 add. hidden_out may alias
+ * hidden_in. */
+int npn_residual_add_partials(const uint16_t* hidden_in, const float* partial, int split_k,
+                              const float* scale, uint16_t* hidden_out, int M, int H,
+                              void* stream);
 int npn_deltanet_split_partials(const float* partial, int split_k, const float* scale, int ld,
                                 uint16_t* mixed_qkv, uint16_t* z, float* a_out, float* b_out,
                                 int M, int qkv_n, int z_n, int hv, void* stream);

@@ -277,6 +277,25 @@ int grid_for(size_t chunks) {
   return (int)(blocks < 4096 ? (blocks > 0 ? blocks : 1) : 4096);
 }
 
+// ---- hidden += bf16(scale * sum of split-K partials), no norm (the slice's last residual):
+// one thread per 8 columns, the partials summed by PartSrc in the GEMM reduction's order.
+__global__ __launch_bounds__(256) void residual_add_partials_kernel(
+    const uint16_t* h_in, PartSrc delta, uint16_t* h_out, int M, int H) {  // h_out may alias h_in
+  const int nc = H / 8;
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (size_t)M * nc) return;
+  const size_t row = i / nc;
+  const int col = 8 * (int)(i - row * nc);
+  const u32x4 hv = *reinterpret_cast<const u32x4*>(h_in + row * H + col);
+  const u32x4 dv = delta.load(row, col);
+  float x[8], d[8];
+  unpack8(hv, x);
+  unpack8(dv, d);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) x[j] = npn::bf16_to_f32(npn::f32_to_bf16(x[j] + d[j]));
+  *reinterpret_cast<u32x4*>(h_out + row * H + col) = pack8(x);
+}
+
 }  // namespace
 
 extern "C" int npn_residual_rmsnorm(const uint16_t* hidden_in, const uint16_t* delta,
@@ -313,6 +332,23 @@ extern "C" int npn_residual_rmsnorm_partials(const uint16_t* hidden_in, const fl
   hipLaunchKernelGGL(residual_rmsnorm_kernel<PartSrc>, dim3(M), dim3(kNormThreads), 0,
                      static_cast<hipStream_t>(stream), hidden_in, src, true, weight, hidden_out,
                      normed, H, eps);
+  return npn_launch_status();
+}
+
+extern "C" int npn_residual_add_partials(const uint16_t* hidden_in, const float* partial,
+                                         int split_k, const float* scale, uint16_t* hidden_out,
+                                         int M, int H, void* stream) {
+  NPN_REQUIRE(hidden_in && partial && scale && hidden_out, NPN_ERR_NULL);
+  NPN_REQUIRE(M >= 1 && H >= 8 && H % 8 == 0 && split_k >= 1 && split_k <= kMaxSplit &&
+                  (int64_t)M * H < ((int64_t)1 << 40),
+              NPN_ERR_SHAPE);
+  NPN_REQUIRE(NPN_ALIGNED16(hidden_in) && NPN_ALIGNED16(partial) && NPN_ALIGNED16(scale) &&
+                  NPN_ALIGNED16(hidden_out),
+              NPN_ERR_ALIGN);
+  const PartSrc src{partial, scale, H, split_k, (size_t)M * H};
+  const int64_t n = (int64_t)M * (H / 8);
+  hipLaunchKernelGGL(residual_add_partials_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256),
+                     0, static_cast<hipStream_t>(stream), hidden_in, src, hidden_out, M, H);
   return npn_launch_status();
 }
 

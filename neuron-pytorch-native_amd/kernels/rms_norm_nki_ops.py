@@ -10,6 +10,8 @@ plus the residual form the decode loop applies before every norm
   normfuse::residual_rms_norm(hidden, delta, weight, eps) -> (hidden + delta, rms_norm(...))
   normfuse::residual_rms_norm_partials(hidden, partials, scale, weight, eps): the same with
       delta taken from fp8::matmul_partials output (the GEMM reduction fused in)
+  normfuse::residual_add_partials(hidden, partials, scale) -> hidden + delta, no norm (the
+      residual add that ends the layer stack)
 
 The reference op takes one token's [H] vector; this one takes any number of rows.
 """
@@ -85,3 +87,26 @@ def residual_rms_norm_partials(hidden: torch.Tensor, partials: torch.Tensor, sca
 @residual_rms_norm_partials.register_fake
 def _(hidden, partials, scale, weight, eps=RMS_EPS):
     return torch.empty_like(hidden), torch.empty_like(hidden)
+
+
+@torch.library.custom_op("normfuse::residual_add_partials", mutates_args=(), device_types="cuda")
+def residual_add_partials(hidden: torch.Tensor, partials: torch.Tensor,
+                         scale: torch.Tensor) -> torch.Tensor:
+    """hidden + bf16(scale * partials.sum(0)) (summed in order) in bf16, with the partials
+    of fp8::matmul_partials [S, M, H]: bit-identical to fp8::matmul followed by a bf16 add.
+    The residual add that ends the layer stack (static_decode.py:533-542)."""
+    M, H = _rows(hidden)
+    require(hidden, "hidden", torch.bfloat16)
+    if partials.dim() != 3 or tuple(partials.shape[1:]) != (M, H):
+        raise RuntimeError(f"partials must be [S, {M}, {H}], got {tuple(partials.shape)}")
+    require(partials, "partials", torch.float32)
+    require(scale, "scale", torch.float32, numel=H)
+    h_out = torch.empty_like(hidden)
+    call("npn_residual_add_partials", hidden, partials, partials.shape[0], scale, h_out, M, H,
+         stream_of(hidden))
+    return h_out
+
+
+@residual_add_partials.register_fake
+def _(hidden, partials, scale):
+    return torch.empty_like(hidden)

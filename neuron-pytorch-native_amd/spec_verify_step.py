@@ -219,7 +219,7 @@ class VerifySlice:
         return fp8_project(attn.reshape(B * T, GQA_HQ * GQA_DH), L["o_proj"], self.timer,
                            f"fp8.matmul[{B * T}x{GQA_HQ * GQA_DH}x{HIDDEN}]", self.fuse_splitk)
 
-    def _mlp(self, L, h, last=False):
+    def _mlp(self, L, h):
         M = h.shape[0]
         if self.fuse_swiglu:
             w, sc = L["gate_up"]
@@ -229,7 +229,7 @@ class VerifySlice:
             gu = fp8_linear(h, L["gate_up"], self.timer, f"fp8.matmul[{M}x{HIDDEN}x{2 * INTER}]")
             act = self.timer("glue.silu_mul", torch.ops.glue.silu_mul, gu)
         return fp8_project(act, L["down"], self.timer, f"fp8.matmul[{M}x{INTER}x{HIDDEN}]",
-                           self.fuse_splitk and not last)
+                           self.fuse_splitk)
 
     def _add_norm(self, hidden, d, weight):
         """(hidden + d, its (1+w) RMSNorm); d is a bf16 delta or (partials, scale)."""
@@ -264,9 +264,12 @@ class VerifySlice:
             if trace is not None:
                 trace.append(hidden)
             last = i + 1 == len(layers)
-            d = self._mlp(L, normed, last)
+            d = self._mlp(L, normed)
             if not last:
                 hidden, normed = self._add_norm(hidden, d, layers[i + 1]["in_norm"])
+            elif isinstance(d, tuple):
+                hidden = self.timer("normfuse.residual_add",
+                                    torch.ops.normfuse.residual_add_partials, hidden, *d)
             else:
                 hidden = hidden + d
         if trace is not None:

@@ -1,5 +1,6 @@
 """The split-K reduction of the FP8 GEMM fused into the glue ops that consume its output
-(fp8::matmul_partials + normfuse::residual_rms_norm_partials / glue::*_split_partials)
+(fp8::matmul_partials + normfuse::residual_rms_norm_partials / residual_add_partials /
+glue::*_split_partials)
 against fp8::matmul followed by the bf16 forms of the same ops.
 
 Bar: bit-exact. The fused ops compute bf16(scale * (p_0 + ... + p_{S-1})) in the order of the
@@ -62,6 +63,21 @@ def test_residual_rms_norm_partials(ops, M, K):
     assert p.shape[0] > 1
     assert torch.equal(_bits(h_f), _bits(h_r))
     assert torch.equal(_bits(n_f), _bits(n_r))
+
+
+@pytest.mark.parametrize("M,K", [(256, 17408), (256, 6144), (8, 17408), (13, 6144)])
+def test_residual_add_partials(ops, M, K):
+    """The stack's last residual add from the down-projection's partials equals fp8::matmul
+    followed by a bf16 add."""
+    H = 5120
+    x, w, sc = _inputs(M, K, H, K + 1)
+    g = torch.Generator(device="cuda").manual_seed(9)
+    hid = (torch.randn(M, H, generator=g, device="cuda") * 2).to(torch.bfloat16)
+    p = ops.fp8.matmul_partials(x, w)
+    got = ops.normfuse.residual_add_partials(hid, p, sc)
+    ref = hid + ops.fp8.matmul(x, w, sc)
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(got), _bits(ref))
 
 
 def test_deltanet_split_partials(ops):

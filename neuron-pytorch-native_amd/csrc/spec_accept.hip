@@ -537,7 +537,12 @@ struct SampleRow {
   float mp, mq;    // chunk maxima of the chunk being weighed
   uint64_t fp;     // F^p_c (the bonus weight is E^p F^p_c)
   u128 gp, gq;     // F^p_c Zq and F^q_c Zp
+  double gpd, gqd; // the same, rounded to fp64 (relative error below 2^-51)
 };
+
+__device__ __forceinline__ double u128_to_f64(u128 x) {
+  return (double)(uint64_t)(x >> 64) * 0x1p64 + (double)(uint64_t)x;
+}
 
 // The sampling rows of sequence b at position acc (the first rejection, or K: bonus), with
 // row maxima Mp, Mq and totals Zp, Zq, positioned at the CHK chunk c.
@@ -562,6 +567,8 @@ __device__ __forceinline__ SampleRow<TT> sample_row(const RejArgs& a, int b, int
     s.mq = 0.f;
     s.gq = 0;
   }
+  s.gpd = u128_to_f64(s.gp);
+  s.gqd = u128_to_f64(s.gq);
   return s;
 }
 
@@ -573,6 +580,18 @@ __device__ __forceinline__ u192 weight_of(const SampleRow<TT>& s, float pv, floa
   const uint32_t eq = expfix(scaled(qv, inv_temp) - s.mq);
   const u192 x = mul128x32(s.gp, ep), y = mul128x32(s.gq, eq);
   return gt192(x, y) ? sub192(x, y) : u192{0, 0, 0};
+}
+
+// Whether an entry after a rejection has residual weight, gp E^p > gq E^q, decided exactly.
+// Each fp64 product is within a relative 2^-50 of the exact one, so a margin of 2^-40 settles
+// every pair that is not nearly tied; the rest compare the exact 160-bit products.
+template <typename TT>
+__device__ __forceinline__ bool residual_positive(const SampleRow<TT>& s, uint32_t ep,
+                                                  uint32_t eq) {
+  const double x = s.gpd * (double)ep, y = s.gqd * (double)eq;
+  if (x > y * (1.0 + 0x1p-40)) return true;
+  if (y > x * (1.0 + 0x1p-40)) return false;
+  return gt192(mul128x32(s.gp, ep), mul128x32(s.gq, eq));
 }
 
 // This thread's PER_M consecutive sampling-row entries starting at v0 (p, and q after a
@@ -624,6 +643,35 @@ __device__ __forceinline__ RunVals load_run(const RejArgs& a, const SampleRow<TT
     }
   }
   return r;
+}
+
+// Sampling weight of the run's entries below V, exactly: after a rejection the sum of
+// gp E^p - gq E^q over the entries with positive residual equals gp (sum of their E^p) -
+// gq (sum of their E^q), so each entry costs its two exponentials, an fp64 membership test
+// and two 64-bit adds, and the 192-bit products are formed once per run. The bonus row's
+// weights E^p F^p sum to F^p (sum of E^p).
+template <typename TT>
+__device__ __forceinline__ u192 run_mass(const SampleRow<TT>& s, const RunVals& r, int v0, int V,
+                                         float inv_temp) {
+  uint64_t sp = 0, sq = 0;
+  if (s.q == nullptr) {
+#pragma unroll
+    for (int j = 0; j < PER_M; ++j)
+      if (v0 + j < V) sp += expfix(scaled(r.p[j], inv_temp) - s.mp);
+    return mul64x128(sp, (u128)s.fp);
+  }
+#pragma unroll
+  for (int j = 0; j < PER_M; ++j) {
+    if (v0 + j < V) {
+      const uint32_t ep = expfix(scaled(r.p[j], inv_temp) - s.mp);
+      const uint32_t eq = expfix(scaled(r.q[j], inv_temp) - s.mq);
+      if (residual_positive(s, ep, eq)) {
+        sp += ep;
+        sq += eq;
+      }
+    }
+  }
+  return sub192(mul64x128(sp, s.gp), mul64x128(sq, s.gq));
 }
 
 // ---- 192-bit wave and block sums and scans -----------------------------------------------
@@ -755,12 +803,7 @@ __global__ __launch_bounds__(THREADS) void rej_mass_kernel(RejArgs a) {
                                          a.dec_z[2 * b], a.dec_z[2 * b + 1], (c * MCHK) / CHK);
   const int v0 = c * MCHK + (int)threadIdx.x * PER_M;
   u192 m{0, 0, 0};
-  if (v0 < a.V) {
-    const RunVals r = load_run(a, s, v0);
-#pragma unroll
-    for (int j = 0; j < PER_M; ++j)
-      if (v0 + j < a.V) m = add192(m, weight_of(s, r.p[j], r.q[j], a.inv_temp));
-  }
+  if (v0 < a.V) m = run_mass(s, load_run(a, s, v0), v0, a.V, a.inv_temp);
   __shared__ u192 sh[THREADS / 64];
   m = block_sum_u192(m, sh);
   if (threadIdx.x == 0) a.cmass[(size_t)b * a.nchm + c] = m;
@@ -858,9 +901,7 @@ __global__ __launch_bounds__(THREADS) void rej_pick_kernel(RejArgs a) {
   u192 run{0, 0, 0};
   if (v0 < a.V) {
     rv = load_run(a, s, v0);
-#pragma unroll
-    for (int j = 0; j < PER_M; ++j)
-      if (v0 + j < a.V) run = add192(run, weight_of(s, rv.p[j], rv.q[j], a.inv_temp));
+    run = run_mass(s, rv, v0, a.V, a.inv_temp);
   }
   const u192 incl = wave_incl_scan_u192(run);
   if (lane == 63) s_wtot[w] = incl;

@@ -98,6 +98,31 @@ def test_rejection_equal_distributions_always_accept(ops):
     assert np.array_equal(out[:, :5], ids.numpy())
 
 
+@pytest.mark.parametrize("V", [1000, 151936])
+def test_rejection_residual_with_exact_ties(ops, V):
+    """Drafts equal to their target rows but for two swapped entries a and c (target 5 at a
+    and 1 at c, the draft the reverse), the draft token at c and u near 1: the first draft
+    is rejected, and the residual's weights tie exactly (p_v Zq = q_v Zp) at every entry but
+    a and c, so the residual has all its mass at a. Entries that are -inf in both rows tie
+    at zero. Every tie must be decided exactly, as the oracle decides it."""
+    B, K = 3, 2
+    g = torch.Generator().manual_seed(77)
+    target = torch.randn(B, K + 1, V, generator=g)
+    target[:, :, 10:40] = float("-inf")
+    draft = target[:, :K].clone()
+    a, c = V // 2 + 3, V // 3 + 1
+    target[:, 0, a], target[:, 0, c] = 5.0, 1.0
+    draft[:, 0, a], draft[:, 0, c] = 1.0, 5.0
+    ids = torch.full((B, K), c, dtype=torch.int64)
+    u = torch.full((B, K), 0.999)
+    us = torch.rand(B, generator=g)
+    acc, out = _rejection(ops, target, draft, ids, u, us)
+    racc, rout = oa.accept_rejection(target.numpy(), draft.numpy(), ids.numpy(), u.numpy(),
+                                     us.numpy())
+    assert (acc == 0).all() and (out[:, 0] == a).all()
+    assert np.array_equal(acc, racc) and np.array_equal(out, rout)
+
+
 @pytest.mark.parametrize("B,K,V,seed,inv_t", [(3, 2, 151936, 4, 1.0), (2, 3, 20001, 5, 0.7)])
 def test_rejection_row_sums_bit_exact(ops, B, K, V, seed, inv_t):
     from npn_native import call, query, stream_of

@@ -543,6 +543,8 @@ struct MergeArgs {
   int T, Hq, Hkv, R, npairs;
 };
 
+constexpr int kMergeRowsMinPairs = 64;  // pairs from which gqa_merge_rows_kernel merges
+
 __global__ __launch_bounds__(256) void gqa_merge_kernel(MergeArgs a) {
   const int r = blockIdx.x;
   const int pr = blockIdx.y;
@@ -646,6 +648,93 @@ __global__ __launch_bounds__(256) void gqa_merge_kernel(MergeArgs a) {
     const float g1 = npn::sigmoid(npn::bf16_to_f32((uint16_t)(gw[j] >> 16)));
     w[j] = npn::f32_to_bf16(ot[2 * j] * inv * g0) |
            ((uint32_t)npn::f32_to_bf16(ot[2 * j + 1] * inv * g1) << 16);
+  }
+  *reinterpret_cast<uint2*>(a.out + oi) = make_uint2(w[0], w[1]);
+}
+
+// The same merge with one wave per query row (four rows per block) walking all of the pair's
+// segments itself: for batches whose pairs have a few segments each (the host picks it when
+// there are at least 64 pairs, about 8 segments per pair or fewer), a quarter as many blocks
+// and no LDS exchange. Segments are loaded four at a time; the first four stay in registers
+// for both the max pass and the sum pass.
+__global__ __launch_bounds__(256) void gqa_merge_rows_kernel(MergeArgs a) {
+  const int q = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int grp = a.Hq / a.Hkv;
+  const int r = blockIdx.x * 4 + q;  // query row of the pair, t * grp + head; a.R >= T * grp
+  if (r >= a.T * grp) return;        // wave-uniform; the kernel has no block barrier
+  const int pr = blockIdx.y;
+  const int b = pr / a.Hkv, g = pr - b * a.Hkv;
+  const int S = a.pstart[a.npairs];
+  const int64_t W = attn_wgs(S);
+  const int x0 = a.pstart[pr], x1 = a.pstart[pr + 1] - 1;
+  const int w0 = (int)(((int64_t)(x0 + 1) * W - 1) / S);
+  const int w1 = (int)(((int64_t)(x1 + 1) * W - 1) / S);
+  const size_t stride_ml = (size_t)a.R * 2, stride_o = (size_t)a.R * DH;
+  const float* pml = a.part_ml + ((size_t)(w0 + pr) * a.R + r) * 2;
+  const float* po = a.part_o + ((size_t)(w0 + pr) * a.R + r) * DH + 4 * lane;
+  auto live = [&](int w) { return w <= w1 && wg_first_step(w, S) < wg_first_step(w + 1, S); };
+  const int t = r / grp, qh = g * grp + (r - t * grp);
+  const size_t oi = (((size_t)b * a.T + t) * a.Hq + qh) * DH + 4 * lane;
+  const uint2 gate_bits = *reinterpret_cast<const uint2*>(a.gate + oi);
+  float mv0[4], lv0[4];
+  f32x4 ov0[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int w = w0 + j;
+    const bool ok = live(w);
+    mv0[j] = ok ? pml[(w - w0) * stride_ml] : kNegBig;
+    lv0[j] = ok ? pml[(w - w0) * stride_ml + 1] : 0.f;
+    ov0[j] = ok ? *reinterpret_cast<const f32x4*>(po + (w - w0) * stride_o)
+                : f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  float M = kNegBig;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) M = fmaxf(M, mv0[j]);
+  for (int base = w0 + 4; base <= w1; base += 4) {
+    float mv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int w = base + j;
+      mv[j] = live(w) ? pml[(w - w0) * stride_ml] : kNegBig;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) M = fmaxf(M, mv[j]);
+  }
+  float l = 0.f;
+  f32x4 o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float f = exp2f(mv0[j] - M);
+    l += f * lv0[j];
+    o += f * ov0[j];
+  }
+  for (int base = w0 + 4; base <= w1; base += 4) {
+    float mv[4], lv[4];
+    f32x4 ov[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int w = base + j;
+      const bool ok = live(w);
+      mv[j] = ok ? pml[(w - w0) * stride_ml] : kNegBig;
+      lv[j] = ok ? pml[(w - w0) * stride_ml + 1] : 0.f;
+      ov[j] = ok ? *reinterpret_cast<const f32x4*>(po + (w - w0) * stride_o)
+                 : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float f = exp2f(mv[j] - M);
+      l += f * lv[j];
+      o += f * ov[j];
+    }
+  }
+  const float inv = 1.0f / l;
+  const uint32_t gw[2] = {gate_bits.x, gate_bits.y};
+  uint32_t w[2];
+  for (int j = 0; j < 2; ++j) {
+    const float g0 = npn::sigmoid(npn::bf16_to_f32((uint16_t)(gw[j] & 0xFFFFu)));
+    const float g1 = npn::sigmoid(npn::bf16_to_f32((uint16_t)(gw[j] >> 16)));
+    w[j] = npn::f32_to_bf16(o[2 * j] * inv * g0) |
+           ((uint32_t)npn::f32_to_bf16(o[2 * j + 1] * inv * g1) << 16);
   }
   *reinterpret_cast<uint2*>(a.out + oi) = make_uint2(w[0], w[1]);
 }
@@ -818,7 +907,11 @@ static int tail_verify_launch(const uint16_t* query, const uint16_t* gate, const
   else hipLaunchKernelGGL((gqa_attn_kernel<3, 2>), grid, dim3(192), 0, s, aa);
 
   MergeArgs ma{po, pml, pstart, gate, out, T, q_heads, kv_heads, p.R, p.P};
-  hipLaunchKernelGGL(gqa_merge_kernel, dim3(T * p.grp, p.P), dim3(256), 0, s, ma);
+  if (p.P >= kMergeRowsMinPairs)
+    hipLaunchKernelGGL(gqa_merge_rows_kernel, dim3((T * p.grp + 3) / 4, p.P), dim3(256), 0, s,
+                       ma);
+  else
+    hipLaunchKernelGGL(gqa_merge_kernel, dim3(T * p.grp, p.P), dim3(256), 0, s, ma);
   return npn_launch_status();
 }
 

@@ -75,6 +75,17 @@ def test_tail_verify_many_short_ragged_pairs(ops):
     assert_rel_close(_run_verify(ops, d), _oracle_verify(d), out_unit=BF16_U, name="ragged")
 
 
+def test_tail_verify_many_pairs_padded_rows_and_one_long_pair(ops):
+    """80 pairs (the per-row merge), 30 query rows per pair in a 32-row tile, and one pair
+    with a 4000-row cache among short ones, so that most attention workgroups work on that
+    pair and its merge walks hundreds of segments."""
+    B = 40
+    kv = np.random.default_rng(43).integers(0, 60, size=B)
+    kv[7] = 4000
+    d = gqa_verify_inputs(B, 5, 12, 2, kv.tolist(), 4096, seed=43)
+    assert_rel_close(_run_verify(ops, d), _oracle_verify(d), out_unit=BF16_U, name="padded")
+
+
 def test_tail_verify_full_width_long(ops):
     """Config-2-like: 24/4 heads, T=8, KV lengths 4096..8192 (oracle-affordable)."""
     d = gqa_verify_inputs(2, 8, 24, 4, [4096, 8000], 8200, seed=2)

@@ -3,7 +3,7 @@
 TEST INFRASTRUCTURE ONLY. Nothing in the product path (the HIP library, the
 host ops under ``neuron-pytorch-native_amd/``) may import, call or link
 anything in this package. Only ``tests/``, ``__graft_entry__.smoke()`` and the
-``cpu_baseline`` leg of ``bench.py`` use it, and only as the checker.
+``cpu_baseline`` leg of ``bench.py`` use it, and only to check or time against it.
 
 Every function restates the reference's algorithm in numpy (float64 unless a
 function says otherwise) and cites the reference file:line it follows.

@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Writes tests/golden/deltanet_chunked_hf.npz: chunked gated-DeltaNet prefill vectors
 computed with HF transformers' torch_chunk_gated_delta_rule (third-party; transformers
-5.15.0 in the build container, qwen3_next.modeling_qwen3_next), used to pin
+5.15.0, qwen3_next.modeling_qwen3_next), used to pin
 oracle/deltanet_chunked.py.
 
 Inputs per case (op layouts, head-major rows h*S + t): raw q, k [Hv*S, 128], v [Hv*S, 128],
@@ -9,7 +9,7 @@ g, beta [Hv*S, 1] with the model's gates g = -exp(A_log) * softplus(a + dt),
 beta = sigmoid(b) (contrib/qwen3.6-27b/static_decode.py:628-629), initial state
 [Hv*128, 128]. HF is run with use_qk_l2norm_in_kernel=True (its l2norm is
 x * rsqrt(sum x^2 + 1e-6), as the reference kernel normalises) in float32.
-Run here only (the GPU box does not need it):
+Needs transformers; the tests read only the .npz it writes:
     python tests/golden/make_deltanet_chunked_fixture.py
 """
 import os

@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Writes tests/golden/deltanet_hf.npz: multi-token gated-DeltaNet vectors computed with
-HF transformers' Qwen3.5 reference functions (third-party; transformers 5.15.0 in the
-build container), used to pin oracle/deltanet.py.
+HF transformers' Qwen3.5 reference functions (third-party; transformers 5.15.0), used
+to pin oracle/deltanet.py.
 
   conv      transformers ... qwen3_5.modeling_qwen3_5.causal_conv1d_update (activation silu)
   recurrence torch_recurrent_gated_delta_rule(use_qk_l2norm_in_kernel=True), run on every
@@ -9,8 +9,8 @@ build container), used to pin oracle/deltanet.py.
   output    Qwen3_5RMSNormGated on fp32 inputs (weight * rmsnorm(o) * silu(z))
 
 Gates follow the reference kernel: g = -exp(A_log) * softplus(a + dt_bias), beta = sigmoid(b)
-(contrib/qwen3.6-27b/kernels/deltanet_full.py:174-212). Run here only (the GPU box does not
-need it): python tests/golden/make_deltanet_fixture.py
+(contrib/qwen3.6-27b/kernels/deltanet_full.py:174-212). Needs transformers; the tests
+read only the .npz it writes: python tests/golden/make_deltanet_fixture.py
 """
 import os
 

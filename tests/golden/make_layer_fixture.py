@@ -1,6 +1,6 @@
 #!/usr/bin/env python3
 """Writes tests/golden/layers_hf.npz: T-token verify vectors of whole decoder layers computed
-with HF transformers' Qwen3.5 modules (third-party; transformers 5.15.0 in the build container:
+with HF transformers' Qwen3.5 modules (third-party; transformers 5.15.0:
 Qwen3_5DecoderLayer with Qwen3_5GatedDeltaNet / Qwen3_5Attention / Qwen3_5MLP / Qwen3_5RMSNorm,
 and their DynamicCache), used to pin the layer composition of oracle/verify_step.py.
 
@@ -36,7 +36,8 @@ Each case runs twice:
     records each mixer's output, the MLP's input and output per layer, the states and the
     appended rows.
 
-Run here only (the GPU box does not need it): python tests/golden/make_layer_fixture.py
+Needs transformers; the tests read only the .npz it writes:
+    python tests/golden/make_layer_fixture.py
 """
 import os
 

@@ -858,9 +858,12 @@ __global__ __launch_bounds__(THREADS) void rej_pick_kernel(RejArgs a) {
       }
       carry = shfl_u192(incl, 63);
     }
+    // (selected limb by limb: a select of whole structs went through private memory)
+    const u192 bsel{found ? before.w0 : carry.w0, found ? before.w1 : carry.w1,
+                    found ? before.w2 : carry.w2};
     if (lane == 0) {
       s_chunk = chunk;
-      s_before = found ? before : carry;
+      s_before = bsel;
       s_target = target;
       s_tok = 0x7FFFFFFF;
     }

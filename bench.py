@@ -296,6 +296,21 @@ def cpu_model():
     return None
 
 
+def cpu_share():
+    """(threads, affinity cores, cgroup CPU quota or None): the cores this process may run
+    on (os.sched_getaffinity), capped by the cgroup v2 quota in /sys/fs/cgroup/cpu.max."""
+    affinity = len(os.sched_getaffinity(0))
+    quota = None
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            q, period = f.read().split()[:2]
+        if q != "max":
+            quota = max(1, int(int(q) // int(period)))
+    except (OSError, ValueError):
+        pass
+    return (min(affinity, quota) if quota else affinity), affinity, quota
+
+
 def cpu_baseline(model, snap, kv_start, x, inputs, first, budget_s=20.0):
     """The batched torch CPU float32 step (oracle/torch_step.py) on the whole workload (all B
     sequences, the same weights, initial state, inputs and logits as the first GPU step),
@@ -305,6 +320,10 @@ def cpu_baseline(model, snap, kv_start, x, inputs, first, budget_s=20.0):
     import torch
     from oracle import torch_step as ts
     from spec_verify_step import rope_tables
+    # one thread per core this process may run on: its CPU affinity, capped by a cgroup CPU
+    # quota where one is set (a container's share of a larger host)
+    threads, affinity, quota = cpu_share()
+    torch.set_num_threads(threads)
     ws = host_weights(model, ts.decode_fp8)
     xc = x.cpu().float()
     tgt, drf, ids, u, us = (t.cpu() for t in inputs)
@@ -333,9 +352,9 @@ def cpu_baseline(model, snap, kv_start, x, inputs, first, budget_s=20.0):
     per_step = sum(times) / len(times)
     tokens = int((acc.long() + 1).sum())
     same = int(((acc == first["accepted"]) & (out_ids == first["out_ids"]).all(1)).sum())
-    threads = torch.get_num_threads()
     return {"value": round(tokens / per_step, 2), "unit": "tokens/s", "cores": threads,
             "kind": "port", "cpu": cpu_model(), "threads": threads,
+            "affinity_cores": affinity, "cgroup_cpu_quota": quota,
             "sample": f"the whole first step (all {B} sequences, {tokens} committed tokens) from "
                       f"the same initial state and inputs, {len(times)} run(s), "
                       f"{per_step:.2f} s per step; oracle/torch_step.py, batched torch float32 "

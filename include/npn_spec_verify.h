@@ -262,6 +262,13 @@ int npn_fp8_matmul_rowmax(const uint16_t* x, const int8_t* w, const float* scale
 /* Split-K factor S of the GEMM plan for these sizes (1: no split; 0: unsupported sizes). */
 int npn_fp8_matmul_split_k(int M, int K, int N);
 
+/* The GEMM plan for these sizes, host-only (no device work), for tests and tuning -- no
+ * reference counterpart. info[4] receives: kind (0 narrow kernel on a tiles x split grid,
+ * 1 narrow kernel in stream-K, 2 wide kernel), the split-K factor (stream-K: partial slots),
+ * the tile parameter (narrow: 16-row blocks per tile; wide: 16-column tiles per wave) and
+ * the workgroups launched. NPN_ERR_SHAPE for unsupported sizes. */
+int npn_fp8_matmul_plan(int M, int K, int N, int* info);
+
 /* torch.ops.fp8.matmul_partials -- new op, no reference counterpart: the GEMM of
  * npn_fp8_matmul without its reduction and scaling, for consumers that fuse them.
  *   partial [S][M][N] f32, S = npn_fp8_matmul_split_k(M, K, N): the unscaled products of x
@@ -275,6 +282,11 @@ int npn_fp8_matmul_partials(const uint16_t* x, const int8_t* w, float* partial, 
  * Acceptance. T = K+1 verify positions per sequence, vocabulary V.
  * Outputs: accepted [B] int32 in [0, K]; out_ids [B, T] int64: accepted drafts,
  * then the correction/bonus token, then -1.
+ * Draft ids outside [0, V) are never accepted, by every acceptance call: greedy compares
+ * them with an argmax, which is always in range, and rejection sampling counts such a
+ * position as a rejection whatever its uniform and samples its token from the residual as
+ * for any rejection. So every emitted id lies in [0, V), and no logit is read at an
+ * out-of-range id (the device code makes no host round trip to check them).
  * ------------------------------------------------------------------------- */
 
 /* Workspace bytes for the acceptance calls. */
@@ -301,8 +313,10 @@ int npn_accept_greedy(const float* target_logits, const int64_t* draft_ids, int3
  *   sample from R_v = max(0, Wp_v*Zq - Wq_v*Zp) (bonus: R_v = Wp_v of row K):
  *   the smallest v with 2^24 * sum_{w<=v} R_w > U_s * sum_w R_w (exact to 2^192).
  *   A row with no finite entry relative to its maximum (all NaN or -inf, or a +inf
- *   entry) has Z = 0 and passes the accept test; if the bonus row has no mass the
- *   token is its argmax (NaN counts as the maximum, ties go to the lowest index).
+ *   entry) has Z = 0 and passes the accept test; if the sampling row has no mass (a
+ *   bonus row, or the residual after an out-of-range draft id where Wp*Zq == Wq*Zp
+ *   everywhere) the token is the target row's argmax (NaN counts as the maximum, ties
+ *   go to the lowest index).
  *   target_logits [B, K+1, V] f32, draft_logits [B, K, V] f32, draft_ids [B, K]
  *   int64, u_accept [B, K] f32 in [0,1), u_sample [B] f32 in [0,1),
  *   inv_temperature > 0 (logits are multiplied by it), V <= 2^20.
@@ -331,7 +345,9 @@ int npn_accept_rejection(const float* target_logits, const float* draft_logits,
  * uses that GPU's one array, so calls that overlap on one GPU (concurrent streams, or
  * threads) race and must be serialised by the caller; each call writes every scratch word it
  * reads, so nothing needs clearing between calls. The stream's device (the current device
- * for the null stream) selects the array. Results are bit-identical to
+ * for the null stream) selects the array. The first call on a device looks the array's
+ * address up (hipGetSymbolAddress); make it outside stream capture, after which a call only
+ * enqueues kernels and may be captured in a HIP graph. Results are bit-identical to
  * npn_accept_rejection; the scratch is not readable through this interface. */
 int npn_accept_rejection_noalloc(const float* target_logits, const float* draft_logits,
                                  const int64_t* draft_ids, const float* u_accept,
@@ -455,7 +471,10 @@ int npn_spec_commit(const int32_t* accepted, int32_t* prev_accepted, int32_t* kv
  * and npn_spec_commit. Same results as those calls; 1 launch instead of layers + 1.
  *   mixed_qkv, conv_state: host arrays of `layers` (0..8) device pointers, layer l's
  *   [B, T, QKV] bf16 verify inputs and its [B, QKV, 3] bf16 window (rolled back in place);
- *   accepted [B] int32; prev_accepted, kv_len, committed [B] int32 (each may be NULL). */
+ *   accepted [B] int32; prev_accepted, kv_len, committed [B] int32 (each may be NULL).
+ *   An accepted value outside [0, T-1] is clamped into it, on the device, for every output
+ *   alike (windows, prev_accepted, kv_len, committed), so the conv windows and the KV length
+ *   always count the same tokens; npn_spec_commit alone adds accepted as given. */
 int npn_deltanet_rollback_commit(const uint16_t* const* mixed_qkv, uint16_t* const* conv_state,
                                  int layers, const int32_t* accepted, int32_t* prev_accepted,
                                  int32_t* kv_len, int32_t* committed, int B, int T, int k_heads,

@@ -253,8 +253,10 @@ __global__ void dn_conv_window_kernel(const uint16_t* conv_state,
 
 // The bookkeeping after acceptance in one launch: every DeltaNet layer's conv window rolled
 // back in place (as dn_conv_window_kernel), and, in the last block, the per-sequence commit
-// prev_accepted = accepted, kv_len += accepted + 1, committed += accepted + 1 (null pointers
-// skipped). The two parts touch disjoint memory and only read `accepted`.
+// prev_accepted = a, kv_len += a + 1, committed += a + 1 (null pointers skipped), with
+// a = accepted clamped into [0, T-1] exactly as the conv windows clamp it, so the windows and
+// the KV length always count the same tokens. The two parts touch disjoint memory and only
+// read `accepted`.
 constexpr int kMaxRollbackLayers = 8;
 struct RollbackCommitArgs {
   const uint16_t* mixed[kMaxRollbackLayers];
@@ -271,7 +273,8 @@ struct RollbackCommitArgs {
 __global__ __launch_bounds__(256) void dn_rollback_commit_kernel(RollbackCommitArgs a) {
   if (blockIdx.x == a.conv_blocks) {
     for (int b = threadIdx.x; b < a.B; b += blockDim.x) {
-      const int acc = a.accepted[b];
+      int acc = a.accepted[b];
+      acc = acc < 0 ? 0 : (acc >= a.T ? a.T - 1 : acc);
       if (a.prev_accepted != nullptr) a.prev_accepted[b] = acc;
       if (a.kv_len != nullptr) a.kv_len[b] += acc + 1;
       if (a.committed != nullptr) a.committed[b] += acc + 1;

@@ -1084,6 +1084,24 @@ extern "C" int npn_fp8_matmul_split_k(int M, int K, int N) {
   return plan(M, K, N).split_k;
 }
 
+extern "C" int npn_fp8_matmul_plan(int M, int K, int N, int* info) {
+  NPN_REQUIRE(info != nullptr, NPN_ERR_NULL);
+  NPN_REQUIRE(shape_ok(M, K, N), NPN_ERR_SHAPE);
+  const GemmPlan p = plan(M, K, N);
+  if (p.wide) {
+    info[0] = 2;
+    info[1] = p.split_k;
+    info[2] = p.ntm;
+    info[3] = ((p.groups * p.split_k + 7) / 8) * 8 * p.passes;
+  } else {
+    info[0] = p.sk_wg > 0 ? 1 : 0;
+    info[1] = p.split_k;
+    info[2] = p.mt;
+    info[3] = p.sk_wg > 0 ? p.sk_wg : ((N + NT - 1) / NT) * p.split_k * p.passes;
+  }
+  return NPN_OK;
+}
+
 extern "C" int npn_fp8_matmul_partials(const uint16_t* x, const int8_t* w, float* partial, int M,
                                        int K, int N, void* stream) {
   NPN_REQUIRE(x && w && partial, NPN_ERR_NULL);
@@ -1201,8 +1219,14 @@ extern "C" int npn_deltanet_full_fp8(
   const int qkv = (2 * k_heads + v_heads) * 128, zn = v_heads * 128;
   NPN_REQUIRE(shape_ok(1, hidden, qkv), NPN_ERR_SHAPE);
   NPN_REQUIRE(NPN_ALIGNED16(x) && NPN_ALIGNED16(qkv_w) && NPN_ALIGNED16(z_w), NPN_ERR_ALIGN);
-  // the new conv window is written before the token step reads the old one
-  NPN_REQUIRE(new_conv_state != conv_state, NPN_ERR_VALUE);
+  // the new conv window is written before the token step reads the old one, so the two
+  // [QKV, 3] bf16 spans must not share a byte
+  {
+    const uintptr_t n0 = reinterpret_cast<uintptr_t>(new_conv_state);
+    const uintptr_t c0 = reinterpret_cast<uintptr_t>(conv_state);
+    const uintptr_t span = (uintptr_t)qkv * 3 * sizeof(uint16_t);
+    NPN_REQUIRE(n0 + span <= c0 || c0 + span <= n0, NPN_ERR_VALUE);
+  }
   const FullFp8Layout l = full_fp8_layout(hidden, qkv, v_heads);
   NPN_REQUIRE(workspace != nullptr && workspace_bytes >= l.total, NPN_ERR_WORKSPACE);
   NPN_REQUIRE(NPN_ALIGNED16(workspace), NPN_ERR_ALIGN);

@@ -411,7 +411,12 @@ __device__ __forceinline__ const TT* target_row(const RejArgs& a, int row) {
   return static_cast<const TT*>(a.target) + (size_t)row * a.V;
 }
 
-// Draft token whose E this row reports, or -1 (bonus rows).
+// Whether a draft id names a vocabulary entry. Ids outside [0, V) are never accepted: the
+// position is a rejection whatever the uniform (greedy rejects them too, an argmax being in
+// range), so no emitted id lies outside the vocabulary.
+__device__ __forceinline__ bool draft_id_ok(int64_t x, int V) { return x >= 0 && x < V; }
+
+// Draft token whose E this row reports, or -1 (bonus rows, and out-of-range draft ids).
 __device__ __forceinline__ int row_token(const RejArgs& a, int row) {
   const int nt = a.B * (a.K + 1);
   int b, i;
@@ -423,9 +428,8 @@ __device__ __forceinline__ int row_token(const RejArgs& a, int row) {
     b = (row - nt) / a.K;
     i = (row - nt) - b * a.K;
   }
-  long x = a.draft_ids[(size_t)b * a.K + i];
-  x = x < 0 ? 0 : (x >= a.V ? a.V - 1 : x);
-  return (int)x;
+  const int64_t x = a.draft_ids[(size_t)b * a.K + i];
+  return draft_id_ok(x, a.V) ? (int)x : -1;
 }
 
 // This thread's entries of chunk [v0, v0 + CHK) of a row, in registers, scaled (NaN for
@@ -776,7 +780,7 @@ __global__ __launch_bounds__(1024) void rej_decide_kernel(RejArgs a) {
     const uint32_t U = uniform_fix(a.u_accept[(size_t)b * K + lane]);
     const u192 lhs = mul192x32(mul64x128(s_w[T + lane], s_z[lane]), U);
     const u192 rhs = shl24_192(mul64x128(s_w[lane], s_z[T + lane]));
-    reject = gt192(lhs, rhs);
+    reject = !draft_id_ok(a.draft_ids[(size_t)b * K + lane], a.V) || gt192(lhs, rhs);
   }
   const uint64_t rej = __builtin_amdgcn_ballot_w64(reject);
   const int acc = rej ? __builtin_ctzll(rej) : K;

@@ -41,6 +41,7 @@ SIGNATURES = {
     "npn_deltanet_split": (_I, [_P, _I] + [_P] * 4 + [_I] * 4 + [_P]),
     "npn_gqa_split": (_I, [_P, _I] + [_P] * 4 + [_I] * 4 + [_P]),
     "npn_fp8_matmul_split_k": (_I, [_I] * 3),
+    "npn_fp8_matmul_plan": (_I, [_I] * 3 + [_P]),
     "npn_fp8_matmul_partials": (_I, [_P] * 3 + [_I] * 3 + [_P]),
     "npn_residual_rmsnorm_partials": (_I, [_P, _P, _I] + [_P] * 4 + [_I, _I, _F, _P]),
     "npn_residual_add_partials": (_I, [_P, _P, _I, _P, _P, _I, _I, _P]),

@@ -40,12 +40,17 @@ referred to the chunk's own maximum, and chunks to the row maximum by exact fact
 - At the first rejection sample from R_v = max(0, W^p_v Z_q - W^q_v Z_p); if all
   K drafts are accepted sample the bonus from R_v = W^p_v of row K. The token is
   the smallest v with 2^24 * sum_{w<=v} R_w > U_s * sum_w R_w (integers below 2^184).
+- Draft ids outside [0, V) are never accepted: such a position is a rejection whatever the
+  uniform, and its token is sampled from the residual R as for any rejection (greedy
+  acceptance rejects them too, since an argmax is always in range). Emitted ids therefore
+  always lie in [0, V).
 - Rows without mass: Z = 0 when no entry is finite relative to the maximum (all NaN or
   -inf, or a +inf entry). Such a target or draft row passes the accept test (both sides
-  are 0). A residual after a rejection always has mass (sum_v (W^p_v Z_q - W^q_v Z_p) = 0
-  with a negative term at the rejected token), so only a bonus row can be empty; its token
-  is then the greedy one, argmax of the target row (NaN counts as the maximum, first index
-  on ties).
+  are 0). A residual after a test that failed always has mass (sum_v (W^p_v Z_q - W^q_v Z_p)
+  = 0 with a negative term at the rejected token), so only a bonus row, or the residual
+  after an out-of-range draft id when W^p Z_q == W^q Z_p everywhere, can be empty; the
+  token is then the greedy one, argmax of the target row (NaN counts as the maximum, first
+  index on ties).
 """
 import numpy as np
 
@@ -173,6 +178,9 @@ def accept_rejection(target, draft, draft_ids, u_accept, u_sample, inv_temp=1.0)
             Ep, Zp, _ = row_weights(target[b, i], inv_temp)
             Eq, Zq, _ = row_weights(draft[b, i], inv_temp)
             x = int(draft_ids[b, i])
+            if x < 0 or x >= V:                  # out-of-range draft id: a rejection
+                a = i
+                break
             U = uniform_fix(u_accept[b, i])
             if U * int(Eq[x]) * Zp > (int(Ep[x]) * Zq << U_BITS):
                 a = i

@@ -182,3 +182,31 @@ def test_rejection_empty_bonus_rows(ops, V):
     assert np.array_equal(acc, racc) and np.array_equal(out, rout)
     assert out[0, K] == 0 and out[1, K] == 0 and out[2, K] == V // 3 and out[4, K] == V - 1
     assert ((out[:, K] >= 0) & (out[:, K] < V)).all()
+
+
+@pytest.mark.parametrize("V", [40, 151936])
+def test_out_of_range_draft_ids(ops, V):
+    """Draft ids -1, V and -2^40 are never accepted: rejection sampling counts the position
+    as a rejection whatever the uniform and samples it from the residual (here p == q for
+    some sequences, an empty residual, so the target row's argmax), greedy rejects them, and
+    every emitted id lies in [0, V) -- bit-exact against the oracle."""
+    B, K = 6, 3
+    g = torch.Generator().manual_seed(41)
+    target = torch.randn(B, K + 1, V, generator=g)
+    draft = target[:, :K].clone()
+    draft[3:] = 0.8 * target[3:, :K] + 0.6 * torch.randn(3, K, V, generator=g)
+    ids = torch.randint(0, V, (B, K), generator=g)
+    ids[0, 0], ids[1, 1], ids[2, 2] = -1, V, -(1 << 40)
+    ids[3, 0], ids[4, 2], ids[5, 1] = V, -1, V + 7
+    u = torch.zeros(B, K)
+    us = torch.rand(B, generator=g)
+    acc, out = _rejection(ops, target, draft, ids, u, us)
+    racc, rout = oa.accept_rejection(target.numpy(), draft.numpy(), ids.numpy(), u.numpy(),
+                                     us.numpy())
+    assert acc.tolist()[:3] == [0, 1, 2]
+    assert np.array_equal(acc, racc) and np.array_equal(out, rout)
+    assert ((out >= -1) & (out < V)).all()
+    gacc, gout = _greedy(ops, target, ids)
+    racc, rout = oa.accept_greedy(target.numpy(), ids.numpy())
+    assert np.array_equal(gacc, racc) and np.array_equal(gout, rout)
+    assert ((gout >= -1) & (gout < V)).all()

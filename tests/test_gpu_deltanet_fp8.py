@@ -104,6 +104,18 @@ def test_full_fp8_rejects_bad_arguments(ops):
     with pytest.raises(RuntimeError, match="status 6"):
         call("npn_deltanet_full_fp8", *args, ns, args[2], out, HIDDEN, 4, 12,
              ws, n_ws, stream_of(ws))
+    # a partial overlap (the new window one row, 6 bytes, past the old one's start; and one
+    # ending a row into it) is refused the same way
+    qkv = args[2].shape[0]
+    pad = torch.zeros(qkv + 2, 3, dtype=torch.bfloat16, device="cuda")
+    pad[1:qkv + 1] = args[2]
+    args_pad = list(args)
+    args_pad[2] = pad[1:qkv + 1]
+    for alias in (pad[2:qkv + 2], pad[0:qkv]):
+        with pytest.raises(RuntimeError, match="status 6"):
+            call("npn_deltanet_full_fp8", *args_pad, ns, alias, out, HIDDEN, 4, 12,
+                 ws, n_ws, stream_of(ws))
+    assert torch.equal(pad[1:qkv + 1], args[2])
     with pytest.raises(RuntimeError, match="status 4"):
         call("npn_deltanet_full_fp8", *args, ns, cs, out, HIDDEN, 4, 12, ws, n_ws - 256,
              stream_of(ws))

@@ -63,6 +63,51 @@ def test_split_16(ops, M, K, N):
     _check(ops, M, K, N, seed=K + N)
 
 
+# The nine (M, N) shapes of the FP8 projection workload at K = 5120, each with the plan it
+# runs: (kind, split-K or stream-K slots, tile parameter, workgroups); kind 0 = narrow
+# kernel on a tiles x split grid, 1 = narrow kernel in stream-K, 2 = wide kernel.
+CONFIG3_PLANS = {
+    (8, 5120): (0, 16, 1, 320),
+    (8, 17408): (1, 7, 1, 476),
+    (8, 34816): (1, 5, 1, 512),
+    (64, 5120): (0, 8, 4, 160),
+    (64, 17408): (1, 7, 4, 476),
+    (64, 34816): (1, 5, 4, 512),
+    (256, 5120): (2, 4, 3, 216),
+    (256, 17408): (2, 2, 5, 224),
+    (256, 34816): (2, 1, 5, 224),
+}
+
+
+def _plan(M, K, N):
+    import ctypes
+    import npn_native
+    info = (ctypes.c_int * 4)()
+    assert npn_native.lib().npn_fp8_matmul_plan(M, K, N, info) == 0
+    return tuple(info)
+
+
+@pytest.mark.parametrize("M,N", sorted(CONFIG3_PLANS))
+def test_config3_every_column(ops, M, N):
+    """Every (M, N) of the projection workload at K = 5120, every column against the oracle
+    (so every 256-column tile, stream-K slot boundary and wide column group is covered), with
+    the plan each shape runs asserted first."""
+    K = 5120
+    assert _plan(M, K, N) == CONFIG3_PLANS[(M, N)]
+    g = torch.Generator().manual_seed(M * 7 + N)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    w, scale = fp8_weights(N, K, seed=N + 1)
+    got = ops.fp8.matmul(x.cuda(), w.cuda(), scale.reshape(N, 1).cuda())
+    torch.cuda.synchronize()
+    got = got.float().cpu().double().numpy()
+    wn, sn, xb = w.numpy(), scale.numpy(), bits(x)
+    for c0 in range(0, N, 8192):  # column blocks keep the fp64 weights near 300 MB
+        c1 = min(N, c0 + 8192)
+        ref = of.fp8_matmul(xb, wn[:, c0:c1], sn[c0:c1])
+        assert_rel_close(got[:, c0:c1], round_to_bf16(ref), out_unit=BF16_U,
+                         name=f"fp8 M={M} K={K} N={N} cols {c0}:{c1}")
+
+
 @pytest.mark.parametrize("M,N", [(8, 5120), (64, 17408), (256, 34816)])
 def test_verify_shapes_sampled(ops, M, N):
     rng = np.random.default_rng(M)

@@ -53,7 +53,8 @@ def test_commit(ops):
 def test_rollback_commit_equals_separate_ops(ops, layers):
     """deltanet::rollback_commit_ (every layer's conv window in place + the commit, one
     launch) against conv_rollback_ per layer and commit_, bit for bit, with accepted values
-    out of range on both sides (clamped for the windows, added as given by the commit)."""
+    out of range on both sides: clamped into [0, T-1] for the windows and for the commit
+    alike (commit_ alone adds its input as given, so it gets the clamped values)."""
     B, T, QKV = 5, 8, 10240
     g = torch.Generator(device="cuda").manual_seed(7 + layers)
     mixed = [torch.randn(B * T * QKV, generator=g, device="cuda").to(torch.bfloat16)
@@ -67,7 +68,7 @@ def test_rollback_commit_equals_separate_ops(ops, layers):
     ref_state = [s.clone() for s in state]
     for m, c in zip(mixed, ref_conv):
         ops.deltanet.conv_rollback_(m, c, acc, 48)
-    ops.spec.commit_(acc, *ref_state)
+    ops.spec.commit_(acc.clamp(0, T - 1), *ref_state)
     ops.deltanet.rollback_commit_(mixed, conv, acc, *state, 48)
     torch.cuda.synchronize()
     for c, r in zip(conv, ref_conv):

@@ -233,6 +233,39 @@ def test_empty_bonus_row_takes_the_greedy_token():
                                         oa.uniform_fix(us[3]))
 
 
+def test_out_of_range_draft_ids_are_rejected():
+    """Draft ids -1 and V are never accepted: rejection sampling stops at them whatever the
+    uniform (u = 0 accepts every valid draft) and samples that position from the residual,
+    greedy rejects them as an argmax is always in range, and no emitted id leaves [0, V)."""
+    B, K, V = 4, 3, 40
+    target, draft, ids, u, us = _all_accepting_inputs(B, K, V, 13)
+    u[:] = 0.0
+    ids[0, 0] = -1
+    ids[1, 1] = V
+    ids[2, 2] = -(1 << 40)
+    acc, out = oa.accept_rejection(target, draft, ids, u, us)
+    assert acc.tolist() == [0, 1, 2, K]
+    assert np.array_equal(out[3, :K], ids[3])
+    assert ((out >= -1) & (out < V)).all()
+    for b in range(3):
+        a = int(acc[b])
+        assert np.array_equal(out[b, :a], ids[b, :a]) and (out[b, a + 1:] == -1).all()
+        # p == q: the residual has no mass, so the token is the target row's argmax
+        assert out[b, a] == oa.argmax_first(target[b, a])
+    # with p != q the residual after an out-of-range id is sampled as after any rejection
+    g = np.random.default_rng(14)
+    draft2 = (0.8 * target[:, :K] + 0.6 * g.standard_normal((B, K, V))).astype(np.float32)
+    acc2, out2 = oa.accept_rejection(target, draft2, np.full((B, K), V), u, us)
+    assert (acc2 == 0).all()
+    for b in range(B):
+        Ep, Zp, _ = oa.row_weights(target[b, 0])
+        Eq, Zq, _ = oa.row_weights(draft2[b, 0])
+        R = [max(0, int(ep) * Zq - int(eq) * Zp) for ep, eq in zip(Ep, Eq)]
+        assert out2[b, 0] == oa._inverse_cdf(R, oa.uniform_fix(us[b]))
+    gacc, gout = oa.accept_greedy(target, np.where(ids < 0, -1, np.minimum(ids, V)))
+    assert gacc[0] == 0 and gacc[1] <= 1 and ((gout >= -1) & (gout < V)).all()
+
+
 def test_empty_rows_pass_the_accept_test():
     """Z = 0 in a target or a draft row makes both sides of the accept test 0."""
     B, K, V = 2, 3, 40

@@ -73,3 +73,36 @@ def test_noalloc_refuses_problems_beyond_the_scratch(ops):
     status = lib().npn_accept_rejection_noalloc(p, p, p, p, p, 1.0, p, p, B, K, V, None)
     assert status == NPN_ERR_SCRATCH
     assert "scratch" in lib().npn_status_string(status).decode()
+
+
+def test_noalloc_under_graph_capture(ops):
+    """The entry point captured in a HIP graph (after one eager call on the device, which
+    looks up the scratch address), replayed on three new input sets copied into the captured
+    buffers with eager work and synchronisations between replays: every replay bit-identical
+    to npn_accept_rejection on the same inputs."""
+    B, K, V, inv_t = 8, 7, 151936, 1.0
+    static = _inputs(B, K, V, 50)
+    _noalloc(B, K, V, static, inv_t)                     # eager first call on this device
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        acc_g = torch.full((B,), -7, dtype=torch.int32, device="cuda")
+        out_g = torch.full((B, K + 1), -7, dtype=torch.int64, device="cuda")
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph, stream=stream):
+        from npn_native import call, stream_of
+        call("npn_accept_rejection_noalloc", *static, inv_t, acc_g, out_g, B, K, V,
+             stream_of(static[0]))
+    for seed in (51, 52, 53):
+        print(f"noalloc graph replay seed={seed}", flush=True)
+        new = _inputs(B, K, V, seed)
+        for dst, src in zip(static, new):
+            dst.copy_(src)
+        acc_w, out_w = _with_workspace(B, K, V, new, inv_t)   # eager work between replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(acc_g, acc_w), seed
+        assert torch.equal(out_g, out_w), seed

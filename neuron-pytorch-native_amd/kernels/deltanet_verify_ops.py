@@ -267,13 +267,16 @@ def _(mixed_qkv, conv_state, accepted, v_heads):
 def deltanet_rollback_commit_(
     mixed_qkvs: list[torch.Tensor],   # per DeltaNet layer: [B*T*QKV_DIM] bf16
     conv_states: list[torch.Tensor],  # per DeltaNet layer: [B*QKV_DIM, 3] bf16, in place
-    accepted: torch.Tensor,           # [B] int32 in [0, T-1]
+    accepted: torch.Tensor,           # [B] int32 in [0, T-1] (clamped into it on the device)
     prev_accepted: torch.Tensor,      # [B] int32, set to accepted
     kv_len: torch.Tensor,             # [B] int32, += accepted + 1
     committed: torch.Tensor,          # [B] int32, += accepted + 1
     v_heads: int,
+    verify_T: int = -1,               # T; -1: from the layers' shapes (required without layers)
 ) -> None:
-    """deltanet::conv_rollback_ over every layer plus spec::commit_, in one launch."""
+    """deltanet::conv_rollback_ over every layer plus spec::commit_, in one launch. accepted is
+    clamped into [0, T-1] for every output alike, so the windows and kv_len count the same
+    tokens."""
     B = accepted.numel()
     if len(mixed_qkvs) != len(conv_states) or len(conv_states) > 8:
         raise RuntimeError("rollback_commit_: one mixed_qkv per conv_state, at most 8 layers")
@@ -289,6 +292,12 @@ def deltanet_rollback_commit_(
         require(conv, "conv_state", torch.bfloat16, shape=(B * qkv, 3))
     if len({(m.numel(), c.shape) for m, c in zip(mixed_qkvs, conv_states)}) > 1:
         raise RuntimeError("rollback_commit_: every layer must have the same shapes")
+    if verify_T != -1:
+        if conv_states and verify_T != T:
+            raise RuntimeError(f"rollback_commit_: verify_T {verify_T} but the layers hold T={T}")
+        T = verify_T
+    elif not conv_states:
+        raise RuntimeError("rollback_commit_: without layers, verify_T must be given")
     n = len(conv_states)
     mp = (ctypes.c_void_p * max(n, 1))(*[m.data_ptr() for m in mixed_qkvs])
     cp = (ctypes.c_void_p * max(n, 1))(*[c.data_ptr() for c in conv_states])
@@ -297,5 +306,5 @@ def deltanet_rollback_commit_(
 
 
 @deltanet_rollback_commit_.register_fake
-def _(mixed_qkvs, conv_states, accepted, prev_accepted, kv_len, committed, v_heads):
+def _(mixed_qkvs, conv_states, accepted, prev_accepted, kv_len, committed, v_heads, verify_T=-1):
     return None

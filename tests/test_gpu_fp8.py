@@ -5,7 +5,7 @@ N in {5120, 17408, 34816}) on sampled columns, the reference's per-rank decode s
 not a multiple of 16, and the OCP-only codes 0x78..0x7E (256..448).
 The oracle's product is rounded to bf16 as the op's output is, so what remains is the
 accumulation order (fp32 MFMA sums vs fp64): the 2e-3 bar, and elementwise one bf16 ulp
-where that order flips a rounding.
+(2^-7 relative at most) where that order flips a rounding.
 """
 import numpy as np
 import pytest
@@ -13,7 +13,7 @@ import torch
 
 from oracle import fp8 as of
 from oracle.numerics import round_to_bf16
-from _util import BF16_U, assert_rel_close, bits, fp8_weights
+from _util import BF16_ULP, assert_rel_close, bits, fp8_weights
 
 pytestmark = pytest.mark.gpu
 
@@ -31,7 +31,7 @@ def _check(ops, M, K, N, seed, cols=None, fp8_max=448.0):
         got = got[:, sel]
     else:
         ref = of.fp8_matmul(bits(x), w.numpy(), scale.numpy())
-    assert_rel_close(got, round_to_bf16(ref), out_unit=BF16_U, name=f"fp8 M={M} K={K} N={N}")
+    assert_rel_close(got, round_to_bf16(ref), out_unit=BF16_ULP, name=f"fp8 M={M} K={K} N={N}")
 
 
 @pytest.mark.parametrize("M", [1, 8, 13, 64, 100, 256])
@@ -101,11 +101,25 @@ def test_config3_every_column(ops, M, N):
     torch.cuda.synchronize()
     got = got.float().cpu().double().numpy()
     wn, sn, xb = w.numpy(), scale.numpy(), bits(x)
+    flips = 0
     for c0 in range(0, N, 8192):  # column blocks keep the fp64 weights near 300 MB
         c1 = min(N, c0 + 8192)
         ref = of.fp8_matmul(xb, wn[:, c0:c1], sn[c0:c1])
-        assert_rel_close(got[:, c0:c1], round_to_bf16(ref), out_unit=BF16_U,
+        rref = round_to_bf16(ref)
+        assert_rel_close(got[:, c0:c1], rref, out_unit=BF16_ULP,
                          name=f"fp8 M={M} K={K} N={N} cols {c0}:{c1}")
+        # where fp32 accumulation and the fp64 sum round differently, they land on adjacent
+        # bf16 values, and only where the exact sum sits near a rounding midpoint (rare);
+        # outputs near zero (cancellation) are left to the absolute bound above
+        diff = got[:, c0:c1] != rref
+        diff &= np.abs(rref) >= 1e-3 * np.abs(rref).max()
+        r32 = rref.astype(np.float32)
+        ulp = np.maximum(np.abs(np.nextafter(r32, np.float32(np.inf)) - rref),
+                         np.abs(np.nextafter(r32, np.float32(-np.inf)) - rref))
+        ulp = ulp * 2.0 ** 16                           # fp32 ulp -> bf16 ulp (16 fewer bits)
+        assert np.all(np.abs(got[:, c0:c1] - rref)[diff] <= ulp[diff] * 1.0001)
+        flips += int(diff.sum())
+    assert flips <= 0.01 * M * N, f"{flips} of {M * N} outputs differ from the rounded oracle"
 
 
 @pytest.mark.parametrize("M,N", [(8, 5120), (64, 17408), (256, 34816)])
@@ -132,7 +146,7 @@ def test_ocp_only_codes(ops):
     scale = torch.full((N,), 1.0 / 448.0)
     got = ops.fp8.matmul(x.cuda(), w.cuda(), scale.reshape(N, 1).cuda()).float().cpu().numpy()
     ref = of.fp8_matmul(bits(x), codes, scale.numpy())
-    assert_rel_close(got, round_to_bf16(ref), out_unit=BF16_U, name="ocp codes")
+    assert_rel_close(got, round_to_bf16(ref), out_unit=BF16_ULP, name="ocp codes")
 
 
 def test_rejects_bad_shapes(ops):

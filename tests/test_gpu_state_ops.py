@@ -69,7 +69,7 @@ def test_rollback_commit_equals_separate_ops(ops, layers):
     for m, c in zip(mixed, ref_conv):
         ops.deltanet.conv_rollback_(m, c, acc, 48)
     ops.spec.commit_(acc.clamp(0, T - 1), *ref_state)
-    ops.deltanet.rollback_commit_(mixed, conv, acc, *state, 48)
+    ops.deltanet.rollback_commit_(mixed, conv, acc, *state, 48, T)
     torch.cuda.synchronize()
     for c, r in zip(conv, ref_conv):
         assert torch.equal(c.view(torch.int16), r.view(torch.int16))

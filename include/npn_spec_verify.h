@@ -304,7 +304,7 @@ int npn_accept_greedy(const float* target_logits, const int64_t* draft_ids, int3
  * al. 2023, Alg. 1) under an integer softmax contract, so the result is
  * bit-identical to a CPU restatement for the same logits and uniforms, and every
  * sum comes from one pass over the logits:
- *   s_v = t_v*inv_temperature (fp32); the vocabulary is cut into chunks of 8192;
+ *   s_v = t_v*inv_temperature (fp32); the vocabulary is cut into chunks of 64;
  *   m_c = max of chunk c's non-NaN s_v, M = max_c m_c; E_v = floor(2^31 *
  *   exp_c(s_v - m_c)), F_c = floor(2^31 * exp_c(m_c - M)) with exp_c a fixed fp32
  *   Cody-Waite + degree-7 Taylor evaluation in fused multiply-adds; the weight of v
@@ -320,9 +320,11 @@ int npn_accept_greedy(const float* target_logits, const int64_t* draft_ids, int3
  *   target_logits [B, K+1, V] f32, draft_logits [B, K, V] f32, draft_ids [B, K]
  *   int64, u_accept [B, K] f32 in [0,1), u_sample [B] f32 in [0,1),
  *   inv_temperature > 0 (logits are multiplied by it), V <= 2^20.
- * Four launches: the one logit pass (per row and chunk: m_c, the sum of E, E at the draft
- * token), the row totals and the decision (one workgroup per sequence), the residual mass
- * per 2048-entry chunk, the inverse CDF.
+ * Three launches: the one pass over the logits (every row's chunk maxima m_c and sums of E),
+ * the row totals (M, Z and the weight of the draft token, one workgroup per row), and the
+ * sampling kernel (one workgroup per 2048 entries of each sequence: the decision, re-derived
+ * by each, and the residual or bonus mass of its entries; the last workgroup of a sequence to
+ * finish runs the inverse CDF and writes the sequence's outputs).
  * On return the workspace starts with every row's Z (unsigned 128-bit, low 64-bit word
  * first [R]) and, at byte offset 16R rounded up to a multiple of 256, every row's max
  * scaled logit M (float [R]); R = B*(2K+1) rows: target row (b, i) at b*(K+1)+i, then
@@ -333,18 +335,19 @@ int npn_accept_rejection(const float* target_logits, const float* draft_logits,
                          int64_t* out_ids, int B, int K, int V, void* workspace,
                          size_t workspace_bytes, void* stream);
 
-/* Bytes of the fixed per-GPU scratch behind npn_accept_rejection_noalloc (4 MiB). */
-#define NPN_ACCEPT_SCRATCH_BYTES (4u << 20)
+/* Bytes of the fixed per-GPU scratch behind npn_accept_rejection_noalloc (16 MiB). */
+#define NPN_ACCEPT_SCRATCH_BYTES (16u << 20)
 
 /* npn_accept_rejection without a workspace argument and without any allocation. No
  * counterpart in the reference: for callers that cannot allocate device memory (code under
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). The workspace
  * is a fixed device array of NPN_ACCEPT_SCRATCH_BYTES per GPU, held from the first call on
  * that GPU until the process ends; problems whose npn_accept_workspace_size(B, K, V) exceeds
- * it return NPN_ERR_SCRATCH (B = 32, K = 7, V = 151936 needs 179 KiB). Every call on a GPU
+ * it return NPN_ERR_SCRATCH (B = 32, K = 7, V = 151936 needs 13.1 MiB). Every call on a GPU
  * uses that GPU's one array, so calls that overlap on one GPU (concurrent streams, or
  * threads) race and must be serialised by the caller; each call writes every scratch word it
- * reads, so nothing needs clearing between calls. The stream's device (the current device
+ * reads before reading it (its counters are cleared by its own kernels), so nothing needs
+ * clearing between calls. The stream's device (the current device
  * for the null stream) selects the array. The first call on a device looks the array's
  * address up (hipGetSymbolAddress); make it outside stream capture, after which a call only
  * enqueues kernels and may be captured in a HIP graph. Results are bit-identical to
@@ -370,12 +373,14 @@ int npn_accept_greedy_parts(const void* parts, int nparts, const int64_t* draft_
 /* torch.ops.spec.accept_rejection_lm_head -- new op: npn_accept_rejection with the target
  * logits produced by the LM head in the same call. hidden [B*(K+1), H] bf16 (the final-normed
  * verify rows, row b*(K+1) + t), lm_head_w [H, V] e4m3fn bytes, lm_head_scale [V] f32:
- * target_logits [B*(K+1), V] bf16 is written (= npn_fp8_matmul's out), and the rejection
- * pass reads the target rows in bf16 (half the bytes of fp32 rows). accepted / out_ids equal
+ * target_logits [B*(K+1), V] bf16 is written (= npn_fp8_matmul's out), and the GEMM's epilogue
+ * also writes the contract's chunk statistics of every target row, so the target rows are
+ * never read back in full: the logit pass covers only the draft rows, and the sampling kernel
+ * re-reads only each sequence's sampling row. accepted / out_ids equal
  * npn_accept_rejection's on the fp32 cast of target_logits, bit for bit, with the same
  * draft logits, ids, uniforms and inv_temperature (> 0). V % 64 == 0, H % 64 == 0, the other
  * rules as npn_accept_rejection. Workspace: npn_accept_rejection_lm_head_workspace_size
- * (0: unsupported sizes). */
+ * (0: unsupported sizes); it starts with the rows' Z and M as npn_accept_rejection's does. */
 size_t npn_accept_rejection_lm_head_workspace_size(int B, int K, int H, int V);
 int npn_accept_rejection_lm_head(const uint16_t* hidden, const int8_t* lm_head_w,
                                  const float* lm_head_scale, const float* draft_logits,

@@ -16,4 +16,4 @@ extern "C" const char* npn_status_string(int status) {
   }
 }
 
-extern "C" int npn_abi_version(void) { return 101; }
+extern "C" int npn_abi_version(void) { return 102; }

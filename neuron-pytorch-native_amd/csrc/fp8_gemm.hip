@@ -13,7 +13,8 @@
 // with v_cvt_scalef32_pk_bf16_fp8 (exact: every e4m3fn value is a bf16 value). Above 64 rows
 // (the wide kernel, MFMA-bound) the B operands are read back transposed (ds_read_b64_tr_b8)
 // and converted the same way; details with each kernel below.
-#include "npn_common.h"
+#include "accept_contract.h"
+#include "npn_internal.h"
 
 namespace {
 
@@ -99,7 +100,18 @@ struct GemmArgs {
   ArgPart* amax;     // row argmax partials [M][column groups] instead of out (split_k == 1)
   float* gmax;       // with out: per-(row, column group) max of the bf16 outputs, NaN ignored
   int sk_wg;         // narrow kernel, > 0: stream-K over this many workgroups (split_k slots)
+  // with out (split_k == 1): the acceptance contract's statistics of each row's 64-column
+  // chunks of the bf16 outputs scaled by inv_temp, [M][N / 64] (cmax == nullptr: none)
+  float* cmax;
+  uint64_t* csum;
+  float inv_temp;
 };
+
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
+  const uint32_t lo = __shfl_xor((uint32_t)v, m, 64);
+  const uint32_t hi = __shfl_xor((uint32_t)(v >> 32), m, 64);
+  return ((uint64_t)hi << 32) | lo;
+}
 
 // ---------------------------------------------------------------------------------------
 // Narrow kernel for M <= 64 rows (HBM-bound: each weight byte feeds 2*M flops).
@@ -354,6 +366,32 @@ __global__ __launch_bounds__(NWV * 64, 1) void fp8_gemm_narrow_kernel(GemmArgs a
         for (int off = 8; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
         if (i == 0 && m < a.M) a.gmax[(size_t)m * groups + grp] = mx;
       }
+      if (a.cmax != nullptr) {
+        // Contract chunk statistics: a 64-column chunk is held by LPC adjacent lanes of the
+        // 16-lane group (N % 64 == 0, so a chunk is wholly inside or wholly past N).
+        constexpr int LPC = 64 / CB;
+        float xs[CB];
+#pragma unroll
+        for (int c = 0; c < CB / 2; ++c) {
+          xs[2 * c] = npn::scaled(npn::bf16lo(pk[c]), a.inv_temp);
+          xs[2 * c + 1] = npn::scaled(npn::bf16hi(pk[c]), a.inv_temp);
+        }
+        float cmx = -__builtin_inff();
+#pragma unroll
+        for (int c = 0; c < CB; ++c) cmx = fmaxf(cmx, xs[c]);
+#pragma unroll
+        for (int off = LPC / 2; off > 0; off >>= 1) cmx = fmaxf(cmx, __shfl_xor(cmx, off, 64));
+        uint64_t csm = 0;
+#pragma unroll
+        for (int c = 0; c < CB; ++c) csm += npn::expfix_rel(xs[c], cmx);
+#pragma unroll
+        for (int off = LPC / 2; off > 0; off >>= 1) csm += shfl_xor_u64(csm, off);
+        if (i % LPC == 0 && col_ok && m < a.M) {
+          const size_t o = (size_t)m * (a.N / 64) + (nc >> 6);
+          a.cmax[o] = cmx;
+          a.csum[o] = csm;
+        }
+      }
     }
   } else {
     store_partial(sk, n0, acc, false);
@@ -402,6 +440,13 @@ struct WideArgs {
   // workgroup takes gate units u0..u1 (at most NH) and the up units N/2 columns to their
   // right, wave column half 0 computing gate and 1 up; out [M, N/2] = bf16(bf16(silu(g)) * u)
   int swiglu;
+  int ualign;      // column groups hold whole runs of ualign units (4: 64-column chunks)
+  // with out (split_k == 1): the acceptance contract's statistics of each row's 64-column
+  // chunks of the bf16 outputs scaled by inv_temp, [M][N / 64] (cmax == nullptr: none;
+  // then ualign == 4)
+  float* cmax;
+  uint64_t* csum;
+  float inv_temp;
 };
 
 typedef int i32x2 __attribute__((ext_vector_type(2)));
@@ -444,6 +489,43 @@ __device__ __forceinline__ void staged_row_max(const uint16_t* st, int rs, float
   if (half == 0 && m_base + row < M) gmax[(size_t)(m_base + row) * ld + grp] = mx;
 }
 
+// The acceptance contract's statistics of a staged bf16 tile (256 rows of 16 nu values, row
+// stride rs; nu a multiple of 4 and the tile's column 0 at output column n0, a multiple of 64):
+// per (row, 64-column chunk) the max of s = value * inv_temp (NaN ignored) and the sum of
+// expfix(s - max), into cmax / csum [M][nc]. Two threads per row, 32 columns of each chunk.
+__device__ __forceinline__ void staged_chunk_stats(const uint16_t* st, int rs, float* cmax,
+                                                   uint64_t* csum, float inv_temp, int nc,
+                                                   int m_base, int M, int n0, int nu) {
+  const int row = threadIdx.x >> 1, half = threadIdx.x & 1;
+  const int m = m_base + row;
+  for (int q = 0; q < nu / 4; ++q) {
+    float x[32];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const uint4 v = *reinterpret_cast<const uint4*>(st + row * rs + 64 * q + 32 * half + 8 * p);
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        x[8 * p + 2 * k] = npn::scaled(npn::bf16lo(w[k]), inv_temp);
+        x[8 * p + 2 * k + 1] = npn::scaled(npn::bf16hi(w[k]), inv_temp);
+      }
+    }
+    float mx = -__builtin_inff();
+#pragma unroll
+    for (int e = 0; e < 32; ++e) mx = fmaxf(mx, x[e]);
+    mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
+    uint64_t sm = 0;
+#pragma unroll
+    for (int e = 0; e < 32; ++e) sm += npn::expfix_rel(x[e], mx);
+    sm += shfl_xor_u64(sm, 1);
+    if (half == 0 && m < M) {
+      const size_t o = (size_t)m * nc + (n0 >> 6) + q;
+      cmax[o] = mx;
+      csum[o] = sm;
+    }
+  }
+}
+
 template <int NH>
 constexpr int kSwigluStageOff = 4 * 64 * 16 * NH * 2;
 
@@ -466,8 +548,9 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void fp8_gemm_wide_kernel(WideArgs
   const int sk = logical % a.split_k;
   const int grp = logical / a.split_k;
   if (grp >= a.groups) return;
-  const int u0 = (int)((long)grp * a.units / a.groups);
-  const int u1 = (int)((long)(grp + 1) * a.units / a.groups);
+  const int ua = a.ualign;  // groups of whole ua-unit runs, balanced over the workgroups
+  const int u0 = ua * (int)((long)grp * (a.units / ua) / a.groups);
+  const int u1 = ua * (int)((long)(grp + 1) * (a.units / ua) / a.groups);
   const int nu = u1 - u0;
   if (nu <= 0) return;
   const int n0 = 16 * u0;
@@ -720,6 +803,8 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void fp8_gemm_wide_kernel(WideArgs
     __syncthreads();
     store_staged_bf16(st, RSW, a.out, a.N, m_base, a.M, n0, nu);
     if (a.gmax != nullptr) staged_row_max(st, RSW, a.gmax, a.groups, grp, m_base, a.M, nu);
+    if (a.cmax != nullptr)
+      staged_chunk_stats(st, RSW, a.cmax, a.csum, a.inv_temp, a.N / 64, m_base, a.M, n0, nu);
     return;
   }
   // fp32 partials (unscaled; the scale pointer may then be NULL), staged 128 rows at a time
@@ -793,7 +878,8 @@ struct GemmPlan {
   size_t ws;
   bool wide;
   int units, groups, ntm;
-  int sk_wg;  // narrow: stream-K workgroups (0: a tiles x split_k grid)
+  int sk_wg;   // narrow: stream-K workgroups (0: a tiles x split_k grid)
+  int ualign;  // wide: column groups hold whole runs of ualign 16-column units
 };
 
 // Wide-kernel instantiations: column tiles per wave (a workgroup holds twice as many units).
@@ -812,8 +898,10 @@ constexpr int kWideNH[] = {1, 2, 3, 4, 5, 6};
 // workgroups is taken: fewest padded tiles, and every workgroup's tiles nearly all real.
 // Wider N (an LM head's vocabulary) runs in rounds of 256 workgroups of the widest tiles,
 // without split-K. `no_split` (the argmax epilogue, which needs whole sums) keeps s = 1.
-bool plan_wide(int M, int K, int N, GemmPlan& p, bool no_split) {
-  if (M <= 64 || K % KC != 0 || N % 16 != 0) return false;
+// ua > 1 makes every column group a whole number of ua-unit runs (4: the 64-column chunks of
+// the acceptance statistics), so a group of up to 2 ntm units holds floor(2 ntm / ua) runs.
+bool plan_wide(int M, int K, int N, GemmPlan& p, bool no_split, int ua) {
+  if (M <= 64 || K % KC != 0 || N % (16 * ua) != 0) return false;
   const int units = N / 16;
   const int passes = (M + 255) / 256;
   double best = 1e30;
@@ -822,15 +910,19 @@ bool plan_wide(int M, int K, int N, GemmPlan& p, bool no_split) {
     const double part_bytes = (double)s * M * N * 4;
     if (s > 1 && part_bytes > 48e6) break;
     const int gmax = WIDE_WG / s;
+    const int runs = units / ua;
     int ntm = 0, groups = 0;
     for (int v : kWideNH) {
-      const int g = (units + 2 * v - 1) / (2 * v);
+      const int cap = 2 * v / ua;  // runs per group
+      if (cap == 0) continue;
+      const int g = (runs + cap - 1) / cap;
       if (g <= gmax) { ntm = v; groups = g; break; }
     }
     if (ntm == 0) {
       if (s > 1) continue;
       ntm = kWideNH[sizeof(kWideNH) / sizeof(kWideNH[0]) - 1];
-      groups = (units + 2 * ntm - 1) / (2 * ntm);
+      const int cap = 2 * ntm / ua;
+      groups = (runs + cap - 1) / cap;
     }
     const int rounds = (groups * s + WIDE_WG - 1) / WIDE_WG;
     const double kk = (double)K / s;
@@ -849,14 +941,16 @@ bool plan_wide(int M, int K, int N, GemmPlan& p, bool no_split) {
   }
   if (!p.wide) return false;
   p.passes = passes;
+  p.ualign = ua;
   p.ws = p.split_k > 1 ? (size_t)p.split_k * M * N * sizeof(float) : 0;
   return true;
 }
 
-GemmPlan plan(int M, int K, int N, bool no_split = false) {
+GemmPlan plan(int M, int K, int N, bool no_split = false, int ua = 1) {
   GemmPlan p{};
-  if (plan_wide(M, K, N, p, no_split)) return p;
+  if (plan_wide(M, K, N, p, no_split, ua)) return p;
   p = GemmPlan{};
+  p.ualign = 1;
   // Narrow plan: one pass of RB = 1, 2 or 4 row blocks (M <= 64), and a split-K factor: the
   // largest power of two up to 8 whose grid stays at or under 576 workgroups (up to 16 and
   // 1152 workgroups for at most 16 rows, whose partials are small) with at least 8 k steps
@@ -916,12 +1010,13 @@ bool shape_ok(int M, int K, int N) {
 int launch_gemm(const GemmPlan& p, const uint16_t* x, const int8_t* w, const float* scale,
                 uint16_t* out, float* partial, int M, int K, int N, int to_partial, bool reduce,
                 hipStream_t s, ArgPart* amax = nullptr, bool swiglu = false,
-                float* gmax = nullptr) {
+                float* gmax = nullptr, float* cmax = nullptr, uint64_t* csum = nullptr,
+                float inv_temp = 1.0f) {
   if (p.wide) {
     // SwiGLU: the same groups, each of at most ntm gate units (plus their up units)
     WideArgs wa{x, reinterpret_cast<const uint8_t*>(w), scale, out, partial, M, K, N,
                 swiglu ? p.units / 2 : p.units, p.groups, p.split_k, to_partial, amax, gmax,
-                swiglu ? 1 : 0};
+                swiglu ? 1 : 0, p.ualign, cmax, csum, inv_temp};
     const int nwg = ((p.groups * p.split_k + 7) / 8) * 8;  // multiple of 8 for the XCD map
     const dim3 grid(nwg, p.passes);
     const dim3 block(WIDE_THREADS);
@@ -935,7 +1030,7 @@ int launch_gemm(const GemmPlan& p, const uint16_t* x, const int8_t* w, const flo
     }
   } else {
     GemmArgs ga{x, reinterpret_cast<const uint8_t*>(w), scale, out, partial, M, K, N, p.split_k,
-                to_partial, amax, gmax, p.sk_wg};
+                to_partial, amax, gmax, p.sk_wg, cmax, csum, inv_temp};
     const dim3 grid = p.sk_wg > 0 ? dim3(p.sk_wg, 1, 1) : dim3((N + NT - 1) / NT, p.split_k, p.passes);
     switch (p.mt) {
       case 1: hipLaunchKernelGGL((fp8_gemm_narrow_kernel<1, 4, 4>), grid, dim3(256), 0, s, ga); break;
@@ -1191,6 +1286,27 @@ extern "C" int npn_fp8_matmul_rowmax(const uint16_t* x, const int8_t* w, const f
   return launch_gemm(p, x, w, scale, out, nullptr, M, K, N, 0, false,
                      static_cast<hipStream_t>(stream), nullptr, false, gmax);
 }
+
+namespace npn {
+
+bool fp8_matmul_chunk_stats_ok(int M, int K, int N) {
+  if (!shape_ok(M, K, N) || N % 64 != 0) return false;
+  const GemmPlan p = plan(M, K, N, true, 4);
+  return p.split_k == 1 && (!p.wide || p.ualign == 4);
+}
+
+int fp8_matmul_chunk_stats(const uint16_t* x, const int8_t* w, const float* scale, uint16_t* out,
+                           float* cmax, uint64_t* csum, float inv_temp, int M, int K, int N,
+                           hipStream_t stream) {
+  NPN_REQUIRE(x && w && scale && out && cmax && csum, NPN_ERR_NULL);
+  NPN_REQUIRE(fp8_matmul_chunk_stats_ok(M, K, N), NPN_ERR_SHAPE);
+  NPN_REQUIRE(NPN_ALIGNED16(x) && NPN_ALIGNED16(w) && NPN_ALIGNED16(out), NPN_ERR_ALIGN);
+  const GemmPlan p = plan(M, K, N, true, 4);
+  return launch_gemm(p, x, w, scale, out, nullptr, M, K, N, 0, false, stream, nullptr, false,
+                     nullptr, cmax, csum, inv_temp);
+}
+
+}  // namespace npn
 
 // deltanet::full_fp8: the four in-projections of one decode token, then the token step of
 // deltanet::full on their outputs. Four launches: the qkv and z GEMMs writing split-K partials

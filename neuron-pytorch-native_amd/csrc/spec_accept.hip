@@ -6,82 +6,46 @@
 //   accepted a_b = number of leading drafts equal to tid[b, position before them].
 //
 // Rejection sampling (Leviathan et al. 2023, Alg. 1) under an integer softmax contract
-// that this file and its CPU restatement evaluate with identical IEEE-754 operations:
-//   s_v = t_v * inv_temp (fp32); m = max_v s_v; E_v = floor(2^31 * exp_c(s_v - m)) where
-//   exp_c is a Cody-Waite reduction + degree-7 Taylor polynomial evaluated with explicit
-//   fp32 fused multiply-adds (this file is compiled with -ffp-contract=off, so no other
-//   multiply and add is fused);
-//   Z = sum_v E_v in 64-bit integers (exact, so the reduction order does not matter).
-//   Accept draft x at position i iff U * Eq_x * Zp <= 2^24 * Ep_x * Zq (128-bit integers,
-//   U = floor(u * 2^24)). At the first rejection sample from R_v = max(0, Ep_v Zq - Eq_v Zp),
-//   after K acceptances from R_v = Ep_v of the bonus row: the token is the smallest v with
-//   2^24 * sum_{w<=v} R_w > U_s * sum_w R_w.
+// (accept_contract.h) that this file and its CPU restatement evaluate with identical
+// IEEE-754 operations:
+//   s_v = t_v * inv_temp (fp32); 64-entry chunks c with maxima m_c; E_v = floor(2^31 *
+//   exp_c(s_v - m_c)); S_c = sum of E over the chunk; M = max_c m_c; F_c = floor(2^31 *
+//   exp_c(m_c - M)); the weight of v is W_v = E_v F_c and Z = sum_c F_c S_c (exact integers).
+//   Accept draft x at position i iff U * Wq_x * Zp <= 2^24 * Wp_x * Zq (U = floor(u * 2^24));
+//   a draft id outside [0, V) is a rejection. At the first rejection sample from
+//   R_v = max(0, Wp_v Zq - Wq_v Zp), after K acceptances from R_v = Wp_v of the bonus row: the
+//   token is the smallest v with 2^24 * sum_{w<=v} R_w > U_s * sum_w R_w.
 //
-// Kernels (each over B sequences, T = K+1 positions, vocabulary split into 8192-wide chunks):
-//   greedy:    argmax partials per (row, chunk) -> per-sequence merge + accept
-//   rejection: one pass per (row, chunk): the chunk maximum, the sum of E and E at the draft
-//              token -> per-sequence row totals and decision -> residual/bonus mass per
-//              (sequence, chunk) -> per-sequence inverse-CDF pick
-#include "npn_common.h"
+// Kernels (each over B sequences, T = K+1 positions):
+//   greedy:    argmax partials per (row, 8192-entry chunk) -> per-sequence merge + accept
+//   rejection: chunk statistics (m_c, S_c) of every row in one pass over the logits (for the
+//              LM head the target rows' come from the GEMM epilogue) -> per-row totals M, Z
+//              and the draft token's weight -> one sampling kernel: every block re-derives the
+//              sequence's decision, adds the residual (or bonus) mass of its 2048 entries,
+//              and the last block of each sequence to finish runs the inverse CDF
+#include "accept_contract.h"
+#include "npn_internal.h"
 
 #include <mutex>
 
 namespace {
 
-constexpr int CHK = 8192;      // vocabulary entries per chunk (logit passes)
+constexpr int CHK = 8192;      // vocabulary entries per greedy argmax partial
 constexpr int THREADS = 256;   // CHK / THREADS = 32 entries per thread
 constexpr int PER_T = CHK / THREADS;
-constexpr int MCHK = 2048;     // entries per chunk of the residual mass / inverse-CDF pass
-constexpr int PER_M = MCHK / THREADS;  // 8 consecutive entries per thread
+constexpr int CC = npn::kContractChunk;  // 64 entries per chunk of the rejection contract
+constexpr int SBLK = 8192;     // entries per block of the chunk-statistics pass (128 chunks)
+constexpr int MCHK = 2048;     // entries per block of the sampling kernel
+constexpr int PER_M = MCHK / THREADS;  // 8 consecutive entries per thread, inside one chunk
 constexpr int kRejMaxV = 1 << 20;  // largest vocabulary of the rejection path
+static_assert(SBLK / THREADS == 32 && CC % PER_M == 0, "entry layouts of the rejection kernels");
 
 typedef unsigned __int128 u128;
 
-// ---- exp contract (must match oracle.accept.expfix bit for bit) -------------------------
-constexpr float kL2E = 0x1.715476p+0f;        // log2(e) in fp32
-constexpr float kLn2Hi = 0x1.62ep-1f;         // ln2, low 12 mantissa bits cleared
-constexpr float kLn2Lo = 0x1.0bfbe8p-15f;     // ln2 - kLn2Hi in fp32
-constexpr float kMagic = 0x1.8p+23f;          // 1.5 * 2^23: fma(x, kL2E, kMagic) rounds to an integer
-// Taylor coefficients 1/k! in fp32, scaled by 2^31 (exact), k = 7..0
-constexpr float kP7 = 0x1.a01a02p+18f;
-constexpr float kP6 = 0x1.6c16c2p+21f;
-constexpr float kP5 = 0x1.111112p+24f;
-constexpr float kP4 = 0x1.555556p+26f;
-constexpr float kP3 = 0x1.555556p+28f;
-constexpr float kP2 = 0x1p+30f;
-constexpr float kP1 = 0x1p+31f;               // 2^31 / 1! and 2^31 / 0!
-constexpr float kXMin = -32.0f;               // at and below: 2^31 exp(x) < 1
-
-// E = floor(2^31 * exp_c(x)) for x <= 0 (NaN and x <= -32 give 0; E(0) = 2^31).
-// kf = t - kMagic is round(x * log2 e) as an exact fp32 integer, and t's bit pattern holds
-// kf in its low bits, so adding (bits(t) << 23) to p's pattern multiplies p by 2^kf exactly
-// (the exponent stays in the normal range: p >= 2^30 and kf >= -47). The conversion to
-// uint32 truncates, which is the floor of a value in [0, 2^31].
-__device__ __forceinline__ uint32_t expfix(float x) {
-  x = fmaxf(x, kXMin);
-  const float t = __builtin_fmaf(x, kL2E, kMagic);
-  const float kf = t - kMagic;
-  float r = __builtin_fmaf(-kf, kLn2Hi, x);
-  r = __builtin_fmaf(-kf, kLn2Lo, r);
-  float p = __builtin_fmaf(kP7, r, kP6);
-  p = __builtin_fmaf(p, r, kP5);
-  p = __builtin_fmaf(p, r, kP4);
-  p = __builtin_fmaf(p, r, kP3);
-  p = __builtin_fmaf(p, r, kP2);
-  p = __builtin_fmaf(p, r, kP1);
-  p = __builtin_fmaf(p, r, kP1);
-  return (uint32_t)__uint_as_float(__float_as_uint(p) + (__float_as_uint(t) << 23));
-}
-
-__device__ __forceinline__ float scaled(float v, float inv_temp) {
-#pragma clang fp contract(off)
-  return v * inv_temp;
-}
-
-__device__ __forceinline__ uint32_t uniform_fix(float u) {
-#pragma clang fp contract(off)
-  return (uint32_t)(u * 16777216.0f);
-}
+using npn::expfix;
+using npn::expfix_rel;
+using npn::scaled;
+using npn::uniform_fix;
 
 // ---- block reductions ----------------------------------------------------------------------
 __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
@@ -164,39 +128,6 @@ __device__ __forceinline__ void visit_chunk(const float* src, int v0, int V, boo
     for (int j = 0; j < PER_T; ++j) {
       const int v = v0 + j * THREADS + (int)threadIdx.x;
       if (v < V) f(v, src[v]);
-    }
-  }
-}
-
-// The same over a bf16 row (the LM head's logits): with vec (row 16-byte aligned, V % 8 == 0)
-// the thread reads PER_T/8 16-byte pieces of 8 entries at v0 + 8 * (j * THREADS + tid).
-template <typename F>
-__device__ __forceinline__ void visit_chunk(const uint16_t* src, int v0, int V, bool vec, F f) {
-  auto unpack = [&](int v, uint4 x) {
-    const uint32_t w[4] = {x.x, x.y, x.z, x.w};
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      f(v + 2 * k, npn::bf16_to_f32(w[k] & 0xFFFFu));
-      f(v + 2 * k + 1, npn::bf16_to_f32(w[k] >> 16));
-    }
-  };
-  if (vec && v0 + CHK <= V) {
-    uint4 x[PER_T / 8];
-#pragma unroll
-    for (int j = 0; j < PER_T / 8; ++j)
-      x[j] = *reinterpret_cast<const uint4*>(src + v0 + 8 * (j * THREADS + (int)threadIdx.x));
-#pragma unroll
-    for (int j = 0; j < PER_T / 8; ++j) unpack(v0 + 8 * (j * THREADS + (int)threadIdx.x), x[j]);
-  } else if (vec) {
-#pragma unroll
-    for (int j = 0; j < PER_T / 8; ++j) {
-      const int v = v0 + 8 * (j * THREADS + (int)threadIdx.x);
-      if (v < V) unpack(v, *reinterpret_cast<const uint4*>(src + v));
-    }
-  } else {
-    for (int j = 0; j < PER_T; ++j) {
-      const int v = v0 + j * THREADS + (int)threadIdx.x;
-      if (v < V) f(v, npn::bf16_to_f32(src[v]));
     }
   }
 }
@@ -329,12 +260,10 @@ __global__ __launch_bounds__(1024) void greedy_accept_parts_kernel(
 
 // ---- rejection sampling ------------------------------------------------------------------
 // 192-bit unsigned integers (three 64-bit limbs, little end first) for the exact products of
-// the contract: W (< 2^63) times Z (< 2^80), times a 24-bit uniform or shift.
+// the contract: W (<= 2^62) times Z (<= 2^82), times a 24-bit uniform or shift.
 struct u192 {
   uint64_t w0, w1, w2;
 };
-
-__device__ __forceinline__ u192 u192_from(u128 x) { return u192{(uint64_t)x, (uint64_t)(x >> 64), 0}; }
 
 __device__ __forceinline__ u192 add192(u192 a, u192 b) {
   const u128 s0 = (u128)a.w0 + b.w0;
@@ -392,18 +321,16 @@ struct RejArgs {
   float inv_temp;
   int32_t* accepted;
   int64_t* out_ids;
-  int B, K, V, nch, nchm;  // chunks of CHK (logit pass) and of MCHK (mass / pick)
-  bool vec4;          // logit rows 16-byte aligned and V % 4 == 0 (V % 8 for bf16 rows)
-  // workspace (rows = B*(K+1) target rows, then B*K draft rows)
-  u128* zrow;         // [rows]        Z of each row
-  float* mrow;        // [rows]        row maximum M (scaled logits)
-  uint32_t* ex;       // [rows]        E at the row's draft token (target/draft rows i < K)
-  float* rmax;        // [rows][nch]   chunk maxima m_c
-  uint64_t* rsum;     // [rows][nch]   chunk sums S_c
-  int32_t* dec_row;   // [B]           sampling position (target row; draft row or none)
-  u128* dec_z;        // [B][2]        Zp, Zq of the sampling rows
-  float* dec_m;       // [B][2]        row maxima of the sampling rows
-  u192* cmass;        // [B][nchm]
+  int B, K, V, nc, nchm;  // contract chunks per row; sampling-kernel blocks per row
+  bool vec4;              // fp32 logit rows 16-byte aligned and V % 4 == 0 (bf16: V % 8)
+  // workspace (rows: the B*(K+1) target rows, then the B*K draft rows)
+  u128* zrow;             // [rows]      Z of each row
+  float* mrow;            // [rows]      row maximum M (scaled logits)
+  uint64_t* wtok;         // [rows]      W of the row's draft token (0: bonus row, bad id)
+  float* cmax;            // [rows][nc]  chunk maxima m_c
+  uint64_t* csum;         // [rows][nc]  chunk sums S_c
+  u192* cmass;            // [B][nchm]   sampling mass of each sampling-kernel block
+  uint32_t* cnt;          // [B]         sampling-kernel blocks finished, per sequence
 };
 
 template <typename TT>
@@ -416,7 +343,7 @@ __device__ __forceinline__ const TT* target_row(const RejArgs& a, int row) {
 // range), so no emitted id lies outside the vocabulary.
 __device__ __forceinline__ bool draft_id_ok(int64_t x, int V) { return x >= 0 && x < V; }
 
-// Draft token whose E this row reports, or -1 (bonus rows, and out-of-range draft ids).
+// Draft token whose weight this row reports, or -1 (bonus rows, and out-of-range draft ids).
 __device__ __forceinline__ int row_token(const RejArgs& a, int row) {
   const int nt = a.B * (a.K + 1);
   int b, i;
@@ -432,115 +359,149 @@ __device__ __forceinline__ int row_token(const RejArgs& a, int row) {
   return draft_id_ok(x, a.V) ? (int)x : -1;
 }
 
-// This thread's entries of chunk [v0, v0 + CHK) of a row, in registers, scaled (NaN for
-// entries past V: the maximum ignores them and they get E = 0). Same entry assignment as
-// visit_chunk; the sums are exact, so the assignment does not affect results.
+// The 16-lane shuffles of the statistics pass (lanes that share a chunk).
+__device__ __forceinline__ float max16(float m) {
+#pragma unroll
+  for (int off = 8; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+  return m;
+}
+
+__device__ __forceinline__ uint64_t sum16(uint64_t s) {
+#pragma unroll
+  for (int off = 8; off > 0; off >>= 1) s += shfl_xor_u64(s, off);
+  return s;
+}
+
+// Chunk statistics of fp32 logit rows: block (x, y) reads entries [8192 x, 8192 x + 8192) of
+// row row0 + y once, into registers (thread t holds the float4s at v0 + 4 (256 j + t),
+// j < 8, so for each j the 16 lanes of a 16-lane group hold one 64-entry chunk), and writes
+// each chunk's maximum m_c of the scaled logits (NaN ignored; entries past V read as NaN)
+// and S_c = sum of expfix(s_v - m_c).
 template <bool kUnitTemp>
-__device__ __forceinline__ void load_chunk(const float* src, int v0, int V, bool vec4,
-                                           float inv_temp, float (&x)[PER_T]) {
-  if (vec4 && v0 + CHK <= V) {
+__global__ __launch_bounds__(THREADS) void rej_stats_kernel(RejArgs a, int row0) {
+  const int row = row0 + (int)blockIdx.y;
+  const int nt = a.B * (a.K + 1);
+  const float* src = row < nt ? static_cast<const float*>(a.target) + (size_t)row * a.V
+                              : a.draft + (size_t)(row - nt) * a.V;
+  const int v0 = (int)blockIdx.x * SBLK;
+  const int t = threadIdx.x;
+  float x[32];
+  if (a.vec4 && v0 + SBLK <= a.V) {  // whole block inside the row: all loads first, no guards
 #pragma unroll
-    for (int j = 0; j < PER_T / 4; ++j) {
-      const float4 f =
-          *reinterpret_cast<const float4*>(src + v0 + 4 * (j * THREADS + (int)threadIdx.x));
-      x[4 * j] = f.x; x[4 * j + 1] = f.y; x[4 * j + 2] = f.z; x[4 * j + 3] = f.w;
-    }
-  } else if (vec4) {
-#pragma unroll
-    for (int j = 0; j < PER_T / 4; ++j) {
-      const int v = v0 + 4 * (j * THREADS + (int)threadIdx.x);
-      float4 f = make_float4(NAN, NAN, NAN, NAN);
-      if (v < V) f = *reinterpret_cast<const float4*>(src + v);
+    for (int j = 0; j < 8; ++j) {
+      const float4 f = *reinterpret_cast<const float4*>(src + v0 + 4 * (j * THREADS + t));
       x[4 * j] = f.x; x[4 * j + 1] = f.y; x[4 * j + 2] = f.z; x[4 * j + 3] = f.w;
     }
   } else {
 #pragma unroll
-    for (int j = 0; j < PER_T; ++j) {
-      const int v = v0 + j * THREADS + (int)threadIdx.x;
-      x[j] = v < V ? src[v] : NAN;
-    }
-  }
-  if (!kUnitTemp) {
-#pragma unroll
-    for (int j = 0; j < PER_T; ++j) x[j] = scaled(x[j], inv_temp);
-  }
-}
-
-template <bool kUnitTemp>
-__device__ __forceinline__ void load_chunk(const uint16_t* src, int v0, int V, bool vec,
-                                           float inv_temp, float (&x)[PER_T]) {
-  if (vec) {
-#pragma unroll
-    for (int j = 0; j < PER_T / 8; ++j) {
-      const int v = v0 + 8 * (j * THREADS + (int)threadIdx.x);
-      uint4 q = make_uint4(0x7FC07FC0u, 0x7FC07FC0u, 0x7FC07FC0u, 0x7FC07FC0u);  // bf16 NaNs
-      if (v < V) q = *reinterpret_cast<const uint4*>(src + v);
-      const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+    for (int j = 0; j < 8; ++j)
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        x[8 * j + 2 * k] = npn::bf16_to_f32(w[k] & 0xFFFFu);
-        x[8 * j + 2 * k + 1] = npn::bf16_to_f32(w[k] >> 16);
+        const int v = v0 + 4 * (j * THREADS + t) + k;
+        x[4 * j + k] = v < a.V ? src[v] : NAN;
       }
-    }
-  } else {
-#pragma unroll
-    for (int j = 0; j < PER_T; ++j) {
-      const int v = v0 + j * THREADS + (int)threadIdx.x;
-      x[j] = v < V ? npn::bf16_to_f32(src[v]) : NAN;
-    }
   }
   if (!kUnitTemp) {
 #pragma unroll
-    for (int j = 0; j < PER_T; ++j) x[j] = scaled(x[j], inv_temp);
+    for (int e = 0; e < 32; ++e) x[e] = scaled(x[e], a.inv_temp);
   }
-}
-
-// The one logit pass: chunk c of a row, read once into registers; its maximum m_c, then
-// S_c = sum of E_v = expfix(s_v - m_c), and E at the row's draft token if it lies here.
-// kUnitTemp skips the multiply by inv_temp == 1 (x * 1 == x, NaN stays NaN).
-template <bool kUnitTemp, typename TT>
-__global__ __launch_bounds__(THREADS) void rej_scan_kernel(RejArgs a) {
-  __shared__ float shm[THREADS / 64];
-  __shared__ uint64_t shs[THREADS / 64];
-  const int row = (int)blockIdx.y, c = (int)blockIdx.x;
-  const int nt = a.B * (a.K + 1);
-  const int v0 = c * CHK;
-  float x[PER_T];
-  if (row >= nt)
-    load_chunk<kUnitTemp>(a.draft + (size_t)(row - nt) * a.V, v0, a.V, a.vec4, a.inv_temp, x);
-  else
-    load_chunk<kUnitTemp>(target_row<TT>(a, row), v0, a.V, a.vec4, a.inv_temp, x);
-  float m = -INFINITY;
+  float* cm = a.cmax + (size_t)row * a.nc;
+  uint64_t* cs = a.csum + (size_t)row * a.nc;
 #pragma unroll
-  for (int j = 0; j < PER_T; ++j) m = fmaxf(m, x[j]);
-  m = block_max(m, shm);
-  uint64_t z = 0;
+  for (int j = 0; j < 8; ++j) {
+    float m = -INFINITY;
 #pragma unroll
-  for (int j = 0; j < PER_T; ++j) z += expfix(x[j] - m);
-  z = block_sum_u64(z, shs);
-  if (threadIdx.x == 0) {
-    a.rmax[(size_t)row * a.nch + c] = m;
-    a.rsum[(size_t)row * a.nch + c] = z;
-    const int tok = row_token(a, row);
-    if (tok >= v0 && tok < v0 + CHK) {
-      const float xt = row >= nt ? a.draft[(size_t)(row - nt) * a.V + tok]
-                                 : elem(target_row<TT>(a, row), tok);
-      a.ex[row] = expfix(scaled(xt, a.inv_temp) - m);
+    for (int k = 0; k < 4; ++k) m = fmaxf(m, x[4 * j + k]);
+    m = max16(m);
+    uint64_t s = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) s += expfix_rel(x[4 * j + k], m);
+    s = sum16(s);
+    const int c = (v0 >> 6) + ((j * THREADS + t) >> 4);
+    if ((t & 15) == 0 && c < a.nc) {
+      cm[c] = m;
+      cs[c] = s;
     }
   }
 }
 
-// Sampling weight of vocabulary entry v for sequence b (residual or bonus), in one MCHK chunk
-// (inside one CHK chunk c, whose m_c and F_c are fixed per call). After a rejection the
-// residual W^p Zq - W^q Zp = E^p (F^p Zq) - E^q (F^q Zp): the two bracketed products
-// (< 2^111) are formed once per call, so each entry costs two 32 x 128-bit products.
+__device__ __forceinline__ float elem_at(const RejArgs& a, int row, int v, const float*) {
+  const int nt = a.B * (a.K + 1);
+  return row < nt ? static_cast<const float*>(a.target)[(size_t)row * a.V + v]
+                  : a.draft[(size_t)(row - nt) * a.V + v];
+}
+
+__device__ __forceinline__ float elem_at(const RejArgs& a, int row, int v, const uint16_t*) {
+  const int nt = a.B * (a.K + 1);
+  return row < nt ? npn::bf16_to_f32(static_cast<const uint16_t*>(a.target)[(size_t)row * a.V + v])
+                  : a.draft[(size_t)(row - nt) * a.V + v];
+}
+
+// Row totals, one block per row: M = max_c m_c, Z = sum_c F_c S_c (F_c = expfix(m_c - M)),
+// and W = E F_c of the row's draft token (its logit and chunk maximum are loaded first). The
+// first target row of each sequence also clears the sequence's counter of finished
+// sampling-kernel blocks (the sampling kernel runs after this one, on the same stream).
+template <typename TT>
+__global__ __launch_bounds__(THREADS) void rej_rowtotal_kernel(RejArgs a) {
+  __shared__ float shm[THREADS / 64];
+  __shared__ u128 shz[THREADS / 64];
+  const int row = (int)blockIdx.x;
+  const int nt = a.B * (a.K + 1);
+  const float* cm = a.cmax + (size_t)row * a.nc;
+  const uint64_t* cs = a.csum + (size_t)row * a.nc;
+  const int tok = row_token(a, row);
+  float xt = 0.f, mt = 0.f;
+  if (threadIdx.x == 0 && tok >= 0) {
+    xt = elem_at(a, row, tok, static_cast<const TT*>(nullptr));
+    mt = cm[tok / CC];
+  }
+  constexpr int U = 8;  // chunks per thread per batch, loads issued together
+  float M = -INFINITY;
+  for (int c0 = threadIdx.x; c0 < a.nc; c0 += U * THREADS) {
+    float v[U];
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      const int c = c0 + k * THREADS;
+      v[k] = c < a.nc ? cm[c] : -INFINITY;
+    }
+#pragma unroll
+    for (int k = 0; k < U; ++k) M = fmaxf(M, v[k]);
+  }
+  M = block_max(M, shm);
+  u128 z = 0;
+  for (int c0 = threadIdx.x; c0 < a.nc; c0 += U * THREADS) {
+    float v[U];
+    uint64_t s[U];
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      const int c = c0 + k * THREADS;
+      v[k] = c < a.nc ? cm[c] : -INFINITY;
+      s[k] = c < a.nc ? cs[c] : 0;
+    }
+#pragma unroll
+    for (int k = 0; k < U; ++k) z += (u128)s[k] * expfix_rel(v[k], M);
+  }
+  z = block_sum_u128(z, shz);
+  if (threadIdx.x == 0) {
+    a.zrow[row] = z;
+    a.mrow[row] = M;
+    a.wtok[row] = tok < 0 ? 0
+                          : (uint64_t)expfix_rel(scaled(xt, a.inv_temp), mt) * expfix_rel(mt, M);
+    if (row < nt && row % (a.K + 1) == 0) a.cnt[row / (a.K + 1)] = 0;
+  }
+}
+
+// The sampling rows of one sequence, as seen by one thread at the contract chunk cc of its
+// run: after a rejection at position acc the residual W^p Zq - W^q Zp = E^p (F^p Zq) -
+// E^q (F^q Zp), whose bracketed products (< 2^114) are formed once per thread; for the bonus
+// row the weight is E^p F^p.
 template <typename TT>
 struct SampleRow {
   const TT* p;
   const float* q;  // nullptr for the bonus row
-  float mp, mq;    // chunk maxima of the chunk being weighed
-  uint64_t fp;     // F^p_c (the bonus weight is E^p F^p_c)
-  u128 gp, gq;     // F^p_c Zq and F^q_c Zp
+  float mp, mq;    // chunk maxima of chunk cc
+  uint64_t fp;     // F^p of chunk cc
+  u128 gp, gq;     // F^p Zq and F^q Zp
   double gpd, gqd; // the same, rounded to fp64 (relative error below 2^-51)
 };
 
@@ -548,24 +509,29 @@ __device__ __forceinline__ double u128_to_f64(u128 x) {
   return (double)(uint64_t)(x >> 64) * 0x1p64 + (double)(uint64_t)x;
 }
 
-// The sampling rows of sequence b at position acc (the first rejection, or K: bonus), with
-// row maxima Mp, Mq and totals Zp, Zq, positioned at the CHK chunk c.
+// Decision of sequence b, shared by the blocks of the sampling kernel.
+struct Decision {
+  int acc;         // accepted drafts (the sampling position)
+  float mp, mq;    // row maxima of the sampling rows (mq: draft row, after a rejection)
+  u128 zp, zq;     // their totals
+};
+
 template <typename TT>
-__device__ __forceinline__ SampleRow<TT> sample_row(const RejArgs& a, int b, int acc, float Mp,
-                                                    float Mq, u128 zp, u128 zq, int c) {
+__device__ __forceinline__ SampleRow<TT> sample_row(const RejArgs& a, int b, const Decision& d,
+                                                    int cc) {
   const int K = a.K, T = K + 1;
   const int nt = a.B * T;
   SampleRow<TT> s;
-  const int rp = b * T + acc;
+  const int rp = b * T + d.acc;
   s.p = target_row<TT>(a, rp);
-  s.mp = a.rmax[(size_t)rp * a.nch + c];
-  s.fp = expfix(s.mp - Mp);
-  s.gp = (u128)s.fp * zq;
-  if (acc < K) {
-    const int rq = nt + b * K + acc;
-    s.q = a.draft + (size_t)(b * K + acc) * a.V;
-    s.mq = a.rmax[(size_t)rq * a.nch + c];
-    s.gq = (u128)expfix(s.mq - Mq) * zp;
+  s.mp = a.cmax[(size_t)rp * a.nc + cc];
+  s.fp = expfix_rel(s.mp, d.mp);
+  s.gp = (u128)s.fp * d.zq;
+  if (d.acc < K) {
+    const int rq = nt + b * K + d.acc;
+    s.q = a.draft + (size_t)(b * K + d.acc) * a.V;
+    s.mq = a.cmax[(size_t)rq * a.nc + cc];
+    s.gq = (u128)expfix_rel(s.mq, d.mq) * d.zp;
   } else {
     s.q = nullptr;
     s.mq = 0.f;
@@ -579,9 +545,9 @@ __device__ __forceinline__ SampleRow<TT> sample_row(const RejArgs& a, int b, int
 template <typename TT>
 __device__ __forceinline__ u192 weight_of(const SampleRow<TT>& s, float pv, float qv,
                                           float inv_temp) {
-  const uint32_t ep = expfix(scaled(pv, inv_temp) - s.mp);
+  const uint32_t ep = expfix_rel(scaled(pv, inv_temp), s.mp);
   if (s.q == nullptr) return u192{(uint64_t)ep * s.fp, 0, 0};
-  const uint32_t eq = expfix(scaled(qv, inv_temp) - s.mq);
+  const uint32_t eq = expfix_rel(scaled(qv, inv_temp), s.mq);
   const u192 x = mul128x32(s.gp, ep), y = mul128x32(s.gq, eq);
   return gt192(x, y) ? sub192(x, y) : u192{0, 0, 0};
 }
@@ -599,8 +565,7 @@ __device__ __forceinline__ bool residual_positive(const SampleRow<TT>& s, uint32
 }
 
 // This thread's PER_M consecutive sampling-row entries starting at v0 (p, and q after a
-// rejection), loaded once; entries at or past V read as p = q = -inf (weight 0 is not
-// used for them: callers stop at V).
+// rejection), loaded once; entries at or past V read as p = -inf (callers stop at V).
 struct RunVals {
   float p[PER_M], q[PER_M];
 };
@@ -661,14 +626,14 @@ __device__ __forceinline__ u192 run_mass(const SampleRow<TT>& s, const RunVals& 
   if (s.q == nullptr) {
 #pragma unroll
     for (int j = 0; j < PER_M; ++j)
-      if (v0 + j < V) sp += expfix(scaled(r.p[j], inv_temp) - s.mp);
+      if (v0 + j < V) sp += expfix_rel(scaled(r.p[j], inv_temp), s.mp);
     return mul64x128(sp, (u128)s.fp);
   }
 #pragma unroll
   for (int j = 0; j < PER_M; ++j) {
     if (v0 + j < V) {
-      const uint32_t ep = expfix(scaled(r.p[j], inv_temp) - s.mp);
-      const uint32_t eq = expfix(scaled(r.q[j], inv_temp) - s.mq);
+      const uint32_t ep = expfix_rel(scaled(r.p[j], inv_temp), s.mp);
+      const uint32_t eq = expfix_rel(scaled(r.q[j], inv_temp), s.mq);
       if (residual_positive(s, ep, eq)) {
         sp += ep;
         sq += eq;
@@ -706,6 +671,13 @@ __device__ __forceinline__ u192 shfl_xor_u192(u192 v, int m) {
               ((uint64_t)w[5] << 32) | w[4]};
 }
 
+__device__ __forceinline__ u128 shfl_u128(u128 v, int src_lane) {
+  uint32_t w[4] = {(uint32_t)v, (uint32_t)(v >> 32), (uint32_t)(v >> 64), (uint32_t)(v >> 96)};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) w[k] = __shfl(w[k], src_lane, 64);
+  return ((u128)w[3] << 96) | ((u128)w[2] << 64) | ((u128)w[1] << 32) | w[0];
+}
+
 // Inclusive prefix sum over the 64 lanes of a wave.
 __device__ __forceinline__ u192 wave_incl_scan_u192(u192 v) {
   const int lane = threadIdx.x & 63;
@@ -728,102 +700,68 @@ __device__ u192 block_sum_u192(u192 v, u192* sh) {
   return s;
 }
 
-// ---- decision + residual mass -------------------------------------------------------------
-constexpr int kMaxRowsPerSeq = 2 * 64 + 1;  // 2K+1 rows of a sequence (K <= 64)
-
-__device__ __forceinline__ u128 wave_sum_u128(u128 v) {
-  for (int off = 32; off > 0; off >>= 1) {
-    const uint64_t lo = shfl_xor_u64((uint64_t)v, off);
-    const uint64_t hi = shfl_xor_u64((uint64_t)(v >> 64), off);
-    v += ((u128)hi << 64) | lo;
-  }
-  return v;
-}
-
-// One workgroup per sequence. Its waves take the sequence's 2K+1 rows (target rows j <= K,
-// then draft rows), each row's chunks spread over the lanes: M = max_c m_c,
-// Z = sum_c F_c * S_c with F_c = expfix(m_c - M), and the weight W = E * F_c of the row's
-// draft token; Z and M go to the workspace. Then lane i < K of wave 0 runs the accept test
-// of draft position i (all tests at once; the first failing lane is the rejection), and the
-// decision, the emitted draft ids and the sampling rows' Z and M are recorded.
-__global__ __launch_bounds__(1024) void rej_decide_kernel(RejArgs a) {
-  const int b = blockIdx.x;
-  const int K = a.K, T = K + 1;
-  const int nt = a.B * T;
-  const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = blockDim.x >> 6;
-  __shared__ u128 s_z[kMaxRowsPerSeq];
-  __shared__ float s_m[kMaxRowsPerSeq];
-  __shared__ uint64_t s_w[kMaxRowsPerSeq];
-  for (int j = wv; j < T + K; j += nw) {
-    const int row = j < T ? b * T + j : nt + b * K + (j - T);
-    const float* rm = a.rmax + (size_t)row * a.nch;
-    const uint64_t* rs = a.rsum + (size_t)row * a.nch;
-    float M = -INFINITY;
-    for (int c = lane; c < a.nch; c += 64) M = fmaxf(M, rm[c]);
-    M = npn::wave_max(M);
-    u128 z = 0;
-    for (int c = lane; c < a.nch; c += 64) z += (u128)rs[c] * expfix(rm[c] - M);
-    z = wave_sum_u128(z);
-    if (lane == 0) {
-      const int tok = row_token(a, row);
-      s_z[j] = z;
-      s_m[j] = M;
-      s_w[j] = tok < 0 ? 0 : (uint64_t)a.ex[row] * expfix(rm[tok / CHK] - M);
-      a.zrow[row] = z;
-      a.mrow[row] = M;
-    }
-  }
-  __syncthreads();
-  if (wv != 0) return;
+// The accept decision of sequence b, by wave 0 (lane i < K tests draft position i, all at
+// once; the first failing lane is the rejection), with the sampling rows' maxima and totals.
+// Lane l <= K also loads target row l's M and Z, so the bonus row's are at hand.
+__device__ Decision decide(const RejArgs& a, int b) {
+  const int K = a.K, T = K + 1, nt = a.B * T;
+  const int lane = threadIdx.x & 63;
   bool reject = false;
+  u128 zp = 0, zq = 0;
+  float mp = 0.f, mq = 0.f;
+  if (lane <= K) {
+    const int rp = b * T + lane;
+    zp = a.zrow[rp];
+    mp = a.mrow[rp];
+  }
   if (lane < K) {
+    const int rp = b * T + lane, rq = nt + b * K + lane;
+    const int64_t id = a.draft_ids[(size_t)b * K + lane];
+    zq = a.zrow[rq];
+    mq = a.mrow[rq];
+    const uint64_t wp = a.wtok[rp], wq = a.wtok[rq];
     const uint32_t U = uniform_fix(a.u_accept[(size_t)b * K + lane]);
-    const u192 lhs = mul192x32(mul64x128(s_w[T + lane], s_z[lane]), U);
-    const u192 rhs = shl24_192(mul64x128(s_w[lane], s_z[T + lane]));
-    reject = !draft_id_ok(a.draft_ids[(size_t)b * K + lane], a.V) || gt192(lhs, rhs);
+    const u192 lhs = mul192x32(mul64x128(wq, zp), U);
+    const u192 rhs = shl24_192(mul64x128(wp, zq));
+    reject = !draft_id_ok(id, a.V) || gt192(lhs, rhs);
   }
   const uint64_t rej = __builtin_amdgcn_ballot_w64(reject);
-  const int acc = rej ? __builtin_ctzll(rej) : K;
-  if (lane == 0) {
-    a.accepted[b] = acc;
-    a.dec_row[b] = acc;
-    a.dec_z[2 * b] = s_z[acc];
-    a.dec_z[2 * b + 1] = acc < K ? s_z[T + acc] : 0;
-    a.dec_m[2 * b] = s_m[acc];  // maxima of the sampling rows
-    a.dec_m[2 * b + 1] = acc < K ? s_m[T + acc] : 0.f;
+  Decision d;
+  d.acc = rej ? __builtin_ctzll(rej) : K;
+  if (d.acc < 64) {
+    d.zp = shfl_u128(zp, d.acc);
+    d.mp = __shfl(mp, d.acc, 64);
+  } else {  // the bonus row of K = 64 has no lane
+    d.zp = a.zrow[b * T + K];
+    d.mp = a.mrow[b * T + K];
   }
-  for (int t = lane; t < T; t += 64) {
-    if (t < acc) a.out_ids[(size_t)b * T + t] = a.draft_ids[(size_t)b * K + t];
-    else if (t > acc) a.out_ids[(size_t)b * T + t] = -1;
+  if (d.acc < K) {
+    d.zq = shfl_u128(zq, d.acc);
+    d.mq = __shfl(mq, d.acc, 64);
+  } else {
+    d.zq = 0;
+    d.mq = 0.f;
   }
+  return d;
 }
 
-// Residual (or bonus) mass of sequence b's MCHK chunk c.
+// Sampling: block (c, b) re-derives sequence b's decision (wave 0, then shared), adds the
+// residual (or bonus) mass of entries [2048 c, 2048 c + 2048) -- each thread a run of 8 inside
+// one contract chunk -- and publishes it. The last block of the sequence to finish (a counter
+// cleared by the row-totals kernel, bumped after a device-scope fence) then runs the inverse
+// CDF: wave 0 finds the 2048-entry block whose inclusive mass crosses the target (64 blocks per
+// scan window, carry between windows); each thread sums its run of that block (values held in
+// registers), a block-wide exclusive scan of the runs gives every thread its starting prefix,
+// and the thread whose run crosses reports the first crossing entry (atomicMin over the block).
+// The same block writes the sequence's outputs.
 template <typename TT>
-__global__ __launch_bounds__(THREADS) void rej_mass_kernel(RejArgs a) {
-  const int b = blockIdx.y, c = blockIdx.x;
-  const int acc = a.dec_row[b];
-  const SampleRow<TT> s = sample_row<TT>(a, b, acc, a.dec_m[2 * b], a.dec_m[2 * b + 1],
-                                         a.dec_z[2 * b], a.dec_z[2 * b + 1], (c * MCHK) / CHK);
-  const int v0 = c * MCHK + (int)threadIdx.x * PER_M;
-  u192 m{0, 0, 0};
-  if (v0 < a.V) m = run_mass(s, load_run(a, s, v0), v0, a.V, a.inv_temp);
-  __shared__ u192 sh[THREADS / 64];
-  m = block_sum_u192(m, sh);
-  if (threadIdx.x == 0) a.cmass[(size_t)b * a.nchm + c] = m;
-}
-
-// Inverse CDF: the smallest v with 2^24 * C_v > U_s * S (C_v the inclusive prefix of the
-// sampling weights, S their total). Wave 0 finds the MCHK chunk whose inclusive mass
-// crosses the target (64 chunks per scan window, carry between windows); then each thread
-// sums its run of PER_M consecutive entries of that chunk (values held in registers), a
-// block-wide exclusive scan of the runs gives every thread its starting prefix, and the
-// thread whose run crosses reports the first crossing entry (atomicMin over the block).
-template <typename TT>
-__global__ __launch_bounds__(THREADS) void rej_pick_kernel(RejArgs a) {
-  const int b = blockIdx.x;
+__global__ __launch_bounds__(THREADS) void rej_sample_kernel(RejArgs a) {
+  const int b = (int)blockIdx.y, c = (int)blockIdx.x;
   const int K = a.K, T = K + 1;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  __shared__ Decision s_dec;
+  __shared__ u192 sh[THREADS / 64];
+  __shared__ int s_last;
   __shared__ int s_chunk;
   __shared__ u192 s_before;
   __shared__ u192 s_target;
@@ -831,15 +769,33 @@ __global__ __launch_bounds__(THREADS) void rej_pick_kernel(RejArgs a) {
   __shared__ int s_tok;
   __shared__ int s_empty;
   __shared__ ArgPart s_best[THREADS / 64];
+  if (w == 0) {
+    const Decision d = decide(a, b);
+    if (lane == 0) s_dec = d;
+  }
+  __syncthreads();
+  const Decision d = s_dec;
+  {
+    const int v0 = c * MCHK + (int)threadIdx.x * PER_M;
+    u192 m{0, 0, 0};
+    if (v0 < a.V) {
+      const SampleRow<TT> s = sample_row<TT>(a, b, d, v0 / CC);
+      m = run_mass(s, load_run(a, s, v0), v0, a.V, a.inv_temp);
+    }
+    m = block_sum_u192(m, sh);
+    if (threadIdx.x == 0) {
+      a.cmass[(size_t)b * a.nchm + c] = m;
+      __threadfence();  // the mass is visible device-wide before the count says so
+      s_last = atomicAdd(&a.cnt[b], 1u) == (unsigned)(a.nchm - 1);
+    }
+    __syncthreads();
+  }
+  if (!s_last) return;
+  __threadfence();  // every other block's mass, published before its count, is visible
   const u192* cm = a.cmass + (size_t)b * a.nchm;
-  // The sampling row's decision values do not depend on the chunk: their loads are issued
-  // before the chunk search, so they are in registers when it ends.
-  const int acc = a.dec_row[b];
-  const float dmp = a.dec_m[2 * b], dmq = a.dec_m[2 * b + 1];
-  const u128 dzp = a.dec_z[2 * b], dzq = a.dec_z[2 * b + 1];
   if (w == 0) {
     u192 tot{0, 0, 0};
-    for (int c = lane; c < a.nchm; c += 64) tot = add192(tot, cm[c]);
+    for (int k = lane; k < a.nchm; k += 64) tot = add192(tot, cm[k]);
     tot = wave_incl_scan_u192(tot);
     tot = shfl_u192(tot, 63);
     if (lane == 0) s_empty = is_zero192(tot);
@@ -849,11 +805,11 @@ __global__ __launch_bounds__(THREADS) void rej_pick_kernel(RejArgs a) {
     u192 before{0, 0, 0};
     bool found = false;
     for (int c0 = 0; c0 < a.nchm && !found; c0 += 64) {
-      const int c = c0 + lane;
-      const u192 m = c < a.nchm ? cm[c] : u192{0, 0, 0};
+      const int k = c0 + lane;
+      const u192 m = k < a.nchm ? cm[k] : u192{0, 0, 0};
       const u192 incl = add192(wave_incl_scan_u192(m), carry);
       const uint64_t hit =
-          __builtin_amdgcn_ballot_w64(c < a.nchm && gt192(shl24_192(incl), target));
+          __builtin_amdgcn_ballot_w64(k < a.nchm && gt192(shl24_192(incl), target));
       if (hit != 0) {
         const int l = __builtin_ctzll(hit);
         chunk = c0 + l;
@@ -873,10 +829,13 @@ __global__ __launch_bounds__(THREADS) void rej_pick_kernel(RejArgs a) {
     }
   }
   __syncthreads();
+  const int acc = d.acc;
+  int tok;
   if (s_empty) {
     // No sampling mass: every weight of the sampling row is 0, which happens only for a
-    // bonus row whose logits are all NaN or -inf or include +inf (a residual after a
-    // rejection always has mass). The token is then the row's greedy choice: its argmax,
+    // bonus row whose logits are all NaN or -inf or include +inf, or for the residual after
+    // an out-of-range draft id where Wp Zq == Wq Zp everywhere (a residual after a failed
+    // test always has mass). The token is then the target row's greedy choice: its argmax,
     // NaN counting as the maximum and ties going to the lowest index (the order of
     // argmax_chunk_kernel).
     const TT* p = target_row<TT>(a, b * T + acc);
@@ -893,53 +852,60 @@ __global__ __launch_bounds__(THREADS) void rej_pick_kernel(RejArgs a) {
     }
     if (lane == 0) s_best[w] = ArgPart{bv, bi};
     __syncthreads();
-    if (threadIdx.x == 0) {
-      ArgPart best = s_best[0];
-      for (int k = 1; k < THREADS / 64; ++k)
-        if (beats(s_best[k].v, s_best[k].i, best.v, best.i)) best = s_best[k];
-      a.out_ids[(size_t)b * T + acc] = best.i;
+    ArgPart best = s_best[0];
+    for (int k = 1; k < THREADS / 64; ++k)
+      if (beats(s_best[k].v, s_best[k].i, best.v, best.i)) best = s_best[k];
+    tok = best.i;
+  } else {
+    const int chunk = s_chunk;
+    const int v0 = chunk * MCHK + (int)threadIdx.x * PER_M;
+    RunVals rv;
+    u192 run{0, 0, 0};
+    SampleRow<TT> s;
+    if (v0 < a.V) {
+      s = sample_row<TT>(a, b, d, v0 / CC);
+      rv = load_run(a, s, v0);
+      run = run_mass(s, rv, v0, a.V, a.inv_temp);
     }
-    return;
-  }
-  const int chunk = s_chunk;
-  const SampleRow<TT> s = sample_row<TT>(a, b, acc, dmp, dmq, dzp, dzq, (chunk * MCHK) / CHK);
-  const int v0 = chunk * MCHK + (int)threadIdx.x * PER_M;
-  RunVals rv;
-  u192 run{0, 0, 0};
-  if (v0 < a.V) {
-    rv = load_run(a, s, v0);
-    run = run_mass(s, rv, v0, a.V, a.inv_temp);
-  }
-  const u192 incl = wave_incl_scan_u192(run);
-  if (lane == 63) s_wtot[w] = incl;
-  __syncthreads();
-  u192 c = add192(s_before, sub192(incl, run));
-  for (int k = 0; k < w; ++k) c = add192(c, s_wtot[k]);
-  const u192 target = s_target;
-  if (v0 < a.V && gt192(shl24_192(add192(c, run)), target)) {  // the crossing is in this run
+    const u192 incl = wave_incl_scan_u192(run);
+    if (lane == 63) s_wtot[w] = incl;
+    __syncthreads();
+    u192 cpre = add192(s_before, sub192(incl, run));
+    for (int k = 0; k < w; ++k) cpre = add192(cpre, s_wtot[k]);
+    const u192 target = s_target;
+    if (v0 < a.V && gt192(shl24_192(add192(cpre, run)), target)) {  // crossing in this run
 #pragma unroll
-    for (int j = 0; j < PER_M; ++j) {
-      const int v = v0 + j;
-      if (v >= a.V) break;
-      const u192 wv = weight_of(s, rv.p[j], rv.q[j], a.inv_temp);
-      c = add192(c, wv);
-      if (!is_zero192(wv) && gt192(shl24_192(c), target)) {
-        atomicMin(&s_tok, v);
-        break;
+      for (int j = 0; j < PER_M; ++j) {
+        const int v = v0 + j;
+        if (v >= a.V) break;
+        const u192 wv = weight_of(s, rv.p[j], rv.q[j], a.inv_temp);
+        cpre = add192(cpre, wv);
+        if (!is_zero192(wv) && gt192(shl24_192(cpre), target)) {
+          atomicMin(&s_tok, v);
+          break;
+        }
       }
     }
+    __syncthreads();
+    tok = s_tok;
   }
-  __syncthreads();
-  if (threadIdx.x == 0) a.out_ids[(size_t)b * T + acc] = s_tok;
+  if (threadIdx.x == 0) a.accepted[b] = acc;
+  for (int t = (int)threadIdx.x; t < T; t += THREADS) {
+    int64_t id = -1;
+    if (t < acc) id = a.draft_ids[(size_t)b * K + t];
+    else if (t == acc) id = tok;
+    a.out_ids[(size_t)b * T + t] = id;
+  }
 }
 
-// The per-row Z sums come first and the row maxima second: the header documents both as
-// results that the rejection call leaves in the workspace.
+// Workspace of the acceptance calls. The per-row Z sums come first and the row maxima second:
+// the header documents both as results that the rejection call leaves in the workspace.
 struct WsLayout {
-  size_t zrow, mrow, ex, rmax, rsum, dec_row, dec_z, dec_m, cmass, total;
+  size_t zrow, mrow, wtok, cmax, csum, cmass, cnt, total;
 };
 
 WsLayout layout(int B, int K, int V) {
+  const int nc = (V + CC - 1) / CC;
   const int nch = (V + CHK - 1) / CHK;
   const size_t rows = (size_t)B * (2 * K + 1);
   auto up = [](size_t x) { return (x + 255) & ~size_t(255); };
@@ -947,16 +913,14 @@ WsLayout layout(int B, int K, int V) {
   size_t o = 0;
   l.zrow = o; o += up(rows * sizeof(u128));
   l.mrow = o; o += up(rows * sizeof(float));
-  l.ex = o; o += up(rows * sizeof(uint32_t));
+  l.wtok = o; o += up(rows * sizeof(uint64_t));
   // chunk maxima; the greedy path's argmax partials share the region
-  l.rmax = o; o += up(rows * nch * sizeof(float) > (size_t)B * (K + 1) * nch * sizeof(ArgPart)
-                          ? rows * nch * sizeof(float)
-                          : (size_t)B * (K + 1) * nch * sizeof(ArgPart));
-  l.rsum = o; o += up(rows * nch * sizeof(uint64_t));
-  l.dec_row = o; o += up((size_t)B * sizeof(int32_t));
-  l.dec_z = o; o += up((size_t)B * 2 * sizeof(u128));
-  l.dec_m = o; o += up((size_t)B * 2 * sizeof(float));
+  const size_t cmax_bytes = rows * nc * sizeof(float);
+  const size_t part_bytes = (size_t)B * (K + 1) * nch * sizeof(ArgPart);
+  l.cmax = o; o += up(cmax_bytes > part_bytes ? cmax_bytes : part_bytes);
+  l.csum = o; o += up(rows * nc * sizeof(uint64_t));
   l.cmass = o; o += up((size_t)B * ((V + MCHK - 1) / MCHK) * sizeof(u192));
+  l.cnt = o; o += up((size_t)B * sizeof(uint32_t));
   l.total = o;
   return l;
 }
@@ -982,7 +946,7 @@ extern "C" int npn_accept_greedy(const float* target_logits, const int64_t* draf
   NPN_REQUIRE(NPN_ALIGNED16(workspace), NPN_ERR_ALIGN);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int nch = (V + CHK - 1) / CHK;
-  ArgPart* part = reinterpret_cast<ArgPart*>(static_cast<uint8_t*>(workspace) + l.rmax);
+  ArgPart* part = reinterpret_cast<ArgPart*>(static_cast<uint8_t*>(workspace) + l.cmax);
   const bool vec4 = V % 4 == 0 && NPN_ALIGNED16(target_logits);
   hipLaunchKernelGGL(argmax_chunk_kernel, dim3(nch, B * (K + 1)), dim3(THREADS), 0, s,
                      target_logits, part, V, nch, vec4);
@@ -994,7 +958,7 @@ extern "C" int npn_accept_greedy(const float* target_logits, const int64_t* draf
 namespace {
 
 // Argument checks shared by the rejection entry points (everything but the workspace).
-int rejection_args_ok(const float* target_logits, const float* draft_logits,
+int rejection_args_ok(const void* target_logits, const float* draft_logits,
                       const int64_t* draft_ids, const float* u_accept, const float* u_sample,
                       float inv_temperature, const int32_t* accepted, const int64_t* out_ids,
                       int B, int K, int V) {
@@ -1002,52 +966,66 @@ int rejection_args_ok(const float* target_logits, const float* draft_logits,
                   out_ids,
               NPN_ERR_NULL);
   NPN_REQUIRE(shape_ok(B, K, V), NPN_ERR_SHAPE);
-  // Z < 2^80 and every residual sum below 2^162 for V <= 2^20, so the contract's products
-  // stay below 2^192
+  // Z <= V 2^62 <= 2^82 and every residual sum at most 2^164 for V <= 2^20, so the
+  // contract's products stay below 2^192
   NPN_REQUIRE(V <= kRejMaxV, NPN_ERR_SHAPE);
   NPN_REQUIRE(inv_temperature > 0.0f && inv_temperature < 1e30f, NPN_ERR_VALUE);
   return NPN_OK;
 }
 
-// The four rejection kernels on `stream` (one logit pass, row totals + decision, residual
-// mass, pick),
-// with the workspace at `ws` (layout(B, K, V).total bytes, 16-byte aligned, checked by the
-// caller). TT is the target rows' element type: float, or bf16 bits (uint16_t) for the
-// LM-head form.
+RejArgs rej_args(const void* target_logits, const float* draft_logits, const int64_t* draft_ids,
+                 const float* u_accept, const float* u_sample, float inv_temperature,
+                 int32_t* accepted, int64_t* out_ids, int B, int K, int V, bool bf16_target,
+                 uint8_t* ws) {
+  const WsLayout l = layout(B, K, V);
+  // 16-byte pieces of whole rows: V % 8 for bf16 target rows (and V % 4 for the fp32 ones)
+  const bool vec4 = V % (bf16_target ? 8 : 4) == 0 && NPN_ALIGNED16(target_logits) &&
+                    NPN_ALIGNED16(draft_logits);
+  return RejArgs{target_logits, draft_logits, draft_ids, u_accept, u_sample, inv_temperature,
+                 accepted, out_ids, B, K, V, (V + CC - 1) / CC, (V + MCHK - 1) / MCHK, vec4,
+                 reinterpret_cast<u128*>(ws + l.zrow), reinterpret_cast<float*>(ws + l.mrow),
+                 reinterpret_cast<uint64_t*>(ws + l.wtok), reinterpret_cast<float*>(ws + l.cmax),
+                 reinterpret_cast<uint64_t*>(ws + l.csum), reinterpret_cast<u192*>(ws + l.cmass),
+                 reinterpret_cast<uint32_t*>(ws + l.cnt)};
+}
+
+// Chunk statistics of `rows` fp32 rows starting at row0.
+void launch_stats(const RejArgs& a, int row0, int rows, hipStream_t s) {
+  const dim3 grid((a.V + SBLK - 1) / SBLK, rows);
+  if (a.inv_temp == 1.0f)
+    hipLaunchKernelGGL(rej_stats_kernel<true>, grid, dim3(THREADS), 0, s, a, row0);
+  else
+    hipLaunchKernelGGL(rej_stats_kernel<false>, grid, dim3(THREADS), 0, s, a, row0);
+}
+
+// Row totals and sampling (every row's chunk statistics in place). TT is the target rows'
+// element type: float, or bf16 bits (uint16_t) for the LM-head form.
 template <typename TT>
-int rejection_launch(const TT* target_logits, const float* draft_logits,
+int launch_decide_sample(const RejArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL(rej_rowtotal_kernel<TT>, dim3(a.B * (2 * a.K + 1)), dim3(THREADS), 0, s, a);
+  hipLaunchKernelGGL(rej_sample_kernel<TT>, dim3(a.nchm, a.B), dim3(THREADS), 0, s, a);
+  return npn_launch_status();
+}
+
+// The three rejection kernels over fp32 logits on `stream`, with the workspace at `ws`
+// (layout(B, K, V).total bytes, 16-byte aligned, checked by the caller).
+int rejection_launch(const float* target_logits, const float* draft_logits,
                      const int64_t* draft_ids, const float* u_accept, const float* u_sample,
                      float inv_temperature, int32_t* accepted, int64_t* out_ids, int B, int K,
                      int V, uint8_t* ws, hipStream_t s) {
-  const WsLayout l = layout(B, K, V);
-  const int nch = (V + CHK - 1) / CHK;
-  // 16-byte pieces of whole rows: V % 8 for bf16 target rows (and V % 4 for the fp32 ones)
-  const bool vec4 = V % (sizeof(TT) == 2 ? 8 : 4) == 0 && NPN_ALIGNED16(target_logits) &&
-                    NPN_ALIGNED16(draft_logits);
-  RejArgs a{target_logits, draft_logits, draft_ids, u_accept, u_sample, inv_temperature,
-            accepted, out_ids, B, K, V, nch, (V + MCHK - 1) / MCHK, vec4,
-            reinterpret_cast<u128*>(ws + l.zrow), reinterpret_cast<float*>(ws + l.mrow),
-            reinterpret_cast<uint32_t*>(ws + l.ex), reinterpret_cast<float*>(ws + l.rmax),
-            reinterpret_cast<uint64_t*>(ws + l.rsum), reinterpret_cast<int32_t*>(ws + l.dec_row),
-            reinterpret_cast<u128*>(ws + l.dec_z), reinterpret_cast<float*>(ws + l.dec_m),
-            reinterpret_cast<u192*>(ws + l.cmass)};
-  const int rows = B * (2 * K + 1);
-  if (inv_temperature == 1.0f)
-    hipLaunchKernelGGL((rej_scan_kernel<true, TT>), dim3(nch, rows), dim3(THREADS), 0, s, a);
-  else
-    hipLaunchKernelGGL((rej_scan_kernel<false, TT>), dim3(nch, rows), dim3(THREADS), 0, s, a);
-  const int dthreads = 64 * (2 * K + 1 < 16 ? 2 * K + 1 : 16);
-  hipLaunchKernelGGL(rej_decide_kernel, dim3(B), dim3(dthreads), 0, s, a);
-  hipLaunchKernelGGL(rej_mass_kernel<TT>, dim3(a.nchm, B), dim3(THREADS), 0, s, a);
-  hipLaunchKernelGGL(rej_pick_kernel<TT>, dim3(B), dim3(THREADS), 0, s, a);
-  return npn_launch_status();
+  const RejArgs a = rej_args(target_logits, draft_logits, draft_ids, u_accept, u_sample,
+                             inv_temperature, accepted, out_ids, B, K, V, false, ws);
+  launch_stats(a, 0, B * (2 * K + 1), s);
+  return launch_decide_sample<float>(a, s);
 }
 
 // ---- no-allocation variant -------------------------------------------------------------------
 // The workspace of npn_accept_rejection_noalloc: a fixed device array. Each GPU holds its own
 // copy, at its own address, for the life of the process. In host code `scratch` names a host
 // stand-in, not device memory: kernels get the address hipGetSymbolAddress returns for the
-// device they run on (scratch_on_device), never the array's name.
+// device they run on (scratch_on_device), never the array's name. Nothing in it needs clearing
+// between calls: every word a call reads was written earlier in the same call (the counters of
+// the sampling kernel are cleared by the row-totals kernel before it).
 constexpr size_t kScratchBytes = (size_t)NPN_ACCEPT_SCRATCH_BYTES;
 __device__ __align__(256) uint8_t scratch[kScratchBytes];
 
@@ -1131,26 +1109,22 @@ extern "C" int npn_argmax_parts(const void* parts, int nparts, int64_t* ids, flo
                                 int M, void* stream) {
   NPN_REQUIRE(parts && ids, NPN_ERR_NULL);
   NPN_REQUIRE(M >= 1 && nparts >= 1, NPN_ERR_SHAPE);
-  hipLaunchKernelGGL(argmax_parts_kernel, dim3((M + 3) / 4), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), static_cast<const ArgPart*>(parts), nparts,
-                     ids, values, M);
+  hipLaunchKernelGGL(argmax_parts_kernel, dim3((M + 3) / 4), dim3(256),
+                     0, static_cast<hipStream_t>(stream), static_cast<const ArgPart*>(parts),
+                     nparts, ids, values, M);
   return npn_launch_status();
 }
 
 // ---- rejection sampling straight from the LM head --------------------------------------------
-// The LM head's GEMM writes the target logits in bf16; the rejection pass then reads the
-// target rows in bf16 (half the bytes). The decisions equal npn_accept_rejection's on the
-// same logits cast to fp32 (every step of the contract sees the same values).
-namespace {
-
-size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
-
-}  // namespace
-
+// The LM head's GEMM writes the target logits in bf16 and, in its epilogue, the contract's
+// chunk statistics of every target row, so the target rows are never read back in full: the
+// statistics pass covers only the draft rows, and the sampling kernel re-reads only each
+// sequence's sampling row. The decisions equal npn_accept_rejection's on the same logits cast
+// to fp32 (every step of the contract sees the same values).
 extern "C" size_t npn_accept_rejection_lm_head_workspace_size(int B, int K, int H, int V) {
   if (!shape_ok(B, K, V) || V > kRejMaxV) return 0;
-  if (npn_fp8_matmul_argmax_groups(B * (K + 1), H, V) <= 0) return 0;  // GEMM shape rules
-  return align256(layout(B, K, V).total) + npn_fp8_matmul_workspace_size(B * (K + 1), H, V);
+  if (!npn::fp8_matmul_chunk_stats_ok(B * (K + 1), H, V)) return 0;  // GEMM shape rules
+  return layout(B, K, V).total;
 }
 
 extern "C" int npn_accept_rejection_lm_head(const uint16_t* hidden, const int8_t* lm_head_w,
@@ -1162,21 +1136,23 @@ extern "C" int npn_accept_rejection_lm_head(const uint16_t* hidden, const int8_t
                                             int H, int V, void* workspace,
                                             size_t workspace_bytes, void* stream) {
   NPN_REQUIRE(hidden && lm_head_w && lm_head_scale, NPN_ERR_NULL);
-  const int st = rejection_args_ok(reinterpret_cast<const float*>(target_logits), draft_logits,
-                                   draft_ids, u_accept, u_sample, inv_temperature, accepted,
-                                   out_ids, B, K, V);
+  const int st = rejection_args_ok(target_logits, draft_logits, draft_ids, u_accept, u_sample,
+                                   inv_temperature, accepted, out_ids, B, K, V);
   if (st != NPN_OK) return st;
-  const int M = B * (K + 1);
+  const int T = K + 1, M = B * T;
   const size_t need = npn_accept_rejection_lm_head_workspace_size(B, K, H, V);
   NPN_REQUIRE(need > 0, NPN_ERR_SHAPE);
   NPN_REQUIRE(workspace != nullptr && workspace_bytes >= need, NPN_ERR_WORKSPACE);
   NPN_REQUIRE(NPN_ALIGNED16(workspace), NPN_ERR_ALIGN);
-  uint8_t* ws = static_cast<uint8_t*>(workspace);
-  const size_t gemm_off = align256(layout(B, K, V).total);
-  const int gst = npn_fp8_matmul(hidden, lm_head_w, lm_head_scale, target_logits, M, H, V,
-                                 ws + gemm_off, need - gemm_off, stream);
+  NPN_REQUIRE(NPN_ALIGNED16(hidden) && NPN_ALIGNED16(lm_head_w) && NPN_ALIGNED16(target_logits),
+              NPN_ERR_ALIGN);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const RejArgs a = rej_args(target_logits, draft_logits, draft_ids, u_accept, u_sample,
+                             inv_temperature, accepted, out_ids, B, K, V, true,
+                             static_cast<uint8_t*>(workspace));
+  launch_stats(a, M, B * K, s);  // draft rows
+  const int gst = npn::fp8_matmul_chunk_stats(hidden, lm_head_w, lm_head_scale, target_logits,
+                                              a.cmax, a.csum, inv_temperature, M, H, V, s);
   if (gst != NPN_OK) return gst;
-  return rejection_launch(static_cast<const uint16_t*>(target_logits), draft_logits, draft_ids,
-                          u_accept, u_sample, inv_temperature, accepted, out_ids, B, K, V, ws,
-                          static_cast<hipStream_t>(stream));
+  return launch_decide_sample<uint16_t>(a, s);
 }

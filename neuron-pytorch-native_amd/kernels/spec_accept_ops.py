@@ -138,8 +138,9 @@ def accept_rejection_lm_head(hidden: torch.Tensor, lm_head_w: torch.Tensor,
     """New op: rejection sampling with the target logits made by the LM head in the same
     call: hidden [B*(K+1), H] bf16 (row b*(K+1) + t), lm_head_w [H, V] e4m3fn bytes,
     lm_head_scale [V] f32 -> (accepted [B] int32, out_ids [B, K+1] int64, target_logits
-    [B, K+1, V] bf16). The sampling pass reads the target rows once, in bf16. Equal, bit for
-    bit, to accept_rejection(fp8::matmul(hidden, w, scale).float().view(B, K+1, V), ...)."""
+    [B, K+1, V] bf16). The GEMM's epilogue produces the target rows' chunk statistics, so
+    only each sequence's sampling row is read back. Equal, bit for bit, to
+    accept_rejection(fp8::matmul(hidden, w, scale).float().view(B, K+1, V), ...)."""
     B, K, V = draft_logits.shape
     T = K + 1
     require(hidden, "hidden", torch.bfloat16)

@@ -22,8 +22,10 @@ and q(x) > 0 = p(x) (always reject, residual = p restricted to p > q)
 Integer softmax contract (shared bit-for-bit with ``csrc/spec_accept.hip``), built so
 that one pass over the logits gives every sum (each vocabulary chunk's values are
 referred to the chunk's own maximum, and chunks to the row maximum by exact factors):
-- s_v = t_v * inv_temp (fp32 multiply). The vocabulary is cut into chunks of CHUNK = 8192
-  entries; m_c = max of the non-NaN s_v of chunk c (-inf if none), M = max_c m_c.
+- s_v = t_v * inv_temp (fp32 multiply). The vocabulary is cut into chunks of CHUNK = 64
+  entries; m_c = max of the non-NaN s_v of chunk c (-inf if none), M = max_c m_c. (64
+  divides every column group of the LM-head GEMM, whose epilogue produces m_c and S_c of
+  the target rows while their logits are still in registers.)
 - E_v = floor(2^31 * exp_c(s_v - m_c)) for v in chunk c (fp32 subtraction; NaN gives 0),
   F_c = floor(2^31 * exp_c(m_c - M)), both below 2^31 + 1, with exp_c the fp32
   Cody-Waite reduction + degree-7 Taylor polynomial below, evaluated with correctly
@@ -31,15 +33,15 @@ referred to the chunk's own maximum, and chunks to the row maximum by exact fact
   IEEE-754 operation that CPU and GPU round identically.
 - The weight of v is W_v = E_v * F_c (an integer below 2^62 + 1) and the row's total is
   Z = sum_v W_v = sum_c F_c * S_c with S_c = sum_{v in c} E_v, in exact integers
-  (order-independent; Z < 2^80 for V <= 2^20). W_v / Z approximates softmax(s)_v to about
-  2^-30 relative for every entry within 21 of its chunk maximum whose chunk maximum is
-  within 21 of M.
+  (order-independent; Z <= V * 2^62 <= 2^82 for V <= 2^20). W_v / Z approximates
+  softmax(s)_v to about 2^-30 relative for every entry within 21 of its chunk maximum
+  whose chunk maximum is within 21 of M.
 - p(v) = W^p_v / Z_p, q(v) = W^q_v / Z_q. Uniforms u are read as U = floor(u * 2^24).
 - Accept draft x at position i iff U * W^q_x * Z_p <= 2^24 * W^p_x * Z_q
-  (integers below 2^166).
+  (integers below 2^169).
 - At the first rejection sample from R_v = max(0, W^p_v Z_q - W^q_v Z_p); if all
   K drafts are accepted sample the bonus from R_v = W^p_v of row K. The token is
-  the smallest v with 2^24 * sum_{w<=v} R_w > U_s * sum_w R_w (integers below 2^184).
+  the smallest v with 2^24 * sum_{w<=v} R_w > U_s * sum_w R_w (integers below 2^189).
 - Draft ids outside [0, V) are never accepted: such a position is a rejection whatever the
   uniform, and its token is sampled from the residual R as for any rejection (greedy
   acceptance rejects them too, since an argmax is always in range). Emitted ids therefore
@@ -115,7 +117,7 @@ def expfix(x):
     return bits.view(np.float32).astype(np.uint32)
 
 
-CHUNK = 8192                                     # vocabulary entries per chunk
+CHUNK = 64                                       # vocabulary entries per chunk
 
 
 def row_chunks(logits_row, inv_temp=1.0):
@@ -123,15 +125,14 @@ def row_chunks(logits_row, inv_temp=1.0):
     s = (np.asarray(logits_row, np.float32) * _F(inv_temp)).astype(np.float32)
     V = s.shape[0]
     nch = (V + CHUNK - 1) // CHUNK
-    m = np.empty(nch, np.float32)
-    E = np.empty(V, np.uint32)
-    S = []
-    for c in range(nch):
-        seg = s[c * CHUNK:(c + 1) * CHUNK]
-        m[c] = np.fmax.reduce(seg, initial=_F(-np.inf))   # NaN entries are ignored
-        E[c * CHUNK:(c + 1) * CHUNK] = expfix((seg - m[c]).astype(np.float32))
-        S.append(int(E[c * CHUNK:(c + 1) * CHUNK].sum(dtype=np.uint64)))
-    return s, m, S, E
+    seg = np.full(nch * CHUNK, np.nan, np.float32)     # a partial last chunk padded with NaN
+    seg[:V] = s
+    seg = seg.reshape(nch, CHUNK)
+    m = np.fmax.reduce(seg, axis=1, initial=_F(-np.inf)).astype(np.float32)  # NaN ignored
+    with np.errstate(invalid="ignore"):                # -inf - -inf and NaN entries: E = 0
+        E = expfix((seg - m[:, None]).astype(np.float32))
+    S = E.sum(axis=1, dtype=np.uint64).tolist()        # each below 64 * 2^31 + 1
+    return s, m, S, E.reshape(-1)[:V]
 
 
 def row_weights(logits_row, inv_temp=1.0):
@@ -139,7 +140,8 @@ def row_weights(logits_row, inv_temp=1.0):
     W_v = E_v * F_c (below 2^62 + 1, exact in uint64), Z = sum_c F_c * S_c, M the row max."""
     _, m, S, E = row_chunks(logits_row, inv_temp)
     M = np.fmax.reduce(m, initial=_F(-np.inf))
-    F = expfix((m - M).astype(np.float32))
+    with np.errstate(invalid="ignore"):
+        F = expfix((m - M).astype(np.float32))
     Z = sum(int(f) * sc for f, sc in zip(F.tolist(), S))
     W = E.astype(np.uint64) * np.repeat(F.astype(np.uint64), CHUNK)[:E.shape[0]]
     return W, Z, M

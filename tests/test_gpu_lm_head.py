@@ -16,7 +16,10 @@ Bars:
     rows made ±inf and NaN by an infinite activation;
   - accept_rejection_lm_head == accept_rejection over the fp32 cast of the same logits,
     bit-exact (accepted lengths, ids and the logits it returns), at the 27B verify batch
-    (M = 256, wide kernel) and a small one (M = 64, narrow kernel), temperature 1 and 1/0.7.
+    (M = 256, wide kernel) and a small one (M = 64, narrow kernel), temperature 1 and 1/0.7;
+  - the contract statistics its GEMM epilogue produces: every row's Z and M (left in the
+    workspace) bit-identical to accept_rejection's and to the oracle's row_weights, through
+    both GEMM kernels (M = 256 wide, M = 32 narrow), with +-inf and NaN logits in some rows.
 """
 import numpy as np
 import pytest
@@ -151,3 +154,58 @@ def test_accept_rejection_lm_head(ops, B, V, inv_t):
     assert torch.equal(acc_f, acc_r), (acc_f.tolist(), acc_r.tolist())
     assert torch.equal(ids_f, ids_r)
     assert 0 < acc_f.float().mean() < K  # neither all accepted nor all rejected
+
+
+def _zm(ws, R):
+    """Every row's Z (unsigned 128-bit, low word first) and M from a rejection workspace."""
+    off = (16 * R + 255) // 256 * 256
+    zw = ws[:16 * R].cpu().numpy().view(np.uint64).reshape(R, 2)
+    z = [int(lo) | (int(hi) << 64) for lo, hi in zw]
+    m = ws[off:off + 4 * R].cpu().numpy().view(np.float32)
+    return z, m
+
+
+@pytest.mark.parametrize("B,V,inv_t", [(32, 248320, 1.0), (4, 151936, 1.0 / 0.7)])
+def test_lm_head_chunk_stats_bit_exact(ops, B, V, inv_t):
+    from oracle import accept as oa
+    from npn_native import call, query, stream_of
+    K, H = 7, 1024
+    T = K + 1
+    g = torch.Generator(device="cuda").manual_seed(B * 3 + V)
+    hid = torch.randn(B * T, H, generator=g, device="cuda").to(torch.bfloat16)
+    hid[1, 5] = float("inf")                     # rows of +-inf and NaN logits
+    hid[T + 2, 7] = float("nan")
+    w, sc = _gpu_weights(H, V, B + 5)
+    logits = ops.fp8.matmul(hid, w, sc).float().view(B, T, V).contiguous()
+    draft = (0.8 * logits[:, :K].nan_to_num(0.0, 50.0, -50.0)
+             + 0.6 * torch.randn(B, K, V, generator=g, device="cuda")).contiguous()
+    ids = torch.randint(0, V, (B, K), generator=g, device="cuda")
+    u = torch.rand(B, K, generator=g, device="cuda")
+    us = torch.rand(B, generator=g, device="cuda")
+    R = B * (2 * K + 1)
+    st = stream_of(hid)
+    n_lm = query("npn_accept_rejection_lm_head_workspace_size", B, K, H, V)
+    n_pl = query("npn_accept_workspace_size", B, K, V)
+    ws_lm = torch.empty(n_lm, dtype=torch.uint8, device="cuda")
+    ws_pl = torch.empty(n_pl, dtype=torch.uint8, device="cuda")
+    lg = torch.empty((B, T, V), dtype=torch.bfloat16, device="cuda")
+    acc = [torch.empty(B, dtype=torch.int32, device="cuda") for _ in range(2)]
+    out = [torch.empty((B, T), dtype=torch.int64, device="cuda") for _ in range(2)]
+    call("npn_accept_rejection_lm_head", hid, w, sc, draft, ids, u, us, float(inv_t), lg,
+         acc[0], out[0], B, K, H, V, ws_lm, n_lm, st)
+    call("npn_accept_rejection", logits, draft, ids, u, us, float(inv_t), acc[1], out[1],
+         B, K, V, ws_pl, n_pl, st)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(lg.float(), logits, rtol=0, atol=0, equal_nan=True)
+    z_lm, m_lm = _zm(ws_lm, R)
+    z_pl, m_pl = _zm(ws_pl, R)
+    assert z_lm == z_pl
+    assert np.array_equal(m_lm.view(np.uint32), m_pl.view(np.uint32))
+    assert torch.equal(acc[0], acc[1]) and torch.equal(out[0], out[1])
+    # the oracle, for the rows holding +-inf / NaN and a spread of others
+    lc, dc = logits.cpu().numpy(), draft.cpu().numpy()
+    for r in sorted({0, 1, T + 2, B * T - 1, B * T, R - 1, (B * T) // 2}):
+        row = lc.reshape(B * T, V)[r] if r < B * T else dc.reshape(B * K, V)[r - B * T]
+        _, Z, M = oa.row_weights(row, inv_t)
+        assert z_lm[r] == Z, f"row {r}"
+        assert m_lm[r].view(np.uint32) == np.float32(M).view(np.uint32), f"row {r}"

@@ -31,7 +31,7 @@ def test_library_exports_every_declared_symbol():
 def test_status_strings_and_version():
     import npn_native
     lib = npn_native.lib()
-    assert lib.npn_abi_version() == 101
+    assert lib.npn_abi_version() == 102
     assert lib.npn_status_string(0) == b"ok"
     for code in range(1, 7):
         assert lib.npn_status_string(code) not in (b"ok", b"unknown status")

@@ -279,7 +279,7 @@ def test_empty_rows_pass_the_accept_test():
 
 
 def test_multichunk_weights_follow_softmax():
-    """With several 8192-entry chunks whose maxima differ (the row maximum in chunk 2, one
+    """With several 64-entry chunks whose maxima differ (the row maximum in chunk 2, one
     chunk 40 below it), the contract's p = W / Z equals float64 softmax(s) to the contract's
     precision (2^-19 relative + 2^-29 absolute), Z is exactly the sum of the weights, the top chunk's weights are E * 2^31, and
     the far chunk gets weight 0. A factor taken against the wrong maximum, or a chunk left out

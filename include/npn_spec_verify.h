@@ -304,14 +304,16 @@ int npn_accept_greedy(const float* target_logits, const int64_t* draft_ids, int3
  * al. 2023, Alg. 1) under an integer softmax contract, so the result is
  * bit-identical to a CPU restatement for the same logits and uniforms, and every
  * sum comes from one pass over the logits:
- *   s_v = t_v*inv_temperature (fp32); the vocabulary is cut into chunks of 64;
- *   m_c = max of chunk c's non-NaN s_v, M = max_c m_c; E_v = floor(2^31 *
- *   exp_c(s_v - m_c)), F_c = floor(2^31 * exp_c(m_c - M)) with exp_c a fixed fp32
+ *   s_v = t_v*inv_temperature (fp32); the vocabulary is cut into chunks of 64
+ *   and blocks of 8192; m_c = max of chunk c's non-NaN s_v, M_b = max of block b's
+ *   m_c, M = max_b M_b; E_v = floor(2^31 * exp_c(s_v - m_c)), F_c = floor(2^31 *
+ *   exp_c(m_c - M_b)), G_b = floor(2^31 * exp_c(M_b - M)) with exp_c a fixed fp32
  *   Cody-Waite + degree-7 Taylor evaluation in fused multiply-adds; the weight of v
- *   is W_v = E_v * F_c and Z = sum_v W_v (exact integers); U = floor(u * 2^24).
- *   Accept draft x iff U * Wq_x * Zp <= 2^24 * Wp_x * Zq. At the first rejection
- *   sample from R_v = max(0, Wp_v*Zq - Wq_v*Zp) (bonus: R_v = Wp_v of row K):
- *   the smallest v with 2^24 * sum_{w<=v} R_w > U_s * sum_w R_w (exact to 2^192).
+ *   is W_v = E_v * F_c * G_b and Z = sum_v W_v (exact integers, Z <= 2^113);
+ *   U = floor(u * 2^24). Accept draft x iff U * Wq_x * Zp <= 2^24 * Wp_x * Zq. At
+ *   the first rejection sample from R_v = max(0, Wp_v*Zq - Wq_v*Zp) (bonus: R_v =
+ *   Wp_v of row K): the smallest v with 2^24 * sum_{w<=v} R_w > U_s * sum_w R_w
+ *   (exact to 2^256).
  *   A row with no finite entry relative to its maximum (all NaN or -inf, or a +inf
  *   entry) has Z = 0 and passes the accept test; if the sampling row has no mass (a
  *   bonus row, or the residual after an out-of-range draft id where Wp*Zq == Wq*Zp
@@ -320,11 +322,10 @@ int npn_accept_greedy(const float* target_logits, const int64_t* draft_ids, int3
  *   target_logits [B, K+1, V] f32, draft_logits [B, K, V] f32, draft_ids [B, K]
  *   int64, u_accept [B, K] f32 in [0,1), u_sample [B] f32 in [0,1),
  *   inv_temperature > 0 (logits are multiplied by it), V <= 2^20.
- * Three launches: the one pass over the logits (every row's chunk maxima m_c and sums of E),
- * the row totals (M, Z and the weight of the draft token, one workgroup per row), and the
- * sampling kernel (one workgroup per 2048 entries of each sequence: the decision, re-derived
- * by each, and the residual or bonus mass of its entries; the last workgroup of a sequence to
- * finish runs the inverse CDF and writes the sequence's outputs).
+ * Four launches: the one pass over the logits (every row's block maxima M_b and sums S_b;
+ * the chunk statistics stay on chip), the row totals and the decision (one workgroup per
+ * sequence), the residual (or bonus) mass per 2048 entries of each sequence, and the inverse
+ * CDF (one workgroup per sequence).
  * On return the workspace starts with every row's Z (unsigned 128-bit, low 64-bit word
  * first [R]) and, at byte offset 16R rounded up to a multiple of 256, every row's max
  * scaled logit M (float [R]); R = B*(2K+1) rows: target row (b, i) at b*(K+1)+i, then
@@ -335,15 +336,15 @@ int npn_accept_rejection(const float* target_logits, const float* draft_logits,
                          int64_t* out_ids, int B, int K, int V, void* workspace,
                          size_t workspace_bytes, void* stream);
 
-/* Bytes of the fixed per-GPU scratch behind npn_accept_rejection_noalloc (16 MiB). */
-#define NPN_ACCEPT_SCRATCH_BYTES (16u << 20)
+/* Bytes of the fixed per-GPU scratch behind npn_accept_rejection_noalloc (4 MiB). */
+#define NPN_ACCEPT_SCRATCH_BYTES (4u << 20)
 
 /* npn_accept_rejection without a workspace argument and without any allocation. No
  * counterpart in the reference: for callers that cannot allocate device memory (code under
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). The workspace
  * is a fixed device array of NPN_ACCEPT_SCRATCH_BYTES per GPU, held from the first call on
  * that GPU until the process ends; problems whose npn_accept_workspace_size(B, K, V) exceeds
- * it return NPN_ERR_SCRATCH (B = 32, K = 7, V = 151936 needs 13.1 MiB). Every call on a GPU
+ * it return NPN_ERR_SCRATCH (B = 32, K = 7, V = 151936 needs 267 KiB). Every call on a GPU
  * uses that GPU's one array, so calls that overlap on one GPU (concurrent streams, or
  * threads) race and must be serialised by the caller; each call writes every scratch word it
  * reads before reading it (its counters are cleared by its own kernels), so nothing needs

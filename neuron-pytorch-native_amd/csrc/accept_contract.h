@@ -2,11 +2,13 @@
 // kernels and the LM-head GEMM epilogue that produces the target rows' chunk statistics.
 //
 //   s_v = t_v * inv_temp (fp32); the vocabulary is cut into chunks of kContractChunk = 64
-//   entries; m_c = max of chunk c's non-NaN s_v; E_v = floor(2^31 * exp_c(s_v - m_c));
-//   S_c = sum of the chunk's E_v (< 2^37). exp_c is a Cody-Waite reduction + degree-7 Taylor
-//   polynomial written as explicit fp32 fused multiply-adds; every other operation here is a
-//   single IEEE-754 operation, never contracted into a fused multiply-add, so this code and
-//   its CPU restatement round identically. Each function below disables contraction for its
+//   entries and blocks of kContractBlock = 8192; m_c = max of chunk c's non-NaN s_v;
+//   E_v = floor(2^31 * exp_c(s_v - m_c)); S_c = sum of the chunk's E_v (< 2^37); chunk and
+//   block factors F_c = floor(2^31 * exp_c(m_c - M_b)) and G_b = floor(2^31 * exp_c(M_b - M))
+//   refer chunks to their block's maximum and blocks to the row's. exp_c is a Cody-Waite
+//   reduction + degree-7 Taylor polynomial written as explicit fp32 fused multiply-adds;
+//   every other operation here is a single IEEE-754 operation, never contracted into a fused
+//   multiply-add, so this code and its CPU restatement round identically. Each function below disables contraction for its
 //   own body, and every multiply whose result feeds an add or subtract of the contract
 //   happens inside one of them.
 #pragma once
@@ -15,7 +17,8 @@
 
 namespace npn {
 
-constexpr int kContractChunk = 64;   // vocabulary entries per chunk of the contract
+constexpr int kContractChunk = 64;     // vocabulary entries per chunk of the contract
+constexpr int kContractBlock = 8192;   // vocabulary entries per block (128 chunks)
 
 constexpr float kL2E = 0x1.715476p+0f;        // log2(e) in fp32
 constexpr float kLn2Hi = 0x1.62ep-1f;         // ln2, low 12 mantissa bits cleared

@@ -369,7 +369,8 @@ __global__ __launch_bounds__(NWV * 64, 1) void fp8_gemm_narrow_kernel(GemmArgs a
       if (a.cmax != nullptr) {
         // Contract chunk statistics: a 64-column chunk is held by LPC adjacent lanes of the
         // 16-lane group (N % 64 == 0, so a chunk is wholly inside or wholly past N).
-        constexpr int LPC = 64 / CB;
+        constexpr int LPC = 64 / CB;  // 16, 8 or 4: a DPP row, half-row or quad
+        constexpr int STEPS = LPC == 16 ? 4 : (LPC == 8 ? 3 : 2);
         float xs[CB];
 #pragma unroll
         for (int c = 0; c < CB / 2; ++c) {
@@ -379,13 +380,11 @@ __global__ __launch_bounds__(NWV * 64, 1) void fp8_gemm_narrow_kernel(GemmArgs a
         float cmx = -__builtin_inff();
 #pragma unroll
         for (int c = 0; c < CB; ++c) cmx = fmaxf(cmx, xs[c]);
-#pragma unroll
-        for (int off = LPC / 2; off > 0; off >>= 1) cmx = fmaxf(cmx, __shfl_xor(cmx, off, 64));
+        cmx = npn::row_max_dpp<STEPS>(cmx);
         uint64_t csm = 0;
 #pragma unroll
         for (int c = 0; c < CB; ++c) csm += npn::expfix_rel(xs[c], cmx);
-#pragma unroll
-        for (int off = LPC / 2; off > 0; off >>= 1) csm += shfl_xor_u64(csm, off);
+        csm = npn::row_sum_dpp<STEPS>(csm);
         if (i % LPC == 0 && col_ok && m < a.M) {
           const size_t o = (size_t)m * (a.N / 64) + (nc >> 6);
           a.cmax[o] = cmx;
@@ -513,11 +512,11 @@ __device__ __forceinline__ void staged_chunk_stats(const uint16_t* st, int rs, f
     float mx = -__builtin_inff();
 #pragma unroll
     for (int e = 0; e < 32; ++e) mx = fmaxf(mx, x[e]);
-    mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
+    mx = npn::row_max_dpp<1>(mx);  // the row's two threads are lanes 2j, 2j + 1
     uint64_t sm = 0;
 #pragma unroll
     for (int e = 0; e < 32; ++e) sm += npn::expfix_rel(x[e], mx);
-    sm += shfl_xor_u64(sm, 1);
+    sm = npn::row_sum_dpp<1>(sm);
     if (half == 0 && m < M) {
       const size_t o = (size_t)m * nc + (n0 >> 6) + q;
       cmax[o] = mx;

@@ -49,6 +49,41 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// ---- reductions inside 16-lane rows by DPP (VALU lane permutes, no LDS traffic) -----------
+// quad_perm [1,0,3,2] and [2,3,0,1] combine lanes within each quad; row_half_mirror (lane i with
+// 7 - i of its half-row) then row_mirror (i with 15 - i of its row) combine the quads and the
+// halves. After n steps every lane holds the reduction over its aligned group of 2^n lanes
+// (n = 2: quads, 3: eight lanes, 4: the 16-lane row).
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+
+constexpr int kDppStep[4] = {0xB1, 0x4E, 0x141, 0x140};
+
+template <int STEPS>
+__device__ __forceinline__ float row_max_dpp(float v) {
+  if constexpr (STEPS >= 1) v = fmaxf(v, __uint_as_float(dpp32<kDppStep[0]>(__float_as_uint(v))));
+  if constexpr (STEPS >= 2) v = fmaxf(v, __uint_as_float(dpp32<kDppStep[1]>(__float_as_uint(v))));
+  if constexpr (STEPS >= 3) v = fmaxf(v, __uint_as_float(dpp32<kDppStep[2]>(__float_as_uint(v))));
+  if constexpr (STEPS >= 4) v = fmaxf(v, __uint_as_float(dpp32<kDppStep[3]>(__float_as_uint(v))));
+  return v;
+}
+
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp64(uint64_t v) {
+  return ((uint64_t)dpp32<CTRL>((uint32_t)(v >> 32)) << 32) | dpp32<CTRL>((uint32_t)v);
+}
+
+template <int STEPS>
+__device__ __forceinline__ uint64_t row_sum_dpp(uint64_t v) {
+  if constexpr (STEPS >= 1) v += dpp64<kDppStep[0]>(v);
+  if constexpr (STEPS >= 2) v += dpp64<kDppStep[1]>(v);
+  if constexpr (STEPS >= 3) v += dpp64<kDppStep[2]>(v);
+  if constexpr (STEPS >= 4) v += dpp64<kDppStep[3]>(v);
+  return v;
+}
+
 // ---- LDS DMA -----------------------------------------------------------------------------
 // 16 bytes per lane from global address g into LDS at lds_base + 16 * lane
 // (global_load_lds_dwordx4; lds_base must be the same for the whole wave). Issued through

@@ -8,9 +8,10 @@
 // Rejection sampling (Leviathan et al. 2023, Alg. 1) under an integer softmax contract
 // (accept_contract.h) that this file and its CPU restatement evaluate with identical
 // IEEE-754 operations:
-//   s_v = t_v * inv_temp (fp32); 64-entry chunks c with maxima m_c; E_v = floor(2^31 *
-//   exp_c(s_v - m_c)); S_c = sum of E over the chunk; M = max_c m_c; F_c = floor(2^31 *
-//   exp_c(m_c - M)); the weight of v is W_v = E_v F_c and Z = sum_c F_c S_c (exact integers).
+//   s_v = t_v * inv_temp (fp32); 64-entry chunks c with maxima m_c inside 8192-entry blocks b
+//   with maxima M_b; E_v = floor(2^31 exp_c(s_v - m_c)), F_c = floor(2^31 exp_c(m_c - M_b)),
+//   G_b = floor(2^31 exp_c(M_b - M)); the weight of v is W_v = E_v F_c G_b and
+//   Z = sum_b G_b S_b with S_b = sum_c F_c S_c, S_c = sum of the chunk's E (exact integers).
 //   Accept draft x at position i iff U * Wq_x * Zp <= 2^24 * Wp_x * Zq (U = floor(u * 2^24));
 //   a draft id outside [0, V) is a rejection. At the first rejection sample from
 //   R_v = max(0, Wp_v Zq - Wq_v Zp), after K acceptances from R_v = Wp_v of the bonus row: the
@@ -18,11 +19,12 @@
 //
 // Kernels (each over B sequences, T = K+1 positions):
 //   greedy:    argmax partials per (row, 8192-entry chunk) -> per-sequence merge + accept
-//   rejection: chunk statistics (m_c, S_c) of every row in one pass over the logits (for the
-//              LM head the target rows' come from the GEMM epilogue) -> per-row totals M, Z
-//              and the draft token's weight -> one sampling kernel: every block re-derives the
-//              sequence's decision, adds the residual (or bonus) mass of its 2048 entries,
-//              and the last block of each sequence to finish runs the inverse CDF
+//   rejection: block statistics (M_b, S_b) of every row in one pass over the logits, the
+//              64-entry chunk statistics kept on chip (for the LM head the target rows' chunk
+//              statistics come from the GEMM epilogue and a small kernel folds them into
+//              blocks) -> per-sequence row totals and decision -> residual (or bonus) mass
+//              per 2048 entries, the chunk maxima recomputed from the logits read anyway ->
+//              per-sequence inverse CDF
 #include "accept_contract.h"
 #include "npn_internal.h"
 
@@ -34,11 +36,11 @@ constexpr int CHK = 8192;      // vocabulary entries per greedy argmax partial
 constexpr int THREADS = 256;   // CHK / THREADS = 32 entries per thread
 constexpr int PER_T = CHK / THREADS;
 constexpr int CC = npn::kContractChunk;  // 64 entries per chunk of the rejection contract
-constexpr int SBLK = 8192;     // entries per block of the chunk-statistics pass (128 chunks)
 constexpr int MCHK = 2048;     // entries per block of the sampling kernel
 constexpr int PER_M = MCHK / THREADS;  // 8 consecutive entries per thread, inside one chunk
 constexpr int kRejMaxV = 1 << 20;  // largest vocabulary of the rejection path
-static_assert(SBLK / THREADS == 32 && CC % PER_M == 0, "entry layouts of the rejection kernels");
+static_assert(npn::kContractBlock / THREADS == 32 && CC % PER_M == 0,
+              "entry layouts of the rejection kernels");
 
 typedef unsigned __int128 u128;
 
@@ -259,34 +261,77 @@ __global__ __launch_bounds__(1024) void greedy_accept_parts_kernel(
 }
 
 // ---- rejection sampling ------------------------------------------------------------------
-// 192-bit unsigned integers (three 64-bit limbs, little end first) for the exact products of
-// the contract: W (<= 2^62) times Z (<= 2^82), times a 24-bit uniform or shift.
+// Exact unsigned integers of 192 and 256 bits (64-bit limbs, little end first) for the
+// contract's products: W (<= 2^93) times Z (<= 2^113), times a 24-bit uniform or shift.
 struct u192 {
   uint64_t w0, w1, w2;
 };
 
-__device__ __forceinline__ u192 add192(u192 a, u192 b) {
+struct u256 {
+  uint64_t w0, w1, w2, w3;
+};
+
+constexpr u256 kZero256 = {0, 0, 0, 0};
+
+__device__ __forceinline__ u256 add256(u256 a, u256 b) {
   const u128 s0 = (u128)a.w0 + b.w0;
   const u128 s1 = (u128)a.w1 + b.w1 + (uint64_t)(s0 >> 64);
-  return u192{(uint64_t)s0, (uint64_t)s1, a.w2 + b.w2 + (uint64_t)(s1 >> 64)};
+  const u128 s2 = (u128)a.w2 + b.w2 + (uint64_t)(s1 >> 64);
+  return u256{(uint64_t)s0, (uint64_t)s1, (uint64_t)s2, a.w3 + b.w3 + (uint64_t)(s2 >> 64)};
 }
 
-__device__ __forceinline__ u192 sub192(u192 a, u192 b) {  // a >= b
-  const uint64_t b0 = a.w0 < b.w0;
-  const u128 d1 = (u128)a.w1 - b.w1 - b0;
-  const uint64_t b1 = (uint64_t)(d1 >> 64) != 0;  // borrow out of limb 1
-  return u192{a.w0 - b.w0, (uint64_t)d1, a.w2 - b.w2 - b1};
+__device__ __forceinline__ u256 sub256(u256 a, u256 b) {  // a >= b
+  const u128 d0 = (u128)a.w0 - b.w0;
+  const uint64_t c0 = (uint64_t)(d0 >> 64) != 0;
+  const u128 d1 = (u128)a.w1 - b.w1 - c0;
+  const uint64_t c1 = (uint64_t)(d1 >> 64) != 0;
+  const u128 d2 = (u128)a.w2 - b.w2 - c1;
+  const uint64_t c2 = (uint64_t)(d2 >> 64) != 0;
+  return u256{(uint64_t)d0, (uint64_t)d1, (uint64_t)d2, a.w3 - b.w3 - c2};
 }
 
-__device__ __forceinline__ bool gt192(u192 a, u192 b) {
+__device__ __forceinline__ bool gt256(u256 a, u256 b) {
+  if (a.w3 != b.w3) return a.w3 > b.w3;
   if (a.w2 != b.w2) return a.w2 > b.w2;
   if (a.w1 != b.w1) return a.w1 > b.w1;
   return a.w0 > b.w0;
 }
 
-__device__ __forceinline__ bool is_zero192(u192 a) { return (a.w0 | a.w1 | a.w2) == 0; }
+__device__ __forceinline__ bool is_zero256(u256 a) { return (a.w0 | a.w1 | a.w2 | a.w3) == 0; }
 
-// x * y for x < 2^64 and y < 2^128, exact (< 2^192).
+__device__ __forceinline__ u256 shl24_256(u256 a) {
+  return u256{a.w0 << 24, (a.w1 << 24) | (a.w0 >> 40), (a.w2 << 24) | (a.w1 >> 40),
+              (a.w3 << 24) | (a.w2 >> 40)};
+}
+
+// a * b for a, b < 2^128, exact.
+__device__ __forceinline__ u256 mul128x128(u128 a, u128 b) {
+  const uint64_t a0 = (uint64_t)a, a1 = (uint64_t)(a >> 64);
+  const uint64_t b0 = (uint64_t)b, b1 = (uint64_t)(b >> 64);
+  const u128 p00 = (u128)a0 * b0, p01 = (u128)a0 * b1, p10 = (u128)a1 * b0, p11 = (u128)a1 * b1;
+  const u128 mid = (p00 >> 64) + (uint64_t)p01 + (uint64_t)p10;
+  const u128 hi = (mid >> 64) + (p01 >> 64) + (p10 >> 64) + (uint64_t)p11;
+  return u256{(uint64_t)p00, (uint64_t)mid, (uint64_t)hi,
+              (uint64_t)(hi >> 64) + (uint64_t)(p11 >> 64)};
+}
+
+// a * m for m < 2^64, exact while the product stays below 2^256.
+__device__ __forceinline__ u256 mul192x64(u192 a, uint64_t m) {
+  const u128 p0 = (u128)a.w0 * m;
+  const u128 p1 = (u128)a.w1 * m + (uint64_t)(p0 >> 64);
+  const u128 p2 = (u128)a.w2 * m + (uint64_t)(p1 >> 64);
+  return u256{(uint64_t)p0, (uint64_t)p1, (uint64_t)p2, (uint64_t)(p2 >> 64)};
+}
+
+// a * m for m < 2^32, exact while the product stays below 2^256.
+__device__ __forceinline__ u256 mul256x32(u256 a, uint32_t m) {
+  const u128 p0 = (u128)a.w0 * m;
+  const u128 p1 = (u128)a.w1 * m + (uint64_t)(p0 >> 64);
+  const u128 p2 = (u128)a.w2 * m + (uint64_t)(p1 >> 64);
+  return u256{(uint64_t)p0, (uint64_t)p1, (uint64_t)p2, a.w3 * m + (uint64_t)(p2 >> 64)};
+}
+
+// x * y for x < 2^64 and y < 2^128 (< 2^192).
 __device__ __forceinline__ u192 mul64x128(uint64_t x, u128 y) {
   const u128 lo = (u128)x * (uint64_t)y;
   const u128 hi = (u128)x * (uint64_t)(y >> 64);
@@ -294,23 +339,83 @@ __device__ __forceinline__ u192 mul64x128(uint64_t x, u128 y) {
   return u192{(uint64_t)lo, (uint64_t)mid, (uint64_t)(hi >> 64) + (uint64_t)(mid >> 64)};
 }
 
-// x * m for x < 2^128 and m < 2^32, exact (< 2^160).
-__device__ __forceinline__ u192 mul128x32(u128 x, uint32_t m) {
-  const u128 p0 = (u128)(uint64_t)x * m;
-  const u128 p1 = (u128)(uint64_t)(x >> 64) * m + (uint64_t)(p0 >> 64);
-  return u192{(uint64_t)p0, (uint64_t)p1, (uint64_t)(p1 >> 64)};
+__device__ __forceinline__ double u192_to_f64(u192 x) {
+  return (double)x.w2 * 0x1p128 + (double)x.w1 * 0x1p64 + (double)x.w0;
 }
 
-// a * m for m < 2^32 (exact while the product stays below 2^192).
-__device__ __forceinline__ u192 mul192x32(u192 a, uint32_t m) {
-  const u128 p0 = (u128)a.w0 * m;
-  const u128 p1 = (u128)a.w1 * m + (uint64_t)(p0 >> 64);
-  return u192{(uint64_t)p0, (uint64_t)p1, a.w2 * m + (uint64_t)(p1 >> 64)};
+// 64-bit, 128-bit and 256-bit values through lane shuffles (32-bit words).
+__device__ __forceinline__ u128 shfl_u128(u128 v, int src_lane) {
+  uint32_t w[4] = {(uint32_t)v, (uint32_t)(v >> 32), (uint32_t)(v >> 64), (uint32_t)(v >> 96)};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) w[k] = __shfl(w[k], src_lane, 64);
+  return ((u128)w[3] << 96) | ((u128)w[2] << 64) | ((u128)w[1] << 32) | w[0];
 }
 
-__device__ __forceinline__ u192 shl24_192(u192 a) {
-  return u192{a.w0 << 24, (a.w1 << 24) | (a.w0 >> 40), (a.w2 << 24) | (a.w1 >> 40)};
+template <typename F>
+__device__ __forceinline__ u256 map256(u256 v, F f) {
+  uint32_t w[8] = {(uint32_t)v.w0, (uint32_t)(v.w0 >> 32), (uint32_t)v.w1, (uint32_t)(v.w1 >> 32),
+                   (uint32_t)v.w2, (uint32_t)(v.w2 >> 32), (uint32_t)v.w3, (uint32_t)(v.w3 >> 32)};
+#pragma unroll
+  for (int k = 0; k < 8; ++k) w[k] = f(w[k]);
+  return u256{((uint64_t)w[1] << 32) | w[0], ((uint64_t)w[3] << 32) | w[2],
+              ((uint64_t)w[5] << 32) | w[4], ((uint64_t)w[7] << 32) | w[6]};
 }
+
+__device__ __forceinline__ u256 shfl_u256(u256 v, int src) {
+  return map256(v, [&](uint32_t x) { return (uint32_t)__shfl(x, src, 64); });
+}
+__device__ __forceinline__ u256 shfl_up_u256(u256 v, int d) {
+  return map256(v, [&](uint32_t x) { return (uint32_t)__shfl_up(x, d, 64); });
+}
+__device__ __forceinline__ u256 shfl_xor_u256(u256 v, int m) {
+  return map256(v, [&](uint32_t x) { return (uint32_t)__shfl_xor(x, m, 64); });
+}
+template <int CTRL>
+__device__ __forceinline__ u256 dpp_u256(u256 v) {
+  return map256(v, [](uint32_t x) { return npn::dpp32<CTRL>(x); });
+}
+
+// Sum over the 64 lanes of a wave, in every lane: DPP inside each 16-lane row, then rows.
+__device__ __forceinline__ u256 wave_sum_u256(u256 v) {
+  v = add256(v, dpp_u256<npn::kDppStep[0]>(v));
+  v = add256(v, dpp_u256<npn::kDppStep[1]>(v));
+  v = add256(v, dpp_u256<npn::kDppStep[2]>(v));
+  v = add256(v, dpp_u256<npn::kDppStep[3]>(v));
+  v = add256(v, shfl_xor_u256(v, 16));
+  return add256(v, shfl_xor_u256(v, 32));
+}
+
+// Inclusive prefix sum over the 64 lanes of a wave.
+__device__ __forceinline__ u256 wave_incl_scan_u256(u256 v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const u256 o = shfl_up_u256(v, d);
+    if (lane >= d) v = add256(v, o);
+  }
+  return v;
+}
+
+__device__ __forceinline__ u128 wave_sum_u128(u128 v) {
+  for (int off = 32; off > 0; off >>= 1) {
+    const uint64_t lo = shfl_xor_u64((uint64_t)v, off);
+    const uint64_t hi = shfl_xor_u64((uint64_t)(v >> 64), off);
+    v += ((u128)hi << 64) | lo;
+  }
+  return v;
+}
+
+constexpr int CPB = npn::kContractBlock / CC;  // contract chunks per block (128)
+constexpr int kMaxRowsPerSeq = 2 * 64 + 1;      // 2K+1 rows of a sequence (K <= 64)
+
+// The accept decision of one sequence and its sampling rows (target row acc, and draft row
+// acc after a rejection): their maxima and totals.
+struct Decision {
+  u128 zp, zq;
+  float mp, mq;
+  int acc;
+  int pad;
+};
 
 struct RejArgs {
   const void* target;    // [B][K+1][V] fp32, or bf16 (the LM head's logits)
@@ -321,16 +426,15 @@ struct RejArgs {
   float inv_temp;
   int32_t* accepted;
   int64_t* out_ids;
-  int B, K, V, nc, nchm;  // contract chunks per row; sampling-kernel blocks per row
+  int B, K, V, nb, nchm;  // contract blocks per row; 2048-entry sub-chunks per row
   bool vec4;              // fp32 logit rows 16-byte aligned and V % 4 == 0 (bf16: V % 8)
   // workspace (rows: the B*(K+1) target rows, then the B*K draft rows)
   u128* zrow;             // [rows]      Z of each row
   float* mrow;            // [rows]      row maximum M (scaled logits)
-  uint64_t* wtok;         // [rows]      W of the row's draft token (0: bonus row, bad id)
-  float* cmax;            // [rows][nc]  chunk maxima m_c
-  uint64_t* csum;         // [rows][nc]  chunk sums S_c
-  u192* cmass;            // [B][nchm]   sampling mass of each sampling-kernel block
-  uint32_t* cnt;          // [B]         sampling-kernel blocks finished, per sequence
+  float* bmax;            // [rows][nb]  block maxima M_b
+  u128* bsum;             // [rows][nb]  block sums S_b
+  Decision* dec;          // [B]
+  u256* cmass;            // [B][nchm]   sampling mass of each 2048-entry sub-chunk
 };
 
 template <typename TT>
@@ -359,34 +463,55 @@ __device__ __forceinline__ int row_token(const RejArgs& a, int row) {
   return draft_id_ok(x, a.V) ? (int)x : -1;
 }
 
-// The 16-lane shuffles of the statistics pass (lanes that share a chunk).
-__device__ __forceinline__ float max16(float m) {
-#pragma unroll
-  for (int off = 8; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-  return m;
+__device__ __forceinline__ float elem_at(const RejArgs& a, int row, int v, const float*) {
+  const int nt = a.B * (a.K + 1);
+  return row < nt ? static_cast<const float*>(a.target)[(size_t)row * a.V + v]
+                  : a.draft[(size_t)(row - nt) * a.V + v];
 }
 
-__device__ __forceinline__ uint64_t sum16(uint64_t s) {
-#pragma unroll
-  for (int off = 8; off > 0; off >>= 1) s += shfl_xor_u64(s, off);
-  return s;
+__device__ __forceinline__ float elem_at(const RejArgs& a, int row, int v, const uint16_t*) {
+  const int nt = a.B * (a.K + 1);
+  return row < nt ? npn::bf16_to_f32(static_cast<const uint16_t*>(a.target)[(size_t)row * a.V + v])
+                  : a.draft[(size_t)(row - nt) * a.V + v];
 }
 
-// Chunk statistics of fp32 logit rows: block (x, y) reads entries [8192 x, 8192 x + 8192) of
-// row row0 + y once, into registers (thread t holds the float4s at v0 + 4 (256 j + t),
-// j < 8, so for each j the 16 lanes of a 16-lane group hold one 64-entry chunk), and writes
-// each chunk's maximum m_c of the scaled logits (NaN ignored; entries past V read as NaN)
-// and S_c = sum of expfix(s_v - m_c).
+// Block statistics of one 8192-entry block from its 128 chunk statistics, one chunk per
+// thread (every thread of the workgroup calls this; threads past the chunks pass m = -inf,
+// s = 0): M_b = max m_c, S_b = sum F_c S_c with F_c = expfix(m_c - M_b), in every thread.
+__device__ __forceinline__ void block_from_chunks(float m, uint64_t s, float* sh_m, u128* sh_s,
+                                                  float& Mb, u128& Sb) {
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = blockDim.x >> 6;
+  const float mx = npn::wave_max(m);
+  if (lane == 0) sh_m[w] = mx;
+  __syncthreads();
+  Mb = sh_m[0];
+  for (int i = 1; i < nw; ++i) Mb = fmaxf(Mb, sh_m[i]);
+  const u128 t = wave_sum_u128((u128)s * expfix_rel(m, Mb));
+  if (lane == 0) sh_s[w] = t;
+  __syncthreads();
+  Sb = 0;
+  for (int i = 0; i < nw; ++i) Sb += sh_s[i];
+}
+
+// Block statistics of fp32 logit rows: block (x, y) reads entries [8192 x, 8192 x + 8192) of
+// row row0 + y once, into registers (thread t holds the float4s at v0 + 4 (256 j + t), j < 8,
+// so for each j the 16 lanes of a DPP row hold one 64-entry chunk); each chunk's maximum m_c
+// of the scaled logits (NaN ignored; entries past V read as NaN) and S_c = sum of
+// expfix(s_v - m_c) stay on chip, and only M_b and S_b = sum F_c S_c are written.
 template <bool kUnitTemp>
 __global__ __launch_bounds__(THREADS) void rej_stats_kernel(RejArgs a, int row0) {
+  __shared__ float sh_cm[CPB];
+  __shared__ uint64_t sh_cs[CPB];
+  __shared__ float sh_m[THREADS / 64];
+  __shared__ u128 sh_s[THREADS / 64];
   const int row = row0 + (int)blockIdx.y;
   const int nt = a.B * (a.K + 1);
   const float* src = row < nt ? static_cast<const float*>(a.target) + (size_t)row * a.V
                               : a.draft + (size_t)(row - nt) * a.V;
-  const int v0 = (int)blockIdx.x * SBLK;
+  const int v0 = (int)blockIdx.x * npn::kContractBlock;
   const int t = threadIdx.x;
   float x[32];
-  if (a.vec4 && v0 + SBLK <= a.V) {  // whole block inside the row: all loads first, no guards
+  if (a.vec4 && v0 + npn::kContractBlock <= a.V) {  // whole block inside the row
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const float4 f = *reinterpret_cast<const float4*>(src + v0 + 4 * (j * THREADS + t));
@@ -405,431 +530,406 @@ __global__ __launch_bounds__(THREADS) void rej_stats_kernel(RejArgs a, int row0)
 #pragma unroll
     for (int e = 0; e < 32; ++e) x[e] = scaled(x[e], a.inv_temp);
   }
-  float* cm = a.cmax + (size_t)row * a.nc;
-  uint64_t* cs = a.csum + (size_t)row * a.nc;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     float m = -INFINITY;
 #pragma unroll
     for (int k = 0; k < 4; ++k) m = fmaxf(m, x[4 * j + k]);
-    m = max16(m);
-    uint64_t s = 0;
+    m = npn::row_max_dpp<4>(m);
+    uint64_t sm = 0;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) s += expfix_rel(x[4 * j + k], m);
-    s = sum16(s);
-    const int c = (v0 >> 6) + ((j * THREADS + t) >> 4);
-    if ((t & 15) == 0 && c < a.nc) {
-      cm[c] = m;
-      cs[c] = s;
+    for (int k = 0; k < 4; ++k) sm += expfix_rel(x[4 * j + k], m);
+    sm = npn::row_sum_dpp<4>(sm);
+    if ((t & 15) == 0) {
+      sh_cm[(j * THREADS + t) >> 4] = m;
+      sh_cs[(j * THREADS + t) >> 4] = sm;
     }
+  }
+  __syncthreads();
+  float Mb;
+  u128 Sb;
+  block_from_chunks(t < CPB ? sh_cm[t] : -INFINITY, t < CPB ? sh_cs[t] : 0, sh_m, sh_s, Mb, Sb);
+  if (t == 0) {
+    a.bmax[(size_t)row * a.nb + blockIdx.x] = Mb;
+    a.bsum[(size_t)row * a.nb + blockIdx.x] = Sb;
   }
 }
 
-__device__ __forceinline__ float elem_at(const RejArgs& a, int row, int v, const float*) {
-  const int nt = a.B * (a.K + 1);
-  return row < nt ? static_cast<const float*>(a.target)[(size_t)row * a.V + v]
-                  : a.draft[(size_t)(row - nt) * a.V + v];
-}
-
-__device__ __forceinline__ float elem_at(const RejArgs& a, int row, int v, const uint16_t*) {
-  const int nt = a.B * (a.K + 1);
-  return row < nt ? npn::bf16_to_f32(static_cast<const uint16_t*>(a.target)[(size_t)row * a.V + v])
-                  : a.draft[(size_t)(row - nt) * a.V + v];
-}
-
-// Row totals, one block per row: M = max_c m_c, Z = sum_c F_c S_c (F_c = expfix(m_c - M)),
-// and W = E F_c of the row's draft token (its logit and chunk maximum are loaded first). The
-// first target row of each sequence also clears the sequence's counter of finished
-// sampling-kernel blocks (the sampling kernel runs after this one, on the same stream).
-template <typename TT>
-__global__ __launch_bounds__(THREADS) void rej_rowtotal_kernel(RejArgs a) {
-  __shared__ float shm[THREADS / 64];
-  __shared__ u128 shz[THREADS / 64];
-  const int row = (int)blockIdx.x;
-  const int nt = a.B * (a.K + 1);
-  const float* cm = a.cmax + (size_t)row * a.nc;
-  const uint64_t* cs = a.csum + (size_t)row * a.nc;
-  const int tok = row_token(a, row);
-  float xt = 0.f, mt = 0.f;
-  if (threadIdx.x == 0 && tok >= 0) {
-    xt = elem_at(a, row, tok, static_cast<const TT*>(nullptr));
-    mt = cm[tok / CC];
-  }
-  constexpr int U = 8;  // chunks per thread per batch, loads issued together
-  float M = -INFINITY;
-  for (int c0 = threadIdx.x; c0 < a.nc; c0 += U * THREADS) {
-    float v[U];
-#pragma unroll
-    for (int k = 0; k < U; ++k) {
-      const int c = c0 + k * THREADS;
-      v[k] = c < a.nc ? cm[c] : -INFINITY;
-    }
-#pragma unroll
-    for (int k = 0; k < U; ++k) M = fmaxf(M, v[k]);
-  }
-  M = block_max(M, shm);
-  u128 z = 0;
-  for (int c0 = threadIdx.x; c0 < a.nc; c0 += U * THREADS) {
-    float v[U];
-    uint64_t s[U];
-#pragma unroll
-    for (int k = 0; k < U; ++k) {
-      const int c = c0 + k * THREADS;
-      v[k] = c < a.nc ? cm[c] : -INFINITY;
-      s[k] = c < a.nc ? cs[c] : 0;
-    }
-#pragma unroll
-    for (int k = 0; k < U; ++k) z += (u128)s[k] * expfix_rel(v[k], M);
-  }
-  z = block_sum_u128(z, shz);
+// Block statistics from chunk statistics ([rows][nc], the LM-head GEMM epilogue's), one
+// 128-thread workgroup per (block, row); chunks past the row's last read as empty.
+__global__ __launch_bounds__(CPB) void rej_block_from_chunks_kernel(RejArgs a, int row0,
+                                                                    const float* cmax,
+                                                                    const uint64_t* csum,
+                                                                    int nc) {
+  __shared__ float sh_m[CPB / 64];
+  __shared__ u128 sh_s[CPB / 64];
+  const int b = (int)blockIdx.x, r = (int)blockIdx.y;
+  const int c = b * CPB + (int)threadIdx.x;
+  const float m = c < nc ? cmax[(size_t)r * nc + c] : -INFINITY;
+  const uint64_t s = c < nc ? csum[(size_t)r * nc + c] : 0;
+  float Mb;
+  u128 Sb;
+  block_from_chunks(m, s, sh_m, sh_s, Mb, Sb);
   if (threadIdx.x == 0) {
-    a.zrow[row] = z;
-    a.mrow[row] = M;
-    a.wtok[row] = tok < 0 ? 0
-                          : (uint64_t)expfix_rel(scaled(xt, a.inv_temp), mt) * expfix_rel(mt, M);
-    if (row < nt && row % (a.K + 1) == 0) a.cnt[row / (a.K + 1)] = 0;
+    a.bmax[(size_t)(row0 + r) * a.nb + b] = Mb;
+    a.bsum[(size_t)(row0 + r) * a.nb + b] = Sb;
   }
 }
 
-// The sampling rows of one sequence, as seen by one thread at the contract chunk cc of its
-// run: after a rejection at position acc the residual W^p Zq - W^q Zp = E^p (F^p Zq) -
-// E^q (F^q Zp), whose bracketed products (< 2^114) are formed once per thread; for the bonus
-// row the weight is E^p F^p.
+// Row totals and the decision, one workgroup per sequence (one wave per row, rows in turn):
+// M = max_b M_b, Z = sum_b G_b S_b (G_b = expfix(M_b - M)), and the weight W = E F G of the
+// row's draft token, whose chunk (64 entries, read with the block statistics) gives its m_c,
+// E = expfix(s - m_c) and F = expfix(m_c - M_b). Then lane i < K of wave 0 runs the accept test
+// of draft position i (all at once; the first failing lane is the rejection). Writes every
+// row's Z and M, the sequence's decision record, accepted[b] and out_ids but the sampled token.
+template <typename TT>
+__global__ __launch_bounds__(1024) void rej_decide_kernel(RejArgs a) {
+  const int b = (int)blockIdx.x;
+  const int K = a.K, T = K + 1, nt = a.B * T;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  __shared__ u128 s_z[kMaxRowsPerSeq];
+  __shared__ u128 s_w[kMaxRowsPerSeq];
+  __shared__ float s_m[kMaxRowsPerSeq];
+  for (int j = w; j < T + K; j += nw) {
+    const int row = j < T ? b * T + j : nt + b * K + (j - T);
+    const int tok = row_token(a, row);
+    // the token's chunk, and the row's block statistics (two blocks per lane at most)
+    float xv = NAN;
+    if (tok >= 0) {
+      const int v = (tok / CC) * CC + lane;
+      if (v < a.V) xv = scaled(elem_at(a, row, v, static_cast<const TT*>(nullptr)), a.inv_temp);
+    }
+    float bm[2];
+    u128 bs[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int bb = lane + 64 * k;
+      bm[k] = bb < a.nb ? a.bmax[(size_t)row * a.nb + bb] : -INFINITY;
+      bs[k] = bb < a.nb ? a.bsum[(size_t)row * a.nb + bb] : 0;
+    }
+    const float M = npn::wave_max(fmaxf(bm[0], bm[1]));
+    const u128 z = wave_sum_u128((u128)bs[0] * expfix_rel(bm[0], M) +
+                                 (u128)bs[1] * expfix_rel(bm[1], M));
+    u128 wt = 0;
+    if (tok >= 0) {
+      const float mc = npn::wave_max(xv);
+      const float xs = __shfl(xv, tok % CC, 64);
+      const int tb = tok / npn::kContractBlock;
+      const float Mb = __shfl(tb < 64 ? bm[0] : bm[1], tb & 63, 64);
+      wt = (u128)((uint64_t)expfix_rel(xs, mc) * expfix_rel(mc, Mb)) * expfix_rel(Mb, M);
+    }
+    if (lane == 0) {
+      s_z[j] = z;
+      s_m[j] = M;
+      s_w[j] = wt;
+      a.zrow[row] = z;
+      a.mrow[row] = M;
+    }
+  }
+  __syncthreads();
+  if (w != 0) return;
+  bool reject = false;
+  if (lane < K) {
+    const int64_t id = a.draft_ids[(size_t)b * K + lane];
+    const uint32_t U = uniform_fix(a.u_accept[(size_t)b * K + lane]);
+    const u256 lhs = mul256x32(mul128x128(s_w[T + lane], s_z[lane]), U);
+    const u256 rhs = shl24_256(mul128x128(s_w[lane], s_z[T + lane]));
+    reject = !draft_id_ok(id, a.V) || gt256(lhs, rhs);
+  }
+  const uint64_t rej = __builtin_amdgcn_ballot_w64(reject);
+  const int acc = rej ? __builtin_ctzll(rej) : K;
+  if (lane == 0) {
+    Decision d;
+    d.acc = acc;
+    d.pad = 0;
+    d.zp = s_z[acc];
+    d.mp = s_m[acc];
+    d.zq = acc < K ? s_z[T + acc] : 0;
+    d.mq = acc < K ? s_m[T + acc] : 0.f;
+    a.dec[b] = d;
+    a.accepted[b] = acc;
+  }
+  for (int t = lane; t < T; t += 64)
+    if (t != acc) a.out_ids[(size_t)b * T + t] = t < acc ? a.draft_ids[(size_t)b * K + t] : -1;
+}
+
+// The sampling rows of one sequence for a thread's run inside one contract chunk: after a
+// rejection at position acc the residual W^p Zq - W^q Zp = E^p (F^p G^p Zq) - E^q (F^q G^q Zp),
+// whose bracketed products (< 2^176) are formed once per run; the bonus row's weight is
+// E^p (F^p G^p).
 template <typename TT>
 struct SampleRow {
   const TT* p;
   const float* q;  // nullptr for the bonus row
-  float mp, mq;    // chunk maxima of chunk cc
-  uint64_t fp;     // F^p of chunk cc
-  u128 gp, gq;     // F^p Zq and F^q Zp
-  double gpd, gqd; // the same, rounded to fp64 (relative error below 2^-51)
+  float mp, mq;    // chunk maxima of the run's chunk
+  uint64_t fgp;    // F^p G^p
+  u192 gp, gq;     // F^p G^p Zq and F^q G^q Zp
+  float r;         // gq / gp rounded to fp32 (via fp64; +inf for gp = 0, NaN for both 0)
 };
 
-__device__ __forceinline__ double u128_to_f64(u128 x) {
-  return (double)(uint64_t)(x >> 64) * 0x1p64 + (double)(uint64_t)x;
-}
-
-// Decision of sequence b, shared by the blocks of the sampling kernel.
-struct Decision {
-  int acc;         // accepted drafts (the sampling position)
-  float mp, mq;    // row maxima of the sampling rows (mq: draft row, after a rejection)
-  u128 zp, zq;     // their totals
-};
-
-template <typename TT>
-__device__ __forceinline__ SampleRow<TT> sample_row(const RejArgs& a, int b, const Decision& d,
-                                                    int cc) {
-  const int K = a.K, T = K + 1;
-  const int nt = a.B * T;
-  SampleRow<TT> s;
-  const int rp = b * T + d.acc;
-  s.p = target_row<TT>(a, rp);
-  s.mp = a.cmax[(size_t)rp * a.nc + cc];
-  s.fp = expfix_rel(s.mp, d.mp);
-  s.gp = (u128)s.fp * d.zq;
-  if (d.acc < K) {
-    const int rq = nt + b * K + d.acc;
-    s.q = a.draft + (size_t)(b * K + d.acc) * a.V;
-    s.mq = a.cmax[(size_t)rq * a.nc + cc];
-    s.gq = (u128)expfix_rel(s.mq, d.mq) * d.zp;
-  } else {
-    s.q = nullptr;
-    s.mq = 0.f;
-    s.gq = 0;
-  }
-  s.gpd = u128_to_f64(s.gp);
-  s.gqd = u128_to_f64(s.gq);
-  return s;
-}
-
-template <typename TT>
-__device__ __forceinline__ u192 weight_of(const SampleRow<TT>& s, float pv, float qv,
-                                          float inv_temp) {
-  const uint32_t ep = expfix_rel(scaled(pv, inv_temp), s.mp);
-  if (s.q == nullptr) return u192{(uint64_t)ep * s.fp, 0, 0};
-  const uint32_t eq = expfix_rel(scaled(qv, inv_temp), s.mq);
-  const u192 x = mul128x32(s.gp, ep), y = mul128x32(s.gq, eq);
-  return gt192(x, y) ? sub192(x, y) : u192{0, 0, 0};
-}
-
-// Whether an entry after a rejection has residual weight, gp E^p > gq E^q, decided exactly.
-// Each fp64 product is within a relative 2^-50 of the exact one, so a margin of 2^-40 settles
-// every pair that is not nearly tied; the rest compare the exact 160-bit products.
-template <typename TT>
-__device__ __forceinline__ bool residual_positive(const SampleRow<TT>& s, uint32_t ep,
-                                                  uint32_t eq) {
-  const double x = s.gpd * (double)ep, y = s.gqd * (double)eq;
-  if (x > y * (1.0 + 0x1p-40)) return true;
-  if (y > x * (1.0 + 0x1p-40)) return false;
-  return gt192(mul128x32(s.gp, ep), mul128x32(s.gq, eq));
-}
-
-// This thread's PER_M consecutive sampling-row entries starting at v0 (p, and q after a
-// rejection), loaded once; entries at or past V read as p = -inf (callers stop at V).
+// The thread's N entries [v0, v0 + N) of the sampling rows, loaded once (p, and q after a
+// rejection); entries at or past V read as p = -inf, q = NaN (weight 0, and ignored by the
+// chunk maxima).
+template <int N>
 struct RunVals {
-  float p[PER_M], q[PER_M];
+  float p[N], q[N];
 };
 
-__device__ __forceinline__ void load_p(const float* p, int v0, float (&dst)[PER_M]) {
+template <int N>
+__device__ __forceinline__ void load_p(const float* p, int v0, float (&dst)[N]) {
 #pragma unroll
-  for (int j = 0; j < PER_M; j += 4) {
+  for (int j = 0; j < N; j += 4) {
     const float4 pv = *reinterpret_cast<const float4*>(p + v0 + j);
     dst[j] = pv.x; dst[j + 1] = pv.y; dst[j + 2] = pv.z; dst[j + 3] = pv.w;
   }
 }
 
-__device__ __forceinline__ void load_p(const uint16_t* p, int v0, float (&dst)[PER_M]) {
-  static_assert(PER_M == 8, "one 16-byte piece of bf16 per run");
-  const uint4 x = *reinterpret_cast<const uint4*>(p + v0);
-  const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+template <int N>
+__device__ __forceinline__ void load_p(const uint16_t* p, int v0, float (&dst)[N]) {
+  static_assert(N % 8 == 0, "16-byte pieces of bf16");
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    dst[2 * k] = npn::bf16_to_f32(w[k] & 0xFFFFu);
-    dst[2 * k + 1] = npn::bf16_to_f32(w[k] >> 16);
+  for (int j = 0; j < N; j += 8) {
+    const uint4 x = *reinterpret_cast<const uint4*>(p + v0 + j);
+    const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      dst[j + 2 * k] = npn::bf16_to_f32(w[k] & 0xFFFFu);
+      dst[j + 2 * k + 1] = npn::bf16_to_f32(w[k] >> 16);
+    }
   }
 }
 
-template <typename TT>
-__device__ __forceinline__ RunVals load_run(const RejArgs& a, const SampleRow<TT>& s, int v0) {
-  RunVals r;
-  if (a.vec4 && v0 + PER_M <= a.V) {
-    load_p(s.p, v0, r.p);
-#pragma unroll
-    for (int j = 0; j < PER_M; j += 4) {
-      if (s.q != nullptr) {
-        const float4 qv = *reinterpret_cast<const float4*>(s.q + v0 + j);
-        r.q[j] = qv.x; r.q[j + 1] = qv.y; r.q[j + 2] = qv.z; r.q[j + 3] = qv.w;
-      } else {
-        r.q[j] = r.q[j + 1] = r.q[j + 2] = r.q[j + 3] = 0.f;
-      }
-    }
+template <int N, bool kUnitTemp, typename TT>
+__device__ __forceinline__ RunVals<N> load_run(const RejArgs& a, const TT* p, const float* q,
+                                               int v0) {
+  RunVals<N> r;
+  if (a.vec4 && v0 + N <= a.V) {
+    load_p<N>(p, v0, r.p);
+    if (q != nullptr) load_p<N>(q, v0, r.q);
   } else {
 #pragma unroll
-    for (int j = 0; j < PER_M; ++j) {
+    for (int j = 0; j < N; ++j) {
       const int v = v0 + j;
-      r.p[j] = v < a.V ? elem(s.p, v) : -INFINITY;
-      r.q[j] = (v < a.V && s.q != nullptr) ? s.q[v] : 0.f;
+      r.p[j] = v < a.V ? elem(p, v) : NAN;
+      r.q[j] = (v < a.V && q != nullptr) ? q[v] : NAN;
+    }
+  }
+  if (q == nullptr) {
+#pragma unroll
+    for (int j = 0; j < N; ++j) r.q[j] = NAN;
+  }
+  if (!kUnitTemp) {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      r.p[j] = scaled(r.p[j], a.inv_temp);
+      r.q[j] = scaled(r.q[j], a.inv_temp);
     }
   }
   return r;
 }
 
-// Sampling weight of the run's entries below V, exactly: after a rejection the sum of
-// gp E^p - gq E^q over the entries with positive residual equals gp (sum of their E^p) -
-// gq (sum of their E^q), so each entry costs its two exponentials, an fp64 membership test
-// and two 64-bit adds, and the 192-bit products are formed once per run. The bonus row's
-// weights E^p F^p sum to F^p (sum of E^p).
+// The run's constants from its chunk maxima (reduced by the caller over the chunk's lanes) and
+// the sampling rows' block maxima of the run's block.
 template <typename TT>
-__device__ __forceinline__ u192 run_mass(const SampleRow<TT>& s, const RunVals& r, int v0, int V,
-                                         float inv_temp) {
-  uint64_t sp = 0, sq = 0;
-  if (s.q == nullptr) {
-#pragma unroll
-    for (int j = 0; j < PER_M; ++j)
-      if (v0 + j < V) sp += expfix_rel(scaled(r.p[j], inv_temp), s.mp);
-    return mul64x128(sp, (u128)s.fp);
+__device__ __forceinline__ SampleRow<TT> sample_row(const Decision& d, const TT* p,
+                                                    const float* q, float mpc, float mqc,
+                                                    float Mbp, float Mbq) {
+  SampleRow<TT> s;
+  s.p = p;
+  s.q = q;
+  s.mp = mpc;
+  s.fgp = (uint64_t)expfix_rel(mpc, Mbp) * expfix_rel(Mbp, d.mp);
+  s.gp = mul64x128(s.fgp, d.zq);
+  if (q != nullptr) {
+    s.mq = mqc;
+    const uint64_t fgq = (uint64_t)expfix_rel(mqc, Mbq) * expfix_rel(Mbq, d.mq);
+    s.gq = mul64x128(fgq, d.zp);
+  } else {
+    s.mq = 0.f;
+    s.gq = u192{0, 0, 0};
   }
-#pragma unroll
-  for (int j = 0; j < PER_M; ++j) {
-    if (v0 + j < V) {
-      const uint32_t ep = expfix_rel(scaled(r.p[j], inv_temp), s.mp);
-      const uint32_t eq = expfix_rel(scaled(r.q[j], inv_temp), s.mq);
-      if (residual_positive(s, ep, eq)) {
-        sp += ep;
-        sq += eq;
-      }
-    }
-  }
-  return sub192(mul64x128(sp, s.gp), mul64x128(sq, s.gq));
-}
-
-// ---- 192-bit wave and block sums and scans -----------------------------------------------
-__device__ __forceinline__ u192 shfl_u192(u192 v, int src_lane) {
-  uint32_t w[6] = {(uint32_t)v.w0, (uint32_t)(v.w0 >> 32), (uint32_t)v.w1,
-                   (uint32_t)(v.w1 >> 32), (uint32_t)v.w2, (uint32_t)(v.w2 >> 32)};
-#pragma unroll
-  for (int k = 0; k < 6; ++k) w[k] = __shfl(w[k], src_lane, 64);
-  return u192{((uint64_t)w[1] << 32) | w[0], ((uint64_t)w[3] << 32) | w[2],
-              ((uint64_t)w[5] << 32) | w[4]};
-}
-
-__device__ __forceinline__ u192 shfl_up_u192(u192 v, int d) {
-  uint32_t w[6] = {(uint32_t)v.w0, (uint32_t)(v.w0 >> 32), (uint32_t)v.w1,
-                   (uint32_t)(v.w1 >> 32), (uint32_t)v.w2, (uint32_t)(v.w2 >> 32)};
-#pragma unroll
-  for (int k = 0; k < 6; ++k) w[k] = __shfl_up(w[k], d, 64);
-  return u192{((uint64_t)w[1] << 32) | w[0], ((uint64_t)w[3] << 32) | w[2],
-              ((uint64_t)w[5] << 32) | w[4]};
-}
-
-__device__ __forceinline__ u192 shfl_xor_u192(u192 v, int m) {
-  uint32_t w[6] = {(uint32_t)v.w0, (uint32_t)(v.w0 >> 32), (uint32_t)v.w1,
-                   (uint32_t)(v.w1 >> 32), (uint32_t)v.w2, (uint32_t)(v.w2 >> 32)};
-#pragma unroll
-  for (int k = 0; k < 6; ++k) w[k] = __shfl_xor(w[k], m, 64);
-  return u192{((uint64_t)w[1] << 32) | w[0], ((uint64_t)w[3] << 32) | w[2],
-              ((uint64_t)w[5] << 32) | w[4]};
-}
-
-__device__ __forceinline__ u128 shfl_u128(u128 v, int src_lane) {
-  uint32_t w[4] = {(uint32_t)v, (uint32_t)(v >> 32), (uint32_t)(v >> 64), (uint32_t)(v >> 96)};
-#pragma unroll
-  for (int k = 0; k < 4; ++k) w[k] = __shfl(w[k], src_lane, 64);
-  return ((u128)w[3] << 96) | ((u128)w[2] << 64) | ((u128)w[1] << 32) | w[0];
-}
-
-// Inclusive prefix sum over the 64 lanes of a wave.
-__device__ __forceinline__ u192 wave_incl_scan_u192(u192 v) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const u192 o = shfl_up_u192(v, d);
-    if (lane >= d) v = add192(v, o);
-  }
-  return v;
-}
-
-__device__ u192 block_sum_u192(u192 v, u192* sh) {
-  for (int off = 32; off > 0; off >>= 1) v = add192(v, shfl_xor_u192(v, off));
-  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  if (lane == 0) sh[w] = v;
-  __syncthreads();
-  u192 s{0, 0, 0};
-  for (int i = 0; i < (int)(blockDim.x >> 6); ++i) s = add192(s, sh[i]);
-  __syncthreads();
+  s.r = (float)(u192_to_f64(s.gq) / u192_to_f64(s.gp));
   return s;
 }
 
-// The accept decision of sequence b, by wave 0 (lane i < K tests draft position i, all at
-// once; the first failing lane is the rejection), with the sampling rows' maxima and totals.
-// Lane l <= K also loads target row l's M and Z, so the bonus row's are at hand.
-__device__ Decision decide(const RejArgs& a, int b) {
-  const int K = a.K, T = K + 1, nt = a.B * T;
-  const int lane = threadIdx.x & 63;
-  bool reject = false;
-  u128 zp = 0, zq = 0;
-  float mp = 0.f, mq = 0.f;
-  if (lane <= K) {
-    const int rp = b * T + lane;
-    zp = a.zrow[rp];
-    mp = a.mrow[rp];
-  }
-  if (lane < K) {
-    const int rp = b * T + lane, rq = nt + b * K + lane;
-    const int64_t id = a.draft_ids[(size_t)b * K + lane];
-    zq = a.zrow[rq];
-    mq = a.mrow[rq];
-    const uint64_t wp = a.wtok[rp], wq = a.wtok[rq];
-    const uint32_t U = uniform_fix(a.u_accept[(size_t)b * K + lane]);
-    const u192 lhs = mul192x32(mul64x128(wq, zp), U);
-    const u192 rhs = shl24_192(mul64x128(wp, zq));
-    reject = !draft_id_ok(id, a.V) || gt192(lhs, rhs);
-  }
-  const uint64_t rej = __builtin_amdgcn_ballot_w64(reject);
-  Decision d;
-  d.acc = rej ? __builtin_ctzll(rej) : K;
-  if (d.acc < 64) {
-    d.zp = shfl_u128(zp, d.acc);
-    d.mp = __shfl(mp, d.acc, 64);
-  } else {  // the bonus row of K = 64 has no lane
-    d.zp = a.zrow[b * T + K];
-    d.mp = a.mrow[b * T + K];
-  }
-  if (d.acc < K) {
-    d.zq = shfl_u128(zq, d.acc);
-    d.mq = __shfl(mq, d.acc, 64);
-  } else {
-    d.zq = 0;
-    d.mq = 0.f;
-  }
-  return d;
+__device__ __forceinline__ bool gt192(u192 a, u192 b) {
+  if (a.w2 != b.w2) return a.w2 > b.w2;
+  if (a.w1 != b.w1) return a.w1 > b.w1;
+  return a.w0 > b.w0;
 }
 
-// Sampling: block (c, b) re-derives sequence b's decision (wave 0, then shared), adds the
-// residual (or bonus) mass of entries [2048 c, 2048 c + 2048) -- each thread a run of 8 inside
-// one contract chunk -- and publishes it. The last block of the sequence to finish (a counter
-// cleared by the row-totals kernel, bumped after a device-scope fence) then runs the inverse
-// CDF: wave 0 finds the 2048-entry block whose inclusive mass crosses the target (64 blocks per
-// scan window, carry between windows); each thread sums its run of that block (values held in
-// registers), a block-wide exclusive scan of the runs gives every thread its starting prefix,
-// and the thread whose run crosses reports the first crossing entry (atomicMin over the block).
-// The same block writes the sequence's outputs.
+// a * m for m < 2^32 (< 2^224, exact).
+__device__ __forceinline__ u256 mul192x32(u192 a, uint32_t m) { return mul192x64(a, m); }
+
+// Whether an entry after a rejection has residual weight, gp E^p > gq E^q, decided exactly.
+// In fp32, x = E^p and y = E^q r (r = gq / gp) are each within 4 roundings of 2^-24 of the
+// exact ratio's sides, so a margin of 2^-20 settles every pair that is not nearly tied; the
+// rest (and the NaN cases 0 * inf and 0 / 0, where both comparisons fail) compare the exact
+// products. An r outside fp32's normal range only meets E values of [0, 2^31] far from a
+// tie, where its lost precision cannot change the side.
 template <typename TT>
-__global__ __launch_bounds__(THREADS) void rej_sample_kernel(RejArgs a) {
-  const int b = (int)blockIdx.y, c = (int)blockIdx.x;
-  const int K = a.K, T = K + 1;
+__device__ __forceinline__ bool residual_positive(const SampleRow<TT>& s, uint32_t ep,
+                                                  uint32_t eq) {
+#pragma clang fp contract(off)
+  const float x = (float)ep, y = (float)eq * s.r;
+  if (x > y * (1.0f + 0x1p-20f)) return true;
+  if (y > x * (1.0f + 0x1p-20f)) return false;
+  return gt256(mul192x32(s.gp, ep), mul192x32(s.gq, eq));
+}
+
+// Exact sampling weight of one entry (scaled logits pv, qv).
+template <typename TT>
+__device__ __forceinline__ u256 weight_of(const SampleRow<TT>& s, float pv, float qv) {
+  const uint32_t ep = expfix_rel(pv, s.mp);
+  if (s.q == nullptr) {
+    const u128 w = (u128)s.fgp * ep;
+    return u256{(uint64_t)w, (uint64_t)(w >> 64), 0, 0};
+  }
+  const uint32_t eq = expfix_rel(qv, s.mq);
+  const u256 x = mul192x32(s.gp, ep), y = mul192x32(s.gq, eq);
+  return gt256(x, y) ? sub256(x, y) : kZero256;
+}
+
+// Sampling weight of the run's entries below V, exactly: after a rejection the sum of
+// gp E^p - gq E^q over the entries with positive residual equals gp (sum of their E^p) -
+// gq (sum of their E^q), so each entry costs its two exponentials, a membership test and two
+// 64-bit adds, and the wide products are formed once per run. The bonus row's weights
+// E^p F^p G^p sum to F^p G^p (sum of E^p).
+template <int N, typename TT>
+__device__ __forceinline__ u256 run_mass(const SampleRow<TT>& s, const RunVals<N>& r) {
+  uint64_t sp = 0, sq = 0;
+  if (s.q == nullptr) {
+#pragma unroll
+    for (int j = 0; j < N; ++j) sp += expfix_rel(r.p[j], s.mp);
+    const u128 w = (u128)s.fgp * sp;
+    return u256{(uint64_t)w, (uint64_t)(w >> 64), 0, 0};
+  }
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    const uint32_t ep = expfix_rel(r.p[j], s.mp);
+    const uint32_t eq = expfix_rel(r.q[j], s.mq);
+    if (residual_positive(s, ep, eq)) {
+      sp += ep;
+      sq += eq;
+    }
+  }
+  return sub256(mul192x64(s.gp, sp), mul192x64(s.gq, sq));
+}
+
+// Max of a run's values and the other lanes of its chunk (LANES adjacent lanes, 2 or 8).
+template <int LANES, int N>
+__device__ __forceinline__ float chunk_max(const float (&v)[N]) {
+  float m = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < N; ++j) m = fmaxf(m, v[j]);
+  return npn::row_max_dpp<LANES == 2 ? 1 : (LANES == 4 ? 2 : 3)>(m);
+}
+
+// Residual (or bonus) mass per 2048-entry sub-chunk of the sampling rows: block x holds the
+// 8192-entry contract block x (each wave one sub-chunk), each lane a run of 32 entries, the
+// lanes 2c, 2c + 1 of a wave forming chunk c of its sub-chunk (whose maxima they reduce
+// between them). The decision comes from the decide kernel. The wave's sum goes to cmass;
+// no barrier, and no block reads another's results (the pick kernel, launched after this
+// one, does).
+constexpr int MRUN = MCHK / 64;  // entries per lane of the mass kernel
+static_assert(2 * MRUN == CC, "two lanes per contract chunk");
+
+template <bool kUnitTemp, typename TT>
+__global__ __launch_bounds__(THREADS) void rej_mass_kernel(RejArgs a) {
+  const int b = (int)blockIdx.y;
+  const int lane = threadIdx.x & 63;
+  const int sub = (int)blockIdx.x * (THREADS / 64) + (int)(threadIdx.x >> 6);
+  if (sub >= a.nchm) return;  // the whole wave
+  const Decision d = a.dec[b];
+  const int K = a.K, T = K + 1, nt = a.B * T;
+  const int rp = b * T + d.acc, rq = nt + b * K + d.acc;
+  const TT* p = target_row<TT>(a, rp);
+  const float* q = d.acc < K ? a.draft + (size_t)(b * K + d.acc) * a.V : nullptr;
+  const float Mbp = a.bmax[(size_t)rp * a.nb + blockIdx.x];
+  const float Mbq = q != nullptr ? a.bmax[(size_t)rq * a.nb + blockIdx.x] : 0.f;
+  const int v0 = sub * MCHK + lane * MRUN;
+  const RunVals<MRUN> rv = load_run<MRUN, kUnitTemp>(a, p, q, v0);
+  const float mpc = chunk_max<2>(rv.p), mqc = chunk_max<2>(rv.q);
+  u256 m = kZero256;
+  if (v0 < a.V) m = run_mass<MRUN>(sample_row<TT>(d, p, q, mpc, mqc, Mbp, Mbq), rv);
+  m = wave_sum_u256(m);
+  if (lane == 0) a.cmass[(size_t)b * a.nchm + sub] = m;
+}
+
+// Inverse CDF, one block per sequence. Wave 0 loads the sequence's sub-chunk masses (lane l a
+// group of G = ceil(nchm / 64) consecutive ones); one scan of the group sums gives the total
+// and the group whose inclusive mass first crosses the target, whose masses (broadcast from
+// its lane) then locate the sub-chunk. Each thread sums its run of 8 entries of that
+// sub-chunk (8 threads per contract chunk); a block-wide exclusive scan of the runs finds the
+// run that crosses, whose 8 entries lanes 0..7 of wave 0 then weigh exactly and scan, the
+// first crossing lane giving the token.
+constexpr int kPickMaxGroup = 8;  // sub-chunk masses per lane: V <= 64 * 8 * 2048
+
+template <bool kUnitTemp, typename TT>
+__global__ __launch_bounds__(THREADS) void rej_pick_kernel(RejArgs a) {
+  const int b = (int)blockIdx.x;
+  const int K = a.K, T = K + 1, nt = a.B * T;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  __shared__ Decision s_dec;
-  __shared__ u192 sh[THREADS / 64];
-  __shared__ int s_last;
   __shared__ int s_chunk;
-  __shared__ u192 s_before;
-  __shared__ u192 s_target;
-  __shared__ u192 s_wtot[THREADS / 64];
+  __shared__ u256 s_before;
+  __shared__ u256 s_target;
+  __shared__ u256 s_wtot[THREADS / 64];
   __shared__ int s_tok;
   __shared__ int s_empty;
+  __shared__ int s_run;
+  __shared__ u256 s_cpre;
+  __shared__ float s_mc[2];
   __shared__ ArgPart s_best[THREADS / 64];
+  const Decision d = a.dec[b];
+  const u256* cm = a.cmass + (size_t)b * a.nchm;
   if (w == 0) {
-    const Decision d = decide(a, b);
-    if (lane == 0) s_dec = d;
-  }
-  __syncthreads();
-  const Decision d = s_dec;
-  {
-    const int v0 = c * MCHK + (int)threadIdx.x * PER_M;
-    u192 m{0, 0, 0};
-    if (v0 < a.V) {
-      const SampleRow<TT> s = sample_row<TT>(a, b, d, v0 / CC);
-      m = run_mass(s, load_run(a, s, v0), v0, a.V, a.inv_temp);
+    const int G = (a.nchm + 63) / 64;
+    u256 mv[kPickMaxGroup];
+#pragma unroll
+    for (int k = 0; k < kPickMaxGroup; ++k) {
+      const int c = lane * G + k;
+      mv[k] = (k < G && c < a.nchm) ? cm[c] : kZero256;
     }
-    m = block_sum_u192(m, sh);
-    if (threadIdx.x == 0) {
-      a.cmass[(size_t)b * a.nchm + c] = m;
-      __threadfence();  // the mass is visible device-wide before the count says so
-      s_last = atomicAdd(&a.cnt[b], 1u) == (unsigned)(a.nchm - 1);
-    }
-    __syncthreads();
-  }
-  if (!s_last) return;
-  __threadfence();  // every other block's mass, published before its count, is visible
-  const u192* cm = a.cmass + (size_t)b * a.nchm;
-  if (w == 0) {
-    u192 tot{0, 0, 0};
-    for (int k = lane; k < a.nchm; k += 64) tot = add192(tot, cm[k]);
-    tot = wave_incl_scan_u192(tot);
-    tot = shfl_u192(tot, 63);
-    if (lane == 0) s_empty = is_zero192(tot);
-    const u192 target = mul192x32(tot, uniform_fix(a.u_sample[b]));  // need 2^24 C > target
-    u192 carry{0, 0, 0};
+    u256 gsum = kZero256;
+#pragma unroll
+    for (int k = 0; k < kPickMaxGroup; ++k) gsum = add256(gsum, mv[k]);
+    const u256 incl = wave_incl_scan_u256(gsum);
+    const u256 tot = shfl_u256(incl, 63);
+    const u256 target = mul256x32(tot, uniform_fix(a.u_sample[b]));  // need 2^24 C > target
+    // a positive total always crosses (U < 2^24); with none the chunk is unused
+    const uint64_t hit = __builtin_amdgcn_ballot_w64(gt256(shl24_256(incl), target));
     int chunk = a.nchm - 1;
-    u192 before{0, 0, 0};
-    bool found = false;
-    for (int c0 = 0; c0 < a.nchm && !found; c0 += 64) {
-      const int k = c0 + lane;
-      const u192 m = k < a.nchm ? cm[k] : u192{0, 0, 0};
-      const u192 incl = add192(wave_incl_scan_u192(m), carry);
-      const uint64_t hit =
-          __builtin_amdgcn_ballot_w64(k < a.nchm && gt192(shl24_192(incl), target));
-      if (hit != 0) {
-        const int l = __builtin_ctzll(hit);
-        chunk = c0 + l;
-        before = shfl_u192(sub192(incl, m), l);
-        found = true;
+    u256 before = kZero256;
+    if (hit != 0) {
+      const int l = __builtin_ctzll(hit);
+      u256 run = shfl_u256(sub256(incl, gsum), l);  // mass before lane l's group
+      bool found = false;
+#pragma unroll
+      for (int k = 0; k < kPickMaxGroup; ++k) {
+        const u256 mk = shfl_u256(mv[k], l);
+        const u256 next = add256(run, mk);
+        if (k < G && !found && gt256(shl24_256(next), target)) {
+          chunk = l * G + k;
+          before = run;
+          found = true;
+        }
+        run = next;
       }
-      carry = shfl_u192(incl, 63);
     }
-    // (selected limb by limb: a select of whole structs went through private memory)
-    const u192 bsel{found ? before.w0 : carry.w0, found ? before.w1 : carry.w1,
-                    found ? before.w2 : carry.w2};
     if (lane == 0) {
+      s_empty = is_zero256(tot);
       s_chunk = chunk;
-      s_before = bsel;
+      s_before = before;
       s_target = target;
-      s_tok = 0x7FFFFFFF;
+      s_run = 0;
+      s_cpre = before;
     }
   }
   __syncthreads();
   const int acc = d.acc;
+  const int rp = b * T + acc, rq = nt + b * K + acc;
+  const TT* p = target_row<TT>(a, rp);
+  const float* q = acc < K ? a.draft + (size_t)(b * K + acc) * a.V : nullptr;
   int tok;
   if (s_empty) {
     // No sampling mass: every weight of the sampling row is 0, which happens only for a
@@ -838,7 +938,6 @@ __global__ __launch_bounds__(THREADS) void rej_sample_kernel(RejArgs a) {
     // test always has mass). The token is then the target row's greedy choice: its argmax,
     // NaN counting as the maximum and ties going to the lowest index (the order of
     // argmax_chunk_kernel).
-    const TT* p = target_row<TT>(a, b * T + acc);
     float bv = -INFINITY;
     int bi = 0x7FFFFFFF;
     for (int v = (int)threadIdx.x; v < a.V; v += THREADS) {
@@ -857,55 +956,66 @@ __global__ __launch_bounds__(THREADS) void rej_sample_kernel(RejArgs a) {
       if (beats(s_best[k].v, s_best[k].i, best.v, best.i)) best = s_best[k];
     tok = best.i;
   } else {
-    const int chunk = s_chunk;
-    const int v0 = chunk * MCHK + (int)threadIdx.x * PER_M;
-    RunVals rv;
-    u192 run{0, 0, 0};
-    SampleRow<TT> s;
-    if (v0 < a.V) {
-      s = sample_row<TT>(a, b, d, v0 / CC);
-      rv = load_run(a, s, v0);
-      run = run_mass(s, rv, v0, a.V, a.inv_temp);
-    }
-    const u192 incl = wave_incl_scan_u192(run);
+    const int sub = s_chunk;
+    const int blk = sub / (npn::kContractBlock / MCHK);
+    const float Mbp = a.bmax[(size_t)rp * a.nb + blk];
+    const float Mbq = q != nullptr ? a.bmax[(size_t)rq * a.nb + blk] : 0.f;
+    const int v0 = sub * MCHK + (int)threadIdx.x * PER_M;
+    const RunVals<PER_M> rv = load_run<PER_M, kUnitTemp>(a, p, q, v0);
+    const float mpc = chunk_max<8>(rv.p), mqc = chunk_max<8>(rv.q);
+    u256 run = kZero256;
+    if (v0 < a.V) run = run_mass<PER_M>(sample_row<TT>(d, p, q, mpc, mqc, Mbp, Mbq), rv);
+    const u256 incl = wave_incl_scan_u256(run);
     if (lane == 63) s_wtot[w] = incl;
     __syncthreads();
-    u192 cpre = add192(s_before, sub192(incl, run));
-    for (int k = 0; k < w; ++k) cpre = add192(cpre, s_wtot[k]);
-    const u192 target = s_target;
-    if (v0 < a.V && gt192(shl24_192(add192(cpre, run)), target)) {  // crossing in this run
-#pragma unroll
-      for (int j = 0; j < PER_M; ++j) {
-        const int v = v0 + j;
-        if (v >= a.V) break;
-        const u192 wv = weight_of(s, rv.p[j], rv.q[j], a.inv_temp);
-        cpre = add192(cpre, wv);
-        if (!is_zero192(wv) && gt192(shl24_192(cpre), target)) {
-          atomicMin(&s_tok, v);
-          break;
-        }
+    u256 cpre = add256(s_before, sub256(incl, run));
+    for (int k = 0; k < w; ++k) cpre = add256(cpre, s_wtot[k]);
+    const u256 target = s_target;
+    // the one run that crosses: the target not passed before it, passed at its end (a run
+    // mass is the exact sum of its entries' weights, so the crossing entry lies in it)
+    if (v0 < a.V && !gt256(shl24_256(cpre), target) &&
+        gt256(shl24_256(add256(cpre, run)), target)) {
+      s_run = (int)threadIdx.x;
+      s_cpre = cpre;
+      s_mc[0] = mpc;
+      s_mc[1] = mqc;
+    }
+    __syncthreads();
+    // that run's entries weighed exactly, one per lane of wave 0, then scanned
+    if (w == 0) {
+      const int rv0 = sub * MCHK + s_run * PER_M;
+      const int v = rv0 + (lane & (PER_M - 1));
+      u256 wv = kZero256;
+      if (lane < PER_M && v < a.V) {
+        const SampleRow<TT> s = sample_row<TT>(d, p, q, s_mc[0], s_mc[1], Mbp, Mbq);
+        const float pv = kUnitTemp ? elem(p, v) : scaled(elem(p, v), a.inv_temp);
+        const float qv = q == nullptr ? NAN : (kUnitTemp ? q[v] : scaled(q[v], a.inv_temp));
+        wv = weight_of(s, pv, qv);
       }
+#pragma unroll
+      for (int dd = 1; dd < PER_M; dd <<= 1) {  // inclusive scan over lanes 0..7
+        const u256 o = shfl_up_u256(wv, dd);
+        if ((lane & (PER_M - 1)) >= dd) wv = add256(wv, o);
+      }
+      const u256 c = add256(s_cpre, wv);
+      const uint64_t hit = __builtin_amdgcn_ballot_w64(lane < PER_M && v < a.V &&
+                                                        gt256(shl24_256(c), target));
+      if (lane == 0) s_tok = rv0 + (hit ? __builtin_ctzll(hit) : 0);
     }
     __syncthreads();
     tok = s_tok;
   }
-  if (threadIdx.x == 0) a.accepted[b] = acc;
-  for (int t = (int)threadIdx.x; t < T; t += THREADS) {
-    int64_t id = -1;
-    if (t < acc) id = a.draft_ids[(size_t)b * K + t];
-    else if (t == acc) id = tok;
-    a.out_ids[(size_t)b * T + t] = id;
-  }
+  if (threadIdx.x == 0) a.out_ids[(size_t)b * T + acc] = tok;
 }
 
 // Workspace of the acceptance calls. The per-row Z sums come first and the row maxima second:
 // the header documents both as results that the rejection call leaves in the workspace.
 struct WsLayout {
-  size_t zrow, mrow, wtok, cmax, csum, cmass, cnt, total;
+  size_t zrow, mrow, bmax, bsum, dec, cmass, total;
 };
 
 WsLayout layout(int B, int K, int V) {
-  const int nc = (V + CC - 1) / CC;
+  const int nb = (V + npn::kContractBlock - 1) / npn::kContractBlock;
   const int nch = (V + CHK - 1) / CHK;
   const size_t rows = (size_t)B * (2 * K + 1);
   auto up = [](size_t x) { return (x + 255) & ~size_t(255); };
@@ -913,14 +1023,13 @@ WsLayout layout(int B, int K, int V) {
   size_t o = 0;
   l.zrow = o; o += up(rows * sizeof(u128));
   l.mrow = o; o += up(rows * sizeof(float));
-  l.wtok = o; o += up(rows * sizeof(uint64_t));
-  // chunk maxima; the greedy path's argmax partials share the region
-  const size_t cmax_bytes = rows * nc * sizeof(float);
+  // block maxima; the greedy path's argmax partials share the region
+  const size_t bmax_bytes = rows * nb * sizeof(float);
   const size_t part_bytes = (size_t)B * (K + 1) * nch * sizeof(ArgPart);
-  l.cmax = o; o += up(cmax_bytes > part_bytes ? cmax_bytes : part_bytes);
-  l.csum = o; o += up(rows * nc * sizeof(uint64_t));
-  l.cmass = o; o += up((size_t)B * ((V + MCHK - 1) / MCHK) * sizeof(u192));
-  l.cnt = o; o += up((size_t)B * sizeof(uint32_t));
+  l.bmax = o; o += up(bmax_bytes > part_bytes ? bmax_bytes : part_bytes);
+  l.bsum = o; o += up(rows * nb * sizeof(u128));
+  l.dec = o; o += up((size_t)B * sizeof(Decision));
+  l.cmass = o; o += up((size_t)B * ((V + MCHK - 1) / MCHK) * sizeof(u256));
   l.total = o;
   return l;
 }
@@ -946,7 +1055,7 @@ extern "C" int npn_accept_greedy(const float* target_logits, const int64_t* draf
   NPN_REQUIRE(NPN_ALIGNED16(workspace), NPN_ERR_ALIGN);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int nch = (V + CHK - 1) / CHK;
-  ArgPart* part = reinterpret_cast<ArgPart*>(static_cast<uint8_t*>(workspace) + l.cmax);
+  ArgPart* part = reinterpret_cast<ArgPart*>(static_cast<uint8_t*>(workspace) + l.bmax);
   const bool vec4 = V % 4 == 0 && NPN_ALIGNED16(target_logits);
   hipLaunchKernelGGL(argmax_chunk_kernel, dim3(nch, B * (K + 1)), dim3(THREADS), 0, s,
                      target_logits, part, V, nch, vec4);
@@ -966,8 +1075,8 @@ int rejection_args_ok(const void* target_logits, const float* draft_logits,
                   out_ids,
               NPN_ERR_NULL);
   NPN_REQUIRE(shape_ok(B, K, V), NPN_ERR_SHAPE);
-  // Z <= V 2^62 <= 2^82 and every residual sum at most 2^164 for V <= 2^20, so the
-  // contract's products stay below 2^192
+  // Z <= V 2^93 <= 2^113 and every residual sum at most 2^226 for V <= 2^20, so the
+  // contract's products stay below 2^256
   NPN_REQUIRE(V <= kRejMaxV, NPN_ERR_SHAPE);
   NPN_REQUIRE(inv_temperature > 0.0f && inv_temperature < 1e30f, NPN_ERR_VALUE);
   return NPN_OK;
@@ -982,32 +1091,41 @@ RejArgs rej_args(const void* target_logits, const float* draft_logits, const int
   const bool vec4 = V % (bf16_target ? 8 : 4) == 0 && NPN_ALIGNED16(target_logits) &&
                     NPN_ALIGNED16(draft_logits);
   return RejArgs{target_logits, draft_logits, draft_ids, u_accept, u_sample, inv_temperature,
-                 accepted, out_ids, B, K, V, (V + CC - 1) / CC, (V + MCHK - 1) / MCHK, vec4,
+                 accepted, out_ids, B, K, V,
+                 (V + npn::kContractBlock - 1) / npn::kContractBlock, (V + MCHK - 1) / MCHK, vec4,
                  reinterpret_cast<u128*>(ws + l.zrow), reinterpret_cast<float*>(ws + l.mrow),
-                 reinterpret_cast<uint64_t*>(ws + l.wtok), reinterpret_cast<float*>(ws + l.cmax),
-                 reinterpret_cast<uint64_t*>(ws + l.csum), reinterpret_cast<u192*>(ws + l.cmass),
-                 reinterpret_cast<uint32_t*>(ws + l.cnt)};
+                 reinterpret_cast<float*>(ws + l.bmax), reinterpret_cast<u128*>(ws + l.bsum),
+                 reinterpret_cast<Decision*>(ws + l.dec), reinterpret_cast<u256*>(ws + l.cmass)};
 }
 
-// Chunk statistics of `rows` fp32 rows starting at row0.
+// Block statistics of `rows` fp32 rows starting at row0.
 void launch_stats(const RejArgs& a, int row0, int rows, hipStream_t s) {
-  const dim3 grid((a.V + SBLK - 1) / SBLK, rows);
+  const dim3 grid(a.nb, rows);
   if (a.inv_temp == 1.0f)
     hipLaunchKernelGGL(rej_stats_kernel<true>, grid, dim3(THREADS), 0, s, a, row0);
   else
     hipLaunchKernelGGL(rej_stats_kernel<false>, grid, dim3(THREADS), 0, s, a, row0);
 }
 
-// Row totals and sampling (every row's chunk statistics in place). TT is the target rows'
-// element type: float, or bf16 bits (uint16_t) for the LM-head form.
+// Decision, sampling mass and pick (every row's block statistics in place). TT is the target
+// rows' element type: float, or bf16 bits (uint16_t) for the LM-head form.
 template <typename TT>
 int launch_decide_sample(const RejArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL(rej_rowtotal_kernel<TT>, dim3(a.B * (2 * a.K + 1)), dim3(THREADS), 0, s, a);
-  hipLaunchKernelGGL(rej_sample_kernel<TT>, dim3(a.nchm, a.B), dim3(THREADS), 0, s, a);
+  const int rows = 2 * a.K + 1;
+  hipLaunchKernelGGL(rej_decide_kernel<TT>, dim3(a.B), dim3(64 * (rows < 16 ? rows : 16)), 0, s,
+                     a);
+  const dim3 mgrid((a.nchm + THREADS / 64 - 1) / (THREADS / 64), a.B);
+  if (a.inv_temp == 1.0f) {
+    hipLaunchKernelGGL((rej_mass_kernel<true, TT>), mgrid, dim3(THREADS), 0, s, a);
+    hipLaunchKernelGGL((rej_pick_kernel<true, TT>), dim3(a.B), dim3(THREADS), 0, s, a);
+  } else {
+    hipLaunchKernelGGL((rej_mass_kernel<false, TT>), mgrid, dim3(THREADS), 0, s, a);
+    hipLaunchKernelGGL((rej_pick_kernel<false, TT>), dim3(a.B), dim3(THREADS), 0, s, a);
+  }
   return npn_launch_status();
 }
 
-// The three rejection kernels over fp32 logits on `stream`, with the workspace at `ws`
+// The four rejection kernels over fp32 logits on `stream`, with the workspace at `ws`
 // (layout(B, K, V).total bytes, 16-byte aligned, checked by the caller).
 int rejection_launch(const float* target_logits, const float* draft_logits,
                      const int64_t* draft_ids, const float* u_accept, const float* u_sample,
@@ -1024,8 +1142,7 @@ int rejection_launch(const float* target_logits, const float* draft_logits,
 // copy, at its own address, for the life of the process. In host code `scratch` names a host
 // stand-in, not device memory: kernels get the address hipGetSymbolAddress returns for the
 // device they run on (scratch_on_device), never the array's name. Nothing in it needs clearing
-// between calls: every word a call reads was written earlier in the same call (the counters of
-// the sampling kernel are cleared by the row-totals kernel before it).
+// between calls: every word a call reads was written earlier in the same call.
 constexpr size_t kScratchBytes = (size_t)NPN_ACCEPT_SCRATCH_BYTES;
 __device__ __align__(256) uint8_t scratch[kScratchBytes];
 
@@ -1121,10 +1238,30 @@ extern "C" int npn_argmax_parts(const void* parts, int nparts, int64_t* ids, flo
 // statistics pass covers only the draft rows, and the sampling kernel re-reads only each
 // sequence's sampling row. The decisions equal npn_accept_rejection's on the same logits cast
 // to fp32 (every step of the contract sees the same values).
+namespace {
+
+// The LM-head call's workspace: the acceptance layout, then the GEMM epilogue's chunk
+// statistics of the target rows ([M][V / 64] maxima and sums).
+struct LmLayout {
+  size_t cmax, csum, total;
+};
+
+LmLayout lm_layout(int B, int K, int V) {
+  auto up = [](size_t x) { return (x + 255) & ~size_t(255); };
+  const size_t rows = (size_t)B * (K + 1), nc = (size_t)V / CC;
+  LmLayout l{};
+  l.cmax = up(layout(B, K, V).total);
+  l.csum = l.cmax + up(rows * nc * sizeof(float));
+  l.total = l.csum + up(rows * nc * sizeof(uint64_t));
+  return l;
+}
+
+}  // namespace
+
 extern "C" size_t npn_accept_rejection_lm_head_workspace_size(int B, int K, int H, int V) {
   if (!shape_ok(B, K, V) || V > kRejMaxV) return 0;
   if (!npn::fp8_matmul_chunk_stats_ok(B * (K + 1), H, V)) return 0;  // GEMM shape rules
-  return layout(B, K, V).total;
+  return lm_layout(B, K, V).total;
 }
 
 extern "C" int npn_accept_rejection_lm_head(const uint16_t* hidden, const int8_t* lm_head_w,
@@ -1147,12 +1284,17 @@ extern "C" int npn_accept_rejection_lm_head(const uint16_t* hidden, const int8_t
   NPN_REQUIRE(NPN_ALIGNED16(hidden) && NPN_ALIGNED16(lm_head_w) && NPN_ALIGNED16(target_logits),
               NPN_ERR_ALIGN);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  const LmLayout ll = lm_layout(B, K, V);
+  float* cmax = reinterpret_cast<float*>(ws + ll.cmax);
+  uint64_t* csum = reinterpret_cast<uint64_t*>(ws + ll.csum);
   const RejArgs a = rej_args(target_logits, draft_logits, draft_ids, u_accept, u_sample,
-                             inv_temperature, accepted, out_ids, B, K, V, true,
-                             static_cast<uint8_t*>(workspace));
+                             inv_temperature, accepted, out_ids, B, K, V, true, ws);
   launch_stats(a, M, B * K, s);  // draft rows
   const int gst = npn::fp8_matmul_chunk_stats(hidden, lm_head_w, lm_head_scale, target_logits,
-                                              a.cmax, a.csum, inv_temperature, M, H, V, s);
+                                              cmax, csum, inv_temperature, M, H, V, s);
   if (gst != NPN_OK) return gst;
+  hipLaunchKernelGGL(rej_block_from_chunks_kernel, dim3(a.nb, M), dim3(CPB), 0, s, a, 0, cmax,
+                     csum, V / CC);
   return launch_decide_sample<uint16_t>(a, s);
 }

@@ -20,28 +20,33 @@ and q(x) > 0 = p(x) (always reject, residual = p restricted to p > q)
 (tests/test_oracle_accept.py).
 
 Integer softmax contract (shared bit-for-bit with ``csrc/spec_accept.hip``), built so
-that one pass over the logits gives every sum (each vocabulary chunk's values are
-referred to the chunk's own maximum, and chunks to the row maximum by exact factors):
+that one pass over the logits gives every sum, in three levels: each vocabulary chunk's
+values are referred to the chunk's own maximum, each chunk to its block's maximum and each
+block to the row maximum, by exact integer factors:
 - s_v = t_v * inv_temp (fp32 multiply). The vocabulary is cut into chunks of CHUNK = 64
-  entries; m_c = max of the non-NaN s_v of chunk c (-inf if none), M = max_c m_c. (64
-  divides every column group of the LM-head GEMM, whose epilogue produces m_c and S_c of
-  the target rows while their logits are still in registers.)
+  entries and blocks of BLOCK = 8192 entries (128 chunks); m_c = max of the non-NaN s_v of
+  chunk c (-inf if none), M_b = max of block b's m_c, M = max_b M_b. (64 divides every
+  column group of the LM-head GEMM, whose epilogue produces m_c and S_c of the target rows
+  while their logits are still in registers; the block level lets one pass over plain
+  logits write only 20 bytes per block.)
 - E_v = floor(2^31 * exp_c(s_v - m_c)) for v in chunk c (fp32 subtraction; NaN gives 0),
-  F_c = floor(2^31 * exp_c(m_c - M)), both below 2^31 + 1, with exp_c the fp32
-  Cody-Waite reduction + degree-7 Taylor polynomial below, evaluated with correctly
-  rounded fp32 fused multiply-adds (IEEE-754 fusedMultiplyAdd), so every step is one
-  IEEE-754 operation that CPU and GPU round identically.
-- The weight of v is W_v = E_v * F_c (an integer below 2^62 + 1) and the row's total is
-  Z = sum_v W_v = sum_c F_c * S_c with S_c = sum_{v in c} E_v, in exact integers
-  (order-independent; Z <= V * 2^62 <= 2^82 for V <= 2^20). W_v / Z approximates
-  softmax(s)_v to about 2^-30 relative for every entry within 21 of its chunk maximum
-  whose chunk maximum is within 21 of M.
+  F_c = floor(2^31 * exp_c(m_c - M_b)) for c in block b, G_b = floor(2^31 * exp_c(M_b - M)),
+  each at most 2^31, with exp_c the fp32 Cody-Waite reduction + degree-7 Taylor polynomial
+  below, evaluated with correctly rounded fp32 fused multiply-adds (IEEE-754
+  fusedMultiplyAdd), so every step is one IEEE-754 operation that CPU and GPU round
+  identically.
+- The weight of v is W_v = E_v * F_c * G_b (an integer of at most 2^93) and the row's total
+  is Z = sum_v W_v = sum_b G_b * S_b with S_b = sum_{c in b} F_c * S_c and
+  S_c = sum_{v in c} E_v, in exact integers (order-independent; Z <= V * 2^93 <= 2^113 for
+  V <= 2^20). W_v / Z approximates softmax(s)_v to about 2^-29 relative for every entry
+  within 21 of its chunk maximum, in a chunk within 21 of its block maximum, in a block
+  within 21 of M.
 - p(v) = W^p_v / Z_p, q(v) = W^q_v / Z_q. Uniforms u are read as U = floor(u * 2^24).
 - Accept draft x at position i iff U * W^q_x * Z_p <= 2^24 * W^p_x * Z_q
-  (integers below 2^169).
+  (integers below 2^231).
 - At the first rejection sample from R_v = max(0, W^p_v Z_q - W^q_v Z_p); if all
   K drafts are accepted sample the bonus from R_v = W^p_v of row K. The token is
-  the smallest v with 2^24 * sum_{w<=v} R_w > U_s * sum_w R_w (integers below 2^189).
+  the smallest v with 2^24 * sum_{w<=v} R_w > U_s * sum_w R_w (integers below 2^251).
 - Draft ids outside [0, V) are never accepted: such a position is a rejection whatever the
   uniform, and its token is sampled from the residual R as for any rejection (greedy
   acceptance rejects them too, since an argmax is always in range). Emitted ids therefore
@@ -118,6 +123,7 @@ def expfix(x):
 
 
 CHUNK = 64                                       # vocabulary entries per chunk
+BLOCK = 8192                                     # vocabulary entries per block (128 chunks)
 
 
 def row_chunks(logits_row, inv_temp=1.0):
@@ -135,15 +141,36 @@ def row_chunks(logits_row, inv_temp=1.0):
     return s, m, S, E.reshape(-1)[:V]
 
 
-def row_weights(logits_row, inv_temp=1.0):
-    """(W [V] uint64, Z python int, M fp32) for one logits row under the contract:
-    W_v = E_v * F_c (below 2^62 + 1, exact in uint64), Z = sum_c F_c * S_c, M the row max."""
+def row_blocks(logits_row, inv_temp=1.0):
+    """(m [nch] chunk maxima, F [nch] uint32 chunk factors, Mb [nb] block maxima,
+    Sb [nb] python ints, E [V] uint32) of one row: F_c = expfix(m_c - M_b),
+    S_b = sum_{c in b} F_c * S_c."""
     _, m, S, E = row_chunks(logits_row, inv_temp)
-    M = np.fmax.reduce(m, initial=_F(-np.inf))
+    cpb = BLOCK // CHUNK
+    nch = m.shape[0]
+    nb = (nch + cpb - 1) // cpb
+    mp = np.full(nb * cpb, -np.inf, np.float32)
+    mp[:nch] = m
+    Mb = np.fmax.reduce(mp.reshape(nb, cpb), axis=1, initial=_F(-np.inf)).astype(np.float32)
     with np.errstate(invalid="ignore"):
-        F = expfix((m - M).astype(np.float32))
-    Z = sum(int(f) * sc for f, sc in zip(F.tolist(), S))
-    W = E.astype(np.uint64) * np.repeat(F.astype(np.uint64), CHUNK)[:E.shape[0]]
+        F = expfix((m - np.repeat(Mb, cpb)[:nch]).astype(np.float32))
+    Fi, Si = F.tolist(), S
+    Sb = [sum(Fi[c] * Si[c] for c in range(b * cpb, min(nch, (b + 1) * cpb))) for b in range(nb)]
+    return m, F, Mb, Sb, E
+
+
+def row_weights(logits_row, inv_temp=1.0):
+    """(W [V] python ints (object array), Z python int, M fp32) for one logits row under the
+    contract: W_v = E_v * F_c * G_b (at most 2^93), Z = sum_b G_b * S_b, M the row max."""
+    m, F, Mb, Sb, E = row_blocks(logits_row, inv_temp)
+    M = np.fmax.reduce(Mb, initial=_F(-np.inf))
+    with np.errstate(invalid="ignore"):
+        G = expfix((Mb - M).astype(np.float32))
+    Gi = G.tolist()
+    Z = sum(g * sb for g, sb in zip(Gi, Sb))
+    cpb = BLOCK // CHUNK
+    FG = np.array([f * Gi[c // cpb] for c, f in enumerate(F.tolist())], dtype=object)
+    W = E.astype(object) * np.repeat(FG, CHUNK)[:E.shape[0]]
     return W, Z, M
 
 

@@ -279,33 +279,47 @@ def test_empty_rows_pass_the_accept_test():
 
 
 def test_multichunk_weights_follow_softmax():
-    """With several 64-entry chunks whose maxima differ (the row maximum in chunk 2, one
-    chunk 40 below it), the contract's p = W / Z equals float64 softmax(s) to the contract's
-    precision (2^-19 relative + 2^-29 absolute), Z is exactly the sum of the weights, the top chunk's weights are E * 2^31, and
-    the far chunk gets weight 0. A factor taken against the wrong maximum, or a chunk left out
-    of Z, moves p by orders of magnitude more than the bound."""
+    """Rows over several 8192-entry blocks of 64-entry chunks whose maxima differ: inside
+    block 1 one chunk 6 below, one 8 above (the row maximum) and one 40 below (factor F = 0);
+    block 2 6 below the others and block 3, a partial one, 40 below (factor G = 0). The
+    contract's p = W / Z equals float64 softmax(s) to its precision (2^-19 relative + 2^-29
+    absolute), Z is exactly the sum of the weights, the top chunk's weights are E * 2^62 (both
+    of its factors 2^31) and the far chunk and block get weight 0. A factor taken against the
+    wrong maximum, a chunk or block left out of Z, or a level skipped moves p by orders of
+    magnitude more than the bound."""
     rng = np.random.default_rng(5)
-    C = oa.CHUNK
-    V = 4 * C + 1000
+    C, BL = oa.CHUNK, oa.BLOCK
+    V = 3 * BL + 500
     t = rng.normal(0.0, 2.0, V).astype(np.float32)
-    t[C:2 * C] -= 6.0            # chunk 1 below the others
-    t[2 * C:3 * C] += 3.0        # the row maximum lives in chunk 2
-    t[3 * C:4 * C] -= 40.0       # a chunk whose factor is 0
+    b1 = BL
+    t[b1 + C:b1 + 2 * C] -= 6.0          # a chunk below the others of block 1
+    t[b1 + 2 * C:b1 + 3 * C] += 8.0      # the row maximum lives in chunk 2 of block 1
+    t[b1 + 3 * C:b1 + 4 * C] -= 40.0     # a chunk whose factor is 0
+    t[2 * BL:3 * BL] -= 6.0              # a block below the others
+    t[3 * BL:] -= 40.0                   # a (partial) block whose factor is 0
     for inv_t in (1.0, 0.7):
         W, Z, M = oa.row_weights(t, inv_t)
-        assert Z == int(W.astype(object).sum())
+        assert Z == int(W.sum())
         s = (t * np.float32(inv_t)).astype(np.float32).astype(np.float64)
         ref = np.exp(s - s.max())
         ref /= ref.sum()
         p = np.array([int(w) / Z for w in W.tolist()])
         # each factor is exp to ~2^-21 relative plus one unit of flooring: |dp| is at most
-        # about 2^-20 p + 2^31 / Z, with Z >= 2^62 (the row maximum's own weight)
+        # about 3 * 2^-21 p + 3 * 2^62 / Z, with Z >= 2^93 (the row maximum's own weight)
         assert np.all(np.abs(p - ref) <= 2.0 ** -19 * ref + 2.0 ** -29)
-        assert np.all(W[3 * C:4 * C] == 0)
+        assert np.all(W[b1 + 3 * C:b1 + 4 * C] == 0) and np.all(W[3 * BL:] == 0)
+        assert np.all(W[2 * BL:3 * BL] > 0)
         _, m, S, E = oa.row_chunks(t, inv_t)
-        assert M == m.max() and np.argmax(m) == 2
-        top = W[2 * C:3 * C]
-        assert np.array_equal(top, E[2 * C:3 * C].astype(np.uint64) << np.uint64(31))
+        assert M == m.max() and np.argmax(m) == b1 // C + 2
+        top = W[b1 + 2 * C:b1 + 3 * C]
+        assert np.array_equal(top, E[b1 + 2 * C:b1 + 3 * C].astype(object) << 62)
+        # the levels: every chunk factor refers to its block's maximum, every block to M
+        m2, F, Mb, Sb, E2 = oa.row_blocks(t, inv_t)
+        assert np.array_equal(E2, E) and np.array_equal(m2, m)
+        cpb = BL // C
+        for b in range(len(Mb)):
+            assert Mb[b] == m[b * cpb:(b + 1) * cpb].max()
+            assert Sb[b] == sum(int(F[c]) * int(S[c]) for c in range(b * cpb, min(len(m), (b + 1) * cpb)))
 
 
 def test_multichunk_p_equals_q_accepts_and_residual_is_valid():

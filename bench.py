@@ -587,7 +587,8 @@ LM_MIN_WARMUP = 64
 def lm_head_bench(args):
     """LM head [B*T, 5120] x [5120, 248320] fp8 + greedy acceptance: fused (row argmax in the
     GEMM epilogue, no logits) vs the GEMM writing bf16 logits, a float cast and
-    accept_greedy. Two weight copies (2.5 GB) alternate so the weights come from HBM."""
+    accept_greedy; the same for rejection sampling; and the bare GEMM for reference. Two weight
+    copies (2.5 GB) alternate so the weights come from HBM."""
     import torch
     from spec_verify_step import HIDDEN, random_fp8_linear
     dev = "cuda"
@@ -605,9 +606,13 @@ def lm_head_bench(args):
         logits = torch.ops.fp8.matmul(x, w, sc).float().view(B, T, LM_VOCAB)
         return torch.ops.spec.accept_greedy(logits, drafts)
 
+    def gemm(i):  # the bare LM-head GEMM writing bf16 logits, for reference
+        w, sc = ws[i % 2]
+        return torch.ops.fp8.matmul(x, w, sc)
+
     res = {}
     warmup = max(args.warmup, LM_MIN_WARMUP)
-    for name, fn in (("fused", fused), ("unfused", unfused)):
+    for name, fn in (("gemm", gemm), ("fused", fused), ("unfused", unfused)):
         for i in range(warmup):
             fn(i)
         torch.cuda.synchronize()
@@ -621,9 +626,10 @@ def lm_head_bench(args):
     a_f, o_f = fused(0)
     a_u, o_u = unfused(0)
 
-    # Rejection sampling at temperature 1 over the same LM head: the fused op (GEMM writing
-    # bf16 logits and row-group maxima, sampling passes over bf16 target rows without a max
-    # pass over them) against the GEMM, a float cast and accept_rejection.
+    # Rejection sampling at temperature 1 over the same LM head: the fused op (the GEMM writes
+    # bf16 logits and, in its epilogue, the contract's 64-column chunk statistics, so only the
+    # draft rows get a statistics pass and of the target rows only the sampling rows are read
+    # back) against the GEMM, a float cast and accept_rejection.
     draft = torch.randn(B, K, LM_VOCAB, generator=g, device=dev)
     rids = torch.randint(0, LM_VOCAB, (B, K), generator=g, device=dev)
     u = torch.rand(B, K, generator=g, device=dev)
@@ -655,6 +661,7 @@ def lm_head_bench(args):
     print(json.dumps({
         "workload": f"LM head [{B * T}x{HIDDEN}]x[{HIDDEN}x{LM_VOCAB}] fp8 + greedy acceptance, "
                     f"B={B}, K={K}",
+        "gemm_ms": round(res["gemm"], 4),
         "fused_ms": round(res["fused"], 4), "unfused_ms": round(res["unfused"], 4),
         "fused_tflops": round(flops / res["fused"] / 1e9, 1),
         "weights_gb": round(HIDDEN * LM_VOCAB / 1e9, 3),
@@ -663,6 +670,7 @@ def lm_head_bench(args):
             "workload": "the same LM head + rejection sampling at temperature 1 against "
                         f"[{B}, {K}, {LM_VOCAB}] fp32 draft logits",
             "fused_ms": round(res["rej_fused"], 4), "unfused_ms": round(res["rej_unfused"], 4),
+            "fused_over_gemm": round(res["rej_fused"] / res["gemm"], 4),
             "identical": bool(torch.equal(ra_f, ra_u) and torch.equal(ro_f, ro_u))},
         "steps": args.steps, "warmup": warmup}))
 

@@ -322,10 +322,11 @@ int npn_accept_greedy(const float* target_logits, const int64_t* draft_ids, int3
  *   target_logits [B, K+1, V] f32, draft_logits [B, K, V] f32, draft_ids [B, K]
  *   int64, u_accept [B, K] f32 in [0,1), u_sample [B] f32 in [0,1),
  *   inv_temperature > 0 (logits are multiplied by it), V <= 2^20.
- * Four launches: the one pass over the logits (every row's block maxima M_b and sums S_b;
- * the chunk statistics stay on chip), the row totals and the decision (one workgroup per
- * sequence), the residual (or bonus) mass per 2048 entries of each sequence, and the inverse
- * CDF (one workgroup per sequence).
+ * Three launches: the one pass over the logits (every row's block maxima M_b and sums S_b,
+ * and the draft token's E*F; the chunk statistics stay on chip), the residual (or bonus) mass
+ * per 64 and per 2048 entries of each sequence's sampling rows (each workgroup first works
+ * the row totals and the decision out from the block statistics), and the inverse CDF (one
+ * workgroup per sequence).
  * On return the workspace starts with every row's Z (unsigned 128-bit, low 64-bit word
  * first [R]) and, at byte offset 16R rounded up to a multiple of 256, every row's max
  * scaled logit M (float [R]); R = B*(2K+1) rows: target row (b, i) at b*(K+1)+i, then
@@ -344,14 +345,13 @@ int npn_accept_rejection(const float* target_logits, const float* draft_logits,
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). The workspace
  * is a fixed device array of NPN_ACCEPT_SCRATCH_BYTES per GPU, held from the first call on
  * that GPU until the process ends; problems whose npn_accept_workspace_size(B, K, V) exceeds
- * it return NPN_ERR_SCRATCH (B = 32, K = 7, V = 151936 needs 267 KiB). Every call on a GPU
+ * it return NPN_ERR_SCRATCH (B = 32, K = 7, V = 151936 needs 2.6 MiB). Every call on a GPU
  * uses that GPU's one array, so calls that overlap on one GPU (concurrent streams, or
  * threads) race and must be serialised by the caller; each call writes every scratch word it
- * reads before reading it (its counters are cleared by its own kernels), so nothing needs
- * clearing between calls. The stream's device (the current device
- * for the null stream) selects the array. The first call on a device looks the array's
- * address up (hipGetSymbolAddress); make it outside stream capture, after which a call only
- * enqueues kernels and may be captured in a HIP graph. Results are bit-identical to
+ * reads before reading it, so nothing needs clearing between calls. The stream's device
+ * (the current device for the null stream) selects the array. The first call on a device
+ * looks the array's address up (hipGetSymbolAddress); make it outside stream capture, after
+ * which a call only enqueues kernels and may be captured in a HIP graph. Results are bit-identical to
  * npn_accept_rejection; the scratch is not readable through this interface. */
 int npn_accept_rejection_noalloc(const float* target_logits, const float* draft_logits,
                                  const int64_t* draft_ids, const float* u_accept,

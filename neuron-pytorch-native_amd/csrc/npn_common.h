@@ -53,21 +53,28 @@ __device__ __forceinline__ float wave_max(float v) {
 // quad_perm [1,0,3,2] and [2,3,0,1] combine lanes within each quad; row_half_mirror (lane i with
 // 7 - i of its half-row) then row_mirror (i with 15 - i of its row) combine the quads and the
 // halves. After n steps every lane holds the reduction over its aligned group of 2^n lanes
-// (n = 2: quads, 3: eight lanes, 4: the 16-lane row).
+// (n = 2: quads, 3: eight lanes, 4: the 16-lane row). Every source lane of these patterns is
+// inside the row, so the move needs no old value (bound_ctrl), which lets the compiler fold it
+// into the operation that uses it.
 template <int CTRL>
 __device__ __forceinline__ uint32_t dpp32(uint32_t v) {
-  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xF, 0xF, true);
 }
 
 constexpr int kDppStep[4] = {0xB1, 0x4E, 0x141, 0x140};
 
+// Maximum of a non-NaN float over the aligned group of 2^STEPS lanes. The reduction runs on an
+// order-preserving integer key (bits, with the magnitude bits flipped for negatives; -0 sorts
+// below +0), as v_max_i32 with the DPP move folded in.
 template <int STEPS>
 __device__ __forceinline__ float row_max_dpp(float v) {
-  if constexpr (STEPS >= 1) v = fmaxf(v, __uint_as_float(dpp32<kDppStep[0]>(__float_as_uint(v))));
-  if constexpr (STEPS >= 2) v = fmaxf(v, __uint_as_float(dpp32<kDppStep[1]>(__float_as_uint(v))));
-  if constexpr (STEPS >= 3) v = fmaxf(v, __uint_as_float(dpp32<kDppStep[2]>(__float_as_uint(v))));
-  if constexpr (STEPS >= 4) v = fmaxf(v, __uint_as_float(dpp32<kDppStep[3]>(__float_as_uint(v))));
-  return v;
+  const uint32_t u = __float_as_uint(v);
+  int k = (int)(u ^ ((uint32_t)((int)u >> 31) & 0x7FFFFFFFu));
+  if constexpr (STEPS >= 1) k = max(k, (int)dpp32<kDppStep[0]>((uint32_t)k));
+  if constexpr (STEPS >= 2) k = max(k, (int)dpp32<kDppStep[1]>((uint32_t)k));
+  if constexpr (STEPS >= 3) k = max(k, (int)dpp32<kDppStep[2]>((uint32_t)k));
+  if constexpr (STEPS >= 4) k = max(k, (int)dpp32<kDppStep[3]>((uint32_t)k));
+  return __uint_as_float((uint32_t)k ^ ((uint32_t)(k >> 31) & 0x7FFFFFFFu));
 }
 
 template <int CTRL>

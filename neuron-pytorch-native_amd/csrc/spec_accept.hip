@@ -19,12 +19,14 @@
 //
 // Kernels (each over B sequences, T = K+1 positions):
 //   greedy:    argmax partials per (row, 8192-entry chunk) -> per-sequence merge + accept
-//   rejection: block statistics (M_b, S_b) of every row in one pass over the logits, the
-//              64-entry chunk statistics kept on chip (for the LM head the target rows' chunk
-//              statistics come from the GEMM epilogue and a small kernel folds them into
-//              blocks) -> per-sequence row totals and decision -> residual (or bonus) mass
-//              per 2048 entries, the chunk maxima recomputed from the logits read anyway ->
-//              per-sequence inverse CDF
+//   rejection: block statistics (M_b, S_b) of every row, and each row's draft-token weight
+//              E F, in one pass over the logits, the 64-entry chunk statistics kept on chip
+//              (for the LM head the target rows' chunk statistics come from the GEMM epilogue
+//              and a small kernel folds them into blocks) -> row totals and decision (every
+//              workgroup of the next kernel works it out from the block statistics) with the
+//              residual (or bonus) mass per 64-entry chunk and per 2048 entries, the chunk
+//              maxima recomputed from the logits read anyway -> per-sequence inverse CDF
+//              walking sub-chunk, chunk and entry
 #include "accept_contract.h"
 #include "npn_internal.h"
 
@@ -36,11 +38,9 @@ constexpr int CHK = 8192;      // vocabulary entries per greedy argmax partial
 constexpr int THREADS = 256;   // CHK / THREADS = 32 entries per thread
 constexpr int PER_T = CHK / THREADS;
 constexpr int CC = npn::kContractChunk;  // 64 entries per chunk of the rejection contract
-constexpr int MCHK = 2048;     // entries per block of the sampling kernel
-constexpr int PER_M = MCHK / THREADS;  // 8 consecutive entries per thread, inside one chunk
+constexpr int MCHK = 2048;     // entries per sub-chunk of the sampling masses
 constexpr int kRejMaxV = 1 << 20;  // largest vocabulary of the rejection path
-static_assert(npn::kContractBlock / THREADS == 32 && CC % PER_M == 0,
-              "entry layouts of the rejection kernels");
+static_assert(npn::kContractBlock / THREADS == 32, "entry layout of the statistics pass");
 
 typedef unsigned __int128 u128;
 
@@ -426,15 +426,17 @@ struct RejArgs {
   float inv_temp;
   int32_t* accepted;
   int64_t* out_ids;
-  int B, K, V, nb, nchm;  // contract blocks per row; 2048-entry sub-chunks per row
+  int B, K, V, nb, nchm, nc;  // contract blocks, 2048-entry sub-chunks, contract chunks per row
   bool vec4;              // fp32 logit rows 16-byte aligned and V % 4 == 0 (bf16: V % 8)
   // workspace (rows: the B*(K+1) target rows, then the B*K draft rows)
   u128* zrow;             // [rows]      Z of each row
   float* mrow;            // [rows]      row maximum M (scaled logits)
   float* bmax;            // [rows][nb]  block maxima M_b
   u128* bsum;             // [rows][nb]  block sums S_b
+  uint64_t* tw;           // [rows]      E F of the row's draft token (rows that have one)
   Decision* dec;          // [B]
   u256* cmass;            // [B][nchm]   sampling mass of each 2048-entry sub-chunk
+  u256* cm64;             // [B][nc]     sampling mass of each contract chunk
 };
 
 template <typename TT>
@@ -447,20 +449,33 @@ __device__ __forceinline__ const TT* target_row(const RejArgs& a, int row) {
 // range), so no emitted id lies outside the vocabulary.
 __device__ __forceinline__ bool draft_id_ok(int64_t x, int V) { return x >= 0 && x < V; }
 
-// Draft token whose weight this row reports, or -1 (bonus rows, and out-of-range draft ids).
-__device__ __forceinline__ int row_token(const RejArgs& a, int row) {
+// *p through a per-lane (vector) load, even when p is uniform: the compiler cannot see that
+// the lane offset is 0, so the load is waited for with the other vector loads, in issue order.
+__device__ __forceinline__ int64_t load_opaque(const int64_t* p) {
+  int z;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+  return p[z];
+}
+
+// The draft id a row's token weight refers to, or nullptr for bonus rows.
+__device__ __forceinline__ const int64_t* row_draft_id(const RejArgs& a, int row) {
   const int nt = a.B * (a.K + 1);
   int b, i;
   if (row < nt) {
     b = row / (a.K + 1);
     i = row - b * (a.K + 1);
-    if (i == a.K) return -1;
+    if (i == a.K) return nullptr;
   } else {
     b = (row - nt) / a.K;
     i = (row - nt) - b * a.K;
   }
-  const int64_t x = a.draft_ids[(size_t)b * a.K + i];
-  return draft_id_ok(x, a.V) ? (int)x : -1;
+  return a.draft_ids + (size_t)b * a.K + i;
+}
+
+// Draft token whose weight this row reports, or -1 (bonus rows, and out-of-range draft ids).
+__device__ __forceinline__ int row_token(const RejArgs& a, int row) {
+  const int64_t* id = row_draft_id(a, row);
+  return id != nullptr && draft_id_ok(*id, a.V) ? (int)*id : -1;
 }
 
 __device__ __forceinline__ float elem_at(const RejArgs& a, int row, int v, const float*) {
@@ -497,7 +512,9 @@ __device__ __forceinline__ void block_from_chunks(float m, uint64_t s, float* sh
 // row row0 + y once, into registers (thread t holds the float4s at v0 + 4 (256 j + t), j < 8,
 // so for each j the 16 lanes of a DPP row hold one 64-entry chunk); each chunk's maximum m_c
 // of the scaled logits (NaN ignored; entries past V read as NaN) and S_c = sum of
-// expfix(s_v - m_c) stay on chip, and only M_b and S_b = sum F_c S_c are written.
+// expfix(s_v - m_c) stay on chip, and only M_b and S_b = sum F_c S_c are written. The thread
+// that holds the row's draft token also writes its E F = expfix(s - m_c) expfix(m_c - M_b),
+// so the decision reads no logits.
 template <bool kUnitTemp>
 __global__ __launch_bounds__(THREADS) void rej_stats_kernel(RejArgs a, int row0) {
   __shared__ float sh_cm[CPB];
@@ -510,6 +527,7 @@ __global__ __launch_bounds__(THREADS) void rej_stats_kernel(RejArgs a, int row0)
                               : a.draft + (size_t)(row - nt) * a.V;
   const int v0 = (int)blockIdx.x * npn::kContractBlock;
   const int t = threadIdx.x;
+  const int64_t* idp = row_draft_id(a, row);
   float x[32];
   if (a.vec4 && v0 + npn::kContractBlock <= a.V) {  // whole block inside the row
 #pragma unroll
@@ -526,9 +544,23 @@ __global__ __launch_bounds__(THREADS) void rej_stats_kernel(RejArgs a, int row0)
         x[4 * j + k] = v < a.V ? src[v] : NAN;
       }
   }
+  // the draft id through a vector load issued after the logits', so that no wait for it holds
+  // them back (a scalar load of the uniform address would be waited for first)
+  const int64_t id = idp != nullptr ? load_opaque(idp) : -1;
   if (!kUnitTemp) {
 #pragma unroll
     for (int e = 0; e < 32; ++e) x[e] = scaled(x[e], a.inv_temp);
+  }
+  // the thread whose float4 (toff >> 2 = 256 j + t) holds the draft token keeps its value
+  const int toff = draft_id_ok(id, a.V) ? (int)id - v0 : -1;
+  const bool tok_here =
+      toff >= 0 && toff < npn::kContractBlock && ((toff >> 2) & (THREADS - 1)) == t;
+  float tx = 0.f;
+  if (tok_here) {
+    const int e = ((toff >> 10) << 2) | (toff & 3);
+#pragma unroll
+    for (int k = 0; k < 32; ++k)
+      if (k == e) tx = x[k];
   }
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
@@ -553,104 +585,152 @@ __global__ __launch_bounds__(THREADS) void rej_stats_kernel(RejArgs a, int row0)
     a.bmax[(size_t)row * a.nb + blockIdx.x] = Mb;
     a.bsum[(size_t)row * a.nb + blockIdx.x] = Sb;
   }
+  if (tok_here) {
+    const float tm = sh_cm[toff / CC];
+    a.tw[row] = (uint64_t)expfix_rel(tx, tm) * expfix_rel(tm, Mb);
+  } else if (toff < 0 && blockIdx.x == 0 && t == 0) {
+    a.tw[row] = 0;  // no token: every row's entry is written
+  }
 }
 
-// Block statistics from chunk statistics ([rows][nc], the LM-head GEMM epilogue's), one
-// 128-thread workgroup per (block, row); chunks past the row's last read as empty.
+// Block statistics from chunk statistics ([rows][nc], the LM-head GEMM epilogue's) of bf16
+// target rows, one 128-thread workgroup per (block, row); chunks past the row's last read as
+// empty. The thread of the draft token's chunk also writes the token's E F, reading the one
+// logit.
 __global__ __launch_bounds__(CPB) void rej_block_from_chunks_kernel(RejArgs a, int row0,
                                                                     const float* cmax,
                                                                     const uint64_t* csum,
                                                                     int nc) {
   __shared__ float sh_m[CPB / 64];
   __shared__ u128 sh_s[CPB / 64];
-  const int b = (int)blockIdx.x, r = (int)blockIdx.y;
+  const int b = (int)blockIdx.x, r = (int)blockIdx.y, row = row0 + r;
   const int c = b * CPB + (int)threadIdx.x;
   const float m = c < nc ? cmax[(size_t)r * nc + c] : -INFINITY;
   const uint64_t s = c < nc ? csum[(size_t)r * nc + c] : 0;
+  const int tok = row_token(a, row);
+  const bool has_tok = tok >= 0 && tok / CC == c;
+  const float tx =
+      has_tok ? scaled(elem_at(a, row, tok, static_cast<const uint16_t*>(nullptr)), a.inv_temp)
+              : 0.f;
   float Mb;
   u128 Sb;
   block_from_chunks(m, s, sh_m, sh_s, Mb, Sb);
   if (threadIdx.x == 0) {
-    a.bmax[(size_t)(row0 + r) * a.nb + b] = Mb;
-    a.bsum[(size_t)(row0 + r) * a.nb + b] = Sb;
+    a.bmax[(size_t)row * a.nb + b] = Mb;
+    a.bsum[(size_t)row * a.nb + b] = Sb;
   }
+  if (has_tok)
+    a.tw[row] = (uint64_t)expfix_rel(tx, m) * expfix_rel(m, Mb);
+  else if (tok < 0 && c == 0)
+    a.tw[row] = 0;  // no token: every row's entry is written
 }
 
-// Row totals and the decision, one workgroup per sequence (one wave per row, rows in turn):
-// M = max_b M_b, Z = sum_b G_b S_b (G_b = expfix(M_b - M)), and the weight W = E F G of the
-// row's draft token, whose chunk (64 entries, read with the block statistics) gives its m_c,
-// E = expfix(s - m_c) and F = expfix(m_c - M_b). Then lane i < K of wave 0 runs the accept test
-// of draft position i (all at once; the first failing lane is the rejection). Writes every
-// row's Z and M, the sequence's decision record, accepted[b] and out_ids but the sampled token.
-template <typename TT>
-__global__ __launch_bounds__(1024) void rej_decide_kernel(RejArgs a) {
-  const int b = (int)blockIdx.x;
+// Sum over each 16-lane row (DPP), in every lane of the row.
+template <int CTRL>
+__device__ __forceinline__ u128 dpp_u128(u128 v) {
+  return ((u128)npn::dpp64<CTRL>((uint64_t)(v >> 64)) << 64) | npn::dpp64<CTRL>((uint64_t)v);
+}
+
+__device__ __forceinline__ u128 row_sum_u128(u128 v) {
+  v += dpp_u128<npn::kDppStep[0]>(v);
+  v += dpp_u128<npn::kDppStep[1]>(v);
+  v += dpp_u128<npn::kDppStep[2]>(v);
+  return v + dpp_u128<npn::kDppStep[3]>(v);
+}
+
+// Block statistics per lane in the decision: V <= 2^20 gives at most 128 blocks, 8 per lane.
+constexpr int kDecideBlocksPerLane = (kRejMaxV / npn::kContractBlock + 15) / 16;
+
+struct DecideSmem {
+  u128 z[kMaxRowsPerSeq];
+  u128 w[kMaxRowsPerSeq];
+  float m[kMaxRowsPerSeq];
+  Decision d;
+};
+
+// Row totals and the decision of sequence b, by a whole THREADS-wide workgroup: each 16-lane
+// row of lanes takes one of the sequence's 2K+1 rows at a time, lane l its blocks l, l + 16, ...:
+// M = max_b M_b, Z = sum_b G_b S_b (G_b = expfix(M_b - M)), and the weight of the row's draft
+// token W = (E F) G_b from the statistics pass's E F. Then lane i < K of wave 0 runs the
+// accept test of position i (all at once; the first failing lane is the rejection). With
+// `write` it also stores every row's Z and M, the decision record, accepted[b] and out_ids but
+// the sampled token. Ends with a barrier, after which sm.d holds the decision.
+__device__ void decide_sequence(const RejArgs& a, int b, bool write, DecideSmem& sm) {
   const int K = a.K, T = K + 1, nt = a.B * T;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  __shared__ u128 s_z[kMaxRowsPerSeq];
-  __shared__ u128 s_w[kMaxRowsPerSeq];
-  __shared__ float s_m[kMaxRowsPerSeq];
-  for (int j = w; j < T + K; j += nw) {
+  const int t = threadIdx.x, lane = t & 63, gl = t & 15;
+  int64_t id = 0;  // wave 0's accept-test inputs, issued first
+  float u = 0.f;
+  if (t < K) {
+    id = a.draft_ids[(size_t)b * K + t];
+    u = a.u_accept[(size_t)b * K + t];
+  }
+  for (int j = t >> 4; j < T + K; j += THREADS / 16) {
     const int row = j < T ? b * T + j : nt + b * K + (j - T);
     const int tok = row_token(a, row);
-    // the token's chunk, and the row's block statistics (two blocks per lane at most)
-    float xv = NAN;
-    if (tok >= 0) {
-      const int v = (tok / CC) * CC + lane;
-      if (v < a.V) xv = scaled(elem_at(a, row, v, static_cast<const TT*>(nullptr)), a.inv_temp);
-    }
-    float bm[2];
-    u128 bs[2];
+    const uint64_t ef = a.tw[row];  // issued with the other loads; 0 without a token
+    float bm[kDecideBlocksPerLane];
+    u128 bs[kDecideBlocksPerLane];
+    float mx = -INFINITY;
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      const int bb = lane + 64 * k;
+    for (int k = 0; k < kDecideBlocksPerLane; ++k) {
+      const int bb = gl + 16 * k;
       bm[k] = bb < a.nb ? a.bmax[(size_t)row * a.nb + bb] : -INFINITY;
       bs[k] = bb < a.nb ? a.bsum[(size_t)row * a.nb + bb] : 0;
+      mx = fmaxf(mx, bm[k]);
     }
-    const float M = npn::wave_max(fmaxf(bm[0], bm[1]));
-    const u128 z = wave_sum_u128((u128)bs[0] * expfix_rel(bm[0], M) +
-                                 (u128)bs[1] * expfix_rel(bm[1], M));
-    u128 wt = 0;
-    if (tok >= 0) {
-      const float mc = npn::wave_max(xv);
-      const float xs = __shfl(xv, tok % CC, 64);
-      const int tb = tok / npn::kContractBlock;
-      const float Mb = __shfl(tb < 64 ? bm[0] : bm[1], tb & 63, 64);
-      wt = (u128)((uint64_t)expfix_rel(xs, mc) * expfix_rel(mc, Mb)) * expfix_rel(Mb, M);
-    }
-    if (lane == 0) {
-      s_z[j] = z;
-      s_m[j] = M;
-      s_w[j] = wt;
-      a.zrow[row] = z;
-      a.mrow[row] = M;
+    const float M = npn::row_max_dpp<4>(mx);
+    u128 z = 0;
+#pragma unroll
+    for (int k = 0; k < kDecideBlocksPerLane; ++k) z += bs[k] * expfix_rel(bm[k], M);
+    z = row_sum_u128(z);
+    // M_b of the token's block: lane tb & 15 of the row holds it in bm[tb >> 4]
+    const int tb = tok >= 0 ? tok / npn::kContractBlock : 0;
+    float mb = bm[0];
+#pragma unroll
+    for (int k = 1; k < kDecideBlocksPerLane; ++k)
+      if ((tb >> 4) == k) mb = bm[k];
+    mb = __shfl(mb, (lane & 48) | (tb & 15), 64);
+    if (gl == 0) {
+      sm.z[j] = z;
+      sm.m[j] = M;
+      sm.w[j] = tok >= 0 ? (u128)ef * expfix_rel(mb, M) : 0;
+      if (write) {
+        a.zrow[row] = z;
+        a.mrow[row] = M;
+      }
     }
   }
   __syncthreads();
-  if (w != 0) return;
-  bool reject = false;
-  if (lane < K) {
-    const int64_t id = a.draft_ids[(size_t)b * K + lane];
-    const uint32_t U = uniform_fix(a.u_accept[(size_t)b * K + lane]);
-    const u256 lhs = mul256x32(mul128x128(s_w[T + lane], s_z[lane]), U);
-    const u256 rhs = shl24_256(mul128x128(s_w[lane], s_z[T + lane]));
-    reject = !draft_id_ok(id, a.V) || gt256(lhs, rhs);
+  if (t < 64) {
+    bool reject = false;
+    if (lane < K) {
+      const uint32_t U = uniform_fix(u);
+      const u256 lhs = mul256x32(mul128x128(sm.w[T + lane], sm.z[lane]), U);
+      const u256 rhs = shl24_256(mul128x128(sm.w[lane], sm.z[T + lane]));
+      reject = !draft_id_ok(id, a.V) || gt256(lhs, rhs);
+    }
+    const uint64_t rej = __builtin_amdgcn_ballot_w64(reject);
+    const int acc = rej ? __builtin_ctzll(rej) : K;
+    if (lane == 0) {
+      Decision d;
+      d.acc = acc;
+      d.pad = 0;
+      d.zp = sm.z[acc];
+      d.mp = sm.m[acc];
+      d.zq = acc < K ? sm.z[T + acc] : 0;
+      d.mq = acc < K ? sm.m[T + acc] : 0.f;
+      sm.d = d;
+      if (write) {
+        a.dec[b] = d;
+        a.accepted[b] = acc;
+      }
+    }
+    // position tt < acc holds lane tt's draft id (tt < acc <= K <= 64 only in the first pass)
+    if (write)
+      for (int tt = lane; tt < T; tt += 64)
+        if (tt != acc) a.out_ids[(size_t)b * T + tt] = tt < acc ? id : -1;
   }
-  const uint64_t rej = __builtin_amdgcn_ballot_w64(reject);
-  const int acc = rej ? __builtin_ctzll(rej) : K;
-  if (lane == 0) {
-    Decision d;
-    d.acc = acc;
-    d.pad = 0;
-    d.zp = s_z[acc];
-    d.mp = s_m[acc];
-    d.zq = acc < K ? s_z[T + acc] : 0;
-    d.mq = acc < K ? s_m[T + acc] : 0.f;
-    a.dec[b] = d;
-    a.accepted[b] = acc;
-  }
-  for (int t = lane; t < T; t += 64)
-    if (t != acc) a.out_ids[(size_t)b * T + t] = t < acc ? a.draft_ids[(size_t)b * K + t] : -1;
+  __syncthreads();
 }
 
 // The sampling rows of one sequence for a thread's run inside one contract chunk: after a
@@ -825,22 +905,25 @@ __device__ __forceinline__ float chunk_max(const float (&v)[N]) {
   return npn::row_max_dpp<LANES == 2 ? 1 : (LANES == 4 ? 2 : 3)>(m);
 }
 
-// Residual (or bonus) mass per 2048-entry sub-chunk of the sampling rows: block x holds the
-// 8192-entry contract block x (each wave one sub-chunk), each lane a run of 32 entries, the
-// lanes 2c, 2c + 1 of a wave forming chunk c of its sub-chunk (whose maxima they reduce
-// between them). The decision comes from the decide kernel. The wave's sum goes to cmass;
-// no barrier, and no block reads another's results (the pick kernel, launched after this
-// one, does).
+// Residual (or bonus) mass per contract chunk and per 2048-entry sub-chunk of the sampling rows.
+// Every workgroup first works out its sequence's decision (block statistics only; workgroup
+// x == 0 writes it out), then block x covers the contract block x of the sampling rows, each
+// wave one sub-chunk, each lane a run of 32 entries, the lanes 2c, 2c + 1 of a wave forming
+// chunk c of its sub-chunk (whose maxima they reduce between them). The chunk masses go to
+// cm64 and the wave's sum to cmass; no workgroup reads another's results (the pick kernel,
+// launched after this one, does).
 constexpr int MRUN = MCHK / 64;  // entries per lane of the mass kernel
 static_assert(2 * MRUN == CC, "two lanes per contract chunk");
 
 template <bool kUnitTemp, typename TT>
 __global__ __launch_bounds__(THREADS) void rej_mass_kernel(RejArgs a) {
+  __shared__ DecideSmem sm;
   const int b = (int)blockIdx.y;
+  decide_sequence(a, b, blockIdx.x == 0, sm);
   const int lane = threadIdx.x & 63;
   const int sub = (int)blockIdx.x * (THREADS / 64) + (int)(threadIdx.x >> 6);
   if (sub >= a.nchm) return;  // the whole wave
-  const Decision d = a.dec[b];
+  const Decision d = sm.d;
   const int K = a.K, T = K + 1, nt = a.B * T;
   const int rp = b * T + d.acc, rq = nt + b * K + d.acc;
   const TT* p = target_row<TT>(a, rp);
@@ -852,37 +935,38 @@ __global__ __launch_bounds__(THREADS) void rej_mass_kernel(RejArgs a) {
   const float mpc = chunk_max<2>(rv.p), mqc = chunk_max<2>(rv.q);
   u256 m = kZero256;
   if (v0 < a.V) m = run_mass<MRUN>(sample_row<TT>(d, p, q, mpc, mqc, Mbp, Mbq), rv);
+  const u256 mc = add256(m, dpp_u256<npn::kDppStep[0]>(m));  // lanes 2c and 2c + 1
+  const int c = v0 / CC;
+  if ((lane & 1) == 0 && c < a.nc) a.cm64[(size_t)b * a.nc + c] = mc;
   m = wave_sum_u256(m);
   if (lane == 0) a.cmass[(size_t)b * a.nchm + sub] = m;
 }
 
-// Inverse CDF, one block per sequence. Wave 0 loads the sequence's sub-chunk masses (lane l a
-// group of G = ceil(nchm / 64) consecutive ones); one scan of the group sums gives the total
-// and the group whose inclusive mass first crosses the target, whose masses (broadcast from
-// its lane) then locate the sub-chunk. Each thread sums its run of 8 entries of that
-// sub-chunk (8 threads per contract chunk); a block-wide exclusive scan of the runs finds the
-// run that crosses, whose 8 entries lanes 0..7 of wave 0 then weigh exactly and scan, the
-// first crossing lane giving the token.
+// Inverse CDF, one block per sequence, three levels walked by wave 0. (1) The sequence's
+// sub-chunk masses, lane l a group of G = ceil(nchm / 64) consecutive ones: one scan of the
+// group sums gives the total and the group whose inclusive mass first crosses the target, whose
+// masses (broadcast from its lane) then locate the sub-chunk. (2) That sub-chunk's 32 chunk
+// masses, one per lane, scanned: the crossing chunk. (3) That chunk's 64 entries, one per lane,
+// weighed exactly and scanned: the first crossing lane gives the token. Chunk masses are exact
+// sums of their entries' weights, so each level's crossing lies inside the previous level's.
+// With no mass at all every wave helps with the argmax fallback.
 constexpr int kPickMaxGroup = 8;  // sub-chunk masses per lane: V <= 64 * 8 * 2048
+static_assert(MCHK / CC <= 64, "one lane per chunk of a sub-chunk");
 
 template <bool kUnitTemp, typename TT>
 __global__ __launch_bounds__(THREADS) void rej_pick_kernel(RejArgs a) {
   const int b = (int)blockIdx.x;
   const int K = a.K, T = K + 1, nt = a.B * T;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  __shared__ int s_chunk;
-  __shared__ u256 s_before;
-  __shared__ u256 s_target;
-  __shared__ u256 s_wtot[THREADS / 64];
-  __shared__ int s_tok;
-  __shared__ int s_empty;
-  __shared__ int s_run;
-  __shared__ u256 s_cpre;
-  __shared__ float s_mc[2];
+  __shared__ int s_tok;  // -1: no sampling mass
   __shared__ ArgPart s_best[THREADS / 64];
   const Decision d = a.dec[b];
-  const u256* cm = a.cmass + (size_t)b * a.nchm;
+  const int acc = d.acc;
+  const int rp = b * T + acc, rq = nt + b * K + acc;
+  const TT* p = target_row<TT>(a, rp);
+  const float* q = acc < K ? a.draft + (size_t)(b * K + acc) * a.V : nullptr;
   if (w == 0) {
+    const u256* cm = a.cmass + (size_t)b * a.nchm;
     const int G = (a.nchm + 63) / 64;
     u256 mv[kPickMaxGroup];
 #pragma unroll
@@ -896,42 +980,62 @@ __global__ __launch_bounds__(THREADS) void rej_pick_kernel(RejArgs a) {
     const u256 incl = wave_incl_scan_u256(gsum);
     const u256 tot = shfl_u256(incl, 63);
     const u256 target = mul256x32(tot, uniform_fix(a.u_sample[b]));  // need 2^24 C > target
-    // a positive total always crosses (U < 2^24); with none the chunk is unused
+    // a positive total always crosses (U < 2^24)
     const uint64_t hit = __builtin_amdgcn_ballot_w64(gt256(shl24_256(incl), target));
-    int chunk = a.nchm - 1;
-    u256 before = kZero256;
-    if (hit != 0) {
+    if (hit == 0) {
+      if (lane == 0) s_tok = -1;
+    } else {
       const int l = __builtin_ctzll(hit);
       u256 run = shfl_u256(sub256(incl, gsum), l);  // mass before lane l's group
+      int sub = a.nchm - 1;
+      u256 before = kZero256;
       bool found = false;
 #pragma unroll
       for (int k = 0; k < kPickMaxGroup; ++k) {
         const u256 mk = shfl_u256(mv[k], l);
         const u256 next = add256(run, mk);
         if (k < G && !found && gt256(shl24_256(next), target)) {
-          chunk = l * G + k;
+          sub = l * G + k;
           before = run;
           found = true;
         }
         run = next;
       }
-    }
-    if (lane == 0) {
-      s_empty = is_zero256(tot);
-      s_chunk = chunk;
-      s_before = before;
-      s_target = target;
-      s_run = 0;
-      s_cpre = before;
+      // (2) the sub-chunk's chunk masses
+      const int c = sub * (MCHK / CC) + lane;
+      const bool cin = lane < MCHK / CC && c < a.nc;
+      const u256 mc = cin ? a.cm64[(size_t)b * a.nc + c] : kZero256;
+      const int blk = sub / (npn::kContractBlock / MCHK);
+      const float Mbp = a.bmax[(size_t)rp * a.nb + blk];
+      const float Mbq = q != nullptr ? a.bmax[(size_t)rq * a.nb + blk] : 0.f;
+      const u256 cincl = wave_incl_scan_u256(mc);
+      const uint64_t chit =
+          __builtin_amdgcn_ballot_w64(cin && gt256(shl24_256(add256(before, cincl)), target));
+      const int cl = chit ? __builtin_ctzll(chit) : 0;
+      const u256 cbefore = add256(before, shfl_u256(sub256(cincl, mc), cl));
+      // (3) the chunk's entries
+      const int v = (sub * (MCHK / CC) + cl) * CC + lane;
+      float pv = NAN, qv = NAN;
+      if (v < a.V) {
+        pv = elem(p, v);
+        if (q != nullptr) qv = q[v];
+      }
+      if (!kUnitTemp) {
+        pv = scaled(pv, a.inv_temp);
+        qv = scaled(qv, a.inv_temp);
+      }
+      const float mpc = npn::wave_max(fmaxf(pv, -INFINITY));
+      const float mqc = npn::wave_max(fmaxf(qv, -INFINITY));
+      const u256 wv = weight_of(sample_row<TT>(d, p, q, mpc, mqc, Mbp, Mbq), pv, qv);
+      const u256 vincl = add256(cbefore, wave_incl_scan_u256(wv));
+      const uint64_t vhit =
+          __builtin_amdgcn_ballot_w64(v < a.V && gt256(shl24_256(vincl), target));
+      if (lane == 0) s_tok = v + (vhit ? __builtin_ctzll(vhit) : 0);
     }
   }
   __syncthreads();
-  const int acc = d.acc;
-  const int rp = b * T + acc, rq = nt + b * K + acc;
-  const TT* p = target_row<TT>(a, rp);
-  const float* q = acc < K ? a.draft + (size_t)(b * K + acc) * a.V : nullptr;
-  int tok;
-  if (s_empty) {
+  int tok = s_tok;
+  if (tok < 0) {
     // No sampling mass: every weight of the sampling row is 0, which happens only for a
     // bonus row whose logits are all NaN or -inf or include +inf, or for the residual after
     // an out-of-range draft id where Wp Zq == Wq Zp everywhere (a residual after a failed
@@ -940,9 +1044,9 @@ __global__ __launch_bounds__(THREADS) void rej_pick_kernel(RejArgs a) {
     // argmax_chunk_kernel).
     float bv = -INFINITY;
     int bi = 0x7FFFFFFF;
-    for (int v = (int)threadIdx.x; v < a.V; v += THREADS) {
-      const float pv = elem(p, v);
-      if (beats(pv, v, bv, bi)) { bv = pv; bi = v; }
+    for (int vv = (int)threadIdx.x; vv < a.V; vv += THREADS) {
+      const float pv = elem(p, vv);
+      if (beats(pv, vv, bv, bi)) { bv = pv; bi = vv; }
     }
     for (int off = 32; off > 0; off >>= 1) {
       const float ov = __shfl_xor(bv, off, 64);
@@ -955,55 +1059,6 @@ __global__ __launch_bounds__(THREADS) void rej_pick_kernel(RejArgs a) {
     for (int k = 1; k < THREADS / 64; ++k)
       if (beats(s_best[k].v, s_best[k].i, best.v, best.i)) best = s_best[k];
     tok = best.i;
-  } else {
-    const int sub = s_chunk;
-    const int blk = sub / (npn::kContractBlock / MCHK);
-    const float Mbp = a.bmax[(size_t)rp * a.nb + blk];
-    const float Mbq = q != nullptr ? a.bmax[(size_t)rq * a.nb + blk] : 0.f;
-    const int v0 = sub * MCHK + (int)threadIdx.x * PER_M;
-    const RunVals<PER_M> rv = load_run<PER_M, kUnitTemp>(a, p, q, v0);
-    const float mpc = chunk_max<8>(rv.p), mqc = chunk_max<8>(rv.q);
-    u256 run = kZero256;
-    if (v0 < a.V) run = run_mass<PER_M>(sample_row<TT>(d, p, q, mpc, mqc, Mbp, Mbq), rv);
-    const u256 incl = wave_incl_scan_u256(run);
-    if (lane == 63) s_wtot[w] = incl;
-    __syncthreads();
-    u256 cpre = add256(s_before, sub256(incl, run));
-    for (int k = 0; k < w; ++k) cpre = add256(cpre, s_wtot[k]);
-    const u256 target = s_target;
-    // the one run that crosses: the target not passed before it, passed at its end (a run
-    // mass is the exact sum of its entries' weights, so the crossing entry lies in it)
-    if (v0 < a.V && !gt256(shl24_256(cpre), target) &&
-        gt256(shl24_256(add256(cpre, run)), target)) {
-      s_run = (int)threadIdx.x;
-      s_cpre = cpre;
-      s_mc[0] = mpc;
-      s_mc[1] = mqc;
-    }
-    __syncthreads();
-    // that run's entries weighed exactly, one per lane of wave 0, then scanned
-    if (w == 0) {
-      const int rv0 = sub * MCHK + s_run * PER_M;
-      const int v = rv0 + (lane & (PER_M - 1));
-      u256 wv = kZero256;
-      if (lane < PER_M && v < a.V) {
-        const SampleRow<TT> s = sample_row<TT>(d, p, q, s_mc[0], s_mc[1], Mbp, Mbq);
-        const float pv = kUnitTemp ? elem(p, v) : scaled(elem(p, v), a.inv_temp);
-        const float qv = q == nullptr ? NAN : (kUnitTemp ? q[v] : scaled(q[v], a.inv_temp));
-        wv = weight_of(s, pv, qv);
-      }
-#pragma unroll
-      for (int dd = 1; dd < PER_M; dd <<= 1) {  // inclusive scan over lanes 0..7
-        const u256 o = shfl_up_u256(wv, dd);
-        if ((lane & (PER_M - 1)) >= dd) wv = add256(wv, o);
-      }
-      const u256 c = add256(s_cpre, wv);
-      const uint64_t hit = __builtin_amdgcn_ballot_w64(lane < PER_M && v < a.V &&
-                                                        gt256(shl24_256(c), target));
-      if (lane == 0) s_tok = rv0 + (hit ? __builtin_ctzll(hit) : 0);
-    }
-    __syncthreads();
-    tok = s_tok;
   }
   if (threadIdx.x == 0) a.out_ids[(size_t)b * T + acc] = tok;
 }
@@ -1011,7 +1066,7 @@ __global__ __launch_bounds__(THREADS) void rej_pick_kernel(RejArgs a) {
 // Workspace of the acceptance calls. The per-row Z sums come first and the row maxima second:
 // the header documents both as results that the rejection call leaves in the workspace.
 struct WsLayout {
-  size_t zrow, mrow, bmax, bsum, dec, cmass, total;
+  size_t zrow, mrow, bmax, bsum, tw, dec, cmass, cm64, total;
 };
 
 WsLayout layout(int B, int K, int V) {
@@ -1028,8 +1083,10 @@ WsLayout layout(int B, int K, int V) {
   const size_t part_bytes = (size_t)B * (K + 1) * nch * sizeof(ArgPart);
   l.bmax = o; o += up(bmax_bytes > part_bytes ? bmax_bytes : part_bytes);
   l.bsum = o; o += up(rows * nb * sizeof(u128));
+  l.tw = o; o += up(rows * sizeof(uint64_t));
   l.dec = o; o += up((size_t)B * sizeof(Decision));
   l.cmass = o; o += up((size_t)B * ((V + MCHK - 1) / MCHK) * sizeof(u256));
+  l.cm64 = o; o += up((size_t)B * ((V + CC - 1) / CC) * sizeof(u256));
   l.total = o;
   return l;
 }
@@ -1092,10 +1149,12 @@ RejArgs rej_args(const void* target_logits, const float* draft_logits, const int
                     NPN_ALIGNED16(draft_logits);
   return RejArgs{target_logits, draft_logits, draft_ids, u_accept, u_sample, inv_temperature,
                  accepted, out_ids, B, K, V,
-                 (V + npn::kContractBlock - 1) / npn::kContractBlock, (V + MCHK - 1) / MCHK, vec4,
-                 reinterpret_cast<u128*>(ws + l.zrow), reinterpret_cast<float*>(ws + l.mrow),
-                 reinterpret_cast<float*>(ws + l.bmax), reinterpret_cast<u128*>(ws + l.bsum),
-                 reinterpret_cast<Decision*>(ws + l.dec), reinterpret_cast<u256*>(ws + l.cmass)};
+                 (V + npn::kContractBlock - 1) / npn::kContractBlock, (V + MCHK - 1) / MCHK,
+                 (V + CC - 1) / CC, vec4, reinterpret_cast<u128*>(ws + l.zrow),
+                 reinterpret_cast<float*>(ws + l.mrow), reinterpret_cast<float*>(ws + l.bmax),
+                 reinterpret_cast<u128*>(ws + l.bsum), reinterpret_cast<uint64_t*>(ws + l.tw),
+                 reinterpret_cast<Decision*>(ws + l.dec), reinterpret_cast<u256*>(ws + l.cmass),
+                 reinterpret_cast<u256*>(ws + l.cm64)};
 }
 
 // Block statistics of `rows` fp32 rows starting at row0.
@@ -1107,13 +1166,11 @@ void launch_stats(const RejArgs& a, int row0, int rows, hipStream_t s) {
     hipLaunchKernelGGL(rej_stats_kernel<false>, grid, dim3(THREADS), 0, s, a, row0);
 }
 
-// Decision, sampling mass and pick (every row's block statistics in place). TT is the target
-// rows' element type: float, or bf16 bits (uint16_t) for the LM-head form.
+// Decision with sampling mass, then the pick (every row's block statistics and draft-token
+// weight in place). TT is the target rows' element type: float, or bf16 bits (uint16_t) for
+// the LM-head form.
 template <typename TT>
 int launch_decide_sample(const RejArgs& a, hipStream_t s) {
-  const int rows = 2 * a.K + 1;
-  hipLaunchKernelGGL(rej_decide_kernel<TT>, dim3(a.B), dim3(64 * (rows < 16 ? rows : 16)), 0, s,
-                     a);
   const dim3 mgrid((a.nchm + THREADS / 64 - 1) / (THREADS / 64), a.B);
   if (a.inv_temp == 1.0f) {
     hipLaunchKernelGGL((rej_mass_kernel<true, TT>), mgrid, dim3(THREADS), 0, s, a);
@@ -1125,7 +1182,7 @@ int launch_decide_sample(const RejArgs& a, hipStream_t s) {
   return npn_launch_status();
 }
 
-// The four rejection kernels over fp32 logits on `stream`, with the workspace at `ws`
+// The three rejection kernels over fp32 logits on `stream`, with the workspace at `ws`
 // (layout(B, K, V).total bytes, 16-byte aligned, checked by the caller).
 int rejection_launch(const float* target_logits, const float* draft_logits,
                      const int64_t* draft_ids, const float* u_accept, const float* u_sample,

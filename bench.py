@@ -582,6 +582,7 @@ LM_VOCAB = 248320  # Qwen3.6-27B vocabulary (static_decode.py:107)
 # untimed calls per variant before its timed ones, at least: with 3 the shader clock has not
 # settled for the first variant (measured: fused 0.808 ms per call after 3, 0.772 after 64)
 LM_MIN_WARMUP = 64
+LM_ROUNDS = 5       # alternating timing rounds per path in --lm-head
 
 
 def lm_head_bench(args):
@@ -610,19 +611,7 @@ def lm_head_bench(args):
         w, sc = ws[i % 2]
         return torch.ops.fp8.matmul(x, w, sc)
 
-    res = {}
     warmup = max(args.warmup, LM_MIN_WARMUP)
-    for name, fn in (("gemm", gemm), ("fused", fused), ("unfused", unfused)):
-        for i in range(warmup):
-            fn(i)
-        torch.cuda.synchronize()
-        s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        s_ev.record()
-        for i in range(args.steps):
-            fn(i)
-        e_ev.record()
-        torch.cuda.synchronize()
-        res[name] = s_ev.elapsed_time(e_ev) / args.steps
     a_f, o_f = fused(0)
     a_u, o_u = unfused(0)
 
@@ -644,17 +633,26 @@ def lm_head_bench(args):
         logits = torch.ops.fp8.matmul(x, w, sc).float().view(B, T, LM_VOCAB)
         return torch.ops.spec.accept_rejection(logits, draft, rids, u, us, 1.0)
 
-    for name, fn in (("rej_fused", rej_fused), ("rej_unfused", rej_unfused)):
+    # Every path warmed up, then LM_ROUNDS rounds that time each path in turn (args.steps
+    # calls each); the median round per path. Back-to-back runs of one path drift with the
+    # clock by several percent, so paths timed in separate blocks are not comparable.
+    paths = (("gemm", gemm), ("fused", fused), ("unfused", unfused), ("rej_fused", rej_fused),
+             ("rej_unfused", rej_unfused))
+    for _, fn in paths:
         for i in range(warmup):
             fn(i)
-        torch.cuda.synchronize()
-        s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        s_ev.record()
-        for i in range(args.steps):
-            fn(i)
-        e_ev.record()
-        torch.cuda.synchronize()
-        res[name] = s_ev.elapsed_time(e_ev) / args.steps
+    torch.cuda.synchronize()
+    times = {name: [] for name, _ in paths}
+    for _ in range(LM_ROUNDS):
+        for name, fn in paths:
+            s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s_ev.record()
+            for i in range(args.steps):
+                fn(i)
+            e_ev.record()
+            torch.cuda.synchronize()
+            times[name].append(s_ev.elapsed_time(e_ev) / args.steps)
+    res = {name: sorted(v)[len(v) // 2] for name, v in times.items()}
     ra_f, ro_f = rej_fused(0)
     ra_u, ro_u = rej_unfused(0)
     flops = 2.0 * B * T * HIDDEN * LM_VOCAB
@@ -672,7 +670,7 @@ def lm_head_bench(args):
             "fused_ms": round(res["rej_fused"], 4), "unfused_ms": round(res["rej_unfused"], 4),
             "fused_over_gemm": round(res["rej_fused"] / res["gemm"], 4),
             "identical": bool(torch.equal(ra_f, ra_u) and torch.equal(ro_f, ro_u))},
-        "steps": args.steps, "warmup": warmup}))
+        "steps": args.steps, "warmup": warmup, "rounds": LM_ROUNDS}))
 
 
 PF_HEADS, PF_TOKENS, PF_CHUNK, PF_DIM = 48, 4096, 64, 128

@@ -53,6 +53,25 @@ __device__ __forceinline__ void arg_merge16(float& v, int& i) {
   }
 }
 
+// The same merge over each aligned 16-lane row by DPP moves (quad, quad pairs, half-row
+// mirror, row mirror): the rule is a total order, so the pairing does not change the result.
+template <int CTRL>
+__device__ __forceinline__ void arg_step_dpp(float& v, int& i) {
+  const float ov = __uint_as_float(npn::dpp32<CTRL>(__float_as_uint(v)));
+  const int oi = (int)npn::dpp32<CTRL>((uint32_t)i);
+  if (arg_beats(ov, oi, v, i)) {
+    v = ov;
+    i = oi;
+  }
+}
+
+__device__ __forceinline__ void arg_merge16_dpp(float& v, int& i) {
+  arg_step_dpp<npn::kDppStep[0]>(v, i);
+  arg_step_dpp<npn::kDppStep[1]>(v, i);
+  arg_step_dpp<npn::kDppStep[2]>(v, i);
+  arg_step_dpp<npn::kDppStep[3]>(v, i);
+}
+
 __device__ __forceinline__ float bf16_round(float x) {
   return npn::bf16_to_f32(npn::f32_to_bf16(x));
 }
@@ -612,6 +631,20 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void fp8_gemm_wide_kernel(WideArgs
   // Ring: chunk c in stage (c - c_lo) % 3, issued two chunks ahead of its use.
   if (c_lo < c_hi) issue(c_lo, 0);
   if (c_lo + 1 < c_hi) issue(c_lo + 1, 1);
+  // The scales of this lane's output columns, loaded now so that the epilogue does not wait
+  // for them after the last MFMA (every epilogue but the fp32 partials scales its sums):
+  // SwiGLU column tile nt of column half wc is gate (wc 0) or up (wc 1) unit u0 + nt, the
+  // others tile NH wc + nt of the group.
+  float scp[NH];
+  {
+    const bool scaled_out = a.swiglu || a.amax != nullptr || (a.split_k == 1 && !a.to_partial);
+#pragma unroll
+    for (int nt = 0; nt < NH; ++nt) {
+      const int unit = a.swiglu ? nt : NH * wc + nt;
+      const int col = a.swiglu ? wc * (a.N / 2) + n0 + 16 * nt + i : n0 + 16 * unit + i;
+      scp[nt] = scaled_out && unit < nu ? a.scale[col] : 0.0f;
+    }
+  }
 
   for (int c = c_lo; c < c_hi; ++c) {
     const int st = (c - c_lo) % NSTAGE;
@@ -687,7 +720,7 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void fp8_gemm_wide_kernel(WideArgs
 #pragma unroll
     for (int nt = 0; nt < NH; ++nt) {
       if (nt >= nu) continue;
-      const float sc = a.scale[wc * I + n0 + 16 * nt + i];
+      const float sc = scp[nt];
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) {
         if ((mt >> 1) == wc) continue;
@@ -703,8 +736,7 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void fp8_gemm_wide_kernel(WideArgs
 #pragma unroll
     for (int nt = 0; nt < NH; ++nt) {
       if (nt >= nu) continue;
-      const int col = n0 + 16 * nt + i;
-      const float sc = a.scale[wc * I + col];
+      const float sc = scp[nt];
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) {
         if ((mt >> 1) != wc) continue;
@@ -738,13 +770,17 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void fp8_gemm_wide_kernel(WideArgs
       const int unit = NH * wc + nt;
       if (unit >= nu) continue;
       const int col = n0 + 16 * unit + i;
-      const float sc = a.scale[col];
+      const float sc = scp[nt];
+      // a lane meets its columns in increasing order, so after its first column a later one
+      // wins only by being strictly larger, or NaN against a number (the first NaN stays):
+      // arg_beats for a larger index
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const float v = bf16_round(acc[mt][nt][r] * sc);
-          if (arg_beats(v, col, bv[mt][r], bi[mt][r])) {
+          const float b = bv[mt][r];
+          if (bi[mt][r] == 0x7FFFFFFF || (b == b && (v > b || v != v))) {
             bv[mt][r] = v;
             bi[mt][r] = col;
           }
@@ -753,7 +789,7 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void fp8_gemm_wide_kernel(WideArgs
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) arg_merge16(bv[mt][r], bi[mt][r]);
+      for (int r = 0; r < 4; ++r) arg_merge16_dpp(bv[mt][r], bi[mt][r]);
     // The column half wc = 1 hands its per-row bests to wc = 0 through LDS (the stages are
     // free once every wave has passed this barrier).
     __syncthreads();
@@ -791,7 +827,7 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void fp8_gemm_wide_kernel(WideArgs
     for (int nt = 0; nt < NH; ++nt) {
       const int unit = NH * wc + nt;
       if (unit >= nu) continue;
-      const float sc = a.scale[n0 + 16 * unit + i];
+      const float sc = scp[nt];
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
@@ -882,7 +918,8 @@ struct GemmPlan {
 };
 
 // Wide-kernel instantiations: column tiles per wave (a workgroup holds twice as many units).
-constexpr int kWideNH[] = {1, 2, 3, 4, 5, 6};
+// 7 is the widest whose 3-stage ring fits the 160 KiB of LDS (8 would need 168 KiB).
+constexpr int kWideNH[] = {1, 2, 3, 4, 5, 6, 7};
 
 // Wide-kernel plan: split-K factor s, column groups g (one workgroup per (group, split)),
 // column tiles per wave ntm. Modelled time, additive because the three do not overlap well
@@ -1025,7 +1062,8 @@ int launch_gemm(const GemmPlan& p, const uint16_t* x, const int8_t* w, const flo
       case 3: hipLaunchKernelGGL(fp8_gemm_wide_kernel<3>, grid, block, 0, s, wa); break;
       case 4: hipLaunchKernelGGL(fp8_gemm_wide_kernel<4>, grid, block, 0, s, wa); break;
       case 5: hipLaunchKernelGGL(fp8_gemm_wide_kernel<5>, grid, block, 0, s, wa); break;
-      default: hipLaunchKernelGGL(fp8_gemm_wide_kernel<6>, grid, block, 0, s, wa); break;
+      case 6: hipLaunchKernelGGL(fp8_gemm_wide_kernel<6>, grid, block, 0, s, wa); break;
+      default: hipLaunchKernelGGL(fp8_gemm_wide_kernel<7>, grid, block, 0, s, wa); break;
     }
   } else {
     GemmArgs ga{x, reinterpret_cast<const uint8_t*>(w), scale, out, partial, M, K, N, p.split_k,
@@ -1292,6 +1330,26 @@ bool fp8_matmul_chunk_stats_ok(int M, int K, int N) {
   if (!shape_ok(M, K, N) || N % 64 != 0) return false;
   const GemmPlan p = plan(M, K, N, true, 4);
   return p.split_k == 1 && (!p.wide || p.ualign == 4);
+}
+
+bool fp8_matmul_stats_pass_cheaper(int M, int K, int N) {
+  if (!shape_ok(M, K, N)) return false;
+  const GemmPlan q = plan(M, K, N);
+  if (!q.wide || q.split_k != 1) return false;
+  if (!fp8_matmul_chunk_stats_ok(M, K, N)) return true;
+  const GemmPlan e = plan(M, K, N, true, 4);
+  if (!e.wide) return false;
+  return (q.groups + WIDE_WG - 1) / WIDE_WG < (e.groups + WIDE_WG - 1) / WIDE_WG;
+}
+
+int fp8_matmul_unsplit(const uint16_t* x, const int8_t* w, const float* scale, uint16_t* out,
+                       int M, int K, int N, hipStream_t stream) {
+  NPN_REQUIRE(x && w && scale && out, NPN_ERR_NULL);
+  NPN_REQUIRE(shape_ok(M, K, N), NPN_ERR_SHAPE);
+  NPN_REQUIRE(NPN_ALIGNED16(x) && NPN_ALIGNED16(w) && NPN_ALIGNED16(out), NPN_ERR_ALIGN);
+  const GemmPlan p = plan(M, K, N);
+  NPN_REQUIRE(p.split_k == 1, NPN_ERR_SHAPE);
+  return launch_gemm(p, x, w, scale, out, nullptr, M, K, N, 0, false, stream);
 }
 
 int fp8_matmul_chunk_stats(const uint16_t* x, const int8_t* w, const float* scale, uint16_t* out,

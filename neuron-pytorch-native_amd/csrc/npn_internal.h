@@ -17,4 +17,14 @@ int fp8_matmul_chunk_stats(const uint16_t* x, const int8_t* w, const float* scal
                            float* cmax, uint64_t* csum, float inv_temp, int M, int K, int N,
                            hipStream_t stream);
 
+// Whether the statistics are better computed by a pass over plain logits: true when the plain
+// GEMM's plan is the wide kernel without split-K and needs fewer rounds of workgroups than the
+// plan with the statistics epilogue (whose column groups must hold whole 64-column chunks,
+// 12 of the widest tile's 14 units), or when the epilogue plan is not available.
+bool fp8_matmul_stats_pass_cheaper(int M, int K, int N);
+// out [M, N] = npn_fp8_matmul's output, for shapes whose plan has no split-K (no workspace);
+// NPN_ERR_SHAPE otherwise.
+int fp8_matmul_unsplit(const uint16_t* x, const int8_t* w, const float* scale, uint16_t* out,
+                       int M, int K, int N, hipStream_t stream);
+
 }  // namespace npn

@@ -205,15 +205,24 @@ __global__ void greedy_accept_kernel(const ArgPart* __restrict__ part,
 }
 
 // Best of one row's nparts partials, in every lane of the calling wave: lanes take the
-// partials lane, lane + 64, ... (each lane keeps its first best), then a shuffle tree. The
-// rule (NaN max, lower index on ties) is order-independent, so this equals a serial scan.
+// partials lane, lane + 64, ..., eight loads in flight per lane at a time, then a shuffle
+// tree. The rule (NaN max, lower index on ties) is a total order, so any grouping equals a
+// serial scan.
 __device__ __forceinline__ ArgPart wave_best(const ArgPart* __restrict__ row, int nparts) {
+  constexpr int kBatch = 8;
   const int lane = threadIdx.x & 63;
   float bv = -INFINITY;
   int bi = 0x7FFFFFFF;
-  for (int c = lane; c < nparts; c += 64) {
-    const ArgPart p = row[c];
-    if (beats(p.v, p.i, bv, bi)) { bv = p.v; bi = p.i; }
+  for (int c0 = lane; c0 < nparts; c0 += 64 * kBatch) {
+    ArgPart p[kBatch];
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const int c = c0 + 64 * k;
+      p[k] = c < nparts ? row[c] : ArgPart{-INFINITY, 0x7FFFFFFF};
+    }
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k)
+      if (beats(p[k].v, p[k].i, bv, bi)) { bv = p[k].v; bi = p[k].i; }
   }
   for (int off = 32; off > 0; off >>= 1) {
     const float ov = __shfl_xor(bv, off, 64);
@@ -508,32 +517,26 @@ __device__ __forceinline__ void block_from_chunks(float m, uint64_t s, float* sh
   for (int i = 0; i < nw; ++i) Sb += sh_s[i];
 }
 
-// Block statistics of fp32 logit rows: block (x, y) reads entries [8192 x, 8192 x + 8192) of
-// row row0 + y once, into registers (thread t holds the float4s at v0 + 4 (256 j + t), j < 8,
-// so for each j the 16 lanes of a DPP row hold one 64-entry chunk); each chunk's maximum m_c
-// of the scaled logits (NaN ignored; entries past V read as NaN) and S_c = sum of
-// expfix(s_v - m_c) stay on chip, and only M_b and S_b = sum F_c S_c are written. The thread
-// that holds the row's draft token also writes its E F = expfix(s - m_c) expfix(m_c - M_b),
-// so the decision reads no logits.
-template <bool kUnitTemp>
-__global__ __launch_bounds__(THREADS) void rej_stats_kernel(RejArgs a, int row0) {
-  __shared__ float sh_cm[CPB];
-  __shared__ uint64_t sh_cs[CPB];
-  __shared__ float sh_m[THREADS / 64];
-  __shared__ u128 sh_s[THREADS / 64];
-  const int row = row0 + (int)blockIdx.y;
-  const int nt = a.B * (a.K + 1);
-  const float* src = row < nt ? static_cast<const float*>(a.target) + (size_t)row * a.V
-                              : a.draft + (size_t)(row - nt) * a.V;
-  const int v0 = (int)blockIdx.x * npn::kContractBlock;
+// Entries [v0, v0 + 8192) of one logit row into registers: thread t holds entries
+// v0 + 4 (256 j + t) + k, j < 8, k < 4 (16-byte float4 loads for fp32 rows, 8-byte loads of
+// four bf16 for bf16 rows) when the whole block lies inside the row and rows are aligned
+// (`full`), else element by element with entries past V read as NaN.
+template <typename T>
+__device__ __forceinline__ void load_block(const T* src, int v0, int V, bool full,
+                                           float (&x)[32]) {
   const int t = threadIdx.x;
-  const int64_t* idp = row_draft_id(a, row);
-  float x[32];
-  if (a.vec4 && v0 + npn::kContractBlock <= a.V) {  // whole block inside the row
+  if (full) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const float4 f = *reinterpret_cast<const float4*>(src + v0 + 4 * (j * THREADS + t));
-      x[4 * j] = f.x; x[4 * j + 1] = f.y; x[4 * j + 2] = f.z; x[4 * j + 3] = f.w;
+      const int v = v0 + 4 * (j * THREADS + t);
+      if constexpr (sizeof(T) == 4) {
+        const float4 f = *reinterpret_cast<const float4*>(src + v);
+        x[4 * j] = f.x; x[4 * j + 1] = f.y; x[4 * j + 2] = f.z; x[4 * j + 3] = f.w;
+      } else {
+        const uint2 h = *reinterpret_cast<const uint2*>(src + v);
+        x[4 * j] = npn::bf16lo(h.x); x[4 * j + 1] = npn::bf16hi(h.x);
+        x[4 * j + 2] = npn::bf16lo(h.y); x[4 * j + 3] = npn::bf16hi(h.y);
+      }
     }
   } else {
 #pragma unroll
@@ -541,9 +544,35 @@ __global__ __launch_bounds__(THREADS) void rej_stats_kernel(RejArgs a, int row0)
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         const int v = v0 + 4 * (j * THREADS + t) + k;
-        x[4 * j + k] = v < a.V ? src[v] : NAN;
+        x[4 * j + k] = v < V ? elem(src, v) : NAN;
       }
   }
+}
+
+// Block statistics of logit rows (target rows of element type TT: fp32, or bf16 from the LM
+// head; draft rows fp32): block (x, y) reads entries [8192 x, 8192 x + 8192) of row row0 + y
+// once, into registers (for each j the 16 lanes of a DPP row hold one 64-entry chunk); each
+// chunk's maximum m_c of the scaled logits (NaN ignored; entries past V read as NaN) and
+// S_c = sum of expfix(s_v - m_c) stay on chip, and only M_b and S_b = sum F_c S_c are written.
+// The thread that holds the row's draft token also writes its E F = expfix(s - m_c)
+// expfix(m_c - M_b), so the decision reads no logits.
+template <bool kUnitTemp, typename TT>
+__global__ __launch_bounds__(THREADS) void rej_stats_kernel(RejArgs a, int row0) {
+  __shared__ float sh_cm[CPB];
+  __shared__ uint64_t sh_cs[CPB];
+  __shared__ float sh_m[THREADS / 64];
+  __shared__ u128 sh_s[THREADS / 64];
+  const int row = row0 + (int)blockIdx.y;
+  const int nt = a.B * (a.K + 1);
+  const int v0 = (int)blockIdx.x * npn::kContractBlock;
+  const int t = threadIdx.x;
+  const int64_t* idp = row_draft_id(a, row);
+  float x[32];
+  const bool full = a.vec4 && v0 + npn::kContractBlock <= a.V;
+  if (row < nt)
+    load_block(target_row<TT>(a, row), v0, a.V, full, x);
+  else
+    load_block(a.draft + (size_t)(row - nt) * a.V, v0, a.V, full, x);
   // the draft id through a vector load issued after the logits', so that no wait for it holds
   // them back (a scalar load of the uniform address would be waited for first)
   const int64_t id = idp != nullptr ? load_opaque(idp) : -1;
@@ -551,7 +580,7 @@ __global__ __launch_bounds__(THREADS) void rej_stats_kernel(RejArgs a, int row0)
 #pragma unroll
     for (int e = 0; e < 32; ++e) x[e] = scaled(x[e], a.inv_temp);
   }
-  // the thread whose float4 (toff >> 2 = 256 j + t) holds the draft token keeps its value
+  // the thread whose four entries (toff >> 2 = 256 j + t) include the draft token keeps its value
   const int toff = draft_id_ok(id, a.V) ? (int)id - v0 : -1;
   const bool tok_here =
       toff >= 0 && toff < npn::kContractBlock && ((toff >> 2) & (THREADS - 1)) == t;
@@ -1157,13 +1186,14 @@ RejArgs rej_args(const void* target_logits, const float* draft_logits, const int
                  reinterpret_cast<u256*>(ws + l.cm64)};
 }
 
-// Block statistics of `rows` fp32 rows starting at row0.
+// Block statistics of `rows` rows starting at row0 (target rows of element type TT).
+template <typename TT>
 void launch_stats(const RejArgs& a, int row0, int rows, hipStream_t s) {
   const dim3 grid(a.nb, rows);
   if (a.inv_temp == 1.0f)
-    hipLaunchKernelGGL(rej_stats_kernel<true>, grid, dim3(THREADS), 0, s, a, row0);
+    hipLaunchKernelGGL((rej_stats_kernel<true, TT>), grid, dim3(THREADS), 0, s, a, row0);
   else
-    hipLaunchKernelGGL(rej_stats_kernel<false>, grid, dim3(THREADS), 0, s, a, row0);
+    hipLaunchKernelGGL((rej_stats_kernel<false, TT>), grid, dim3(THREADS), 0, s, a, row0);
 }
 
 // Decision with sampling mass, then the pick (every row's block statistics and draft-token
@@ -1190,7 +1220,7 @@ int rejection_launch(const float* target_logits, const float* draft_logits,
                      int V, uint8_t* ws, hipStream_t s) {
   const RejArgs a = rej_args(target_logits, draft_logits, draft_ids, u_accept, u_sample,
                              inv_temperature, accepted, out_ids, B, K, V, false, ws);
-  launch_stats(a, 0, B * (2 * K + 1), s);
+  launch_stats<float>(a, 0, B * (2 * K + 1), s);
   return launch_decide_sample<float>(a, s);
 }
 
@@ -1347,7 +1377,15 @@ extern "C" int npn_accept_rejection_lm_head(const uint16_t* hidden, const int8_t
   uint64_t* csum = reinterpret_cast<uint64_t*>(ws + ll.csum);
   const RejArgs a = rej_args(target_logits, draft_logits, draft_ids, u_accept, u_sample,
                              inv_temperature, accepted, out_ids, B, K, V, true, ws);
-  launch_stats(a, M, B * K, s);  // draft rows
+  if (npn::fp8_matmul_stats_pass_cheaper(M, H, V)) {
+    // the plain GEMM, then one statistics pass over the bf16 target rows and the draft rows
+    const int gst = npn::fp8_matmul_unsplit(hidden, lm_head_w, lm_head_scale, target_logits, M,
+                                            H, V, s);
+    if (gst != NPN_OK) return gst;
+    launch_stats<uint16_t>(a, 0, B * (2 * K + 1), s);
+    return launch_decide_sample<uint16_t>(a, s);
+  }
+  launch_stats<uint16_t>(a, M, B * K, s);  // draft rows
   const int gst = npn::fp8_matmul_chunk_stats(hidden, lm_head_w, lm_head_scale, target_logits,
                                               cmax, csum, inv_temperature, M, H, V, s);
   if (gst != NPN_OK) return gst;

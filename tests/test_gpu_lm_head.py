@@ -165,8 +165,14 @@ def _zm(ws, R):
     return z, m
 
 
-@pytest.mark.parametrize("B,V,inv_t", [(32, 248320, 1.0), (4, 151936, 1.0 / 0.7)])
+@pytest.mark.parametrize("B,V,inv_t", [(32, 248320, 1.0), (4, 151936, 1.0 / 0.7),
+                                       (32, 16384, 1.0 / 0.7)])
 def test_lm_head_chunk_stats_bit_exact(ops, B, V, inv_t):
+    """The LM-head form's rows' Z and M against accept_rejection's and the oracle's. The shapes
+    take both routes: the plain GEMM then a statistics pass (B = 32, V = 248320, where the
+    chunk-aligned epilogue plan would need an extra round of workgroups) and the statistics
+    written by the GEMM epilogue (the narrow kernel at B = 4; the wide kernel at B = 32,
+    V = 16384, where both plans fit one round)."""
     from oracle import accept as oa
     from npn_native import call, query, stream_of
     K, H = 7, 1024

@@ -145,8 +145,9 @@ def test_fp8_split_k_plan():
     assert query("npn_fp8_matmul_split_k", 256, 5120, 14336) == 2
     assert query("npn_fp8_matmul_split_k", 256, 5120, 34816) == 1
     assert query("npn_fp8_matmul_split_k", 256, 100, 5120) == 0
-    # argmax mode never splits K; the LM head's vocabulary runs in rounds of 12-unit groups
-    assert query("npn_fp8_matmul_argmax_groups", 256, 5120, 248320) == 1294
+    # argmax mode never splits K; the LM head's vocabulary runs in rounds of 256 workgroups
+    # of the widest tiles (14 units of 16 columns: ceil(15520 / 14) = 1109 groups)
+    assert query("npn_fp8_matmul_argmax_groups", 256, 5120, 248320) == 1109
     # below 65 rows: 256-column tiles of 4 column slices (2 at 33..64 rows), and the grid
     # kept at or under 576 workgroups (1152 up to 16 rows)
     assert query("npn_fp8_matmul_argmax_groups", 16, 5120, 248320) == 248320 // 64

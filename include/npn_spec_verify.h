@@ -374,10 +374,12 @@ int npn_accept_greedy_parts(const void* parts, int nparts, const int64_t* draft_
 /* torch.ops.spec.accept_rejection_lm_head -- new op: npn_accept_rejection with the target
  * logits produced by the LM head in the same call. hidden [B*(K+1), H] bf16 (the final-normed
  * verify rows, row b*(K+1) + t), lm_head_w [H, V] e4m3fn bytes, lm_head_scale [V] f32:
- * target_logits [B*(K+1), V] bf16 is written (= npn_fp8_matmul's out), and the GEMM's epilogue
- * also writes the contract's chunk statistics of every target row, so the target rows are
- * never read back in full: the logit pass covers only the draft rows, and the sampling kernel
- * re-reads only each sequence's sampling row. accepted / out_ids equal
+ * target_logits [B*(K+1), V] bf16 is written (= npn_fp8_matmul's out). The contract's chunk
+ * statistics of the target rows come from the GEMM's epilogue where that costs the GEMM no
+ * extra round of workgroups (then the logit pass covers only the draft rows and the sampling
+ * kernel re-reads only each sequence's sampling row), else from one pass over the bf16 target
+ * rows with the draft rows (at B*(K+1) = 256 with a 248320-entry vocabulary the epilogue's
+ * chunk-aligned column groups would need a sixth round). accepted / out_ids equal
  * npn_accept_rejection's on the fp32 cast of target_logits, bit for bit, with the same
  * draft logits, ids, uniforms and inv_temperature (> 0). V % 64 == 0, H % 64 == 0, the other
  * rules as npn_accept_rejection. Workspace: npn_accept_rejection_lm_head_workspace_size

@@ -264,9 +264,10 @@ int npn_fp8_matmul_split_k(int M, int K, int N);
 
 /* The GEMM plan for these sizes, host-only (no device work), for tests and tuning -- no
  * reference counterpart. info[4] receives: kind (0 narrow kernel on a tiles x split grid,
- * 1 narrow kernel in stream-K, 2 wide kernel), the split-K factor (stream-K: partial slots),
- * the tile parameter (narrow: 16-row blocks per tile; wide: 16-column tiles per wave) and
- * the workgroups launched. NPN_ERR_SHAPE for unsupported sizes. */
+ * 1 narrow kernel in stream-K, 2 wide kernel on 256-row tiles, 3 wide kernel on 128-row
+ * tiles), the split-K factor (stream-K: partial slots), the tile parameter (narrow: 16-row
+ * blocks per tile; kind 2: 16-column tiles per wave; kind 3: 16-column units per workgroup)
+ * and the workgroups launched. NPN_ERR_SHAPE for unsupported sizes. */
 int npn_fp8_matmul_plan(int M, int K, int N, int* info);
 
 /* torch.ops.fp8.matmul_partials -- new op, no reference counterpart: the GEMM of

@@ -873,6 +873,299 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void fp8_gemm_wide_kernel(WideArgs
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// The wide kernel on 128-row tiles (64 < M), chosen by the plan where it needs less padded
+// MFMA work per CU than the 256-row kernel at the same split-K factor. Row tiles of one
+// column group take adjacent logical workgroup indices, so they run on one XCD at the same
+// time and each W byte comes from HBM once; each CU streams half the x block of the 256-row
+// kernel, and its W row pieces are about twice as long.
+// Waves: row half rh = w >> 2 (64 rows) and column quarter q. The workgroup's units form two
+// halves of H units, each half two quarters of NH and NH - ODD column tiles; quarters 0/1 are
+// half 0 and 2/3 half 1 (SwiGLU: half 0 gate units, half 1 the up units N/2 to their right,
+// so quarter q and q + 2 hold gate and up for the same rows and columns, lane for lane).
+// With ODD the quarters of one SIMD's two waves are q and q ^ 1 (q = (w & 3) ^ rh, the waves
+// of a workgroup going to the SIMDs in turn), one long and one short: every SIMD issues
+// 2 NH - 1 tiles' MFMAs per k step, and a workgroup holds 4 NH - 2 units instead of 4 NH,
+// a granularity that fits the step's shapes into 256 workgroups with less padding (gate/up:
+// 121 groups of 18 units instead of 218 of 10 at 256 rows). Same x / W stage layouts, DMA
+// ring, B-operand reads and per-output k order as the 256-row kernel, so every output (and
+// every split-K partial) is bit-identical to it.
+template <int N>
+struct TileCount {
+  static constexpr int value = N;
+};
+
+template <int NH, bool ODD>
+__global__ __launch_bounds__(WIDE_THREADS, 1) void fp8_gemm_wide128_kernel(WideArgs a) {
+  constexpr int H = ODD ? 2 * NH - 1 : 2 * NH;  // units per half
+  constexpr int QN0 = NH, QN1 = ODD ? NH - 1 : NH;
+  constexpr int NUP = 2 * H + 1;                // W stage row stride in 16-byte units (odd)
+  constexpr int XBYTES = 128 * KC * 2;          // 16 KiB x stage
+  constexpr int XI = XBYTES / (WIDE_THREADS * 16);
+  constexpr int WI = (KC * NUP + WIDE_THREADS - 1) / WIDE_THREADS;
+  constexpr int WBYTES = WI * WIDE_THREADS * 16;
+  constexpr int STAGE = XBYTES + WBYTES;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[NSTAGE * STAGE];
+  constexpr int RSW = 32 * H + 8;  // bf16 staging row stride (16 bytes of padding)
+  constexpr int RSF = 32 * H + 4;  // fp32 staging row stride, 64 rows at a time
+  constexpr int SWOFF = 4 * 64 * 16 * NH * 2;  // SwiGLU staging past the exchange slots
+  constexpr int RS2 = 16 * H + 8;
+  static_assert(128 * RSW * 2 <= NSTAGE * STAGE, "bf16 staging exceeds the LDS ring");
+  static_assert(64 * RSF * 4 <= NSTAGE * STAGE, "fp32 staging exceeds the LDS ring");
+  static_assert(SWOFF + 128 * RS2 * 2 <= NSTAGE * STAGE, "SwiGLU staging exceeds the LDS ring");
+
+  const int nwg = gridDim.x;
+  const int per_xcd = nwg / 8;
+  const int logical = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+  const int rtiles = (a.M + 127) >> 7;
+  const int rt = logical % rtiles;
+  const int gs = logical / rtiles;
+  const int sk = gs % a.split_k;
+  const int grp = gs / a.split_k;
+  if (grp >= a.groups) return;
+  const int u0 = (int)((long)grp * a.units / a.groups);
+  const int u1 = (int)((long)(grp + 1) * a.units / a.groups);
+  const int nu = u1 - u0;  // units (SwiGLU: gate units) of this group
+  if (nu <= 0) return;
+  const int n0 = 16 * u0;
+  const int nch_all = a.K / KC;
+  const int c_lo = (int)((long)nch_all * sk / a.split_k);
+  const int nchunks = (int)((long)nch_all * (sk + 1) / a.split_k) - c_lo;
+  const int m_base = rt * 128;
+  const int tid = threadIdx.x;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int rh = wv >> 2;
+  const int q = (wv & 3) ^ (ODD ? rh : 0);
+  const int qslot = (q >= 2 ? H : 0) + ((q & 1) ? QN0 : 0);  // the quarter's first unit slot
+  const bool is_short = ODD && (q & 1);
+  const int i = lane & 15, G = lane >> 4;
+  const int mlast = a.M - 1;
+  const int halfcol = a.swiglu ? a.N / 2 : 16 * H;  // column offset of half 1
+
+  // DMA of chunk c (relative to c_lo) into stage st: x rows, then W rows.
+  auto issue = [&](int c, int st) {
+    uint8_t* xs = smem + st * STAGE;
+    uint8_t* ws = xs + XBYTES;
+    const int kc = (c_lo + c) * KC;
+#pragma unroll
+    for (int qq = 0; qq < XI; ++qq) {
+      const int f = qq * WIDE_THREADS + tid;  // 16-byte slot in the x stage
+      const int row = f >> 3, pos = f & 7;
+      int m = m_base + row;
+      m = m <= mlast ? m : mlast;
+      const uint16_t* src = a.x + (size_t)m * a.K + kc + 8 * (pos ^ ((row >> 1) & 7));
+      npn::lds_dma16(src, xs + qq * (WIDE_THREADS * 16) + (tid & ~63) * 16);
+    }
+#pragma unroll
+    for (int qq = 0; qq < WI; ++qq) {
+      int f = qq * WIDE_THREADS + tid;        // 16-byte slot of the W stage
+      if (f >= KC * NUP) f = 0;               // lanes past the stage re-read slot 0 (slack)
+      const int r = f / NUP;
+      const int s = f - r * NUP;
+      int col;
+      if (a.swiglu) {                         // slots [0, H) gate, [H, 2H) up, 2H pad
+        const int hs = s >= H && s < 2 * H ? 1 : 0;
+        int uu = s - H * hs;
+        uu = uu < nu ? uu : 0;                // unused or pad slot: re-read unit u0
+        col = n0 + 16 * uu + hs * halfcol;
+      } else {
+        col = n0 + 16 * (s < nu ? s : 0);
+      }
+      const uint8_t* src = a.w + (size_t)(kc + r) * a.N + col;
+      npn::lds_dma16(src, ws + qq * (WIDE_THREADS * 16) + (tid & ~63) * 16);
+    }
+  };
+
+  f32x4 acc[4][NH];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < NH; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int trow = 8 * G + (i >> 1);
+  const int tcol = 8 * (i & 1) + 16 * qslot;
+
+  if (0 < nchunks) issue(0, 0);
+  if (1 < nchunks) issue(1, 1);
+  // column scales of this lane's tiles, loaded before the main loop (scaled epilogues only)
+  const bool scaled_out = a.swiglu || (a.split_k == 1 && !a.to_partial);
+  float scp[NH];
+#pragma unroll
+  for (int nt = 0; nt < NH; ++nt) {
+    const int s = qslot + nt;
+    const int hs = s >= H ? 1 : 0;
+    const int uu = s - H * hs;
+    const bool ok = a.swiglu ? uu < nu : s < nu;
+    scp[nt] = scaled_out && ok ? a.scale[n0 + 16 * uu + hs * halfcol + i] : 0.0f;
+  }
+
+  // The chunk loop for a wave of NTW column tiles (both loops pass the same barriers).
+  auto main_loop = [&](auto tiles) {
+    constexpr int NTW = decltype(tiles)::value;
+    for (int c = 0; c < nchunks; ++c) {
+      const int st = c % NSTAGE;
+      if (c + 1 < nchunks) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(XI + WI) : "memory");
+      else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      if (c + 2 < nchunks) issue(c + 2, (c + 2) % NSTAGE);
+      const uint8_t* xs = smem + st * STAGE;
+      const uint8_t* ws = xs + XBYTES;
+      bf16x8 aop[2][4];
+      i32x2 raw[2][NTW];
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+          const int row = 64 * rh + 16 * mt + i;
+          const int pos = (4 * ks + G) ^ ((row >> 1) & 7);
+          aop[ks][mt] = *reinterpret_cast<const bf16x8*>(xs + row * (KC * 2) + pos * 16);
+        }
+        const uint8_t* wrow = ws + (32 * ks + trow) * (16 * NUP) + tcol;
+#pragma unroll
+        for (int nt = 0; nt < NTW; ++nt) raw[ks][nt] = lds_tr8(wrow + 16 * nt);
+      }
+      bf16x8 bop[2][NTW];
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int nt = 0; nt < NTW; ++nt) {
+          u32x4 bw;
+          bw[0] = fp8x2_to_bf16x2<false>((uint32_t)raw[ks][nt][0]);
+          bw[1] = fp8x2_to_bf16x2<true>((uint32_t)raw[ks][nt][0]);
+          bw[2] = fp8x2_to_bf16x2<false>((uint32_t)raw[ks][nt][1]);
+          bw[3] = fp8x2_to_bf16x2<true>((uint32_t)raw[ks][nt][1]);
+          bop[ks][nt] = __builtin_bit_cast(bf16x8, bw);
+        }
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int nt = 0; nt < NTW; ++nt)
+#pragma unroll
+          for (int mt = 0; mt < 4; ++mt)
+            acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop[ks][mt], bop[ks][nt],
+                                                                  acc[mt][nt], 0, 0, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2 * (4 + NTW), 0);  // LDS reads
+      __builtin_amdgcn_sched_group_barrier(0x002, 4 * NTW, 0);        // k-step 0 conversions
+#pragma unroll
+      for (int j = 0; j < 4 * NTW; ++j) {                             // k-step 0 MFMAs with
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);            // k-step 1 conversions
+        __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 4 * NTW, 0);        // k-step 1 MFMAs
+    }
+  };
+  if (is_short) main_loop(TileCount<QN1>{});
+  else main_loop(TileCount<QN0>{});
+  const int ntw = is_short ? QN1 : QN0;
+
+  // Epilogues: lane (i, G) holds rows 64 rh + 16 mt + 4 G + r, unit slot qslot + nt, column i.
+  if (a.swiglu) {
+    // The gate wave (quarter q < 2) finishes row blocks 0-1 and the up wave (q + 2) blocks
+    // 2-3, each handing the other its bf16 values of the other's blocks through LDS.
+    const int I = a.N / 2;
+    __syncthreads();
+    const int pair = rh * 2 + (q & 1);
+    const int gw = q >> 1;  // 0 gate, 1 up
+    uint16_t* slot = reinterpret_cast<uint16_t*>(smem) + (size_t)(pair * 64 + lane) * (16 * NH);
+#pragma unroll
+    for (int nt = 0; nt < NH; ++nt) {
+      if (nt >= ntw) continue;
+      const float sc = scp[nt];
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+        if ((mt >> 1) == gw) continue;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) slot[16 * nt + 4 * mt + r] = npn::f32_to_bf16(acc[mt][nt][r] * sc);
+      }
+    }
+    __syncthreads();
+    uint16_t* st = reinterpret_cast<uint16_t*>(smem + SWOFF);
+    const int gbase = (q & 1) ? QN0 : 0;  // gate unit of this wave's tile 0
+#pragma unroll
+    for (int nt = 0; nt < NH; ++nt) {
+      if (nt >= ntw) continue;
+      const float sc = scp[nt];
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+        if ((mt >> 1) != gw) continue;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = 64 * rh + 16 * mt + 4 * G + r;
+          const float own = npn::bf16_to_f32(npn::f32_to_bf16(acc[mt][nt][r] * sc));
+          const float other = npn::bf16_to_f32(slot[16 * nt + 4 * mt + r]);
+          const float g = gw == 0 ? own : other, u = gw == 0 ? other : own;
+          const float sg = npn::bf16_to_f32(npn::f32_to_bf16(npn::silu(g)));
+          st[row * RS2 + 16 * (gbase + nt) + i] = npn::f32_to_bf16(sg * u);
+        }
+      }
+    }
+    __syncthreads();
+    const int pieces = 2 * nu;
+    for (int p = tid; p < 128 * pieces; p += WIDE_THREADS) {
+      const int row = p / pieces, qq = p - row * pieces;
+      const int m = m_base + row;
+      if (m < a.M)
+        *reinterpret_cast<uint4*>(a.out + (size_t)m * I + n0 + 8 * qq) =
+            *reinterpret_cast<const uint4*>(st + row * RS2 + 8 * qq);
+    }
+    return;
+  }
+  __syncthreads();
+  if (a.split_k == 1 && !a.to_partial) {
+    uint16_t* st = reinterpret_cast<uint16_t*>(smem);
+#pragma unroll
+    for (int nt = 0; nt < NH; ++nt) {
+      const int s = qslot + nt;
+      if (nt >= ntw || s >= nu) continue;
+      const float sc = scp[nt];
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          st[(64 * rh + 16 * mt + 4 * G + r) * RSW + 16 * s + i] =
+              npn::f32_to_bf16(acc[mt][nt][r] * sc);
+    }
+    __syncthreads();
+    const int pieces = 2 * nu;
+    for (int p = tid; p < 128 * pieces; p += WIDE_THREADS) {
+      const int row = p / pieces, qq = p - row * pieces;
+      const int m = m_base + row;
+      if (m < a.M)
+        *reinterpret_cast<uint4*>(a.out + (size_t)m * a.N + n0 + 8 * qq) =
+            *reinterpret_cast<const uint4*>(st + row * RSW + 8 * qq);
+    }
+    return;
+  }
+  // fp32 partials (unscaled) into slot sk, staged one row half at a time
+  float* stf = reinterpret_cast<float*>(smem);
+  float* part = a.partial + (size_t)sk * a.M * a.N;
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+    if (rh == half) {
+#pragma unroll
+      for (int nt = 0; nt < NH; ++nt) {
+        const int s = qslot + nt;
+        if (nt >= ntw || s >= nu) continue;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) stf[(16 * mt + 4 * G + r) * RSF + 16 * s + i] = acc[mt][nt][r];
+      }
+    }
+    __syncthreads();
+    const int pieces = 4 * nu;  // 16-byte pieces per staged row
+    for (int p = tid; p < 64 * pieces; p += WIDE_THREADS) {
+      const int row = p / pieces, qq = p - row * pieces;
+      const int m = m_base + 64 * half + row;
+      if (m < a.M)
+        *reinterpret_cast<float4*>(part + (size_t)m * a.N + n0 + 4 * qq) =
+            *reinterpret_cast<const float4*>(stf + row * RSF + 4 * qq);
+    }
+    __syncthreads();
+  }
+}
+
 // out = bf16(scale * sum_s partial[s]), summed in order s = 0..split_k-1.
 __global__ void fp8_splitk_reduce_kernel(const float* __restrict__ partial,
                                          const float* __restrict__ scale,
@@ -915,7 +1208,21 @@ struct GemmPlan {
   int units, groups, ntm;
   int sk_wg;   // narrow: stream-K workgroups (0: a tiles x split_k grid)
   int ualign;  // wide: column groups hold whole runs of ualign 16-column units
+  // wide on 128-row tiles (fp8_gemm_wide128_kernel<ntm, odd>): groups column groups of up to
+  // 2 h128 units, each run for every 128-row tile
+  bool rows128, odd;
+  int h128;
 };
+
+// 128-row wide kernel instantiations (NH, ODD), by units per half H = 2 NH - ODD: a
+// workgroup holds up to 2 H units (SwiGLU: H gate units and their up units).
+struct Wide128Cfg {
+  int nh;
+  bool odd;
+};
+constexpr Wide128Cfg kWide128[] = {{1, false}, {2, true}, {2, false}, {3, true}, {3, false},
+                                   {4, true},  {4, false}, {5, true}, {5, false}, {6, true},
+                                   {6, false}};
 
 // Wide-kernel instantiations: column tiles per wave (a workgroup holds twice as many units).
 // 7 is the widest whose 3-stage ring fits the 160 KiB of LDS (8 would need 168 KiB).
@@ -982,9 +1289,42 @@ bool plan_wide(int M, int K, int N, GemmPlan& p, bool no_split, int ua) {
   return true;
 }
 
+// The 128-row kernel at the 256-row plan's split-K factor s, when its whole grid fits in one
+// round of 256 workgroups and it computes at most 92 % of the padded MFMA work per workgroup
+// (128 rows x 2 H units against 256 rows x 2 ntm units per pass and round). Measured on
+// MI355X at M = 256, weights rotated through 700 MB, against the 256-row kernel at the same
+// split: gate/up 5120 x 34816 with the SwiGLU epilogue 111 -> 99 us (H = 9, 242 workgroups),
+// q/k/v 5120 x 14336 split 2 45.9 -> 43.1 us, out-projection 6144 x 5120 split 4 26.5 ->
+// 24.8 us, DeltaNet in-projection 5120 x 16512 split 2 51.8 -> 50.9 us; at equal padded
+// work (down, 17408 x 5120 split 8: 52.1 against 54.5 us) the 256-row kernel stays.
+void plan_wide128(int M, GemmPlan& p) {
+  const int rtiles = (M + 127) / 128;
+  const int s = p.split_k;
+  for (const Wide128Cfg& c : kWide128) {
+    const int h = 2 * c.nh - (c.odd ? 1 : 0);
+    const int groups = (p.units + 2 * h - 1) / (2 * h);
+    if ((long)groups * rtiles * s > WIDE_WG) continue;
+    const int rounds = (p.groups * s + WIDE_WG - 1) / WIDE_WG;
+    const long work128 = 128L * 2 * h;
+    const long work256 = 256L * 2 * p.ntm * p.passes * rounds;
+    if (100 * work128 <= 92 * work256) {
+      p.rows128 = true;
+      p.odd = c.odd;
+      p.ntm = c.nh;
+      p.h128 = h;
+      p.groups = groups;
+    }
+    return;
+  }
+}
+
 GemmPlan plan(int M, int K, int N, bool no_split = false, int ua = 1) {
   GemmPlan p{};
-  if (plan_wide(M, K, N, p, no_split, ua)) return p;
+  if (plan_wide(M, K, N, p, no_split, ua)) {
+    // the argmax and chunk-statistics epilogues exist only in the 256-row kernel
+    if (!no_split && ua == 1) plan_wide128(M, p);
+    return p;
+  }
   p = GemmPlan{};
   p.ualign = 1;
   // Narrow plan: one pass of RB = 1, 2 or 4 row blocks (M <= 64), and a split-K factor: the
@@ -1048,7 +1388,30 @@ int launch_gemm(const GemmPlan& p, const uint16_t* x, const int8_t* w, const flo
                 hipStream_t s, ArgPart* amax = nullptr, bool swiglu = false,
                 float* gmax = nullptr, float* cmax = nullptr, uint64_t* csum = nullptr,
                 float inv_temp = 1.0f) {
-  if (p.wide) {
+  if (p.wide && p.rows128) {
+    // amax / gmax / cmax are never requested on these plans (the planner keeps them on the
+    // 256-row kernel)
+    WideArgs wa{x, reinterpret_cast<const uint8_t*>(w), scale, out, partial, M, K, N,
+                swiglu ? p.units / 2 : p.units, p.groups, p.split_k, to_partial, nullptr,
+                nullptr, swiglu ? 1 : 0, 1, nullptr, nullptr, 1.0f};
+    const int rtiles = (M + 127) / 128;
+    const dim3 grid(((p.groups * rtiles * p.split_k + 7) / 8) * 8);
+    const dim3 block(WIDE_THREADS);
+#define NPN_W128(NH, ODD) \
+  if (p.ntm == NH && p.odd == ODD) hipLaunchKernelGGL((fp8_gemm_wide128_kernel<NH, ODD>), grid, block, 0, s, wa)
+    NPN_W128(1, false);
+    NPN_W128(2, true);
+    NPN_W128(2, false);
+    NPN_W128(3, true);
+    NPN_W128(3, false);
+    NPN_W128(4, true);
+    NPN_W128(4, false);
+    NPN_W128(5, true);
+    NPN_W128(5, false);
+    NPN_W128(6, true);
+    NPN_W128(6, false);
+#undef NPN_W128
+  } else if (p.wide) {
     // SwiGLU: the same groups, each of at most ntm gate units (plus their up units)
     WideArgs wa{x, reinterpret_cast<const uint8_t*>(w), scale, out, partial, M, K, N,
                 swiglu ? p.units / 2 : p.units, p.groups, p.split_k, to_partial, amax, gmax,
@@ -1220,7 +1583,12 @@ extern "C" int npn_fp8_matmul_plan(int M, int K, int N, int* info) {
   NPN_REQUIRE(info != nullptr, NPN_ERR_NULL);
   NPN_REQUIRE(shape_ok(M, K, N), NPN_ERR_SHAPE);
   const GemmPlan p = plan(M, K, N);
-  if (p.wide) {
+  if (p.wide && p.rows128) {
+    info[0] = 3;
+    info[1] = p.split_k;
+    info[2] = 2 * p.h128;
+    info[3] = ((p.groups * ((M + 127) / 128) * p.split_k + 7) / 8) * 8;
+  } else if (p.wide) {
     info[0] = 2;
     info[1] = p.split_k;
     info[2] = p.ntm;
@@ -1339,7 +1707,8 @@ bool fp8_matmul_stats_pass_cheaper(int M, int K, int N) {
   if (!fp8_matmul_chunk_stats_ok(M, K, N)) return true;
   const GemmPlan e = plan(M, K, N, true, 4);
   if (!e.wide) return false;
-  return (q.groups + WIDE_WG - 1) / WIDE_WG < (e.groups + WIDE_WG - 1) / WIDE_WG;
+  const int q_rounds = q.rows128 ? 1 : (q.groups + WIDE_WG - 1) / WIDE_WG;
+  return q_rounds < (e.groups + WIDE_WG - 1) / WIDE_WG;
 }
 
 int fp8_matmul_unsplit(const uint16_t* x, const int8_t* w, const float* scale, uint16_t* out,

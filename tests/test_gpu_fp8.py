@@ -65,7 +65,9 @@ def test_split_16(ops, M, K, N):
 
 # The nine (M, N) shapes of the FP8 projection workload at K = 5120, each with the plan it
 # runs: (kind, split-K or stream-K slots, tile parameter, workgroups); kind 0 = narrow
-# kernel on a tiles x split grid, 1 = narrow kernel in stream-K, 2 = wide kernel.
+# kernel on a tiles x split grid, 1 = narrow kernel in stream-K, 2 = wide kernel on 256-row
+# tiles (tile parameter: column tiles per wave), 3 = wide kernel on 128-row tiles (tile
+# parameter: units of 16 columns per workgroup).
 CONFIG3_PLANS = {
     (8, 5120): (0, 16, 1, 320),
     (8, 17408): (1, 7, 1, 476),
@@ -73,9 +75,9 @@ CONFIG3_PLANS = {
     (64, 5120): (0, 8, 4, 160),
     (64, 17408): (1, 7, 4, 476),
     (64, 34816): (1, 5, 4, 512),
-    (256, 5120): (2, 4, 3, 216),
-    (256, 17408): (2, 2, 5, 224),
-    (256, 34816): (2, 1, 5, 224),
+    (256, 5120): (3, 4, 10, 256),
+    (256, 17408): (3, 2, 18, 248),
+    (256, 34816): (3, 1, 18, 248),
 }
 
 
@@ -120,6 +122,53 @@ def test_config3_every_column(ops, M, N):
         assert np.all(np.abs(got[:, c0:c1] - rref)[diff] <= ulp[diff] * 1.0001)
         flips += int(diff.sum())
     assert flips <= 0.01 * M * N, f"{flips} of {M * N} outputs differ from the rounded oracle"
+
+
+# One shape for every 128-row configuration (units per workgroup 4..24, i.e. 1..6 column
+# tiles per long quarter, with and without the short quarters), without and with split-K,
+# at row counts that leave the last 128-row tile partial (72, 130, 300).
+ROWS128_SHAPES = [
+    (72, 512, 9216, 1, 4), (72, 512, 17408, 1, 6), (72, 512, 25600, 1, 8),
+    (72, 512, 33792, 1, 10), (300, 512, 14336, 1, 12), (130, 512, 25600, 1, 14),
+    (300, 512, 19456, 1, 16), (130, 512, 33792, 1, 18), (300, 512, 24576, 1, 20),
+    (300, 512, 27648, 1, 22), (300, 512, 30720, 1, 24),
+    (72, 1024, 2048, 8, 4), (72, 1024, 5120, 4, 6), (72, 1024, 7168, 4, 8),
+    (72, 1024, 9216, 4, 10), (72, 2048, 11264, 4, 12), (72, 2048, 13312, 4, 14),
+    (300, 1024, 5120, 4, 16), (130, 2048, 9216, 4, 18), (300, 2048, 6144, 4, 20),
+    (300, 2048, 7168, 4, 22)]
+
+
+@pytest.mark.parametrize("M,K,N,S,U", ROWS128_SHAPES)
+def test_rows128_plans(ops, M, K, N, S, U):
+    """The wide kernel on 128-row tiles, one shape per configuration: the plan asserted,
+    columns of the first, a middle and the last column group plus a random sample against
+    the oracle, and, where K is not split, every output bit-identical to the 256-row kernel
+    (npn_fp8_matmul_rowmax never takes the 128-row plans, and both sum every output's k
+    steps in the same order)."""
+    kind, split, units, _ = _plan(M, K, N)
+    assert (kind, split, units) == (3, S, U)
+    g = torch.Generator().manual_seed(M + K + N)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    w, scale = fp8_weights(N, K, seed=N + 3)
+    xd, wd, sd = x.cuda(), w.cuda(), scale.reshape(N, 1).cuda()
+    got = ops.fp8.matmul(xd, wd, sd)
+    if S == 1:
+        from npn_native import call, query, stream_of
+        G = query("npn_fp8_matmul_argmax_groups", M, K, N)
+        ref = torch.empty_like(got)
+        gmax = torch.empty((M, G), dtype=torch.float32, device="cuda")
+        call("npn_fp8_matmul_rowmax", xd, wd, sd, ref, gmax, M, K, N, stream_of(xd))
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(N)
+    span = 16 * U
+    mid = (N // 2) // span * span
+    cols = np.unique(np.concatenate([np.arange(span), np.arange(mid, mid + span),
+                                     np.arange(N - span, N), rng.choice(N, 256, replace=False)]))
+    ref = of.fp8_matmul(bits(x), w.numpy()[:, cols], scale.numpy()[cols])
+    assert_rel_close(got.float().cpu().double().numpy()[:, cols], round_to_bf16(ref),
+                     out_unit=BF16_ULP, name=f"fp8 rows128 M={M} K={K} N={N}")
 
 
 @pytest.mark.parametrize("M,N", [(8, 5120), (64, 17408), (256, 34816)])

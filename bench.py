@@ -431,7 +431,7 @@ def config1_bench(args):
 
         ms_v = time_calls(verify, args.steps, args.warmup)
         ms_r = time_calls(rollback, args.steps, args.warmup)
-        row = {"B": nb, "workgroups": nb * Hv, "verify_ms": round(ms_v, 4),
+        row = {"B": nb, "heads": nb * Hv, "verify_ms": round(ms_v, 4),
                "rollback_ms": round(ms_r, 4)}
         row.update(hbm_row(dn_verify_bytes(nb), ms_v))
         rows.append(row)

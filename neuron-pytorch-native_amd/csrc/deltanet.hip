@@ -41,6 +41,7 @@ struct DnArgs {
   float* ckpt;
   uint16_t* out;
   int B, T, Hk, Hv;
+  int nsplit;  // workgroups per head, each storing 128 / nsplit of the head's columns
 };
 
 // Depthwise causal conv (4 taps, oldest first) + bias + SiLU of channel c over T tokens.
@@ -76,16 +77,27 @@ __device__ __forceinline__ void conv_channel(const uint16_t* __restrict__ cs,
 // checkpoint row is one 256-byte coalesced store per wave; the q / k L2 norms (before the
 // loop) and the output RMS norm (after it) are wave reductions over the head's 128 channels.
 // The per-token q, k, v and o vectors live in LDS.
+// Small batches run nsplit (2 or 4) workgroups per head: each computes the whole head (the
+// same operations in the same order, so the same bits) but stores only its 128 / nsplit
+// columns of every checkpoint and output row. The checkpoint stores, which a CU issues at a
+// limited rate, then spread over nsplit times as many CUs; a head's workgroups are heads
+// blocks apart, so with heads % 8 == 0 they share an XCD (and its L2 copy of the state).
 template <int TMAX, int P>
 __global__ __launch_bounds__(128 * P) void dn_verify_kernel(DnArgs a) {
   constexpr int R = D / P;             // state rows per thread
   constexpr int NT = 128 * P;
-  const int b = blockIdx.x / a.Hv;
-  const int h = blockIdx.x - b * a.Hv;
+  const int heads = a.B * a.Hv;
+  const int split = blockIdx.x / heads;
+  const int bh = blockIdx.x - split * heads;
+  const int b = bh / a.Hv;
+  const int h = bh - b * a.Hv;
+  const int cspan = D / a.nsplit;
+  const int cs0 = split * cspan;        // this workgroup stores columns [cs0, cs0 + cspan)
   const int tid = threadIdx.x;
   const int lane = tid & (npn::kWave - 1);
   const int wid = tid >> 6;
   const int c = (wid & 1) * 64 + lane;   // state column (v index)
+  const bool c_mine = c >= cs0 && c < cs0 + cspan;
   const int part = wid >> 1;             // rows part * R .. part * R + R - 1
   const int r0 = part * R;
   const int T = a.T;
@@ -194,8 +206,10 @@ __global__ __launch_bounds__(128 * P) void dn_verify_kernel(DnArgs a) {
       // Nontemporal stores: write-allocating ones leave part of the checkpoints to drain from
       // the memory-side cache during the GEMMs that follow (the step measured ~1% slower).
       float* dst = ck + (size_t)t * a.Hv * tile;
+      if (c_mine) {
 #pragma unroll
-      for (int r = 0; r < R; ++r) __builtin_nontemporal_store(S[r], dst + (size_t)r * D);
+        for (int r = 0; r < R; ++r) __builtin_nontemporal_store(S[r], dst + (size_t)r * D);
+      }
     }
   }
   __syncthreads();
@@ -211,8 +225,8 @@ __global__ __launch_bounds__(128 * P) void dn_verify_kernel(DnArgs a) {
     }
   }
   __syncthreads();
-  for (int idx = tid; idx < T * D; idx += NT) {
-    const int t = idx / D, cc = idx - t * D;
+  for (int idx = tid; idx < T * cspan; idx += NT) {
+    const int t = idx / cspan, cc = cs0 + (idx - t * cspan);
     const size_t oi = (((size_t)b * T + t) * a.Hv + h) * D + cc;
     const float zz = npn::bf16_to_f32(a.z[oi]);
     a.out[oi] = npn::f32_to_bf16(s_o[t][cc] * s_ro[t] * a.norm_weight[cc] * npn::silu(zz));
@@ -313,13 +327,20 @@ int check_heads(int k_heads, int v_heads) {
 // 183 us, 67 % of HBM peak).
 int row_parts(int heads) { return heads < 192 ? 8 : (heads < 1536 ? 4 : 2); }
 
+// Workgroups per head: enough that up to 128 heads still occupy about 192 CUs. Measured at
+// 16/48 heads, T = 8, B = 1: 17.2 us with one workgroup per head, 15.9 us with four, 28.3 us
+// with eight (two workgroups per CU, each computing its whole head).
+int col_splits(int heads) { return heads <= 64 ? 4 : (heads <= 128 ? 2 : 1); }
+
 template <int TMAX>
-void launch_verify(const DnArgs& a, hipStream_t s) {
+void launch_verify(DnArgs a, hipStream_t s) {
   const int heads = a.B * a.Hv;
+  a.nsplit = col_splits(heads);
+  const dim3 grid(heads * a.nsplit);
   switch (row_parts(heads)) {
-    case 2: hipLaunchKernelGGL((dn_verify_kernel<TMAX, 2>), dim3(heads), dim3(256), 0, s, a); break;
-    case 4: hipLaunchKernelGGL((dn_verify_kernel<TMAX, 4>), dim3(heads), dim3(512), 0, s, a); break;
-    default: hipLaunchKernelGGL((dn_verify_kernel<TMAX, 8>), dim3(heads), dim3(1024), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((dn_verify_kernel<TMAX, 2>), grid, dim3(256), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((dn_verify_kernel<TMAX, 4>), grid, dim3(512), 0, s, a); break;
+    default: hipLaunchKernelGGL((dn_verify_kernel<TMAX, 8>), grid, dim3(1024), 0, s, a); break;
   }
 }
 

@@ -3,7 +3,8 @@
 Covers deltanet::full / full_batched (the reference's per-rank decode shapes, seed 11 as in
 contrib/qwen3.6-27b/kernels/tests/test_deltanet_full.py:58-73), deltanet::verify_batched at
 the single-layer workload (B=1, T=5, 4/4 heads) and full width (16/48 heads, T=8), index-based
-and copy-based rollback, and a B=32 full-size run checked on sampled sequences.
+and copy-based rollback, a B=32 full-size run checked on sampled sequences, and the
+column-split launch of small batches against the unsplit one, bit for bit.
 Bar: 2e-3 relative (tests/_util.py); conv windows are data movement and must be bit-exact.
 """
 import numpy as np
@@ -168,6 +169,24 @@ def test_row_split_batches_sampled(ops, B, parts):
         ck, out = od.deltanet_verify(*deltanet_oracle_args(sl), Hk, Hv)
         assert_rel_close(gck[b:b + 1], ck, name=f"ckpt[b={b}]")
         assert_rel_close(gout[b:b + 1], out, out_unit=BF16_U, name=f"out[b={b}]")
+
+
+def test_column_split_launch_is_bit_identical(ops):
+    """Up to 128 heads a head runs as 4 (up to 64 heads) or 2 workgroups that each compute the
+    whole head and store a quarter or half of its columns; from 129 heads one workgroup per
+    head. All three launches use 8 row parts below 192 heads, so a sequence's checkpoints
+    and outputs must come out bit for bit the same at B = 1 (48 heads, 4 splits), B = 2
+    (96 heads, 2 splits) and B = 3 (144 heads, unsplit). The split launch itself is checked
+    against the oracle by test_row_split_batches_sampled at B = 1."""
+    Hk, Hv, T = 16, 48, 8
+    d = deltanet_inputs(3, T, Hk, Hv, seed=77)
+    ck3, out3 = _verify_gpu(ops, d)
+    for B in (1, 2):
+        sl = {k: (v[:B] if k in ("state", "mixed_qkv", "conv_state", "a_out", "b_out", "z")
+                  else v) for k, v in d.items()}
+        ck, out = _verify_gpu(ops, sl)
+        assert np.array_equal(ck, ck3[:B]), f"ckpt B={B}"
+        assert np.array_equal(out, out3[:B]), f"out B={B}"
 
 
 def test_rejects_bad_shapes(ops):

@@ -19,7 +19,11 @@ Bars:
     (M = 256, wide kernel) and a small one (M = 64, narrow kernel), temperature 1 and 1/0.7;
   - the contract statistics its GEMM epilogue produces: every row's Z and M (left in the
     workspace) bit-identical to accept_rejection's and to the oracle's row_weights, through
-    both GEMM kernels (M = 256 wide, M = 32 narrow), with +-inf and NaN logits in some rows.
+    both GEMM kernels (M = 256 wide, M = 32 narrow), with +-inf and NaN logits in some rows;
+  - the argmax epilogue with planted exact ties (copies of a row's best column at lower and
+    higher columns, in other column groups) and NaN columns, through the wide kernel in rounds
+    (M = 256, N = 248320), in one round (N = 34816) and the narrow kernel (M = 40), against
+    fp8::matmul + torch.argmax.
 """
 import numpy as np
 import pytest
@@ -51,6 +55,39 @@ def test_matmul_argmax_equals_torch_argmax(ops, M, K, N):
     torch.cuda.synchronize()
     assert torch.equal(ids, torch.argmax(logits, dim=-1))
     assert torch.equal(ids, ref_ids) and torch.equal(vals, ref_vals)
+
+
+@pytest.mark.parametrize("M,K,N,nan_cols", [(256, 256, 248320, False), (256, 256, 248320, True),
+                                            (256, 512, 34816, True), (40, 256, 151936, False),
+                                            (40, 256, 151936, True)])
+def test_matmul_argmax_ties_and_nan(ops, M, K, N, nan_cols):
+    """Exact ties at the row maximum: the best columns of some rows copied (weights and scale)
+    to lower and higher columns in other column groups, so the lowest copy must win; with
+    nan_cols, two columns made NaN by an e4m3fn NaN weight, so every row takes the first."""
+    g = torch.Generator(device="cuda").manual_seed(N + K + M)
+    x = torch.randn(M, K, generator=g, device="cuda").to(torch.bfloat16)
+    w, sc = _gpu_weights(K, N, N)
+    best = ops.fp8.matmul(x, w, sc).float().argmax(1)
+    rng = np.random.default_rng(N + M)
+    for m in rng.choice(M, min(M, 24), replace=False).tolist():
+        j = int(best[m])
+        for dst in (j // 3, (j + N) // 2, int(rng.integers(0, N))):
+            if dst != j:
+                w[:, dst] = w[:, j]
+                sc[dst] = sc[j]
+    if nan_cols:
+        for c in (N // 3 + 5, 2 * N // 3 + 1):
+            w[7, c] = 0x7F                             # e4m3fn NaN
+    vals, ids = ops.fp8.matmul_argmax(x, w, sc)
+    logits = ops.fp8.matmul(x, w, sc).float()
+    torch.cuda.synchronize()
+    assert torch.equal(ids, torch.argmax(logits, dim=-1))
+    if nan_cols:
+        assert (ids == N // 3 + 5).all() and torch.isnan(vals).all()
+    else:
+        assert torch.equal(vals, logits.max(dim=-1).values)
+        ties = (logits == logits.max(dim=-1, keepdim=True).values).sum(1)
+        assert (ties >= 2).sum() >= min(M, 24) // 2    # the planted ties are there
 
 
 def test_matmul_argmax_matches_oracle(ops):

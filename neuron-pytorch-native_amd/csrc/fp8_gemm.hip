@@ -746,7 +746,7 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void fp8_gemm_wide_kernel(WideArgs
           const float own = npn::bf16_to_f32(npn::f32_to_bf16(acc[mt][nt][r] * sc));
           const float other = npn::bf16_to_f32(slot[16 * nt + 4 * mt + r]);
           const float g = wc == 0 ? own : other, u = wc == 0 ? other : own;
-          const float sg = npn::bf16_to_f32(npn::f32_to_bf16(npn::silu(g)));
+          const float sg = npn::bf16_to_f32(npn::f32_to_bf16(npn::silu_bf16(g)));
           st[row * RSW + 16 * nt + i] = npn::f32_to_bf16(sg * u);
         }
       }
@@ -1102,7 +1102,7 @@ __global__ __launch_bounds__(WIDE_THREADS, 1) void fp8_gemm_wide128_kernel(WideA
           const float own = npn::bf16_to_f32(npn::f32_to_bf16(acc[mt][nt][r] * sc));
           const float other = npn::bf16_to_f32(slot[16 * nt + 4 * mt + r]);
           const float g = gw == 0 ? own : other, u = gw == 0 ? other : own;
-          const float sg = npn::bf16_to_f32(npn::f32_to_bf16(npn::silu(g)));
+          const float sg = npn::bf16_to_f32(npn::f32_to_bf16(npn::silu_bf16(g)));
           st[row * RS2 + 16 * (gbase + nt) + i] = npn::f32_to_bf16(sg * u);
         }
       }
@@ -1204,7 +1204,7 @@ __global__ void fp8_splitk_swiglu_kernel(const float* __restrict__ partial,
   }
   const float gb = npn::bf16_to_f32(npn::f32_to_bf16(g * scale[j]));
   const float ub = npn::bf16_to_f32(npn::f32_to_bf16(u * scale[I + j]));
-  const float sb = npn::bf16_to_f32(npn::f32_to_bf16(npn::silu(gb)));
+  const float sb = npn::bf16_to_f32(npn::f32_to_bf16(npn::silu_bf16(gb)));
   out[idx] = npn::f32_to_bf16(sb * ub);
 }
 

@@ -164,7 +164,7 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restric
     unpack8(*reinterpret_cast<const u32x4*>(gu + m * 2 * I + I + 8 * j), u);
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      const float s = npn::bf16_to_f32(npn::f32_to_bf16(npn::silu(g[k])));
+      const float s = npn::bf16_to_f32(npn::f32_to_bf16(npn::silu_bf16(g[k])));
       o[k] = s * u[k];
     }
     *reinterpret_cast<u32x4*>(y + m * I + 8 * j) = pack8(o);

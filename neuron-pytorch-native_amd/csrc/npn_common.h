@@ -16,12 +16,14 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t b) {
   return __uint_as_float(static_cast<uint32_t>(b) << 16);
 }
 
-// float -> bf16 bits, round to nearest even (NaN kept quiet).
+// float -> bf16 bits, round to nearest even (NaN kept quiet). Both results are formed and one
+// is selected (v_cndmask): an early return for NaN compiled to an exec-mask branch around
+// every conversion of the GEMM epilogues.
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x007FFFFFu)) return static_cast<uint16_t>((u >> 16) | 0x40u);
-  u += 0x7FFFu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t rounded = (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+  const uint32_t quiet = (u >> 16) | 0x40u;
+  return static_cast<uint16_t>(f != f ? quiet : rounded);
 }
 
 // Two bf16 packed in a uint32 (low half = first element).
@@ -29,6 +31,11 @@ __device__ __forceinline__ float bf16lo(uint32_t p) { return __uint_as_float(p <
 __device__ __forceinline__ float bf16hi(uint32_t p) { return __uint_as_float(p & 0xFFFF0000u); }
 
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x)); }
+// The same with the fast division (reciprocal and multiply, denominators past 2^96 scaled
+// first; about 2 ulp in fp32 instead of a correctly rounded quotient), for the SwiGLU, whose
+// callers round the result to bf16 at once. Every SwiGLU path (the GEMM epilogues, the split-K
+// SwiGLU and glue::silu_mul) uses this one, so fused and unfused outputs stay bit-identical.
+__device__ __forceinline__ float silu_bf16(float x) { return __fdividef(x, 1.0f + __expf(-x)); }
 __device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + __expf(-x)); }
 __device__ __forceinline__ float softplus(float x) {
   // torch.nn.functional.softplus (beta=1, threshold=20)

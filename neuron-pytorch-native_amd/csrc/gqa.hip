@@ -334,6 +334,7 @@ __global__ __launch_bounds__(NRT * 64, NST <= 2 ? 2 : 1) void gqa_attn_kernel(At
   const int row = w * 16 + i;  // this lane's query row (B-operand column / C column)
 
   __shared__ __attribute__((aligned(16))) uint8_t smem[NST * STAGE];
+  const unsigned smem_lds = __builtin_amdgcn_readfirstlane(npn::lds_addr(smem));
 
   // Per-lane constants. DMA source offset within a 2-row block; LDS bases of the operand
   // reads: K row i (+16 for the second key tile), chunk 4*ks + G; V (transposed reads)
@@ -365,22 +366,36 @@ __global__ __launch_bounds__(NRT * 64, NST <= 2 ? 2 : 1) void gqa_attn_kernel(At
     // V block j - 16, DPW slots per wave; slots past 32 (NRT * DPW > 32) fill the slack.
     // A step that reaches past kend (a pair's last) clamps its rows to kend - 1, so V rows
     // the mask removes still hold finite cache data.
+    // Each slot's LDS offset within a stage and its source at step 0 are fixed for the
+    // segment (wave-uniform, kept in SGPRs), so a step's DMAs are one 64-bit add each; the
+    // test for a step past kend is made once per step rather than once per slot.
+    unsigned sdst[DPW];
+    const uint8_t* ssrc[DPW];
+#pragma unroll
+    for (int q = 0; q < DPW; ++q) {
+      const int j = w + NRT * q;  // wave-uniform slot
+      const bool isv = j >= KS / 2;
+      const int blk = (isv ? j - KS / 2 : j) & (KS / 2 - 1);
+      sdst[q] = j < KS ? (isv ? KTILE + blk * VBLK : blk * KBLK) : KTILE + VTILE;
+      ssrc[q] = (isv ? vb : kb) + (size_t)(c0 + 2 * blk) * DH * 2;
+    }
     auto dma = [&](int s) {
       const int k0 = c0 + s * KS;
       uint8_t* st = smem + (s % NST) * STAGE;
-      const bool tail = k0 + KS > kend;
+      if (k0 + KS <= kend) {
+        const size_t step = (size_t)s * KS * DH * 2;
+        const unsigned st_lds = smem_lds + (unsigned)((s % NST) * STAGE);
 #pragma unroll
-      for (int q = 0; q < DPW; ++q) {
-        const int j = w + NRT * q;  // wave-uniform slot
-        const bool isv = j >= KS / 2;
-        const int blk = (isv ? j - KS / 2 : j) & (KS / 2 - 1);
-        uint8_t* dst = j < KS ? st + (isv ? KTILE + blk * VBLK : blk * KBLK) : st + KTILE + VTILE;
-        const uint8_t* src = isv ? vb : kb;
-        if (!tail) {
-          npn::lds_dma16_soff(src + (size_t)(k0 + 2 * blk) * DH * 2, lane_src, dst);
-        } else {
+        for (int q = 0; q < DPW; ++q) npn::lds_dma16_soff(ssrc[q] + step, lane_src, st_lds + sdst[q]);
+      } else {
+#pragma unroll
+        for (int q = 0; q < DPW; ++q) {
+          const int j = w + NRT * q;
+          const bool isv = j >= KS / 2;
+          const int blk = (isv ? j - KS / 2 : j) & (KS / 2 - 1);
           const int key = min(k0 + 2 * blk + (lane & 1), kend - 1);
-          npn::lds_dma16_soff(src, (unsigned)key * DH * 2 + (unsigned)(lane >> 1) * 16, dst);
+          npn::lds_dma16_soff(isv ? vb : kb, (unsigned)key * DH * 2 + (unsigned)(lane >> 1) * 16,
+                              st + sdst[q]);
         }
       }
     };

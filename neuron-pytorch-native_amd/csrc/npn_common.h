@@ -124,12 +124,33 @@ __device__ __forceinline__ void lds_dma16(const void* g, const void* lds_base) {
       : "memory");
 }
 
-// Same DMA with a wave-uniform global base (SGPR pair) and a 32-bit per-lane byte offset,
-// which keeps one VGPR per lane live instead of a 64-bit address.
+// Same DMA with a wave-uniform global base (SGPR pair), a 32-bit per-lane byte offset (one
+// VGPR per lane live instead of a 64-bit address) and the LDS base as a wave-uniform LDS
+// address (no generic-to-LDS pointer conversion, whose null check costs four scalar
+// instructions per DMA).
+__device__ __forceinline__ void lds_dma16_soff(const void* sbase, unsigned voff,
+                                               unsigned lds_addr) {
+  const unsigned base = __builtin_amdgcn_readfirstlane(lds_addr);
+  unsigned saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %3\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, %2\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(voff), "s"(sbase), "s"(base)
+      : "memory");
+}
+
+// LDS address of a pointer into __shared__ memory.
+__device__ __forceinline__ unsigned lds_addr(const void* p) {
+  return (unsigned)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
+}
+
 __device__ __forceinline__ void lds_dma16_soff(const void* sbase, unsigned voff,
                                                const void* lds_base) {
-  const unsigned base = __builtin_amdgcn_readfirstlane(
-      (unsigned)(uintptr_t)(__attribute__((address_space(3))) const void*)lds_base);
+  const unsigned base = __builtin_amdgcn_readfirstlane(lds_addr(lds_base));
   unsigned saved;
   asm volatile(
       "s_mov_b32 %0, m0\n\t"

@@ -124,6 +124,11 @@ struct GemmArgs {
   float* cmax;
   uint64_t* csum;
   float inv_temp;
+  // narrow kernel, tiles1 > 0: a second matrix in the same launch (partials only, no
+  // stream-K): column tiles [0, tiles1) are w's, the rest w2's [K, N2] with partials2
+  const uint8_t* w2;
+  float* partial2;
+  int N2, tiles1;
 };
 
 __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
@@ -167,7 +172,16 @@ __device__ __forceinline__ void wait_tiles(int pend) {
 }
 
 template <int RB, int NS, int NWV>
-__global__ __launch_bounds__(NWV * 64, 1) void fp8_gemm_narrow_kernel(GemmArgs a) {
+__global__ __launch_bounds__(NWV * 64, 1) void fp8_gemm_narrow_kernel(GemmArgs ka) {
+  // A two-matrix launch runs the second matrix's tiles with its pointers and width.
+  GemmArgs a = ka;
+  int tile = blockIdx.x;
+  if (ka.tiles1 > 0 && tile >= ka.tiles1) {
+    a.w = ka.w2;
+    a.N = ka.N2;
+    a.partial = ka.partial2;
+    tile -= ka.tiles1;
+  }
   constexpr int NTH = NWV * 64;
   constexpr int CH = NWV / RB;               // column slices
   constexpr int CB = 16 / CH;                // columns (bytes) per lane
@@ -312,7 +326,7 @@ __global__ __launch_bounds__(NWV * 64, 1) void fp8_gemm_narrow_kernel(GemmArgs a
     return;
   }
 
-  const int n0 = blockIdx.x * NT;
+  const int n0 = tile * NT;
   const int sk = blockIdx.y;
   const int ks_lo = (int)(((long)nks * sk) / a.split_k);
   const int ks_hi = (int)(((long)nks * (sk + 1)) / a.split_k);
@@ -1453,6 +1467,31 @@ int launch_gemm(const GemmPlan& p, const uint16_t* x, const int8_t* w, const flo
   return npn_launch_status();
 }
 
+// The split-K partials of two GEMMs of the same x ([M, K], M <= 64) in one narrow launch,
+// W1 [K, N1] into p1 [S][M][N1] and W2 [K, N2] into p2 [S][M][N2]: the same tiles, k ranges
+// and sums as two launches of their plans, which must be narrow tiles x split grids with one
+// pass and the same row blocks and split-K factor S. Returns false (nothing launched) when
+// they are not.
+bool launch_gemm_pair_partials(const uint16_t* x, const int8_t* w1, float* p1, int N1,
+                               const int8_t* w2, float* p2, int N2, int M, int K,
+                               hipStream_t s) {
+  const GemmPlan a = plan(M, K, N1), b = plan(M, K, N2);
+  if (a.wide || b.wide || a.sk_wg > 0 || b.sk_wg > 0 || a.passes != 1 || b.passes != 1 ||
+      a.mt != b.mt || a.split_k != b.split_k)
+    return false;
+  const int t1 = (N1 + NT - 1) / NT, t2 = (N2 + NT - 1) / NT;
+  GemmArgs ga{x, reinterpret_cast<const uint8_t*>(w1), nullptr, nullptr, p1, M, K, N1,
+              a.split_k, 1, nullptr, nullptr, 0, nullptr, nullptr, 1.0f,
+              reinterpret_cast<const uint8_t*>(w2), p2, N2, t1};
+  const dim3 grid(t1 + t2, a.split_k, 1);
+  switch (a.mt) {
+    case 1: hipLaunchKernelGGL((fp8_gemm_narrow_kernel<1, 4, 4>), grid, dim3(256), 0, s, ga); break;
+    case 2: hipLaunchKernelGGL((fp8_gemm_narrow_kernel<2, 4, 8>), grid, dim3(512), 0, s, ga); break;
+    default: hipLaunchKernelGGL((fp8_gemm_narrow_kernel<4, 4, 8>), grid, dim3(512), 0, s, ga); break;
+  }
+  return true;
+}
+
 // The end of deltanet::full_fp8's in-projections, in one launch after the two GEMMs:
 //  - blocks [0, nq): the qkv GEMM's split-K partials reduced in slot order and scaled into
 //    bf16 mixed_qkv (the values npn_fp8_matmul writes; a sum of one slot is that slot), and the
@@ -1742,8 +1781,9 @@ int fp8_matmul_chunk_stats(const uint16_t* x, const int8_t* w, const float* scal
 }  // namespace npn
 
 // deltanet::full_fp8: the four in-projections of one decode token, then the token step of
-// deltanet::full on their outputs. Four launches: the qkv and z GEMMs writing split-K partials
-// (the plans of npn_fp8_matmul for one row), the finishing kernel above (mixed_qkv and z as
+// deltanet::full on their outputs. Three launches: the qkv and z GEMMs writing split-K partials
+// (the plans of npn_fp8_matmul for one row, both in one narrow launch where the two plans share
+// their split-K factor, else one launch each), the finishing kernel above (mixed_qkv and z as
 // npn_fp8_matmul's bf16 outputs, the new conv window, a_out and b_out in float32, not rounded),
 // and the DeltaNet token step (npn_deltanet_verify with T = 1).
 extern "C" size_t npn_deltanet_full_fp8_workspace_size(int hidden, int k_heads, int v_heads) {
@@ -1783,10 +1823,17 @@ extern "C" int npn_deltanet_full_fp8(
   hipStream_t s = static_cast<hipStream_t>(stream);
   float* pq = reinterpret_cast<float*>(ws + l.pq);
   float* pz = reinterpret_cast<float*>(ws + l.pz);
-  int st = launch_gemm(plan(1, hidden, qkv), x, qkv_w, nullptr, nullptr, pq, 1, hidden, qkv, 1,
+  // both GEMMs in one launch where their plans allow (the same partials as two launches)
+  int st = NPN_OK;
+  if (launch_gemm_pair_partials(x, qkv_w, pq, qkv, z_w, pz, zn, 1, hidden, s)) {
+    st = npn_launch_status();
+  } else {
+    st = launch_gemm(plan(1, hidden, qkv), x, qkv_w, nullptr, nullptr, pq, 1, hidden, qkv, 1,
+                     false, s);
+    if (st == NPN_OK)
+      st = launch_gemm(plan(1, hidden, zn), x, z_w, nullptr, nullptr, pz, 1, hidden, zn, 1,
                        false, s);
-  if (st != NPN_OK) return st;
-  st = launch_gemm(plan(1, hidden, zn), x, z_w, nullptr, nullptr, pz, 1, hidden, zn, 1, false, s);
+  }
   if (st != NPN_OK) return st;
   InprojFinishArgs fa{pq, qkv_s, reinterpret_cast<uint16_t*>(ws), conv_state, new_conv_state,
                       pz, z_s, reinterpret_cast<uint16_t*>(ws + l.z), x,

@@ -502,8 +502,8 @@ def full_fp8_bench(args):
     print(json.dumps({
         "workload": "deltanet::full_fp8, one decode token of one sequence, HIDDEN 5120, fp8 "
                     "in-projections (qkv, z, a, b) + DeltaNet token step",
-        "kernel": "deltanet.full_fp8 (two narrow fp8 GEMMs, dn_fp8_inproj_finish_kernel, "
-                  "dn_verify_kernel)", "bound": "hbm", "peak": HBM_PEAK_GBS, "rows": rows,
+        "kernel": "deltanet.full_fp8 (fp8_gemm_narrow_kernel: qkv + z in one launch, "
+                  "dn_fp8_inproj_finish_kernel, dn_verify_kernel)", "bound": "hbm", "peak": HBM_PEAK_GBS, "rows": rows,
         "steps": args.steps, "warmup": max(args.warmup, CFG_MIN_WARMUP)}))
 
 

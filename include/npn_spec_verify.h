@@ -81,8 +81,9 @@ int npn_deltanet_full_batched(const float* state, const uint16_t* mixed_qkv,
  * arguments, same outputs; new_conv_state must not overlap conv_state). mixed_qkv and z are
  * bit-identical to npn_fp8_matmul's outputs. hidden % 64 == 0; workspace of
  * npn_deltanet_full_fp8_workspace_size(hidden, k_heads, v_heads) bytes (0: unsupported sizes),
- * 16-byte aligned. Four launches: the qkv and z GEMMs (split-K partials), one kernel that
- * reduces them, shifts the conv window and computes a_out and b_out, then the token step. */
+ * 16-byte aligned. Three launches: the qkv and z GEMMs (split-K partials, one launch where
+ * their plans agree), one kernel that reduces them, shifts the conv window and computes a_out
+ * and b_out, then the token step. */
 size_t npn_deltanet_full_fp8_workspace_size(int hidden, int k_heads, int v_heads);
 int npn_deltanet_full_fp8(const uint16_t* x, const float* state, const uint16_t* conv_state,
                           const float* conv_weight, const float* conv_bias, const float* A_log,

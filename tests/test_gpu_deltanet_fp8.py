@@ -3,7 +3,8 @@ into deltanet::full; contrib/qwen3.6-27b/kernels/deltanet_full_fp8_ops.py:7-32) 
 oracle (oracle.deltanet.deltanet_full_fp8, pinned to HF's DeltaNet layer in
 test_oracle_layers.py), at the reference's per-rank shapes (HIDDEN 5120, 4 k / 12 v heads,
 seed 11 and state std 0.1 as contrib/qwen3.6-27b/kernels/tests/test_deltanet_full.py:58-73)
-and at full width (16 / 48 heads). Weights are the harness's per-channel quantisation of
+at full width (16 / 48 heads), and at 32 / 64 heads (where the qkv and z GEMMs take different
+one-row plans and so run as two launches). Weights are the harness's per-channel quantisation of
 N(0, 0.02) (static_decode.py:283-304).
 
 Bars: state and gated output within 2e-3 relative (tests/_util.py); the new conv window's
@@ -57,8 +58,20 @@ def _oracle(d, hk, hv):
         w("a_w"), n("a_s").reshape(-1), w("b_w"), n("b_s").reshape(-1), hk, hv)
 
 
-@pytest.mark.parametrize("hk,hv,seed", [(4, 12, 11), (16, 48, 12)])
+def _plan_kind(N):
+    import ctypes
+    import npn_native
+    info = (ctypes.c_int * 4)()
+    assert npn_native.lib().npn_fp8_matmul_plan(1, HIDDEN, N, info) == 0
+    return tuple(info[:2])
+
+
+# 32 / 64 heads: the qkv GEMM's one-row plan is stream-K (64 tiles) while z's is a tiles x
+# split grid, so the two GEMMs run as separate launches instead of one
+@pytest.mark.parametrize("hk,hv,seed", [(4, 12, 11), (16, 48, 12), (32, 64, 13)])
 def test_full_fp8_matches_oracle(ops, hk, hv, seed):
+    if hk == 32:
+        assert _plan_kind((2 * hk + hv) * D)[0] == 1 and _plan_kind(hv * D)[0] == 0
     d = _inputs(hk, hv, seed)
     args = _gpu_args(d)
     ns, ncs, out = ops.deltanet.full_fp8(*args)
